@@ -1,0 +1,207 @@
+"""Benchmark: int8-weight LoRA linear forward + dX + dA + dB on Wan-2.1-14B block shapes, 1 GPU.
+
+One step = one pass over the six projections of a Wan-2.1-14B transformer block at 32760 tokens
+(480x832x81 frames: latent 21x60x104, patch 1x2x2): self-attention q/k/v/o 5120->5120 and the FFN
+5120->13824->5120, each an int8 per-output-channel frozen weight (packed from bf16 ~N(0, 0.02))
+with a rank-32 LoRA (alpha 32, A and B ~N(0, 0.01)), bf16 activations ~N(0, 1) and output
+gradients ~N(0, 1). Forward runs q, k, v, o, ffn.0, ffn.2; backward runs them in reverse, each
+producing dX, dA and dB. Inputs are synthetic and already resident in HBM when timing starts.
+
+Prints one JSON line (see the keys below). Per-kernel durations come from HIP events recorded by
+the library around every launch on the launch stream, over the timed steps themselves.
+
+    python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--cpu-seconds 15]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+METRIC = ("TFLOP/s and % bf16-MFMA peak, int8-W LoRA linear fwd+bwd, Wan-14B shapes, 1 GPU")
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA (published)
+PEAK_HBM_GBS = 8000.0
+TOKENS = 32760
+RANK = 32
+ALPHA = 32.0
+PROJECTIONS = [("self_attn.q", 5120, 5120), ("self_attn.k", 5120, 5120),
+               ("self_attn.v", 5120, 5120), ("self_attn.o", 5120, 5120),
+               ("ffn.0", 5120, 13824), ("ffn.2", 13824, 5120)]
+
+
+def linear_flops(M, K, N, r):
+    return 4.0 * M * N * K + 6.0 * M * r * (K + N)
+
+
+def gemm_flops(mode, M, K, N, r):
+    """Algorithmic flops of one i8gemm launch: the base product plus the fused LoRA term."""
+    return 2.0 * M * N * K + 2.0 * M * r * (N if mode == "fwd" else K)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0,
+                    help="approximate CPU work for the cpu_baseline sample (0 disables it)")
+    ap.add_argument("--tokens", type=int, default=TOKENS)
+    return ap.parse_args()
+
+
+class Projection:
+    def __init__(self, name, K, N, M, r, dev, gen):
+        import torch
+        from reels_amd import quantize_frozen_matrix, workspace_bytes, _lib
+        self.name, self.K, self.N, self.M, self.r = name, K, N, M, r
+        w = torch.randn((N, K), generator=gen, device=dev, dtype=torch.float32).mul_(0.02)
+        self.W = quantize_frozen_matrix(w.to(torch.bfloat16))
+        del w
+        bf = torch.bfloat16
+        self.x = torch.randn((M, K), generator=gen, device=dev, dtype=torch.float32).to(bf)
+        self.dy = torch.randn((M, N), generator=gen, device=dev, dtype=torch.float32).to(bf)
+        self.A = (torch.randn((K, r), generator=gen, device=dev) * 0.01).to(bf)
+        self.B = (torch.randn((r, N), generator=gen, device=dev) * 0.01).to(bf)
+        self.y = torch.empty((M, N), dtype=bf, device=dev)
+        self.h = torch.empty((M, r), dtype=bf, device=dev)
+        self.dx = torch.empty((M, K), dtype=bf, device=dev)
+        self.dA = torch.empty((K, r), dtype=torch.float32, device=dev)
+        self.dB = torch.empty((r, N), dtype=torch.float32, device=dev)
+        self.wsf_n = workspace_bytes(M, K, N, r, _lib.WS_FWD)
+        self.wsb_n = workspace_bytes(M, K, N, r, _lib.WS_BWD)
+        self.wsf = torch.empty((self.wsf_n,), dtype=torch.uint8, device=dev)
+        self.wsb = torch.empty((self.wsb_n,), dtype=torch.uint8, device=dev)
+        c = float(torch.tensor(ALPHA, dtype=torch.float32) / torch.tensor(float(r)))
+        p = lambda t: ctypes.c_void_p(t.data_ptr())
+        st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        self.fwd_args = (p(self.x), p(self.W.values), p(self.W.scales), p(self.A), p(self.B), None,
+                         M, K, N, r, c, p(self.y), p(self.h), p(self.wsf), self.wsf_n, st)
+        self.bwd_args = (p(self.dy), p(self.x), p(self.h), p(self.W.values), p(self.W.scales),
+                         p(self.A), p(self.B), M, K, N, r, c, p(self.dx), p(self.dA), p(self.dB),
+                         p(self.wsb), self.wsb_n, st)
+
+
+def run_step(L, projs, check):
+    for pr in projs:
+        check("reels_hip_i8lora_fwd", L.reels_hip_i8lora_fwd(*pr.fwd_args))
+    for pr in reversed(projs):
+        check("reels_hip_i8lora_bwd", L.reels_hip_i8lora_bwd(*pr.bwd_args))
+
+
+def cpu_baseline(seconds):
+    """The reference's CPU path (fp32: dequantize-materialise + BLAS sgemm + rank-r GEMMs, see
+    oracle/cpu_path.py) on a bounded sample of the same six projections at fewer tokens."""
+    import torch
+    from oracle import cpu_path
+    threads = torch.get_num_threads()
+    shapes = [(K, N) for (_, K, N) in PROJECTIONS]
+    t_cal, f_cal = cpu_path.time_block(shapes, 128, RANK)
+    rate = f_cal / max(t_cal, 1e-9)
+    per_token = f_cal / 128
+    m = int(seconds * rate / per_token) // 128 * 128
+    m = max(128, min(m, TOKENS))
+    t, f = cpu_path.time_block(shapes, m, RANK, seed=1)
+    return {"value": round(f / t / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": (f"Wan-14B block projections (q,k,v,o 5120->5120, ffn 5120->13824->5120), "
+                       f"r=32, fwd+dX+dA+dB at {m} tokens (of {TOKENS}), fp32 materialised "
+                       f"dequant + torch CPU BLAS, {threads} threads, {t:.2f} s")}
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py runs on exactly one GPU (asked for --gpus {args.gpus}, WORLD_SIZE "
+              f"{world}); the multi-GPU path is not built", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from reels_amd import _lib
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    L = _lib.lib()
+    gen = torch.Generator(device=dev).manual_seed(1234)
+    M = args.tokens
+    projs = [Projection(n, K, N, M, RANK, dev, gen) for (n, K, N) in PROJECTIONS]
+    torch.cuda.synchronize()
+
+    for _ in range(args.warmup):
+        run_step(L, projs, _lib.check)
+    torch.cuda.synchronize()
+
+    launches_per_step = 64
+    _lib.check("reels_hip_trace_start", L.reels_hip_trace_start(launches_per_step * args.steps))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        run_step(L, projs, _lib.check)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    recs = _lib.trace_records()
+
+    ms_per_step = (t1 - t0) * 1e3 / args.steps
+    step_flops = sum(linear_flops(M, K, N, RANK) for (_, K, N) in PROJECTIONS)
+    value = step_flops / (ms_per_step * 1e-3) / 1e12
+
+    # per-kernel statistics from the event trace (launch order is fixed within a step)
+    per_step = len(recs) // max(args.steps, 1)
+    kern = {}
+    for name, ms in recs:
+        d = kern.setdefault(name, [0, 0.0])
+        d[0] += 1
+        d[1] += ms
+    gemm_ms = {"fwd": 0.0, "dx": 0.0}
+    gemm_n = {"fwd": 0, "dx": 0}
+    gemm_fl = {"fwd": 0.0, "dx": 0.0}
+    for step in range(args.steps):
+        rs = recs[step * per_step:(step + 1) * per_step]
+        fi = [ms for (n, ms) in rs if n == "i8gemm_kernel<0>"]
+        bi = [ms for (n, ms) in rs if n == "i8gemm_kernel<1>"]
+        for (pr, ms) in zip(projs, fi):
+            gemm_ms["fwd"] += ms; gemm_n["fwd"] += 1
+            gemm_fl["fwd"] += gemm_flops("fwd", M, pr.K, pr.N, RANK)
+        for (pr, ms) in zip(reversed(projs), bi):
+            gemm_ms["dx"] += ms; gemm_n["dx"] += 1
+            gemm_fl["dx"] += gemm_flops("dx", M, pr.K, pr.N, RANK)
+    tot_ms = gemm_ms["fwd"] + gemm_ms["dx"]
+    achieved = (gemm_fl["fwd"] + gemm_fl["dx"]) / (tot_ms * 1e-3) / 1e12 if tot_ms > 0 else 0.0
+    roofline = {
+        "kernel": "i8gemm_kernel (fwd <0> and dX <1>, int8 weight dequantised to bf16 on MFMA)",
+        "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+        "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+        "avg_launch_ms": {k: round(gemm_ms[k] / max(gemm_n[k], 1), 4) for k in gemm_ms},
+        "launches": gemm_n,
+    }
+    kernels = {n: {"launches": c, "avg_ms": round(t / c, 4), "ms_per_step": round(t / args.steps, 4)}
+               for n, (c, t) in sorted(kern.items(), key=lambda kv: -kv[1][1])}
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        cpu = cpu_baseline(args.cpu_seconds)
+
+    out = {
+        "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "wan2.1-14b block projections: self_attn q/k/v/o 5120->5120, "
+                               "ffn 5120->13824->5120; int8 per-channel frozen weights; LoRA "
+                               "r=32 alpha=32; forward + dX + dA + dB",
+                   "tokens": M, "rank": RANK, "flops_per_step": step_flops},
+        "frac_of_bf16_peak": round(value / PEAK_BF16_TFLOPS, 4),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "kernels": kernels,
+        "device": torch.cuda.get_device_name(dev),
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,131 @@
+/*
+ * reels_hip: MI355X (gfx950) HIP kernels for Reels.jl's int8 frozen-weight LoRA linear.
+ *
+ * C ABI only: plain pointers, sizes and a hipStream_t passed as void*. Every pointer argument
+ * is a device pointer unless stated otherwise. The caller owns every buffer; the library never
+ * allocates caller-visible memory, never frees and keeps no pointer past return. All work is
+ * enqueued on `stream` (NULL = the default stream) without host synchronisation, so buffers must
+ * stay alive until the caller synchronises that stream.
+ *
+ * Conventions follow the reference's only native bridge (deps/sentencepiece_bridge.cpp:11-87):
+ * an int status (0 = success, negative = error) and a thread-local message retrieved with
+ * reels_hip_last_error(), valid until the next call on the same thread.
+ *
+ * Physical layouts (row-major "[a][b]": a rows of b contiguous elements). They are the memory
+ * of the reference's column-major Julia arrays, so a Julia caller passes its arrays unchanged:
+ *   x  [M][K] bf16  = Julia x::(K,M)            q  [N][K] int8 = transpose(Julia (K,N) Int8)
+ *   s  [N]    f32   = QuantizedMatrix.scales     A  [K][r] bf16 = Julia A::(r,K)
+ *   B  [r][N] bf16  = Julia B::(N,r)             y  [M][N] bf16 = Julia y::(N,M)
+ *   dy [M][N] bf16, dx [M][K] bf16, dA [K][r] f32 (= Julia (r,K)), dB [r][N] f32 (= (N,r))
+ * M = tokens, K = in_features, N = out_features, r = LoRA rank, lora_scale = alpha / r.
+ */
+#ifndef REELS_HIP_H
+#define REELS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define REELS_HIP_ABI_VERSION 1
+
+/* element type codes */
+#define REELS_HIP_F32 0
+#define REELS_HIP_BF16 1
+#define REELS_HIP_F16 2
+
+/* status codes */
+#define REELS_HIP_OK 0
+#define REELS_HIP_EINVAL (-1)     /* bad argument: NULL pointer, shape, leading dimension */
+#define REELS_HIP_EDTYPE (-2)     /* unsupported element type */
+#define REELS_HIP_EWORKSPACE (-3) /* workspace NULL or smaller than reels_hip_*_workspace_bytes */
+#define REELS_HIP_EHIP (-4)       /* HIP runtime or launch failure */
+
+/* workspace selectors for reels_hip_i8lora_workspace_bytes */
+#define REELS_HIP_WS_FWD 0
+#define REELS_HIP_WS_BWD 1
+
+/* ABI version of the loaded library; compare with REELS_HIP_ABI_VERSION. No reference
+ * counterpart (the reference has no native library for this path). */
+int reels_hip_abi_version(void);
+
+/* Message for the last failed call on this thread ("" if none). Mirrors reels_sp_last_error,
+ * deps/sentencepiece_bridge.cpp:11-16 and 83-87. */
+const char* reels_hip_last_error(void);
+
+/*
+ * quantize_frozen_matrix(W, T), src/layers/quantization.jl:35-44: per output channel
+ * (row n of W), absmax over K in f32, scale = absmax / 127f0 (IEEE divide), scale = 1 for a zero
+ * row, q = Int8(round_ties_even(clamp(w / scale, -127, 127))). Bit-exact with the reference.
+ *   w      [N][ld_w] of dtype REELS_HIP_BF16, REELS_HIP_F16 or REELS_HIP_F32 (ld_w >= K)
+ *   q      [N][K] int8 out; scales [N] f32 out
+ *   status one device int32, set to 0 then to 1 if any weight is non-finite (the reference
+ *          throws InexactError from Int8(NaN)); such elements are written as 0. May be NULL.
+ * Replaces the host-CPU packing in _move_weight (quantization.jl:111-125) and
+ * quantized_umt5_state_dict (src/models/wan21/text_encoder.jl:318).
+ */
+int reels_hip_i8_pack(const void* w, int dtype, int64_t N, int64_t K, int64_t ld_w, int8_t* q,
+                      float* scales, int32_t* status, void* stream);
+
+/* Bytes of device workspace needed by reels_hip_i8lora_fwd (which = REELS_HIP_WS_FWD) or
+ * reels_hip_i8lora_bwd (REELS_HIP_WS_BWD) for these sizes. Always a multiple of 256. */
+size_t reels_hip_i8lora_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t r, int which);
+
+/*
+ * lora_forward(layer, x), src/layers/lora.jl:56-95, for a LoRALinear whose weight is a
+ * QuantizedMatrix, with _weight_mul (quantization.jl:73-74) done without materialising deq(W):
+ *   h = bf16(x * A)                                    [M][r]
+ *   y = bf16(s[n] * sum_k x[m][k] q[n][k] + lora_scale * sum_j h[m][j] B[j][n] + bias[n])
+ * bias may be NULL. r = 0 (A, B NULL) gives the base-only linear(::DenseLayer) of
+ * src/layers/linear.jl:38-46. h_save (bf16 [M][r] or NULL) receives h for the backward.
+ * workspace: device memory of reels_hip_i8lora_workspace_bytes(M, K, N, r, REELS_HIP_WS_FWD).
+ */
+int reels_hip_i8lora_fwd(const void* x, const int8_t* q, const float* scales, const void* A,
+                         const void* B, const void* bias, int64_t M, int64_t K, int64_t N,
+                         int64_t r, float lora_scale, void* y, void* h_save, void* workspace,
+                         size_t ws_bytes, void* stream);
+
+/*
+ * lora_backward(layer, x, dy), src/layers/lora.jl:106-118, with the frozen-weight pullback of
+ * src/training/ad_rules.jl:70-80 (_weight_transpose_mul, quantization.jl:75-76):
+ *   u  = bf16(dy * B^T)                                                      [M][r]
+ *   dx = bf16(sum_n bf16(dy[m][n] s[n]) q[n][k] + lora_scale * sum_j u[m][j] A[k][j])
+ *   dA = lora_scale * x^T u   (f32 [K][r]);   dB = lora_scale * h^T dy   (f32 [r][N])
+ * h: the forward's h_save (bf16 [M][r]) or NULL to recompute it. dx, dA, dB may each be NULL to
+ * skip that output. r = 0 gives dx = deq(W)^T dy alone (_weight_transpose_mul). dA and dB are
+ * overwritten (not accumulated) and are bitwise reproducible run to run.
+ */
+int reels_hip_i8lora_bwd(const void* dy, const void* x, const void* h, const int8_t* q,
+                         const float* scales, const void* A, const void* B, int64_t M, int64_t K,
+                         int64_t N, int64_t r, float lora_scale, void* dx, float* dA, float* dB,
+                         void* workspace, size_t ws_bytes, void* stream);
+
+/* gelu_tanh, src/layers/linear.jl:61-68: y = bf16(0.5x(1 + tanh(sqrt(2/pi)(x + 0.044715x^3))))
+ * computed in f32 on bf16 x[n]. */
+int reels_hip_gelu_tanh(const void* x, void* y, int64_t n, void* stream);
+
+/* Pullback of gelu_tanh (the reference lets Zygote differentiate linear.jl:61-68):
+ * dx = bf16(dy * gelu'(x)) with the analytic derivative in f32. */
+int reels_hip_gelu_tanh_bwd(const void* x, const void* dy, void* dx, int64_t n, void* stream);
+
+/*
+ * Kernel timing instrumentation. No counterpart in the reference (it has no profiler hooks);
+ * used by benchmarks to time individual kernels with HIP events on the stream each kernel is
+ * launched on. While enabled, every kernel the library enqueues is bracketed by two event
+ * records (events are created on first use and kept). Not thread-safe against concurrent calls
+ * of the entry points on other threads while enabled.
+ *   reels_hip_trace_start(capacity): clear old records and record up to `capacity` launches
+ *   reels_hip_trace_stop(): stop recording; returns the number of launches recorded
+ *   reels_hip_trace_get(i, &name, &ms): kernel name and duration of launch i; the caller must
+ *     have synchronised the streams first. Returns REELS_HIP_EINVAL for a bad index.
+ */
+int reels_hip_trace_start(int capacity);
+int reels_hip_trace_stop(void);
+int reels_hip_trace_get(int index, const char** name, float* ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* REELS_HIP_H */

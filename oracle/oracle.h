@@ -1,0 +1,97 @@
+/*
+ * Oracle for the int8 frozen-weight LoRA linear: a plain-C, CPU-only restatement of
+ * Reels.jl's algorithm (file:line citations are relative to the Reels.jl repository).
+ *
+ * TEST INFRASTRUCTURE ONLY. The only callers are tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py, and only as the checker. The product path (reels_amd/) never
+ * links, loads or calls anything here.
+ *
+ * Physical layouts (row-major, "[a][b]" = a rows of b contiguous elements), identical to the
+ * Julia column-major arrays they restate:
+ *   x  [M][K] bf16   (Julia x::(K,M))          q  [N][K] int8 (Julia values::(N,K) as transpose)
+ *   s  [N]    f32                              A  [K][r] bf16 (Julia A::(r,K))
+ *   B  [r][N] bf16   (Julia B::(N,r))          y  [M][N]      (Julia y::(N,M))
+ *   dy [M][N]        dx [M][K]                 dA [K][r]      dB [r][N]
+ *
+ * Parity status of each function is stated beside it.
+ */
+#ifndef REELS_ORACLE_H
+#define REELS_ORACLE_H
+#include <stdint.h>
+#include <stddef.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* bf16 <-> f32 exactly as src/models/interface.jl:13-25 (RNE bit trick, no NaN special case).
+ * Pinned by: exhaustive 2^16 round trip, textbook RNE ties, torch's bf16 cast on finite values. */
+float    oracle_bf16_to_f32(uint16_t h);
+uint16_t oracle_f32_to_bf16(float f);
+void     oracle_f32_to_bf16_array(const float* in, uint16_t* out, int64_t n);
+void     oracle_bf16_to_f32_array(const uint16_t* in, float* out, int64_t n);
+
+/* quantize_frozen_matrix, src/layers/quantization.jl:35-44.
+ * w: [N][K] with leading dimension ld (elements). dtype: 0 = f32, 1 = bf16, 2 = f16.
+ * Returns 0, or 1 if any element is non-finite (Julia's Int8(NaN) InexactError), in which case
+ * the rows holding non-finite codes are left with the value 0 in q. -1 on bad arguments.
+ * Pinned by: a second independent numpy restatement (bit-exact agreement), closed-form special
+ * cases (zero rows, exact scale 1 and 2 ties-to-even rows, single spikes, denormal absmax),
+ * invariants, and committed golden codes for the real Wan weights in
+ * test/fixtures/wan21_block_tiny.safetensors. */
+int oracle_pack(const void* w, int dtype, int64_t N, int64_t K, int64_t ld, int8_t* q, float* s);
+
+/* Dequantization variants, src/layers/quantization.jl:25-29 and 61-64.
+ * mode 0: Float32(q)*s (f32 out); mode 1: Float16(q)*Float16(s) rounded to f16 (u16 bits out);
+ * mode 2: bf16_rne(Float32(q)*s) (u16 bits out). Pinned by closed forms per element. */
+void oracle_dequant(const int8_t* q, const float* s, int64_t N, int64_t K, int mode, void* out);
+
+/* lora_forward, src/layers/lora.jl:56-95 with _weight_mul (quantization.jl:73-74), computed in
+ * f64 from bf16 inputs (the exact value of the math): for each listed row m,
+ *   y[m][n] = sum_k x[m][k]*q[n][k]*s[n] + c*sum_j h[m][j]*B[j][n] + bias[n],
+ *   h[m][j] = sum_k x[m][k]*A[k][j].
+ * rows: row indices to compute (NULL = all M; nrows then ignored). Output rows are packed in
+ * the order given (y_out [nrows][N], h_out [nrows][r], either may be NULL). bias may be NULL.
+ * Pinned by: brute-force small cases with integer-valued inputs (exact in f64), linearity,
+ * B = 0 reducing to the base GEMM (test/unit/lora.jl:6), merged-weight identity (lora.jl:8). */
+void oracle_lora_forward(const uint16_t* x, const int8_t* q, const float* s, const uint16_t* A,
+                         const uint16_t* B, const uint16_t* bias, int64_t M, int64_t K, int64_t N,
+                         int64_t r, float c, const int64_t* rows, int64_t nrows, double* y_out,
+                         double* h_out);
+
+/* lora_backward, src/layers/lora.jl:106-118 (and the frozen-weight rrule of
+ * src/training/ad_rules.jl:70-80), in f64:
+ *   u[m][j]  = sum_n dy[m][n]*B[j][n]
+ *   dx[m][k] = sum_n dy[m][n]*s[n]*q[n][k] + c*sum_j u[m][j]*A[k][j]   (listed rows only)
+ *   dA[k][j] = c*sum_m u[m][j]*x[m][k]       (all M; listed k columns only, kcols NULL = all)
+ *   dB[j][n] = c*sum_m h[m][j]*dy[m][n]      (all M; listed n columns only, ncols NULL = all)
+ * with h = x*A in f64. Outputs packed in listed order: dx_out [nrows][K], dA_out [nk][r],
+ * dB_out [r][nn]; any may be NULL. Pinned by: central finite differences of
+ * oracle_lora_forward (as test/unit/lora.jl:12-21), brute-force integer cases. */
+void oracle_lora_backward(const uint16_t* dy, const uint16_t* x, const int8_t* q, const float* s,
+                          const uint16_t* A, const uint16_t* B, int64_t M, int64_t K, int64_t N,
+                          int64_t r, float c, const int64_t* rows, int64_t nrows,
+                          const int64_t* kcols, int64_t nk, const int64_t* ncols, int64_t nn,
+                          double* dx_out, double* dA_out, double* dB_out);
+
+/* gelu_tanh, src/layers/linear.jl:61-68, in f32 on bf16 inputs, result rounded to bf16, and its
+ * analytic derivative applied to an upstream gradient (dx = bf16(dy * gelu'(x))).
+ * Pinned by: closed-form values (gelu(0)=0, odd-part identity gelu(x)-gelu(-x)=x), central
+ * finite differences for the derivative. */
+void oracle_gelu_tanh(const uint16_t* x, uint16_t* y, int64_t n);
+void oracle_gelu_tanh_backward(const uint16_t* x, const uint16_t* dy, uint16_t* dx, int64_t n);
+
+/* Philox4x32-10 (Salmon et al., SC'11) counter-based generator for seeded test inputs.
+ * Pinned by the published Random123 known-answer vectors. */
+void oracle_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
+/* Normal(0, sigma) values from Philox + Box-Muller (in f64), element i uses counter
+ * (i_lo, i_hi, stream, 0) and key (seed_lo, seed_hi). Outliers: if outlier_rate > 0 an element
+ * whose third word is < outlier_rate*2^32 becomes +-outlier_sigma*sigma (sign: bit 0 of the
+ * fourth word). Written as bf16 (RNE) or f32. */
+void oracle_normal_bf16(uint64_t seed, uint32_t stream, int64_t n, double sigma,
+                        double outlier_rate, double outlier_sigma, uint16_t* out);
+void oracle_normal_f32(uint64_t seed, uint32_t stream, int64_t n, double sigma, float* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

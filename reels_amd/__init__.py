@@ -1,0 +1,29 @@
+"""reels_amd: MI355X (gfx950) HIP implementation of Reels.jl's int8 frozen-weight LoRA linear.
+
+The compute lives in libreels_hip.so (C ABI: include/reels_hip.h); this package is the host-side
+mirror of the reference layer API (src/layers/quantization.jl, lora.jl, linear.jl).
+"""
+from ._lib import ReelsHIPError, ReelsHIPUnavailable, library_path  # noqa: F401
+from .layers import (  # noqa: F401
+    DenseLayer,
+    FrozenWeightTransfer,
+    I8LoRALinearFunction,
+    LoRALinear,
+    QuantizedMatrix,
+    _weight_mul,
+    _weight_transpose_mul,
+    frozen_weight_transfer,
+    gelu_tanh,
+    gelu_tanh_backward,
+    i8lora_backward,
+    i8lora_forward,
+    linear,
+    lora_backward,
+    lora_forward,
+    lora_parameters,
+    merged_weight,
+    move_weight,
+    quantize_frozen_matrix,
+    set_adapter_enabled,
+    workspace_bytes,
+)

@@ -1,0 +1,256 @@
+// Dense int8-weight GEMMs of the LoRA linear, bf16 MFMA on gfx950.
+//
+//   FWD (_weight_mul, src/layers/quantization.jl:73-74, inside lora_forward, lora.jl:56-95):
+//     out[m][n] = bf16( s[n] * sum_k act[m][k] q[n][k] + c * sum_j L[m][j] R[n][j] + bias[n] )
+//     act = x [M][K], L = h [M][rp], R = B^T [N][rp]
+//   DX  (_weight_transpose_mul, quantization.jl:75-76, inside lora_backward, lora.jl:115-116):
+//     out[m][k] = bf16( sum_n act[m][n] q[n][k] + c * sum_j L[m][j] R[k][j] )
+//     act = bf16(dy * s) [M][N], L = u [M][rp], R = A [K][rp]
+//
+// Block tile: 256 output columns (n in FWD, k in DX) x 256 tokens, reduction step 64, 256 threads
+// = 4 waves in a 2 x 2 grid, each wave 128 x 128 = 4 x 4 tiles of v_mfma_f32_32x32x16_bf16.
+// The MFMA A operand is the weight (rows = output columns) and the B operand the activations
+// (columns = tokens), so each lane ends with 4 consecutive output columns of one token and the
+// epilogue stores 8 bytes per lane.
+//
+// LDS (double-buffered, 96 KiB):
+//   activations: [256 tokens][64] bf16, 16-byte chunks XOR-swizzled by f(row) so the 32-row
+//                MFMA operand reads (ds_read_b128) hit distinct banks;
+//   weights: int8 as loaded from HBM (half the LDS bytes of bf16), converted exactly to bf16 in
+//            registers after the read:
+//     FWD [256 n][64 k]: operand = 8 consecutive k of one row n -> ds_read_b64
+//     DX  [64 n][256 k]: operand = 8 consecutive n of one column k -> ds_read_b64_tr_b8 (gfx950
+//         transpose read: lane i of a 16-lane group receives byte i%8 of the 8 bytes addressed
+//         by lane 2j + i/8, j = 0..7)
+#include "i8gemm.h"
+
+#include <mutex>
+
+namespace reels {
+
+namespace gemm {
+constexpr int BM = 256;  // tokens per block
+constexpr int BN = 256;  // output columns per block
+constexpr int BK = 64;   // reduction per step
+constexpr int NT = 256;
+constexpr int ACT_BYTES = BM * BK * 2;  // 32 KiB
+constexpr int W_BYTES = BN * BK;        // 16 KiB
+constexpr int STAGE_BYTES = ACT_BYTES + W_BYTES;
+}  // namespace gemm
+
+
+// swizzles (see the header comment); all map [0, 8) or [0, 16) onto itself for a fixed row
+__device__ __forceinline__ int act_swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+__device__ __forceinline__ int wf_swz(int row) { return ((row >> 1) & 7) ^ ((row >> 4) & 1); }
+__device__ __forceinline__ int wd_swz(int row) { return (row & 7) | ((row & 1) << 3); }
+
+template <int MODE>  // 0 = FWD, 1 = DX
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void i8gemm_kernel(GemmArgs a) {
+  using namespace gemm;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = t >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t n0 = (int64_t)blockIdx.x * BN;  // output column block
+  const int64_t m0 = (int64_t)blockIdx.y * BM;  // token block
+  const int64_t M = a.M, Ncols = a.Ncols, Kred = a.Kred;
+  const int nk = (int)((Kred + BK - 1) / BK);
+
+  // ---- global -> register staging --------------------------------------------------------
+  u32x4 ra[8], rw[4];
+  auto load_tiles = [&](int kt) {
+    const int64_t r0 = (int64_t)kt * BK;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = (t >> 3) + 32 * i, c = t & 7;
+      const int64_t m = m0 + row, k = r0 + c * 8;
+      const bool ok = (m < M) && (k < Kred);
+      const int64_t mc = m < M ? m : M - 1, kc = k < Kred ? k : 0;
+      u32x4 v = *reinterpret_cast<const u32x4*>(a.act + mc * Kred + kc);
+      ra[i] = ok ? v : u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      int64_t wr, wc;
+      bool ok;
+      if (MODE == 0) {  // rows n (output columns), 64 contiguous k
+        const int row = (t >> 2) + 64 * i, c = t & 3;
+        wr = n0 + row; wc = r0 + c * 16;
+        ok = (wr < Ncols) && (wc < Kred);
+        if (wr >= Ncols) wr = Ncols - 1;
+        if (wc >= Kred) wc = 0;
+      } else {          // rows n (reduction), 256 contiguous k (output columns)
+        const int row = (t >> 4) + 16 * i, c = t & 15;
+        wr = r0 + row; wc = n0 + c * 16;
+        ok = (wr < Kred) && (wc < Ncols);
+        if (wr >= Kred) wr = Kred - 1;
+        if (wc >= Ncols) wc = 0;
+      }
+      u32x4 v = *reinterpret_cast<const u32x4*>(a.q + wr * a.ldq + wc);
+      rw[i] = ok ? v : u32x4{0, 0, 0, 0};
+    }
+  };
+
+  // ---- register -> LDS ------------------------------------------------------------------
+  auto store_tiles = [&](int buf) {
+    uint8_t* sa = smem + buf * STAGE_BYTES;
+    uint8_t* sw = sa + ACT_BYTES;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = (t >> 3) + 32 * i, c = t & 7;
+      *reinterpret_cast<u32x4*>(sa + row * 128 + ((c ^ act_swz(row)) << 4)) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (MODE == 0) {
+        const int row = (t >> 2) + 64 * i, c = t & 3;
+        const int g = wf_swz(row);
+        u32x4 v = rw[i];
+        if (g & 1) v = u32x4{v[2], v[3], v[0], v[1]};
+        *reinterpret_cast<u32x4*>(sw + row * 64 + ((c ^ (g >> 1)) << 4)) = v;
+      } else {
+        const int row = (t >> 4) + 16 * i, c = t & 15;
+        *reinterpret_cast<u32x4*>(sw + row * 256 + ((c ^ wd_swz(row)) << 4)) = rw[i];
+      }
+    }
+  };
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  // per-lane LDS read offsets (independent of the k step)
+  const int l32 = lane & 31, lhi = lane >> 5;
+
+  auto compute = [&](int buf) {
+    const uint8_t* sa = smem + buf * STAGE_BYTES;
+    const uint8_t* sw = sa + ACT_BYTES;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      bf16x8 bfr[4], afr[4];
+#pragma unroll
+      for (int tj = 0; tj < 4; ++tj) {
+        const int row = wm * 128 + tj * 32 + l32;
+        const int c = kk * 2 + lhi;
+        bfr[tj] = as_bf16x8(*reinterpret_cast<const u32x4*>(sa + row * 128 + ((c ^ act_swz(row)) << 4)));
+      }
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti) {
+        u32x2 raw;
+        if (MODE == 0) {
+          const int row = wn * 128 + ti * 32 + l32;
+          const int sub = kk * 2 + lhi;
+          raw = *reinterpret_cast<const u32x2*>(sw + row * 64 + ((sub ^ wf_swz(row)) << 3));
+        } else {
+          const int g = lane >> 4, i16 = lane & 15;
+          const int row = kk * 16 + (g >> 1) * 8 + (i16 >> 1);
+          const int col = wn * 128 + ti * 32 + 16 * (g & 1) + 8 * (i16 & 1);
+          const int sub = col >> 3;  // 0..31
+          const uint8_t* p = sw + row * 256 + ((sub ^ (wd_swz(row) << 1)) << 3);
+          i32x2 v = __builtin_amdgcn_ds_read_tr8_b64_v2i32(LDS_PTR(i32x2, p));
+          raw = u32x2{(uint32_t)v[0], (uint32_t)v[1]};
+        }
+        afr[ti] = i8x8_to_bf16x8(raw[0], raw[1]);
+      }
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+        for (int tj = 0; tj < 4; ++tj)
+          acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(afr[ti], bfr[tj], acc[ti][tj], 0, 0, 0);
+    }
+  };
+
+  load_tiles(0);
+  store_tiles(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) load_tiles(kt + 1);
+    compute(cur);
+    if (kt + 1 < nk) store_tiles(cur ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: scale, LoRA up-projection on MFMA, bias, one bf16 rounding ----------------
+  const int nsteps = a.rp >> 4;
+#pragma unroll
+  for (int ti = 0; ti < 4; ++ti) {
+    const int64_t nrow = n0 + wn * 128 + ti * 32 + l32;  // R operand row of this lane
+    const int64_t nrc = nrow < Ncols ? nrow : Ncols - 1;
+    // per-lane output columns: n = nbase + g4*8 + (0..3)
+    const int64_t nbase = n0 + wn * 128 + ti * 32 + lhi * 4;
+    float sc[16], bs[16];
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int64_t n = nbase + g4 * 8;
+      const bool ok = n < Ncols;
+      f32x4 s4 = {1.0f, 1.0f, 1.0f, 1.0f};
+      if (a.colscale != nullptr && ok) s4 = *reinterpret_cast<const f32x4*>(a.colscale + n);
+      u32x2 b2 = {0, 0};
+      if (a.bias != nullptr && ok) b2 = *reinterpret_cast<const u32x2*>(a.bias + n);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sc[g4 * 4 + e] = s4[e];
+      bs[g4 * 4 + 0] = bf16_lo(b2[0]); bs[g4 * 4 + 1] = bf16_hi(b2[0]);
+      bs[g4 * 4 + 2] = bf16_lo(b2[1]); bs[g4 * 4 + 3] = bf16_hi(b2[1]);
+    }
+#pragma unroll
+    for (int tj = 0; tj < 4; ++tj) {
+      const int64_t m = m0 + wm * 128 + tj * 32 + l32;
+      const int64_t mc = m < M ? m : M - 1;
+      f32x16 lo;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) lo[v] = 0.0f;
+      for (int s = 0; s < nsteps; ++s) {
+        u32x4 rv = *reinterpret_cast<const u32x4*>(a.R + nrc * a.rp + s * 16 + lhi * 8);
+        u32x4 lv = *reinterpret_cast<const u32x4*>(a.L + mc * a.rp + s * 16 + lhi * 8);
+        if (nrow >= Ncols) rv = u32x4{0, 0, 0, 0};
+        if (m >= M) lv = u32x4{0, 0, 0, 0};
+        lo = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(rv), as_bf16x8(lv), lo, 0, 0, 0);
+      }
+      if (m < M) {
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int64_t n = nbase + g4 * 8;
+          if (n < Ncols) {
+            float o[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int v = g4 * 4 + e;
+              o[e] = sc[v] * acc[ti][tj][v] + a.c * lo[v] + bs[v];
+            }
+            u32x2 pk = {pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+            *reinterpret_cast<u32x2*>(a.out + m * Ncols + n) = pk;
+          }
+        }
+      }
+    }
+  }
+}
+
+int launch_i8gemm(int mode, const GemmArgs& a, hipStream_t st) {
+  using namespace gemm;
+  dim3 grid((unsigned)ceil_div(a.Ncols, BN), (unsigned)ceil_div(a.M, BM));
+  const size_t lds = 2 * STAGE_BYTES;
+  static std::once_flag once;
+  static hipError_t attr_err = hipSuccess;
+  std::call_once(once, [&] {
+    attr_err = hipFuncSetAttribute((const void*)i8gemm_kernel<0>,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr_err == hipSuccess)
+      attr_err = hipFuncSetAttribute((const void*)i8gemm_kernel<1>,
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  });
+  if (attr_err != hipSuccess)
+    return fail(REELS_HIP_EHIP, std::string("i8gemm: hipFuncSetAttribute: ") + hipGetErrorString(attr_err));
+  if (mode == 0) { TraceScope _ts(st, "i8gemm_kernel<0>"); i8gemm_kernel<0><<<grid, NT, lds, st>>>(a); }
+  else { TraceScope _ts(st, "i8gemm_kernel<1>"); i8gemm_kernel<1><<<grid, NT, lds, st>>>(a); }
+  return check_launch(mode == 0 ? "i8gemm_kernel<FWD>" : "i8gemm_kernel<DX>");
+}
+
+}  // namespace reels

@@ -1,0 +1,623 @@
+// LoRA-side kernels and the forward/backward entry points of the int8 LoRA linear.
+//
+// Forward (lora_forward, src/layers/lora.jl:56-95):
+//   1. transpose A [K][r] -> At [r][K], B [r][N] -> Bt [N][rp]           (tiny)
+//   2. rowproj:  h = bf16(x * A)                      [M][rp]            (HBM-bound, reads x once)
+//   3. i8gemm<FWD>: y = bf16(s * (x q^T) + c * h Bt^T + bias)            (MFMA-bound)
+// Backward (lora_backward, lora.jl:106-118):
+//   1. rowproj (+ scaled copy): u = bf16(dy * B^T), dys = bf16(dy * s)   (reads dy once)
+//   2. i8gemm<DX>: dx = bf16(dys q + c * u A^T)                          (MFMA-bound)
+//   3. colgrad: dA = c x^T u, dB = c (dy^T h)^T as split-M partials, then a fixed-order sum
+//      (no float atomics: bitwise reproducible)                          (HBM-bound)
+// Any shape the fast kernels do not take (K, N or r not multiples of 16, r > 128, unaligned
+// pointers) runs through the generic kernels at the bottom, which compute the same formulas with
+// the same bf16 rounding points, one output element per thread.
+#include "i8gemm.h"
+
+namespace reels {
+
+
+
+// ---------------------------------------------------------------------------------------------
+// transpose: out[c][r] = in[r][c] for r < rows, zero for rows <= r < rows_pad (bf16)
+__global__ void transpose_pad_kernel(const uint16_t* __restrict__ in, int64_t rows, int64_t cols,
+                                     int64_t rows_pad, uint16_t* __restrict__ out) {
+  __shared__ uint16_t tile[32][33];
+  const int64_t r0 = (int64_t)blockIdx.y * 32, c0 = (int64_t)blockIdx.x * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 256 threads: 32 x 8
+  for (int i = ty; i < 32; i += 8) {
+    const int64_t r = r0 + i, c = c0 + tx;
+    tile[i][tx] = (r < rows && c < cols) ? in[r * cols + c] : (uint16_t)0;
+  }
+  __syncthreads();
+  for (int i = ty; i < 32; i += 8) {
+    const int64_t c = c0 + i, r = r0 + tx;
+    if (c < cols && r < rows_pad) out[c * rows_pad + r] = tile[tx][i];
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// rowproj: out[m][j] = bf16(sum_k src[m][k] * P[j][k]) for j < r, 0 for r <= j < rp.
+// src [M][Kd] bf16 (x or dy), P [r][Kd] bf16 (At or B). When SCALED, also writes
+// scaled[m][k] = bf16(src[m][k] * s[k]) (the dy * s operand of the DX GEMM).
+// Block = 4 waves on 32 rows; wave w takes a quarter of the k16 steps. MFMA A operand = 16 bytes
+// of one src row straight from HBM (each src byte is read once), B operand = 16 bytes of P
+// (L2-resident). The four partial 32 x (32*RT) tiles are summed in LDS in wave order.
+template <int RT, bool SCALED>
+__global__ __launch_bounds__(256) void rowproj_kernel(const uint16_t* __restrict__ src, int64_t M,
+                                                      int64_t Kd, const uint16_t* __restrict__ P,
+                                                      int r, int rp, uint16_t* __restrict__ out,
+                                                      const float* __restrict__ s,
+                                                      uint16_t* __restrict__ scaled) {
+  __shared__ float red[RT][16][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l32 = lane & 31, lhi = lane >> 5;
+  const int64_t m = (int64_t)blockIdx.x * 32 + l32;
+  const int64_t mc = m < M ? m : M - 1;
+  const int64_t steps = Kd / 16;
+  const int64_t per = (steps + 3) / 4;
+  const int64_t s0 = wave * per, s1 = (s0 + per < steps) ? s0 + per : steps;
+  f32x16 acc[RT];
+#pragma unroll
+  for (int t = 0; t < RT; ++t)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[t][v] = 0.0f;
+  const uint16_t* srow = src + mc * Kd + lhi * 8;
+  constexpr int U = 8;
+  int64_t st = s0;
+  for (; st + U <= s1; st += U) {
+    u32x4 xv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) xv[u] = *reinterpret_cast<const u32x4*>(srow + (st + u) * 16);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t k = (st + u) * 16 + lhi * 8;
+      if (SCALED && m < M) {
+        f32x4 sa = *reinterpret_cast<const f32x4*>(s + k);
+        f32x4 sb = *reinterpret_cast<const f32x4*>(s + k + 4);
+        u32x4 o;
+        o[0] = pack_bf16x2(bf16_lo(xv[u][0]) * sa[0], bf16_hi(xv[u][0]) * sa[1]);
+        o[1] = pack_bf16x2(bf16_lo(xv[u][1]) * sa[2], bf16_hi(xv[u][1]) * sa[3]);
+        o[2] = pack_bf16x2(bf16_lo(xv[u][2]) * sb[0], bf16_hi(xv[u][2]) * sb[1]);
+        o[3] = pack_bf16x2(bf16_lo(xv[u][3]) * sb[2], bf16_hi(xv[u][3]) * sb[3]);
+        *reinterpret_cast<u32x4*>(scaled + m * Kd + k) = o;
+      }
+      const u32x4 xm = m < M ? xv[u] : u32x4{0, 0, 0, 0};
+#pragma unroll
+      for (int t = 0; t < RT; ++t) {
+        const int j = t * 32 + l32;
+        u32x4 pv = {0, 0, 0, 0};
+        if (j < r) pv = *reinterpret_cast<const u32x4*>(P + (int64_t)j * Kd + k);
+        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(xm), as_bf16x8(pv), acc[t], 0, 0, 0);
+      }
+    }
+  }
+  for (; st < s1; ++st) {
+    const int64_t k = st * 16 + lhi * 8;
+    u32x4 xv = *reinterpret_cast<const u32x4*>(srow + st * 16);
+    if (SCALED && m < M) {
+      f32x4 sa = *reinterpret_cast<const f32x4*>(s + k);
+      f32x4 sb = *reinterpret_cast<const f32x4*>(s + k + 4);
+      u32x4 o;
+      o[0] = pack_bf16x2(bf16_lo(xv[0]) * sa[0], bf16_hi(xv[0]) * sa[1]);
+      o[1] = pack_bf16x2(bf16_lo(xv[1]) * sa[2], bf16_hi(xv[1]) * sa[3]);
+      o[2] = pack_bf16x2(bf16_lo(xv[2]) * sb[0], bf16_hi(xv[2]) * sb[1]);
+      o[3] = pack_bf16x2(bf16_lo(xv[3]) * sb[2], bf16_hi(xv[3]) * sb[3]);
+      *reinterpret_cast<u32x4*>(scaled + m * Kd + k) = o;
+    }
+    if (m >= M) xv = u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+      const int j = t * 32 + l32;
+      u32x4 pv = {0, 0, 0, 0};
+      if (j < r) pv = *reinterpret_cast<const u32x4*>(P + (int64_t)j * Kd + k);
+      acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(xv), as_bf16x8(pv), acc[t], 0, 0, 0);
+    }
+  }
+  // D lane layout: row (token) = (v/4)*8 + lhi*4 + v%4, column (j) = t*32 + l32.
+  // Sum the four wave partials in wave order (deterministic), one wave at a time.
+  for (int w = 0; w < 4; ++w) {
+    if (wave == w) {
+#pragma unroll
+      for (int t = 0; t < RT; ++t)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) red[t][v][lane] = (w == 0 ? 0.0f : red[t][v][lane]) + acc[t][v];
+    }
+    __syncthreads();
+  }
+  if (out == nullptr) return;
+  // 256 threads finalise 32 rows x (32*RT) columns
+  for (int idx = threadIdx.x; idx < 32 * 32 * RT; idx += 256) {
+    const int t = idx / 1024, rem = idx % 1024;
+    const int row = rem / 32, col = rem % 32;  // row = token within block, col = j within tile
+    const int v = (row / 8) * 4 + (row % 4), ln = ((row / 4) & 1) * 32 + col;
+    const float sum = red[t][v][ln];
+    const int64_t mm = (int64_t)blockIdx.x * 32 + row;
+    const int j = t * 32 + col;
+    if (mm < M && j < rp) out[mm * rp + j] = j < r ? (uint16_t)f32_to_bf16_bits(sum) : (uint16_t)0;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// colgrad partials: part[sp][o][j] = sum over this split's tokens of src[m][o] * Lm[m][j]
+// (o < Od output index, j < rp). D = src^T Lm on MFMA; both operands need 8 consecutive tokens
+// per lane, read transposed out of row-major LDS tiles with ds_read_b64_tr_b16 (lane i of a
+// 16-lane group receives element i%4 of the 4 elements addressed by lane 4j + i/4, j = 0..3).
+namespace cg {
+constexpr int BO = 128;           // output rows (o) per block: 4 waves x 32
+constexpr int TM = 64;            // tokens per step
+constexpr int SROW = BO + 16;     // padded LDS row (elements)
+constexpr int LROW = 128 + 16;    // Lm tile row (rp <= 128)
+}  // namespace cg
+
+template <int RT>
+__global__ __launch_bounds__(256) void colgrad_kernel(const uint16_t* __restrict__ src, int64_t M,
+                                                      int64_t Od, const uint16_t* __restrict__ Lm,
+                                                      int rp, int64_t tokens_per_split,
+                                                      float* __restrict__ part) {
+  using namespace cg;
+  __shared__ __attribute__((aligned(16))) uint16_t ssrc[TM * SROW];
+  __shared__ __attribute__((aligned(16))) uint16_t slm[TM * LROW];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t o0 = (int64_t)blockIdx.x * BO;
+  const int sp = blockIdx.y;
+  const int64_t mbeg = (int64_t)sp * tokens_per_split;
+  const int64_t mend = (mbeg + tokens_per_split < M) ? mbeg + tokens_per_split : M;
+  f32x16 acc[RT];
+#pragma unroll
+  for (int t = 0; t < RT; ++t)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[t][v] = 0.0f;
+
+  const int g = lane >> 4, i16 = lane & 15;
+  const int jj = i16 >> 2, qq = i16 & 3;  // providing-lane roles for the transpose reads
+  for (int64_t mb = mbeg; mb < mend; mb += TM) {
+    // src tile [64 tokens][128 o]: 1024 chunks of 8 bf16, 4 per thread
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int id = tid + 256 * i, row = id >> 4, c = id & 15;
+      const int64_t m = mb + row, o = o0 + c * 8;
+      u32x4 v = {0, 0, 0, 0};
+      if (m < mend && o < Od) v = *reinterpret_cast<const u32x4*>(src + m * Od + o);
+      *reinterpret_cast<u32x4*>(&ssrc[row * SROW + c * 8]) = v;
+    }
+    // Lm tile [64 tokens][32*RT]
+    for (int id = tid; id < TM * RT * 4; id += 256) {
+      const int row = id / (RT * 4), c = id % (RT * 4);
+      const int64_t m = mb + row;
+      u32x4 v = {0, 0, 0, 0};
+      if (m < mend && c * 8 < rp) v = *reinterpret_cast<const u32x4*>(Lm + m * rp + c * 8);
+      *reinterpret_cast<u32x4*>(&slm[row * LROW + c * 8]) = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < TM / 16; ++ks) {
+      // A operand: src^T rows o = wave*32 + (0..31), tokens ks*16 + (lane/32)*8 + (0..7)
+      u32x4 av;
+      {
+        const int rowb = ks * 16 + (g >> 1) * 8 + jj;
+        const int col = wave * 32 + 16 * (g & 1) + 4 * qq;
+        i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(i16x4, &ssrc[rowb * SROW + col]));
+        i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(i16x4, &ssrc[(rowb + 4) * SROW + col]));
+        av[0] = (uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16);
+        av[1] = (uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16);
+        av[2] = (uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16);
+        av[3] = (uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16);
+      }
+#pragma unroll
+      for (int t = 0; t < RT; ++t) {
+        u32x4 bv;
+        const int rowb = ks * 16 + (g >> 1) * 8 + jj;
+        const int col = t * 32 + 16 * (g & 1) + 4 * qq;
+        i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(i16x4, &slm[rowb * LROW + col]));
+        i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(i16x4, &slm[(rowb + 4) * LROW + col]));
+        bv[0] = (uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16);
+        bv[1] = (uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16);
+        bv[2] = (uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16);
+        bv[3] = (uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16);
+        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(av), as_bf16x8(bv), acc[t], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+  // D lane layout: row (o) = wave*32 + (v/4)*8 + (lane/32)*4 + v%4, column j = t*32 + lane%32
+  const int l32 = lane & 31, lhi = lane >> 5;
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    const int j = t * 32 + l32;
+    if (j >= rp) continue;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int64_t o = o0 + wave * 32 + (v / 4) * 8 + lhi * 4 + (v % 4);
+      if (o < Od) part[((int64_t)sp * Od + o) * rp + j] = acc[t][v];
+    }
+  }
+}
+
+// out = c * sum_sp part[sp][o][j] in split order; TRANS: out[j][o] (dB [r][N]) else out[o][j]
+template <bool TRANS>
+__global__ void reduce_partials_kernel(const float* __restrict__ part, int splits, int64_t Od,
+                                       int rp, int r, float c, float* __restrict__ out) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= Od * r) return;
+  int64_t o, j;
+  if (TRANS) { j = idx / Od; o = idx % Od; } else { o = idx / r; j = idx % r; }
+  float sum = 0.0f;
+  for (int sp = 0; sp < splits; ++sp) sum += part[((int64_t)sp * Od + o) * rp + j];
+  out[idx] = c * sum;
+}
+
+__global__ void fill_f32_kernel(float* p, int64_t n, float v) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+// ---------------------------------------------------------------------------------------------
+// generic kernels (any shape / alignment)
+// out[m][j] = bf16(sum_k src[m*Kd + k] * P[k*ps_k + j*ps_j]) (j < r), row stride ld_out
+__global__ void g_rowproj_kernel(const uint16_t* __restrict__ src, int64_t M, int64_t Kd,
+                                 const uint16_t* __restrict__ P, int64_t ps_k, int64_t ps_j, int r,
+                                 uint16_t* __restrict__ out, int64_t ld_out) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= M * r) return;
+  const int64_t m = idx / r, j = idx % r;
+  float acc = 0.0f;
+  for (int64_t k = 0; k < Kd; ++k) acc += bf16_to_f32(src[m * Kd + k]) * bf16_to_f32(P[k * ps_k + j * ps_j]);
+  out[m * ld_out + j] = (uint16_t)f32_to_bf16_bits(acc);
+}
+
+__global__ void g_fwd_kernel(const uint16_t* __restrict__ x, const int8_t* __restrict__ q,
+                             const float* __restrict__ s, const uint16_t* __restrict__ h,
+                             int64_t ldh, const uint16_t* __restrict__ B,
+                             const uint16_t* __restrict__ bias, int64_t M, int64_t K, int64_t N,
+                             int r, float c, uint16_t* __restrict__ y) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= M * N) return;
+  const int64_t m = idx / N, n = idx % N;
+  float acc = 0.0f;
+  for (int64_t k = 0; k < K; ++k) acc += bf16_to_f32(x[m * K + k]) * (float)q[n * K + k];
+  float lo = 0.0f;
+  for (int j = 0; j < r; ++j) lo += bf16_to_f32(h[m * ldh + j]) * bf16_to_f32(B[(int64_t)j * N + n]);
+  float o = s[n] * acc + c * lo + (bias ? bf16_to_f32(bias[n]) : 0.0f);
+  y[idx] = (uint16_t)f32_to_bf16_bits(o);
+}
+
+__global__ void g_dx_kernel(const uint16_t* __restrict__ dy, const int8_t* __restrict__ q,
+                            const float* __restrict__ s, const uint16_t* __restrict__ u,
+                            int64_t ldu, const uint16_t* __restrict__ A, int64_t M, int64_t K,
+                            int64_t N, int r, float c, uint16_t* __restrict__ dx) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= M * K) return;
+  const int64_t m = idx / K, k = idx % K;
+  float acc = 0.0f;
+  for (int64_t n = 0; n < N; ++n) {
+    const float dys = bf16_to_f32((uint16_t)f32_to_bf16_bits(bf16_to_f32(dy[m * N + n]) * s[n]));
+    acc += dys * (float)q[n * K + k];
+  }
+  float lo = 0.0f;
+  for (int j = 0; j < r; ++j) lo += bf16_to_f32(u[m * ldu + j]) * bf16_to_f32(A[k * r + j]);
+  dx[idx] = (uint16_t)f32_to_bf16_bits(acc + c * lo);
+}
+
+// out[o][j] (or [j][o] when TRANS) = c * sum_m src[m][o] * Lm[m][j]
+template <bool TRANS>
+__global__ void g_colgrad_kernel(const uint16_t* __restrict__ src, int64_t M, int64_t Od,
+                                 const uint16_t* __restrict__ Lm, int64_t ldl, int r, float c,
+                                 float* __restrict__ out) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= Od * r) return;
+  int64_t o, j;
+  if (TRANS) { j = idx / Od; o = idx % Od; } else { o = idx / r; j = idx % r; }
+  float acc = 0.0f;
+  for (int64_t m = 0; m < M; ++m) acc += bf16_to_f32(src[m * Od + o]) * bf16_to_f32(Lm[m * ldl + j]);
+  out[idx] = c * acc;
+}
+
+// ---------------------------------------------------------------------------------------------
+// gelu_tanh, src/layers/linear.jl:61-68 (f32 math, bf16 in/out)
+__device__ __forceinline__ float gelu_f(float x) {
+  const float k = 0.7978845608028654f;  // sqrt(Float32(2 / pi))
+  const float inner = x + 0.044715f * (x * x * x);
+  return 0.5f * x * (1.0f + tanhf(k * inner));
+}
+__device__ __forceinline__ float gelu_grad_f(float x) {
+  const float k = 0.7978845608028654f, a = 0.044715f;
+  const float t = tanhf(k * (x + a * x * x * x));
+  return 0.5f * (1.0f + t) + 0.5f * x * (1.0f - t * t) * k * (1.0f + 3.0f * a * x * x);
+}
+__global__ void gelu_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ y, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = (uint16_t)f32_to_bf16_bits(gelu_f(bf16_to_f32(x[i])));
+}
+__global__ void gelu_bwd_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ dy,
+                                uint16_t* __restrict__ dx, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) dx[i] = (uint16_t)f32_to_bf16_bits(bf16_to_f32(dy[i]) * gelu_grad_f(bf16_to_f32(x[i])));
+}
+
+// ---------------------------------------------------------------------------------------------
+// host side
+struct Plan {
+  bool fast;
+  int rp;       // row stride of h/u buffers
+  int splits;   // split-M count for dA/dB
+  int64_t tps;  // tokens per split (multiple of 64)
+};
+
+static Plan make_plan(int64_t M, int64_t K, int64_t N, int64_t r, bool ptrs_aligned) {
+  Plan p;
+  p.fast = ptrs_aligned && (K % 16 == 0) && (N % 16 == 0) && (r % 16 == 0) && r <= 128;
+  p.rp = (int)r;
+  int64_t s = (M + 2047) / 2048;
+  if (s < 1) s = 1;
+  if (s > 16) s = 16;
+  p.tps = ((M + s - 1) / s + 63) / 64 * 64;
+  if (p.tps < 64) p.tps = 64;
+  p.splits = (int)((M + p.tps - 1) / p.tps);
+  if (p.splits < 1) p.splits = 1;
+  return p;
+}
+
+// workspace layout (byte offsets, 256-aligned); identical computation for sizing and use
+struct WsLayout {
+  size_t h, u, dys, at, bt, pa, pb, total;
+};
+
+static WsLayout ws_layout(int64_t M, int64_t K, int64_t N, int64_t r, int which, const Plan& p) {
+  WsLayout w{};
+  size_t off = 0;
+  auto take = [&](size_t bytes) { size_t o = off; off = align_up(off + bytes, 256); return o; };
+  const size_t rp = (size_t)p.rp;
+  w.h = take((size_t)M * rp * 2);
+  w.at = take(r > 0 ? (size_t)r * K * 2 : 0);
+  if (which == REELS_HIP_WS_FWD) {
+    w.bt = take(p.fast ? (size_t)N * rp * 2 : 0);
+  } else {
+    w.u = take((size_t)M * rp * 2);
+    w.dys = take(p.fast ? (size_t)M * N * 2 : 0);
+    w.pa = take(p.fast && r > 0 ? (size_t)p.splits * K * rp * 4 : 0);
+    w.pb = take(p.fast && r > 0 ? (size_t)p.splits * N * rp * 4 : 0);
+  }
+  w.total = off == 0 ? 256 : off;
+  return w;
+}
+
+static int grid1(int64_t n, int bs = 256) { return (int)ceil_div(n, bs); }
+
+static int launch_rowproj(const uint16_t* src, int64_t M, int64_t Kd, const uint16_t* P, int r,
+                          int rp, uint16_t* out, const float* s, uint16_t* scaled, hipStream_t st) {
+  const dim3 grid((unsigned)ceil_div(M, 32));
+  const int rt = (r + 31) / 32;
+  if (scaled) {
+    if (rt <= 1) { TraceScope _ts(st, "rowproj_kernel<1,true>"); rowproj_kernel<1, true><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, s, scaled); }
+    else if (rt == 2) { TraceScope _ts(st, "rowproj_kernel<2,true>"); rowproj_kernel<2, true><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, s, scaled); }
+    else { TraceScope _ts(st, "rowproj_kernel<4,true>"); rowproj_kernel<4, true><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, s, scaled); }
+  } else {
+    if (rt <= 1) { TraceScope _ts(st, "rowproj_kernel<1,false>"); rowproj_kernel<1, false><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, s, scaled); }
+    else if (rt == 2) { TraceScope _ts(st, "rowproj_kernel<2,false>"); rowproj_kernel<2, false><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, s, scaled); }
+    else { TraceScope _ts(st, "rowproj_kernel<4,false>"); rowproj_kernel<4, false><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, s, scaled); }
+  }
+  return check_launch("rowproj_kernel");
+}
+
+static int launch_colgrad(const uint16_t* src, int64_t M, int64_t Od, const uint16_t* Lm, int r,
+                          int rp, const Plan& p, float c, float* part, float* out, bool trans,
+                          hipStream_t st) {
+  const dim3 grid((unsigned)ceil_div(Od, cg::BO), (unsigned)p.splits);
+  const int rt = (rp + 31) / 32;
+  if (rt <= 1) { TraceScope _ts(st, "colgrad_kernel<1>"); colgrad_kernel<1><<<grid, 256, 0, st>>>(src, M, Od, Lm, rp, p.tps, part); }
+  else if (rt == 2) { TraceScope _ts(st, "colgrad_kernel<2>"); colgrad_kernel<2><<<grid, 256, 0, st>>>(src, M, Od, Lm, rp, p.tps, part); }
+  else { TraceScope _ts(st, "colgrad_kernel<4>"); colgrad_kernel<4><<<grid, 256, 0, st>>>(src, M, Od, Lm, rp, p.tps, part); }
+  int rc = check_launch("colgrad_kernel");
+  if (rc) return rc;
+  if (trans) { TraceScope _ts(st, "reduce_partials_kernel<true>"); reduce_partials_kernel<true><<<grid1(Od * r), 256, 0, st>>>(part, p.splits, Od, rp, r, c, out); }
+  else { TraceScope _ts(st, "reduce_partials_kernel<false>"); reduce_partials_kernel<false><<<grid1(Od * r), 256, 0, st>>>(part, p.splits, Od, rp, r, c, out); }
+  return check_launch("reduce_partials_kernel");
+}
+
+}  // namespace reels
+
+using namespace reels;
+
+extern "C" size_t reels_hip_i8lora_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t r,
+                                                   int which) {
+  if (M < 0 || K < 0 || N < 0 || r < 0) return 0;
+  // sized for the fast layout when the shape allows it (pointer alignment cannot be known here;
+  // the fast layout is never smaller than the generic one)
+  Plan p = make_plan(M, K, N, r, true);
+  return ws_layout(M, K, N, r, which, p).total;
+}
+
+static bool all_aligned(std::initializer_list<const void*> ps) {
+  for (const void* p : ps)
+    if (p != nullptr && !aligned16(p)) return false;
+  return true;
+}
+
+extern "C" int reels_hip_i8lora_fwd(const void* x, const int8_t* q, const float* scales,
+                                    const void* A, const void* B, const void* bias, int64_t M,
+                                    int64_t K, int64_t N, int64_t r, float lora_scale, void* y,
+                                    void* h_save, void* workspace, size_t ws_bytes, void* stream) {
+  clear_error();
+  if (M < 0 || K <= 0 || N <= 0 || r < 0 || r > 4096)
+    return fail(REELS_HIP_EINVAL, "reels_hip_i8lora_fwd: need M >= 0, K > 0, N > 0, 0 <= r <= 4096");
+  if (!(lora_scale == lora_scale))
+    return fail(REELS_HIP_EINVAL, "reels_hip_i8lora_fwd: lora_scale is NaN");
+  if (M == 0) return REELS_HIP_OK;
+  if (!x || !q || !scales || !y || (r > 0 && (!A || !B)))
+    return fail(REELS_HIP_EINVAL, "reels_hip_i8lora_fwd: NULL x, q, scales, y, or A/B with r > 0");
+  const bool al = all_aligned({x, q, scales, A, B, y, h_save}) &&
+                  (bias == nullptr || (reinterpret_cast<uintptr_t>(bias) & 7u) == 0);
+  Plan p = make_plan(M, K, N, r, al);
+  WsLayout w = ws_layout(M, K, N, r, REELS_HIP_WS_FWD, p);
+  if (workspace == nullptr || ws_bytes < w.total)
+    return fail(REELS_HIP_EWORKSPACE, "reels_hip_i8lora_fwd: workspace NULL or smaller than "
+                                      "reels_hip_i8lora_workspace_bytes(..., REELS_HIP_WS_FWD)");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  const uint16_t* xb = static_cast<const uint16_t*>(x);
+  uint16_t* h = r > 0 ? (h_save ? static_cast<uint16_t*>(h_save) : reinterpret_cast<uint16_t*>(ws + w.h)) : nullptr;
+  int rc;
+  if (!p.fast) {
+    if (r > 0) {
+      { TraceScope _ts(st, "g_rowproj_kernel"); g_rowproj_kernel<<<grid1(M * r), 256, 0, st>>>(xb, M, K, static_cast<const uint16_t*>(A), r, 1,
+                                                    (int)r, h, r); }
+      if ((rc = check_launch("g_rowproj_kernel"))) return rc;
+    }
+    { TraceScope _ts(st, "g_fwd_kernel"); g_fwd_kernel<<<grid1(M * N), 256, 0, st>>>(xb, q, scales, h, r, static_cast<const uint16_t*>(B),
+                                              static_cast<const uint16_t*>(bias), M, K, N, (int)r,
+                                              lora_scale, static_cast<uint16_t*>(y)); }
+    return check_launch("g_fwd_kernel");
+  }
+  uint16_t* bt = nullptr;
+  if (r > 0) {
+    uint16_t* at = reinterpret_cast<uint16_t*>(ws + w.at);
+    bt = reinterpret_cast<uint16_t*>(ws + w.bt);
+    // At [r][K] from A [K][r]; Bt [N][rp] from B [r][N]
+    { TraceScope _ts(st, "transpose_pad_kernel"); transpose_pad_kernel<<<dim3((unsigned)ceil_div(r, 32), (unsigned)ceil_div(K, 32)), 256, 0, st>>>(
+        static_cast<const uint16_t*>(A), K, r, K, at); }
+    if ((rc = check_launch("transpose_pad_kernel"))) return rc;
+    { TraceScope _ts(st, "transpose_pad_kernel"); transpose_pad_kernel<<<dim3((unsigned)ceil_div(N, 32), (unsigned)ceil_div(r, 32)), 256, 0, st>>>(
+        static_cast<const uint16_t*>(B), r, N, p.rp, bt); }
+    if ((rc = check_launch("transpose_pad_kernel"))) return rc;
+    if ((rc = launch_rowproj(xb, M, K, at, (int)r, p.rp, h, nullptr, nullptr, st))) return rc;
+  }
+  GemmArgs g{};
+  g.act = xb; g.q = q; g.colscale = scales; g.L = h; g.R = bt;
+  g.bias = static_cast<const uint16_t*>(bias); g.out = static_cast<uint16_t*>(y);
+  g.M = M; g.Ncols = N; g.Kred = K; g.ldq = K; g.rp = r > 0 ? p.rp : 0; g.c = lora_scale;
+  return launch_i8gemm(0, g, st);
+}
+
+extern "C" int reels_hip_i8lora_bwd(const void* dy, const void* x, const void* h, const int8_t* q,
+                                    const float* scales, const void* A, const void* B, int64_t M,
+                                    int64_t K, int64_t N, int64_t r, float lora_scale, void* dx,
+                                    float* dA, float* dB, void* workspace, size_t ws_bytes,
+                                    void* stream) {
+  clear_error();
+  if (M < 0 || K <= 0 || N <= 0 || r < 0 || r > 4096)
+    return fail(REELS_HIP_EINVAL, "reels_hip_i8lora_bwd: need M >= 0, K > 0, N > 0, 0 <= r <= 4096");
+  if (!(lora_scale == lora_scale))
+    return fail(REELS_HIP_EINVAL, "reels_hip_i8lora_bwd: lora_scale is NaN");
+  if (r == 0) { dA = nullptr; dB = nullptr; }
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  int rc;
+  if (M == 0) {  // empty token set: the reductions over tokens are zero
+    if (dA) {
+      { TraceScope _ts(st, "fill_f32_kernel"); fill_f32_kernel<<<grid1(K * r), 256, 0, st>>>(dA, K * r, 0.0f); }
+      if ((rc = check_launch("fill_f32_kernel"))) return rc;
+    }
+    if (dB) {
+      { TraceScope _ts(st, "fill_f32_kernel"); fill_f32_kernel<<<grid1(N * r), 256, 0, st>>>(dB, N * r, 0.0f); }
+      if ((rc = check_launch("fill_f32_kernel"))) return rc;
+    }
+    return REELS_HIP_OK;
+  }
+  if (!dy || !q || !scales || (r > 0 && (!A || !B)) || ((dA || (dB && !h)) && !x))
+    return fail(REELS_HIP_EINVAL, "reels_hip_i8lora_bwd: NULL dy, q, scales, A/B with r > 0, or x "
+                                  "needed for dA / recomputing h");
+  if (!dx && !dA && !dB) return REELS_HIP_OK;
+  const bool al = all_aligned({dy, x, h, q, scales, A, B, dx, dA, dB});
+  Plan p = make_plan(M, K, N, r, al);
+  WsLayout w = ws_layout(M, K, N, r, REELS_HIP_WS_BWD, p);
+  if (workspace == nullptr || ws_bytes < w.total)
+    return fail(REELS_HIP_EWORKSPACE, "reels_hip_i8lora_bwd: workspace NULL or smaller than "
+                                      "reels_hip_i8lora_workspace_bytes(..., REELS_HIP_WS_BWD)");
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  const uint16_t* dyb = static_cast<const uint16_t*>(dy);
+  const uint16_t* xb = static_cast<const uint16_t*>(x);
+  const uint16_t* Ab = static_cast<const uint16_t*>(A);
+  const uint16_t* Bb = static_cast<const uint16_t*>(B);
+  uint16_t* u = reinterpret_cast<uint16_t*>(ws + w.u);
+  const uint16_t* hh = static_cast<const uint16_t*>(h);
+  const bool need_h = (dB != nullptr) && r > 0;
+
+  if (!p.fast) {
+    if (r > 0 && (dx || dA)) {
+      { TraceScope _ts(st, "g_rowproj_kernel"); g_rowproj_kernel<<<grid1(M * r), 256, 0, st>>>(dyb, M, N, Bb, 1, N, (int)r, u, r); }
+      if ((rc = check_launch("g_rowproj_kernel"))) return rc;
+    }
+    if (need_h && !hh) {
+      uint16_t* hw = reinterpret_cast<uint16_t*>(ws + w.h);
+      { TraceScope _ts(st, "g_rowproj_kernel"); g_rowproj_kernel<<<grid1(M * r), 256, 0, st>>>(xb, M, K, Ab, r, 1, (int)r, hw, r); }
+      if ((rc = check_launch("g_rowproj_kernel"))) return rc;
+      hh = hw;
+    }
+    if (dx) {
+      { TraceScope _ts(st, "g_dx_kernel"); g_dx_kernel<<<grid1(M * K), 256, 0, st>>>(dyb, q, scales, u, r, Ab, M, K, N, (int)r, lora_scale,
+                                               static_cast<uint16_t*>(dx)); }
+      if ((rc = check_launch("g_dx_kernel"))) return rc;
+    }
+    if (dA) {
+      { TraceScope _ts(st, "g_colgrad_kernel<false>"); g_colgrad_kernel<false><<<grid1(K * r), 256, 0, st>>>(xb, M, K, u, r, (int)r, lora_scale, dA); }
+      if ((rc = check_launch("g_colgrad_kernel"))) return rc;
+    }
+    if (dB) {
+      { TraceScope _ts(st, "g_colgrad_kernel<true>"); g_colgrad_kernel<true><<<grid1(N * r), 256, 0, st>>>(dyb, M, N, hh, r, (int)r, lora_scale, dB); }
+      if ((rc = check_launch("g_colgrad_kernel"))) return rc;
+    }
+    return REELS_HIP_OK;
+  }
+
+  uint16_t* dys = reinterpret_cast<uint16_t*>(ws + w.dys);
+  // 1. u = dy B^T and dys = dy * s in one pass over dy (the scaled copy only when dx is wanted)
+  if (r > 0 || dx) {
+    if (r > 0) {
+      if ((rc = launch_rowproj(dyb, M, N, Bb, (int)r, p.rp, u, scales, dx ? dys : nullptr, st))) return rc;
+    } else {
+      // r = 0: only the scaled copy is needed (no projection output)
+      if ((rc = launch_rowproj(dyb, M, N, Bb, 0, 0, nullptr, scales, dys, st))) return rc;
+    }
+  }
+  // 2. dx = dys q + c u A^T
+  if (dx) {
+    GemmArgs g{};
+    g.act = dys; g.q = q; g.colscale = nullptr; g.L = r > 0 ? u : nullptr; g.R = Ab; g.bias = nullptr;
+    g.out = static_cast<uint16_t*>(dx);
+    g.M = M; g.Ncols = K; g.Kred = N; g.ldq = K; g.rp = r > 0 ? p.rp : 0; g.c = lora_scale;
+    if ((rc = launch_i8gemm(1, g, st))) return rc;
+  }
+  // 3. dA = c x^T u ; dB = c (dy^T h)^T
+  if (dA) {
+    if ((rc = launch_colgrad(xb, M, K, u, (int)r, p.rp, p, lora_scale,
+                             reinterpret_cast<float*>(ws + w.pa), dA, false, st))) return rc;
+  }
+  if (dB) {
+    if (!hh) {
+      uint16_t* at = reinterpret_cast<uint16_t*>(ws + w.at);
+      uint16_t* hw = reinterpret_cast<uint16_t*>(ws + w.h);
+      { TraceScope _ts(st, "transpose_pad_kernel"); transpose_pad_kernel<<<dim3((unsigned)ceil_div(r, 32), (unsigned)ceil_div(K, 32)), 256, 0, st>>>(
+          Ab, K, r, K, at); }
+      if ((rc = check_launch("transpose_pad_kernel"))) return rc;
+      if ((rc = launch_rowproj(xb, M, K, at, (int)r, p.rp, hw, nullptr, nullptr, st))) return rc;
+      hh = hw;
+    }
+    if ((rc = launch_colgrad(dyb, M, N, hh, (int)r, p.rp, p, lora_scale,
+                             reinterpret_cast<float*>(ws + w.pb), dB, true, st))) return rc;
+  }
+  return REELS_HIP_OK;
+}
+
+extern "C" int reels_hip_gelu_tanh(const void* x, void* y, int64_t n, void* stream) {
+  clear_error();
+  if (n < 0) return fail(REELS_HIP_EINVAL, "reels_hip_gelu_tanh: n < 0");
+  if (n == 0) return REELS_HIP_OK;
+  if (!x || !y) return fail(REELS_HIP_EINVAL, "reels_hip_gelu_tanh: NULL pointer");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  { TraceScope _ts(st, "gelu_kernel");
+    gelu_kernel<<<grid1(n), 256, 0, st>>>(static_cast<const uint16_t*>(x), static_cast<uint16_t*>(y), n); }
+  return check_launch("gelu_kernel");
+}
+
+extern "C" int reels_hip_gelu_tanh_bwd(const void* x, const void* dy, void* dx, int64_t n, void* stream) {
+  clear_error();
+  if (n < 0) return fail(REELS_HIP_EINVAL, "reels_hip_gelu_tanh_bwd: n < 0");
+  if (n == 0) return REELS_HIP_OK;
+  if (!x || !dy || !dx) return fail(REELS_HIP_EINVAL, "reels_hip_gelu_tanh_bwd: NULL pointer");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  { TraceScope _ts(st, "gelu_bwd_kernel");
+    gelu_bwd_kernel<<<grid1(n), 256, 0, st>>>(static_cast<const uint16_t*>(x),
+                                              static_cast<const uint16_t*>(dy),
+                                              static_cast<uint16_t*>(dx), n); }
+  return check_launch("gelu_bwd_kernel");
+}

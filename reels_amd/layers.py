@@ -1,0 +1,384 @@
+"""Host-side mirror of Reels.jl's int8 frozen-weight layer API over the HIP C ABI.
+
+Names, argument meaning and error behaviour follow src/layers/quantization.jl,
+src/layers/lora.jl and src/layers/linear.jl. Arrays are torch tensors holding the same memory the
+reference's column-major Julia arrays hold: a Julia matrix of size (a, b) is a torch tensor of
+shape (b, a). So Julia x::(K, M) is x[M][K]; LoRA A::(r, K) is A[K][r]; B::(N, r) is B[r][N];
+QuantizedMatrix.values (logically (N, K)) is stored [N][K] (K contiguous), the layout of the
+SafeTensors I8 format (src/checkpoints/safetensors.jl:52-58).
+
+Every compute call runs the HIP kernels; there is no PyTorch or CPU fallback. Device tensors must
+live on a ROCm device; CPU tensors raise.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+_DTYPE_CODE = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _need_device(t: torch.Tensor, name: str) -> None:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a ROCm device tensor (got {t.device}); the int8 path "
+                         "runs only on the GPU")
+
+
+def _contig(t: Optional[torch.Tensor], dtype: torch.dtype, name: str) -> Optional[torch.Tensor]:
+    if t is None:
+        return None
+    _need_device(t, name)
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    return t.contiguous()
+
+
+# ---- storage ---------------------------------------------------------------------------------
+@dataclass
+class QuantizedMatrix:
+    """Per-output-channel symmetric int8 storage of a frozen weight (quantization.jl:5-9).
+
+    values: int8 [N][K]; scales: float32 [N]; compute_dtype: the dtype produced when the weight
+    is materialised (the reference's type parameter T)."""
+
+    values: torch.Tensor
+    scales: torch.Tensor
+    compute_dtype: torch.dtype = torch.bfloat16
+
+    @property
+    def shape(self):  # Base.size (quantization.jl:16): (out, in)
+        return tuple(self.values.shape)
+
+    def size(self, dim=None):
+        return self.shape if dim is None else self.shape[dim]
+
+    def dequantize(self, dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+        """_host_dequantize (quantization.jl:25-29): cast(T, Float32(q) * s). A debugging and
+        merged-weight helper; the forward and backward never materialise it."""
+        d = dtype or self.compute_dtype
+        return (self.values.float() * self.scales[:, None]).to(d)
+
+
+def quantize_frozen_matrix(weight: torch.Tensor, T: Optional[torch.dtype] = None,
+                           stream=None) -> QuantizedMatrix:
+    """quantize_frozen_matrix (quantization.jl:35-44) on the GPU, bit-exact.
+
+    weight: [N][K] float32 / bfloat16 / float16 device tensor (rows = output channels).
+    Raises ValueError (the reference's InexactError from Int8(NaN)) on non-finite weights."""
+    _need_device(weight, "weight")
+    if weight.dim() != 2:
+        raise ValueError("weight must be a matrix")
+    if weight.dtype not in _DTYPE_CODE:
+        raise TypeError(f"unsupported weight dtype {weight.dtype}")
+    if weight.stride(1) != 1:
+        weight = weight.contiguous()
+    N, K = weight.shape
+    values = torch.empty((N, K), dtype=torch.int8, device=weight.device)
+    scales = torch.empty((N,), dtype=torch.float32, device=weight.device)
+    status = torch.empty((1,), dtype=torch.int32, device=weight.device)
+    st = _stream(weight.device) if stream is None else stream
+    _lib.check("reels_hip_i8_pack", _lib.lib().reels_hip_i8_pack(
+        _ptr(weight), _DTYPE_CODE[weight.dtype], N, K, weight.stride(0), _ptr(values),
+        _ptr(scales), _ptr(status), st))
+    if int(status.item()) != 0:
+        raise ValueError("InexactError: Int8(NaN) — weight contains non-finite values")
+    return QuantizedMatrix(values, scales, T or (weight.dtype if weight.dtype != torch.float32
+                                                 else torch.bfloat16))
+
+
+# ---- raw entry points -------------------------------------------------------------------------
+def workspace_bytes(M: int, K: int, N: int, r: int, which: int) -> int:
+    return int(_lib.lib().reels_hip_i8lora_workspace_bytes(M, K, N, r, which))
+
+
+def i8lora_forward(x, weight: QuantizedMatrix, A=None, B=None, bias=None, lora_scale=1.0,
+                   save_h: bool = False):
+    """y = bf16(x deq(Wq)^T + lora_scale * bf16(x A) B + bias); returns (y, h or None).
+
+    x [M][K] bf16; A [K][r], B [r][N] bf16 (Julia A::(r,K), B::(N,r)); bias [N] bf16."""
+    x = _contig(x, torch.bfloat16, "x")
+    M, K = x.shape
+    N, Kw = weight.values.shape
+    if Kw != K:
+        raise ValueError("DimensionMismatch: LoRA input and weight dimensions differ")
+    r = 0 if A is None else A.shape[1]
+    A = _contig(A, torch.bfloat16, "A")
+    B = _contig(B, torch.bfloat16, "B")
+    if r and (tuple(A.shape) != (K, r) or tuple(B.shape) != (r, N)):
+        raise ValueError(f"A must be [K][r] = {(K, r)} and B [r][N] = {(r, N)}")
+    bias = _contig(bias, torch.bfloat16, "bias")
+    dev = x.device
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    h = torch.empty((M, r), dtype=torch.bfloat16, device=dev) if (save_h and r) else None
+    nbytes = workspace_bytes(M, K, N, r, _lib.WS_FWD)
+    ws = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
+    _lib.check("reels_hip_i8lora_fwd", _lib.lib().reels_hip_i8lora_fwd(
+        _ptr(x), _ptr(weight.values), _ptr(weight.scales), _ptr(A), _ptr(B), _ptr(bias),
+        M, K, N, r, float(lora_scale), _ptr(y), _ptr(h), _ptr(ws), nbytes, _stream(dev)))
+    return y, h
+
+
+def i8lora_backward(dy, x, weight: QuantizedMatrix, A=None, B=None, lora_scale=1.0, h=None,
+                    want_dx=True, want_dA=True, want_dB=True):
+    """(dx bf16 [M][K], dA f32 [K][r], dB f32 [r][N]) of lora_backward (lora.jl:106-118)."""
+    dy = _contig(dy, torch.bfloat16, "dy")
+    M, N = dy.shape
+    Nw, K = weight.values.shape
+    if Nw != N:
+        raise ValueError("DimensionMismatch: dy and weight output dimensions differ")
+    r = 0 if A is None else A.shape[1]
+    A = _contig(A, torch.bfloat16, "A")
+    B = _contig(B, torch.bfloat16, "B")
+    x = _contig(x, torch.bfloat16, "x") if x is not None else None
+    h = _contig(h, torch.bfloat16, "h")
+    dev = dy.device
+    dx = torch.empty((M, K), dtype=torch.bfloat16, device=dev) if want_dx else None
+    dA = torch.empty((K, r), dtype=torch.float32, device=dev) if (want_dA and r) else None
+    dB = torch.empty((r, N), dtype=torch.float32, device=dev) if (want_dB and r) else None
+    nbytes = workspace_bytes(M, K, N, r, _lib.WS_BWD)
+    ws = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
+    _lib.check("reels_hip_i8lora_bwd", _lib.lib().reels_hip_i8lora_bwd(
+        _ptr(dy), _ptr(x), _ptr(h), _ptr(weight.values), _ptr(weight.scales), _ptr(A), _ptr(B),
+        M, K, N, r, float(lora_scale), _ptr(dx), _ptr(dA), _ptr(dB), _ptr(ws), nbytes,
+        _stream(dev)))
+    return dx, dA, dB
+
+
+# ---- reference-named layer API ----------------------------------------------------------------
+def _weight_mul(weight: QuantizedMatrix, x: torch.Tensor) -> torch.Tensor:
+    """_weight_mul (quantization.jl:73-74): x deq(W)^T without materialising deq(W)."""
+    return i8lora_forward(x, weight)[0]
+
+
+def _weight_transpose_mul(weight: QuantizedMatrix, dy: torch.Tensor) -> torch.Tensor:
+    """_weight_transpose_mul (quantization.jl:75-76): dy deq(W) (the frozen-weight pullback of
+    src/training/ad_rules.jl:70-80)."""
+    return i8lora_backward(dy, None, weight, want_dA=False, want_dB=False)[0]
+
+
+@dataclass
+class DenseLayer:
+    """DenseLayer (linear.jl:1-4) with a QuantizedMatrix weight."""
+
+    weight: QuantizedMatrix
+    bias: Optional[torch.Tensor] = None
+
+    def __call__(self, x):
+        return linear(self, x)
+
+
+def _flatten(x: torch.Tensor, features: int):
+    if x.shape[-1] != features:
+        raise ValueError("DimensionMismatch: input and weight dimensions differ")
+    return x.reshape(-1, features), x.shape[:-1]
+
+
+def linear(layer: DenseLayer, x: torch.Tensor) -> torch.Tensor:
+    """linear(layer, x) (linear.jl:38-46): x deq(W)^T + bias, trailing dims kept."""
+    N, K = layer.weight.shape
+    xf, lead = _flatten(x, K)
+    y, _ = i8lora_forward(xf, layer.weight, bias=layer.bias)
+    return y.reshape(*lead, N)
+
+
+class LoRALinear:
+    """LoRALinear (lora.jl:1-35) over a QuantizedMatrix base weight.
+
+    A: [K][r] (Julia A::(r, K)), B: [r][N] (Julia B::(N, r)), bf16 on the device. The constructor
+    initialises A ~ randn / sqrt(in) and B = 0 like the reference (lora.jl:22-24)."""
+
+    def __init__(self, weight: QuantizedMatrix, rank: int, alpha: Optional[float] = None,
+                 dropout: float = 0.0, bias: Optional[torch.Tensor] = None,
+                 train_bias: bool = False, generator: Optional[torch.Generator] = None,
+                 A: Optional[torch.Tensor] = None, B: Optional[torch.Tensor] = None):
+        if rank <= 0:
+            raise ValueError("rank must be positive")
+        alpha = float(rank if alpha is None else alpha)
+        if not (math.isfinite(alpha) and alpha > 0):
+            raise ValueError("alpha must be finite and positive")
+        if not (0 <= dropout < 1):
+            raise ValueError("dropout must be in [0, 1)")
+        if dropout > 0:
+            raise NotImplementedError("LoRA dropout masks are not part of the int8 HIP path")
+        if train_bias and bias is None:
+            raise ValueError("cannot train a missing linear bias")
+        out, inp = weight.shape
+        dev = weight.values.device
+        if A is None:
+            A = (torch.randn((inp, rank), generator=generator, dtype=torch.float32, device=dev)
+                 * (1.0 / math.sqrt(inp))).to(torch.bfloat16)
+        if B is None:
+            B = torch.zeros((rank, out), dtype=torch.bfloat16, device=dev)
+        self.weight, self.A, self.B = weight, A, B
+        self.alpha, self.dropout = alpha, float(dropout)
+        self.enabled, self.train_bias = True, train_bias
+        self.base_bias = bias
+        self.bias = bias.clone() if (train_bias and bias is not None) else bias
+
+    @property
+    def rank(self) -> int:
+        return self.A.shape[1]
+
+    @property
+    def lora_scale(self) -> float:
+        # layer.alpha / size(layer.A, 1) evaluated in Float32 (lora.jl:89, 111)
+        return float(torch.tensor(self.alpha, dtype=torch.float32) /
+                     torch.tensor(float(self.rank), dtype=torch.float32))
+
+    def __call__(self, x, **kw):
+        return lora_forward(self, x, **kw)
+
+
+def set_adapter_enabled(layer: LoRALinear, enabled: bool) -> LoRALinear:
+    """set_adapter_enabled! (lora.jl:39)."""
+    layer.enabled = bool(enabled)
+    return layer
+
+
+def lora_parameters(layer: LoRALinear):
+    """lora_parameters (lora.jl:37-38)."""
+    p = {"A": layer.A, "B": layer.B}
+    if layer.train_bias:
+        p["bias"] = layer.bias
+    return p
+
+
+def lora_forward(layer: LoRALinear, x: torch.Tensor, training: bool = False,
+                 save_h: bool = False, **_):
+    """lora_forward (lora.jl:56-95): y = x deq(W)^T + bias + (alpha/r) (x A) B, one fused pass.
+
+    x: [..., K] bf16. Returns y [..., N] (and h when save_h)."""
+    N, K = layer.weight.shape
+    xf, lead = _flatten(x, K)
+    active_bias = layer.base_bias if (layer.train_bias and not layer.enabled) else layer.bias
+    if not layer.enabled:
+        y, h = i8lora_forward(xf, layer.weight, bias=active_bias)
+    else:
+        y, h = i8lora_forward(xf, layer.weight, layer.A, layer.B, active_bias,
+                              layer.lora_scale, save_h=save_h)
+    y = y.reshape(*lead, N)
+    return (y, h) if save_h else y
+
+
+def lora_backward(layer: LoRALinear, x: torch.Tensor, dy: torch.Tensor, h=None):
+    """lora_backward (lora.jl:106-118): returns {"dx", "A", "B"} with dA [K][r] and dB [r][N]
+    in float32 (Julia dA::(r, K), dB::(N, r))."""
+    N, K = layer.weight.shape
+    if tuple(x.shape[:-1]) != tuple(dy.shape[:-1]):
+        raise ValueError("DimensionMismatch: LoRA input and output trailing dimensions differ")
+    xf, lead = _flatten(x, K)
+    dyf, _ = _flatten(dy, N)
+    dx, dA, dB = i8lora_backward(dyf, xf, layer.weight, layer.A, layer.B, layer.lora_scale, h=h)
+    return {"dx": dx.reshape(*lead, K), "A": dA, "B": dB}
+
+
+def merged_weight(layer: LoRALinear) -> torch.Tensor:
+    """merged_weight (lora.jl:120-122) as float32 [N][K]: deq(W) + (alpha/r) (A B)^T."""
+    return (layer.weight.dequantize(torch.float32)
+            + layer.lora_scale * (layer.A.float() @ layer.B.float()).t())
+
+
+class I8LoRALinearFunction(torch.autograd.Function):
+    """Autograd rule for lora_forward: the fused analogue of the reference's Zygote pullbacks
+    (src/training/ad_rules.jl:53-80 for the frozen weight, Zygote's own rule for B*(A*z)).
+    Returns no gradient for the frozen weight, like NoTangent()."""
+
+    @staticmethod
+    def forward(ctx, x, A, B, values, scales, bias, lora_scale):
+        weight = QuantizedMatrix(values, scales)
+        y, h = i8lora_forward(x, weight, A, B, bias, lora_scale, save_h=True)
+        ctx.save_for_backward(x, A, B, values, scales, h)
+        ctx.lora_scale = lora_scale
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, A, B, values, scales, h = ctx.saved_tensors
+        weight = QuantizedMatrix(values, scales)
+        dx, dA, dB = i8lora_backward(dy.contiguous(), x, weight, A, B, ctx.lora_scale, h=h,
+                                     want_dx=ctx.needs_input_grad[0],
+                                     want_dA=ctx.needs_input_grad[1],
+                                     want_dB=ctx.needs_input_grad[2])
+        return (dx, None if dA is None else dA.to(A.dtype),
+                None if dB is None else dB.to(B.dtype), None, None, None, None)
+
+
+def gelu_tanh(x: torch.Tensor) -> torch.Tensor:
+    """gelu_tanh (linear.jl:61-68), bf16 in and out, f32 math."""
+    x = _contig(x, torch.bfloat16, "x")
+    y = torch.empty_like(x)
+    _lib.check("reels_hip_gelu_tanh", _lib.lib().reels_hip_gelu_tanh(
+        _ptr(x), _ptr(y), x.numel(), _stream(x.device)))
+    return y
+
+
+def gelu_tanh_backward(x: torch.Tensor, dy: torch.Tensor) -> torch.Tensor:
+    x = _contig(x, torch.bfloat16, "x")
+    dy = _contig(dy, torch.bfloat16, "dy")
+    dx = torch.empty_like(x)
+    _lib.check("reels_hip_gelu_tanh_bwd", _lib.lib().reels_hip_gelu_tanh_bwd(
+        _ptr(x), _ptr(dy), _ptr(dx), x.numel(), _stream(x.device)))
+    return dx
+
+
+# ---- transfer policy --------------------------------------------------------------------------
+@dataclass
+class FrozenWeightTransfer:
+    """FrozenWeightTransfer (quantization.jl:78-86)."""
+
+    device: str
+    precision: str
+    quantization: str
+    cpu_offload: bool
+
+
+def frozen_weight_transfer(device: str, precision: str, quantization: str = "none",
+                           cpu_offload: bool = False) -> FrozenWeightTransfer:
+    """frozen_weight_transfer (quantization.jl:88-101).
+
+    The reference rejects int8 with bf16 compute because its backward runs through an fp32
+    shadow model; here bf16 is the compute precision of the HIP kernels, so the combination is
+    accepted on the ROCm device. fp16 / fp32 compute with int8 is not implemented by these
+    kernels and raises."""
+    if quantization not in ("none", "int8"):
+        raise ValueError("frozen weight quantization must be none or int8")
+    if device not in ("cpu", "cuda", "hip"):
+        raise ValueError("device must be cpu, cuda or hip")
+    if cpu_offload and device == "cpu":
+        raise ValueError("CPU weight offloading requires a GPU device")
+    if cpu_offload:
+        raise NotImplementedError("cpu_offload streaming is not part of the int8 HIP path")
+    if quantization == "int8":
+        if device == "cpu":
+            raise ValueError("the int8 HIP path runs on the GPU only")
+        if precision != "bf16":
+            raise NotImplementedError("int8 frozen weights run with bf16 compute on MI355X; "
+                                      f"{precision} compute is not implemented")
+    return FrozenWeightTransfer(device, precision, quantization, cpu_offload)
+
+
+def move_weight(weight, transfer: FrozenWeightTransfer):
+    """_move_weight (quantization.jl:111-144): quantize a frozen matrix on the device; an existing
+    QuantizedMatrix is kept as is (re-moving keeps identical codes)."""
+    if isinstance(weight, QuantizedMatrix):
+        if transfer.quantization == "int8":
+            return weight
+        return weight.dequantize(torch.bfloat16)
+    if transfer.quantization == "int8":
+        w = weight if weight.is_cuda else weight.to("cuda")
+        return quantize_frozen_matrix(w, torch.bfloat16)
+    return weight.to("cuda" if transfer.device != "cpu" else "cpu")

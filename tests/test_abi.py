@@ -1,0 +1,131 @@
+"""CPU tests of the C ABI library (loads, exports every declared symbol, validates arguments
+before touching the GPU) and of the host-side policy logic. No GPU compute is called here."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from reels_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "reels_hip.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(reels_hip_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declarations_match_binding_table():
+    assert declared_symbols() == sorted(_lib.EXPORTS)
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    L = _lib.lib()
+    for name in declared_symbols():
+        assert hasattr(L, name), name
+    assert L.reels_hip_abi_version() == _lib.ABI_VERSION
+
+
+def test_header_constants_match_binding():
+    text = open(HEADER).read()
+    consts = dict(re.findall(r"#define (REELS_HIP_\w+) \(?(-?\d+)\)?", text))
+    assert int(consts["REELS_HIP_ABI_VERSION"]) == _lib.ABI_VERSION
+    assert (int(consts["REELS_HIP_F32"]), int(consts["REELS_HIP_BF16"]),
+            int(consts["REELS_HIP_F16"])) == (_lib.F32, _lib.BF16, _lib.F16)
+    assert (int(consts["REELS_HIP_WS_FWD"]), int(consts["REELS_HIP_WS_BWD"])) == (_lib.WS_FWD,
+                                                                               _lib.WS_BWD)
+
+
+def test_workspace_sizes():
+    L = _lib.lib()
+    for (M, K, N, r) in [(32760, 5120, 5120, 32), (1024, 1536, 1536, 16), (77, 5120, 5120, 32),
+                         (4, 5, 7, 3), (0, 16, 16, 0)]:
+        for which in (0, 1):
+            b = L.reels_hip_i8lora_workspace_bytes(M, K, N, r, which)
+            assert b > 0 and b % 256 == 0
+    # backward holds dy*s [M][N] bf16 and the h/u panels
+    assert L.reels_hip_i8lora_workspace_bytes(32760, 5120, 5120, 32, 1) >= 32760 * 5120 * 2
+    assert L.reels_hip_i8lora_workspace_bytes(-1, 5, 5, 1, 0) == 0
+
+
+def _err():
+    return _lib.lib().reels_hip_last_error().decode()
+
+
+def test_argument_errors_before_any_gpu_work():
+    L = _lib.lib()
+    fake = ctypes.c_void_p(4096)
+    # pack: empty rows (Julia's maximum over an empty collection throws), bad dtype
+    assert L.reels_hip_i8_pack(fake, 1, 4, 0, 0, fake, fake, None, None) == -1
+    assert "K > 0" in _err()
+    assert L.reels_hip_i8_pack(fake, 7, 4, 4, 4, fake, fake, None, None) == -2
+    assert L.reels_hip_i8_pack(fake, 1, 4, 8, 4, fake, fake, None, None) == -1  # ld < K
+    assert L.reels_hip_i8_pack(None, 1, 4, 8, 8, fake, fake, None, None) == -1
+    # forward / backward: workspace missing, bad shapes, NULL operands
+    assert L.reels_hip_i8lora_fwd(fake, fake, fake, None, None, None, 8, 16, 16, 0, 1.0, fake,
+                                  None, None, 0, None) == -3
+    assert "workspace" in _err()
+    assert L.reels_hip_i8lora_fwd(fake, fake, fake, None, None, None, 8, 0, 16, 0, 1.0, fake,
+                                  None, fake, 1 << 20, None) == -1
+    assert L.reels_hip_i8lora_fwd(fake, fake, fake, None, None, None, 8, 16, 16, 4, 1.0, fake,
+                                  None, fake, 1 << 20, None) == -1  # r > 0 needs A and B
+    assert L.reels_hip_i8lora_fwd(fake, fake, fake, None, None, None, 8, 16, 16, 0,
+                                  float("nan"), fake, None, fake, 1 << 20, None) == -1
+    assert L.reels_hip_i8lora_bwd(fake, fake, None, fake, fake, fake, fake, 8, 16, 16, 16, 1.0,
+                                  fake, None, None, None, 0, None) == -3
+    assert L.reels_hip_i8lora_bwd(None, fake, None, fake, fake, fake, fake, 8, 16, 16, 16, 1.0,
+                                  fake, None, None, fake, 1 << 20, None) == -1
+    # a successful-looking call clears the message of the previous failure
+    assert L.reels_hip_gelu_tanh(None, None, 0, None) == 0
+    assert _err() == ""
+    assert L.reels_hip_gelu_tanh(None, None, -1, None) == -1
+
+
+def test_library_path_override(monkeypatch, tmp_path):
+    monkeypatch.setenv("REELS_HIP_LIBRARY", str(tmp_path / "missing.so"))
+    assert _lib.library_path() == str(tmp_path / "missing.so")
+
+
+# ---- host policy logic (src/layers/quantization.jl:88-101, lora.jl:13-28) ------------------
+def test_frozen_weight_transfer_policy():
+    from reels_amd import frozen_weight_transfer
+    t = frozen_weight_transfer("hip", "bf16", quantization="int8")
+    assert t.quantization == "int8"
+    with pytest.raises(ValueError):
+        frozen_weight_transfer("hip", "bf16", quantization="int4")
+    with pytest.raises(ValueError):
+        frozen_weight_transfer("cpu", "fp32", cpu_offload=True)
+    with pytest.raises(ValueError):
+        frozen_weight_transfer("cpu", "fp32", quantization="int8")
+    with pytest.raises(NotImplementedError):
+        frozen_weight_transfer("hip", "fp16", quantization="int8")
+    assert frozen_weight_transfer("cpu", "fp32").quantization == "none"
+
+
+def test_lora_linear_constructor_validation():
+    import torch
+    from reels_amd import LoRALinear, QuantizedMatrix
+    w = QuantizedMatrix(torch.zeros((3, 4), dtype=torch.int8), torch.ones(3))
+    with pytest.raises(ValueError):
+        LoRALinear(w, rank=0)
+    with pytest.raises(ValueError):
+        LoRALinear(w, rank=2, alpha=float("inf"))
+    with pytest.raises(ValueError):
+        LoRALinear(w, rank=2, alpha=-1.0)
+    with pytest.raises(ValueError):
+        LoRALinear(w, rank=2, dropout=1.0)
+    with pytest.raises(ValueError):
+        LoRALinear(w, rank=2, train_bias=True)
+    layer = LoRALinear(w, rank=2, alpha=2)
+    assert layer.A.shape == (4, 2) and layer.B.shape == (2, 3)
+    assert float(layer.B.float().abs().sum()) == 0.0  # B = 0 at construction (lora.jl:24)
+    assert layer.lora_scale == 1.0
+
+
+def test_cpu_tensors_are_rejected_not_computed():
+    import torch
+    from reels_amd import quantize_frozen_matrix
+    with pytest.raises(ValueError, match="ROCm device"):
+        quantize_frozen_matrix(torch.zeros((4, 16)))

@@ -1,0 +1,317 @@
+"""Pins the oracle (CPU restatement of Reels.jl's int8 LoRA linear) before it is trusted as the
+checker: known-answer vectors, a second independent restatement, closed forms and invariants
+chosen so that a dropped term, wrong sign, wrong index or transposed operand fails a test.
+CPU only."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                      "wan21_block_tiny_int8.npz")
+F32 = np.float32
+
+
+def bf(vals):
+    return oracle.f32_to_bf16(np.asarray(vals, F32))
+
+
+# ---- Philox4x32-10: Random123 known-answer vectors ---------------------------------------------
+@pytest.mark.parametrize("ctr,key,want", [
+    ([0, 0, 0, 0], [0, 0], [0x6627e8d5, 0xe169c58d, 0xbc57ac4c, 0x9b00dbd8]),
+    ([0xffffffff] * 4, [0xffffffff] * 2, [0x408f276d, 0x41c83b0e, 0xa20bc7c6, 0x6d5451fd]),
+    ([0x243f6a88, 0x85a308d3, 0x13198a2e, 0x03707344], [0xa4093822, 0x299f31d0],
+     [0xd16cfe09, 0x94fdcceb, 0x5001e420, 0x24126ea1]),
+])
+def test_philox_known_answers(ctr, key, want):
+    assert [int(v) for v in oracle.philox(ctr, key)] == want
+
+
+def test_normal_generator_moments_and_outliers():
+    z = oracle.bf16_to_f32(oracle.normal_bf16(7, (1 << 20,), 1.0)).astype(np.float64)
+    assert abs(z.mean()) < 5e-3 and abs(z.std() - 1.0) < 5e-3
+    w = oracle.bf16_to_f32(oracle.normal_bf16(8, (1 << 20,), 0.02, outlier_rate=1e-3))
+    frac = np.mean(np.abs(w) == oracle.bf16_to_f32(bf([0.4]))[0])
+    assert 0.0007 < frac < 0.0013  # 0.1% outliers at exactly +-20 sigma
+    assert np.array_equal(oracle.normal_bf16(7, (1000,), 1.0), oracle.normal_bf16(7, (1000,), 1.0))
+
+
+# ---- bf16 conversions (src/models/interface.jl:13-25) ----------------------------------------
+def test_bf16_exhaustive_round_trip():
+    h = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    f = oracle.bf16_to_f32(h)
+    assert np.array_equal(oracle.f32_to_bf16(f), h)
+    assert np.array_equal(oracle.c_f32_to_bf16(f), h)
+
+
+def test_bf16_rounding_matches_rne_and_torch():
+    import torch
+    rng = np.random.default_rng(0)
+    bits = rng.integers(0, 1 << 32, size=1 << 18, dtype=np.uint64).astype(np.uint32)
+    f = bits.view(F32)
+    f = f[np.isfinite(f)]
+    ours = oracle.f32_to_bf16(f)
+    assert np.array_equal(ours, oracle.c_f32_to_bf16(f))
+    ref = torch.from_numpy(f.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(ours, ref)
+    # ties to even on exact halfway points
+    ties = np.array([0x3F808000, 0x3F818000, 0xBF808000, 0xBF818000], np.uint32).view(F32)
+    assert list(oracle.f32_to_bf16(ties)) == [0x3F80, 0x3F82, 0xBF80, 0xBF82]
+
+
+# ---- pack: quantize_frozen_matrix (src/layers/quantization.jl:35-44) -------------------------
+def _pack_both(w32):
+    q1, s1, st1 = oracle.pack(w32, "f32")
+    q2, s2, st2 = oracle.numpy_pack(w32)
+    assert st1 == st2
+    assert np.array_equal(q1, q2)
+    assert np.array_equal(s1.view(np.uint32), s2.view(np.uint32))
+    return q1, s1, st1
+
+
+def test_pack_two_restatements_agree_bitwise():
+    w = oracle.normal_bf16(11, (1024, 5120), 0.02, outlier_rate=1e-3)
+    w32 = oracle.bf16_to_f32(w)
+    q, s, st = _pack_both(w32)
+    qb, sb, stb = oracle.pack(w, "bf16")  # bf16 input path = f32 of the same values
+    assert st == 0 and np.array_equal(q, qb) and np.array_equal(s, sb)
+    f = oracle.normal_f32(12, (512, 1536), 1.0)
+    _pack_both(f)
+    # f16 input path = f32 of the same values
+    h16 = f.astype(np.float16)
+    q16, s16, _ = oracle.pack(h16.view(np.uint16), "f16")
+    q32, s32, _ = oracle.pack(h16.astype(F32), "f32")
+    assert np.array_equal(q16, q32) and np.array_equal(s16, s32)
+
+
+def test_pack_closed_forms():
+    rows = np.zeros((8, 10), F32)
+    # absmax 127 -> scale exactly 1: codes are rint(w), ties to even
+    rows[0] = [127, 2.5, 3.5, -2.5, -3.5, 0.5, 1.5, -0.0, 126.5, -126.5]
+    # absmax 254 -> scale exactly 2
+    rows[1, :6] = [254, 5, 7, -5, 1, 3]
+    # zero row -> scale 1, codes 0 (quantization.jl:40)
+    # single spike
+    rows[3, 4] = 0.3
+    # constant row
+    rows[4] = -0.7
+    # negative absmax
+    rows[5, :2] = [-3, 1]
+    # 20-sigma outlier among small values
+    rows[6] = [0.01, -0.02, 0.4, 0.0, 0.015, -0.005, 0.02, 0.0, -0.01, 0.003]
+    rows[7] = np.float32(1e-30)  # tiny but normal
+    q, s, st = _pack_both(rows)
+    assert st == 0
+    assert list(q[0]) == [127, 2, 4, -2, -4, 0, 2, 0, 126, -126] and s[0] == 1.0
+    assert list(q[1, :6]) == [127, 2, 4, -2, 0, 2] and s[1] == 2.0
+    assert s[2] == 1.0 and not q[2].any()
+    assert s[3] == F32(0.3) / F32(127) and list(q[3]) == [0, 0, 0, 0, 127, 0, 0, 0, 0, 0]
+    assert np.all(q[4] == -127)
+    assert q[5, 0] == -127 and q[5, 1] == 42  # 127/3 = 42.33
+    assert q[6, 2] == 127 and s[6] == F32(0.4) / F32(127)
+    assert np.all(q[7] == 127)
+
+
+def test_pack_denormals_are_not_flushed():
+    ulp = np.array([1], np.uint32).view(F32)[0]  # smallest denormal
+    w = np.array([[127 * ulp, 64 * ulp, 0, -127 * ulp],    # scale = 1 ulp exactly
+                  [10 * ulp, 5 * ulp, 10 * ulp, 5 * ulp]],  # scale rounds to 0 -> +-Inf -> 127
+                 F32)
+    q, s, st = _pack_both(w)
+    assert st == 0
+    assert s[0] == ulp and list(q[0]) == [127, 64, 0, -127]
+    assert s[1] == 0.0 and list(q[1]) == [127, 127, 127, 127]
+    # scale 0 with a zero weight gives 0/0 = NaN -> Int8(NaN) throws
+    _, _, st = _pack_both(np.array([[10 * ulp, 0.0]], F32))
+    assert st == 1
+
+
+@pytest.mark.parametrize("bad", [np.nan, np.inf, -np.inf])
+def test_pack_nonfinite_is_an_error(bad):
+    w = np.ones((3, 6), F32)
+    w[1, 2] = bad
+    q, s, st = _pack_both(w)
+    assert st == 1
+    assert np.all(q[0] == 127) and np.all(q[2] == 127)  # other rows unaffected
+
+
+def test_pack_invariants():
+    w = oracle.bf16_to_f32(oracle.normal_bf16(13, (777, 333), 0.02, outlier_rate=5e-3))
+    q, s, st = _pack_both(w)
+    assert st == 0
+    assert q.min() >= -127 and q.max() <= 127           # never -128
+    assert np.all((np.sign(q) == np.sign(w)) | (q == 0))
+    assert np.all(np.abs(q).max(axis=1) == 127)          # every non-zero row reaches 127
+    # |w - q s| <= s/2 up to the f32 rounding of w/s (at most half an ulp of a value < 128)
+    err = np.abs(w.astype(np.float64) - q * s[:, None].astype(np.float64))
+    assert np.all(err <= s[:, None].astype(np.float64) * (0.5 + 2.0 ** -17))
+
+
+@pytest.mark.parametrize("shape,seed", [((7, 5), 950), ((512, 1536), 951)])
+def test_pack_reconstruction_tolerance_of_reference(shape, seed):
+    # test/unit/quantization.jl:3-8: randn weights, Array(quantized) ≈ weight rtol=1e-2
+    # atol=1e-2 (Julia isapprox: norm(a - b) <= max(atol, rtol * max(norm(a), norm(b))))
+    w = oracle.normal_f32(seed, shape, 1.0)
+    q, s, st = _pack_both(w)
+    deq = oracle.dequant(q, s, "f32")
+    assert np.linalg.norm(deq - w) <= max(1e-2, 1e-2 * max(np.linalg.norm(deq), np.linalg.norm(w)))
+
+
+def test_pack_golden_real_wan_weights():
+    g = np.load(GOLDEN)
+    names = sorted({k[:-2] for k in g.files if k.endswith("_q")})
+    assert len(names) == 10
+    for n in names:
+        q, s, st = _pack_both(g[n + "_w"])
+        assert st == 0
+        assert np.array_equal(q, g[n + "_q"]), n
+        assert np.array_equal(s.view(np.uint32), g[n + "_s"].view(np.uint32)), n
+
+
+# ---- dequantization (quantization.jl:25-29, 61-64) --------------------------------------------
+def test_dequant_closed_forms():
+    q = np.array([[-127, -1, 0, 1, 127, 63]], np.int8)
+    s = np.array([0.003141], F32)
+    f32 = oracle.dequant(q, s, "f32")
+    assert np.array_equal(f32, (q.astype(F32) * s[0]).astype(F32))
+    b16 = oracle.dequant(q, s, "bf16")
+    assert np.array_equal(b16, oracle.f32_to_bf16(q.astype(F32) * s[0]))
+    h16 = oracle.dequant(q, s, "f16").view(np.float16)
+    want = q.astype(np.float16) * np.float16(s[0])  # numpy f16 multiply rounds once
+    assert np.array_equal(h16, want)
+
+
+# ---- forward (lora.jl:56-95) ------------------------------------------------------------------
+def _small_int_case(M=5, K=7, N=6, r=3, seed=0):
+    rng = np.random.default_rng(seed)
+    x = rng.integers(-3, 4, size=(M, K)).astype(F32)
+    q = rng.integers(-127, 128, size=(N, K)).astype(np.int8)
+    s = (2.0 ** rng.integers(-4, 2, size=N)).astype(F32)
+    A = rng.integers(-2, 3, size=(K, r)).astype(F32)
+    B = rng.integers(-2, 3, size=(r, N)).astype(F32)
+    bias = rng.integers(-5, 6, size=N).astype(F32)
+    return x, q, s, A, B, bias
+
+
+def test_forward_brute_force_integers():
+    x, q, s, A, B, bias = _small_int_case()
+    c = 2.0
+    y, h = oracle.lora_forward(bf(x), q, s, bf(A), bf(B), c, bias=bf(bias))
+    xi = x.astype(np.int64)
+    want_h = xi @ A.astype(np.int64)
+    want = (xi @ q.astype(np.int64).T) * s.astype(np.float64) + c * (want_h @ B.astype(np.int64)) + bias
+    assert np.array_equal(h, want_h.astype(np.float64))
+    assert np.array_equal(y, want)
+    # row selection returns the same rows
+    y2, _ = oracle.lora_forward(bf(x), q, s, bf(A), bf(B), c, bias=bf(bias), rows=[4, 0])
+    assert np.array_equal(y2, want[[4, 0]])
+
+
+def test_forward_zero_B_is_base_and_merged_weight_identity():
+    # test/unit/lora.jl:6 (B = 0 gives the base product exactly) and :8 (merged weight)
+    x = oracle.normal_bf16(21, (9, 16), 1.0)
+    w = oracle.normal_bf16(22, (12, 16), 0.02)
+    q, s, _ = oracle.pack(w)
+    A = oracle.normal_bf16(23, (16, 4), 0.1)
+    y0, _ = oracle.lora_forward(x, q, s, A, np.zeros((4, 12), np.uint16), 0.5)
+    base, _ = oracle.lora_forward(x, q, s, None, None, 0.0)
+    assert np.array_equal(y0, base)
+    B = oracle.normal_bf16(24, (4, 12), 0.1)
+    y, _ = oracle.lora_forward(x, q, s, A, B, 0.5)
+    merged = q.astype(np.float64) * s.astype(np.float64)[:, None] + 0.5 * (
+        oracle.bf16_to_f32(A).astype(np.float64) @ oracle.bf16_to_f32(B).astype(np.float64)).T
+    np.testing.assert_allclose(y, oracle.bf16_to_f32(x).astype(np.float64) @ merged.T, rtol=1e-12,
+                               atol=1e-12)
+
+
+# ---- backward (lora.jl:106-118): exact finite differences of the linear forward --------------
+def _loss(x, q, s, A, B, c, dy):
+    y, _ = oracle.lora_forward(x, q, s, A, B, c)
+    return float(np.sum(y * oracle.bf16_to_f32(dy).astype(np.float64)))
+
+
+def test_backward_matches_finite_differences():
+    # The loss sum(y .* dy) is linear in A, in B and in x, so a difference quotient between two
+    # bf16 values is exact up to f64 rounding (the reference's own check, test/unit/lora.jl:12-21,
+    # uses a central difference with rtol 2e-2).
+    M, K, N, r, c = 6, 8, 5, 3, 1.5
+    x = oracle.normal_bf16(31, (M, K), 1.0)
+    w = oracle.normal_bf16(32, (N, K), 0.1)
+    q, s, _ = oracle.pack(w)
+    A = oracle.normal_bf16(33, (K, r), 0.3)
+    B = oracle.normal_bf16(34, (r, N), 0.3)
+    dy = oracle.normal_bf16(35, (M, N), 1.0)
+    g = oracle.lora_backward(dy, x, q, s, A, B, c)
+    base = _loss(x, q, s, A, B, c, dy)
+
+    def quotient(arr, idx, name):
+        a = arr.copy()
+        old = oracle.bf16_to_f32(a[idx:idx + 1] if a.ndim == 1 else a[idx][None])[0]
+        new = bf([old + 0.25])[0]
+        a[idx] = new
+        step = float(oracle.bf16_to_f32(np.array([new], np.uint16))[0]) - float(old)
+        args = dict(x=x, A=A, B=B)
+        args[name] = a
+        return (_loss(args["x"], q, s, args["A"], args["B"], c, dy) - base) / step
+
+    for idx in [(0, 0), (K - 1, r - 1), (3, 1)]:
+        assert np.isclose(quotient(A, idx, "A"), g["dA"][idx], rtol=1e-9, atol=1e-9)
+    for idx in [(0, 0), (r - 1, N - 1), (1, 2)]:
+        assert np.isclose(quotient(B, idx, "B"), g["dB"][idx], rtol=1e-9, atol=1e-9)
+    for idx in [(0, 0), (M - 1, K - 1), (2, 5)]:
+        assert np.isclose(quotient(x, idx, "x"), g["dx"][idx], rtol=1e-9, atol=1e-9)
+    # column / row selection returns the same entries
+    g2 = oracle.lora_backward(dy, x, q, s, A, B, c, rows=[5, 1], kcols=[7, 0], ncols=[4, 2])
+    assert np.array_equal(g2["dx"], g["dx"][[5, 1]])
+    assert np.array_equal(g2["dA"], g["dA"][[7, 0]])
+    assert np.array_equal(g2["dB"], g["dB"][:, [4, 2]])
+
+
+def test_backward_brute_force_integers():
+    x, q, s, A, B, _ = _small_int_case(seed=3)
+    dy = np.random.default_rng(4).integers(-3, 4, size=(x.shape[0], q.shape[0])).astype(F32)
+    c = 0.5
+    g = oracle.lora_backward(bf(dy), bf(x), q, s, bf(A), bf(B), c)
+    X, D = x.astype(np.float64), dy.astype(np.float64)
+    Wd = q.astype(np.float64) * s.astype(np.float64)[:, None]
+    Af, Bf = A.astype(np.float64), B.astype(np.float64)
+    u = D @ Bf.T
+    assert np.array_equal(g["dx"], D @ Wd + c * u @ Af.T)
+    assert np.array_equal(g["dA"], c * X.T @ u)
+    assert np.array_equal(g["dB"], c * (X @ Af).T @ D)
+
+
+# ---- gelu_tanh (src/layers/linear.jl:61-68) ----------------------------------------------------
+def test_gelu_closed_forms_and_derivative():
+    xs = np.array([0.0, 1.0, -1.0, 3.0, -3.0, 0.5, 10.0, -10.0], F32)
+    y = oracle.bf16_to_f32(oracle.gelu_tanh(bf(xs)))
+    assert y[0] == 0.0
+    xb = oracle.bf16_to_f32(bf(xs)).astype(np.float64)
+    k = np.sqrt(2 / np.pi)
+    ref = 0.5 * xb * (1 + np.tanh(k * (xb + 0.044715 * xb ** 3)))
+    assert np.allclose(y, ref, rtol=2 ** -7, atol=1e-6)
+    # gelu(x) - gelu(-x) = x
+    for i, j in [(1, 2), (3, 4)]:
+        assert np.isclose(y[i] - y[j], xb[i], rtol=2 ** -6)
+    # derivative: central differences of the f64 formula
+    grid = np.linspace(-4, 4, 81).astype(F32)
+    ones = bf(np.ones_like(grid))
+    d = oracle.bf16_to_f32(oracle.gelu_tanh_backward(bf(grid), ones)).astype(np.float64)
+    gb = oracle.bf16_to_f32(bf(grid)).astype(np.float64)
+    f = lambda v: 0.5 * v * (1 + np.tanh(k * (v + 0.044715 * v ** 3)))
+    fd = (f(gb + 1e-5) - f(gb - 1e-5)) / 2e-5
+    assert np.allclose(d, fd, rtol=2 ** -7, atol=2 ** -8)
+
+
+def test_reference_fp16_path_is_close_but_not_exact():
+    x = oracle.normal_bf16(41, (64, 256), 1.0)
+    w = oracle.normal_bf16(42, (128, 256), 0.02)
+    q, s, _ = oracle.pack(w)
+    A = oracle.normal_bf16(43, (256, 16), 0.01)
+    B = oracle.normal_bf16(44, (16, 128), 0.01)
+    y, _ = oracle.lora_forward(x, q, s, A, B, 1.0)
+    y16 = oracle.reference_fp16_forward(x, q, s, A, B, 1.0)
+    rel = np.abs(y16 - y).max() / np.abs(y).max()
+    assert 1e-6 < rel < 1e-2
