@@ -10,7 +10,12 @@ producing dX, dA and dB. Inputs are synthetic and already resident in HBM when t
 Prints one JSON line (see the keys below). Per-kernel durations come from HIP events recorded by
 the library around every launch on the launch stream, over the timed steps themselves.
 
-    python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--cpu-seconds 15]
+    python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--cpu-seconds 15] [--no-pack]
+
+A second workload, reported under "pack": quantize_frozen_matrix on the full 40-layer
+Wan-2.1-14B weight set (per layer q, k, v, o 5120x5120, ffn.0 13824x5120, ffn.2 5120x13824: 9.857e9
+bf16 elements ~N(0, 0.02) with 0.1% outliers at +-20 sigma), packed as two row-stacked launches
+(all K = 5120 rows, then all K = 13824 rows; packing is row-independent).
 """
 from __future__ import annotations
 
@@ -49,7 +54,88 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="approximate CPU work for the cpu_baseline sample (0 disables it)")
     ap.add_argument("--tokens", type=int, default=TOKENS)
+    ap.add_argument("--no-pack", action="store_true", help="skip the pack workload")
     return ap.parse_args()
+
+
+PACK_LAYERS = 40
+PACK_SETS = [(PACK_LAYERS * (4 * 5120 + 13824), 5120), (PACK_LAYERS * 5120, 13824)]  # (rows, K)
+
+
+def pack_bench(dev, reps=3):
+    """Times the pack kernel on the 40-layer 14B weight set; returns the "pack" result object."""
+    import torch
+    from reels_amd import _lib
+    L = _lib.lib()
+    gen = torch.Generator(device=dev).manual_seed(77)
+    mats = []
+    for rows, K in PACK_SETS:
+        w = torch.empty((rows, K), dtype=torch.bfloat16, device=dev)
+        step = 16384
+        for r0 in range(0, rows, step):
+            r1 = min(rows, r0 + step)
+            c = torch.randn((r1 - r0, K), generator=gen, device=dev).mul_(0.02)
+            u = torch.rand((r1 - r0, K), generator=gen, device=dev)
+            sign = torch.where(u < 0.0005, -1.0, 1.0)
+            c = torch.where(u < 0.001, sign * 0.4, c)
+            w[r0:r1] = c.to(torch.bfloat16)
+            del c, u, sign
+        q = torch.empty((rows, K), dtype=torch.int8, device=dev)
+        sc = torch.empty((rows,), dtype=torch.float32, device=dev)
+        mats.append((w, q, sc, rows, K))
+    status = torch.zeros((1,), dtype=torch.int32, device=dev)
+    st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+
+    def run():
+        for (w, q, sc, rows, K) in mats:
+            _lib.check("reels_hip_i8_pack", L.reels_hip_i8_pack(p(w), _lib.BF16, rows, K, K, p(q),
+                                                                p(sc), p(status), st))
+    run()
+    torch.cuda.synchronize()
+    _lib.check("reels_hip_trace_start", L.reels_hip_trace_start(16 * reps))
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        run()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    recs = [(n, ms) for (n, ms) in _lib.trace_records() if n.startswith("pack_rows")]
+    elems = sum(rows * K for (_, _, _, rows, K) in mats)
+    nbytes = sum(3 * rows * K + 4 * rows for (_, _, _, rows, K) in mats)
+    ms = (t1 - t0) * 1e3 / reps
+    kern_ms = sum(ms_ for (_, ms_) in recs) / reps
+    gbs = nbytes / (kern_ms * 1e-3) / 1e9
+    assert int(status.item()) == 0
+    out = {"metric": "pack GB/s (bf16 read + int8 codes + f32 scales)", "value": round(gbs, 1),
+           "unit": "GB/s", "ms": round(ms, 4), "kernel_ms": round(kern_ms, 4),
+           "elements": elems, "bytes": nbytes,
+           "roofline": {"kernel": "pack_rows_kernel", "bound": "hbm", "achieved": round(gbs, 1),
+                        "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                        "traffic": None}}
+    del mats
+    torch.cuda.empty_cache()
+    return out
+
+
+def pack_cpu_baseline(seconds=5.0):
+    """The reference packs on the host CPU (quantize_frozen_matrix, quantization.jl:35-44 on
+    Float32.(Array(W))); the oracle's C restatement (OpenMP) is timed on a sample of 14B rows."""
+    import numpy as np
+    import oracle
+    import os
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    rows = 2048
+    w = oracle.normal_bf16(5, (rows, 5120), 0.02, outlier_rate=1e-3)
+    t0 = time.perf_counter(); oracle.pack(w, "bf16"); t1 = time.perf_counter()
+    reps = max(1, int(seconds / max(t1 - t0, 1e-6)))
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        oracle.pack(w, "bf16")
+    t1 = time.perf_counter()
+    nbytes = 3 * rows * 5120 + 4 * rows
+    return {"value": round(nbytes * reps / (t1 - t0) / 1e9, 2), "unit": "GB/s", "cores": threads,
+            "kind": "port", "sample": f"{rows}x5120 bf16 rows x {reps} repetitions, C oracle "
+                                      f"(OpenMP, {threads} threads), {t1 - t0:.2f} s"}
 
 
 class Projection:
@@ -161,8 +247,8 @@ def main():
     gemm_fl = {"fwd": 0.0, "dx": 0.0}
     for step in range(args.steps):
         rs = recs[step * per_step:(step + 1) * per_step]
-        fi = [ms for (n, ms) in rs if n == "i8gemm_kernel<0>"]
-        bi = [ms for (n, ms) in rs if n == "i8gemm_kernel<1>"]
+        fi = [ms for (n, ms) in rs if n.startswith("i8gemm") and n.endswith("<0>")]
+        bi = [ms for (n, ms) in rs if n.startswith("i8gemm") and n.endswith("<1>")]
         for (pr, ms) in zip(projs, fi):
             gemm_ms["fwd"] += ms; gemm_n["fwd"] += 1
             gemm_fl["fwd"] += gemm_flops("fwd", M, pr.K, pr.N, RANK)
@@ -172,7 +258,7 @@ def main():
     tot_ms = gemm_ms["fwd"] + gemm_ms["dx"]
     achieved = (gemm_fl["fwd"] + gemm_fl["dx"]) / (tot_ms * 1e-3) / 1e12 if tot_ms > 0 else 0.0
     roofline = {
-        "kernel": "i8gemm_kernel (fwd <0> and dX <1>, int8 weight dequantised to bf16 on MFMA)",
+        "kernel": "i8gemm_v3_kernel (fwd <0> and dX <1>, int8 weight converted to bf16 for MFMA)",
         "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
         "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
         "avg_launch_ms": {k: round(gemm_ms[k] / max(gemm_n[k], 1), 4) for k in gemm_ms},
@@ -184,6 +270,13 @@ def main():
     cpu = None
     if args.cpu_seconds > 0:
         cpu = cpu_baseline(args.cpu_seconds)
+    pack = None
+    if not args.no_pack:
+        del projs
+        torch.cuda.empty_cache()
+        pack = pack_bench(dev)
+        if args.cpu_seconds > 0:
+            pack["cpu_baseline"] = pack_cpu_baseline(min(5.0, args.cpu_seconds))
 
     out = {
         "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1,
@@ -198,6 +291,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": kernels,
+        "pack": pack,
         "device": torch.cuda.get_device_name(dev),
     }
     print(json.dumps(out))

@@ -233,21 +233,270 @@ void i8gemm_kernel(GemmArgs a) {
   }
 }
 
+// FWD weight tile of the three-stage kernel: [256 n][64 k] int8, 16-byte slots XOR-swizzled
+// within the 64-byte row so 32-row fragment reads (ds_read_b128) hit distinct banks
+__device__ __forceinline__ int wf2_swz(int row) { return ((row >> 1) & 3) ^ ((row >> 3) & 1); }
+
+// =============================================================================================
+// Main kernel, used whenever the reduction length is a multiple of 64 (every Wan / LTX shape).
+//
+// * HBM -> LDS with buffer_load_dwordx4 ... lds (no staging registers, no VALU for the copy),
+//   three LDS stages (3 x 48 KiB): the loads for step k+2 are in flight while step k is computed.
+//   SGPR base + per-lane 32-bit voffset; the k advance is the scalar soffset.
+// * 8 waves (two per SIMD, so one wave's MFMAs cover the other's LDS reads and int8 -> bf16
+//   conversion; one wave per SIMD measured at most ~67% of the MFMA rate even without memory
+//   traffic), 256 x 256 block tile, reduction step 64.
+// * FWD reads a weight fragment for two MFMA steps with one ds_read_b128: the 64 reduction
+//   indices of a step pair are assigned so that lane half lhi, step 2p+e uses k = 32p + 16lhi +
+//   8e + (0..7); the activation fragment of that step is 16-byte chunk 4p + 2lhi + e of the row.
+//   (The pairing only reorders the reduction; both operands use the same k for each product.)
+// * DX reads weight fragments with ds_read_b64_tr_b8 as the general kernel does.
+// * Tiles are mapped to XCDs (block b runs on XCD b % 8): each XCD takes a contiguous range of
+//   the tile order, and the order walks 4 token blocks before moving to the next column block,
+//   so the ~32 tiles resident on one XCD share activation and weight tiles in its L2. Wave w owns tokens [128*(w/4), +128) and output columns [64*(w%4), +64): 4 x 2 tiles
+// of 32x32 (128 accumulator registers). Per 64-step and wave: 16 activation fragment reads, 4
+// (FWD, ds_read_b128) or 8 (DX, ds_read_b64_tr_b8) weight fragment reads, 32 MFMAs.
+namespace gemm3 {
+constexpr int BM = 256, BN = 256, BK = 64, NT = 512;
+constexpr int ACT = BM * BK * 2;   // 32 KiB
+constexpr int WB = BN * BK;        // 16 KiB
+constexpr int STAGE = ACT + WB;    // 48 KiB
+constexpr int NSTAGE = 3;
+constexpr int GM = 4;
+}  // namespace gemm3
+
+template <int MODE>
+__global__ __launch_bounds__(512)
+void i8gemm_v3_kernel(GemmArgs a, int tiles_n, int tiles_m) {
+  using namespace gemm3;
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wm = w >> 2, wn = w & 3;
+  const int l32 = lane & 31, lhi = lane >> 5;
+  const int64_t M = a.M, Ncols = a.Ncols, Kred = a.Kred;
+
+  const int nt = tiles_n * tiles_m;
+  const int b = blockIdx.x;
+  const int xcd = b & 7, idx = b >> 3;
+  const int lo = nt >> 3, rem = nt & 7;
+  const int logical = xcd * lo + (xcd < rem ? xcd : rem) + idx;
+  const int group = GM * tiles_n;
+  const int g = logical / group;
+  const int first_m = g * GM;
+  const int gm = (tiles_m - first_m) < GM ? (tiles_m - first_m) : GM;
+  const int within = logical - g * group;
+  const int64_t m0 = (int64_t)(first_m + within % gm) * BM;
+  const int64_t n0 = (int64_t)(within / gm) * BN;
+
+  const __amdgpu_buffer_rsrc_t ract =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.act, (short)0, (int)(M * Kred * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rq =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.q, (short)0, (int)(Ncols * Kred), 0x00020000);
+  uint32_t voa[4], vow[2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = (w * 4 + i) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ act_swz(row);
+    const int64_t m = (m0 + row < M) ? m0 + row : M - 1;
+    voa[i] = (uint32_t)((m * Kred + c * 8) * 2);
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    if (MODE == 0) {
+      const int row = (w * 2 + i) * 16 + (lane >> 2);
+      const int j = (lane & 3) ^ wf2_swz(row);
+      const int64_t n = (n0 + row < Ncols) ? n0 + row : Ncols - 1;
+      vow[i] = (uint32_t)(n * Kred + j * 16);
+    } else {
+      const int row = (w * 2 + i) * 4 + (lane >> 4);
+      const int c = (lane & 15) ^ wd_swz(row);
+      int64_t kc = n0 + c * 16;
+      if (kc >= Ncols) kc = Ncols - 16;
+      vow[i] = (uint32_t)(row * a.ldq + kc);
+    }
+  }
+  const int nk = (int)(Kred / BK);
+  auto issue = [&](int kt, int stage) {
+    uint8_t* base = smem + stage * STAGE;
+    const uint32_t sa = (uint32_t)kt * (BK * 2);
+    const uint32_t sw = MODE == 0 ? (uint32_t)kt * BK : (uint32_t)kt * (uint32_t)(BK * a.ldq);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ract, LDS_PTR(void, base + (w * 4 + i) * 1024), 16,
+                                               voa[i], sa, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, LDS_PTR(void, base + ACT + (w * 2 + i) * 1024), 16,
+                                               vow[i], sw, 0, 0);
+  };
+
+  f32x16 acc[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  auto compute = [&](int stage) {
+    const uint8_t* sa = smem + stage * STAGE;
+    const uint8_t* sw = sa + ACT;
+    auto xchunk = [&](int s) { return MODE == 0 ? 4 * (s >> 1) + 2 * lhi + (s & 1) : 2 * s + lhi; };
+    auto read_x = [&](int s, bf16x8* xf) {
+      const int c = xchunk(s);
+#pragma unroll
+      for (int tj = 0; tj < 4; ++tj) {
+        const int row = wm * 128 + tj * 32 + l32;
+        xf[tj] = as_bf16x8(*reinterpret_cast<const u32x4*>(sa + row * 128 + ((c ^ act_swz(row)) << 4)));
+      }
+    };
+    bf16x8 xf0[4], xf1[4];
+    u32x4 wr[2][2];
+    i32x2 wt[4][2];
+    if (MODE == 0) {
+#pragma unroll
+      for (int pp = 0; pp < 2; ++pp)
+#pragma unroll
+        for (int ti = 0; ti < 2; ++ti) {
+          const int row = wn * 64 + ti * 32 + l32;
+          const int j = 2 * pp + lhi;
+          wr[pp][ti] = *reinterpret_cast<const u32x4*>(sw + row * 64 + ((j ^ wf2_swz(row)) << 4));
+        }
+    } else {
+      const int gq = lane >> 4, i16 = lane & 15;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int ti = 0; ti < 2; ++ti) {
+          const int row = kk * 16 + (gq >> 1) * 8 + (i16 >> 1);
+          const int col = wn * 64 + ti * 32 + 16 * (gq & 1) + 8 * (i16 & 1);
+          const uint8_t* p = sw + row * 256 + (((col >> 3) ^ (wd_swz(row) << 1)) << 3);
+          wt[kk][ti] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(LDS_PTR(i32x2, p));
+        }
+    }
+    // LLVM's GEMM interleave strategies (1 for FWD, 0 for DX measured fastest): LDS reads are
+    // hoisted well ahead of their MFMAs with counted lgkmcnt waits.
+    __builtin_amdgcn_iglp_opt(MODE == 0 ? 1 : 0);
+    read_x(0, xf0);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      bf16x8* cur = (s & 1) ? xf1 : xf0;
+      bf16x8* nxt = (s & 1) ? xf0 : xf1;
+      bf16x8 af[2];
+#pragma unroll
+      for (int ti = 0; ti < 2; ++ti) {
+        if (MODE == 0) {
+          const u32x4& r = wr[s >> 1][ti];
+          af[ti] = (s & 1) ? i8x8_to_bf16x8(r[2], r[3]) : i8x8_to_bf16x8(r[0], r[1]);
+        } else {
+          af[ti] = i8x8_to_bf16x8((uint32_t)wt[s][ti][0], (uint32_t)wt[s][ti][1]);
+        }
+      }
+      if (s < 3) read_x(s + 1, nxt);
+#pragma unroll
+      for (int tj = 0; tj < 4; ++tj)
+#pragma unroll
+        for (int ti = 0; ti < 2; ++ti)
+          acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ti], cur[tj], acc[ti][tj], 0, 0, 0);
+    }
+  };
+
+  issue(0, 0);
+  if (nk > 1) issue(1, 1);
+  for (int kt = 0; kt < nk; ++kt) {
+    if (kt + 1 < nk) __builtin_amdgcn_s_waitcnt(0x0F76);  // vmcnt(6): stage kt+1 may stay in flight
+    else __builtin_amdgcn_s_waitcnt(0x0F70);              // vmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    if (kt + 2 < nk) issue(kt + 2, (kt + 2) % NSTAGE);
+    compute(kt % NSTAGE);
+  }
+
+  // ---- epilogue: wave owns 64 columns x 128 tokens ---------------------------------------
+  const int nsteps = a.rp >> 4;
+#pragma unroll
+  for (int ti = 0; ti < 2; ++ti) {
+    const int64_t nrow = n0 + wn * 64 + ti * 32 + l32;
+    const int64_t nrc = nrow < Ncols ? nrow : Ncols - 1;
+    const int64_t nbase = n0 + wn * 64 + ti * 32 + lhi * 4;
+    float sc[16], bs[16];
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int64_t n = nbase + g4 * 8;
+      const bool ok = n < Ncols;
+      f32x4 s4 = {1.0f, 1.0f, 1.0f, 1.0f};
+      if (a.colscale != nullptr && ok) s4 = *reinterpret_cast<const f32x4*>(a.colscale + n);
+      u32x2 b2 = {0, 0};
+      if (a.bias != nullptr && ok) b2 = *reinterpret_cast<const u32x2*>(a.bias + n);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sc[g4 * 4 + e] = s4[e];
+      bs[g4 * 4 + 0] = bf16_lo(b2[0]); bs[g4 * 4 + 1] = bf16_hi(b2[0]);
+      bs[g4 * 4 + 2] = bf16_lo(b2[1]); bs[g4 * 4 + 3] = bf16_hi(b2[1]);
+    }
+#pragma unroll
+    for (int tj = 0; tj < 4; ++tj) {
+      const int64_t m = m0 + wm * 128 + tj * 32 + l32;
+      const int64_t mc = m < M ? m : M - 1;
+      f32x16 lo;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) lo[v] = 0.0f;
+      for (int s = 0; s < nsteps; ++s) {
+        u32x4 rv = *reinterpret_cast<const u32x4*>(a.R + nrc * a.rp + s * 16 + lhi * 8);
+        u32x4 lv = *reinterpret_cast<const u32x4*>(a.L + mc * a.rp + s * 16 + lhi * 8);
+        if (nrow >= Ncols) rv = u32x4{0, 0, 0, 0};
+        if (m >= M) lv = u32x4{0, 0, 0, 0};
+        lo = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(rv), as_bf16x8(lv), lo, 0, 0, 0);
+      }
+      if (m < M) {
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int64_t n = nbase + g4 * 8;
+          if (n < Ncols) {
+            float o[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int v = g4 * 4 + e;
+              o[e] = sc[v] * acc[ti][tj][v] + a.c * lo[v] + bs[v];
+            }
+            u32x2 pk = {pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+            *reinterpret_cast<u32x2*>(a.out + m * Ncols + n) = pk;
+          }
+        }
+      }
+    }
+  }
+}
+
 int launch_i8gemm(int mode, const GemmArgs& a, hipStream_t st) {
   using namespace gemm;
-  dim3 grid((unsigned)ceil_div(a.Ncols, BN), (unsigned)ceil_div(a.M, BM));
-  const size_t lds = 2 * STAGE_BYTES;
+  // the main kernel needs a reduction in whole 64-steps and 32-bit buffer offsets
+  const int64_t act_bytes = a.M * a.Kred * 2, q_bytes = a.Ncols * a.Kred;
+  const bool v3 = (a.Kred % gemm3::BK == 0) && act_bytes < ((int64_t)1 << 31) &&
+                  q_bytes < ((int64_t)1 << 31) && (a.ldq * gemm3::BK) < ((int64_t)1 << 31);
   static std::once_flag once;
   static hipError_t attr_err = hipSuccess;
   std::call_once(once, [&] {
-    attr_err = hipFuncSetAttribute((const void*)i8gemm_kernel<0>,
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    const int l1 = 2 * STAGE_BYTES, l2 = gemm3::NSTAGE * gemm3::STAGE;
+    attr_err = hipFuncSetAttribute((const void*)i8gemm_kernel<0>, hipFuncAttributeMaxDynamicSharedMemorySize, l1);
     if (attr_err == hipSuccess)
-      attr_err = hipFuncSetAttribute((const void*)i8gemm_kernel<1>,
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      attr_err = hipFuncSetAttribute((const void*)i8gemm_kernel<1>, hipFuncAttributeMaxDynamicSharedMemorySize, l1);
+    if (attr_err == hipSuccess)
+      attr_err = hipFuncSetAttribute((const void*)i8gemm_v3_kernel<0>, hipFuncAttributeMaxDynamicSharedMemorySize, l2);
+    if (attr_err == hipSuccess)
+      attr_err = hipFuncSetAttribute((const void*)i8gemm_v3_kernel<1>, hipFuncAttributeMaxDynamicSharedMemorySize, l2);
   });
   if (attr_err != hipSuccess)
     return fail(REELS_HIP_EHIP, std::string("i8gemm: hipFuncSetAttribute: ") + hipGetErrorString(attr_err));
+  if (v3) {
+    const int tn = (int)ceil_div(a.Ncols, gemm3::BN), tm = (int)ceil_div(a.M, gemm3::BM);
+    const size_t lds = gemm3::NSTAGE * gemm3::STAGE;
+    if (mode == 0) { TraceScope _ts(st, "i8gemm_v3_kernel<0>"); i8gemm_v3_kernel<0><<<tn * tm, gemm3::NT, lds, st>>>(a, tn, tm); }
+    else { TraceScope _ts(st, "i8gemm_v3_kernel<1>"); i8gemm_v3_kernel<1><<<tn * tm, gemm3::NT, lds, st>>>(a, tn, tm); }
+    return check_launch(mode == 0 ? "i8gemm_v3_kernel<FWD>" : "i8gemm_v3_kernel<DX>");
+  }
+  dim3 grid((unsigned)ceil_div(a.Ncols, BN), (unsigned)ceil_div(a.M, BM));
+  const size_t lds = 2 * STAGE_BYTES;
   if (mode == 0) { TraceScope _ts(st, "i8gemm_kernel<0>"); i8gemm_kernel<0><<<grid, NT, lds, st>>>(a); }
   else { TraceScope _ts(st, "i8gemm_kernel<1>"); i8gemm_kernel<1><<<grid, NT, lds, st>>>(a); }
   return check_launch(mode == 0 ? "i8gemm_kernel<FWD>" : "i8gemm_kernel<DX>");

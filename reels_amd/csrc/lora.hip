@@ -40,101 +40,120 @@ __global__ void transpose_pad_kernel(const uint16_t* __restrict__ in, int64_t ro
 // rowproj: out[m][j] = bf16(sum_k src[m][k] * P[j][k]) for j < r, 0 for r <= j < rp.
 // src [M][Kd] bf16 (x or dy), P [r][Kd] bf16 (At or B). When SCALED, also writes
 // scaled[m][k] = bf16(src[m][k] * s[k]) (the dy * s operand of the DX GEMM).
-// Block = 4 waves on 32 rows; wave w takes a quarter of the k16 steps. MFMA A operand = 16 bytes
-// of one src row straight from HBM (each src byte is read once), B operand = 16 bytes of P
-// (L2-resident). The four partial 32 x (32*RT) tiles are summed in LDS in wave order.
+// HBM-bound: a block of 256 threads owns 32 rows and streams them in chunks of 256 columns. Each
+// wave-instruction loads two contiguous 512-byte row segments; the chunk goes to a padded LDS
+// tile (row stride 528 bytes: 8 consecutive rows fall in distinct banks) while the next chunk is
+// already in flight into registers. Wave w multiplies columns [64w, 64w+64) of the chunk on
+// MFMA (A = 32 src rows, B = 32 rows of P staged the same way); the four wave partials are summed
+// in wave order at the end.
+namespace rowp {
+constexpr int ROWS = 32, KC = 256, LROW = KC + 8;  // LDS row: 264 bf16 = 528 bytes
+}  // namespace rowp
+
 template <int RT, bool SCALED>
 __global__ __launch_bounds__(256) void rowproj_kernel(const uint16_t* __restrict__ src, int64_t M,
                                                       int64_t Kd, const uint16_t* __restrict__ P,
-                                                      int r, int rp, uint16_t* __restrict__ out,
+                                                      int r, int rp_, uint16_t* __restrict__ out,
                                                       const float* __restrict__ s,
                                                       uint16_t* __restrict__ scaled) {
+  using namespace rowp;
+  __shared__ __attribute__((aligned(16))) uint16_t xs[ROWS * LROW];
+  __shared__ __attribute__((aligned(16))) uint16_t ps[32 * RT * LROW];
   __shared__ float red[RT][16][64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int l32 = lane & 31, lhi = lane >> 5;
-  const int64_t m = (int64_t)blockIdx.x * 32 + l32;
-  const int64_t mc = m < M ? m : M - 1;
-  const int64_t steps = Kd / 16;
-  const int64_t per = (steps + 3) / 4;
-  const int64_t s0 = wave * per, s1 = (s0 + per < steps) ? s0 + per : steps;
+  const int64_t m0 = (int64_t)blockIdx.x * ROWS;
+  const int nchunks = (int)((Kd + KC - 1) / KC);
+  // loader roles: X chunk = 32 rows x 32 16-byte chunks, 4 per thread; P chunk = 32RT rows, 4RT
+  u32x4 rx[4], rpv[4 * RT];
+  auto load = [&](int ck) {
+    const int64_t k0 = (int64_t)ck * KC;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = (t >> 5) + 8 * i, c = t & 31;
+      const int64_t m = m0 + row, k = k0 + c * 8;
+      u32x4 v = {0, 0, 0, 0};
+      if (m < M && k < Kd) v = *reinterpret_cast<const u32x4*>(src + m * Kd + k);
+      rx[i] = v;
+    }
+#pragma unroll
+    for (int i = 0; i < 4 * RT; ++i) {
+      const int row = (t >> 5) + 8 * i, c = t & 31;
+      const int64_t k = k0 + c * 8;
+      u32x4 v = {0, 0, 0, 0};
+      if (row < r && k < Kd) v = *reinterpret_cast<const u32x4*>(P + (int64_t)row * Kd + k);
+      rpv[i] = v;
+    }
+  };
+  auto stash = [&](int ck) {
+    const int64_t k0 = (int64_t)ck * KC;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = (t >> 5) + 8 * i, c = t & 31;
+      *reinterpret_cast<u32x4*>(&xs[row * LROW + c * 8]) = rx[i];
+      if (SCALED) {
+        const int64_t m = m0 + row, k = k0 + c * 8;
+        if (m < M && k < Kd) {
+          const f32x4 sa = *reinterpret_cast<const f32x4*>(s + k);
+          const f32x4 sb = *reinterpret_cast<const f32x4*>(s + k + 4);
+          const u32x4 x = rx[i];
+          u32x4 o;
+          o[0] = pack_bf16x2(bf16_lo(x[0]) * sa[0], bf16_hi(x[0]) * sa[1]);
+          o[1] = pack_bf16x2(bf16_lo(x[1]) * sa[2], bf16_hi(x[1]) * sa[3]);
+          o[2] = pack_bf16x2(bf16_lo(x[2]) * sb[0], bf16_hi(x[2]) * sb[1]);
+          o[3] = pack_bf16x2(bf16_lo(x[3]) * sb[2], bf16_hi(x[3]) * sb[3]);
+          *reinterpret_cast<u32x4*>(scaled + m * Kd + k) = o;
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4 * RT; ++i) {
+      const int row = (t >> 5) + 8 * i, c = t & 31;
+      *reinterpret_cast<u32x4*>(&ps[row * LROW + c * 8]) = rpv[i];
+    }
+  };
   f32x16 acc[RT];
 #pragma unroll
-  for (int t = 0; t < RT; ++t)
+  for (int j = 0; j < RT; ++j)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) acc[t][v] = 0.0f;
-  const uint16_t* srow = src + mc * Kd + lhi * 8;
-  constexpr int U = 8;
-  int64_t st = s0;
-  for (; st + U <= s1; st += U) {
-    u32x4 xv[U];
+    for (int v = 0; v < 16; ++v) acc[j][v] = 0.0f;
+  load(0);
+  for (int ck = 0; ck < nchunks; ++ck) {
+    stash(ck);
+    __syncthreads();
+    if (ck + 1 < nchunks) load(ck + 1);
 #pragma unroll
-    for (int u = 0; u < U; ++u) xv[u] = *reinterpret_cast<const u32x4*>(srow + (st + u) * 16);
+    for (int ks = 0; ks < 4; ++ks) {
+      const int col = wave * 64 + ks * 16 + lhi * 8;
+      const bf16x8 a = as_bf16x8(*reinterpret_cast<const u32x4*>(&xs[l32 * LROW + col]));
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t k = (st + u) * 16 + lhi * 8;
-      if (SCALED && m < M) {
-        f32x4 sa = *reinterpret_cast<const f32x4*>(s + k);
-        f32x4 sb = *reinterpret_cast<const f32x4*>(s + k + 4);
-        u32x4 o;
-        o[0] = pack_bf16x2(bf16_lo(xv[u][0]) * sa[0], bf16_hi(xv[u][0]) * sa[1]);
-        o[1] = pack_bf16x2(bf16_lo(xv[u][1]) * sa[2], bf16_hi(xv[u][1]) * sa[3]);
-        o[2] = pack_bf16x2(bf16_lo(xv[u][2]) * sb[0], bf16_hi(xv[u][2]) * sb[1]);
-        o[3] = pack_bf16x2(bf16_lo(xv[u][3]) * sb[2], bf16_hi(xv[u][3]) * sb[3]);
-        *reinterpret_cast<u32x4*>(scaled + m * Kd + k) = o;
-      }
-      const u32x4 xm = m < M ? xv[u] : u32x4{0, 0, 0, 0};
-#pragma unroll
-      for (int t = 0; t < RT; ++t) {
-        const int j = t * 32 + l32;
-        u32x4 pv = {0, 0, 0, 0};
-        if (j < r) pv = *reinterpret_cast<const u32x4*>(P + (int64_t)j * Kd + k);
-        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(xm), as_bf16x8(pv), acc[t], 0, 0, 0);
+      for (int j = 0; j < RT; ++j) {
+        const bf16x8 bv = as_bf16x8(*reinterpret_cast<const u32x4*>(&ps[(j * 32 + l32) * LROW + col]));
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bv, acc[j], 0, 0, 0);
       }
     }
+    __syncthreads();
   }
-  for (; st < s1; ++st) {
-    const int64_t k = st * 16 + lhi * 8;
-    u32x4 xv = *reinterpret_cast<const u32x4*>(srow + st * 16);
-    if (SCALED && m < M) {
-      f32x4 sa = *reinterpret_cast<const f32x4*>(s + k);
-      f32x4 sb = *reinterpret_cast<const f32x4*>(s + k + 4);
-      u32x4 o;
-      o[0] = pack_bf16x2(bf16_lo(xv[0]) * sa[0], bf16_hi(xv[0]) * sa[1]);
-      o[1] = pack_bf16x2(bf16_lo(xv[1]) * sa[2], bf16_hi(xv[1]) * sa[3]);
-      o[2] = pack_bf16x2(bf16_lo(xv[2]) * sb[0], bf16_hi(xv[2]) * sb[1]);
-      o[3] = pack_bf16x2(bf16_lo(xv[3]) * sb[2], bf16_hi(xv[3]) * sb[3]);
-      *reinterpret_cast<u32x4*>(scaled + m * Kd + k) = o;
-    }
-    if (m >= M) xv = u32x4{0, 0, 0, 0};
-#pragma unroll
-    for (int t = 0; t < RT; ++t) {
-      const int j = t * 32 + l32;
-      u32x4 pv = {0, 0, 0, 0};
-      if (j < r) pv = *reinterpret_cast<const u32x4*>(P + (int64_t)j * Kd + k);
-      acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(xv), as_bf16x8(pv), acc[t], 0, 0, 0);
-    }
-  }
+  if (out == nullptr) return;
   // D lane layout: row (token) = (v/4)*8 + lhi*4 + v%4, column (j) = t*32 + l32.
   // Sum the four wave partials in wave order (deterministic), one wave at a time.
   for (int w = 0; w < 4; ++w) {
     if (wave == w) {
 #pragma unroll
-      for (int t = 0; t < RT; ++t)
+      for (int j = 0; j < RT; ++j)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) red[t][v][lane] = (w == 0 ? 0.0f : red[t][v][lane]) + acc[t][v];
+        for (int v = 0; v < 16; ++v) red[j][v][lane] = (w == 0 ? 0.0f : red[j][v][lane]) + acc[j][v];
     }
     __syncthreads();
   }
-  if (out == nullptr) return;
-  // 256 threads finalise 32 rows x (32*RT) columns
-  for (int idx = threadIdx.x; idx < 32 * 32 * RT; idx += 256) {
-    const int t = idx / 1024, rem = idx % 1024;
-    const int row = rem / 32, col = rem % 32;  // row = token within block, col = j within tile
+  for (int idx = t; idx < 32 * 32 * RT; idx += 256) {
+    const int j0 = idx / 1024, rem = idx % 1024;
+    const int row = rem / 32, col = rem % 32;
     const int v = (row / 8) * 4 + (row % 4), ln = ((row / 4) & 1) * 32 + col;
-    const float sum = red[t][v][ln];
-    const int64_t mm = (int64_t)blockIdx.x * 32 + row;
-    const int j = t * 32 + col;
-    if (mm < M && j < rp) out[mm * rp + j] = j < r ? (uint16_t)f32_to_bf16_bits(sum) : (uint16_t)0;
+    const float sum = red[j0][v][ln];
+    const int64_t mm = m0 + row;
+    const int j = j0 * 32 + col;
+    if (mm < M && j < rp_) out[mm * rp_ + j] = j < r ? (uint16_t)f32_to_bf16_bits(sum) : (uint16_t)0;
   }
 }
 
@@ -171,25 +190,44 @@ __global__ __launch_bounds__(256) void colgrad_kernel(const uint16_t* __restrict
 
   const int g = lane >> 4, i16 = lane & 15;
   const int jj = i16 >> 2, qq = i16 & 3;  // providing-lane roles for the transpose reads
-  for (int64_t mb = mbeg; mb < mend; mb += TM) {
-    // src tile [64 tokens][128 o]: 1024 chunks of 8 bf16, 4 per thread
+  // register staging of the next token step: src tile [64 tokens][128 o] (4 chunks per thread),
+  // Lm tile [64 tokens][32*RT] (RT chunks per thread)
+  u32x4 rs[4], rl[RT];
+  auto load = [&](int64_t mb) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int id = tid + 256 * i, row = id >> 4, c = id & 15;
       const int64_t m = mb + row, o = o0 + c * 8;
       u32x4 v = {0, 0, 0, 0};
       if (m < mend && o < Od) v = *reinterpret_cast<const u32x4*>(src + m * Od + o);
-      *reinterpret_cast<u32x4*>(&ssrc[row * SROW + c * 8]) = v;
+      rs[i] = v;
     }
-    // Lm tile [64 tokens][32*RT]
-    for (int id = tid; id < TM * RT * 4; id += 256) {
-      const int row = id / (RT * 4), c = id % (RT * 4);
+#pragma unroll
+    for (int i = 0; i < RT; ++i) {
+      const int id = tid + 256 * i, row = id / (RT * 4), c = id % (RT * 4);
       const int64_t m = mb + row;
       u32x4 v = {0, 0, 0, 0};
-      if (m < mend && c * 8 < rp) v = *reinterpret_cast<const u32x4*>(Lm + m * rp + c * 8);
-      *reinterpret_cast<u32x4*>(&slm[row * LROW + c * 8]) = v;
+      if (row < TM && m < mend && c * 8 < rp) v = *reinterpret_cast<const u32x4*>(Lm + m * rp + c * 8);
+      rl[i] = v;
     }
+  };
+  auto stash = [&]() {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int id = tid + 256 * i, row = id >> 4, c = id & 15;
+      *reinterpret_cast<u32x4*>(&ssrc[row * SROW + c * 8]) = rs[i];
+    }
+#pragma unroll
+    for (int i = 0; i < RT; ++i) {
+      const int id = tid + 256 * i, row = id / (RT * 4), c = id % (RT * 4);
+      if (row < TM) *reinterpret_cast<u32x4*>(&slm[row * LROW + c * 8]) = rl[i];
+    }
+  };
+  if (mbeg < mend) load(mbeg);
+  for (int64_t mb = mbeg; mb < mend; mb += TM) {
+    stash();
     __syncthreads();
+    if (mb + TM < mend) load(mb + TM);
 #pragma unroll
     for (int ks = 0; ks < TM / 16; ++ks) {
       // A operand: src^T rows o = wave*32 + (0..31), tokens ks*16 + (lane/32)*8 + (0..7)
@@ -348,9 +386,9 @@ static Plan make_plan(int64_t M, int64_t K, int64_t N, int64_t r, bool ptrs_alig
   Plan p;
   p.fast = ptrs_aligned && (K % 16 == 0) && (N % 16 == 0) && (r % 16 == 0) && r <= 128;
   p.rp = (int)r;
-  int64_t s = (M + 2047) / 2048;
+  int64_t s = (M + 1023) / 1024;
   if (s < 1) s = 1;
-  if (s > 16) s = 16;
+  if (s > 32) s = 32;
   p.tps = ((M + s - 1) / s + 63) / 64 * 64;
   if (p.tps < 64) p.tps = 64;
   p.splits = (int)((M + p.tps - 1) / p.tps);
@@ -386,7 +424,7 @@ static int grid1(int64_t n, int bs = 256) { return (int)ceil_div(n, bs); }
 
 static int launch_rowproj(const uint16_t* src, int64_t M, int64_t Kd, const uint16_t* P, int r,
                           int rp, uint16_t* out, const float* s, uint16_t* scaled, hipStream_t st) {
-  const dim3 grid((unsigned)ceil_div(M, 32));
+  const dim3 grid((unsigned)ceil_div(M, rowp::ROWS));
   const int rt = (r + 31) / 32;
   if (scaled) {
     if (rt <= 1) { TraceScope _ts(st, "rowproj_kernel<1,true>"); rowproj_kernel<1, true><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, s, scaled); }

@@ -51,22 +51,43 @@ __device__ __forceinline__ float wave_max(float v) {
 
 // Quantizes E values with one scale; returns codes packed little-endian (E/4 dwords) and sets
 // bad if any code is non-finite (Julia: Int8(NaN) throws InexactError).
+//
+// Exact shortcut for the IEEE division: when the scale s is a normal float, inv = fl(1/s) is
+// computed once per row and t = fl(w * inv) differs from w/s by at most 2^-23 |w/s| <= 2^-16
+// (|w/s| <= 127 * (1 + 2^-23)), while the correctly rounded quotient fl(w/s) differs from w/s by at
+// most 2^-17. Whenever t lies more than 2^-12 away from every half-integer, t and fl(w/s) are
+// on the same side of it, so rint(clamp(t)) == rint(clamp(fl(w/s))) — the reference's code. The
+// few elements within 2^-12 of a half-integer (and rows whose scale is 0, denormal, Inf or NaN)
+// take the IEEE division itself, so every code is bit-identical to quantization.jl:41-42.
+__device__ __forceinline__ int quantize_one(float w, float scale, float inv, bool fast, bool& bad) {
+  float t = w * inv;
+  const float rt = __builtin_rintf(t);
+  if (!fast || __builtin_fabsf(t - rt) > 0.5f - 0x1p-12f) t = w / scale;
+  const float c = t > 127.0f ? 127.0f : (t < -127.0f ? -127.0f : t);
+  const float rd = __builtin_rintf(c);
+  if (__builtin_isfinite(rd)) return (int)rd;
+  bad = true;
+  return 0;
+}
+
 template <int E>
-__device__ __forceinline__ void quantize_chunk(const float* v, float scale, uint32_t* out, bool& bad) {
+__device__ __forceinline__ void quantize_chunk(const float* v, float scale, float inv, bool fast,
+                                               uint32_t* out, bool& bad) {
 #pragma unroll
   for (int d = 0; d < E / 4; ++d) {
     uint32_t word = 0;
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-      float t = v[d * 4 + b] / scale;
-      float c = t > 127.0f ? 127.0f : (t < -127.0f ? -127.0f : t);
-      float rd = __builtin_rintf(c);
-      int code = 0;
-      if (__builtin_isfinite(rd)) code = (int)rd; else bad = true;
+      const int code = quantize_one(v[d * 4 + b], scale, inv, fast, bad);
       word |= ((uint32_t)(code & 0xff)) << (8 * b);
     }
     out[d] = word;
   }
+}
+
+// scale is a finite normal float: the multiply shortcut applies (see quantize_one)
+__device__ __forceinline__ bool fast_scale(float scale) {
+  return scale >= 0x1p-126f && scale <= 3.4028234663852886e38f;
 }
 
 template <typename T, int MAXC>
@@ -120,6 +141,8 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(const T* __restrict__ w,
   float scale = m / 127.0f;
   if (m == 0.0f) scale = 1.0f;
   if (lane == 0) scales[n] = scale;
+  const bool fast = fast_scale(scale);
+  const float inv = fast ? 1.0f / scale : 0.0f;
 
   bool bad = false;
   int8_t* qrow = q + n * K;
@@ -131,7 +154,7 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(const T* __restrict__ w,
         float v[E];
         Elem<T>::unpack(cache[i], v);
         uint32_t out[E / 4];
-        quantize_chunk<E>(v, scale, out, bad);
+        quantize_chunk<E>(v, scale, inv, fast, out, bad);
         if (E == 8) {
           u32x2 o = {out[0], out[1 % (E / 4)]};
           *reinterpret_cast<u32x2*>(qrow + c * E) = o;
@@ -145,7 +168,7 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(const T* __restrict__ w,
       float v[E];
       Elem<T>::unpack(row[c], v);
       uint32_t out[E / 4];
-      quantize_chunk<E>(v, scale, out, bad);
+      quantize_chunk<E>(v, scale, inv, fast, out, bad);
       if (E == 8) {
         u32x2 o = {out[0], out[1 % (E / 4)]};
         *reinterpret_cast<u32x2*>(qrow + c * E) = o;

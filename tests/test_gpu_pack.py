@@ -126,3 +126,21 @@ def test_pack_wan14b_ffn_matrices_full(dev, N, K):
     # full-size 14B FFN weights with 0.1% outliers at 20 sigma, bit-exact
     w = oracle.normal_bf16(400 + N, (N, K), 0.02, outlier_rate=1e-3)
     check(dev, w, "bf16")
+
+
+def test_pack_near_ties_take_exact_division(dev):
+    # rows whose w/s lands on or within a few ulps of a half-integer for arbitrary scales: the
+    # kernel's multiply shortcut must hand these to the IEEE division (codes bit-exact)
+    rng = np.random.default_rng(77)
+    rows = []
+    for _ in range(512):
+        absmax = np.float32(rng.uniform(1e-3, 10.0))
+        s = np.float32(absmax / np.float32(127.0))
+        k = rng.integers(-126, 126, size=63).astype(np.float64)
+        d = rng.choice([0.0, 1e-7, -1e-7, 2e-6, -2e-6, 3e-5, -3e-5, 1e-3], size=63)
+        vals = ((k + 0.5 + d) * np.float64(s)).astype(F32)
+        vals = np.clip(vals, -absmax, absmax)
+        rows.append(np.concatenate([[absmax], vals]).astype(F32))
+    w = np.stack(rows)
+    check(dev, w, "f32")
+    check(dev, oracle.f32_to_bf16(w), "bf16")
