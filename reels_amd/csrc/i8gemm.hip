@@ -233,6 +233,28 @@ void i8gemm_kernel(GemmArgs a) {
   }
 }
 
+// HBM -> LDS copy of 16 bytes per lane (buffer_load_dwordx4 ... lds): lane i's data lands at
+// LDS byte ldsaddr + 16 i (ldsaddr in M0). Issued through inline asm so the compiler does not
+// order the kernel's LDS reads behind it: the kernel synchronises these copies itself (explicit
+// vmcnt waits followed by a workgroup barrier).
+typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4;
+__device__ __forceinline__ i32x4 buffer_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  i32x4 r;
+  r[0] = (int)(uint32_t)b;
+  r[1] = (int)((b >> 32) & 0xffffu);  // stride 0
+  r[2] = (int)bytes;                  // num_records: reads past it return 0
+  r[3] = 0x00020000;                  // raw buffer, 32-bit data format
+  return r;
+}
+__device__ __forceinline__ void dma16(const i32x4& rsrc, uint32_t voff, uint32_t soff,
+                                      const uint8_t* lds) {
+  const uint32_t ldsaddr = (uint32_t)(uintptr_t)LDS_PTR(const uint8_t, lds);
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc), "s"(soff),
+               "{m0}"(ldsaddr)
+               : "memory");
+}
+
 // FWD weight tile of the three-stage kernel: [256 n][64 k] int8, 16-byte slots XOR-swizzled
 // within the 64-byte row so 32-row fragment reads (ds_read_b128) hit distinct banks
 __device__ __forceinline__ int wf2_swz(int row) { return ((row >> 1) & 3) ^ ((row >> 3) & 1); }
@@ -290,10 +312,8 @@ void i8gemm_v3_kernel(GemmArgs a, int tiles_n, int tiles_m) {
   const int64_t m0 = (int64_t)(first_m + within % gm) * BM;
   const int64_t n0 = (int64_t)(within / gm) * BN;
 
-  const __amdgpu_buffer_rsrc_t ract =
-      __builtin_amdgcn_make_buffer_rsrc((void*)a.act, (short)0, (int)(M * Kred * 2), 0x00020000);
-  const __amdgpu_buffer_rsrc_t rq =
-      __builtin_amdgcn_make_buffer_rsrc((void*)a.q, (short)0, (int)(Ncols * Kred), 0x00020000);
+  const i32x4 ract = buffer_rsrc(a.act, (uint32_t)(M * Kred * 2));
+  const i32x4 rq = buffer_rsrc(a.q, (uint32_t)(Ncols * Kred));
   uint32_t voa[4], vow[2];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -324,12 +344,10 @@ void i8gemm_v3_kernel(GemmArgs a, int tiles_n, int tiles_m) {
     const uint32_t sw = MODE == 0 ? (uint32_t)kt * BK : (uint32_t)kt * (uint32_t)(BK * a.ldq);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ract, LDS_PTR(void, base + (w * 4 + i) * 1024), 16,
-                                               voa[i], sa, 0, 0);
+      dma16(ract, voa[i], sa, base + (w * 4 + i) * 1024);
 #pragma unroll
     for (int i = 0; i < 2; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, LDS_PTR(void, base + ACT + (w * 2 + i) * 1024), 16,
-                                               vow[i], sw, 0, 0);
+      dma16(rq, vow[i], sw, base + ACT + (w * 2 + i) * 1024);
   };
 
   f32x16 acc[2][4];
@@ -340,21 +358,24 @@ void i8gemm_v3_kernel(GemmArgs a, int tiles_n, int tiles_m) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  auto compute = [&](int stage) {
-    const uint8_t* sa = smem + stage * STAGE;
-    const uint8_t* sw = sa + ACT;
-    auto xchunk = [&](int s) { return MODE == 0 ? 4 * (s >> 1) + 2 * lhi + (s & 1) : 2 * s + lhi; };
-    auto read_x = [&](int s, bf16x8* xf) {
-      const int c = xchunk(s);
+  // ---- k loop ----------------------------------------------------------------------------
+  // Registers carry, across the barrier, the weight fragments of the next step and the
+  // activation fragments of its first MFMA sub-step: the barrier (and the wait for the next
+  // stage's loads) sits before the last sub-step of each step, whose MFMAs then cover the LDS
+  // latency of the next step's first reads. Stage j+2 is issued right after the barrier of step
+  // j, into the buffer of step j-1, which every wave has finished reading by then.
+  auto xchunk = [&](int s) { return MODE == 0 ? 4 * (s >> 1) + 2 * lhi + (s & 1) : 2 * s + lhi; };
+  auto read_x = [&](const uint8_t* sa, int s, bf16x8* xf) {
+    const int c = xchunk(s);
 #pragma unroll
-      for (int tj = 0; tj < 4; ++tj) {
-        const int row = wm * 128 + tj * 32 + l32;
-        xf[tj] = as_bf16x8(*reinterpret_cast<const u32x4*>(sa + row * 128 + ((c ^ act_swz(row)) << 4)));
-      }
-    };
-    bf16x8 xf0[4], xf1[4];
-    u32x4 wr[2][2];
-    i32x2 wt[4][2];
+    for (int tj = 0; tj < 4; ++tj) {
+      const int row = wm * 128 + tj * 32 + l32;
+      xf[tj] = as_bf16x8(*reinterpret_cast<const u32x4*>(sa + row * 128 + ((c ^ act_swz(row)) << 4)));
+    }
+  };
+  u32x4 wr[2][2];   // FWD: raw int8 weight slots [pair][ti]
+  i32x2 wt[4][2];   // DX: transposed raw int8 [step][ti]
+  auto read_w = [&](const uint8_t* sw) {
     if (MODE == 0) {
 #pragma unroll
       for (int pp = 0; pp < 2; ++pp)
@@ -376,50 +397,70 @@ void i8gemm_v3_kernel(GemmArgs a, int tiles_n, int tiles_m) {
           wt[kk][ti] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(LDS_PTR(i32x2, p));
         }
     }
-    // LLVM's GEMM interleave strategies (1 for FWD, 0 for DX measured fastest): LDS reads are
-    // hoisted well ahead of their MFMAs with counted lgkmcnt waits.
-    __builtin_amdgcn_iglp_opt(MODE == 0 ? 1 : 0);
-    read_x(0, xf0);
+  };
+  auto convert = [&](int s, bf16x8* af) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      bf16x8* cur = (s & 1) ? xf1 : xf0;
-      bf16x8* nxt = (s & 1) ? xf0 : xf1;
-      bf16x8 af[2];
-#pragma unroll
-      for (int ti = 0; ti < 2; ++ti) {
-        if (MODE == 0) {
-          const u32x4& r = wr[s >> 1][ti];
-          af[ti] = (s & 1) ? i8x8_to_bf16x8(r[2], r[3]) : i8x8_to_bf16x8(r[0], r[1]);
-        } else {
-          af[ti] = i8x8_to_bf16x8((uint32_t)wt[s][ti][0], (uint32_t)wt[s][ti][1]);
-        }
+    for (int ti = 0; ti < 2; ++ti) {
+      if (MODE == 0) {
+        const u32x4& r = wr[s >> 1][ti];
+        af[ti] = (s & 1) ? i8x8_to_bf16x8(r[2], r[3]) : i8x8_to_bf16x8(r[0], r[1]);
+      } else {
+        af[ti] = i8x8_to_bf16x8((uint32_t)wt[s][ti][0], (uint32_t)wt[s][ti][1]);
       }
-      if (s < 3) read_x(s + 1, nxt);
-#pragma unroll
-      for (int tj = 0; tj < 4; ++tj)
-#pragma unroll
-        for (int ti = 0; ti < 2; ++ti)
-          acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ti], cur[tj], acc[ti][tj], 0, 0, 0);
     }
   };
+  auto mfma8 = [&](const bf16x8* af, const bf16x8* xf) {
+#pragma unroll
+    for (int tj = 0; tj < 4; ++tj)
+#pragma unroll
+      for (int ti = 0; ti < 2; ++ti)
+        acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ti], xf[tj], acc[ti][tj], 0, 0, 0);
+  };
 
+  bf16x8 xa[4], xb[4], af[2];
   issue(0, 0);
   if (nk > 1) issue(1, 1);
+  if (nk > 1) __builtin_amdgcn_s_waitcnt(0x0F76);  // vmcnt(6): stage 1 may stay in flight
+  else __builtin_amdgcn_s_waitcnt(0x0F70);
+  __builtin_amdgcn_s_barrier();
+  read_w(smem + ACT);
+  read_x(smem, 0, xa);
   for (int kt = 0; kt < nk; ++kt) {
-    if (kt + 1 < nk) __builtin_amdgcn_s_waitcnt(0x0F76);  // vmcnt(6): stage kt+1 may stay in flight
-    else __builtin_amdgcn_s_waitcnt(0x0F70);              // vmcnt(0)
-    __builtin_amdgcn_s_barrier();
-    if (kt + 2 < nk) issue(kt + 2, (kt + 2) % NSTAGE);
-    compute(kt % NSTAGE);
+    const uint8_t* sa = smem + (kt % NSTAGE) * STAGE;
+    __builtin_amdgcn_iglp_opt(MODE == 0 ? 1 : 0);
+    convert(0, af);
+    read_x(sa, 1, xb);
+    mfma8(af, xa);
+    convert(1, af);
+    read_x(sa, 2, xa);
+    mfma8(af, xb);
+    convert(2, af);
+    read_x(sa, 3, xb);
+    mfma8(af, xa);
+    convert(3, af);
+    if (kt + 1 < nk) {
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): stage kt+1 has landed
+      __builtin_amdgcn_s_barrier();
+      if (kt + 2 < nk) issue(kt + 2, (kt + 2) % NSTAGE);
+      const uint8_t* sn = smem + ((kt + 1) % NSTAGE) * STAGE;
+      read_w(sn + ACT);
+      read_x(sn, 0, xa);
+    }
+    mfma8(af, xb);
   }
 
-  // ---- epilogue: wave owns 64 columns x 128 tokens ---------------------------------------
+  // ---- epilogue: scale, LoRA up-projection on MFMA, bias, one bf16 rounding; the finished
+  // 256 x 256 bf16 tile is staged in LDS (rows of 512 bytes, 16-byte chunks XOR-swizzled by row)
+  // and written to HBM as whole 512-byte row segments.
+  __syncthreads();  // every wave is done reading the last stage
+  uint8_t* stile = smem;
   const int nsteps = a.rp >> 4;
 #pragma unroll
   for (int ti = 0; ti < 2; ++ti) {
     const int64_t nrow = n0 + wn * 64 + ti * 32 + l32;
     const int64_t nrc = nrow < Ncols ? nrow : Ncols - 1;
-    const int64_t nbase = n0 + wn * 64 + ti * 32 + lhi * 4;
+    const int nloc = wn * 64 + ti * 32 + lhi * 4;  // tile-local column of this lane's group 0
+    const int64_t nbase = n0 + nloc;
     float sc[16], bs[16];
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
@@ -436,7 +477,8 @@ void i8gemm_v3_kernel(GemmArgs a, int tiles_n, int tiles_m) {
     }
 #pragma unroll
     for (int tj = 0; tj < 4; ++tj) {
-      const int64_t m = m0 + wm * 128 + tj * 32 + l32;
+      const int mloc = wm * 128 + tj * 32 + l32;
+      const int64_t m = m0 + mloc;
       const int64_t mc = m < M ? m : M - 1;
       f32x16 lo;
 #pragma unroll
@@ -448,22 +490,30 @@ void i8gemm_v3_kernel(GemmArgs a, int tiles_n, int tiles_m) {
         if (m >= M) lv = u32x4{0, 0, 0, 0};
         lo = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(rv), as_bf16x8(lv), lo, 0, 0, 0);
       }
-      if (m < M) {
 #pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          const int64_t n = nbase + g4 * 8;
-          if (n < Ncols) {
-            float o[4];
+      for (int g4 = 0; g4 < 4; ++g4) {
+        float o[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int v = g4 * 4 + e;
-              o[e] = sc[v] * acc[ti][tj][v] + a.c * lo[v] + bs[v];
-            }
-            u32x2 pk = {pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
-            *reinterpret_cast<u32x2*>(a.out + m * Ncols + n) = pk;
-          }
+        for (int e = 0; e < 4; ++e) {
+          const int v = g4 * 4 + e;
+          o[e] = sc[v] * acc[ti][tj][v] + a.c * lo[v] + bs[v];
         }
+        const u32x2 pk = {pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+        const int col = nloc + g4 * 8;                       // 4 columns, 8 bytes
+        const int chunk = (col >> 3) ^ (mloc & 31);          // 16-byte chunk, swizzled
+        *reinterpret_cast<u32x2*>(stile + mloc * 512 + chunk * 16 + (col & 7) * 2) = pk;
       }
+    }
+  }
+  __syncthreads();
+  // 256 rows x 32 chunks of 16 bytes; a wave stores two whole 512-byte row segments per instruction
+#pragma unroll 4
+  for (int i = 0; i < 16; ++i) {
+    const int id = t + 512 * i, row = id >> 5, c = id & 31;
+    const int64_t m = m0 + row, n = n0 + c * 8;
+    if (m < M && n < Ncols) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(stile + row * 512 + ((c ^ (row & 31)) << 4));
+      *reinterpret_cast<u32x4*>(a.out + m * Ncols + n) = v;
     }
   }
 }
