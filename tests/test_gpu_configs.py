@@ -1,0 +1,150 @@
+"""GPU parity on the remaining BASELINE workloads:
+  * cross-attention K/V projections 5120->5120 with 77 / 333 / 512 text tokens (skinny M);
+  * Wan-2.1-1.3B projections at 32760 tokens (q/k/v/o 1536^2, ffn 1536<->8960; sampled rows
+    against the oracle, exact doubling identities over the whole output);
+  * the 1.3B linear stack chained through gelu_tanh (q -> k -> v -> o -> ffn.0 -> GELU -> ffn.2),
+    two layers at 128 tokens: every linear's forward and backward checked against the oracle
+    on the GPU's own intermediates, and the end-to-end drift against an all-oracle chain.
+Tolerances as tests/_util.assert_parity (bf16 bar 1e-2); end-to-end drift 3e-2."""
+import numpy as np
+import pytest
+
+import oracle
+from tests._util import assert_parity, bf16_bits, bf16_f32, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _weights(seed, N, K, r):
+    w = oracle.normal_bf16(seed, (N, K), 0.02)
+    q, s, st = oracle.pack(w, "bf16")
+    assert st == 0
+    A = oracle.normal_bf16(seed + 1, (K, r), 0.01)
+    B = oracle.normal_bf16(seed + 2, (r, N), 0.01)
+    return q, s, A, B
+
+
+def _dev_layer(dev, q, s, A, B):
+    from reels_amd import QuantizedMatrix
+    return QuantizedMatrix(to_dev(q, dev, "raw"), to_dev(s, dev, "raw")), to_dev(A, dev), to_dev(B, dev)
+
+
+@pytest.mark.parametrize("M", [77, 333, 512])
+def test_cross_attention_skinny_tokens(dev, M):
+    import torch
+    from reels_amd import i8lora_backward, i8lora_forward
+    K = N = 5120
+    r, c = 32, 1.0
+    q, s, A, B = _weights(900 + M, N, K, r)
+    x = oracle.normal_bf16(910 + M, (M, K), 1.0)
+    dy = oracle.normal_bf16(920 + M, (M, N), 1.0)
+    print(f"[configs] cross-attn M={M}", flush=True)
+    W, Ad, Bd = _dev_layer(dev, q, s, A, B)
+    y, h = i8lora_forward(to_dev(x, dev), W, Ad, Bd, None, c, save_h=True)
+    dx, dA, dB = i8lora_backward(to_dev(dy, dev), to_dev(x, dev), W, Ad, Bd, c, h=h)
+    torch.cuda.synchronize(dev)
+    rows = np.unique(np.concatenate([np.arange(0, M, max(1, M // 40)), np.arange(max(0, M - 8), M)]))
+    yo, _ = oracle.lora_forward(x, q, s, A, B, c, rows=rows)
+    go = oracle.lora_backward(dy, x, q, s, A, B, c, rows=rows)
+    assert_parity(bf16_f32(y)[rows], yo, f"cross-attn M={M} y")
+    assert_parity(bf16_f32(dx)[rows], go["dx"], f"cross-attn M={M} dx")
+    assert_parity(dA.cpu().numpy(), go["dA"], f"cross-attn M={M} dA")
+    assert_parity(dB.cpu().numpy(), go["dB"], f"cross-attn M={M} dB")
+
+
+@pytest.mark.parametrize("K,N", [(1536, 1536), (1536, 8960), (8960, 1536)])
+def test_wan13b_projections_full_tokens(dev, K, N):
+    import torch
+    from reels_amd import i8lora_backward, i8lora_forward
+    M, r, c = 32760, 32, 1.0
+    q, s, A, B = _weights(1000 + K + N, N, K, r)
+    x = oracle.normal_bf16(1010 + K, (M, K), 1.0)
+    dy = oracle.normal_bf16(1020 + N, (M, N), 1.0)
+    print(f"[configs] wan1.3b M={M} K={K} N={N}", flush=True)
+    W, Ad, Bd = _dev_layer(dev, q, s, A, B)
+    xd, dyd = to_dev(x, dev), to_dev(dy, dev)
+    y, h = i8lora_forward(xd, W, Ad, Bd, None, c, save_h=True)
+    dx, dA, dB = i8lora_backward(dyd, xd, W, Ad, Bd, c, h=h)
+    y2, _ = i8lora_forward(xd * 2, W, Ad, Bd, None, c)
+    dx2, dA2, dB2 = i8lora_backward(dyd * 2, xd, W, Ad, Bd, c, h=h)
+    torch.cuda.synchronize(dev)
+    assert torch.equal(y2, y * 2) and torch.equal(dx2, dx * 2)
+    assert torch.equal(dA2, dA * 2) and torch.equal(dB2, dB * 2)
+    rng = np.random.default_rng(K + N)
+    rows = np.concatenate([rng.choice(M - 32, 24, replace=False), np.arange(M - 8, M)])
+    kc = rng.choice(K, 32, replace=False)
+    nc = rng.choice(N, 32, replace=False)
+    yo, _ = oracle.lora_forward(x, q, s, A, B, c, rows=rows)
+    go = oracle.lora_backward(dy, x, q, s, A, B, c, rows=rows, kcols=kc, ncols=nc)
+    assert_parity(bf16_f32(y)[rows], yo, f"1.3B {K}x{N} y")
+    assert_parity(bf16_f32(dx)[rows], go["dx"], f"1.3B {K}x{N} dx")
+    assert_parity(dA.cpu().numpy()[kc], go["dA"], f"1.3B {K}x{N} dA")
+    assert_parity(dB.cpu().numpy()[:, nc], go["dB"], f"1.3B {K}x{N} dB")
+
+
+def test_wan13b_chain_with_gelu(dev):
+    import torch
+    from reels_amd import gelu_tanh, gelu_tanh_backward, i8lora_backward, i8lora_forward
+    M, D, F, r, c, layers = 128, 1536, 8960, 32, 1.0, 2
+    shapes = [("q", D, D), ("k", D, D), ("v", D, D), ("o", D, D), ("ffn0", D, F), ("ffn2", F, D)]
+    params = []
+    for li in range(layers):
+        for j, (name, K, N) in enumerate(shapes):
+            params.append((f"{li}.{name}", K, N) + _weights(2000 + 10 * (6 * li + j), N, K, r))
+    x0 = oracle.normal_bf16(2999, (M, D), 1.0)
+    print("[configs] 1.3B chain, 2 layers x (q,k,v,o,ffn.0,gelu,ffn.2), M=128", flush=True)
+
+    # ---- forward on the GPU, keeping every intermediate
+    acts, hs, pre_gelu = [x0], [], {}
+    cur = to_dev(x0, dev)
+    dev_params = []
+    for (name, K, N, q, s, A, B) in params:
+        W, Ad, Bd = _dev_layer(dev, q, s, A, B)
+        dev_params.append((W, Ad, Bd))
+        y, h = i8lora_forward(cur, W, Ad, Bd, None, c, save_h=True)
+        hs.append(h)
+        if name.endswith("ffn0"):
+            pre_gelu[name] = y
+            y = gelu_tanh(y)
+        cur = y
+        acts.append(bf16_bits(y))
+    torch.cuda.synchronize(dev)
+
+    # per-linear forward parity on the GPU's own inputs
+    inputs = []
+    xin = x0
+    for i, (name, K, N, q, s, A, B) in enumerate(params):
+        inputs.append(xin)
+        yo, _ = oracle.lora_forward(xin, q, s, A, B, c)
+        got = pre_gelu[name] if name.endswith("ffn0") else None
+        if got is not None:
+            assert_parity(bf16_f32(got), yo, f"chain {name} y")
+            assert np.array_equal(acts[i + 1], bf16_bits(gelu_tanh(got)))
+        else:
+            assert_parity(oracle.bf16_to_f32(acts[i + 1]), yo, f"chain {name} y")
+        xin = acts[i + 1]
+
+    # end-to-end drift against a chain computed entirely by the oracle (bf16 between layers)
+    xo = x0
+    for (name, K, N, q, s, A, B) in params:
+        yo, _ = oracle.lora_forward(xo, q, s, A, B, c)
+        yb = oracle.f32_to_bf16(yo.astype(np.float32))
+        xo = oracle.gelu_tanh(yb) if name.endswith("ffn0") else yb
+    assert_parity(oracle.bf16_to_f32(acts[-1]), oracle.bf16_to_f32(xo), "chain output drift", tol=3e-2)
+
+    # ---- backward on the GPU, layer by layer, each checked against the oracle on its inputs
+    g = oracle.normal_bf16(3999, (M, D), 1.0)
+    gd = to_dev(g, dev)
+    for i in reversed(range(len(params))):
+        name, K, N, q, s, A, B = params[i]
+        W, Ad, Bd = dev_params[i]
+        if name.endswith("ffn0"):
+            gd = gelu_tanh_backward(pre_gelu[name], gd)
+        dyb = bf16_bits(gd)
+        dx, dA, dB = i8lora_backward(gd, to_dev(inputs[i], dev), W, Ad, Bd, c, h=hs[i])
+        torch.cuda.synchronize(dev)
+        go = oracle.lora_backward(dyb, inputs[i], q, s, A, B, c)
+        assert_parity(bf16_f32(dx), go["dx"], f"chain {name} dx")
+        assert_parity(dA.cpu().numpy(), go["dA"], f"chain {name} dA")
+        assert_parity(dB.cpu().numpy(), go["dB"], f"chain {name} dB")
+        gd = dx
