@@ -32,6 +32,13 @@ PEAK_HBM_GBS = 8000.0
 TOKENS = 32760
 RANK = 32
 ALPHA = 32.0
+# HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs of this script (KiB per
+# dispatch scaled by a 1 GiB device copy: FETCH x 2.0, WRITE x 1.0), averaged over one step's
+# launches; the commands and per-kernel figures are in profiles/.
+GEMM_TRAFFIC_BYTES = 3313369504
+GEMM_TRAFFIC_NOTE = ("mean over one step's 12 GEMM launches (q/k/v/o 2.20 GB, ffn 5.34-5.75 GB); "
+                     "FETCH_SIZE includes Infinity Cache hits; algorithmic mean 0.905 GB")
+PACK_TRAFFIC_BYTES = 14792000000  # mean of the two launches (21.088 + 8.496 GB), ratio 1.000
 PROJECTIONS = [("self_attn.q", 5120, 5120), ("self_attn.k", 5120, 5120),
                ("self_attn.v", 5120, 5120), ("self_attn.o", 5120, 5120),
                ("ffn.0", 5120, 13824), ("ffn.2", 13824, 5120)]
@@ -55,7 +62,32 @@ def parse():
                     help="approximate CPU work for the cpu_baseline sample (0 disables it)")
     ap.add_argument("--tokens", type=int, default=TOKENS)
     ap.add_argument("--no-pack", action="store_true", help="skip the pack workload")
+    ap.add_argument("--pack-only", action="store_true", help="run only the pack workload")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run three 1 GiB device-to-device copies (the reference kernel for "
+                         "scaling FETCH_SIZE / WRITE_SIZE counters to bytes) and exit")
     return ap.parse_args()
+
+
+def vendor_gemm_tflops(dev, M, K, N, reps=5):
+    """bf16 x bf16 -> bf16 torch.matmul (hipBLASLt) on one Wan-14B projection shape: the
+    practical MFMA ceiling for a dense GEMM of this size on this GPU, measured in the same run."""
+    import torch
+    x = torch.randn((M, K), device=dev).to(torch.bfloat16)
+    w = torch.randn((N, K), device=dev).to(torch.bfloat16)
+    for _ in range(2):
+        torch.matmul(x, w.t())
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        torch.matmul(x, w.t())
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    del x, w
+    torch.cuda.empty_cache()
+    return 2.0 * M * N * K / (ms * 1e-3) / 1e12
 
 
 PACK_LAYERS = 40
@@ -111,7 +143,7 @@ def pack_bench(dev, reps=3):
            "elements": elems, "bytes": nbytes,
            "roofline": {"kernel": "pack_rows_kernel", "bound": "hbm", "achieved": round(gbs, 1),
                         "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
-                        "traffic": None}}
+                        "traffic": PACK_TRAFFIC_BYTES}}
     del mats
     torch.cuda.empty_cache()
     return out
@@ -211,7 +243,18 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.calibrate_copy:
+        a = torch.empty((1 << 30,), dtype=torch.uint8, device=dev).fill_(1)
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print("copied 3 x 1 GiB device to device")
+        return
     L = _lib.lib()
+    if args.pack_only:
+        print(json.dumps({"pack": pack_bench(dev)}))
+        return
     gen = torch.Generator(device=dev).manual_seed(1234)
     M = args.tokens
     projs = [Projection(n, K, N, M, RANK, dev, gen) for (n, K, N) in PROJECTIONS]
@@ -257,12 +300,20 @@ def main():
             gemm_fl["dx"] += gemm_flops("dx", M, pr.K, pr.N, RANK)
     tot_ms = gemm_ms["fwd"] + gemm_ms["dx"]
     achieved = (gemm_fl["fwd"] + gemm_fl["dx"]) / (tot_ms * 1e-3) / 1e12 if tot_ms > 0 else 0.0
+    gemm_names = sorted({n for (n, _) in recs if n.startswith("i8gemm")})
+    vendor = vendor_gemm_tflops(dev, M, 5120, 5120)
     roofline = {
-        "kernel": "i8gemm_v3_kernel (fwd <0> and dX <1>, int8 weight converted to bf16 for MFMA)",
+        "kernel": " + ".join(gemm_names) + " (<0> fwd, <1> dX; int8 weight converted to bf16 "
+                                           "for MFMA)",
         "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
-        "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+        "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+        "traffic": GEMM_TRAFFIC_BYTES,
+        "traffic_note": GEMM_TRAFFIC_NOTE,
         "avg_launch_ms": {k: round(gemm_ms[k] / max(gemm_n[k], 1), 4) for k in gemm_ms},
         "launches": gemm_n,
+        "vendor_bf16_gemm": {"what": f"torch.matmul bf16 (hipBLASLt), {M}x5120 by 5120x5120, "
+                                     "same run", "tflops": round(vendor, 1),
+                             "achieved_over_vendor": round(achieved / vendor, 4)},
     }
     kernels = {n: {"launches": c, "avg_ms": round(t / c, 4), "ms_per_step": round(t / args.steps, 4)}
                for n, (c, t) in sorted(kern.items(), key=lambda kv: -kv[1][1])}

@@ -247,11 +247,14 @@ __device__ __forceinline__ i32x4 buffer_rsrc(const void* base, uint32_t bytes) {
   r[3] = 0x00020000;                  // raw buffer, 32-bit data format
   return r;
 }
+// The compiler writes M0 right before the asm but does not know that the copy reads it: on
+// this GPU generation an LDS-DMA instruction needs one wait state after an SALU write of M0,
+// hence the s_nop.
 __device__ __forceinline__ void dma16(const i32x4& rsrc, uint32_t voff, uint32_t soff,
                                       const uint8_t* lds) {
   const uint32_t ldsaddr = (uint32_t)(uintptr_t)LDS_PTR(const uint8_t, lds);
-  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc), "s"(soff),
-               "{m0}"(ldsaddr)
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc),
+               "s"(soff), "{m0}"(ldsaddr)
                : "memory");
 }
 
@@ -265,9 +268,10 @@ __device__ __forceinline__ int wf2_swz(int row) { return ((row >> 1) & 3) ^ ((ro
 // * HBM -> LDS with buffer_load_dwordx4 ... lds (no staging registers, no VALU for the copy),
 //   three LDS stages (3 x 48 KiB): the loads for step k+2 are in flight while step k is computed.
 //   SGPR base + per-lane 32-bit voffset; the k advance is the scalar soffset.
-// * 8 waves (two per SIMD, so one wave's MFMAs cover the other's LDS reads and int8 -> bf16
-//   conversion; one wave per SIMD measured at most ~67% of the MFMA rate even without memory
-//   traffic), 256 x 256 block tile, reduction step 64.
+// * 8 waves (two per SIMD, so one wave's MFMAs cover the other's LDS reads, int8 -> bf16
+//   conversion and copies), 256 x 256 block tile, reduction step 64. A four-wave layout with
+//   128 x 128 wave tiles (half the LDS read traffic, explicitly interleaved schedule) measured
+//   the same throughput on the Wan shapes.
 // * FWD reads a weight fragment for two MFMA steps with one ds_read_b128: the 64 reduction
 //   indices of a step pair are assigned so that lane half lhi, step 2p+e uses k = 32p + 16lhi +
 //   8e + (0..7); the activation fragment of that step is 16-byte chunk 4p + 2lhi + e of the row.
