@@ -3,8 +3,11 @@
 //
 // One wavefront per output row n (64 lanes). Lane l owns the 16-byte chunks l, l+64, l+128, ...
 // of the row, so every load and store instruction of a wave is one contiguous, coalesced span.
-//   pass 1: absmax over the row in f32 (wave max via xor shuffles); NaN tracked separately so it
-//           propagates like Julia's maximum (quantization.jl:38)
+//   pass 1: absmax over the row as an unsigned maximum of magnitude bits (sign cleared): for
+//           IEEE formats that order equals the order of |x|, with every NaN above Inf, so a NaN
+//           anywhere in the row shows up as a maximum above the Inf pattern and propagates like
+//           Julia's maximum (quantization.jl:38); bf16 / f16 rows take two elements per packed
+//           16-bit max, then a wave max via xor shuffles
 //   scale = absmax / 127f0 (IEEE division), 1 where absmax == 0 (quantization.jl:39-40)
 //   pass 2: q = rint(clamp(w / scale, -127, 127)), ties to even (quantization.jl:41-42)
 // The row stays in registers when it fits in MAXC chunks per lane; otherwise pass 2 re-reads it
@@ -17,12 +20,23 @@ namespace reels {
 
 template <typename T>
 struct Elem;
+// Per element type: unpack a 16-byte chunk to f32, fold a chunk into the running maximum of
+// magnitude bits (mag), and turn that maximum into |x|max as f32 (absmax).
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, a),
+                                                                __builtin_bit_cast(u16x2, b)));
+}
 template <>
 struct Elem<float> {
   static constexpr int E = 4;  // elements per 16-byte chunk
   __device__ static void unpack(const u32x4& c, float* v) {
     for (int i = 0; i < 4; ++i) v[i] = __uint_as_float(c[i]);
   }
+  __device__ static void mag(const u32x4& c, uint32_t& m) {
+    for (int i = 0; i < 4; ++i) m = max(m, c[i] & 0x7fffffffu);
+  }
+  __device__ static float absmax(uint32_t m) { return __uint_as_float(m); }
 };
 template <>
 struct Elem<__bf16> {
@@ -30,6 +44,10 @@ struct Elem<__bf16> {
   __device__ static void unpack(const u32x4& c, float* v) {
     for (int i = 0; i < 4; ++i) { v[2 * i] = bf16_lo(c[i]); v[2 * i + 1] = bf16_hi(c[i]); }
   }
+  __device__ static void mag(const u32x4& c, uint32_t& m) {  // both halves at once
+    for (int i = 0; i < 4; ++i) m = pk_max_u16(m, c[i] & 0x7fff7fffu);
+  }
+  __device__ static float absmax(uint32_t m) { return __uint_as_float(max(m & 0xffffu, m >> 16) << 16); }
 };
 template <>
 struct Elem<_Float16> {
@@ -42,10 +60,20 @@ struct Elem<_Float16> {
       v[2 * i + 1] = (float)hi;
     }
   }
+  __device__ static void mag(const u32x4& c, uint32_t& m) {
+    for (int i = 0; i < 4; ++i) m = pk_max_u16(m, c[i] & 0x7fff7fffu);
+  }
+  __device__ static float absmax(uint32_t m) {  // f16 NaN converts to an f32 NaN
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)max(m & 0xffffu, m >> 16));
+  }
 };
 
 __device__ __forceinline__ float wave_max(float v) {
   for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  for (int off = 32; off >= 1; off >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, off, 64));
   return v;
 }
 
@@ -85,6 +113,33 @@ __device__ __forceinline__ void quantize_chunk(const float* v, float scale, floa
   }
 }
 
+// Fast path of quantize_chunk for a normal finite scale (every element of such a row is finite):
+// t = w * inv, c = clamp(t) (v_med3), and u = c + 1.5 * 2^23 rounds c to the nearest integer,
+// ties to even, leaving the two's complement code in u's low byte (c + 1.5 * 2^23 lies in
+// [2^23, 2^24), where the float spacing is 1). Returns true when some |c - rint(c)| exceeds
+// 0.5 - 2^-12: that chunk is redone with the IEEE division (the shortcut argument above).
+// Clamping before rounding equals the reference's clamp-then-round: the bounds are integers.
+template <int E>
+__device__ __forceinline__ bool quantize_chunk_fast(const float* v, float inv, uint32_t* out) {
+  constexpr float MAGIC = 12582912.0f;  // 1.5 * 2^23
+  float emax = 0.0f;
+  uint32_t ub[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const float c = __builtin_amdgcn_fmed3f(v[e] * inv, -127.0f, 127.0f);
+    const float u = c + MAGIC;
+    emax = fmaxf(emax, __builtin_fabsf(c - (u - MAGIC)));
+    ub[e] = __float_as_uint(u);
+  }
+#pragma unroll
+  for (int d = 0; d < E / 4; ++d) {
+    const uint32_t lo = __builtin_amdgcn_perm(ub[4 * d + 1], ub[4 * d + 0], 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm(ub[4 * d + 3], ub[4 * d + 2], 0x0c0c0400u);
+    out[d] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+  }
+  return emax > 0.5f - 0x1p-12f;
+}
+
 // scale is a finite normal float: the multiply shortcut applies (see quantize_one)
 __device__ __forceinline__ bool fast_scale(float scale) {
   return scale >= 0x1p-126f && scale <= 3.4028234663852886e38f;
@@ -102,8 +157,7 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(const T* __restrict__ w,
   const u32x4* row = reinterpret_cast<const u32x4*>(w + n * ld);
 
   u32x4 cache[MAXC > 0 ? MAXC : 1];
-  float m = 0.0f;
-  bool nan_seen = false;
+  uint32_t mb = 0;
   if (MAXC > 0) {
 #pragma unroll
     for (int i = 0; i < MAXC; ++i) {
@@ -113,31 +167,14 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(const T* __restrict__ w,
 #pragma unroll
     for (int i = 0; i < MAXC; ++i) {
       int64_t c = lane + 64 * (int64_t)i;
-      if (c < chunks) {
-        float v[E];
-        Elem<T>::unpack(cache[i], v);
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-          float a = fabsf(v[e]);
-          nan_seen |= (a != a);
-          m = fmaxf(m, a);
-        }
-      }
+      if (c < chunks) Elem<T>::mag(cache[i], mb);
     }
   } else {
-    for (int64_t c = lane; c < chunks; c += 64) {
-      float v[E];
-      Elem<T>::unpack(row[c], v);
-#pragma unroll
-      for (int e = 0; e < E; ++e) {
-        float a = fabsf(v[e]);
-        nan_seen |= (a != a);
-        m = fmaxf(m, a);
-      }
-    }
+    for (int64_t c = lane; c < chunks; c += 64) Elem<T>::mag(row[c], mb);
   }
-  m = wave_max(m);
-  if (__any(nan_seen)) m = __builtin_nanf("");
+  // this lane's |x|max as f32 bits (non-negative floats order as unsigned integers, NaN above Inf)
+  const uint32_t wm = wave_max_u32(__float_as_uint(Elem<T>::absmax(mb)));
+  const float m = wm > 0x7f800000u ? __builtin_nanf("") : __uint_as_float(wm);
   float scale = m / 127.0f;
   if (m == 0.0f) scale = 1.0f;
   if (lane == 0) scales[n] = scale;
@@ -154,7 +191,8 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(const T* __restrict__ w,
         float v[E];
         Elem<T>::unpack(cache[i], v);
         uint32_t out[E / 4];
-        quantize_chunk<E>(v, scale, inv, fast, out, bad);
+        if (!fast || quantize_chunk_fast<E>(v, inv, out))
+          quantize_chunk<E>(v, scale, inv, false, out, bad);
         if (E == 8) {
           u32x2 o = {out[0], out[1 % (E / 4)]};
           *reinterpret_cast<u32x2*>(qrow + c * E) = o;
@@ -168,7 +206,8 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(const T* __restrict__ w,
       float v[E];
       Elem<T>::unpack(row[c], v);
       uint32_t out[E / 4];
-      quantize_chunk<E>(v, scale, inv, fast, out, bad);
+      if (!fast || quantize_chunk_fast<E>(v, inv, out))
+        quantize_chunk<E>(v, scale, inv, false, out, bad);
       if (E == 8) {
         u32x2 o = {out[0], out[1 % (E / 4)]};
         *reinterpret_cast<u32x2*>(qrow + c * E) = o;
