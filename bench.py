@@ -138,15 +138,39 @@ def pack_bench(dev, reps=3):
     kern_ms = sum(ms_ for (_, ms_) in recs) / reps
     gbs = nbytes / (kern_ms * 1e-3) / 1e9
     assert int(status.item()) == 0
+    del mats
+    torch.cuda.empty_cache()
+    copy = copy_gbs(dev)
     out = {"metric": "pack GB/s (bf16 read + int8 codes + f32 scales)", "value": round(gbs, 1),
            "unit": "GB/s", "ms": round(ms, 4), "kernel_ms": round(kern_ms, 4),
            "elements": elems, "bytes": nbytes,
            "roofline": {"kernel": "pack_rows_kernel", "bound": "hbm", "achieved": round(gbs, 1),
                         "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
-                        "traffic": PACK_TRAFFIC_BYTES}}
-    del mats
-    torch.cuda.empty_cache()
+                        "traffic": PACK_TRAFFIC_BYTES,
+                        "device_copy": {"what": "torch copy_ of a 4 GiB buffer (read + write bytes), "
+                                                "same run", "gbs": round(copy, 1),
+                                        "achieved_over_copy": round(gbs / copy, 4)}}}
     return out
+
+
+def copy_gbs(dev, nbytes=4 << 30, reps=5):
+    """Device-to-device copy bandwidth (bytes read + written per second): the practical ceiling
+    of a streaming kernel that reads and writes HBM, measured in the same run."""
+    import torch
+    a = torch.empty((nbytes,), dtype=torch.uint8, device=dev).fill_(3)
+    b = torch.empty_like(a)
+    b.copy_(a)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        b.copy_(a)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    del a, b
+    torch.cuda.empty_cache()
+    return 2.0 * nbytes / (ms * 1e-3) / 1e9
 
 
 def pack_cpu_baseline(seconds=5.0):

@@ -195,9 +195,9 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(const T* __restrict__ w,
           quantize_chunk<E>(v, scale, inv, false, out, bad);
         if (E == 8) {
           u32x2 o = {out[0], out[1 % (E / 4)]};
-          *reinterpret_cast<u32x2*>(qrow + c * E) = o;
+          __builtin_nontemporal_store(o, reinterpret_cast<u32x2*>(qrow + c * E));
         } else {
-          *reinterpret_cast<uint32_t*>(qrow + c * E) = out[0];
+          __builtin_nontemporal_store(out[0], reinterpret_cast<uint32_t*>(qrow + c * E));
         }
       }
     }
@@ -210,9 +210,9 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(const T* __restrict__ w,
         quantize_chunk<E>(v, scale, inv, false, out, bad);
       if (E == 8) {
         u32x2 o = {out[0], out[1 % (E / 4)]};
-        *reinterpret_cast<u32x2*>(qrow + c * E) = o;
+        __builtin_nontemporal_store(o, reinterpret_cast<u32x2*>(qrow + c * E));
       } else {
-        *reinterpret_cast<uint32_t*>(qrow + c * E) = out[0];
+        __builtin_nontemporal_store(out[0], reinterpret_cast<uint32_t*>(qrow + c * E));
       }
     }
   }
