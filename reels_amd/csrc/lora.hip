@@ -40,36 +40,40 @@ __global__ void transpose_pad_kernel(const uint16_t* __restrict__ in, int64_t ro
 // rowproj: out[m][j] = bf16(sum_k src[m][k] * P[j][k]) for j < r, 0 for r <= j < rp.
 // src [M][Kd] bf16 (x or dy), P [r][Kd] bf16 (At or B). When SCALED, also writes
 // scaled[m][k] = bf16(src[m][k] * s[k]) (the dy * s operand of the DX GEMM).
-// HBM-bound: a block of 256 threads owns 32 rows and streams them in chunks of 256 columns. Each
-// wave-instruction loads two contiguous 512-byte row segments; the chunk goes to a padded LDS
-// tile (row stride 528 bytes: 8 consecutive rows fall in distinct banks) while the next chunk is
-// already in flight into registers. Wave w multiplies columns [64w, 64w+64) of the chunk on
-// MFMA (A = 32 src rows, B = 32 rows of P staged the same way); the four wave partials are summed
-// in wave order at the end.
+// HBM-bound: a block of 256 threads owns ROWS rows (32 or 64) and streams them in chunks of 256
+// columns. Each wave-instruction loads two contiguous 512-byte row segments; the chunk goes to a
+// padded LDS tile (row stride 528 bytes: 8 consecutive rows fall in distinct banks) while the
+// next chunk is already in flight into registers. Wave w multiplies columns [64w, 64w+64) of the
+// chunk on MFMA (A = 32 src rows per row group, B = 32 rows of P staged the same way); the four
+// wave partials are summed in wave order at the end. Every block streams all of P (r x Kd, from
+// L2), so 64-row blocks halve that traffic per output row; 32-row blocks are used when there are
+// too few tokens to give every CU a 64-row block.
 namespace rowp {
-constexpr int ROWS = 32, KC = 256, LROW = KC + 8;  // LDS row: 264 bf16 = 528 bytes
+constexpr int KC = 256, LROW = KC + 8;  // LDS row: 264 bf16 = 528 bytes
 }  // namespace rowp
 
-template <int RT, bool SCALED>
+template <int RT, bool SCALED, int ROWS>
 __global__ __launch_bounds__(256) void rowproj_kernel(const uint16_t* __restrict__ src, int64_t M,
                                                       int64_t Kd, const uint16_t* __restrict__ P,
                                                       int r, int rp_, uint16_t* __restrict__ out,
                                                       const float* __restrict__ s,
                                                       uint16_t* __restrict__ scaled) {
   using namespace rowp;
+  constexpr int RG = ROWS / 32;  // 32-row MFMA groups
   __shared__ __attribute__((aligned(16))) uint16_t xs[ROWS * LROW];
   __shared__ __attribute__((aligned(16))) uint16_t ps[32 * RT * LROW];
-  __shared__ float red[RT][16][64];
+  __shared__ float red[RG][RT][16][64];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int l32 = lane & 31, lhi = lane >> 5;
   const int64_t m0 = (int64_t)blockIdx.x * ROWS;
   const int nchunks = (int)((Kd + KC - 1) / KC);
-  // loader roles: X chunk = 32 rows x 32 16-byte chunks, 4 per thread; P chunk = 32RT rows, 4RT
-  u32x4 rx[4], rpv[4 * RT];
+  // loader roles: X chunk = ROWS rows x 32 16-byte chunks, ROWS/8 per thread; P chunk = 32RT
+  // rows, 4RT per thread
+  u32x4 rx[ROWS / 8], rpv[4 * RT];
   auto load = [&](int ck) {
     const int64_t k0 = (int64_t)ck * KC;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < ROWS / 8; ++i) {
       const int row = (t >> 5) + 8 * i, c = t & 31;
       const int64_t m = m0 + row, k = k0 + c * 8;
       u32x4 v = {0, 0, 0, 0};
@@ -88,7 +92,7 @@ __global__ __launch_bounds__(256) void rowproj_kernel(const uint16_t* __restrict
   auto stash = [&](int ck) {
     const int64_t k0 = (int64_t)ck * KC;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < ROWS / 8; ++i) {
       const int row = (t >> 5) + 8 * i, c = t & 31;
       *reinterpret_cast<u32x4*>(&xs[row * LROW + c * 8]) = rx[i];
       if (SCALED) {
@@ -112,11 +116,13 @@ __global__ __launch_bounds__(256) void rowproj_kernel(const uint16_t* __restrict
       *reinterpret_cast<u32x4*>(&ps[row * LROW + c * 8]) = rpv[i];
     }
   };
-  f32x16 acc[RT];
+  f32x16 acc[RG][RT];
 #pragma unroll
-  for (int j = 0; j < RT; ++j)
+  for (int g = 0; g < RG; ++g)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) acc[j][v] = 0.0f;
+    for (int j = 0; j < RT; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[g][j][v] = 0.0f;
   load(0);
   for (int ck = 0; ck < nchunks; ++ck) {
     stash(ck);
@@ -125,33 +131,41 @@ __global__ __launch_bounds__(256) void rowproj_kernel(const uint16_t* __restrict
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const int col = wave * 64 + ks * 16 + lhi * 8;
-      const bf16x8 a = as_bf16x8(*reinterpret_cast<const u32x4*>(&xs[l32 * LROW + col]));
+      bf16x8 a[RG];
+#pragma unroll
+      for (int g = 0; g < RG; ++g)
+        a[g] = as_bf16x8(*reinterpret_cast<const u32x4*>(&xs[(g * 32 + l32) * LROW + col]));
 #pragma unroll
       for (int j = 0; j < RT; ++j) {
         const bf16x8 bv = as_bf16x8(*reinterpret_cast<const u32x4*>(&ps[(j * 32 + l32) * LROW + col]));
-        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bv, acc[j], 0, 0, 0);
+#pragma unroll
+        for (int g = 0; g < RG; ++g)
+          acc[g][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[g], bv, acc[g][j], 0, 0, 0);
       }
     }
     __syncthreads();
   }
   if (out == nullptr) return;
-  // D lane layout: row (token) = (v/4)*8 + lhi*4 + v%4, column (j) = t*32 + l32.
+  // D lane layout: row (token) = g*32 + (v/4)*8 + lhi*4 + v%4, column (j) = t*32 + l32.
   // Sum the four wave partials in wave order (deterministic), one wave at a time.
   for (int w = 0; w < 4; ++w) {
     if (wave == w) {
 #pragma unroll
-      for (int j = 0; j < RT; ++j)
+      for (int g = 0; g < RG; ++g)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) red[j][v][lane] = (w == 0 ? 0.0f : red[j][v][lane]) + acc[j][v];
+        for (int j = 0; j < RT; ++j)
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            red[g][j][v][lane] = (w == 0 ? 0.0f : red[g][j][v][lane]) + acc[g][j][v];
     }
     __syncthreads();
   }
-  for (int idx = t; idx < 32 * 32 * RT; idx += 256) {
-    const int j0 = idx / 1024, rem = idx % 1024;
+  for (int idx = t; idx < ROWS * 32 * RT; idx += 256) {
+    const int g = idx / (1024 * RT), j0 = (idx / 1024) % RT, rem = idx % 1024;
     const int row = rem / 32, col = rem % 32;
     const int v = (row / 8) * 4 + (row % 4), ln = ((row / 4) & 1) * 32 + col;
-    const float sum = red[j0][v][ln];
-    const int64_t mm = m0 + row;
+    const float sum = red[g][j0][v][ln];
+    const int64_t mm = m0 + g * 32 + row;
     const int j = j0 * 32 + col;
     if (mm < M && j < rp_) out[mm * rp_ + j] = j < r ? (uint16_t)f32_to_bf16_bits(sum) : (uint16_t)0;
   }
@@ -422,18 +436,28 @@ static WsLayout ws_layout(int64_t M, int64_t K, int64_t N, int64_t r, int which,
 
 static int grid1(int64_t n, int bs = 256) { return (int)ceil_div(n, bs); }
 
+template <bool SCALED, int ROWS>
+static void launch_rowproj_t(int rt, const uint16_t* src, int64_t M, int64_t Kd, const uint16_t* P,
+                             int r, int rp, uint16_t* out, const float* s, uint16_t* scaled,
+                             hipStream_t st) {
+  const dim3 grid((unsigned)ceil_div(M, ROWS));
+  TraceScope _ts(st, SCALED ? (rt <= 1 ? "rowproj_kernel<1,true>" : rt == 2 ? "rowproj_kernel<2,true>" : "rowproj_kernel<4,true>")
+                            : (rt <= 1 ? "rowproj_kernel<1,false>" : rt == 2 ? "rowproj_kernel<2,false>" : "rowproj_kernel<4,false>"));
+  if (rt <= 1) rowproj_kernel<1, SCALED, ROWS><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, s, scaled);
+  else if (rt == 2) rowproj_kernel<2, SCALED, ROWS><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, s, scaled);
+  else rowproj_kernel<4, SCALED, ROWS><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, s, scaled);
+}
+
 static int launch_rowproj(const uint16_t* src, int64_t M, int64_t Kd, const uint16_t* P, int r,
                           int rp, uint16_t* out, const float* s, uint16_t* scaled, hipStream_t st) {
-  const dim3 grid((unsigned)ceil_div(M, rowp::ROWS));
   const int rt = (r + 31) / 32;
+  const bool wide = ceil_div(M, 64) >= 256;  // enough tokens for a 64-row block on every CU
   if (scaled) {
-    if (rt <= 1) { TraceScope _ts(st, "rowproj_kernel<1,true>"); rowproj_kernel<1, true><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, s, scaled); }
-    else if (rt == 2) { TraceScope _ts(st, "rowproj_kernel<2,true>"); rowproj_kernel<2, true><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, s, scaled); }
-    else { TraceScope _ts(st, "rowproj_kernel<4,true>"); rowproj_kernel<4, true><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, s, scaled); }
+    if (wide) launch_rowproj_t<true, 64>(rt, src, M, Kd, P, r, rp, out, s, scaled, st);
+    else launch_rowproj_t<true, 32>(rt, src, M, Kd, P, r, rp, out, s, scaled, st);
   } else {
-    if (rt <= 1) { TraceScope _ts(st, "rowproj_kernel<1,false>"); rowproj_kernel<1, false><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, s, scaled); }
-    else if (rt == 2) { TraceScope _ts(st, "rowproj_kernel<2,false>"); rowproj_kernel<2, false><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, s, scaled); }
-    else { TraceScope _ts(st, "rowproj_kernel<4,false>"); rowproj_kernel<4, false><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, s, scaled); }
+    if (wide) launch_rowproj_t<false, 64>(rt, src, M, Kd, P, r, rp, out, s, scaled, st);
+    else launch_rowproj_t<false, 32>(rt, src, M, Kd, P, r, rp, out, s, scaled, st);
   }
   return check_launch("rowproj_kernel");
 }
