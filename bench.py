@@ -69,15 +69,22 @@ def parse():
     return ap.parse_args()
 
 
-def vendor_gemm_tflops(dev, M, K, N, reps=5):
-    """bf16 x bf16 -> bf16 torch.matmul (hipBLASLt) on one Wan-14B projection shape: the
-    practical MFMA ceiling for a dense GEMM of this size on this GPU, measured in the same run."""
+def vendor_gemm_tflops(dev, M, K, N, seconds=1.5):
+    """bf16 x bf16 -> bf16 torch.matmul (hipBLASLt) on one Wan-14B projection shape, timed over a
+    sustained loop (~seconds, like the timed bench steps: the GPU runs at its power cap, so short
+    bursts and sustained loops clock differently): the practical MFMA ceiling for a dense GEMM
+    of this size on this GPU, measured in the same run."""
     import torch
     x = torch.randn((M, K), device=dev).to(torch.bfloat16)
     w = torch.randn((N, K), device=dev).to(torch.bfloat16)
-    for _ in range(2):
+    for _ in range(3):
         torch.matmul(x, w.t())
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(5):
+        torch.matmul(x, w.t())
+    torch.cuda.synchronize()
+    reps = max(10, int(seconds / max((time.perf_counter() - t0) / 5, 1e-6)))
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(reps):
@@ -288,7 +295,11 @@ def main():
         run_step(L, projs, _lib.check)
     torch.cuda.synchronize()
 
-    launches_per_step = 64
+    # count one step's launches (an untimed traced step) to size the trace buffer exactly
+    _lib.check("reels_hip_trace_start", L.reels_hip_trace_start(4096))
+    run_step(L, projs, _lib.check)
+    torch.cuda.synchronize()
+    launches_per_step = len(_lib.trace_records())
     _lib.check("reels_hip_trace_start", L.reels_hip_trace_start(launches_per_step * args.steps))
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -314,8 +325,8 @@ def main():
     gemm_fl = {"fwd": 0.0, "dx": 0.0}
     for step in range(args.steps):
         rs = recs[step * per_step:(step + 1) * per_step]
-        fi = [ms for (n, ms) in rs if n.startswith("i8gemm") and n.endswith("<0>")]
-        bi = [ms for (n, ms) in rs if n.startswith("i8gemm") and n.endswith("<1>")]
+        fi = [ms for (n, ms) in rs if "gemm_kernel" in n and n.endswith("<0>")]
+        bi = [ms for (n, ms) in rs if "gemm_kernel" in n and n.endswith("<1>")]
         for (pr, ms) in zip(projs, fi):
             gemm_ms["fwd"] += ms; gemm_n["fwd"] += 1
             gemm_fl["fwd"] += gemm_flops("fwd", M, pr.K, pr.N, RANK)
@@ -324,7 +335,7 @@ def main():
             gemm_fl["dx"] += gemm_flops("dx", M, pr.K, pr.N, RANK)
     tot_ms = gemm_ms["fwd"] + gemm_ms["dx"]
     achieved = (gemm_fl["fwd"] + gemm_fl["dx"]) / (tot_ms * 1e-3) / 1e12 if tot_ms > 0 else 0.0
-    gemm_names = sorted({n for (n, _) in recs if n.startswith("i8gemm")})
+    gemm_names = sorted({n for (n, _) in recs if "gemm_kernel" in n})
     vendor = vendor_gemm_tflops(dev, M, 5120, 5120)
     roofline = {
         "kernel": " + ".join(gemm_names) + " (<0> fwd, <1> dX; int8 weight converted to bf16 "
@@ -336,7 +347,7 @@ def main():
         "avg_launch_ms": {k: round(gemm_ms[k] / max(gemm_n[k], 1), 4) for k in gemm_ms},
         "launches": gemm_n,
         "vendor_bf16_gemm": {"what": f"torch.matmul bf16 (hipBLASLt), {M}x5120 by 5120x5120, "
-                                     "same run", "tflops": round(vendor, 1),
+                                     "sustained ~1.5 s loop, same run", "tflops": round(vendor, 1),
                              "achieved_over_vendor": round(achieved / vendor, 4)},
     }
     kernels = {n: {"launches": c, "avg_ms": round(t / c, 4), "ms_per_step": round(t / args.steps, 4)}

@@ -20,4 +20,18 @@ struct GemmArgs {
 // mode 0 = FWD (out = s * act q^T + c L R^T + bias), 1 = DX (out = act q + c L R^T)
 int launch_i8gemm(int mode, const GemmArgs& a, hipStream_t st);
 
+// bf16 x bf16 GEMM with the LoRA epilogue: out = bf16(act wd^T + c L R^T + bias), wd [Ncols][Kred]
+// bf16 (a dequantized weight); a.q and a.colscale are unused. Needs Kred % 64 == 0, 16-byte
+// aligned operands and byte sizes below 2^31 (bfgemm_supported).
+bool bfgemm_supported(int64_t M, int64_t Ncols, int64_t Kred);
+// mode only labels the trace record ("bfgemm_kernel<0>" forward, "<1>" dX)
+int launch_bfgemm(int mode, const GemmArgs& a, const uint16_t* wd, hipStream_t st);
+
+// wd[n][k] = bf16(fl32(q[n][k] * s[n])), q [N][K] row stride ldq (K % 16 == 0)
+int launch_dequant_rows(const int8_t* q, int64_t ldq, const float* s, int64_t N, int64_t K,
+                        uint16_t* wd, hipStream_t st);
+// wt[k][n] = bf16(fl32(q[n][k] * s[n])) (N % 64 == 0, K % 64 == 0)
+int launch_dequant_transpose(const int8_t* q, int64_t ldq, const float* s, int64_t N, int64_t K,
+                             uint16_t* wt, hipStream_t st);
+
 }  // namespace reels

@@ -522,6 +522,290 @@ void i8gemm_v3_kernel(GemmArgs a, int tiles_n, int tiles_m) {
   }
 }
 
+// =============================================================================================
+// Dequantized-weight path (every shape whose K and N are multiples of 64, i.e. every Wan / LTX
+// projection). Like the reference's _materialize_weight (src/layers/quantization.jl:54-64,
+// dequantize then GEMM), the int8 weight is expanded once per call into a bf16 copy
+// wd = bf16(fl32(q * s)) in the caller's workspace, and a plain bf16 GEMM with the LoRA epilogue
+// runs on it. For dX the copy is written transposed, wt[k][n] = bf16(fl32(q[n][k] * s[n])), so
+// the same GEMM computes dx = dy wt^T with the scale folded into the weight. Against the int8
+// GEMM above this takes the int8 -> bf16 conversion (VALU in every wave's inner loop) out of the
+// GEMM at the cost of a streaming pass over the weight (~1-2% of the GEMM's time).
+
+__global__ __launch_bounds__(256) void dequant_rows_kernel(const int8_t* __restrict__ q, int64_t ldq,
+                                                           const float* __restrict__ s, int64_t N,
+                                                           int64_t K, uint16_t* __restrict__ wd) {
+  const int64_t groups = K >> 4;  // 16 codes per thread
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= N * groups) return;
+  const int64_t n = i / groups, c = i - n * groups;
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(q + n * ldq + c * 16));
+  const float sc = s[n];
+  u32x4 o[2];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const uint32_t x = v[d];
+    const float f0 = (float)(int8_t)(x & 0xff) * sc, f1 = (float)(int8_t)((x >> 8) & 0xff) * sc;
+    const float f2 = (float)(int8_t)((x >> 16) & 0xff) * sc, f3 = (float)((int32_t)x >> 24) * sc;
+    o[d >> 1][(d & 1) * 2] = pack_bf16x2(f0, f1);
+    o[d >> 1][(d & 1) * 2 + 1] = pack_bf16x2(f2, f3);
+  }
+  u32x4* dst = reinterpret_cast<u32x4*>(wd + n * K + c * 16);
+  dst[0] = o[0];
+  dst[1] = o[1];
+}
+
+// 64 x 64 tiles through LDS: a thread reads 16 codes of one row n and writes them as bf16 into
+// column n of the [k][n] tile; it then stores 16 consecutive n of one row k (two 16-byte stores).
+__global__ __launch_bounds__(256) void dequant_transpose_kernel(const int8_t* __restrict__ q,
+                                                                int64_t ldq,
+                                                                const float* __restrict__ s,
+                                                                int64_t N, int64_t K,
+                                                                uint16_t* __restrict__ wt) {
+  __shared__ uint16_t tile[64][66];  // [k][n], rows padded to 132 bytes
+  const int64_t n0 = (int64_t)blockIdx.y * 64, k0 = (int64_t)blockIdx.x * 64;
+  const int t = threadIdx.x;
+  {
+    const int nl = t >> 2, kl = (t & 3) * 16;
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(q + (n0 + nl) * ldq + k0 + kl));
+    const float sc = s[n0 + nl];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const float f = (float)(int8_t)((v[j >> 2] >> (8 * (j & 3))) & 0xff) * sc;
+      tile[kl + j][nl] = (uint16_t)f32_to_bf16_bits(f);
+    }
+  }
+  __syncthreads();
+  const int kr = t >> 2, nc = (t & 3) * 16;
+  const uint32_t* row = reinterpret_cast<const uint32_t*>(&tile[kr][nc]);
+  u32x4 o0 = {row[0], row[1], row[2], row[3]}, o1 = {row[4], row[5], row[6], row[7]};
+  u32x4* dst = reinterpret_cast<u32x4*>(wt + (k0 + kr) * N + n0 + nc);
+  dst[0] = o0;
+  dst[1] = o1;
+}
+
+// bf16 GEMM: 256 x 256 block tile, reduction step 64, 8 waves (two per SIMD), each wave 128
+// tokens x 64 output columns (4 x 2 tiles of v_mfma_f32_32x32x16_bf16); HBM -> LDS copies into a
+// two-stage ring of 64 KiB stages (activation and weight tiles [256][64] bf16 with the same
+// 16-byte XOR swizzle). At the barrier that ends step kt every wave has finished reading stage kt
+// (lgkmcnt(0) before it), so the copy of step kt+2 goes into it right away and has one step to
+// land. XCD-aware tile order and the epilogue as in the int8 kernel (minus the column scale).
+namespace bfg {
+constexpr int BM = 256, BN = 256, BK = 64, NT = 512;
+constexpr int ACT = BM * BK * 2;   // 32 KiB
+constexpr int WB = BN * BK * 2;    // 32 KiB
+constexpr int STAGE = ACT + WB;    // 64 KiB
+constexpr int GM = 4;
+}  // namespace bfg
+
+__global__ __launch_bounds__(512)
+void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int tiles_m) {
+  using namespace bfg;
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  const int t = threadIdx.x, lane = t & 63;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wm = w >> 2, wn = w & 3;
+  const int l32 = lane & 31, lhi = lane >> 5;
+  const int64_t M = a.M, Ncols = a.Ncols, Kred = a.Kred;
+
+  const int nt = tiles_n * tiles_m;
+  const int b = blockIdx.x;
+  const int xcd = b & 7, idx = b >> 3;
+  const int lo = nt >> 3, rem = nt & 7;
+  const int logical = xcd * lo + (xcd < rem ? xcd : rem) + idx;
+  const int group = GM * tiles_n;
+  const int g = logical / group;
+  const int first_m = g * GM;
+  const int gm = (tiles_m - first_m) < GM ? (tiles_m - first_m) : GM;
+  const int within = logical - g * group;
+  const int64_t m0 = (int64_t)(first_m + within % gm) * BM;
+  const int64_t n0 = (int64_t)(within / gm) * BN;
+
+  const i32x4 ract = buffer_rsrc(a.act, (uint32_t)(M * Kred * 2));
+  const i32x4 rw = buffer_rsrc(wd, (uint32_t)(Ncols * Kred * 2));
+  uint32_t voa[4], vow[4];  // copies i: rows (w*4+i)*8 + lane/8 of each tile, 16 bytes per lane
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = (w * 4 + i) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ act_swz(row);
+    const int64_t m = (m0 + row < M) ? m0 + row : M - 1;
+    const int64_t n = (n0 + row < Ncols) ? n0 + row : Ncols - 1;
+    voa[i] = (uint32_t)((m * Kred + c * 8) * 2);
+    vow[i] = (uint32_t)((n * Kred + c * 8) * 2);
+  }
+  const int nk = (int)(Kred / BK);
+  auto issue = [&](int kt, int stage) {
+    uint8_t* base = smem + stage * STAGE;
+    const uint32_t so = (uint32_t)kt * (BK * 2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma16(ract, voa[i], so, base + (w * 4 + i) * 1024);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma16(rw, vow[i], so, base + ACT + (w * 4 + i) * 1024);
+  };
+
+  f32x16 acc[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  // sub-step s of a step uses k = 16 s + 8 lhi + (0..7): 16-byte chunk 2 s + lhi of each row
+  auto read_x = [&](const uint8_t* sa, int s, bf16x8* xf) {
+    const int c = 2 * s + lhi;
+#pragma unroll
+    for (int tj = 0; tj < 4; ++tj) {
+      const int row = wm * 128 + tj * 32 + l32;
+      xf[tj] = as_bf16x8(*reinterpret_cast<const u32x4*>(sa + row * 128 + ((c ^ act_swz(row)) << 4)));
+    }
+  };
+  auto read_w = [&](const uint8_t* sw, int s, bf16x8* af) {
+    const int c = 2 * s + lhi;
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti) {
+      const int row = wn * 64 + ti * 32 + l32;
+      af[ti] = as_bf16x8(*reinterpret_cast<const u32x4*>(sw + row * 128 + ((c ^ act_swz(row)) << 4)));
+    }
+  };
+  auto mfma8 = [&](const bf16x8* af, const bf16x8* xf) {
+#pragma unroll
+    for (int tj = 0; tj < 4; ++tj)
+#pragma unroll
+      for (int ti = 0; ti < 2; ++ti)
+        acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ti], xf[tj], acc[ti][tj], 0, 0, 0);
+  };
+
+  bf16x8 xa[4], xb[4], wa[2], wb[2];
+  issue(0, 0);
+  if (nk > 1) issue(1, 1);
+  if (nk > 1) __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8): step 1 may stay in flight
+  else __builtin_amdgcn_s_waitcnt(0x0F70);
+  __builtin_amdgcn_s_barrier();
+  read_w(smem + ACT, 0, wa);
+  read_x(smem, 0, xa);
+  for (int kt = 0; kt < nk; ++kt) {
+    const uint8_t* sa = smem + (kt & 1) * STAGE;
+    __builtin_amdgcn_iglp_opt(1);
+    read_w(sa + ACT, 1, wb);
+    read_x(sa, 1, xb);
+    mfma8(wa, xa);
+    read_w(sa + ACT, 2, wa);
+    read_x(sa, 2, xa);
+    mfma8(wb, xb);
+    read_w(sa + ACT, 3, wb);
+    read_x(sa, 3, xb);
+    mfma8(wa, xa);
+    if (kt + 1 < nk) {
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave is done reading stage kt
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): step kt+1 has landed
+      __builtin_amdgcn_s_barrier();
+      if (kt + 2 < nk) issue(kt + 2, kt & 1);
+      const uint8_t* sn = smem + ((kt + 1) & 1) * STAGE;
+      read_w(sn + ACT, 0, wa);
+      read_x(sn, 0, xa);
+    }
+    mfma8(wb, xb);
+  }
+
+  // epilogue: LoRA up-projection on MFMA, bias, one bf16 rounding; the 256 x 256 tile is staged
+  // in LDS (rows of 512 bytes, 16-byte chunks XOR-swizzled by row) and stored as whole rows
+  __syncthreads();
+  uint8_t* stile = smem;
+  const int nsteps = a.rp >> 4;
+#pragma unroll
+  for (int ti = 0; ti < 2; ++ti) {
+    const int64_t nrow = n0 + wn * 64 + ti * 32 + l32;
+    const int64_t nrc = nrow < Ncols ? nrow : Ncols - 1;
+    const int nloc = wn * 64 + ti * 32 + lhi * 4;
+    const int64_t nbase = n0 + nloc;
+    float bs[16];
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int64_t n = nbase + g4 * 8;
+      u32x2 b2 = {0, 0};
+      if (a.bias != nullptr && n < Ncols) b2 = *reinterpret_cast<const u32x2*>(a.bias + n);
+      bs[g4 * 4 + 0] = bf16_lo(b2[0]); bs[g4 * 4 + 1] = bf16_hi(b2[0]);
+      bs[g4 * 4 + 2] = bf16_lo(b2[1]); bs[g4 * 4 + 3] = bf16_hi(b2[1]);
+    }
+#pragma unroll
+    for (int tj = 0; tj < 4; ++tj) {
+      const int mloc = wm * 128 + tj * 32 + l32;
+      const int64_t m = m0 + mloc;
+      const int64_t mc = m < M ? m : M - 1;
+      f32x16 lor;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) lor[v] = 0.0f;
+      for (int s = 0; s < nsteps; ++s) {
+        u32x4 rv = *reinterpret_cast<const u32x4*>(a.R + nrc * a.rp + s * 16 + lhi * 8);
+        u32x4 lv = *reinterpret_cast<const u32x4*>(a.L + mc * a.rp + s * 16 + lhi * 8);
+        if (nrow >= Ncols) rv = u32x4{0, 0, 0, 0};
+        if (m >= M) lv = u32x4{0, 0, 0, 0};
+        lor = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(rv), as_bf16x8(lv), lor, 0, 0, 0);
+      }
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int v = g4 * 4 + e;
+          o[e] = acc[ti][tj][v] + a.c * lor[v] + bs[v];
+        }
+        const u32x2 pk = {pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+        const int col = nloc + g4 * 8;
+        const int chunk = (col >> 3) ^ (mloc & 31);
+        *reinterpret_cast<u32x2*>(stile + mloc * 512 + chunk * 16 + (col & 7) * 2) = pk;
+      }
+    }
+  }
+  __syncthreads();
+#pragma unroll 4
+  for (int i = 0; i < 16; ++i) {
+    const int id = t + 512 * i, row = id >> 5, c = id & 31;
+    const int64_t m = m0 + row, n = n0 + c * 8;
+    if (m < M && n < Ncols) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(stile + row * 512 + ((c ^ (row & 31)) << 4));
+      *reinterpret_cast<u32x4*>(a.out + m * Ncols + n) = v;
+    }
+  }
+}
+
+bool bfgemm_supported(int64_t M, int64_t Ncols, int64_t Kred) {
+  return Kred % bfg::BK == 0 && Ncols % 16 == 0 && M * Kred * 2 < ((int64_t)1 << 31) &&
+         Ncols * Kred * 2 < ((int64_t)1 << 31);
+}
+
+int launch_bfgemm(int mode, const GemmArgs& a, const uint16_t* wd, hipStream_t st) {
+  if (!bfgemm_supported(a.M, a.Ncols, a.Kred))
+    return fail(REELS_HIP_EINVAL, "bfgemm: shape not supported (reduction not a multiple of 64 or operands of 2 GiB or more)");
+  static std::once_flag once;
+  static hipError_t attr_err = hipSuccess;
+  std::call_once(once, [&] {
+    attr_err = hipFuncSetAttribute((const void*)bfgemm_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, 2 * bfg::STAGE);
+  });
+  if (attr_err != hipSuccess)
+    return fail(REELS_HIP_EHIP, std::string("bfgemm: hipFuncSetAttribute: ") + hipGetErrorString(attr_err));
+  const int tn = (int)ceil_div(a.Ncols, bfg::BN), tm = (int)ceil_div(a.M, bfg::BM);
+  { TraceScope _ts(st, mode == 0 ? "bfgemm_kernel<0>" : "bfgemm_kernel<1>");
+    bfgemm_kernel<<<tn * tm, bfg::NT, 2 * bfg::STAGE, st>>>(a, wd, tn, tm); }
+  return check_launch("bfgemm_kernel");
+}
+
+int launch_dequant_rows(const int8_t* q, int64_t ldq, const float* s, int64_t N, int64_t K,
+                        uint16_t* wd, hipStream_t st) {
+  const int64_t n = N * (K >> 4);
+  { TraceScope _ts(st, "dequant_rows_kernel");
+    dequant_rows_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, st>>>(q, ldq, s, N, K, wd); }
+  return check_launch("dequant_rows_kernel");
+}
+
+int launch_dequant_transpose(const int8_t* q, int64_t ldq, const float* s, int64_t N, int64_t K,
+                             uint16_t* wt, hipStream_t st) {
+  { TraceScope _ts(st, "dequant_transpose_kernel");
+    dequant_transpose_kernel<<<dim3((unsigned)(K / 64), (unsigned)(N / 64)), 256, 0, st>>>(q, ldq, s, N, K, wt); }
+  return check_launch("dequant_transpose_kernel");
+}
+
 int launch_i8gemm(int mode, const GemmArgs& a, hipStream_t st) {
   using namespace gemm;
   // the main kernel needs a reduction in whole 64-steps and 32-bit buffer offsets

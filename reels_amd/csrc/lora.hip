@@ -391,6 +391,7 @@ __global__ void gelu_bwd_kernel(const uint16_t* __restrict__ x, const uint16_t* 
 // host side
 struct Plan {
   bool fast;
+  bool deq;     // fast and K, N multiples of 64: dequantized weight + bf16 GEMM
   int rp;       // row stride of h/u buffers
   int splits;   // split-M count for dA/dB
   int64_t tps;  // tokens per split (multiple of 64)
@@ -399,6 +400,7 @@ struct Plan {
 static Plan make_plan(int64_t M, int64_t K, int64_t N, int64_t r, bool ptrs_aligned) {
   Plan p;
   p.fast = ptrs_aligned && (K % 16 == 0) && (N % 16 == 0) && (r % 16 == 0) && r <= 128;
+  p.deq = p.fast && bfgemm_supported(M, N, K) && bfgemm_supported(M, K, N);
   p.rp = (int)r;
   int64_t s = (M + 1023) / 1024;
   if (s < 1) s = 1;
@@ -412,7 +414,7 @@ static Plan make_plan(int64_t M, int64_t K, int64_t N, int64_t r, bool ptrs_alig
 
 // workspace layout (byte offsets, 256-aligned); identical computation for sizing and use
 struct WsLayout {
-  size_t h, u, dys, at, bt, pa, pb, total;
+  size_t h, u, dys, wd, at, bt, pa, pb, total;
 };
 
 static WsLayout ws_layout(int64_t M, int64_t K, int64_t N, int64_t r, int which, const Plan& p) {
@@ -422,11 +424,12 @@ static WsLayout ws_layout(int64_t M, int64_t K, int64_t N, int64_t r, int which,
   const size_t rp = (size_t)p.rp;
   w.h = take((size_t)M * rp * 2);
   w.at = take(r > 0 ? (size_t)r * K * 2 : 0);
+  w.wd = take(p.deq ? (size_t)N * K * 2 : 0);  // bf16 copy of the dequantized weight
   if (which == REELS_HIP_WS_FWD) {
     w.bt = take(p.fast ? (size_t)N * rp * 2 : 0);
   } else {
     w.u = take((size_t)M * rp * 2);
-    w.dys = take(p.fast ? (size_t)M * N * 2 : 0);
+    w.dys = take(p.fast && !p.deq ? (size_t)M * N * 2 : 0);
     w.pa = take(p.fast && r > 0 ? (size_t)p.splits * K * rp * 4 : 0);
     w.pb = take(p.fast && r > 0 ? (size_t)p.splits * N * rp * 4 : 0);
   }
@@ -548,6 +551,12 @@ extern "C" int reels_hip_i8lora_fwd(const void* x, const int8_t* q, const float*
   g.act = xb; g.q = q; g.colscale = scales; g.L = h; g.R = bt;
   g.bias = static_cast<const uint16_t*>(bias); g.out = static_cast<uint16_t*>(y);
   g.M = M; g.Ncols = N; g.Kred = K; g.ldq = K; g.rp = r > 0 ? p.rp : 0; g.c = lora_scale;
+  if (p.deq) {
+    uint16_t* wd = reinterpret_cast<uint16_t*>(ws + w.wd);
+    if ((rc = launch_dequant_rows(q, K, scales, N, K, wd, st))) return rc;
+    g.q = nullptr; g.colscale = nullptr;
+    return launch_bfgemm(0, g, wd, st);
+  }
   return launch_i8gemm(0, g, st);
 }
 
@@ -622,8 +631,22 @@ extern "C" int reels_hip_i8lora_bwd(const void* dy, const void* x, const void* h
   }
 
   uint16_t* dys = reinterpret_cast<uint16_t*>(ws + w.dys);
-  // 1. u = dy B^T and dys = dy * s in one pass over dy (the scaled copy only when dx is wanted)
-  if (r > 0 || dx) {
+  if (p.deq) {
+    // 1. u = dy B^T; 2. dx = dy wt^T + c u A^T with wt[k][n] = bf16(q[n][k] s[n])
+    if (r > 0 && (dx || dA)) {
+      if ((rc = launch_rowproj(dyb, M, N, Bb, (int)r, p.rp, u, nullptr, nullptr, st))) return rc;
+    }
+    if (dx) {
+      uint16_t* wt = reinterpret_cast<uint16_t*>(ws + w.wd);
+      if ((rc = launch_dequant_transpose(q, K, scales, N, K, wt, st))) return rc;
+      GemmArgs g{};
+      g.act = dyb; g.q = nullptr; g.colscale = nullptr; g.L = r > 0 ? u : nullptr; g.R = Ab;
+      g.bias = nullptr; g.out = static_cast<uint16_t*>(dx);
+      g.M = M; g.Ncols = K; g.Kred = N; g.ldq = N; g.rp = r > 0 ? p.rp : 0; g.c = lora_scale;
+      if ((rc = launch_bfgemm(1, g, wt, st))) return rc;
+    }
+  } else if (r > 0 || dx) {
+    // 1. u = dy B^T and dys = dy * s in one pass over dy (the scaled copy only when dx is wanted)
     if (r > 0) {
       if ((rc = launch_rowproj(dyb, M, N, Bb, (int)r, p.rp, u, scales, dx ? dys : nullptr, st))) return rc;
     } else {
@@ -632,7 +655,7 @@ extern "C" int reels_hip_i8lora_bwd(const void* dy, const void* x, const void* h
     }
   }
   // 2. dx = dys q + c u A^T
-  if (dx) {
+  if (dx && !p.deq) {
     GemmArgs g{};
     g.act = dys; g.q = q; g.colscale = nullptr; g.L = r > 0 ? u : nullptr; g.R = Ab; g.bias = nullptr;
     g.out = static_cast<uint16_t*>(dx);

@@ -45,8 +45,13 @@ def test_workspace_sizes():
         for which in (0, 1):
             b = L.reels_hip_i8lora_workspace_bytes(M, K, N, r, which)
             assert b > 0 and b % 256 == 0
-    # backward holds dy*s [M][N] bf16 and the h/u panels
-    assert L.reels_hip_i8lora_workspace_bytes(32760, 5120, 5120, 32, 1) >= 32760 * 5120 * 2
+    # K and N multiples of 64: both directions hold the bf16 dequantized weight (N x K), the
+    # backward also the h/u panels [M][r]
+    for which in (0, 1):
+        b = L.reels_hip_i8lora_workspace_bytes(32760, 5120, 13824, 32, which)
+        assert b >= 13824 * 5120 * 2 + 32760 * 32 * 2 * (1 + which)
+    # K a multiple of 16 but not of 64: the int8 GEMM path, whose backward holds dy*s [M][N] bf16
+    assert L.reels_hip_i8lora_workspace_bytes(4096, 5136, 5120, 32, 1) >= 4096 * 5120 * 2
     assert L.reels_hip_i8lora_workspace_bytes(-1, 5, 5, 1, 0) == 0
 
 

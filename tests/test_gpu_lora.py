@@ -92,6 +92,8 @@ def test_reference_gpu_test_shape_ragged(dev):
     (130, 1536, 8960, 32, False),   # FFN-in shape
     (100, 8960, 1536, 32, False),   # FFN-out shape
     (65, 48, 80, 16, False),        # K not a multiple of 64
+    (200, 512, 528, 32, True),      # K % 64 == 0, N % 64 != 0: int8 GEMM forward, general dX
+    (200, 528, 512, 16, False),     # N % 64 == 0, K % 64 != 0: general forward, int8 GEMM dX
     (50, 256, 256, 0, True),        # base-only linear(::DenseLayer) with bias
     (40, 24, 20, 2, True),          # ragged: generic path with bias
 ])
