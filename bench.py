@@ -35,9 +35,9 @@ ALPHA = 32.0
 # HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs of this script (KiB per
 # dispatch scaled by a 1 GiB device copy: FETCH x 2.0, WRITE x 1.0), averaged over one step's
 # launches; the commands and per-kernel figures are in profiles/.
-GEMM_TRAFFIC_BYTES = 3313369504
-GEMM_TRAFFIC_NOTE = ("mean over one step's 12 GEMM launches (q/k/v/o 2.20 GB, ffn 5.34-5.75 GB); "
-                     "FETCH_SIZE includes Infinity Cache hits; algorithmic mean 0.905 GB")
+GEMM_TRAFFIC_BYTES = 4700936074
+GEMM_TRAFFIC_NOTE = ("mean over one step's 12 GEMM launches (q/k/v/o 3.08-3.19 GB, ffn 7.60-8.03 GB); "
+                     "FETCH_SIZE includes Infinity Cache hits; algorithmic mean 0.946 GB")
 PACK_TRAFFIC_BYTES = 14792000000  # mean of the two launches (21.088 + 8.496 GB), ratio 1.000
 PROJECTIONS = [("self_attn.q", 5120, 5120), ("self_attn.k", 5120, 5120),
                ("self_attn.v", 5120, 5120), ("self_attn.o", 5120, 5120),
@@ -338,8 +338,8 @@ def main():
     gemm_names = sorted({n for (n, _) in recs if "gemm_kernel" in n})
     vendor = vendor_gemm_tflops(dev, M, 5120, 5120)
     roofline = {
-        "kernel": " + ".join(gemm_names) + " (<0> fwd, <1> dX; int8 weight converted to bf16 "
-                                           "for MFMA)",
+        "kernel": " + ".join(gemm_names) + " (<0> fwd, <1> dX; bf16 MFMA on the dequantized "
+                                           "weight bf16(q*s))",
         "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
         "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
         "traffic": GEMM_TRAFFIC_BYTES,
