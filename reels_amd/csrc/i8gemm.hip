@@ -1,19 +1,25 @@
-// Dense int8-weight GEMMs of the LoRA linear, bf16 MFMA on gfx950.
+// GEMMs of the int8 LoRA linear, bf16 MFMA on gfx950.
 //
 //   FWD (_weight_mul, src/layers/quantization.jl:73-74, inside lora_forward, lora.jl:56-95):
-//     out[m][n] = bf16( s[n] * sum_k act[m][k] q[n][k] + c * sum_j L[m][j] R[n][j] + bias[n] )
+//     out[m][n] = bf16( sum_k act[m][k] deq(W)[n][k] + c * sum_j L[m][j] R[n][j] + bias[n] )
 //     act = x [M][K], L = h [M][rp], R = B^T [N][rp]
 //   DX  (_weight_transpose_mul, quantization.jl:75-76, inside lora_backward, lora.jl:115-116):
-//     out[m][k] = bf16( sum_n act[m][n] q[n][k] + c * sum_j L[m][j] R[k][j] )
-//     act = bf16(dy * s) [M][N], L = u [M][rp], R = A [K][rp]
+//     out[m][k] = bf16( sum_n act[m][n] deq(W)[n][k] + c * sum_j L[m][j] R[k][j] )
+//     act = dy [M][N], L = u [M][rp], R = A [K][rp]
 //
-// Block tile: 256 output columns (n in FWD, k in DX) x 256 tokens, reduction step 64, 256 threads
-// = 4 waves in a 2 x 2 grid, each wave 128 x 128 = 4 x 4 tiles of v_mfma_f32_32x32x16_bf16.
-// The MFMA A operand is the weight (rows = output columns) and the B operand the activations
-// (columns = tokens), so each lane ends with 4 consecutive output columns of one token and the
-// epilogue stores 8 bytes per lane.
+// Kernels in this file:
+// * dequant_rows_kernel / dequant_transpose_kernel + bfgemm_kernel: the path for K and N
+//   multiples of 64 (every Wan / LTX projection): deq(W) = bf16(fl32(q * s)) written once per
+//   call (transposed for DX, scale folded in), then a bf16 GEMM with the LoRA epilogue.
+// * i8gemm_v3_kernel (reduction a multiple of 64) and i8gemm_kernel (any reduction multiple of
+//   16): the int8 codes themselves are staged in LDS and converted exactly to bf16 in registers;
+//   the FWD scale s[n] is applied to the f32 sum, and DX takes act = bf16(dy * s).
 //
-// LDS (double-buffered, 96 KiB):
+// i8gemm_kernel: block tile 256 output columns (n in FWD, k in DX) x 256 tokens, reduction step
+// 64, 256 threads = 4 waves in a 2 x 2 grid, each wave 128 x 128 = 4 x 4 tiles of
+// v_mfma_f32_32x32x16_bf16. The MFMA A operand is the weight (rows = output columns) and the B
+// operand the activations (columns = tokens), so each lane ends with 4 consecutive output
+// columns of one token and the epilogue stores 8 bytes per lane. LDS (double-buffered, 96 KiB):
 //   activations: [256 tokens][64] bf16, 16-byte chunks XOR-swizzled by f(row) so the 32-row
 //                MFMA operand reads (ds_read_b128) hit distinct banks;
 //   weights: int8 as loaded from HBM (half the LDS bytes of bf16), converted exactly to bf16 in
