@@ -639,6 +639,7 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
     voa[i] = (uint32_t)((m * Kred + c * 8) * 2);
     vow[i] = (uint32_t)((n * Kred + c * 8) * 2);
   }
+  const i32x4 rnone = buffer_rsrc(a.act, 0u);  // zero records: a copy through it reads nothing
   const int nk = (int)(Kred / BK);
   auto issue = [&](int kt, int stage) {
     uint8_t* base = smem + stage * STAGE;
@@ -647,6 +648,13 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
     for (int i = 0; i < 4; ++i) dma16(ract, voa[i], so, base + (w * 4 + i) * 1024);
 #pragma unroll
     for (int i = 0; i < 4; ++i) dma16(rw, vow[i], so, base + ACT + (w * 4 + i) * 1024);
+  };
+  // copy i (0-3 activation rows, 4-7 weight rows) of step kt; ra / rb select real or empty copies
+  auto issue_one = [&](int kt, int stage, int i, const i32x4& ra, const i32x4& rb) {
+    uint8_t* base = smem + stage * STAGE;
+    const uint32_t so = (uint32_t)kt * (BK * 2);
+    if (i < 4) dma16(ra, voa[i], so, base + (w * 4 + i) * 1024);
+    else dma16(rb, vow[i - 4], so, base + ACT + (w * 4 + i - 4) * 1024);
   };
 
   f32x16 acc[2][4];
@@ -683,15 +691,8 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
   };
 
   bf16x8 xa[4], xb[4], wa[2], wb[2];
-  issue(0, 0);
-  if (nk > 1) issue(1, 1);
-  if (nk > 1) __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8): step 1 may stay in flight
-  else __builtin_amdgcn_s_waitcnt(0x0F70);
-  __builtin_amdgcn_s_barrier();
-  read_w(smem + ACT, 0, wa);
-  read_x(smem, 0, xa);
-  for (int kt = 0; kt < nk; ++kt) {
-    const uint8_t* sa = smem + (kt & 1) * STAGE;
+  // sub-steps 0-2 of a step (fragments of sub-step 0 already in wa / xa)
+  auto substeps012 = [&](const uint8_t* sa) {
     __builtin_amdgcn_iglp_opt(1);
     read_w(sa + ACT, 1, wb);
     read_x(sa, 1, xb);
@@ -702,17 +703,43 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
     read_w(sa + ACT, 3, wb);
     read_x(sa, 3, xb);
     mfma8(wa, xa);
-    if (kt + 1 < nk) {
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave is done reading stage kt
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): step kt+1 has landed
-      __builtin_amdgcn_s_barrier();
-      if (kt + 2 < nk) issue(kt + 2, kt & 1);
-      const uint8_t* sn = smem + ((kt + 1) & 1) * STAGE;
-      read_w(sn + ACT, 0, wa);
-      read_x(sn, 0, xa);
+  };
+  issue(0, 0);
+  if (nk > 1) issue(1, 1);
+  if (nk > 1) __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8): step 1 may stay in flight
+  else __builtin_amdgcn_s_waitcnt(0x0F70);
+  __builtin_amdgcn_s_barrier();
+  read_w(smem + ACT, 0, wa);
+  read_x(smem, 0, xa);
+  // Steps 0 .. nk-2 (the last step is peeled below so that this loop has no data branches):
+  // after the barrier come the next stage's first fragment reads, then sub-step 3's eight MFMAs
+  // alternating with the eight copies of step kt+2 (each MFMA covers one copy's issue). Past the
+  // end the copies go through a zero-record descriptor: they move no memory and write zeros into
+  // the stage of step kt, which no wave reads any more.
+  for (int kt = 0; kt + 1 < nk; ++kt) {
+    substeps012(smem + (kt & 1) * STAGE);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave is done reading stage kt
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): step kt+1 has landed
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    const bool pre = kt + 2 < nk;
+    const i32x4 ra = pre ? ract : rnone, rb = pre ? rw : rnone;
+    const uint8_t* sn = smem + ((kt + 1) & 1) * STAGE;
+    read_w(sn + ACT, 0, wa);
+    read_x(sn, 0, xa);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      acc[i & 1][i >> 1] =
+          __builtin_amdgcn_mfma_f32_32x32x16_bf16(wb[i & 1], xb[i >> 1], acc[i & 1][i >> 1], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      issue_one(kt + 2, kt & 1, i, ra, rb);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    mfma8(wb, xb);
   }
+  substeps012(smem + ((nk - 1) & 1) * STAGE);
+  mfma8(wb, xb);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // the empty copies have landed before LDS is reused
 
   // epilogue: LoRA up-projection on MFMA, bias, one bf16 rounding; the 256 x 256 tile is staged
   // in LDS (rows of 512 bytes, 16-byte chunks XOR-swizzled by row) and stored as whole rows
