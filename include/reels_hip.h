@@ -69,6 +69,20 @@ const char* reels_hip_last_error(void);
 int reels_hip_i8_pack(const void* w, int dtype, int64_t N, int64_t K, int64_t ld_w, int8_t* q,
                       float* scales, int32_t* status, void* stream);
 
+/*
+ * Dequantization for compute, _dequantize_for_compute / _host_dequantize
+ * (src/layers/quantization.jl:25-29, 54-64): out = cast(T, q * s) per output channel n.
+ *   REELS_HIP_F32   out = fl32(q[n][k] * s[n])            Float32.(values) .* Float32.(scales)
+ *   REELS_HIP_F16   out = f16(q[n][k] * f16(s[n]))        Float16.(values) .* Float16.(scales)
+ *   REELS_HIP_BF16  out = bf16(fl32(q[n][k] * s[n]))      the weight the bf16 GEMMs multiply
+ *   q [N][ld_q] int8 (ld_q >= K), scales [N] f32
+ *   transpose = 0: out [N][K] (row stride K); 1: out [K][N] (row stride N)
+ * The int8 LoRA linear runs the BF16 form internally (plain for the forward, transposed for dX);
+ * this entry point exposes it, e.g. for merged_weight.
+ */
+int reels_hip_i8_dequant(const int8_t* q, const float* scales, int64_t N, int64_t K, int64_t ld_q,
+                         int dtype, int transpose, void* out, void* stream);
+
 /* Bytes of device workspace needed by reels_hip_i8lora_fwd (which = REELS_HIP_WS_FWD) or
  * reels_hip_i8lora_bwd (REELS_HIP_WS_BWD) for these sizes. Always a multiple of 256. */
 size_t reels_hip_i8lora_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t r, int which);

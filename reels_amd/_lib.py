@@ -22,6 +22,7 @@ EXPORTS = (
     "reels_hip_abi_version",
     "reels_hip_last_error",
     "reels_hip_i8_pack",
+    "reels_hip_i8_dequant",
     "reels_hip_i8lora_workspace_bytes",
     "reels_hip_i8lora_fwd",
     "reels_hip_i8lora_bwd",
@@ -66,6 +67,8 @@ def lib():
     L.reels_hip_last_error.restype = ctypes.c_char_p
     L.reels_hip_i8_pack.argtypes = [vp, ctypes.c_int, i64, i64, i64, vp, vp, vp, vp]
     L.reels_hip_i8_pack.restype = ctypes.c_int
+    L.reels_hip_i8_dequant.argtypes = [vp, vp, i64, i64, i64, ctypes.c_int, ctypes.c_int, vp, vp]
+    L.reels_hip_i8_dequant.restype = ctypes.c_int
     L.reels_hip_i8lora_workspace_bytes.argtypes = [i64, i64, i64, i64, ctypes.c_int]
     L.reels_hip_i8lora_workspace_bytes.restype = sz
     L.reels_hip_i8lora_fwd.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, ctypes.c_float,

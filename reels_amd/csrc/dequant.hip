@@ -1,0 +1,139 @@
+// Dequantization for compute: _dequantize_for_compute / _host_dequantize
+// (src/layers/quantization.jl:25-29, 54-64), out = cast(T, q * s) per output channel.
+//   f32:  fl32(q * s)             Float32.(values) .* Float32.(scales)
+//   f16:  f16(q * f16(s))         Float16.(values) .* Float16.(scales) (the product of two
+//                                 binary16 values is exact in f32, then one rounding)
+//   bf16: bf16(fl32(q * s))       the weight the bf16 GEMMs of the LoRA linear multiply
+// The bf16 forms used inside the LoRA linear have streaming kernels (16 codes per thread; 64 x 64
+// LDS tiles for the transpose); every other case runs one element per thread.
+#include <algorithm>
+
+#include "i8gemm.h"
+
+namespace reels {
+
+__global__ __launch_bounds__(256) void dequant_rows_kernel(const int8_t* __restrict__ q, int64_t ldq,
+                                                           const float* __restrict__ s, int64_t N,
+                                                           int64_t K, uint16_t* __restrict__ wd) {
+  const int64_t groups = K >> 4;  // 16 codes per thread
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= N * groups) return;
+  const int64_t n = i / groups, c = i - n * groups;
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(q + n * ldq + c * 16));
+  const float sc = s[n];
+  u32x4 o[2];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const uint32_t x = v[d];
+    const float f0 = (float)(int8_t)(x & 0xff) * sc, f1 = (float)(int8_t)((x >> 8) & 0xff) * sc;
+    const float f2 = (float)(int8_t)((x >> 16) & 0xff) * sc, f3 = (float)((int32_t)x >> 24) * sc;
+    o[d >> 1][(d & 1) * 2] = pack_bf16x2(f0, f1);
+    o[d >> 1][(d & 1) * 2 + 1] = pack_bf16x2(f2, f3);
+  }
+  u32x4* dst = reinterpret_cast<u32x4*>(wd + n * K + c * 16);
+  dst[0] = o[0];
+  dst[1] = o[1];
+}
+
+// 64 x 64 tiles through LDS: a thread reads 16 codes of one row n and writes them as bf16 into
+// column n of the [k][n] tile; it then stores 16 consecutive n of one row k (two 16-byte stores).
+__global__ __launch_bounds__(256) void dequant_transpose_kernel(const int8_t* __restrict__ q,
+                                                                int64_t ldq,
+                                                                const float* __restrict__ s,
+                                                                int64_t N, int64_t K,
+                                                                uint16_t* __restrict__ wt) {
+  __shared__ uint16_t tile[64][66];  // [k][n], rows padded to 132 bytes
+  const int64_t n0 = (int64_t)blockIdx.y * 64, k0 = (int64_t)blockIdx.x * 64;
+  const int t = threadIdx.x;
+  {
+    const int nl = t >> 2, kl = (t & 3) * 16;
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(q + (n0 + nl) * ldq + k0 + kl));
+    const float sc = s[n0 + nl];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const float f = (float)(int8_t)((v[j >> 2] >> (8 * (j & 3))) & 0xff) * sc;
+      tile[kl + j][nl] = (uint16_t)f32_to_bf16_bits(f);
+    }
+  }
+  __syncthreads();
+  const int kr = t >> 2, nc = (t & 3) * 16;
+  const uint32_t* row = reinterpret_cast<const uint32_t*>(&tile[kr][nc]);
+  u32x4 o0 = {row[0], row[1], row[2], row[3]}, o1 = {row[4], row[5], row[6], row[7]};
+  u32x4* dst = reinterpret_cast<u32x4*>(wt + (k0 + kr) * N + n0 + nc);
+  dst[0] = o0;
+  dst[1] = o1;
+}
+
+template <int DT, bool TRANS>  // DT: REELS_HIP_F32 / F16 / BF16
+__global__ __launch_bounds__(256) void dequant_generic_kernel(const int8_t* __restrict__ q,
+                                                              int64_t ldq,
+                                                              const float* __restrict__ s,
+                                                              int64_t N, int64_t K, void* out) {
+  const int64_t total = N * K, stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += stride) {
+    int64_t n, k;  // out index i is row-major in the output layout, so stores coalesce
+    if (TRANS) { k = i / N; n = i - k * N; } else { n = i / K; k = i - n * K; }
+    const float qv = (float)q[n * ldq + k];
+    if (DT == REELS_HIP_F32) static_cast<float*>(out)[i] = qv * s[n];
+    // f16: one correctly rounded binary16 multiply equals f16(fl32(q * f16(s))) (the f32 product
+    // is exact). Written in f32 the compiler folds it into v_fma_mixlo_f16 with a +0 addend,
+    // which turns a -0 product (q < 0, f16(s) == 0) into +0.
+    else if (DT == REELS_HIP_F16) static_cast<_Float16*>(out)[i] = (_Float16)qv * (_Float16)s[n];
+    else static_cast<uint16_t*>(out)[i] = (uint16_t)f32_to_bf16_bits(qv * s[n]);
+  }
+}
+
+int launch_dequant_rows(const int8_t* q, int64_t ldq, const float* s, int64_t N, int64_t K,
+                        uint16_t* wd, hipStream_t st) {
+  const int64_t n = N * (K >> 4);
+  { TraceScope _ts(st, "dequant_rows_kernel");
+    dequant_rows_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, st>>>(q, ldq, s, N, K, wd); }
+  return check_launch("dequant_rows_kernel");
+}
+
+int launch_dequant_transpose(const int8_t* q, int64_t ldq, const float* s, int64_t N, int64_t K,
+                             uint16_t* wt, hipStream_t st) {
+  { TraceScope _ts(st, "dequant_transpose_kernel");
+    dequant_transpose_kernel<<<dim3((unsigned)(K / 64), (unsigned)(N / 64)), 256, 0, st>>>(q, ldq, s, N, K, wt); }
+  return check_launch("dequant_transpose_kernel");
+}
+
+}  // namespace reels
+
+using namespace reels;
+
+extern "C" int reels_hip_i8_dequant(const int8_t* q, const float* scales, int64_t N, int64_t K,
+                                    int64_t ld_q, int dtype, int transpose, void* out,
+                                    void* stream) {
+  clear_error();
+  if (N < 0 || K < 0 || ld_q < K)
+    return fail(REELS_HIP_EINVAL, "reels_hip_i8_dequant: need N >= 0, K >= 0 and ld_q >= K");
+  if (dtype != REELS_HIP_F32 && dtype != REELS_HIP_BF16 && dtype != REELS_HIP_F16)
+    return fail(REELS_HIP_EDTYPE, "reels_hip_i8_dequant: dtype must be REELS_HIP_F32, "
+                                  "REELS_HIP_BF16 or REELS_HIP_F16");
+  if (transpose != 0 && transpose != 1)
+    return fail(REELS_HIP_EINVAL, "reels_hip_i8_dequant: transpose must be 0 or 1");
+  if (N == 0 || K == 0) return REELS_HIP_OK;
+  if (q == nullptr || scales == nullptr || out == nullptr)
+    return fail(REELS_HIP_EINVAL, "reels_hip_i8_dequant: NULL q, scales or out");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const bool al = aligned16(q) && aligned16(out) && ld_q % 16 == 0;
+  if (dtype == REELS_HIP_BF16 && !transpose && al && K % 16 == 0)
+    return launch_dequant_rows(q, ld_q, scales, N, K, static_cast<uint16_t*>(out), st);
+  if (dtype == REELS_HIP_BF16 && transpose && al && N % 64 == 0 && K % 64 == 0)
+    return launch_dequant_transpose(q, ld_q, scales, N, K, static_cast<uint16_t*>(out), st);
+  const unsigned grid = (unsigned)std::min<int64_t>(ceil_div(N * K, 256), 1 << 16);  // grid-stride
+  { TraceScope _ts(st, "dequant_generic_kernel");
+    if (dtype == REELS_HIP_F32) {
+      if (transpose) dequant_generic_kernel<REELS_HIP_F32, true><<<grid, 256, 0, st>>>(q, ld_q, scales, N, K, out);
+      else dequant_generic_kernel<REELS_HIP_F32, false><<<grid, 256, 0, st>>>(q, ld_q, scales, N, K, out);
+    } else if (dtype == REELS_HIP_F16) {
+      if (transpose) dequant_generic_kernel<REELS_HIP_F16, true><<<grid, 256, 0, st>>>(q, ld_q, scales, N, K, out);
+      else dequant_generic_kernel<REELS_HIP_F16, false><<<grid, 256, 0, st>>>(q, ld_q, scales, N, K, out);
+    } else {
+      if (transpose) dequant_generic_kernel<REELS_HIP_BF16, true><<<grid, 256, 0, st>>>(q, ld_q, scales, N, K, out);
+      else dequant_generic_kernel<REELS_HIP_BF16, false><<<grid, 256, 0, st>>>(q, ld_q, scales, N, K, out);
+    }
+  }
+  return check_launch("dequant_generic_kernel");
+}

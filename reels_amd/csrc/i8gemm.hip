@@ -536,59 +536,8 @@ void i8gemm_v3_kernel(GemmArgs a, int tiles_n, int tiles_m) {
 // runs on it. For dX the copy is written transposed, wt[k][n] = bf16(fl32(q[n][k] * s[n])), so
 // the same GEMM computes dx = dy wt^T with the scale folded into the weight. Against the int8
 // GEMM above this takes the int8 -> bf16 conversion (VALU in every wave's inner loop) out of the
-// GEMM at the cost of a streaming pass over the weight (~1-2% of the GEMM's time).
-
-__global__ __launch_bounds__(256) void dequant_rows_kernel(const int8_t* __restrict__ q, int64_t ldq,
-                                                           const float* __restrict__ s, int64_t N,
-                                                           int64_t K, uint16_t* __restrict__ wd) {
-  const int64_t groups = K >> 4;  // 16 codes per thread
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= N * groups) return;
-  const int64_t n = i / groups, c = i - n * groups;
-  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(q + n * ldq + c * 16));
-  const float sc = s[n];
-  u32x4 o[2];
-#pragma unroll
-  for (int d = 0; d < 4; ++d) {
-    const uint32_t x = v[d];
-    const float f0 = (float)(int8_t)(x & 0xff) * sc, f1 = (float)(int8_t)((x >> 8) & 0xff) * sc;
-    const float f2 = (float)(int8_t)((x >> 16) & 0xff) * sc, f3 = (float)((int32_t)x >> 24) * sc;
-    o[d >> 1][(d & 1) * 2] = pack_bf16x2(f0, f1);
-    o[d >> 1][(d & 1) * 2 + 1] = pack_bf16x2(f2, f3);
-  }
-  u32x4* dst = reinterpret_cast<u32x4*>(wd + n * K + c * 16);
-  dst[0] = o[0];
-  dst[1] = o[1];
-}
-
-// 64 x 64 tiles through LDS: a thread reads 16 codes of one row n and writes them as bf16 into
-// column n of the [k][n] tile; it then stores 16 consecutive n of one row k (two 16-byte stores).
-__global__ __launch_bounds__(256) void dequant_transpose_kernel(const int8_t* __restrict__ q,
-                                                                int64_t ldq,
-                                                                const float* __restrict__ s,
-                                                                int64_t N, int64_t K,
-                                                                uint16_t* __restrict__ wt) {
-  __shared__ uint16_t tile[64][66];  // [k][n], rows padded to 132 bytes
-  const int64_t n0 = (int64_t)blockIdx.y * 64, k0 = (int64_t)blockIdx.x * 64;
-  const int t = threadIdx.x;
-  {
-    const int nl = t >> 2, kl = (t & 3) * 16;
-    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(q + (n0 + nl) * ldq + k0 + kl));
-    const float sc = s[n0 + nl];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const float f = (float)(int8_t)((v[j >> 2] >> (8 * (j & 3))) & 0xff) * sc;
-      tile[kl + j][nl] = (uint16_t)f32_to_bf16_bits(f);
-    }
-  }
-  __syncthreads();
-  const int kr = t >> 2, nc = (t & 3) * 16;
-  const uint32_t* row = reinterpret_cast<const uint32_t*>(&tile[kr][nc]);
-  u32x4 o0 = {row[0], row[1], row[2], row[3]}, o1 = {row[4], row[5], row[6], row[7]};
-  u32x4* dst = reinterpret_cast<u32x4*>(wt + (k0 + kr) * N + n0 + nc);
-  dst[0] = o0;
-  dst[1] = o1;
-}
+// GEMM at the cost of a streaming pass over the weight (~1-2% of the GEMM's time); the passes
+// are in dequant.hip.
 
 // bf16 GEMM: 256 x 256 block tile, reduction step 64, 8 waves (two per SIMD), each wave 128
 // tokens x 64 output columns (4 x 2 tiles of v_mfma_f32_32x32x16_bf16); HBM -> LDS copies into a
@@ -822,21 +771,6 @@ int launch_bfgemm(int mode, const GemmArgs& a, const uint16_t* wd, hipStream_t s
   { TraceScope _ts(st, mode == 0 ? "bfgemm_kernel<0>" : "bfgemm_kernel<1>");
     bfgemm_kernel<<<tn * tm, bfg::NT, 2 * bfg::STAGE, st>>>(a, wd, tn, tm); }
   return check_launch("bfgemm_kernel");
-}
-
-int launch_dequant_rows(const int8_t* q, int64_t ldq, const float* s, int64_t N, int64_t K,
-                        uint16_t* wd, hipStream_t st) {
-  const int64_t n = N * (K >> 4);
-  { TraceScope _ts(st, "dequant_rows_kernel");
-    dequant_rows_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, st>>>(q, ldq, s, N, K, wd); }
-  return check_launch("dequant_rows_kernel");
-}
-
-int launch_dequant_transpose(const int8_t* q, int64_t ldq, const float* s, int64_t N, int64_t K,
-                             uint16_t* wt, hipStream_t st) {
-  { TraceScope _ts(st, "dequant_transpose_kernel");
-    dequant_transpose_kernel<<<dim3((unsigned)(K / 64), (unsigned)(N / 64)), 256, 0, st>>>(q, ldq, s, N, K, wt); }
-  return check_launch("dequant_transpose_kernel");
 }
 
 int launch_i8gemm(int mode, const GemmArgs& a, hipStream_t st) {

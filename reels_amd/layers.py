@@ -66,11 +66,29 @@ class QuantizedMatrix:
     def size(self, dim=None):
         return self.shape if dim is None else self.shape[dim]
 
-    def dequantize(self, dtype: Optional[torch.dtype] = None) -> torch.Tensor:
-        """_host_dequantize (quantization.jl:25-29): cast(T, Float32(q) * s). A debugging and
-        merged-weight helper; the forward and backward never materialise it."""
+    def dequantize(self, dtype: Optional[torch.dtype] = None, transpose: bool = False,
+                   stream=None) -> torch.Tensor:
+        """_materialize_weight / _dequantize_for_compute (quantization.jl:54-64) on the GPU
+        (reels_hip_i8_dequant): float32 fl32(q s), float16 f16(q f16(s)), bfloat16
+        bf16(fl32(q s)) - the weight the int8 LoRA linear multiplies. [N][K], or [K][N] with
+        transpose. (The host-side _host_dequantize, quantization.jl:25-29, agrees for float32
+        and bfloat16; for float16 it rounds fl32(q s) instead of multiplying by f16(s).)"""
         d = dtype or self.compute_dtype
-        return (self.values.float() * self.scales[:, None]).to(d)
+        if d not in _DTYPE_CODE:
+            raise TypeError(f"unsupported dtype {d}")
+        _need_device(self.values, "values")
+        N, K = self.values.shape
+        q = self.values if self.values.stride(1) == 1 else self.values.contiguous()
+        sc = self.scales
+        if sc.dtype != torch.float32 or sc.device != q.device or sc.shape != (N,):
+            raise ValueError("scales must be a float32 vector of length N on the codes' device")
+        sc = sc.contiguous()
+        out = torch.empty((K, N) if transpose else (N, K), dtype=d, device=q.device)
+        st = _stream(q.device) if stream is None else stream
+        _lib.check("reels_hip_i8_dequant", _lib.lib().reels_hip_i8_dequant(
+            ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(sc.data_ptr()), N, K,
+            q.stride(0), _DTYPE_CODE[d], int(transpose), ctypes.c_void_p(out.data_ptr()), st))
+        return out
 
 
 def quantize_frozen_matrix(weight: torch.Tensor, T: Optional[torch.dtype] = None,

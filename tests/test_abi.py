@@ -134,3 +134,15 @@ def test_cpu_tensors_are_rejected_not_computed():
     from reels_amd import quantize_frozen_matrix
     with pytest.raises(ValueError, match="ROCm device"):
         quantize_frozen_matrix(torch.zeros((4, 16)))
+
+
+def test_dequant_argument_errors():
+    L = _lib.lib()
+    fake = ctypes.c_void_p(4096)
+    assert L.reels_hip_i8_dequant(fake, fake, 4, 8, 4, 0, 0, fake, None) == -1  # ld_q < K
+    assert L.reels_hip_i8_dequant(fake, fake, -1, 8, 8, 0, 0, fake, None) == -1
+    assert L.reels_hip_i8_dequant(fake, fake, 4, 8, 8, 9, 0, fake, None) == -2
+    assert L.reels_hip_i8_dequant(fake, fake, 4, 8, 8, 0, 2, fake, None) == -1
+    assert L.reels_hip_i8_dequant(None, fake, 4, 8, 8, 1, 0, fake, None) == -1
+    assert "NULL" in _err()
+    assert L.reels_hip_i8_dequant(None, None, 0, 8, 8, 1, 1, None, None) == 0  # empty: no work
