@@ -540,11 +540,11 @@ void i8gemm_v3_kernel(GemmArgs a, int tiles_n, int tiles_m) {
 // are in dequant.hip.
 
 // bf16 GEMM: 256 x 256 block tile, reduction step 64, 8 waves (two per SIMD), each wave 128
-// tokens x 64 output columns (4 x 2 tiles of v_mfma_f32_32x32x16_bf16); HBM -> LDS copies into a
-// two-stage ring of 64 KiB stages (activation and weight tiles [256][64] bf16 with the same
-// 16-byte XOR swizzle). At the barrier that ends step kt every wave has finished reading stage kt
-// (lgkmcnt(0) before it), so the copy of step kt+2 goes into it right away and has one step to
-// land. XCD-aware tile order and the epilogue as in the int8 kernel (minus the column scale).
+// tokens x 64 output columns; HBM -> LDS copies into a two-stage ring of 64 KiB stages
+// (activation and weight tiles [256][64] bf16 with the same 16-byte XOR swizzle). At the barrier
+// that ends step kt every wave has finished reading stage kt (lgkmcnt(0) before it), so the copy
+// of step kt+2 goes into it right away and has one step to land. XCD-aware tile order and the
+// epilogue as in the int8 kernel (minus the column scale).
 namespace bfg {
 constexpr int BM = 256, BN = 256, BK = 64, NT = 512;
 constexpr int ACT = BM * BK * 2;   // 32 KiB
@@ -553,6 +553,13 @@ constexpr int STAGE = ACT + WB;    // 64 KiB
 constexpr int GM = 4;
 }  // namespace bfg
 
+// MFMA shape: v_mfma_f32_16x16x32_bf16, so a wave's 128 x 64 is 8 x 4 tiles of 16 x 16 and a
+// step is two sub-steps of k = 32. Per flop it moves half the accumulator registers of
+// v_mfma_f32_32x32x16_bf16 (4 per 16K flops against 16 per 32K); the GPU runs at its power cap
+// under this load, and sustained register-only loops of the 16 x 16 form run 10-13% faster
+// (this GEMM: +3.5% over the same kernel on 32 x 32 tiles). Lane l supplies row l % 16 of both
+// operands with k = 8 (l / 16) + (0..7) (any k order shared by the two operands gives the same
+// sum); D register v of lane l is output column 4 (l / 16) + v, token l % 16 of the tile.
 __global__ __launch_bounds__(512)
 void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int tiles_m) {
   using namespace bfg;
@@ -560,7 +567,7 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
   const int t = threadIdx.x, lane = t & 63;
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);
   const int wm = w >> 2, wn = w & 3;
-  const int l32 = lane & 31, lhi = lane >> 5;
+  const int l16 = lane & 15, lq = lane >> 4;
   const int64_t M = a.M, Ncols = a.Ncols, Kred = a.Kred;
 
   const int nt = tiles_n * tiles_m;
@@ -598,7 +605,6 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
 #pragma unroll
     for (int i = 0; i < 4; ++i) dma16(rw, vow[i], so, base + ACT + (w * 4 + i) * 1024);
   };
-  // copy i (0-3 activation rows, 4-7 weight rows) of step kt; ra / rb select real or empty copies
   auto issue_one = [&](int kt, int stage, int i, const i32x4& ra, const i32x4& rb) {
     uint8_t* base = smem + stage * STAGE;
     const uint32_t so = (uint32_t)kt * (BK * 2);
@@ -606,67 +612,65 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
     else dma16(rb, vow[i - 4], so, base + ACT + (w * 4 + i - 4) * 1024);
   };
 
-  f32x16 acc[2][4];
+  f32x4 acc[4][8];  // [output-column tile][token tile]
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 8; ++j)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+      for (int v = 0; v < 4; ++v) acc[i][j][v] = 0.0f;
 
-  // sub-step s of a step uses k = 16 s + 8 lhi + (0..7): 16-byte chunk 2 s + lhi of each row
-  auto read_x = [&](const uint8_t* sa, int s, bf16x8* xf) {
-    const int c = 2 * s + lhi;
+  // fragment reads: sub-step s of a step uses the 16-byte chunk 4 s + l / 16 of each row; rows of
+  // a 16-row tile start at multiples of 16, so the row swizzle depends on the lane only
+  const int swz = act_swz(l16);
+  auto read_w = [&](const uint8_t* sw, int s, bf16x8* wf) {
+    const int off = ((4 * s + lq) ^ swz) << 4;
 #pragma unroll
-    for (int tj = 0; tj < 4; ++tj) {
-      const int row = wm * 128 + tj * 32 + l32;
-      xf[tj] = as_bf16x8(*reinterpret_cast<const u32x4*>(sa + row * 128 + ((c ^ act_swz(row)) << 4)));
-    }
+    for (int ti = 0; ti < 4; ++ti)
+      wf[ti] = as_bf16x8(*reinterpret_cast<const u32x4*>(sw + (wn * 64 + ti * 16 + l16) * 128 + off));
   };
-  auto read_w = [&](const uint8_t* sw, int s, bf16x8* af) {
-    const int c = 2 * s + lhi;
-#pragma unroll
-    for (int ti = 0; ti < 2; ++ti) {
-      const int row = wn * 64 + ti * 32 + l32;
-      af[ti] = as_bf16x8(*reinterpret_cast<const u32x4*>(sw + row * 128 + ((c ^ act_swz(row)) << 4)));
-    }
+  auto read_x = [&](const uint8_t* sa, int s, int tj) {
+    const int off = ((4 * s + lq) ^ swz) << 4;
+    return as_bf16x8(*reinterpret_cast<const u32x4*>(sa + (wm * 128 + tj * 16 + l16) * 128 + off));
   };
-  auto mfma8 = [&](const bf16x8* af, const bf16x8* xf) {
+  auto mfma4 = [&](const bf16x8* wf, const bf16x8& xf, int tj) {
 #pragma unroll
-    for (int tj = 0; tj < 4; ++tj)
-#pragma unroll
-      for (int ti = 0; ti < 2; ++ti)
-        acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ti], xf[tj], acc[ti][tj], 0, 0, 0);
+    for (int ti = 0; ti < 4; ++ti)
+      acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[ti], xf, acc[ti][tj], 0, 0, 0);
   };
 
-  bf16x8 xa[4], xb[4], wa[2], wb[2];
-  // sub-steps 0-2 of a step (fragments of sub-step 0 already in wa / xa)
-  auto substeps012 = [&](const uint8_t* sa) {
-    __builtin_amdgcn_iglp_opt(1);
-    read_w(sa + ACT, 1, wb);
-    read_x(sa, 1, xb);
-    mfma8(wa, xa);
-    read_w(sa + ACT, 2, wa);
-    read_x(sa, 2, xa);
-    mfma8(wb, xb);
-    read_w(sa + ACT, 3, wb);
-    read_x(sa, 3, xb);
-    mfma8(wa, xa);
+  bf16x8 w0[4], w1[4], x[8];
+  // sub-step 0 of a stage (w0, x) while sub-step 1's fragments of the same stage are read: each
+  // token fragment is re-read as soon as its four MFMAs are issued
+  // (the sub-step-1 weight fragments are read after the first group, so that the wait before
+  // that group's MFMAs does not cover them)
+  auto sub0 = [&](const uint8_t* sa) {
+#pragma unroll
+    for (int tj = 0; tj < 8; ++tj) {
+      mfma4(w0, x[tj], tj);
+      __builtin_amdgcn_sched_barrier(0);
+      x[tj] = read_x(sa, 1, tj);
+      if (tj == 0) read_w(sa + ACT, 1, w1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   };
   issue(0, 0);
   if (nk > 1) issue(1, 1);
   if (nk > 1) __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8): step 1 may stay in flight
   else __builtin_amdgcn_s_waitcnt(0x0F70);
   __builtin_amdgcn_s_barrier();
-  read_w(smem + ACT, 0, wa);
-  read_x(smem, 0, xa);
-  // Steps 0 .. nk-2 (the last step is peeled below so that this loop has no data branches):
-  // after the barrier come the next stage's first fragment reads, then sub-step 3's eight MFMAs
-  // alternating with the eight copies of step kt+2 (each MFMA covers one copy's issue). Past the
-  // end the copies go through a zero-record descriptor: they move no memory and write zeros into
-  // the stage of step kt, which no wave reads any more.
+  // no scalar loads pending at the loop entry, so the waits at its head count LDS reads only
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_sched_barrier(0);
+  read_w(smem + ACT, 0, w0);
+#pragma unroll
+  for (int tj = 0; tj < 8; ++tj) x[tj] = read_x(smem, 0, tj);
+  // Steps 0 .. nk-2 (the last one is peeled): sub-step 0, then the barrier that ends the reads of
+  // stage kt, then sub-step 1 with the next stage's sub-step-0 reads and the eight copies of step
+  // kt+2 (one per four MFMAs) into stage kt. Past the end the copies go through a zero-record
+  // descriptor: they move no memory and write zeros into a stage no wave reads any more.
   for (int kt = 0; kt + 1 < nk; ++kt) {
-    substeps012(smem + (kt & 1) * STAGE);
+    sub0(smem + (kt & 1) * STAGE);
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave is done reading stage kt
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): step kt+1 has landed
     __builtin_amdgcn_s_barrier();
@@ -674,70 +678,73 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
     const bool pre = kt + 2 < nk;
     const i32x4 ra = pre ? ract : rnone, rb = pre ? rw : rnone;
     const uint8_t* sn = smem + ((kt + 1) & 1) * STAGE;
-    read_w(sn + ACT, 0, wa);
-    read_x(sn, 0, xa);
+    read_w(sn + ACT, 0, w0);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      acc[i & 1][i >> 1] =
-          __builtin_amdgcn_mfma_f32_32x32x16_bf16(wb[i & 1], xb[i >> 1], acc[i & 1][i >> 1], 0, 0, 0);
+    for (int tj = 0; tj < 8; ++tj) {
+      mfma4(w1, x[tj], tj);
       __builtin_amdgcn_sched_barrier(0);
-      issue_one(kt + 2, kt & 1, i, ra, rb);
+      x[tj] = read_x(sn, 0, tj);
+      issue_one(kt + 2, kt & 1, tj, ra, rb);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
-  substeps012(smem + ((nk - 1) & 1) * STAGE);
-  mfma8(wb, xb);
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // the empty copies have landed before LDS is reused
-
-  // epilogue: LoRA up-projection on MFMA, bias, one bf16 rounding; the 256 x 256 tile is staged
-  // in LDS (rows of 512 bytes, 16-byte chunks XOR-swizzled by row) and stored as whole rows
-  __syncthreads();
-  uint8_t* stile = smem;
-  const int nsteps = a.rp >> 4;
+  {
+    const uint8_t* sa = smem + ((nk - 1) & 1) * STAGE;
+    read_w(sa + ACT, 1, w1);
 #pragma unroll
-  for (int ti = 0; ti < 2; ++ti) {
-    const int64_t nrow = n0 + wn * 64 + ti * 32 + l32;
-    const int64_t nrc = nrow < Ncols ? nrow : Ncols - 1;
-    const int nloc = wn * 64 + ti * 32 + lhi * 4;
-    const int64_t nbase = n0 + nloc;
-    float bs[16];
-#pragma unroll
-    for (int g4 = 0; g4 < 4; ++g4) {
-      const int64_t n = nbase + g4 * 8;
-      u32x2 b2 = {0, 0};
-      if (a.bias != nullptr && n < Ncols) b2 = *reinterpret_cast<const u32x2*>(a.bias + n);
-      bs[g4 * 4 + 0] = bf16_lo(b2[0]); bs[g4 * 4 + 1] = bf16_hi(b2[0]);
-      bs[g4 * 4 + 2] = bf16_lo(b2[1]); bs[g4 * 4 + 3] = bf16_hi(b2[1]);
+    for (int tj = 0; tj < 8; ++tj) {
+      mfma4(w0, x[tj], tj);
+      x[tj] = read_x(sa, 1, tj);
     }
 #pragma unroll
-    for (int tj = 0; tj < 4; ++tj) {
-      const int mloc = wm * 128 + tj * 32 + l32;
-      const int64_t m = m0 + mloc;
-      const int64_t mc = m < M ? m : M - 1;
-      f32x16 lor;
+    for (int tj = 0; tj < 8; ++tj) mfma4(w1, x[tj], tj);
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // the empty copies have landed before LDS is reused
+
+  // epilogue: LoRA up-projection on MFMA (k = 32 per instruction, lanes past the rank supply
+  // zeros), bias, one bf16 rounding; the tile is staged in LDS (rows of 512 bytes, 16-byte
+  // chunks XOR-swizzled by row) and stored as whole rows
+  __syncthreads();
+  uint8_t* stile = smem;
+  const int nsteps = (a.rp + 31) >> 5;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) lor[v] = 0.0f;
-      for (int s = 0; s < nsteps; ++s) {
-        u32x4 rv = *reinterpret_cast<const u32x4*>(a.R + nrc * a.rp + s * 16 + lhi * 8);
-        u32x4 lv = *reinterpret_cast<const u32x4*>(a.L + mc * a.rp + s * 16 + lhi * 8);
-        if (nrow >= Ncols) rv = u32x4{0, 0, 0, 0};
-        if (m >= M) lv = u32x4{0, 0, 0, 0};
-        lor = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(rv), as_bf16x8(lv), lor, 0, 0, 0);
+  for (int ti = 0; ti < 4; ++ti) {
+    const int64_t nrow = n0 + wn * 64 + ti * 16 + l16;  // A-operand row of this lane
+    const int64_t nrc = nrow < Ncols ? nrow : Ncols - 1;
+    const int nloc = wn * 64 + ti * 16 + lq * 4;        // this lane's four output columns
+    const int64_t nb = n0 + nloc;
+    float bs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (a.bias != nullptr && nb < Ncols) {
+      const u32x2 b2 = *reinterpret_cast<const u32x2*>(a.bias + nb);
+      bs[0] = bf16_lo(b2[0]); bs[1] = bf16_hi(b2[0]); bs[2] = bf16_lo(b2[1]); bs[3] = bf16_hi(b2[1]);
+    }
+    f32x4 lor[8];
+#pragma unroll
+    for (int tj = 0; tj < 8; ++tj)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) lor[tj][v] = 0.0f;
+    for (int s = 0; s < nsteps; ++s) {
+      const int k0 = s * 32 + lq * 8;
+      u32x4 rv = {0, 0, 0, 0};
+      if (k0 < a.rp && nrow < Ncols) rv = *reinterpret_cast<const u32x4*>(a.R + nrc * a.rp + k0);
+#pragma unroll
+      for (int tj = 0; tj < 8; ++tj) {
+        const int64_t m = m0 + wm * 128 + tj * 16 + l16;
+        u32x4 lv = {0, 0, 0, 0};
+        if (k0 < a.rp && m < M) lv = *reinterpret_cast<const u32x4*>(a.L + m * a.rp + k0);
+        lor[tj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(rv), as_bf16x8(lv), lor[tj], 0, 0, 0);
       }
+    }
 #pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        float o[4];
+    for (int tj = 0; tj < 8; ++tj) {
+      const int mloc = wm * 128 + tj * 16 + l16;
+      float o[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int v = g4 * 4 + e;
-          o[e] = acc[ti][tj][v] + a.c * lor[v] + bs[v];
-        }
-        const u32x2 pk = {pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
-        const int col = nloc + g4 * 8;
-        const int chunk = (col >> 3) ^ (mloc & 31);
-        *reinterpret_cast<u32x2*>(stile + mloc * 512 + chunk * 16 + (col & 7) * 2) = pk;
-      }
+      for (int v = 0; v < 4; ++v) o[v] = acc[ti][tj][v] + a.c * lor[tj][v] + bs[v];
+      const u32x2 pk = {pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+      const int chunk = (nloc >> 3) ^ (mloc & 31);
+      *reinterpret_cast<u32x2*>(stile + mloc * 512 + chunk * 16 + (nloc & 7) * 2) = pk;
     }
   }
   __syncthreads();
