@@ -49,6 +49,11 @@ constexpr int STAGE_BYTES = ACT_BYTES + W_BYTES;
 __device__ __forceinline__ int act_swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 __device__ __forceinline__ int wf_swz(int row) { return ((row >> 1) & 7) ^ ((row >> 4) & 1); }
 __device__ __forceinline__ int wd_swz(int row) { return (row & 7) | ((row & 1) << 3); }
+// bf16 GEMM tiles ([rows][64] bf16, 8 chunks of 16 bytes per row): chunk ^ (row & 7). Its
+// 16x16x32 fragment reads (lanes 0-15 rows r..r+15 of one chunk, lanes 16-63 the next three
+// chunks) are free of bank conflicts; act_swz's extra ^ (row >> 3) costs 2 of 5 LDS cycles per
+// ds_read_b128 in this pattern (SQ_LDS_BANK_CONFLICT).
+__device__ __forceinline__ int bf_swz(int row) { return row & 7; }
 
 template <int MODE>  // 0 = FWD, 1 = DX
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
@@ -589,7 +594,7 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = (w * 4 + i) * 8 + (lane >> 3);
-    const int c = (lane & 7) ^ act_swz(row);
+    const int c = (lane & 7) ^ bf_swz(row);
     const int64_t m = (m0 + row < M) ? m0 + row : M - 1;
     const int64_t n = (n0 + row < Ncols) ? n0 + row : Ncols - 1;
     voa[i] = (uint32_t)((m * Kred + c * 8) * 2);
@@ -622,7 +627,7 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
 
   // fragment reads: sub-step s of a step uses the 16-byte chunk 4 s + l / 16 of each row; rows of
   // a 16-row tile start at multiples of 16, so the row swizzle depends on the lane only
-  const int swz = act_swz(l16);
+  const int swz = bf_swz(l16);
   auto read_w = [&](const uint8_t* sw, int s, bf16x8* wf) {
     const int off = ((4 * s + lq) ^ swz) << 4;
 #pragma unroll
