@@ -61,6 +61,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="approximate CPU work for the cpu_baseline sample (0 disables it)")
     ap.add_argument("--tokens", type=int, default=TOKENS)
+    ap.add_argument("--dtype", choices=("bf16", "f16"), default="bf16",
+                    help="activation / LoRA element type: bf16 (the default workload) or f16 "
+                         "(the reference's own int8 compute precision, the _f16 entry points)")
     ap.add_argument("--no-pack", action="store_true", help="skip the pack workload")
     ap.add_argument("--pack-only", action="store_true", help="run only the pack workload")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -69,14 +72,16 @@ def parse():
     return ap.parse_args()
 
 
-def vendor_gemm_tflops(dev, M, K, N, seconds=1.5):
-    """bf16 x bf16 -> bf16 torch.matmul (hipBLASLt) on one Wan-14B projection shape, timed over a
+def vendor_gemm_tflops(dev, M, K, N, seconds=1.5, dtype=None):
+    """16-bit torch.matmul (hipBLASLt; bf16 unless dtype says otherwise) on one Wan-14B
+    projection shape, timed over a
     sustained loop (~seconds, like the timed bench steps: the GPU runs at its power cap, so short
     bursts and sustained loops clock differently): the practical MFMA ceiling for a dense GEMM
     of this size on this GPU, measured in the same run."""
     import torch
-    x = torch.randn((M, K), device=dev).to(torch.bfloat16)
-    w = torch.randn((N, K), device=dev).to(torch.bfloat16)
+    dtype = dtype or torch.bfloat16
+    x = torch.randn((M, K), device=dev).to(dtype)
+    w = torch.randn((N, K), device=dev).to(dtype)
     for _ in range(3):
         torch.matmul(x, w.t())
     torch.cuda.synchronize()
@@ -202,14 +207,14 @@ def pack_cpu_baseline(seconds=5.0):
 
 
 class Projection:
-    def __init__(self, name, K, N, M, r, dev, gen):
+    def __init__(self, name, K, N, M, r, dev, gen, act=None):
         import torch
         from reels_amd import quantize_frozen_matrix, workspace_bytes, _lib
         self.name, self.K, self.N, self.M, self.r = name, K, N, M, r
+        bf = act or torch.bfloat16
         w = torch.randn((N, K), generator=gen, device=dev, dtype=torch.float32).mul_(0.02)
-        self.W = quantize_frozen_matrix(w.to(torch.bfloat16))
+        self.W = quantize_frozen_matrix(w.to(bf), bf)
         del w
-        bf = torch.bfloat16
         self.x = torch.randn((M, K), generator=gen, device=dev, dtype=torch.float32).to(bf)
         self.dy = torch.randn((M, N), generator=gen, device=dev, dtype=torch.float32).to(bf)
         self.A = (torch.randn((K, r), generator=gen, device=dev) * 0.01).to(bf)
@@ -233,11 +238,12 @@ class Projection:
                          p(self.wsb), self.wsb_n, st)
 
 
-def run_step(L, projs, check):
+def run_step(L, projs, check, sfx=""):
+    fwd, bwd = getattr(L, "reels_hip_i8lora_fwd" + sfx), getattr(L, "reels_hip_i8lora_bwd" + sfx)
     for pr in projs:
-        check("reels_hip_i8lora_fwd", L.reels_hip_i8lora_fwd(*pr.fwd_args))
+        check("reels_hip_i8lora_fwd" + sfx, fwd(*pr.fwd_args))
     for pr in reversed(projs):
-        check("reels_hip_i8lora_bwd", L.reels_hip_i8lora_bwd(*pr.bwd_args))
+        check("reels_hip_i8lora_bwd" + sfx, bwd(*pr.bwd_args))
 
 
 def cpu_baseline(seconds):
@@ -288,23 +294,25 @@ def main():
         return
     gen = torch.Generator(device=dev).manual_seed(1234)
     M = args.tokens
-    projs = [Projection(n, K, N, M, RANK, dev, gen) for (n, K, N) in PROJECTIONS]
+    act = torch.float16 if args.dtype == "f16" else torch.bfloat16
+    sfx = "_f16" if args.dtype == "f16" else ""
+    projs = [Projection(n, K, N, M, RANK, dev, gen, act) for (n, K, N) in PROJECTIONS]
     torch.cuda.synchronize()
 
     for _ in range(args.warmup):
-        run_step(L, projs, _lib.check)
+        run_step(L, projs, _lib.check, sfx)
     torch.cuda.synchronize()
 
     # count one step's launches (an untimed traced step) to size the trace buffer exactly
     _lib.check("reels_hip_trace_start", L.reels_hip_trace_start(4096))
-    run_step(L, projs, _lib.check)
+    run_step(L, projs, _lib.check, sfx)
     torch.cuda.synchronize()
     launches_per_step = len(_lib.trace_records())
     _lib.check("reels_hip_trace_start", L.reels_hip_trace_start(launches_per_step * args.steps))
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        run_step(L, projs, _lib.check)
+        run_step(L, projs, _lib.check, sfx)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     recs = _lib.trace_records()
@@ -336,17 +344,18 @@ def main():
     tot_ms = gemm_ms["fwd"] + gemm_ms["dx"]
     achieved = (gemm_fl["fwd"] + gemm_fl["dx"]) / (tot_ms * 1e-3) / 1e12 if tot_ms > 0 else 0.0
     gemm_names = sorted({n for (n, _) in recs if "gemm_kernel" in n})
-    vendor = vendor_gemm_tflops(dev, M, 5120, 5120)
+    vendor = vendor_gemm_tflops(dev, M, 5120, 5120, dtype=act)
+    deq = "bf16(q*s)" if args.dtype == "bf16" else "f16(q*f16(s))"
     roofline = {
-        "kernel": " + ".join(gemm_names) + " (<0> fwd, <1> dX; bf16 MFMA on the dequantized "
-                                           "weight bf16(q*s))",
+        "kernel": " + ".join(gemm_names) + f" (<0> fwd, <1> dX; {args.dtype} MFMA on the "
+                                           f"dequantized weight {deq})",
         "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
         "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
         "traffic": GEMM_TRAFFIC_BYTES,
         "traffic_note": GEMM_TRAFFIC_NOTE,
         "avg_launch_ms": {k: round(gemm_ms[k] / max(gemm_n[k], 1), 4) for k in gemm_ms},
         "launches": gemm_n,
-        "vendor_bf16_gemm": {"what": f"torch.matmul bf16 (hipBLASLt), {M}x5120 by 5120x5120, "
+        "vendor_bf16_gemm": {"what": f"torch.matmul {args.dtype} (hipBLASLt), {M}x5120 by 5120x5120, "
                                      "sustained ~1.5 s loop, same run", "tflops": round(vendor, 1),
                              "achieved_over_vendor": round(achieved / vendor, 4)},
     }
@@ -367,7 +376,7 @@ def main():
     out = {
         "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": args.dtype,
         "data": "synthetic",
         "config": {"workload": "wan2.1-14b block projections: self_attn q/k/v/o 5120->5120, "
                                "ffn 5120->13824->5120; int8 per-channel frozen weights; LoRA "

@@ -89,12 +89,15 @@ size_t reels_hip_i8lora_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t
 
 /*
  * lora_forward(layer, x), src/layers/lora.jl:56-95, for a LoRALinear whose weight is a
- * QuantizedMatrix, with _weight_mul (quantization.jl:73-74) done without materialising deq(W):
+ * QuantizedMatrix (_weight_mul, quantization.jl:73-74), bf16 activations:
  *   h = bf16(x * A)                                    [M][r]
- *   y = bf16(s[n] * sum_k x[m][k] q[n][k] + lora_scale * sum_j h[m][j] B[j][n] + bias[n])
- * bias may be NULL. r = 0 (A, B NULL) gives the base-only linear(::DenseLayer) of
- * src/layers/linear.jl:38-46. h_save (bf16 [M][r] or NULL) receives h for the backward.
- * workspace: device memory of reels_hip_i8lora_workspace_bytes(M, K, N, r, REELS_HIP_WS_FWD).
+ *   y = bf16(sum_k x[m][k] W[n][k] + lora_scale * sum_j h[m][j] B[j][n] + bias[n])
+ * with W = bf16(fl32(q * s)) written into the workspace once per call when K and N are multiples
+ * of 64 (the reference's _materialize_weight, quantization.jl:54-64), otherwise W = q * s exact
+ * with s[n] applied to the f32 sum. bias may be NULL. r = 0 (A, B NULL) gives the base-only
+ * linear(::DenseLayer) of src/layers/linear.jl:38-46. h_save ([M][r] or NULL) receives h for the
+ * backward. workspace: device memory of reels_hip_i8lora_workspace_bytes(M, K, N, r,
+ * REELS_HIP_WS_FWD).
  */
 int reels_hip_i8lora_fwd(const void* x, const int8_t* q, const float* scales, const void* A,
                          const void* B, const void* bias, int64_t M, int64_t K, int64_t N,
@@ -102,27 +105,51 @@ int reels_hip_i8lora_fwd(const void* x, const int8_t* q, const float* scales, co
                          size_t ws_bytes, void* stream);
 
 /*
+ * The same with binary16 x, A, B, bias, y and h_save: the reference's own int8 compute
+ * precision (Float16, quantization.jl:61-62 and lora.jl:56-95 with T = Float16). Every bf16
+ * rounding above becomes an f16 rounding (nearest even), and the dequantized weight is
+ * W = f16(q * f16(s)) as _dequantize_for_compute computes it. Same workspace size.
+ */
+int reels_hip_i8lora_fwd_f16(const void* x, const int8_t* q, const float* scales, const void* A,
+                             const void* B, const void* bias, int64_t M, int64_t K, int64_t N,
+                             int64_t r, float lora_scale, void* y, void* h_save, void* workspace,
+                             size_t ws_bytes, void* stream);
+
+/*
  * lora_backward(layer, x, dy), src/layers/lora.jl:106-118, with the frozen-weight pullback of
  * src/training/ad_rules.jl:70-80 (_weight_transpose_mul, quantization.jl:75-76):
  *   u  = bf16(dy * B^T)                                                      [M][r]
- *   dx = bf16(sum_n bf16(dy[m][n] s[n]) q[n][k] + lora_scale * sum_j u[m][j] A[k][j])
+ *   dx = bf16(sum_n dy[m][n] W[n][k] + lora_scale * sum_j u[m][j] A[k][j])
  *   dA = lora_scale * x^T u   (f32 [K][r]);   dB = lora_scale * h^T dy   (f32 [r][N])
- * h: the forward's h_save (bf16 [M][r]) or NULL to recompute it. dx, dA, dB may each be NULL to
- * skip that output. r = 0 gives dx = deq(W)^T dy alone (_weight_transpose_mul). dA and dB are
- * overwritten (not accumulated) and are bitwise reproducible run to run.
+ * W as in reels_hip_i8lora_fwd (when K or N is not a multiple of 64, the product is taken as
+ * sum_n bf16(dy[m][n] s[n]) q[n][k]). h: the forward's h_save ([M][r]) or NULL to recompute it.
+ * dx, dA, dB may each be NULL to skip that output. r = 0 gives dx = deq(W)^T dy alone
+ * (_weight_transpose_mul). dA and dB are overwritten (not accumulated) and are bitwise
+ * reproducible run to run.
  */
 int reels_hip_i8lora_bwd(const void* dy, const void* x, const void* h, const int8_t* q,
                          const float* scales, const void* A, const void* B, int64_t M, int64_t K,
                          int64_t N, int64_t r, float lora_scale, void* dx, float* dA, float* dB,
                          void* workspace, size_t ws_bytes, void* stream);
 
+/* The same with binary16 dy, x, h, A, B and dx (dA, dB stay f32); roundings and W as in
+ * reels_hip_i8lora_fwd_f16. */
+int reels_hip_i8lora_bwd_f16(const void* dy, const void* x, const void* h, const int8_t* q,
+                             const float* scales, const void* A, const void* B, int64_t M,
+                             int64_t K, int64_t N, int64_t r, float lora_scale, void* dx, float* dA,
+                             float* dB, void* workspace, size_t ws_bytes, void* stream);
+
 /* gelu_tanh, src/layers/linear.jl:61-68: y = bf16(0.5x(1 + tanh(sqrt(2/pi)(x + 0.044715x^3))))
  * computed in f32 on bf16 x[n]. */
 int reels_hip_gelu_tanh(const void* x, void* y, int64_t n, void* stream);
+/* The same on binary16 x and y. */
+int reels_hip_gelu_tanh_f16(const void* x, void* y, int64_t n, void* stream);
 
 /* Pullback of gelu_tanh (the reference lets Zygote differentiate linear.jl:61-68):
  * dx = bf16(dy * gelu'(x)) with the analytic derivative in f32. */
 int reels_hip_gelu_tanh_bwd(const void* x, const void* dy, void* dx, int64_t n, void* stream);
+/* The same on binary16 x, dy and dx. */
+int reels_hip_gelu_tanh_bwd_f16(const void* x, const void* dy, void* dx, int64_t n, void* stream);
 
 /*
  * Kernel timing instrumentation. No counterpart in the reference (it has no profiler hooks);

@@ -44,12 +44,16 @@ def lib():
         L.oracle_pack.argtypes = [vp, ctypes.c_int, i64, i64, i64, vp, vp]
         L.oracle_pack.restype = ctypes.c_int
         L.oracle_dequant.argtypes = [vp, vp, i64, i64, ctypes.c_int, vp]
+        ci = ctypes.c_int
         L.oracle_lora_forward.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64,
-                                          ctypes.c_float, vp, i64, vp, vp]
+                                          ctypes.c_float, vp, i64, vp, vp, ci]
         L.oracle_lora_backward.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64,
-                                           ctypes.c_float, vp, i64, vp, i64, vp, i64, vp, vp, vp]
-        L.oracle_gelu_tanh.argtypes = [vp, vp, i64]
-        L.oracle_gelu_tanh_backward.argtypes = [vp, vp, vp, i64]
+                                           ctypes.c_float, vp, i64, vp, i64, vp, i64, vp, vp, vp,
+                                           ci]
+        L.oracle_gelu_tanh.argtypes = [vp, vp, i64, ci]
+        L.oracle_gelu_tanh_backward.argtypes = [vp, vp, vp, i64, ci]
+        L.oracle_f16_to_f32_array.argtypes = [vp, vp, i64]
+        L.oracle_f32_to_f16_array.argtypes = [vp, vp, i64]
         L.oracle_philox4x32_10.argtypes = [vp, vp, vp]
         L.oracle_normal_bf16.argtypes = [ctypes.c_uint64, ctypes.c_uint32, i64, ctypes.c_double,
                                          ctypes.c_double, ctypes.c_double, vp]
@@ -138,9 +142,13 @@ def dequant(q, s, mode: str = "f32"):
 
 
 # ---- forward / backward -----------------------------------------------------------------------
-def lora_forward(x, q, s, A, B, c, bias=None, rows=None):
-    """f64 restatement of lora_forward (lora.jl:56-95). x, A, B, bias: bf16 bits (uint16).
-    Returns (y [len(rows)][N] f64, h [len(rows)][r] f64)."""
+_ELT = {"bf16": 0, "f16": 1}
+
+
+def lora_forward(x, q, s, A, B, c, bias=None, rows=None, elt="bf16"):
+    """f64 restatement of lora_forward (lora.jl:56-95). x, A, B, bias: 16-bit patterns (uint16)
+    of bf16 or, with elt="f16", IEEE binary16. Returns (y [len(rows)][N] f64,
+    h [len(rows)][r] f64)."""
     x = _c(x, np.uint16); q = _c(q, np.int8); s = _c(s, np.float32)
     A = _c(A, np.uint16); B = _c(B, np.uint16); bias = _c(bias, np.uint16)
     M, K = x.shape
@@ -153,12 +161,12 @@ def lora_forward(x, q, s, A, B, c, bias=None, rows=None):
     y = np.empty((nrows, N), np.float64)
     h = np.empty((nrows, max(r, 1)), np.float64)
     lib().oracle_lora_forward(_p(x), _p(q), _p(s), _p(A), _p(B), _p(bias), M, K, N, r,
-                              float(c), _p(rws), nrows, _p(y), _p(h))
+                              float(c), _p(rws), nrows, _p(y), _p(h), _ELT[elt])
     return y, h[:, :r]
 
 
 def lora_backward(dy, x, q, s, A, B, c, rows=None, kcols=None, ncols=None,
-                  want=("dx", "dA", "dB")):
+                  want=("dx", "dA", "dB"), elt="bf16"):
     """f64 restatement of lora_backward (lora.jl:106-118). Returns dict of requested grads:
     dx [len(rows)][K], dA [len(kcols)][r], dB [r][len(ncols)]."""
     dy = _c(dy, np.uint16); x = _c(x, np.uint16); q = _c(q, np.int8); s = _c(s, np.float32)
@@ -176,22 +184,37 @@ def lora_backward(dy, x, q, s, A, B, c, rows=None, kcols=None, ncols=None,
     dA = np.empty((nk, r), np.float64) if "dA" in want else None
     dB = np.empty((r, nn), np.float64) if "dB" in want else None
     lib().oracle_lora_backward(_p(dy), _p(x), _p(q), _p(s), _p(A), _p(B), M, K, N, r, float(c),
-                               _p(rws), nrows, _p(kc), nk, _p(nc), nn, _p(dx), _p(dA), _p(dB))
+                               _p(rws), nrows, _p(kc), nk, _p(nc), nn, _p(dx), _p(dA), _p(dB),
+                               _ELT[elt])
     return {"dx": dx, "dA": dA, "dB": dB}
 
 
-def gelu_tanh(x):
+def gelu_tanh(x, elt="bf16"):
     x = _c(x, np.uint16)
     y = np.empty_like(x)
-    lib().oracle_gelu_tanh(_p(x), _p(y), x.size)
+    lib().oracle_gelu_tanh(_p(x), _p(y), x.size, _ELT[elt])
     return y
 
 
-def gelu_tanh_backward(x, dy):
+def gelu_tanh_backward(x, dy, elt="bf16"):
     x = _c(x, np.uint16); dy = _c(dy, np.uint16)
     dx = np.empty_like(x)
-    lib().oracle_gelu_tanh_backward(_p(x), _p(dy), _p(dx), x.size)
+    lib().oracle_gelu_tanh_backward(_p(x), _p(dy), _p(dx), x.size, _ELT[elt])
     return dx
+
+
+def f16_to_f32(h: np.ndarray) -> np.ndarray:
+    h = _c(h, np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().oracle_f16_to_f32_array(_p(h), _p(out), h.size)
+    return out
+
+
+def f32_to_f16(f: np.ndarray) -> np.ndarray:
+    f = _c(f, np.float32)
+    out = np.empty(f.shape, np.uint16)
+    lib().oracle_f32_to_f16_array(_p(f), _p(out), f.size)
+    return out
 
 
 # ---- seeded inputs ----------------------------------------------------------------------------

@@ -77,6 +77,18 @@ static uint16_t f32_to_f16(float f) {
   return sign | (uint16_t)((exp16 << 10) | ((int)scaled - 1024));
 }
 
+void oracle_f16_to_f32_array(const uint16_t* in, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = f16_to_f32(in[i]);
+}
+
+void oracle_f32_to_f16_array(const float* in, uint16_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = f32_to_f16(in[i]);
+}
+
+/* value of a 16-bit element: elt 0 = bf16 bits, 1 = IEEE binary16 bits (both exact in f32) */
+static float in16(uint16_t h, int elt) { return elt ? f16_to_f32(h) : oracle_bf16_to_f32(h); }
+static uint16_t out16(float f, int elt) { return elt ? f32_to_f16(f) : oracle_f32_to_bf16(f); }
+
 /* ---- quantize_frozen_matrix: src/layers/quantization.jl:35-44 --------------------------- */
 static float load_elem(const void* w, int dtype, int64_t idx) {
   if (dtype == 0) return ((const float*)w)[idx];
@@ -144,12 +156,12 @@ void oracle_dequant(const int8_t* q, const float* s, int64_t N, int64_t K, int m
 void oracle_lora_forward(const uint16_t* x, const int8_t* q, const float* s, const uint16_t* A,
                          const uint16_t* B, const uint16_t* bias, int64_t M, int64_t K, int64_t N,
                          int64_t r, float c, const int64_t* rows, int64_t nrows, double* y_out,
-                         double* h_out) {
+                         double* h_out, int elt) {
   if (!rows) nrows = M;
   double* Ad = (double*)malloc(sizeof(double) * (size_t)(K * (r > 0 ? r : 1)));
   double* Bd = (double*)malloc(sizeof(double) * (size_t)((r > 0 ? r : 1) * N));
-  for (int64_t i = 0; i < K * r; ++i) Ad[i] = oracle_bf16_to_f32(A[i]);
-  for (int64_t i = 0; i < r * N; ++i) Bd[i] = oracle_bf16_to_f32(B[i]);
+  for (int64_t i = 0; i < K * r; ++i) Ad[i] = in16(A[i], elt);
+  for (int64_t i = 0; i < r * N; ++i) Bd[i] = in16(B[i], elt);
 #pragma omp parallel
   {
     double* xr = (double*)malloc(sizeof(double) * (size_t)K);
@@ -157,7 +169,7 @@ void oracle_lora_forward(const uint16_t* x, const int8_t* q, const float* s, con
 #pragma omp for schedule(dynamic, 4)
     for (int64_t ii = 0; ii < nrows; ++ii) {
       int64_t m = rows ? rows[ii] : ii;
-      for (int64_t k = 0; k < K; ++k) xr[k] = oracle_bf16_to_f32(x[m * K + k]);
+      for (int64_t k = 0; k < K; ++k) xr[k] = in16(x[m * K + k], elt);
       /* A * z (lora.jl:86) */
       for (int64_t j = 0; j < r; ++j) hr[j] = 0.0;
       for (int64_t k = 0; k < K; ++k)
@@ -172,7 +184,7 @@ void oracle_lora_forward(const uint16_t* x, const int8_t* q, const float* s, con
           for (int64_t k = 0; k < K; ++k) acc += xr[k] * (double)qr[k];
           double y = acc * (double)s[n];
           /* bias: mixed_add(y, bias) (lora.jl:64-67) */
-          if (bias) y += oracle_bf16_to_f32(bias[n]);
+          if (bias) y += in16(bias[n], elt);
           /* adapter = c * B * (A * z) (lora.jl:86-94) */
           double ad = 0.0;
           for (int64_t j = 0; j < r; ++j) ad += hr[j] * Bd[j * N + n];
@@ -192,15 +204,15 @@ void oracle_lora_backward(const uint16_t* dy, const uint16_t* x, const int8_t* q
                           const uint16_t* A, const uint16_t* B, int64_t M, int64_t K, int64_t N,
                           int64_t r, float c, const int64_t* rows, int64_t nrows,
                           const int64_t* kcols, int64_t nk, const int64_t* ncols, int64_t nn,
-                          double* dx_out, double* dA_out, double* dB_out) {
+                          double* dx_out, double* dA_out, double* dB_out, int elt) {
   if (!rows) nrows = M;
   if (!kcols) nk = K;
   if (!ncols) nn = N;
   const int64_t rr = r > 0 ? r : 1;
   double* Ad = (double*)malloc(sizeof(double) * (size_t)(K * rr));
   double* Bd = (double*)malloc(sizeof(double) * (size_t)(rr * N));
-  for (int64_t i = 0; i < K * r; ++i) Ad[i] = oracle_bf16_to_f32(A[i]);
-  for (int64_t i = 0; i < r * N; ++i) Bd[i] = oracle_bf16_to_f32(B[i]);
+  for (int64_t i = 0; i < K * r; ++i) Ad[i] = in16(A[i], elt);
+  for (int64_t i = 0; i < r * N; ++i) Bd[i] = in16(B[i], elt);
   /* u = B' * dy and h = A * x for every token (lora.jl:112-113) */
   double* u = (double*)malloc(sizeof(double) * (size_t)(M * rr));
   double* h = (double*)malloc(sizeof(double) * (size_t)(M * rr));
@@ -208,12 +220,12 @@ void oracle_lora_backward(const uint16_t* dy, const uint16_t* x, const int8_t* q
   for (int64_t m = 0; m < M; ++m) {
     for (int64_t j = 0; j < r; ++j) { u[m * r + j] = 0.0; h[m * r + j] = 0.0; }
     for (int64_t n = 0; n < N; ++n) {
-      double d = oracle_bf16_to_f32(dy[m * N + n]);
+      double d = in16(dy[m * N + n], elt);
       for (int64_t j = 0; j < r; ++j) u[m * r + j] += d * Bd[j * N + n];
     }
     if (dB_out)
       for (int64_t k = 0; k < K; ++k) {
-        double xv = oracle_bf16_to_f32(x[m * K + k]);
+        double xv = in16(x[m * K + k], elt);
         for (int64_t j = 0; j < r; ++j) h[m * r + j] += xv * Ad[k * r + j];
       }
   }
@@ -227,7 +239,7 @@ void oracle_lora_backward(const uint16_t* dy, const uint16_t* x, const int8_t* q
         int64_t m = rows ? rows[ii] : ii;
         for (int64_t k = 0; k < K; ++k) acc[k] = 0.0;
         for (int64_t n = 0; n < N; ++n) {
-          double d = (double)oracle_bf16_to_f32(dy[m * N + n]) * (double)s[n];
+          double d = (double)in16(dy[m * N + n], elt) * (double)s[n];
           const int8_t* qr = q + n * K;
           for (int64_t k = 0; k < K; ++k) acc[k] += d * (double)qr[k];
         }
@@ -248,7 +260,7 @@ void oracle_lora_backward(const uint16_t* dy, const uint16_t* x, const int8_t* q
       double accj[256];
       for (int64_t j = 0; j < r; ++j) accj[j] = 0.0;
       for (int64_t m = 0; m < M; ++m) {
-        double xv = oracle_bf16_to_f32(x[m * K + k]);
+        double xv = in16(x[m * K + k], elt);
         for (int64_t j = 0; j < r; ++j) accj[j] += u[m * r + j] * xv;
       }
       for (int64_t j = 0; j < r; ++j) dA_out[kk * r + j] = (double)c * accj[j];
@@ -262,7 +274,7 @@ void oracle_lora_backward(const uint16_t* dy, const uint16_t* x, const int8_t* q
       double accj[256];
       for (int64_t j = 0; j < r; ++j) accj[j] = 0.0;
       for (int64_t m = 0; m < M; ++m) {
-        double d = oracle_bf16_to_f32(dy[m * N + n]);
+        double d = in16(dy[m * N + n], elt);
         for (int64_t j = 0; j < r; ++j) accj[j] += h[m * r + j] * d;
       }
       for (int64_t j = 0; j < r; ++j) dB_out[j * nn + nn_i] = (double)c * accj[j];
@@ -283,18 +295,19 @@ static float gelu_f32(float x) {
   return 0.5f * x * (1.0f + activated);
 }
 
-void oracle_gelu_tanh(const uint16_t* x, uint16_t* y, int64_t n) {
-  for (int64_t i = 0; i < n; ++i) y[i] = oracle_f32_to_bf16(gelu_f32(oracle_bf16_to_f32(x[i])));
+void oracle_gelu_tanh(const uint16_t* x, uint16_t* y, int64_t n, int elt) {
+  for (int64_t i = 0; i < n; ++i) y[i] = out16(gelu_f32(in16(x[i], elt)), elt);
 }
 
-void oracle_gelu_tanh_backward(const uint16_t* x, const uint16_t* dy, uint16_t* dx, int64_t n) {
+void oracle_gelu_tanh_backward(const uint16_t* x, const uint16_t* dy, uint16_t* dx, int64_t n,
+                               int elt) {
   /* d/dx 0.5x(1+tanh(k(x+a x^3))) = 0.5(1+t) + 0.5x(1-t^2)k(1+3a x^2) */
   const double k = sqrt(2.0 / 3.14159265358979323846), a = 0.044715;
   for (int64_t i = 0; i < n; ++i) {
-    double xv = oracle_bf16_to_f32(x[i]);
+    double xv = in16(x[i], elt);
     double t = tanh(k * (xv + a * xv * xv * xv));
     double d = 0.5 * (1.0 + t) + 0.5 * xv * (1.0 - t * t) * k * (1.0 + 3.0 * a * xv * xv);
-    dx[i] = oracle_f32_to_bf16((float)(d * (double)oracle_bf16_to_f32(dy[i])));
+    dx[i] = out16((float)(d * (double)in16(dy[i], elt)), elt);
   }
 }
 

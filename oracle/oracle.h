@@ -45,8 +45,16 @@ int oracle_pack(const void* w, int dtype, int64_t N, int64_t K, int64_t ld, int8
  * mode 2: bf16_rne(Float32(q)*s) (u16 bits out). Pinned by closed forms per element. */
 void oracle_dequant(const int8_t* q, const float* s, int64_t N, int64_t K, int mode, void* out);
 
+/* 16-bit element codes of the forward / backward / gelu inputs: 0 = bf16 bits, 1 = IEEE binary16
+ * bits (the reference's Float16 compute). Both decode exactly to f32. The f16 conversions are
+ * exported for tests: f16 -> f32 exact, f32 -> f16 round to nearest even (with subnormals).
+ * Pinned by: every one of the 65536 binary16 patterns against numpy's float16, and numpy's
+ * float16 rounding on random and boundary f32 values. */
+void oracle_f16_to_f32_array(const uint16_t* in, float* out, int64_t n);
+void oracle_f32_to_f16_array(const float* in, uint16_t* out, int64_t n);
+
 /* lora_forward, src/layers/lora.jl:56-95 with _weight_mul (quantization.jl:73-74), computed in
- * f64 from bf16 inputs (the exact value of the math): for each listed row m,
+ * f64 from 16-bit inputs (the exact value of the math): for each listed row m,
  *   y[m][n] = sum_k x[m][k]*q[n][k]*s[n] + c*sum_j h[m][j]*B[j][n] + bias[n],
  *   h[m][j] = sum_k x[m][k]*A[k][j].
  * rows: row indices to compute (NULL = all M; nrows then ignored). Output rows are packed in
@@ -56,7 +64,7 @@ void oracle_dequant(const int8_t* q, const float* s, int64_t N, int64_t K, int m
 void oracle_lora_forward(const uint16_t* x, const int8_t* q, const float* s, const uint16_t* A,
                          const uint16_t* B, const uint16_t* bias, int64_t M, int64_t K, int64_t N,
                          int64_t r, float c, const int64_t* rows, int64_t nrows, double* y_out,
-                         double* h_out);
+                         double* h_out, int elt);
 
 /* lora_backward, src/layers/lora.jl:106-118 (and the frozen-weight rrule of
  * src/training/ad_rules.jl:70-80), in f64:
@@ -71,14 +79,15 @@ void oracle_lora_backward(const uint16_t* dy, const uint16_t* x, const int8_t* q
                           const uint16_t* A, const uint16_t* B, int64_t M, int64_t K, int64_t N,
                           int64_t r, float c, const int64_t* rows, int64_t nrows,
                           const int64_t* kcols, int64_t nk, const int64_t* ncols, int64_t nn,
-                          double* dx_out, double* dA_out, double* dB_out);
+                          double* dx_out, double* dA_out, double* dB_out, int elt);
 
-/* gelu_tanh, src/layers/linear.jl:61-68, in f32 on bf16 inputs, result rounded to bf16, and its
- * analytic derivative applied to an upstream gradient (dx = bf16(dy * gelu'(x))).
+/* gelu_tanh, src/layers/linear.jl:61-68, in f32 on 16-bit inputs, result rounded to the input
+ * type, and its analytic derivative applied to an upstream gradient (dx = rnd(dy * gelu'(x))).
  * Pinned by: closed-form values (gelu(0)=0, odd-part identity gelu(x)-gelu(-x)=x), central
  * finite differences for the derivative. */
-void oracle_gelu_tanh(const uint16_t* x, uint16_t* y, int64_t n);
-void oracle_gelu_tanh_backward(const uint16_t* x, const uint16_t* dy, uint16_t* dx, int64_t n);
+void oracle_gelu_tanh(const uint16_t* x, uint16_t* y, int64_t n, int elt);
+void oracle_gelu_tanh_backward(const uint16_t* x, const uint16_t* dy, uint16_t* dx, int64_t n,
+                               int elt);
 
 /* Philox4x32-10 (Salmon et al., SC'11) counter-based generator for seeded test inputs.
  * Pinned by the published Random123 known-answer vectors. */

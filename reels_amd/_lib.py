@@ -25,9 +25,13 @@ EXPORTS = (
     "reels_hip_i8_dequant",
     "reels_hip_i8lora_workspace_bytes",
     "reels_hip_i8lora_fwd",
+    "reels_hip_i8lora_fwd_f16",
     "reels_hip_i8lora_bwd",
+    "reels_hip_i8lora_bwd_f16",
     "reels_hip_gelu_tanh",
+    "reels_hip_gelu_tanh_f16",
     "reels_hip_gelu_tanh_bwd",
+    "reels_hip_gelu_tanh_bwd_f16",
     "reels_hip_trace_start",
     "reels_hip_trace_stop",
     "reels_hip_trace_get",
@@ -71,16 +75,18 @@ def lib():
     L.reels_hip_i8_dequant.restype = ctypes.c_int
     L.reels_hip_i8lora_workspace_bytes.argtypes = [i64, i64, i64, i64, ctypes.c_int]
     L.reels_hip_i8lora_workspace_bytes.restype = sz
-    L.reels_hip_i8lora_fwd.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, ctypes.c_float,
-                                       vp, vp, vp, sz, vp]
-    L.reels_hip_i8lora_fwd.restype = ctypes.c_int
-    L.reels_hip_i8lora_bwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64,
-                                       ctypes.c_float, vp, vp, vp, vp, sz, vp]
-    L.reels_hip_i8lora_bwd.restype = ctypes.c_int
-    L.reels_hip_gelu_tanh.argtypes = [vp, vp, i64, vp]
-    L.reels_hip_gelu_tanh.restype = ctypes.c_int
-    L.reels_hip_gelu_tanh_bwd.argtypes = [vp, vp, vp, i64, vp]
-    L.reels_hip_gelu_tanh_bwd.restype = ctypes.c_int
+    for sfx in ("", "_f16"):
+        fwd, bwd = getattr(L, "reels_hip_i8lora_fwd" + sfx), getattr(L, "reels_hip_i8lora_bwd" + sfx)
+        fwd.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, ctypes.c_float, vp, vp, vp, sz, vp]
+        fwd.restype = ctypes.c_int
+        bwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, ctypes.c_float, vp, vp, vp,
+                        vp, sz, vp]
+        bwd.restype = ctypes.c_int
+        g, gb = getattr(L, "reels_hip_gelu_tanh" + sfx), getattr(L, "reels_hip_gelu_tanh_bwd" + sfx)
+        g.argtypes = [vp, vp, i64, vp]
+        g.restype = ctypes.c_int
+        gb.argtypes = [vp, vp, vp, i64, vp]
+        gb.restype = ctypes.c_int
     L.reels_hip_trace_start.argtypes = [ctypes.c_int]
     L.reels_hip_trace_start.restype = ctypes.c_int
     L.reels_hip_trace_stop.restype = ctypes.c_int

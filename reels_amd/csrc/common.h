@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <string>
+#include <type_traits>
 
 #include "../../include/reels_hip.h"
 
@@ -55,6 +56,76 @@ __device__ __forceinline__ bf16x8 i8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// ---- 16-bit element types of the LoRA linear --------------------------------------------------
+// Elt<REELS_HIP_BF16> and Elt<REELS_HIP_F16> give each kernel its element arithmetic: unpack to
+// f32 (exact), round f32 to the element (nearest even), the MFMA shapes, the exact int8
+// conversion and the dequantized-weight element of the compute type.
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
+
+template <int ELT> struct Elt;
+
+template <> struct Elt<REELS_HIP_BF16> {
+  typedef bf16x8 v8;
+  static __device__ __forceinline__ float to_f32(uint16_t h) { return bf16_to_f32(h); }
+  static __device__ __forceinline__ float lo(uint32_t w) { return bf16_lo(w); }
+  static __device__ __forceinline__ float hi(uint32_t w) { return bf16_hi(w); }
+  static __device__ __forceinline__ uint32_t bits(float f) { return f32_to_bf16_bits(f); }
+  static __device__ __forceinline__ uint32_t pack2(float a, float b) { return pack_bf16x2(a, b); }
+  static __device__ __forceinline__ v8 as8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+  static __device__ __forceinline__ v8 from_i8x8(uint32_t l, uint32_t h) { return i8x8_to_bf16x8(l, h); }
+  static __device__ __forceinline__ f32x4 mfma16(v8 a, v8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x16 mfma32(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  // dequantized weight for bf16 compute: bf16(fl32(q s)) (_host_dequantize with T = BFloat16,
+  // src/layers/quantization.jl:25-29)
+  static __device__ __forceinline__ uint32_t deq(float q, float s) { return f32_to_bf16_bits(q * s); }
+};
+
+template <> struct Elt<REELS_HIP_F16> {
+  typedef f16x8 v8;
+  static __device__ __forceinline__ float to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+  static __device__ __forceinline__ float lo(uint32_t w) { return to_f32((uint16_t)(w & 0xffffu)); }
+  static __device__ __forceinline__ float hi(uint32_t w) { return to_f32((uint16_t)(w >> 16)); }
+  static __device__ __forceinline__ uint32_t bits(float f) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
+  }
+  static __device__ __forceinline__ uint32_t pack2(float a, float b) { return bits(a) | (bits(b) << 16); }
+  static __device__ __forceinline__ v8 as8(u32x4 v) { return __builtin_bit_cast(f16x8, v); }
+  // int8 -> binary16 is exact (|q| <= 127 fits the 11-bit significand)
+  static __device__ __forceinline__ v8 from_i8x8(uint32_t l, uint32_t h) {
+    v8 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      r[i] = (_Float16)(float)(int8_t)((l >> (8 * i)) & 0xffu);
+      r[4 + i] = (_Float16)(float)(int8_t)((h >> (8 * i)) & 0xffu);
+    }
+    return r;
+  }
+  static __device__ __forceinline__ f32x4 mfma16(v8 a, v8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x16 mfma32(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  // dequantized weight for fp16 compute: Float16(q) * Float16(s) (_dequantize_for_compute,
+  // quantization.jl:61-62), one binary16 multiply (equal to rounding the exact f32 product
+  // once). Written as an f32 product rounded to f16, hipcc folds it into v_fma_mixlo_f16 with a
+  // +0 addend, which turns a -0 product (q < 0, f16(s) == 0) into +0.
+  static __device__ __forceinline__ uint32_t deq(float q, float s) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)((_Float16)q * (_Float16)s));
+  }
+};
+
+// calls f(std::integral_constant<int, ELT>) for the run-time element code (bf16 or f16)
+template <typename F>
+inline void with_elt(int elt, F&& f) {
+  if (elt == REELS_HIP_F16) f(std::integral_constant<int, REELS_HIP_F16>{});
+  else f(std::integral_constant<int, REELS_HIP_BF16>{});
+}
 
 // ---- host-side error state -----------------------------------------------------------------
 void set_error(const std::string& msg);

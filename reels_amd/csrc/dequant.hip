@@ -4,14 +4,16 @@
 //   f16:  f16(q * f16(s))         Float16.(values) .* Float16.(scales) (the product of two
 //                                 binary16 values is exact in f32, then one rounding)
 //   bf16: bf16(fl32(q * s))       the weight the bf16 GEMMs of the LoRA linear multiply
-// The bf16 forms used inside the LoRA linear have streaming kernels (16 codes per thread; 64 x 64
-// LDS tiles for the transpose); every other case runs one element per thread.
+// The bf16 and f16 forms (the weights the LoRA linear's GEMMs multiply) have streaming kernels
+// (16 codes per thread; 64 x 64 LDS tiles for the transpose); every other case runs one element
+// per thread.
 #include <algorithm>
 
 #include "i8gemm.h"
 
 namespace reels {
 
+template <int ELT>
 __global__ __launch_bounds__(256) void dequant_rows_kernel(const int8_t* __restrict__ q, int64_t ldq,
                                                            const float* __restrict__ s, int64_t N,
                                                            int64_t K, uint16_t* __restrict__ wd) {
@@ -25,10 +27,10 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(const int8_t* __restr
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
     const uint32_t x = v[d];
-    const float f0 = (float)(int8_t)(x & 0xff) * sc, f1 = (float)(int8_t)((x >> 8) & 0xff) * sc;
-    const float f2 = (float)(int8_t)((x >> 16) & 0xff) * sc, f3 = (float)((int32_t)x >> 24) * sc;
-    o[d >> 1][(d & 1) * 2] = pack_bf16x2(f0, f1);
-    o[d >> 1][(d & 1) * 2 + 1] = pack_bf16x2(f2, f3);
+    const float q0 = (float)(int8_t)(x & 0xff), q1 = (float)(int8_t)((x >> 8) & 0xff);
+    const float q2 = (float)(int8_t)((x >> 16) & 0xff), q3 = (float)((int32_t)x >> 24);
+    o[d >> 1][(d & 1) * 2] = Elt<ELT>::deq(q0, sc) | (Elt<ELT>::deq(q1, sc) << 16);
+    o[d >> 1][(d & 1) * 2 + 1] = Elt<ELT>::deq(q2, sc) | (Elt<ELT>::deq(q3, sc) << 16);
   }
   u32x4* dst = reinterpret_cast<u32x4*>(wd + n * K + c * 16);
   dst[0] = o[0];
@@ -37,6 +39,7 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(const int8_t* __restr
 
 // 64 x 64 tiles through LDS: a thread reads 16 codes of one row n and writes them as bf16 into
 // column n of the [k][n] tile; it then stores 16 consecutive n of one row k (two 16-byte stores).
+template <int ELT>
 __global__ __launch_bounds__(256) void dequant_transpose_kernel(const int8_t* __restrict__ q,
                                                                 int64_t ldq,
                                                                 const float* __restrict__ s,
@@ -51,8 +54,7 @@ __global__ __launch_bounds__(256) void dequant_transpose_kernel(const int8_t* __
     const float sc = s[n0 + nl];
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      const float f = (float)(int8_t)((v[j >> 2] >> (8 * (j & 3))) & 0xff) * sc;
-      tile[kl + j][nl] = (uint16_t)f32_to_bf16_bits(f);
+      tile[kl + j][nl] = (uint16_t)Elt<ELT>::deq((float)(int8_t)((v[j >> 2] >> (8 * (j & 3))) & 0xff), sc);
     }
   }
   __syncthreads();
@@ -75,26 +77,27 @@ __global__ __launch_bounds__(256) void dequant_generic_kernel(const int8_t* __re
     if (TRANS) { k = i / N; n = i - k * N; } else { n = i / K; k = i - n * K; }
     const float qv = (float)q[n * ldq + k];
     if (DT == REELS_HIP_F32) static_cast<float*>(out)[i] = qv * s[n];
-    // f16: one correctly rounded binary16 multiply equals f16(fl32(q * f16(s))) (the f32 product
-    // is exact). Written in f32 the compiler folds it into v_fma_mixlo_f16 with a +0 addend,
-    // which turns a -0 product (q < 0, f16(s) == 0) into +0.
-    else if (DT == REELS_HIP_F16) static_cast<_Float16*>(out)[i] = (_Float16)qv * (_Float16)s[n];
-    else static_cast<uint16_t*>(out)[i] = (uint16_t)f32_to_bf16_bits(qv * s[n]);
+    else if (DT == REELS_HIP_F16) static_cast<uint16_t*>(out)[i] = (uint16_t)Elt<REELS_HIP_F16>::deq(qv, s[n]);
+    else static_cast<uint16_t*>(out)[i] = (uint16_t)Elt<REELS_HIP_BF16>::deq(qv, s[n]);
   }
 }
 
-int launch_dequant_rows(const int8_t* q, int64_t ldq, const float* s, int64_t N, int64_t K,
+int launch_dequant_rows(int elt, const int8_t* q, int64_t ldq, const float* s, int64_t N, int64_t K,
                         uint16_t* wd, hipStream_t st) {
   const int64_t n = N * (K >> 4);
   { TraceScope _ts(st, "dequant_rows_kernel");
-    dequant_rows_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, st>>>(q, ldq, s, N, K, wd); }
+    with_elt(elt, [&](auto e) {
+      dequant_rows_kernel<decltype(e)::value><<<(unsigned)ceil_div(n, 256), 256, 0, st>>>(q, ldq, s, N, K, wd);
+    }); }
   return check_launch("dequant_rows_kernel");
 }
 
-int launch_dequant_transpose(const int8_t* q, int64_t ldq, const float* s, int64_t N, int64_t K,
-                             uint16_t* wt, hipStream_t st) {
+int launch_dequant_transpose(int elt, const int8_t* q, int64_t ldq, const float* s, int64_t N,
+                             int64_t K, uint16_t* wt, hipStream_t st) {
   { TraceScope _ts(st, "dequant_transpose_kernel");
-    dequant_transpose_kernel<<<dim3((unsigned)(K / 64), (unsigned)(N / 64)), 256, 0, st>>>(q, ldq, s, N, K, wt); }
+    with_elt(elt, [&](auto e) {
+      dequant_transpose_kernel<decltype(e)::value><<<dim3((unsigned)(K / 64), (unsigned)(N / 64)), 256, 0, st>>>(q, ldq, s, N, K, wt);
+    }); }
   return check_launch("dequant_transpose_kernel");
 }
 
@@ -118,10 +121,11 @@ extern "C" int reels_hip_i8_dequant(const int8_t* q, const float* scales, int64_
     return fail(REELS_HIP_EINVAL, "reels_hip_i8_dequant: NULL q, scales or out");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const bool al = aligned16(q) && aligned16(out) && ld_q % 16 == 0;
-  if (dtype == REELS_HIP_BF16 && !transpose && al && K % 16 == 0)
-    return launch_dequant_rows(q, ld_q, scales, N, K, static_cast<uint16_t*>(out), st);
-  if (dtype == REELS_HIP_BF16 && transpose && al && N % 64 == 0 && K % 64 == 0)
-    return launch_dequant_transpose(q, ld_q, scales, N, K, static_cast<uint16_t*>(out), st);
+  const bool half = dtype == REELS_HIP_BF16 || dtype == REELS_HIP_F16;
+  if (half && !transpose && al && K % 16 == 0)
+    return launch_dequant_rows(dtype, q, ld_q, scales, N, K, static_cast<uint16_t*>(out), st);
+  if (half && transpose && al && N % 64 == 0 && K % 64 == 0)
+    return launch_dequant_transpose(dtype, q, ld_q, scales, N, K, static_cast<uint16_t*>(out), st);
   const unsigned grid = (unsigned)std::min<int64_t>(ceil_div(N * K, 256), 1 << 16);  // grid-stride
   { TraceScope _ts(st, "dequant_generic_kernel");
     if (dtype == REELS_HIP_F32) {

@@ -17,21 +17,24 @@ struct GemmArgs {
   float c;                 // LoRA scale alpha / r
 };
 
-// mode 0 = FWD (out = s * act q^T + c L R^T + bias), 1 = DX (out = act q + c L R^T)
-int launch_i8gemm(int mode, const GemmArgs& a, hipStream_t st);
+// mode 0 = FWD (out = s * act q^T + c L R^T + bias), 1 = DX (out = act q + c L R^T); elt is the
+// 16-bit element type of act, L, R, bias and out (REELS_HIP_BF16 or REELS_HIP_F16)
+int launch_i8gemm(int mode, int elt, const GemmArgs& a, hipStream_t st);
 
-// bf16 x bf16 GEMM with the LoRA epilogue: out = bf16(act wd^T + c L R^T + bias), wd [Ncols][Kred]
-// bf16 (a dequantized weight); a.q and a.colscale are unused. Needs Kred % 64 == 0, 16-byte
-// aligned operands and byte sizes below 2^31 (bfgemm_supported).
+// 16-bit GEMM with the LoRA epilogue: out = rnd(act wd^T + c L R^T + bias), wd [Ncols][Kred] (a
+// dequantized weight) of element type elt like every other operand; a.q and a.colscale are
+// unused. Needs Kred % 64 == 0, 16-byte aligned operands and byte sizes below 2^31
+// (bfgemm_supported).
 bool bfgemm_supported(int64_t M, int64_t Ncols, int64_t Kred);
 // mode only labels the trace record ("bfgemm_kernel<0>" forward, "<1>" dX)
-int launch_bfgemm(int mode, const GemmArgs& a, const uint16_t* wd, hipStream_t st);
+int launch_bfgemm(int mode, int elt, const GemmArgs& a, const uint16_t* wd, hipStream_t st);
 
-// wd[n][k] = bf16(fl32(q[n][k] * s[n])), q [N][K] row stride ldq (K % 16 == 0)
-int launch_dequant_rows(const int8_t* q, int64_t ldq, const float* s, int64_t N, int64_t K,
+// wd[n][k] = deq(q[n][k], s[n]) in element type elt (bf16: bf16(fl32(q s)); f16: f16(q f16(s))),
+// q [N][K] row stride ldq (K % 16 == 0)
+int launch_dequant_rows(int elt, const int8_t* q, int64_t ldq, const float* s, int64_t N, int64_t K,
                         uint16_t* wd, hipStream_t st);
-// wt[k][n] = bf16(fl32(q[n][k] * s[n])) (N % 64 == 0, K % 64 == 0)
-int launch_dequant_transpose(const int8_t* q, int64_t ldq, const float* s, int64_t N, int64_t K,
-                             uint16_t* wt, hipStream_t st);
+// wt[k][n] = deq(q[n][k], s[n]) (N % 64 == 0, K % 64 == 0)
+int launch_dequant_transpose(int elt, const int8_t* q, int64_t ldq, const float* s, int64_t N,
+                             int64_t K, uint16_t* wt, hipStream_t st);
 
 }  // namespace reels

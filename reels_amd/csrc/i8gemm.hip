@@ -55,9 +55,11 @@ __device__ __forceinline__ int wd_swz(int row) { return (row & 7) | ((row & 1) <
 // ds_read_b128 in this pattern (SQ_LDS_BANK_CONFLICT).
 __device__ __forceinline__ int bf_swz(int row) { return row & 7; }
 
-template <int MODE>  // 0 = FWD, 1 = DX
+template <int MODE, int ELT>  // MODE 0 = FWD, 1 = DX; ELT the 16-bit element type
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void i8gemm_kernel(GemmArgs a) {
+  using E = Elt<ELT>;
+  typedef typename E::v8 V8;
   using namespace gemm;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int t = threadIdx.x;
@@ -144,12 +146,12 @@ void i8gemm_kernel(GemmArgs a) {
     const uint8_t* sw = sa + ACT_BYTES;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      bf16x8 bfr[4], afr[4];
+      V8 bfr[4], afr[4];
 #pragma unroll
       for (int tj = 0; tj < 4; ++tj) {
         const int row = wm * 128 + tj * 32 + l32;
         const int c = kk * 2 + lhi;
-        bfr[tj] = as_bf16x8(*reinterpret_cast<const u32x4*>(sa + row * 128 + ((c ^ act_swz(row)) << 4)));
+        bfr[tj] = E::as8(*reinterpret_cast<const u32x4*>(sa + row * 128 + ((c ^ act_swz(row)) << 4)));
       }
 #pragma unroll
       for (int ti = 0; ti < 4; ++ti) {
@@ -167,13 +169,13 @@ void i8gemm_kernel(GemmArgs a) {
           i32x2 v = __builtin_amdgcn_ds_read_tr8_b64_v2i32(LDS_PTR(i32x2, p));
           raw = u32x2{(uint32_t)v[0], (uint32_t)v[1]};
         }
-        afr[ti] = i8x8_to_bf16x8(raw[0], raw[1]);
+        afr[ti] = E::from_i8x8(raw[0], raw[1]);
       }
 #pragma unroll
       for (int ti = 0; ti < 4; ++ti)
 #pragma unroll
         for (int tj = 0; tj < 4; ++tj)
-          acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(afr[ti], bfr[tj], acc[ti][tj], 0, 0, 0);
+          acc[ti][tj] = E::mfma32(afr[ti], bfr[tj], acc[ti][tj]);
     }
   };
 
@@ -207,8 +209,8 @@ void i8gemm_kernel(GemmArgs a) {
       if (a.bias != nullptr && ok) b2 = *reinterpret_cast<const u32x2*>(a.bias + n);
 #pragma unroll
       for (int e = 0; e < 4; ++e) sc[g4 * 4 + e] = s4[e];
-      bs[g4 * 4 + 0] = bf16_lo(b2[0]); bs[g4 * 4 + 1] = bf16_hi(b2[0]);
-      bs[g4 * 4 + 2] = bf16_lo(b2[1]); bs[g4 * 4 + 3] = bf16_hi(b2[1]);
+      bs[g4 * 4 + 0] = E::lo(b2[0]); bs[g4 * 4 + 1] = E::hi(b2[0]);
+      bs[g4 * 4 + 2] = E::lo(b2[1]); bs[g4 * 4 + 3] = E::hi(b2[1]);
     }
 #pragma unroll
     for (int tj = 0; tj < 4; ++tj) {
@@ -222,7 +224,7 @@ void i8gemm_kernel(GemmArgs a) {
         u32x4 lv = *reinterpret_cast<const u32x4*>(a.L + mc * a.rp + s * 16 + lhi * 8);
         if (nrow >= Ncols) rv = u32x4{0, 0, 0, 0};
         if (m >= M) lv = u32x4{0, 0, 0, 0};
-        lo = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(rv), as_bf16x8(lv), lo, 0, 0, 0);
+        lo = E::mfma32(E::as8(rv), E::as8(lv), lo);
       }
       if (m < M) {
 #pragma unroll
@@ -235,7 +237,7 @@ void i8gemm_kernel(GemmArgs a) {
               const int v = g4 * 4 + e;
               o[e] = sc[v] * acc[ti][tj][v] + a.c * lo[v] + bs[v];
             }
-            u32x2 pk = {pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+            u32x2 pk = {E::pack2(o[0], o[1]), E::pack2(o[2], o[3])};
             *reinterpret_cast<u32x2*>(a.out + m * Ncols + n) = pk;
           }
         }
@@ -302,9 +304,11 @@ constexpr int NSTAGE = 3;
 constexpr int GM = 4;
 }  // namespace gemm3
 
-template <int MODE>
+template <int MODE, int ELT>
 __global__ __launch_bounds__(512)
 void i8gemm_v3_kernel(GemmArgs a, int tiles_n, int tiles_m) {
+  using E = Elt<ELT>;
+  typedef typename E::v8 V8;
   using namespace gemm3;
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   const int t = threadIdx.x;
@@ -380,12 +384,12 @@ void i8gemm_v3_kernel(GemmArgs a, int tiles_n, int tiles_m) {
   // latency of the next step's first reads. Stage j+2 is issued right after the barrier of step
   // j, into the buffer of step j-1, which every wave has finished reading by then.
   auto xchunk = [&](int s) { return MODE == 0 ? 4 * (s >> 1) + 2 * lhi + (s & 1) : 2 * s + lhi; };
-  auto read_x = [&](const uint8_t* sa, int s, bf16x8* xf) {
+  auto read_x = [&](const uint8_t* sa, int s, V8* xf) {
     const int c = xchunk(s);
 #pragma unroll
     for (int tj = 0; tj < 4; ++tj) {
       const int row = wm * 128 + tj * 32 + l32;
-      xf[tj] = as_bf16x8(*reinterpret_cast<const u32x4*>(sa + row * 128 + ((c ^ act_swz(row)) << 4)));
+      xf[tj] = E::as8(*reinterpret_cast<const u32x4*>(sa + row * 128 + ((c ^ act_swz(row)) << 4)));
     }
   };
   u32x4 wr[2][2];   // FWD: raw int8 weight slots [pair][ti]
@@ -413,26 +417,26 @@ void i8gemm_v3_kernel(GemmArgs a, int tiles_n, int tiles_m) {
         }
     }
   };
-  auto convert = [&](int s, bf16x8* af) {
+  auto convert = [&](int s, V8* af) {
 #pragma unroll
     for (int ti = 0; ti < 2; ++ti) {
       if (MODE == 0) {
         const u32x4& r = wr[s >> 1][ti];
-        af[ti] = (s & 1) ? i8x8_to_bf16x8(r[2], r[3]) : i8x8_to_bf16x8(r[0], r[1]);
+        af[ti] = (s & 1) ? E::from_i8x8(r[2], r[3]) : E::from_i8x8(r[0], r[1]);
       } else {
-        af[ti] = i8x8_to_bf16x8((uint32_t)wt[s][ti][0], (uint32_t)wt[s][ti][1]);
+        af[ti] = E::from_i8x8((uint32_t)wt[s][ti][0], (uint32_t)wt[s][ti][1]);
       }
     }
   };
-  auto mfma8 = [&](const bf16x8* af, const bf16x8* xf) {
+  auto mfma8 = [&](const V8* af, const V8* xf) {
 #pragma unroll
     for (int tj = 0; tj < 4; ++tj)
 #pragma unroll
       for (int ti = 0; ti < 2; ++ti)
-        acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ti], xf[tj], acc[ti][tj], 0, 0, 0);
+        acc[ti][tj] = E::mfma32(af[ti], xf[tj], acc[ti][tj]);
   };
 
-  bf16x8 xa[4], xb[4], af[2];
+  V8 xa[4], xb[4], af[2];
   issue(0, 0);
   if (nk > 1) issue(1, 1);
   if (nk > 1) __builtin_amdgcn_s_waitcnt(0x0F76);  // vmcnt(6): stage 1 may stay in flight
@@ -487,8 +491,8 @@ void i8gemm_v3_kernel(GemmArgs a, int tiles_n, int tiles_m) {
       if (a.bias != nullptr && ok) b2 = *reinterpret_cast<const u32x2*>(a.bias + n);
 #pragma unroll
       for (int e = 0; e < 4; ++e) sc[g4 * 4 + e] = s4[e];
-      bs[g4 * 4 + 0] = bf16_lo(b2[0]); bs[g4 * 4 + 1] = bf16_hi(b2[0]);
-      bs[g4 * 4 + 2] = bf16_lo(b2[1]); bs[g4 * 4 + 3] = bf16_hi(b2[1]);
+      bs[g4 * 4 + 0] = E::lo(b2[0]); bs[g4 * 4 + 1] = E::hi(b2[0]);
+      bs[g4 * 4 + 2] = E::lo(b2[1]); bs[g4 * 4 + 3] = E::hi(b2[1]);
     }
 #pragma unroll
     for (int tj = 0; tj < 4; ++tj) {
@@ -503,7 +507,7 @@ void i8gemm_v3_kernel(GemmArgs a, int tiles_n, int tiles_m) {
         u32x4 lv = *reinterpret_cast<const u32x4*>(a.L + mc * a.rp + s * 16 + lhi * 8);
         if (nrow >= Ncols) rv = u32x4{0, 0, 0, 0};
         if (m >= M) lv = u32x4{0, 0, 0, 0};
-        lo = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(rv), as_bf16x8(lv), lo, 0, 0, 0);
+        lo = E::mfma32(E::as8(rv), E::as8(lv), lo);
       }
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
@@ -513,7 +517,7 @@ void i8gemm_v3_kernel(GemmArgs a, int tiles_n, int tiles_m) {
           const int v = g4 * 4 + e;
           o[e] = sc[v] * acc[ti][tj][v] + a.c * lo[v] + bs[v];
         }
-        const u32x2 pk = {pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+        const u32x2 pk = {E::pack2(o[0], o[1]), E::pack2(o[2], o[3])};
         const int col = nloc + g4 * 8;                       // 4 columns, 8 bytes
         const int chunk = (col >> 3) ^ (mloc & 31);          // 16-byte chunk, swizzled
         *reinterpret_cast<u32x2*>(stile + mloc * 512 + chunk * 16 + (col & 7) * 2) = pk;
@@ -565,8 +569,11 @@ constexpr int GM = 4;
 // (this GEMM: +3.5% over the same kernel on 32 x 32 tiles). Lane l supplies row l % 16 of both
 // operands with k = 8 (l / 16) + (0..7) (any k order shared by the two operands gives the same
 // sum); D register v of lane l is output column 4 (l / 16) + v, token l % 16 of the tile.
+template <int ELT>
 __global__ __launch_bounds__(512)
 void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int tiles_m) {
+  using E = Elt<ELT>;
+  typedef typename E::v8 V8;
   using namespace bfg;
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   const int t = threadIdx.x, lane = t & 63;
@@ -628,23 +635,23 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
   // fragment reads: sub-step s of a step uses the 16-byte chunk 4 s + l / 16 of each row; rows of
   // a 16-row tile start at multiples of 16, so the row swizzle depends on the lane only
   const int swz = bf_swz(l16);
-  auto read_w = [&](const uint8_t* sw, int s, bf16x8* wf) {
+  auto read_w = [&](const uint8_t* sw, int s, V8* wf) {
     const int off = ((4 * s + lq) ^ swz) << 4;
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti)
-      wf[ti] = as_bf16x8(*reinterpret_cast<const u32x4*>(sw + (wn * 64 + ti * 16 + l16) * 128 + off));
+      wf[ti] = E::as8(*reinterpret_cast<const u32x4*>(sw + (wn * 64 + ti * 16 + l16) * 128 + off));
   };
   auto read_x = [&](const uint8_t* sa, int s, int tj) {
     const int off = ((4 * s + lq) ^ swz) << 4;
-    return as_bf16x8(*reinterpret_cast<const u32x4*>(sa + (wm * 128 + tj * 16 + l16) * 128 + off));
+    return E::as8(*reinterpret_cast<const u32x4*>(sa + (wm * 128 + tj * 16 + l16) * 128 + off));
   };
-  auto mfma4 = [&](const bf16x8* wf, const bf16x8& xf, int tj) {
+  auto mfma4 = [&](const V8* wf, const V8& xf, int tj) {
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti)
-      acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[ti], xf, acc[ti][tj], 0, 0, 0);
+      acc[ti][tj] = E::mfma16(wf[ti], xf, acc[ti][tj]);
   };
 
-  bf16x8 w0[4], w1[4], x[8];
+  V8 w0[4], w1[4], x[8];
   // sub-step 0 of a stage (w0, x) while sub-step 1's fragments of the same stage are read: each
   // token fragment is re-read as soon as its four MFMAs are issued
   // (the sub-step-1 weight fragments are read after the first group, so that the wait before
@@ -722,7 +729,7 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
     float bs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (a.bias != nullptr && nb < Ncols) {
       const u32x2 b2 = *reinterpret_cast<const u32x2*>(a.bias + nb);
-      bs[0] = bf16_lo(b2[0]); bs[1] = bf16_hi(b2[0]); bs[2] = bf16_lo(b2[1]); bs[3] = bf16_hi(b2[1]);
+      bs[0] = E::lo(b2[0]); bs[1] = E::hi(b2[0]); bs[2] = E::lo(b2[1]); bs[3] = E::hi(b2[1]);
     }
     f32x4 lor[8];
 #pragma unroll
@@ -738,7 +745,7 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
         const int64_t m = m0 + wm * 128 + tj * 16 + l16;
         u32x4 lv = {0, 0, 0, 0};
         if (k0 < a.rp && m < M) lv = *reinterpret_cast<const u32x4*>(a.L + m * a.rp + k0);
-        lor[tj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(rv), as_bf16x8(lv), lor[tj], 0, 0, 0);
+        lor[tj] = E::mfma16(E::as8(rv), E::as8(lv), lor[tj]);
       }
     }
 #pragma unroll
@@ -747,7 +754,7 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
       float o[4];
 #pragma unroll
       for (int v = 0; v < 4; ++v) o[v] = acc[ti][tj][v] + a.c * lor[tj][v] + bs[v];
-      const u32x2 pk = {pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+      const u32x2 pk = {E::pack2(o[0], o[1]), E::pack2(o[2], o[3])};
       const int chunk = (nloc >> 3) ^ (mloc & 31);
       *reinterpret_cast<u32x2*>(stile + mloc * 512 + chunk * 16 + (nloc & 7) * 2) = pk;
     }
@@ -769,23 +776,27 @@ bool bfgemm_supported(int64_t M, int64_t Ncols, int64_t Kred) {
          Ncols * Kred * 2 < ((int64_t)1 << 31);
 }
 
-int launch_bfgemm(int mode, const GemmArgs& a, const uint16_t* wd, hipStream_t st) {
+int launch_bfgemm(int mode, int elt, const GemmArgs& a, const uint16_t* wd, hipStream_t st) {
   if (!bfgemm_supported(a.M, a.Ncols, a.Kred))
     return fail(REELS_HIP_EINVAL, "bfgemm: shape not supported (reduction not a multiple of 64 or operands of 2 GiB or more)");
   static std::once_flag once;
   static hipError_t attr_err = hipSuccess;
   std::call_once(once, [&] {
-    attr_err = hipFuncSetAttribute((const void*)bfgemm_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, 2 * bfg::STAGE);
+    attr_err = hipFuncSetAttribute((const void*)bfgemm_kernel<REELS_HIP_BF16>, hipFuncAttributeMaxDynamicSharedMemorySize, 2 * bfg::STAGE);
+    if (attr_err == hipSuccess)
+      attr_err = hipFuncSetAttribute((const void*)bfgemm_kernel<REELS_HIP_F16>, hipFuncAttributeMaxDynamicSharedMemorySize, 2 * bfg::STAGE);
   });
   if (attr_err != hipSuccess)
     return fail(REELS_HIP_EHIP, std::string("bfgemm: hipFuncSetAttribute: ") + hipGetErrorString(attr_err));
   const int tn = (int)ceil_div(a.Ncols, bfg::BN), tm = (int)ceil_div(a.M, bfg::BM);
   { TraceScope _ts(st, mode == 0 ? "bfgemm_kernel<0>" : "bfgemm_kernel<1>");
-    bfgemm_kernel<<<tn * tm, bfg::NT, 2 * bfg::STAGE, st>>>(a, wd, tn, tm); }
+    with_elt(elt, [&](auto e) {
+      bfgemm_kernel<decltype(e)::value><<<tn * tm, bfg::NT, 2 * bfg::STAGE, st>>>(a, wd, tn, tm);
+    }); }
   return check_launch("bfgemm_kernel");
 }
 
-int launch_i8gemm(int mode, const GemmArgs& a, hipStream_t st) {
+int launch_i8gemm(int mode, int elt, const GemmArgs& a, hipStream_t st) {
   using namespace gemm;
   // the main kernel needs a reduction in whole 64-steps and 32-bit buffer offsets
   const int64_t act_bytes = a.M * a.Kred * 2, q_bytes = a.Ncols * a.Kred;
@@ -795,28 +806,39 @@ int launch_i8gemm(int mode, const GemmArgs& a, hipStream_t st) {
   static hipError_t attr_err = hipSuccess;
   std::call_once(once, [&] {
     const int l1 = 2 * STAGE_BYTES, l2 = gemm3::NSTAGE * gemm3::STAGE;
-    attr_err = hipFuncSetAttribute((const void*)i8gemm_kernel<0>, hipFuncAttributeMaxDynamicSharedMemorySize, l1);
-    if (attr_err == hipSuccess)
-      attr_err = hipFuncSetAttribute((const void*)i8gemm_kernel<1>, hipFuncAttributeMaxDynamicSharedMemorySize, l1);
-    if (attr_err == hipSuccess)
-      attr_err = hipFuncSetAttribute((const void*)i8gemm_v3_kernel<0>, hipFuncAttributeMaxDynamicSharedMemorySize, l2);
-    if (attr_err == hipSuccess)
-      attr_err = hipFuncSetAttribute((const void*)i8gemm_v3_kernel<1>, hipFuncAttributeMaxDynamicSharedMemorySize, l2);
+    const void* k1[] = {(const void*)i8gemm_kernel<0, REELS_HIP_BF16>, (const void*)i8gemm_kernel<1, REELS_HIP_BF16>,
+                        (const void*)i8gemm_kernel<0, REELS_HIP_F16>, (const void*)i8gemm_kernel<1, REELS_HIP_F16>};
+    const void* k3[] = {(const void*)i8gemm_v3_kernel<0, REELS_HIP_BF16>, (const void*)i8gemm_v3_kernel<1, REELS_HIP_BF16>,
+                        (const void*)i8gemm_v3_kernel<0, REELS_HIP_F16>, (const void*)i8gemm_v3_kernel<1, REELS_HIP_F16>};
+    for (const void* k : k1)
+      if (attr_err == hipSuccess) attr_err = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, l1);
+    for (const void* k : k3)
+      if (attr_err == hipSuccess) attr_err = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, l2);
   });
   if (attr_err != hipSuccess)
     return fail(REELS_HIP_EHIP, std::string("i8gemm: hipFuncSetAttribute: ") + hipGetErrorString(attr_err));
   if (v3) {
     const int tn = (int)ceil_div(a.Ncols, gemm3::BN), tm = (int)ceil_div(a.M, gemm3::BM);
     const size_t lds = gemm3::NSTAGE * gemm3::STAGE;
-    if (mode == 0) { TraceScope _ts(st, "i8gemm_v3_kernel<0>"); i8gemm_v3_kernel<0><<<tn * tm, gemm3::NT, lds, st>>>(a, tn, tm); }
-    else { TraceScope _ts(st, "i8gemm_v3_kernel<1>"); i8gemm_v3_kernel<1><<<tn * tm, gemm3::NT, lds, st>>>(a, tn, tm); }
-    return check_launch(mode == 0 ? "i8gemm_v3_kernel<FWD>" : "i8gemm_v3_kernel<DX>");
+    TraceScope _ts(st, mode == 0 ? "i8gemm_v3_kernel<0>" : "i8gemm_v3_kernel<1>");
+    with_elt(elt, [&](auto e) {
+      constexpr int T = decltype(e)::value;
+      if (mode == 0) i8gemm_v3_kernel<0, T><<<tn * tm, gemm3::NT, lds, st>>>(a, tn, tm);
+      else i8gemm_v3_kernel<1, T><<<tn * tm, gemm3::NT, lds, st>>>(a, tn, tm);
+    });
+  } else {
+    dim3 grid((unsigned)ceil_div(a.Ncols, BN), (unsigned)ceil_div(a.M, BM));
+    const size_t lds = 2 * STAGE_BYTES;
+    TraceScope _ts(st, mode == 0 ? "i8gemm_kernel<0>" : "i8gemm_kernel<1>");
+    with_elt(elt, [&](auto e) {
+      constexpr int T = decltype(e)::value;
+      if (mode == 0) i8gemm_kernel<0, T><<<grid, NT, lds, st>>>(a);
+      else i8gemm_kernel<1, T><<<grid, NT, lds, st>>>(a);
+    });
   }
-  dim3 grid((unsigned)ceil_div(a.Ncols, BN), (unsigned)ceil_div(a.M, BM));
-  const size_t lds = 2 * STAGE_BYTES;
-  if (mode == 0) { TraceScope _ts(st, "i8gemm_kernel<0>"); i8gemm_kernel<0><<<grid, NT, lds, st>>>(a); }
-  else { TraceScope _ts(st, "i8gemm_kernel<1>"); i8gemm_kernel<1><<<grid, NT, lds, st>>>(a); }
-  return check_launch(mode == 0 ? "i8gemm_kernel<FWD>" : "i8gemm_kernel<DX>");
+  const char* what = v3 ? (mode == 0 ? "i8gemm_v3_kernel<FWD>" : "i8gemm_v3_kernel<DX>")
+                        : (mode == 0 ? "i8gemm_kernel<FWD>" : "i8gemm_kernel<DX>");
+  return check_launch(what);
 }
 
 }  // namespace reels

@@ -52,12 +52,14 @@ namespace rowp {
 constexpr int KC = 256, LROW = KC + 8;  // LDS row: 264 bf16 = 528 bytes
 }  // namespace rowp
 
-template <int RT, bool SCALED, int ROWS>
+template <int RT, bool SCALED, int ROWS, int ELT>
 __global__ __launch_bounds__(256) void rowproj_kernel(const uint16_t* __restrict__ src, int64_t M,
                                                       int64_t Kd, const uint16_t* __restrict__ P,
                                                       int r, int rp_, uint16_t* __restrict__ out,
                                                       const float* __restrict__ s,
                                                       uint16_t* __restrict__ scaled) {
+  using E = Elt<ELT>;
+  typedef typename E::v8 V8;
   using namespace rowp;
   constexpr int RG = ROWS / 32;  // 32-row MFMA groups
   __shared__ __attribute__((aligned(16))) uint16_t xs[ROWS * LROW];
@@ -102,10 +104,10 @@ __global__ __launch_bounds__(256) void rowproj_kernel(const uint16_t* __restrict
           const f32x4 sb = *reinterpret_cast<const f32x4*>(s + k + 4);
           const u32x4 x = rx[i];
           u32x4 o;
-          o[0] = pack_bf16x2(bf16_lo(x[0]) * sa[0], bf16_hi(x[0]) * sa[1]);
-          o[1] = pack_bf16x2(bf16_lo(x[1]) * sa[2], bf16_hi(x[1]) * sa[3]);
-          o[2] = pack_bf16x2(bf16_lo(x[2]) * sb[0], bf16_hi(x[2]) * sb[1]);
-          o[3] = pack_bf16x2(bf16_lo(x[3]) * sb[2], bf16_hi(x[3]) * sb[3]);
+          o[0] = E::pack2(E::lo(x[0]) * sa[0], E::hi(x[0]) * sa[1]);
+          o[1] = E::pack2(E::lo(x[1]) * sa[2], E::hi(x[1]) * sa[3]);
+          o[2] = E::pack2(E::lo(x[2]) * sb[0], E::hi(x[2]) * sb[1]);
+          o[3] = E::pack2(E::lo(x[3]) * sb[2], E::hi(x[3]) * sb[3]);
           *reinterpret_cast<u32x4*>(scaled + m * Kd + k) = o;
         }
       }
@@ -131,16 +133,16 @@ __global__ __launch_bounds__(256) void rowproj_kernel(const uint16_t* __restrict
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const int col = wave * 64 + ks * 16 + lhi * 8;
-      bf16x8 a[RG];
+      V8 a[RG];
 #pragma unroll
       for (int g = 0; g < RG; ++g)
-        a[g] = as_bf16x8(*reinterpret_cast<const u32x4*>(&xs[(g * 32 + l32) * LROW + col]));
+        a[g] = E::as8(*reinterpret_cast<const u32x4*>(&xs[(g * 32 + l32) * LROW + col]));
 #pragma unroll
       for (int j = 0; j < RT; ++j) {
-        const bf16x8 bv = as_bf16x8(*reinterpret_cast<const u32x4*>(&ps[(j * 32 + l32) * LROW + col]));
+        const V8 bv = E::as8(*reinterpret_cast<const u32x4*>(&ps[(j * 32 + l32) * LROW + col]));
 #pragma unroll
         for (int g = 0; g < RG; ++g)
-          acc[g][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[g], bv, acc[g][j], 0, 0, 0);
+          acc[g][j] = E::mfma32(a[g], bv, acc[g][j]);
       }
     }
     __syncthreads();
@@ -167,7 +169,7 @@ __global__ __launch_bounds__(256) void rowproj_kernel(const uint16_t* __restrict
     const float sum = red[g][j0][v][ln];
     const int64_t mm = m0 + g * 32 + row;
     const int j = j0 * 32 + col;
-    if (mm < M && j < rp_) out[mm * rp_ + j] = j < r ? (uint16_t)f32_to_bf16_bits(sum) : (uint16_t)0;
+    if (mm < M && j < rp_) out[mm * rp_ + j] = j < r ? (uint16_t)E::bits(sum) : (uint16_t)0;
   }
 }
 
@@ -183,11 +185,13 @@ constexpr int SROW = BO + 16;     // padded LDS row (elements)
 constexpr int LROW = 128 + 16;    // Lm tile row (rp <= 128)
 }  // namespace cg
 
-template <int RT>
+template <int RT, int ELT>
 __global__ __launch_bounds__(256) void colgrad_kernel(const uint16_t* __restrict__ src, int64_t M,
                                                       int64_t Od, const uint16_t* __restrict__ Lm,
                                                       int rp, int64_t tokens_per_split,
                                                       float* __restrict__ part) {
+  using E = Elt<ELT>;
+  typedef typename E::v8 V8;
   using namespace cg;
   __shared__ __attribute__((aligned(16))) uint16_t ssrc[TM * SROW];
   __shared__ __attribute__((aligned(16))) uint16_t slm[TM * LROW];
@@ -267,7 +271,7 @@ __global__ __launch_bounds__(256) void colgrad_kernel(const uint16_t* __restrict
         bv[1] = (uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16);
         bv[2] = (uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16);
         bv[3] = (uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16);
-        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(av), as_bf16x8(bv), acc[t], 0, 0, 0);
+        acc[t] = E::mfma32(E::as8(av), E::as8(bv), acc[t]);
       }
     }
     __syncthreads();
@@ -307,61 +311,68 @@ __global__ void fill_f32_kernel(float* p, int64_t n, float v) {
 // ---------------------------------------------------------------------------------------------
 // generic kernels (any shape / alignment)
 // out[m][j] = bf16(sum_k src[m*Kd + k] * P[k*ps_k + j*ps_j]) (j < r), row stride ld_out
+template <int ELT>
 __global__ void g_rowproj_kernel(const uint16_t* __restrict__ src, int64_t M, int64_t Kd,
                                  const uint16_t* __restrict__ P, int64_t ps_k, int64_t ps_j, int r,
                                  uint16_t* __restrict__ out, int64_t ld_out) {
+  using E = Elt<ELT>;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= M * r) return;
   const int64_t m = idx / r, j = idx % r;
   float acc = 0.0f;
-  for (int64_t k = 0; k < Kd; ++k) acc += bf16_to_f32(src[m * Kd + k]) * bf16_to_f32(P[k * ps_k + j * ps_j]);
-  out[m * ld_out + j] = (uint16_t)f32_to_bf16_bits(acc);
+  for (int64_t k = 0; k < Kd; ++k) acc += E::to_f32(src[m * Kd + k]) * E::to_f32(P[k * ps_k + j * ps_j]);
+  out[m * ld_out + j] = (uint16_t)E::bits(acc);
 }
 
+template <int ELT>
 __global__ void g_fwd_kernel(const uint16_t* __restrict__ x, const int8_t* __restrict__ q,
                              const float* __restrict__ s, const uint16_t* __restrict__ h,
                              int64_t ldh, const uint16_t* __restrict__ B,
                              const uint16_t* __restrict__ bias, int64_t M, int64_t K, int64_t N,
                              int r, float c, uint16_t* __restrict__ y) {
+  using E = Elt<ELT>;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= M * N) return;
   const int64_t m = idx / N, n = idx % N;
   float acc = 0.0f;
-  for (int64_t k = 0; k < K; ++k) acc += bf16_to_f32(x[m * K + k]) * (float)q[n * K + k];
+  for (int64_t k = 0; k < K; ++k) acc += E::to_f32(x[m * K + k]) * (float)q[n * K + k];
   float lo = 0.0f;
-  for (int j = 0; j < r; ++j) lo += bf16_to_f32(h[m * ldh + j]) * bf16_to_f32(B[(int64_t)j * N + n]);
-  float o = s[n] * acc + c * lo + (bias ? bf16_to_f32(bias[n]) : 0.0f);
-  y[idx] = (uint16_t)f32_to_bf16_bits(o);
+  for (int j = 0; j < r; ++j) lo += E::to_f32(h[m * ldh + j]) * E::to_f32(B[(int64_t)j * N + n]);
+  float o = s[n] * acc + c * lo + (bias ? E::to_f32(bias[n]) : 0.0f);
+  y[idx] = (uint16_t)E::bits(o);
 }
 
+template <int ELT>
 __global__ void g_dx_kernel(const uint16_t* __restrict__ dy, const int8_t* __restrict__ q,
                             const float* __restrict__ s, const uint16_t* __restrict__ u,
                             int64_t ldu, const uint16_t* __restrict__ A, int64_t M, int64_t K,
                             int64_t N, int r, float c, uint16_t* __restrict__ dx) {
+  using E = Elt<ELT>;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= M * K) return;
   const int64_t m = idx / K, k = idx % K;
   float acc = 0.0f;
   for (int64_t n = 0; n < N; ++n) {
-    const float dys = bf16_to_f32((uint16_t)f32_to_bf16_bits(bf16_to_f32(dy[m * N + n]) * s[n]));
+    const float dys = E::to_f32((uint16_t)E::bits(E::to_f32(dy[m * N + n]) * s[n]));
     acc += dys * (float)q[n * K + k];
   }
   float lo = 0.0f;
-  for (int j = 0; j < r; ++j) lo += bf16_to_f32(u[m * ldu + j]) * bf16_to_f32(A[k * r + j]);
-  dx[idx] = (uint16_t)f32_to_bf16_bits(acc + c * lo);
+  for (int j = 0; j < r; ++j) lo += E::to_f32(u[m * ldu + j]) * E::to_f32(A[k * r + j]);
+  dx[idx] = (uint16_t)E::bits(acc + c * lo);
 }
 
 // out[o][j] (or [j][o] when TRANS) = c * sum_m src[m][o] * Lm[m][j]
-template <bool TRANS>
+template <bool TRANS, int ELT>
 __global__ void g_colgrad_kernel(const uint16_t* __restrict__ src, int64_t M, int64_t Od,
                                  const uint16_t* __restrict__ Lm, int64_t ldl, int r, float c,
                                  float* __restrict__ out) {
+  using E = Elt<ELT>;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= Od * r) return;
   int64_t o, j;
   if (TRANS) { j = idx / Od; o = idx % Od; } else { o = idx / r; j = idx % r; }
   float acc = 0.0f;
-  for (int64_t m = 0; m < M; ++m) acc += bf16_to_f32(src[m * Od + o]) * bf16_to_f32(Lm[m * ldl + j]);
+  for (int64_t m = 0; m < M; ++m) acc += E::to_f32(src[m * Od + o]) * E::to_f32(Lm[m * ldl + j]);
   out[idx] = c * acc;
 }
 
@@ -377,14 +388,18 @@ __device__ __forceinline__ float gelu_grad_f(float x) {
   const float t = tanhf(k * (x + a * x * x * x));
   return 0.5f * (1.0f + t) + 0.5f * x * (1.0f - t * t) * k * (1.0f + 3.0f * a * x * x);
 }
+template <int ELT>
 __global__ void gelu_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ y, int64_t n) {
+  using E = Elt<ELT>;
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) y[i] = (uint16_t)f32_to_bf16_bits(gelu_f(bf16_to_f32(x[i])));
+  if (i < n) y[i] = (uint16_t)E::bits(gelu_f(E::to_f32(x[i])));
 }
+template <int ELT>
 __global__ void gelu_bwd_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ dy,
                                 uint16_t* __restrict__ dx, int64_t n) {
+  using E = Elt<ELT>;
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) dx[i] = (uint16_t)f32_to_bf16_bits(bf16_to_f32(dy[i]) * gelu_grad_f(bf16_to_f32(x[i])));
+  if (i < n) dx[i] = (uint16_t)E::bits(E::to_f32(dy[i]) * gelu_grad_f(E::to_f32(x[i])));
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -440,39 +455,49 @@ static WsLayout ws_layout(int64_t M, int64_t K, int64_t N, int64_t r, int which,
 static int grid1(int64_t n, int bs = 256) { return (int)ceil_div(n, bs); }
 
 template <bool SCALED, int ROWS>
-static void launch_rowproj_t(int rt, const uint16_t* src, int64_t M, int64_t Kd, const uint16_t* P,
-                             int r, int rp, uint16_t* out, const float* s, uint16_t* scaled,
-                             hipStream_t st) {
+static void launch_rowproj_t(int elt, int rt, const uint16_t* src, int64_t M, int64_t Kd,
+                             const uint16_t* P, int r, int rp, uint16_t* out, const float* s,
+                             uint16_t* scaled, hipStream_t st) {
   const dim3 grid((unsigned)ceil_div(M, ROWS));
   TraceScope _ts(st, SCALED ? (rt <= 1 ? "rowproj_kernel<1,true>" : rt == 2 ? "rowproj_kernel<2,true>" : "rowproj_kernel<4,true>")
                             : (rt <= 1 ? "rowproj_kernel<1,false>" : rt == 2 ? "rowproj_kernel<2,false>" : "rowproj_kernel<4,false>"));
-  if (rt <= 1) rowproj_kernel<1, SCALED, ROWS><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, s, scaled);
-  else if (rt == 2) rowproj_kernel<2, SCALED, ROWS><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, s, scaled);
-  else rowproj_kernel<4, SCALED, ROWS><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, s, scaled);
+  with_elt(elt, [&](auto e) {
+    constexpr int T = decltype(e)::value;
+    if (rt <= 1) rowproj_kernel<1, SCALED, ROWS, T><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, s, scaled);
+    else if (rt == 2) rowproj_kernel<2, SCALED, ROWS, T><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, s, scaled);
+    else rowproj_kernel<4, SCALED, ROWS, T><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, s, scaled);
+  });
 }
 
-static int launch_rowproj(const uint16_t* src, int64_t M, int64_t Kd, const uint16_t* P, int r,
-                          int rp, uint16_t* out, const float* s, uint16_t* scaled, hipStream_t st) {
+static int launch_rowproj(int elt, const uint16_t* src, int64_t M, int64_t Kd, const uint16_t* P,
+                          int r, int rp, uint16_t* out, const float* s, uint16_t* scaled,
+                          hipStream_t st) {
   const int rt = (r + 31) / 32;
   const bool wide = ceil_div(M, 64) >= 256;  // enough tokens for a 64-row block on every CU
   if (scaled) {
-    if (wide) launch_rowproj_t<true, 64>(rt, src, M, Kd, P, r, rp, out, s, scaled, st);
-    else launch_rowproj_t<true, 32>(rt, src, M, Kd, P, r, rp, out, s, scaled, st);
+    if (wide) launch_rowproj_t<true, 64>(elt, rt, src, M, Kd, P, r, rp, out, s, scaled, st);
+    else launch_rowproj_t<true, 32>(elt, rt, src, M, Kd, P, r, rp, out, s, scaled, st);
   } else {
-    if (wide) launch_rowproj_t<false, 64>(rt, src, M, Kd, P, r, rp, out, s, scaled, st);
-    else launch_rowproj_t<false, 32>(rt, src, M, Kd, P, r, rp, out, s, scaled, st);
+    if (wide) launch_rowproj_t<false, 64>(elt, rt, src, M, Kd, P, r, rp, out, s, scaled, st);
+    else launch_rowproj_t<false, 32>(elt, rt, src, M, Kd, P, r, rp, out, s, scaled, st);
   }
   return check_launch("rowproj_kernel");
 }
 
-static int launch_colgrad(const uint16_t* src, int64_t M, int64_t Od, const uint16_t* Lm, int r,
-                          int rp, const Plan& p, float c, float* part, float* out, bool trans,
-                          hipStream_t st) {
+static int launch_colgrad(int elt, const uint16_t* src, int64_t M, int64_t Od, const uint16_t* Lm,
+                          int r, int rp, const Plan& p, float c, float* part, float* out,
+                          bool trans, hipStream_t st) {
   const dim3 grid((unsigned)ceil_div(Od, cg::BO), (unsigned)p.splits);
   const int rt = (rp + 31) / 32;
-  if (rt <= 1) { TraceScope _ts(st, "colgrad_kernel<1>"); colgrad_kernel<1><<<grid, 256, 0, st>>>(src, M, Od, Lm, rp, p.tps, part); }
-  else if (rt == 2) { TraceScope _ts(st, "colgrad_kernel<2>"); colgrad_kernel<2><<<grid, 256, 0, st>>>(src, M, Od, Lm, rp, p.tps, part); }
-  else { TraceScope _ts(st, "colgrad_kernel<4>"); colgrad_kernel<4><<<grid, 256, 0, st>>>(src, M, Od, Lm, rp, p.tps, part); }
+  {
+    TraceScope _ts(st, rt <= 1 ? "colgrad_kernel<1>" : rt == 2 ? "colgrad_kernel<2>" : "colgrad_kernel<4>");
+    with_elt(elt, [&](auto e) {
+      constexpr int T = decltype(e)::value;
+      if (rt <= 1) colgrad_kernel<1, T><<<grid, 256, 0, st>>>(src, M, Od, Lm, rp, p.tps, part);
+      else if (rt == 2) colgrad_kernel<2, T><<<grid, 256, 0, st>>>(src, M, Od, Lm, rp, p.tps, part);
+      else colgrad_kernel<4, T><<<grid, 256, 0, st>>>(src, M, Od, Lm, rp, p.tps, part);
+    });
+  }
   int rc = check_launch("colgrad_kernel");
   if (rc) return rc;
   if (trans) { TraceScope _ts(st, "reduce_partials_kernel<true>"); reduce_partials_kernel<true><<<grid1(Od * r), 256, 0, st>>>(part, p.splits, Od, rp, r, c, out); }
@@ -499,24 +524,24 @@ static bool all_aligned(std::initializer_list<const void*> ps) {
   return true;
 }
 
-extern "C" int reels_hip_i8lora_fwd(const void* x, const int8_t* q, const float* scales,
-                                    const void* A, const void* B, const void* bias, int64_t M,
-                                    int64_t K, int64_t N, int64_t r, float lora_scale, void* y,
-                                    void* h_save, void* workspace, size_t ws_bytes, void* stream) {
+static int i8lora_fwd_impl(int elt, const char* fn, const void* x, const int8_t* q,
+                           const float* scales, const void* A, const void* B, const void* bias,
+                           int64_t M, int64_t K, int64_t N, int64_t r, float lora_scale, void* y,
+                           void* h_save, void* workspace, size_t ws_bytes, void* stream) {
   clear_error();
   if (M < 0 || K <= 0 || N <= 0 || r < 0 || r > 4096)
-    return fail(REELS_HIP_EINVAL, "reels_hip_i8lora_fwd: need M >= 0, K > 0, N > 0, 0 <= r <= 4096");
+    return fail(REELS_HIP_EINVAL, std::string(fn) + ": " "need M >= 0, K > 0, N > 0, 0 <= r <= 4096");
   if (!(lora_scale == lora_scale))
-    return fail(REELS_HIP_EINVAL, "reels_hip_i8lora_fwd: lora_scale is NaN");
+    return fail(REELS_HIP_EINVAL, std::string(fn) + ": " "lora_scale is NaN");
   if (M == 0) return REELS_HIP_OK;
   if (!x || !q || !scales || !y || (r > 0 && (!A || !B)))
-    return fail(REELS_HIP_EINVAL, "reels_hip_i8lora_fwd: NULL x, q, scales, y, or A/B with r > 0");
+    return fail(REELS_HIP_EINVAL, std::string(fn) + ": " "NULL x, q, scales, y, or A/B with r > 0");
   const bool al = all_aligned({x, q, scales, A, B, y, h_save}) &&
                   (bias == nullptr || (reinterpret_cast<uintptr_t>(bias) & 7u) == 0);
   Plan p = make_plan(M, K, N, r, al);
   WsLayout w = ws_layout(M, K, N, r, REELS_HIP_WS_FWD, p);
   if (workspace == nullptr || ws_bytes < w.total)
-    return fail(REELS_HIP_EWORKSPACE, "reels_hip_i8lora_fwd: workspace NULL or smaller than "
+    return fail(REELS_HIP_EWORKSPACE, std::string(fn) + ": " "workspace NULL or smaller than "
                                       "reels_hip_i8lora_workspace_bytes(..., REELS_HIP_WS_FWD)");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
@@ -525,13 +550,13 @@ extern "C" int reels_hip_i8lora_fwd(const void* x, const int8_t* q, const float*
   int rc;
   if (!p.fast) {
     if (r > 0) {
-      { TraceScope _ts(st, "g_rowproj_kernel"); g_rowproj_kernel<<<grid1(M * r), 256, 0, st>>>(xb, M, K, static_cast<const uint16_t*>(A), r, 1,
-                                                    (int)r, h, r); }
+      { TraceScope _ts(st, "g_rowproj_kernel"); with_elt(elt, [&](auto e) { g_rowproj_kernel<decltype(e)::value><<<grid1(M * r), 256, 0, st>>>(xb, M, K, static_cast<const uint16_t*>(A), r, 1,
+                                                    (int)r, h, r); }); }
       if ((rc = check_launch("g_rowproj_kernel"))) return rc;
     }
-    { TraceScope _ts(st, "g_fwd_kernel"); g_fwd_kernel<<<grid1(M * N), 256, 0, st>>>(xb, q, scales, h, r, static_cast<const uint16_t*>(B),
+    { TraceScope _ts(st, "g_fwd_kernel"); with_elt(elt, [&](auto e) { g_fwd_kernel<decltype(e)::value><<<grid1(M * N), 256, 0, st>>>(xb, q, scales, h, r, static_cast<const uint16_t*>(B),
                                               static_cast<const uint16_t*>(bias), M, K, N, (int)r,
-                                              lora_scale, static_cast<uint16_t*>(y)); }
+                                              lora_scale, static_cast<uint16_t*>(y)); }); }
     return check_launch("g_fwd_kernel");
   }
   uint16_t* bt = nullptr;
@@ -545,7 +570,7 @@ extern "C" int reels_hip_i8lora_fwd(const void* x, const int8_t* q, const float*
     { TraceScope _ts(st, "transpose_pad_kernel"); transpose_pad_kernel<<<dim3((unsigned)ceil_div(N, 32), (unsigned)ceil_div(r, 32)), 256, 0, st>>>(
         static_cast<const uint16_t*>(B), r, N, p.rp, bt); }
     if ((rc = check_launch("transpose_pad_kernel"))) return rc;
-    if ((rc = launch_rowproj(xb, M, K, at, (int)r, p.rp, h, nullptr, nullptr, st))) return rc;
+    if ((rc = launch_rowproj(elt, xb, M, K, at, (int)r, p.rp, h, nullptr, nullptr, st))) return rc;
   }
   GemmArgs g{};
   g.act = xb; g.q = q; g.colscale = scales; g.L = h; g.R = bt;
@@ -553,23 +578,22 @@ extern "C" int reels_hip_i8lora_fwd(const void* x, const int8_t* q, const float*
   g.M = M; g.Ncols = N; g.Kred = K; g.ldq = K; g.rp = r > 0 ? p.rp : 0; g.c = lora_scale;
   if (p.deq) {
     uint16_t* wd = reinterpret_cast<uint16_t*>(ws + w.wd);
-    if ((rc = launch_dequant_rows(q, K, scales, N, K, wd, st))) return rc;
+    if ((rc = launch_dequant_rows(elt, q, K, scales, N, K, wd, st))) return rc;
     g.q = nullptr; g.colscale = nullptr;
-    return launch_bfgemm(0, g, wd, st);
+    return launch_bfgemm(0, elt, g, wd, st);
   }
-  return launch_i8gemm(0, g, st);
+  return launch_i8gemm(0, elt, g, st);
 }
 
-extern "C" int reels_hip_i8lora_bwd(const void* dy, const void* x, const void* h, const int8_t* q,
-                                    const float* scales, const void* A, const void* B, int64_t M,
-                                    int64_t K, int64_t N, int64_t r, float lora_scale, void* dx,
-                                    float* dA, float* dB, void* workspace, size_t ws_bytes,
-                                    void* stream) {
+static int i8lora_bwd_impl(int elt, const char* fn, const void* dy, const void* x, const void* h,
+                           const int8_t* q, const float* scales, const void* A, const void* B,
+                           int64_t M, int64_t K, int64_t N, int64_t r, float lora_scale, void* dx,
+                           float* dA, float* dB, void* workspace, size_t ws_bytes, void* stream) {
   clear_error();
   if (M < 0 || K <= 0 || N <= 0 || r < 0 || r > 4096)
-    return fail(REELS_HIP_EINVAL, "reels_hip_i8lora_bwd: need M >= 0, K > 0, N > 0, 0 <= r <= 4096");
+    return fail(REELS_HIP_EINVAL, std::string(fn) + ": " "need M >= 0, K > 0, N > 0, 0 <= r <= 4096");
   if (!(lora_scale == lora_scale))
-    return fail(REELS_HIP_EINVAL, "reels_hip_i8lora_bwd: lora_scale is NaN");
+    return fail(REELS_HIP_EINVAL, std::string(fn) + ": " "lora_scale is NaN");
   if (r == 0) { dA = nullptr; dB = nullptr; }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   int rc;
@@ -585,14 +609,14 @@ extern "C" int reels_hip_i8lora_bwd(const void* dy, const void* x, const void* h
     return REELS_HIP_OK;
   }
   if (!dy || !q || !scales || (r > 0 && (!A || !B)) || ((dA || (dB && !h)) && !x))
-    return fail(REELS_HIP_EINVAL, "reels_hip_i8lora_bwd: NULL dy, q, scales, A/B with r > 0, or x "
+    return fail(REELS_HIP_EINVAL, std::string(fn) + ": " "NULL dy, q, scales, A/B with r > 0, or x "
                                   "needed for dA / recomputing h");
   if (!dx && !dA && !dB) return REELS_HIP_OK;
   const bool al = all_aligned({dy, x, h, q, scales, A, B, dx, dA, dB});
   Plan p = make_plan(M, K, N, r, al);
   WsLayout w = ws_layout(M, K, N, r, REELS_HIP_WS_BWD, p);
   if (workspace == nullptr || ws_bytes < w.total)
-    return fail(REELS_HIP_EWORKSPACE, "reels_hip_i8lora_bwd: workspace NULL or smaller than "
+    return fail(REELS_HIP_EWORKSPACE, std::string(fn) + ": " "workspace NULL or smaller than "
                                       "reels_hip_i8lora_workspace_bytes(..., REELS_HIP_WS_BWD)");
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   const uint16_t* dyb = static_cast<const uint16_t*>(dy);
@@ -605,26 +629,26 @@ extern "C" int reels_hip_i8lora_bwd(const void* dy, const void* x, const void* h
 
   if (!p.fast) {
     if (r > 0 && (dx || dA)) {
-      { TraceScope _ts(st, "g_rowproj_kernel"); g_rowproj_kernel<<<grid1(M * r), 256, 0, st>>>(dyb, M, N, Bb, 1, N, (int)r, u, r); }
+      { TraceScope _ts(st, "g_rowproj_kernel"); with_elt(elt, [&](auto e) { g_rowproj_kernel<decltype(e)::value><<<grid1(M * r), 256, 0, st>>>(dyb, M, N, Bb, 1, N, (int)r, u, r); }); }
       if ((rc = check_launch("g_rowproj_kernel"))) return rc;
     }
     if (need_h && !hh) {
       uint16_t* hw = reinterpret_cast<uint16_t*>(ws + w.h);
-      { TraceScope _ts(st, "g_rowproj_kernel"); g_rowproj_kernel<<<grid1(M * r), 256, 0, st>>>(xb, M, K, Ab, r, 1, (int)r, hw, r); }
+      { TraceScope _ts(st, "g_rowproj_kernel"); with_elt(elt, [&](auto e) { g_rowproj_kernel<decltype(e)::value><<<grid1(M * r), 256, 0, st>>>(xb, M, K, Ab, r, 1, (int)r, hw, r); }); }
       if ((rc = check_launch("g_rowproj_kernel"))) return rc;
       hh = hw;
     }
     if (dx) {
-      { TraceScope _ts(st, "g_dx_kernel"); g_dx_kernel<<<grid1(M * K), 256, 0, st>>>(dyb, q, scales, u, r, Ab, M, K, N, (int)r, lora_scale,
-                                               static_cast<uint16_t*>(dx)); }
+      { TraceScope _ts(st, "g_dx_kernel"); with_elt(elt, [&](auto e) { g_dx_kernel<decltype(e)::value><<<grid1(M * K), 256, 0, st>>>(dyb, q, scales, u, r, Ab, M, K, N, (int)r, lora_scale,
+                                               static_cast<uint16_t*>(dx)); }); }
       if ((rc = check_launch("g_dx_kernel"))) return rc;
     }
     if (dA) {
-      { TraceScope _ts(st, "g_colgrad_kernel<false>"); g_colgrad_kernel<false><<<grid1(K * r), 256, 0, st>>>(xb, M, K, u, r, (int)r, lora_scale, dA); }
+      { TraceScope _ts(st, "g_colgrad_kernel<false>"); with_elt(elt, [&](auto e) { g_colgrad_kernel<false, decltype(e)::value><<<grid1(K * r), 256, 0, st>>>(xb, M, K, u, r, (int)r, lora_scale, dA); }); }
       if ((rc = check_launch("g_colgrad_kernel"))) return rc;
     }
     if (dB) {
-      { TraceScope _ts(st, "g_colgrad_kernel<true>"); g_colgrad_kernel<true><<<grid1(N * r), 256, 0, st>>>(dyb, M, N, hh, r, (int)r, lora_scale, dB); }
+      { TraceScope _ts(st, "g_colgrad_kernel<true>"); with_elt(elt, [&](auto e) { g_colgrad_kernel<true, decltype(e)::value><<<grid1(N * r), 256, 0, st>>>(dyb, M, N, hh, r, (int)r, lora_scale, dB); }); }
       if ((rc = check_launch("g_colgrad_kernel"))) return rc;
     }
     return REELS_HIP_OK;
@@ -634,24 +658,24 @@ extern "C" int reels_hip_i8lora_bwd(const void* dy, const void* x, const void* h
   if (p.deq) {
     // 1. u = dy B^T; 2. dx = dy wt^T + c u A^T with wt[k][n] = bf16(q[n][k] s[n])
     if (r > 0 && (dx || dA)) {
-      if ((rc = launch_rowproj(dyb, M, N, Bb, (int)r, p.rp, u, nullptr, nullptr, st))) return rc;
+      if ((rc = launch_rowproj(elt, dyb, M, N, Bb, (int)r, p.rp, u, nullptr, nullptr, st))) return rc;
     }
     if (dx) {
       uint16_t* wt = reinterpret_cast<uint16_t*>(ws + w.wd);
-      if ((rc = launch_dequant_transpose(q, K, scales, N, K, wt, st))) return rc;
+      if ((rc = launch_dequant_transpose(elt, q, K, scales, N, K, wt, st))) return rc;
       GemmArgs g{};
       g.act = dyb; g.q = nullptr; g.colscale = nullptr; g.L = r > 0 ? u : nullptr; g.R = Ab;
       g.bias = nullptr; g.out = static_cast<uint16_t*>(dx);
       g.M = M; g.Ncols = K; g.Kred = N; g.ldq = N; g.rp = r > 0 ? p.rp : 0; g.c = lora_scale;
-      if ((rc = launch_bfgemm(1, g, wt, st))) return rc;
+      if ((rc = launch_bfgemm(1, elt, g, wt, st))) return rc;
     }
   } else if (r > 0 || dx) {
     // 1. u = dy B^T and dys = dy * s in one pass over dy (the scaled copy only when dx is wanted)
     if (r > 0) {
-      if ((rc = launch_rowproj(dyb, M, N, Bb, (int)r, p.rp, u, scales, dx ? dys : nullptr, st))) return rc;
+      if ((rc = launch_rowproj(elt, dyb, M, N, Bb, (int)r, p.rp, u, scales, dx ? dys : nullptr, st))) return rc;
     } else {
       // r = 0: only the scaled copy is needed (no projection output)
-      if ((rc = launch_rowproj(dyb, M, N, Bb, 0, 0, nullptr, scales, dys, st))) return rc;
+      if ((rc = launch_rowproj(elt, dyb, M, N, Bb, 0, 0, nullptr, scales, dys, st))) return rc;
     }
   }
   // 2. dx = dys q + c u A^T
@@ -660,11 +684,11 @@ extern "C" int reels_hip_i8lora_bwd(const void* dy, const void* x, const void* h
     g.act = dys; g.q = q; g.colscale = nullptr; g.L = r > 0 ? u : nullptr; g.R = Ab; g.bias = nullptr;
     g.out = static_cast<uint16_t*>(dx);
     g.M = M; g.Ncols = K; g.Kred = N; g.ldq = K; g.rp = r > 0 ? p.rp : 0; g.c = lora_scale;
-    if ((rc = launch_i8gemm(1, g, st))) return rc;
+    if ((rc = launch_i8gemm(1, elt, g, st))) return rc;
   }
   // 3. dA = c x^T u ; dB = c (dy^T h)^T
   if (dA) {
-    if ((rc = launch_colgrad(xb, M, K, u, (int)r, p.rp, p, lora_scale,
+    if ((rc = launch_colgrad(elt, xb, M, K, u, (int)r, p.rp, p, lora_scale,
                              reinterpret_cast<float*>(ws + w.pa), dA, false, st))) return rc;
   }
   if (dB) {
@@ -674,35 +698,88 @@ extern "C" int reels_hip_i8lora_bwd(const void* dy, const void* x, const void* h
       { TraceScope _ts(st, "transpose_pad_kernel"); transpose_pad_kernel<<<dim3((unsigned)ceil_div(r, 32), (unsigned)ceil_div(K, 32)), 256, 0, st>>>(
           Ab, K, r, K, at); }
       if ((rc = check_launch("transpose_pad_kernel"))) return rc;
-      if ((rc = launch_rowproj(xb, M, K, at, (int)r, p.rp, hw, nullptr, nullptr, st))) return rc;
+      if ((rc = launch_rowproj(elt, xb, M, K, at, (int)r, p.rp, hw, nullptr, nullptr, st))) return rc;
       hh = hw;
     }
-    if ((rc = launch_colgrad(dyb, M, N, hh, (int)r, p.rp, p, lora_scale,
+    if ((rc = launch_colgrad(elt, dyb, M, N, hh, (int)r, p.rp, p, lora_scale,
                              reinterpret_cast<float*>(ws + w.pb), dB, true, st))) return rc;
   }
   return REELS_HIP_OK;
 }
 
-extern "C" int reels_hip_gelu_tanh(const void* x, void* y, int64_t n, void* stream) {
+static int gelu_impl(int elt, const char* fn, const void* x, void* y, int64_t n, void* stream) {
   clear_error();
-  if (n < 0) return fail(REELS_HIP_EINVAL, "reels_hip_gelu_tanh: n < 0");
+  if (n < 0) return fail(REELS_HIP_EINVAL, std::string(fn) + ": " "n < 0");
   if (n == 0) return REELS_HIP_OK;
-  if (!x || !y) return fail(REELS_HIP_EINVAL, "reels_hip_gelu_tanh: NULL pointer");
+  if (!x || !y) return fail(REELS_HIP_EINVAL, std::string(fn) + ": " "NULL pointer");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   { TraceScope _ts(st, "gelu_kernel");
-    gelu_kernel<<<grid1(n), 256, 0, st>>>(static_cast<const uint16_t*>(x), static_cast<uint16_t*>(y), n); }
+    with_elt(elt, [&](auto e) { gelu_kernel<decltype(e)::value><<<grid1(n), 256, 0, st>>>(static_cast<const uint16_t*>(x), static_cast<uint16_t*>(y), n); }); }
   return check_launch("gelu_kernel");
 }
 
-extern "C" int reels_hip_gelu_tanh_bwd(const void* x, const void* dy, void* dx, int64_t n, void* stream) {
+static int gelu_bwd_impl(int elt, const char* fn, const void* x, const void* dy, void* dx, int64_t n,
+                         void* stream) {
   clear_error();
-  if (n < 0) return fail(REELS_HIP_EINVAL, "reels_hip_gelu_tanh_bwd: n < 0");
+  if (n < 0) return fail(REELS_HIP_EINVAL, std::string(fn) + ": " "n < 0");
   if (n == 0) return REELS_HIP_OK;
-  if (!x || !dy || !dx) return fail(REELS_HIP_EINVAL, "reels_hip_gelu_tanh_bwd: NULL pointer");
+  if (!x || !dy || !dx) return fail(REELS_HIP_EINVAL, std::string(fn) + ": " "NULL pointer");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   { TraceScope _ts(st, "gelu_bwd_kernel");
-    gelu_bwd_kernel<<<grid1(n), 256, 0, st>>>(static_cast<const uint16_t*>(x),
+    with_elt(elt, [&](auto e) { gelu_bwd_kernel<decltype(e)::value><<<grid1(n), 256, 0, st>>>(static_cast<const uint16_t*>(x),
                                               static_cast<const uint16_t*>(dy),
-                                              static_cast<uint16_t*>(dx), n); }
+                                              static_cast<uint16_t*>(dx), n); }); }
   return check_launch("gelu_bwd_kernel");
+}
+
+extern "C" int reels_hip_i8lora_fwd(const void* x, const int8_t* q, const float* scales,
+                                    const void* A, const void* B, const void* bias, int64_t M,
+                                    int64_t K, int64_t N, int64_t r, float lora_scale, void* y,
+                                    void* h_save, void* workspace, size_t ws_bytes, void* stream) {
+  return i8lora_fwd_impl(REELS_HIP_BF16, "reels_hip_i8lora_fwd", x, q, scales, A, B, bias, M, K, N,
+                         r, lora_scale, y, h_save, workspace, ws_bytes, stream);
+}
+
+extern "C" int reels_hip_i8lora_fwd_f16(const void* x, const int8_t* q, const float* scales,
+                                        const void* A, const void* B, const void* bias, int64_t M,
+                                        int64_t K, int64_t N, int64_t r, float lora_scale, void* y,
+                                        void* h_save, void* workspace, size_t ws_bytes,
+                                        void* stream) {
+  return i8lora_fwd_impl(REELS_HIP_F16, "reels_hip_i8lora_fwd_f16", x, q, scales, A, B, bias, M, K,
+                         N, r, lora_scale, y, h_save, workspace, ws_bytes, stream);
+}
+
+extern "C" int reels_hip_i8lora_bwd(const void* dy, const void* x, const void* h, const int8_t* q,
+                                    const float* scales, const void* A, const void* B, int64_t M,
+                                    int64_t K, int64_t N, int64_t r, float lora_scale, void* dx,
+                                    float* dA, float* dB, void* workspace, size_t ws_bytes,
+                                    void* stream) {
+  return i8lora_bwd_impl(REELS_HIP_BF16, "reels_hip_i8lora_bwd", dy, x, h, q, scales, A, B, M, K, N,
+                         r, lora_scale, dx, dA, dB, workspace, ws_bytes, stream);
+}
+
+extern "C" int reels_hip_i8lora_bwd_f16(const void* dy, const void* x, const void* h,
+                                        const int8_t* q, const float* scales, const void* A,
+                                        const void* B, int64_t M, int64_t K, int64_t N, int64_t r,
+                                        float lora_scale, void* dx, float* dA, float* dB,
+                                        void* workspace, size_t ws_bytes, void* stream) {
+  return i8lora_bwd_impl(REELS_HIP_F16, "reels_hip_i8lora_bwd_f16", dy, x, h, q, scales, A, B, M, K,
+                         N, r, lora_scale, dx, dA, dB, workspace, ws_bytes, stream);
+}
+
+extern "C" int reels_hip_gelu_tanh(const void* x, void* y, int64_t n, void* stream) {
+  return gelu_impl(REELS_HIP_BF16, "reels_hip_gelu_tanh", x, y, n, stream);
+}
+
+extern "C" int reels_hip_gelu_tanh_f16(const void* x, void* y, int64_t n, void* stream) {
+  return gelu_impl(REELS_HIP_F16, "reels_hip_gelu_tanh_f16", x, y, n, stream);
+}
+
+extern "C" int reels_hip_gelu_tanh_bwd(const void* x, const void* dy, void* dx, int64_t n, void* stream) {
+  return gelu_bwd_impl(REELS_HIP_BF16, "reels_hip_gelu_tanh_bwd", x, dy, dx, n, stream);
+}
+
+extern "C" int reels_hip_gelu_tanh_bwd_f16(const void* x, const void* dy, void* dx, int64_t n,
+                                           void* stream) {
+  return gelu_bwd_impl(REELS_HIP_F16, "reels_hip_gelu_tanh_bwd_f16", x, dy, dx, n, stream);
 }

@@ -38,6 +38,18 @@ def _need_device(t: torch.Tensor, name: str) -> None:
                          "runs only on the GPU")
 
 
+# 16-bit activation types of the LoRA linear and the suffix of their C entry points:
+# bfloat16 (this library's default) and float16 (the reference's int8 compute precision)
+_ACT_SUFFIX = {torch.bfloat16: "", torch.float16: "_f16"}
+
+
+def _act_dtype(t: torch.Tensor, name: str) -> torch.dtype:
+    _need_device(t, name)
+    if t.dtype not in _ACT_SUFFIX:
+        raise TypeError(f"{name} must be bfloat16 or float16, got {t.dtype}")
+    return t.dtype
+
+
 def _contig(t: Optional[torch.Tensor], dtype: torch.dtype, name: str) -> Optional[torch.Tensor]:
     if t is None:
         return None
@@ -125,26 +137,29 @@ def workspace_bytes(M: int, K: int, N: int, r: int, which: int) -> int:
 
 def i8lora_forward(x, weight: QuantizedMatrix, A=None, B=None, bias=None, lora_scale=1.0,
                    save_h: bool = False):
-    """y = bf16(x deq(Wq)^T + lora_scale * bf16(x A) B + bias); returns (y, h or None).
+    """y = rnd(x deq(Wq)^T + lora_scale * rnd(x A) B + bias); returns (y, h or None).
 
-    x [M][K] bf16; A [K][r], B [r][N] bf16 (Julia A::(r,K), B::(N,r)); bias [N] bf16."""
-    x = _contig(x, torch.bfloat16, "x")
+    x [M][K] bfloat16 or float16 (reels_hip_i8lora_fwd / _fwd_f16); A [K][r], B [r][N] and
+    bias [N] of the same dtype (Julia A::(r,K), B::(N,r)); y and h come back in that dtype."""
+    dt = _act_dtype(x, "x")
+    x = x.contiguous()
     M, K = x.shape
     N, Kw = weight.values.shape
     if Kw != K:
         raise ValueError("DimensionMismatch: LoRA input and weight dimensions differ")
     r = 0 if A is None else A.shape[1]
-    A = _contig(A, torch.bfloat16, "A")
-    B = _contig(B, torch.bfloat16, "B")
+    A = _contig(A, dt, "A")
+    B = _contig(B, dt, "B")
     if r and (tuple(A.shape) != (K, r) or tuple(B.shape) != (r, N)):
         raise ValueError(f"A must be [K][r] = {(K, r)} and B [r][N] = {(r, N)}")
-    bias = _contig(bias, torch.bfloat16, "bias")
+    bias = _contig(bias, dt, "bias")
     dev = x.device
-    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-    h = torch.empty((M, r), dtype=torch.bfloat16, device=dev) if (save_h and r) else None
+    y = torch.empty((M, N), dtype=dt, device=dev)
+    h = torch.empty((M, r), dtype=dt, device=dev) if (save_h and r) else None
     nbytes = workspace_bytes(M, K, N, r, _lib.WS_FWD)
     ws = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
-    _lib.check("reels_hip_i8lora_fwd", _lib.lib().reels_hip_i8lora_fwd(
+    fn = "reels_hip_i8lora_fwd" + _ACT_SUFFIX[dt]
+    _lib.check(fn, getattr(_lib.lib(), fn)(
         _ptr(x), _ptr(weight.values), _ptr(weight.scales), _ptr(A), _ptr(B), _ptr(bias),
         M, K, N, r, float(lora_scale), _ptr(y), _ptr(h), _ptr(ws), nbytes, _stream(dev)))
     return y, h
@@ -152,24 +167,28 @@ def i8lora_forward(x, weight: QuantizedMatrix, A=None, B=None, bias=None, lora_s
 
 def i8lora_backward(dy, x, weight: QuantizedMatrix, A=None, B=None, lora_scale=1.0, h=None,
                     want_dx=True, want_dA=True, want_dB=True):
-    """(dx bf16 [M][K], dA f32 [K][r], dB f32 [r][N]) of lora_backward (lora.jl:106-118)."""
-    dy = _contig(dy, torch.bfloat16, "dy")
+    """(dx [M][K], dA f32 [K][r], dB f32 [r][N]) of lora_backward (lora.jl:106-118). dy, x, h,
+    A and B share one dtype, bfloat16 or float16 (reels_hip_i8lora_bwd / _bwd_f16); dx comes
+    back in it."""
+    dt = _act_dtype(dy, "dy")
+    dy = dy.contiguous()
     M, N = dy.shape
     Nw, K = weight.values.shape
     if Nw != N:
         raise ValueError("DimensionMismatch: dy and weight output dimensions differ")
     r = 0 if A is None else A.shape[1]
-    A = _contig(A, torch.bfloat16, "A")
-    B = _contig(B, torch.bfloat16, "B")
-    x = _contig(x, torch.bfloat16, "x") if x is not None else None
-    h = _contig(h, torch.bfloat16, "h")
+    A = _contig(A, dt, "A")
+    B = _contig(B, dt, "B")
+    x = _contig(x, dt, "x") if x is not None else None
+    h = _contig(h, dt, "h")
     dev = dy.device
-    dx = torch.empty((M, K), dtype=torch.bfloat16, device=dev) if want_dx else None
+    dx = torch.empty((M, K), dtype=dt, device=dev) if want_dx else None
     dA = torch.empty((K, r), dtype=torch.float32, device=dev) if (want_dA and r) else None
     dB = torch.empty((r, N), dtype=torch.float32, device=dev) if (want_dB and r) else None
     nbytes = workspace_bytes(M, K, N, r, _lib.WS_BWD)
     ws = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
-    _lib.check("reels_hip_i8lora_bwd", _lib.lib().reels_hip_i8lora_bwd(
+    fn = "reels_hip_i8lora_bwd" + _ACT_SUFFIX[dt]
+    _lib.check(fn, getattr(_lib.lib(), fn)(
         _ptr(dy), _ptr(x), _ptr(h), _ptr(weight.values), _ptr(weight.scales), _ptr(A), _ptr(B),
         M, K, N, r, float(lora_scale), _ptr(dx), _ptr(dA), _ptr(dB), _ptr(ws), nbytes,
         _stream(dev)))
@@ -178,7 +197,8 @@ def i8lora_backward(dy, x, weight: QuantizedMatrix, A=None, B=None, lora_scale=1
 
 # ---- reference-named layer API ----------------------------------------------------------------
 def _weight_mul(weight: QuantizedMatrix, x: torch.Tensor) -> torch.Tensor:
-    """_weight_mul (quantization.jl:73-74): x deq(W)^T without materialising deq(W)."""
+    """_weight_mul (quantization.jl:73-74): x deq(W)^T (deq(W) lives only in the call's
+    workspace, as the reference's _materialize_weight result lives only for the call)."""
     return i8lora_forward(x, weight)[0]
 
 
@@ -216,8 +236,9 @@ def linear(layer: DenseLayer, x: torch.Tensor) -> torch.Tensor:
 class LoRALinear:
     """LoRALinear (lora.jl:1-35) over a QuantizedMatrix base weight.
 
-    A: [K][r] (Julia A::(r, K)), B: [r][N] (Julia B::(N, r)), bf16 on the device. The constructor
-    initialises A ~ randn / sqrt(in) and B = 0 like the reference (lora.jl:22-24)."""
+    A: [K][r] (Julia A::(r, K)), B: [r][N] (Julia B::(N, r)) on the device, in the weight's
+    compute dtype when that is float16, else bfloat16. The constructor initialises
+    A ~ randn / sqrt(in) and B = 0 like the reference (lora.jl:22-24)."""
 
     def __init__(self, weight: QuantizedMatrix, rank: int, alpha: Optional[float] = None,
                  dropout: float = 0.0, bias: Optional[torch.Tensor] = None,
@@ -236,11 +257,12 @@ class LoRALinear:
             raise ValueError("cannot train a missing linear bias")
         out, inp = weight.shape
         dev = weight.values.device
+        dt = weight.compute_dtype if weight.compute_dtype in _ACT_SUFFIX else torch.bfloat16
         if A is None:
             A = (torch.randn((inp, rank), generator=generator, dtype=torch.float32, device=dev)
-                 * (1.0 / math.sqrt(inp))).to(torch.bfloat16)
+                 * (1.0 / math.sqrt(inp))).to(dt)
         if B is None:
-            B = torch.zeros((rank, out), dtype=torch.bfloat16, device=dev)
+            B = torch.zeros((rank, out), dtype=dt, device=dev)
         self.weight, self.A, self.B = weight, A, B
         self.alpha, self.dropout = alpha, float(dropout)
         self.enabled, self.train_bias = True, train_bias
@@ -279,7 +301,8 @@ def lora_forward(layer: LoRALinear, x: torch.Tensor, training: bool = False,
                  save_h: bool = False, **_):
     """lora_forward (lora.jl:56-95): y = x deq(W)^T + bias + (alpha/r) (x A) B, one fused pass.
 
-    x: [..., K] bf16. Returns y [..., N] (and h when save_h)."""
+    x: [..., K] bfloat16 or float16 (the dtype of A and B). Returns y [..., N] (and h when
+    save_h)."""
     N, K = layer.weight.shape
     xf, lead = _flatten(x, K)
     active_bias = layer.base_bias if (layer.train_bias and not layer.enabled) else layer.bias
@@ -336,20 +359,23 @@ class I8LoRALinearFunction(torch.autograd.Function):
 
 
 def gelu_tanh(x: torch.Tensor) -> torch.Tensor:
-    """gelu_tanh (linear.jl:61-68), bf16 in and out, f32 math."""
-    x = _contig(x, torch.bfloat16, "x")
+    """gelu_tanh (linear.jl:61-68), bfloat16 or float16 in and out, f32 math."""
+    dt = _act_dtype(x, "x")
+    x = x.contiguous()
     y = torch.empty_like(x)
-    _lib.check("reels_hip_gelu_tanh", _lib.lib().reels_hip_gelu_tanh(
-        _ptr(x), _ptr(y), x.numel(), _stream(x.device)))
+    fn = "reels_hip_gelu_tanh" + _ACT_SUFFIX[dt]
+    _lib.check(fn, getattr(_lib.lib(), fn)(_ptr(x), _ptr(y), x.numel(), _stream(x.device)))
     return y
 
 
 def gelu_tanh_backward(x: torch.Tensor, dy: torch.Tensor) -> torch.Tensor:
-    x = _contig(x, torch.bfloat16, "x")
-    dy = _contig(dy, torch.bfloat16, "dy")
+    dt = _act_dtype(x, "x")
+    x = x.contiguous()
+    dy = _contig(dy, dt, "dy")
     dx = torch.empty_like(x)
-    _lib.check("reels_hip_gelu_tanh_bwd", _lib.lib().reels_hip_gelu_tanh_bwd(
-        _ptr(x), _ptr(dy), _ptr(dx), x.numel(), _stream(x.device)))
+    fn = "reels_hip_gelu_tanh_bwd" + _ACT_SUFFIX[dt]
+    _lib.check(fn, getattr(_lib.lib(), fn)(_ptr(x), _ptr(dy), _ptr(dx), x.numel(),
+                                           _stream(x.device)))
     return dx
 
 
@@ -368,10 +394,10 @@ def frozen_weight_transfer(device: str, precision: str, quantization: str = "non
                            cpu_offload: bool = False) -> FrozenWeightTransfer:
     """frozen_weight_transfer (quantization.jl:88-101).
 
-    The reference rejects int8 with bf16 compute because its backward runs through an fp32
-    shadow model; here bf16 is the compute precision of the HIP kernels, so the combination is
-    accepted on the ROCm device. fp16 / fp32 compute with int8 is not implemented by these
-    kernels and raises."""
+    int8 with fp16 compute is the reference's own low-VRAM mode and runs on the f16 kernels. The
+    reference rejects int8 with bf16 compute because its backward runs through an fp32 shadow
+    model; here bf16 is a compute precision of the HIP kernels, so that combination is accepted
+    on the ROCm device too. fp32 compute with int8 has no kernels here and raises."""
     if quantization not in ("none", "int8"):
         raise ValueError("frozen weight quantization must be none or int8")
     if device not in ("cpu", "cuda", "hip"):
@@ -383,20 +409,21 @@ def frozen_weight_transfer(device: str, precision: str, quantization: str = "non
     if quantization == "int8":
         if device == "cpu":
             raise ValueError("the int8 HIP path runs on the GPU only")
-        if precision != "bf16":
-            raise NotImplementedError("int8 frozen weights run with bf16 compute on MI355X; "
-                                      f"{precision} compute is not implemented")
+        if precision not in ("bf16", "fp16"):
+            raise NotImplementedError("int8 frozen weights run with bf16 or fp16 compute on "
+                                      f"MI355X; {precision} compute is not implemented")
     return FrozenWeightTransfer(device, precision, quantization, cpu_offload)
 
 
 def move_weight(weight, transfer: FrozenWeightTransfer):
     """_move_weight (quantization.jl:111-144): quantize a frozen matrix on the device; an existing
     QuantizedMatrix is kept as is (re-moving keeps identical codes)."""
+    compute = torch.float16 if transfer.precision == "fp16" else torch.bfloat16
     if isinstance(weight, QuantizedMatrix):
         if transfer.quantization == "int8":
             return weight
-        return weight.dequantize(torch.bfloat16)
+        return weight.dequantize(compute)
     if transfer.quantization == "int8":
         w = weight if weight.is_cuda else weight.to("cuda")
-        return quantize_frozen_matrix(w, torch.bfloat16)
+        return quantize_frozen_matrix(w, compute)
     return weight.to("cuda" if transfer.device != "cpu" else "cpu")

@@ -82,6 +82,14 @@ def test_argument_errors_before_any_gpu_work():
                                   fake, None, None, None, 0, None) == -3
     assert L.reels_hip_i8lora_bwd(None, fake, None, fake, fake, fake, fake, 8, 16, 16, 16, 1.0,
                                   fake, None, None, fake, 1 << 20, None) == -1
+    # the f16 entry points validate the same way and name themselves in the message
+    assert L.reels_hip_i8lora_fwd_f16(fake, fake, fake, None, None, None, 8, 16, 16, 0, 1.0, fake,
+                                      None, None, 0, None) == -3
+    assert "reels_hip_i8lora_fwd_f16" in _err()
+    assert L.reels_hip_i8lora_bwd_f16(None, fake, None, fake, fake, fake, fake, 8, 16, 16, 16, 1.0,
+                                      fake, None, None, fake, 1 << 20, None) == -1
+    assert "reels_hip_i8lora_bwd_f16" in _err()
+    assert L.reels_hip_gelu_tanh_f16(None, None, -1, None) == -1
     # a successful-looking call clears the message of the previous failure
     assert L.reels_hip_gelu_tanh(None, None, 0, None) == 0
     assert _err() == ""
@@ -104,8 +112,10 @@ def test_frozen_weight_transfer_policy():
         frozen_weight_transfer("cpu", "fp32", cpu_offload=True)
     with pytest.raises(ValueError):
         frozen_weight_transfer("cpu", "fp32", quantization="int8")
+    # fp16 with int8 is the reference's own low-VRAM mode (quantization.jl:96-98 accepts it)
+    assert frozen_weight_transfer("hip", "fp16", quantization="int8").precision == "fp16"
     with pytest.raises(NotImplementedError):
-        frozen_weight_transfer("hip", "fp16", quantization="int8")
+        frozen_weight_transfer("hip", "fp32", quantization="int8")
     assert frozen_weight_transfer("cpu", "fp32").quantization == "none"
 
 

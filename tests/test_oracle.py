@@ -315,3 +315,76 @@ def test_reference_fp16_path_is_close_but_not_exact():
     y16 = oracle.reference_fp16_forward(x, q, s, A, B, 1.0)
     rel = np.abs(y16 - y).max() / np.abs(y).max()
     assert 1e-6 < rel < 1e-2
+
+
+# ---- the fp16 element path (the reference's Float16 compute) -----------------------------------
+def h16(a):
+    """IEEE binary16 patterns of the values a (numpy's rounding)."""
+    return np.asarray(a, np.float32).astype(np.float16).view(np.uint16)
+
+
+def test_f16_decode_exhaustive_against_numpy():
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = oracle.f16_to_f32(bits)
+    want = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))  # -0 kept
+
+
+def test_f16_rounding_against_numpy():
+    rng = np.random.default_rng(61)
+    vals = np.concatenate([
+        rng.standard_normal(200000).astype(np.float32) * np.float32(3),
+        (rng.standard_normal(100000) * 1e-5).astype(np.float32),          # subnormal range
+        (rng.standard_normal(50000) * 3e4).astype(np.float32),            # near the top
+        np.array([65504, 65519.99, 65520, -65520, 2 ** -24, 2 ** -25, 3 * 2 ** -26, 2 ** -14,
+                  2 ** -14 - 2 ** -25, 1 + 2 ** -11, 1 + 3 * 2 ** -11, 0.0, -0.0], np.float32)])
+    # exact halfway cases between adjacent binary16 values: ties to even
+    base = rng.integers(0, 0x7bff, size=20000).astype(np.uint16)
+    lo = base.view(np.float16).astype(np.float64)
+    hi = (base + 1).view(np.float16).astype(np.float64)
+    vals = np.concatenate([vals, ((lo + hi) / 2).astype(np.float32)])
+    assert np.array_equal(oracle.f32_to_f16(vals), vals.astype(np.float16).view(np.uint16))
+
+
+def test_f16_forward_backward_equal_bf16_path_on_shared_values():
+    # small integers are exact in both formats: the two element paths must give the same f64
+    x, q, s, A, B, bias = _small_int_case(seed=7)
+    dy = np.random.default_rng(8).integers(-3, 4, size=(x.shape[0], q.shape[0])).astype(F32)
+    c = 0.75
+    yb, hb = oracle.lora_forward(bf(x), q, s, bf(A), bf(B), c, bias=bf(bias))
+    yh, hh = oracle.lora_forward(h16(x), q, s, h16(A), h16(B), c, bias=h16(bias), elt="f16")
+    assert np.array_equal(yb, yh) and np.array_equal(hb, hh)
+    gb = oracle.lora_backward(bf(dy), bf(x), q, s, bf(A), bf(B), c)
+    gh = oracle.lora_backward(h16(dy), h16(x), q, s, h16(A), h16(B), c, elt="f16")
+    for k in ("dx", "dA", "dB"):
+        assert np.array_equal(gb[k], gh[k]), k
+
+
+def test_f16_forward_uses_the_binary16_values():
+    # values with more than 8 significant bits: the f16 decode is exact where bf16 would round
+    x = np.array([[1 + 2 ** -10, -3 - 2 ** -9]], np.float32)
+    q = np.array([[1, 1]], np.int8)
+    s = np.array([1.0], np.float32)
+    y, _ = oracle.lora_forward(h16(x), q, s, None, None, 0.0, elt="f16")
+    assert y[0, 0] == (1 + 2 ** -10) + (-3 - 2 ** -9)
+
+
+def test_f16_gelu_closed_forms():
+    xs = np.array([0.0, 1.0, -1.0, 3.0, -3.0, 0.5, 8.0, -8.0], F32)
+    y = oracle.f16_to_f32(oracle.gelu_tanh(h16(xs), elt="f16")).astype(np.float64)
+    assert y[0] == 0.0
+    k = np.sqrt(2 / np.pi)
+    xb = xs.astype(np.float64)
+    ref = 0.5 * xb * (1 + np.tanh(k * (xb + 0.044715 * xb ** 3)))
+    assert np.allclose(y, ref, rtol=2 ** -10, atol=1e-6)
+    for i, j in [(1, 2), (3, 4)]:
+        assert np.isclose(y[i] - y[j], xb[i], rtol=2 ** -9)
+    grid = np.linspace(-4, 4, 81).astype(F32)
+    d = oracle.f16_to_f32(oracle.gelu_tanh_backward(h16(grid), h16(np.ones_like(grid)),
+                                                    elt="f16")).astype(np.float64)
+    gx = grid.astype(np.float16).astype(np.float64)
+    f = lambda v: 0.5 * v * (1 + np.tanh(k * (v + 0.044715 * v ** 3)))
+    fd = (f(gx + 1e-5) - f(gx - 1e-5)) / 2e-5
+    assert np.allclose(d, fd, rtol=2 ** -10, atol=2 ** -12)
