@@ -61,6 +61,11 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="approximate CPU work for the cpu_baseline sample (0 disables it)")
     ap.add_argument("--tokens", type=int, default=TOKENS)
+    ap.add_argument("--offload", choices=("none", "stream", "sync"), default="none",
+                    help="cpu_offload: int8 codes and scales in pinned host memory, streamed to the "
+                         "GPU one projection ahead of use on a copy stream (stream: WeightStreamer, "
+                         "two slots) or copied right before each use (sync: the reference's "
+                         "per-call upload)")
     ap.add_argument("--dtype", choices=("bf16", "f16"), default="bf16",
                     help="activation / LoRA element type: bf16 (the default workload) or f16 "
                          "(the reference's own int8 compute precision, the _f16 entry points)")
@@ -238,12 +243,31 @@ class Projection:
                          p(self.wsb), self.wsb_n, st)
 
 
-def run_step(L, projs, check, sfx=""):
+def run_step(L, projs, check, sfx="", streamer=None):
     fwd, bwd = getattr(L, "reels_hip_i8lora_fwd" + sfx), getattr(L, "reels_hip_i8lora_bwd" + sfx)
-    for pr in projs:
-        check("reels_hip_i8lora_fwd" + sfx, fwd(*pr.fwd_args))
-    for pr in reversed(projs):
-        check("reels_hip_i8lora_bwd" + sfx, bwd(*pr.bwd_args))
+    if streamer is None:
+        for pr in projs:
+            check("reels_hip_i8lora_fwd" + sfx, fwd(*pr.fwd_args))
+        for pr in reversed(projs):
+            check("reels_hip_i8lora_bwd" + sfx, bwd(*pr.bwd_args))
+        return
+    # offloaded weights: each projection's codes arrive in a device slot while the previous
+    # projection computes; the call takes the slot's pointers
+    from reels_amd.offload import run_streamed
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+
+    def f(i, W):
+        a = list(projs[i].fwd_args); a[1], a[2] = p(W.values), p(W.scales)
+        check("reels_hip_i8lora_fwd" + sfx, fwd(*a))
+
+    rev = list(reversed(projs))
+
+    def b(i, W):
+        a = list(rev[i].bwd_args); a[3], a[4] = p(W.values), p(W.scales)
+        check("reels_hip_i8lora_bwd" + sfx, bwd(*a))
+
+    run_streamed([pr.Wh for pr in projs], f, streamer)
+    run_streamed([pr.Wh for pr in rev], b, streamer)
 
 
 def cpu_baseline(seconds):
@@ -297,25 +321,47 @@ def main():
     act = torch.float16 if args.dtype == "f16" else torch.bfloat16
     sfx = "_f16" if args.dtype == "f16" else ""
     projs = [Projection(n, K, N, M, RANK, dev, gen, act) for (n, K, N) in PROJECTIONS]
+    streamer = None
+    if args.offload != "none":
+        from reels_amd.offload import PerCallUploader, WeightStreamer, offload_weight
+        for pr in projs:
+            pr.Wh = offload_weight(pr.W)
+            pr.W = None
+        torch.cuda.empty_cache()
+        streamer = WeightStreamer(dev, slots=2) if args.offload == "stream" else PerCallUploader(dev)
     torch.cuda.synchronize()
 
     for _ in range(args.warmup):
-        run_step(L, projs, _lib.check, sfx)
+        run_step(L, projs, _lib.check, sfx, streamer)
     torch.cuda.synchronize()
 
     # count one step's launches (an untimed traced step) to size the trace buffer exactly
     _lib.check("reels_hip_trace_start", L.reels_hip_trace_start(4096))
-    run_step(L, projs, _lib.check, sfx)
+    run_step(L, projs, _lib.check, sfx, streamer)
     torch.cuda.synchronize()
     launches_per_step = len(_lib.trace_records())
     _lib.check("reels_hip_trace_start", L.reels_hip_trace_start(launches_per_step * args.steps))
     torch.cuda.synchronize()
+    up0 = streamer.uploads if streamer else 0
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        run_step(L, projs, _lib.check, sfx)
+        run_step(L, projs, _lib.check, sfx, streamer)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     recs = _lib.trace_records()
+    offload = None
+    if streamer is not None:
+        ups = (streamer.uploads - up0) / args.steps
+        per = {id(pr.Wh): pr.Wh.values.numel() + 4 * pr.Wh.scales.numel() for pr in projs}
+        nbytes = sum(per.values()) * ups / len(projs)  # mean bytes per upload x uploads
+        step_s = (t1 - t0) / args.steps
+        offload = {"what": ("int8 codes + f32 scales in pinned host memory, uploaded one "
+                            "projection ahead on a copy stream (WeightStreamer, 2 slots)")
+                           if args.offload == "stream" else
+                           ("int8 codes + f32 scales in pinned host memory, copied on the compute "
+                            "stream right before each use (per-call upload, no overlap)"),
+                   "uploads_per_step": ups, "h2d_bytes_per_step": int(nbytes),
+                   "h2d_gbs_over_step": round(nbytes / step_s / 1e9, 2)}
 
     ms_per_step = (t1 - t0) * 1e3 / args.steps
     step_flops = sum(linear_flops(M, K, N, RANK) for (_, K, N) in PROJECTIONS)
@@ -381,7 +427,11 @@ def main():
         "config": {"workload": "wan2.1-14b block projections: self_attn q/k/v/o 5120->5120, "
                                "ffn 5120->13824->5120; int8 per-channel frozen weights; LoRA "
                                "r=32 alpha=32; forward + dX + dA + dB",
-                   "tokens": M, "rank": RANK, "flops_per_step": step_flops},
+                   "tokens": M, "rank": RANK, "flops_per_step": step_flops,
+                   "weights": {"none": "resident in HBM", "stream": "cpu_offload (pinned host, "
+                               "streamed)", "sync": "cpu_offload (pinned host, per-call upload)"}
+                              [args.offload]},
+        "offload": offload,
         "frac_of_bf16_peak": round(value / PEAK_BF16_TFLOPS, 4),
         "roofline": roofline,
         "cpu_baseline": cpu,

@@ -135,6 +135,15 @@ def workspace_bytes(M: int, K: int, N: int, r: int, which: int) -> int:
     return int(_lib.lib().reels_hip_i8lora_workspace_bytes(M, K, N, r, which))
 
 
+def _on_device(weight: QuantizedMatrix, device) -> QuantizedMatrix:
+    """An offloaded weight (codes in host memory, cpu_offload) is copied to the device for this
+    call, as the reference's _materialize_weight does (quantization.jl:46-59)."""
+    if weight.values.is_cuda:
+        return weight
+    from .offload import upload
+    return upload(weight, device)
+
+
 def i8lora_forward(x, weight: QuantizedMatrix, A=None, B=None, bias=None, lora_scale=1.0,
                    save_h: bool = False):
     """y = rnd(x deq(Wq)^T + lora_scale * rnd(x A) B + bias); returns (y, h or None).
@@ -143,6 +152,7 @@ def i8lora_forward(x, weight: QuantizedMatrix, A=None, B=None, bias=None, lora_s
     bias [N] of the same dtype (Julia A::(r,K), B::(N,r)); y and h come back in that dtype."""
     dt = _act_dtype(x, "x")
     x = x.contiguous()
+    weight = _on_device(weight, x.device)
     M, K = x.shape
     N, Kw = weight.values.shape
     if Kw != K:
@@ -172,6 +182,7 @@ def i8lora_backward(dy, x, weight: QuantizedMatrix, A=None, B=None, lora_scale=1
     back in it."""
     dt = _act_dtype(dy, "dy")
     dy = dy.contiguous()
+    weight = _on_device(weight, dy.device)
     M, N = dy.shape
     Nw, K = weight.values.shape
     if Nw != N:
@@ -404,8 +415,9 @@ def frozen_weight_transfer(device: str, precision: str, quantization: str = "non
         raise ValueError("device must be cpu, cuda or hip")
     if cpu_offload and device == "cpu":
         raise ValueError("CPU weight offloading requires a GPU device")
-    if cpu_offload:
-        raise NotImplementedError("cpu_offload streaming is not part of the int8 HIP path")
+    if cpu_offload and quantization != "int8":
+        raise NotImplementedError("cpu_offload of dense (unquantized) weights is not part of the "
+                                  "int8 HIP path")
     if quantization == "int8":
         if device == "cpu":
             raise ValueError("the int8 HIP path runs on the GPU only")
@@ -421,9 +433,16 @@ def move_weight(weight, transfer: FrozenWeightTransfer):
     compute = torch.float16 if transfer.precision == "fp16" else torch.bfloat16
     if isinstance(weight, QuantizedMatrix):
         if transfer.quantization == "int8":
+            if transfer.cpu_offload and weight.values.is_cuda:
+                from .offload import offload_weight
+                return offload_weight(weight)
             return weight
         return weight.dequantize(compute)
     if transfer.quantization == "int8":
         w = weight if weight.is_cuda else weight.to("cuda")
-        return quantize_frozen_matrix(w, compute)
+        qm = quantize_frozen_matrix(w, compute)
+        if transfer.cpu_offload:  # codes and scales stay in pinned host memory (lines 117-119)
+            from .offload import offload_weight
+            return offload_weight(qm)
+        return qm
     return weight.to("cuda" if transfer.device != "cpu" else "cpu")

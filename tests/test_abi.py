@@ -110,6 +110,10 @@ def test_frozen_weight_transfer_policy():
         frozen_weight_transfer("hip", "bf16", quantization="int4")
     with pytest.raises(ValueError):
         frozen_weight_transfer("cpu", "fp32", cpu_offload=True)
+    # int8 codes kept in pinned host memory, uploaded per use (quantization.jl:111-144)
+    assert frozen_weight_transfer("hip", "bf16", quantization="int8", cpu_offload=True).cpu_offload
+    with pytest.raises(NotImplementedError):
+        frozen_weight_transfer("hip", "fp16", cpu_offload=True)  # dense offload: not this path
     with pytest.raises(ValueError):
         frozen_weight_transfer("cpu", "fp32", quantization="int8")
     # fp16 with int8 is the reference's own low-VRAM mode (quantization.jl:96-98 accepts it)
