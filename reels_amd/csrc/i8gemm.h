@@ -23,8 +23,8 @@ int launch_i8gemm(int mode, int elt, const GemmArgs& a, hipStream_t st);
 
 // 16-bit GEMM with the LoRA epilogue: out = rnd(act wd^T + c L R^T + bias), wd [Ncols][Kred] (a
 // dequantized weight) of element type elt like every other operand; a.q and a.colscale are
-// unused. Needs Kred % 64 == 0, 16-byte aligned operands and byte sizes below 2^31
-// (bfgemm_supported).
+// unused. Needs Kred % 64 == 0, 16-byte aligned operands and a weight below 2^31 bytes
+// (bfgemm_supported); any token count (split into chunks of activations below 2^31 bytes).
 bool bfgemm_supported(int64_t M, int64_t Ncols, int64_t Kred);
 // mode only labels the trace record ("bfgemm_kernel<0>" forward, "<1>" dX)
 int launch_bfgemm(int mode, int elt, const GemmArgs& a, const uint16_t* wd, hipStream_t st);

@@ -772,8 +772,8 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
 }
 
 bool bfgemm_supported(int64_t M, int64_t Ncols, int64_t Kred) {
-  return Kred % bfg::BK == 0 && Ncols % 16 == 0 && M * Kred * 2 < ((int64_t)1 << 31) &&
-         Ncols * Kred * 2 < ((int64_t)1 << 31);
+  (void)M;  // any token count: launch_bfgemm splits the tokens into chunks (below)
+  return Kred % bfg::BK == 0 && Ncols % 16 == 0 && Ncols * Kred * 2 < ((int64_t)1 << 31);
 }
 
 int launch_bfgemm(int mode, int elt, const GemmArgs& a, const uint16_t* wd, hipStream_t st) {
@@ -788,12 +788,24 @@ int launch_bfgemm(int mode, int elt, const GemmArgs& a, const uint16_t* wd, hipS
   });
   if (attr_err != hipSuccess)
     return fail(REELS_HIP_EHIP, std::string("bfgemm: hipFuncSetAttribute: ") + hipGetErrorString(attr_err));
-  const int tn = (int)ceil_div(a.Ncols, bfg::BN), tm = (int)ceil_div(a.M, bfg::BM);
-  { TraceScope _ts(st, mode == 0 ? "bfgemm_kernel<0>" : "bfgemm_kernel<1>");
-    with_elt(elt, [&](auto e) {
-      bfgemm_kernel<decltype(e)::value><<<tn * tm, bfg::NT, 2 * bfg::STAGE, st>>>(a, wd, tn, tm);
-    }); }
-  return check_launch("bfgemm_kernel");
+  // The activation copies address their buffer with 32-bit offsets: token counts whose
+  // activations reach 2 GiB run as consecutive launches over token chunks (multiples of the
+  // 256-token tile) with the activation, output and L pointers advanced.
+  const int64_t chunk = ((((int64_t)1 << 31) - 1) / (a.Kred * 2)) / bfg::BM * bfg::BM;
+  for (int64_t m0 = 0; m0 < a.M; m0 += chunk) {
+    GemmArgs c = a;
+    c.M = (a.M - m0 < chunk) ? a.M - m0 : chunk;
+    c.act = a.act + m0 * a.Kred;
+    c.out = a.out + m0 * a.Ncols;
+    if (a.L) c.L = a.L + m0 * a.rp;
+    const int tn = (int)ceil_div(c.Ncols, bfg::BN), tm = (int)ceil_div(c.M, bfg::BM);
+    { TraceScope _ts(st, mode == 0 ? "bfgemm_kernel<0>" : "bfgemm_kernel<1>");
+      with_elt(elt, [&](auto e) {
+        bfgemm_kernel<decltype(e)::value><<<tn * tm, bfg::NT, 2 * bfg::STAGE, st>>>(c, wd, tn, tm);
+      }); }
+    if (int rc = check_launch("bfgemm_kernel")) return rc;
+  }
+  return REELS_HIP_OK;
 }
 
 int launch_i8gemm(int mode, int elt, const GemmArgs& a, hipStream_t st) {

@@ -198,3 +198,35 @@ def test_gelu_tanh(dev, n):
     assert np.mean(y == yo) > 0.99
     assert np.all(np.abs(dx - dxo) <= 2.0 ** -6 * np.abs(dxo) + 2.0 ** -12 * np.abs(dxo).max())
     assert np.mean(dx == dxo) > 0.95
+
+
+@pytest.mark.parametrize("K,N", [(8960, 1536), (1536, 8960)])
+def test_tokens_beyond_2gib_of_activations(dev, K, N):
+    # 120000 tokens x 8960 bf16 is 2.15 GB: the GEMM whose reduction is 8960 wide (forward for
+    # 8960->1536, dX for 1536->8960) runs as two token chunks (119808 + 192 tokens). y and dx
+    # are row-independent, so rows on both sides of the chunk boundary are checked against the
+    # oracle run on just those rows.
+    import torch
+    from reels_amd import QuantizedMatrix, i8lora_backward, i8lora_forward
+    from tests._util import bf16_bits
+    M, r = 120000, 32
+    print(f"[lora] chunked tokens M={M} K={K} N={N}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(K + N)
+    x = torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16)
+    dy = torch.randn((M, N), generator=g, device=dev).to(torch.bfloat16)
+    w = oracle.normal_bf16(K + N, (N, K), 0.02)
+    q, s, _ = oracle.pack(w, "bf16")
+    A = oracle.normal_bf16(K + N + 1, (K, r), 0.01)
+    B = oracle.normal_bf16(K + N + 2, (r, N), 0.01)
+    W = QuantizedMatrix(to_dev(q, dev, "raw"), to_dev(s, dev, "raw"))
+    Ad, Bd = to_dev(A, dev), to_dev(B, dev)
+    y, h = i8lora_forward(x, W, Ad, Bd, None, 1.0, save_h=True)
+    dx, _, _ = i8lora_backward(dy, x, W, Ad, Bd, 1.0, h=h, want_dA=False, want_dB=False)
+    torch.cuda.synchronize(dev)
+    rows = np.array([0, 1, 119806, 119807, 119808, 119809, 119999])
+    rt = torch.from_numpy(rows).to(dev)
+    xr, dyr = bf16_bits(x[rt]), bf16_bits(dy[rt])
+    yo, _ = oracle.lora_forward(xr, q, s, A, B, 1.0)
+    dxo = oracle.lora_backward(dyr, xr, q, s, A, B, 1.0, want=("dx",))["dx"]
+    assert_parity(bf16_f32(y[rt]), yo, f"chunked {K}->{N} y (rows across the chunk boundary)")
+    assert_parity(bf16_f32(dx[rt]), dxo, f"chunked {K}->{N} dx (rows across the chunk boundary)")
