@@ -558,7 +558,7 @@ namespace bfg {
 constexpr int BM = 256, BN = 256, BK = 64, NT = 512;
 constexpr int ACT = BM * BK * 2;   // 32 KiB
 constexpr int WB = BN * BK * 2;    // 32 KiB
-constexpr int STAGE = ACT + WB;    // 64 KiB
+constexpr int LDS = 3 * ACT + 2 * WB;  // 160 KiB: activation ring of 3 stages, weight ring of 2
 constexpr int GM = 4;
 }  // namespace bfg
 
@@ -609,19 +609,15 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
   }
   const i32x4 rnone = buffer_rsrc(a.act, 0u);  // zero records: a copy through it reads nothing
   const int nk = (int)(Kred / BK);
-  auto issue = [&](int kt, int stage) {
-    uint8_t* base = smem + stage * STAGE;
-    const uint32_t so = (uint32_t)kt * (BK * 2);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) dma16(ract, voa[i], so, base + (w * 4 + i) * 1024);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) dma16(rw, vow[i], so, base + ACT + (w * 4 + i) * 1024);
+  // LDS: activation ring of 3 stages [0, 96 KiB), weight ring of 2 stages [96, 160 KiB); step kt
+  // uses activation stage kt % 3 and weight stage kt % 2
+  auto abase = [&](int kt) { return smem + (kt % 3) * ACT; };
+  auto wbase = [&](int kt) { return smem + 3 * ACT + (kt & 1) * WB; };
+  auto issue_act = [&](int kt, const i32x4& ra, int i) {
+    dma16(ra, voa[i], (uint32_t)kt * (BK * 2), abase(kt) + (w * 4 + i) * 1024);
   };
-  auto issue_one = [&](int kt, int stage, int i, const i32x4& ra, const i32x4& rb) {
-    uint8_t* base = smem + stage * STAGE;
-    const uint32_t so = (uint32_t)kt * (BK * 2);
-    if (i < 4) dma16(ra, voa[i], so, base + (w * 4 + i) * 1024);
-    else dma16(rb, vow[i - 4], so, base + ACT + (w * 4 + i - 4) * 1024);
+  auto issue_w = [&](int kt, const i32x4& rb, int i) {
+    dma16(rb, vow[i], (uint32_t)kt * (BK * 2), wbase(kt) + (w * 4 + i) * 1024);
   };
 
   f32x4 acc[4][8];  // [output-column tile][token tile]
@@ -635,7 +631,7 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
   // fragment reads: sub-step s of a step uses the 16-byte chunk 4 s + l / 16 of each row; rows of
   // a 16-row tile start at multiples of 16, so the row swizzle depends on the lane only
   const int swz = bf_swz(l16);
-  auto read_w = [&](const uint8_t* sw, int s, V8* wf) {
+  auto read_w = [&](const uint8_t* sw, int s, V8* wf) {  // sw: a weight stage
     const int off = ((4 * s + lq) ^ swz) << 4;
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti)
@@ -666,44 +662,64 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  issue(0, 0);
-  if (nk > 1) issue(1, 1);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) { issue_act(0, ract, i); issue_w(0, rw, i); }
+  if (nk > 1) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { issue_act(1, ract, i); issue_w(1, rw, i); }
+  }
   if (nk > 1) __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8): step 1 may stay in flight
   else __builtin_amdgcn_s_waitcnt(0x0F70);
   __builtin_amdgcn_s_barrier();
   // no scalar loads pending at the loop entry, so the waits at its head count LDS reads only
   __builtin_amdgcn_s_waitcnt(0xC07F);
   __builtin_amdgcn_sched_barrier(0);
-  read_w(smem + ACT, 0, w0);
+  read_w(wbase(0), 0, w0);
 #pragma unroll
-  for (int tj = 0; tj < 8; ++tj) x[tj] = read_x(smem, 0, tj);
-  // Steps 0 .. nk-2 (the last one is peeled): sub-step 0, then the barrier that ends the reads of
-  // stage kt, then sub-step 1 with the next stage's sub-step-0 reads and the eight copies of step
-  // kt+2 (one per four MFMAs) into stage kt. Past the end the copies go through a zero-record
-  // descriptor: they move no memory and write zeros into a stage no wave reads any more.
+  for (int tj = 0; tj < 8; ++tj) x[tj] = read_x(abase(0), 0, tj);
+  // Steps 0 .. nk-2 (the last one is peeled). Step kt:
+  // - sub-step 0 reads sub-step 1's fragments and issues the activation copies of step kt+2 (one
+  //   per eight MFMAs) into the activation stage of step kt-1, free since the barrier of step kt-1;
+  // - the barrier: step kt+1 has landed, the four newer activation copies may stay in flight;
+  // - sub-step 1 reads step kt+1's sub-step-0 fragments and issues the weight copies of step kt+2
+  //   into the weight stage of step kt, free since this barrier.
+  // The L2-to-LDS path moves about 64 bytes per clock per CU; eight copies in one sub-step stall
+  // their issue, four per sub-step do not. Past the end the copies go through a zero-record
+  // descriptor: they move no memory and write zeros into stages no wave reads any more.
   for (int kt = 0; kt + 1 < nk; ++kt) {
-    sub0(smem + (kt & 1) * STAGE);
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave is done reading stage kt
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): step kt+1 has landed
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
     const bool pre = kt + 2 < nk;
     const i32x4 ra = pre ? ract : rnone, rb = pre ? rw : rnone;
-    const uint8_t* sn = smem + ((kt + 1) & 1) * STAGE;
-    read_w(sn + ACT, 0, w0);
+    const uint8_t* sa = abase(kt);
+    const uint8_t* sw = wbase(kt);
+#pragma unroll
+    for (int tj = 0; tj < 8; ++tj) {
+      mfma4(w0, x[tj], tj);
+      __builtin_amdgcn_sched_barrier(0);
+      x[tj] = read_x(sa, 1, tj);
+      if (tj == 0) read_w(sw, 1, w1);
+      if (tj & 1) issue_act(kt + 2, ra, tj >> 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave is done reading step kt
+    __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4): step kt+1 has landed
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    const uint8_t* san = abase(kt + 1);
+    const uint8_t* swn = wbase(kt + 1);
+    read_w(swn, 0, w0);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int tj = 0; tj < 8; ++tj) {
       mfma4(w1, x[tj], tj);
       __builtin_amdgcn_sched_barrier(0);
-      x[tj] = read_x(sn, 0, tj);
-      issue_one(kt + 2, kt & 1, tj, ra, rb);
+      x[tj] = read_x(san, 0, tj);
+      if (tj & 1) issue_w(kt + 2, rb, tj >> 1);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
   {
-    const uint8_t* sa = smem + ((nk - 1) & 1) * STAGE;
-    read_w(sa + ACT, 1, w1);
+    const uint8_t* sa = abase(nk - 1);
+    read_w(wbase(nk - 1), 1, w1);
 #pragma unroll
     for (int tj = 0; tj < 8; ++tj) {
       mfma4(w0, x[tj], tj);
@@ -782,9 +798,9 @@ int launch_bfgemm(int mode, int elt, const GemmArgs& a, const uint16_t* wd, hipS
   static std::once_flag once;
   static hipError_t attr_err = hipSuccess;
   std::call_once(once, [&] {
-    attr_err = hipFuncSetAttribute((const void*)bfgemm_kernel<REELS_HIP_BF16>, hipFuncAttributeMaxDynamicSharedMemorySize, 2 * bfg::STAGE);
+    attr_err = hipFuncSetAttribute((const void*)bfgemm_kernel<REELS_HIP_BF16>, hipFuncAttributeMaxDynamicSharedMemorySize, bfg::LDS);
     if (attr_err == hipSuccess)
-      attr_err = hipFuncSetAttribute((const void*)bfgemm_kernel<REELS_HIP_F16>, hipFuncAttributeMaxDynamicSharedMemorySize, 2 * bfg::STAGE);
+      attr_err = hipFuncSetAttribute((const void*)bfgemm_kernel<REELS_HIP_F16>, hipFuncAttributeMaxDynamicSharedMemorySize, bfg::LDS);
   });
   if (attr_err != hipSuccess)
     return fail(REELS_HIP_EHIP, std::string("bfgemm: hipFuncSetAttribute: ") + hipGetErrorString(attr_err));
@@ -801,7 +817,7 @@ int launch_bfgemm(int mode, int elt, const GemmArgs& a, const uint16_t* wd, hipS
     const int tn = (int)ceil_div(c.Ncols, bfg::BN), tm = (int)ceil_div(c.M, bfg::BM);
     { TraceScope _ts(st, mode == 0 ? "bfgemm_kernel<0>" : "bfgemm_kernel<1>");
       with_elt(elt, [&](auto e) {
-        bfgemm_kernel<decltype(e)::value><<<tn * tm, bfg::NT, 2 * bfg::STAGE, st>>>(c, wd, tn, tm);
+        bfgemm_kernel<decltype(e)::value><<<tn * tm, bfg::NT, bfg::LDS, st>>>(c, wd, tn, tm);
       }); }
     if (int rc = check_launch("bfgemm_kernel")) return rc;
   }
