@@ -686,7 +686,14 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
   // The L2-to-LDS path moves about 64 bytes per clock per CU; eight copies in one sub-step stall
   // their issue, four per sub-step do not. Past the end the copies go through a zero-record
   // descriptor: they move no memory and write zeros into stages no wave reads any more.
+  //
+  // Waves w and w + 4 share a SIMD. With equal priorities the older one (w < 4) wins every MFMA
+  // issue slot it wants, runs a whole sub-step ahead, and the younger one then finishes its
+  // sub-step 0 alone, where one wave keeps the pipe only about three quarters busy. The younger
+  // wave therefore takes the higher priority for sub-step 1 and gives it up for sub-step 0, so
+  // both reach the barrier together.
   for (int kt = 0; kt + 1 < nk; ++kt) {
+    if (w >= 4) __builtin_amdgcn_s_setprio(0);
     const bool pre = kt + 2 < nk;
     const i32x4 ra = pre ? ract : rnone, rb = pre ? rw : rnone;
     const uint8_t* sa = abase(kt);
@@ -700,9 +707,14 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
       if (tj & 1) issue_act(kt + 2, ra, tj >> 1);
       __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave is done reading step kt
+    // lgkmcnt(7): the weight fragments of this step have been read (the weight copies issued
+    // after the barrier overwrite their stage). The seven activation reads issued after them may
+    // still be queued at the LDS, which serves requests in order: the activation copies into that
+    // stage are issued a full sub-step after the barrier and land a memory latency later.
+    __builtin_amdgcn_s_waitcnt(0xC77F);
     __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4): step kt+1 has landed
     __builtin_amdgcn_s_barrier();
+    if (w >= 4) __builtin_amdgcn_s_setprio(1);
     __builtin_amdgcn_sched_barrier(0);
     const uint8_t* san = abase(kt + 1);
     const uint8_t* swn = wbase(kt + 1);
@@ -717,6 +729,7 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
       __builtin_amdgcn_sched_barrier(0);
     }
   }
+  if (w >= 4) __builtin_amdgcn_s_setprio(0);
   {
     const uint8_t* sa = abase(nk - 1);
     read_w(wbase(nk - 1), 1, w1);
