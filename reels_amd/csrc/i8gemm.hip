@@ -613,11 +613,29 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
   // uses activation stage kt % 3 and weight stage kt % 2
   auto abase = [&](int kt) { return smem + (kt % 3) * ACT; };
   auto wbase = [&](int kt) { return smem + 3 * ACT + (kt & 1) * WB; };
-  auto issue_act = [&](int kt, const i32x4& ra, int i) {
-    dma16(ra, voa[i], (uint32_t)kt * (BK * 2), abase(kt) + (w * 4 + i) * 1024);
+  auto issue_act = [&](int kt, int i) {
+    dma16(ract, voa[i], (uint32_t)kt * (BK * 2), abase(kt) + (w * 4 + i) * 1024);
   };
-  auto issue_w = [&](int kt, const i32x4& rb, int i) {
-    dma16(rb, vow[i], (uint32_t)kt * (BK * 2), wbase(kt) + (w * 4 + i) * 1024);
+  auto issue_w = [&](int kt, int i) {
+    dma16(rw, vow[i], (uint32_t)kt * (BK * 2), wbase(kt) + (w * 4 + i) * 1024);
+  };
+  // LoRA operands of the epilogue (rank up to 32): the L tile [256 tokens][32] and the R tile
+  // [256 columns][32], rows of 64 bytes, zeros past the rank, share activation stage nk (free
+  // during the last step) as bytes [0, 16) and [16, 32) KiB. Step nk-2 copies them with the four
+  // activation copies it would otherwise issue for a step nk that does not exist (copies 0-1 L,
+  // 2-3 R; copy i of wave w fills 1 KiB = 16 rows). A 16 x 32 fragment is then 1 KiB of
+  // contiguous LDS. Higher ranks read L and R from global memory in the epilogue.
+  const int rp = a.rp;
+  const bool lora = rp > 0 && a.L != nullptr;
+  const bool lr_lds = lora && rp <= 32;
+  auto issue_lr = [&](int kt, int k) {  // copy k (0..3) into activation stage kt
+    const bool isr = k >= 2;
+    const int ci = w * 2 + (k & 1);
+    const int row = ci * 16 + (lane >> 2), c = lane & 3;
+    const int64_t origin = isr ? n0 : m0, rows = isr ? Ncols : M;
+    const uint32_t vo = (c * 8 < rp) ? (uint32_t)((origin + row) * rp * 2 + c * 16) : 0xFFFFFFF0u;
+    const i32x4 rs = lr_lds ? buffer_rsrc(isr ? a.R : a.L, (uint32_t)(rows * rp * 2)) : rnone;
+    dma16(rs, vo, 0u, abase(kt) + (isr ? 16384 : 0) + ci * 1024);
   };
 
   f32x4 acc[4][8];  // [output-column tile][token tile]
@@ -648,28 +666,17 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
   };
 
   V8 w0[4], w1[4], x[8];
-  // sub-step 0 of a stage (w0, x) while sub-step 1's fragments of the same stage are read: each
-  // token fragment is re-read as soon as its four MFMAs are issued
-  // (the sub-step-1 weight fragments are read after the first group, so that the wait before
-  // that group's MFMAs does not cover them)
-  auto sub0 = [&](const uint8_t* sa) {
 #pragma unroll
-    for (int tj = 0; tj < 8; ++tj) {
-      mfma4(w0, x[tj], tj);
-      __builtin_amdgcn_sched_barrier(0);
-      x[tj] = read_x(sa, 1, tj);
-      if (tj == 0) read_w(sa + ACT, 1, w1);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  };
-#pragma unroll
-  for (int i = 0; i < 4; ++i) { issue_act(0, ract, i); issue_w(0, rw, i); }
+  for (int i = 0; i < 4; ++i) { issue_act(0, i); issue_w(0, i); }
   if (nk > 1) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) { issue_act(1, ract, i); issue_w(1, rw, i); }
+    for (int i = 0; i < 4; ++i) { issue_act(1, i); issue_w(1, i); }
+    __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8): step 1 may stay in flight
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) issue_lr(1, k);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
   }
-  if (nk > 1) __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8): step 1 may stay in flight
-  else __builtin_amdgcn_s_waitcnt(0x0F70);
   __builtin_amdgcn_s_barrier();
   // no scalar loads pending at the loop entry, so the waits at its head count LDS reads only
   __builtin_amdgcn_s_waitcnt(0xC07F);
@@ -684,18 +691,18 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
   // - sub-step 1 reads step kt+1's sub-step-0 fragments and issues the weight copies of step kt+2
   //   into the weight stage of step kt, free since this barrier.
   // The L2-to-LDS path moves about 64 bytes per clock per CU; eight copies in one sub-step stall
-  // their issue, four per sub-step do not. Past the end the copies go through a zero-record
-  // descriptor: they move no memory and write zeros into stages no wave reads any more.
+  // their issue, four per sub-step do not. Step nk-2 copies the LoRA operands instead (LR), and
+  // its weight copies go through a zero-record descriptor: they move no memory and write zeros
+  // into a stage no wave reads any more.
   //
   // Waves w and w + 4 share a SIMD. With equal priorities the older one (w < 4) wins every MFMA
   // issue slot it wants, runs a whole sub-step ahead, and the younger one then finishes its
   // sub-step 0 alone, where one wave keeps the pipe only about three quarters busy. The younger
   // wave therefore takes the higher priority for sub-step 1 and gives it up for sub-step 0, so
   // both reach the barrier together.
-  for (int kt = 0; kt + 1 < nk; ++kt) {
+  auto kstep = [&](int kt, auto lr) {
+    constexpr bool LR = decltype(lr)::value;
     if (w >= 4) __builtin_amdgcn_s_setprio(0);
-    const bool pre = kt + 2 < nk;
-    const i32x4 ra = pre ? ract : rnone, rb = pre ? rw : rnone;
     const uint8_t* sa = abase(kt);
     const uint8_t* sw = wbase(kt);
 #pragma unroll
@@ -704,7 +711,10 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
       __builtin_amdgcn_sched_barrier(0);
       x[tj] = read_x(sa, 1, tj);
       if (tj == 0) read_w(sw, 1, w1);
-      if (tj & 1) issue_act(kt + 2, ra, tj >> 1);
+      if (tj & 1) {
+        if constexpr (LR) issue_lr(kt + 2, tj >> 1);
+        else issue_act(kt + 2, tj >> 1);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
     // lgkmcnt(7): the weight fragments of this step have been read (the weight copies issued
@@ -725,10 +735,15 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
       mfma4(w1, x[tj], tj);
       __builtin_amdgcn_sched_barrier(0);
       x[tj] = read_x(san, 0, tj);
-      if (tj & 1) issue_w(kt + 2, rb, tj >> 1);
+      if (tj & 1) {
+        if constexpr (LR) dma16(rnone, 0u, 0u, wbase(kt + 2) + (w * 4 + (tj >> 1)) * 1024);
+        else issue_w(kt + 2, tj >> 1);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
-  }
+  };
+  for (int kt = 0; kt + 2 < nk; ++kt) kstep(kt, std::false_type{});
+  if (nk > 1) kstep(nk - 2, std::true_type{});
   if (w >= 4) __builtin_amdgcn_s_setprio(0);
   {
     const uint8_t* sa = abase(nk - 1);
@@ -741,19 +756,22 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
 #pragma unroll
     for (int tj = 0; tj < 8; ++tj) mfma4(w1, x[tj], tj);
   }
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // the empty copies have landed before LDS is reused
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // the L and R copies have landed
 
   // epilogue: LoRA up-projection on MFMA (k = 32 per instruction, lanes past the rank supply
-  // zeros), bias, one bf16 rounding; the tile is staged in LDS (rows of 512 bytes, 16-byte
-  // chunks XOR-swizzled by row) and stored as whole rows
+  // zeros), bias, one rounding per output (acc + c lor + bias); the tile is staged in LDS and
+  // stored as whole rows. The staging tile's rows of 512 bytes (16-byte chunks XOR-swizzled by
+  // row) fill, 64 rows at a time, the four stages other than activation stage nk, which holds L
+  // and R until every wave has read them.
   __syncthreads();
-  uint8_t* stile = smem;
-  const int nsteps = (a.rp + 31) >> 5;
+  const int lrs = nk % 3;
+  auto srow = [&](int r) { const int q = r >> 6; return smem + (q < lrs ? q : q + 1) * ACT + (r & 63) * 512; };
+  const int nsteps = (rp + 31) >> 5;
+  const uint8_t* sL = abase(nk);
+  const uint8_t* sR = sL + 16384;
 #pragma unroll
   for (int ti = 0; ti < 4; ++ti) {
-    const int64_t nrow = n0 + wn * 64 + ti * 16 + l16;  // A-operand row of this lane
-    const int64_t nrc = nrow < Ncols ? nrow : Ncols - 1;
-    const int nloc = wn * 64 + ti * 16 + lq * 4;        // this lane's four output columns
+    const int nloc = wn * 64 + ti * 16 + lq * 4;  // this lane's four output columns
     const int64_t nb = n0 + nloc;
     float bs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (a.bias != nullptr && nb < Ncols) {
@@ -765,16 +783,27 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
     for (int tj = 0; tj < 8; ++tj)
 #pragma unroll
       for (int v = 0; v < 4; ++v) lor[tj][v] = 0.0f;
-    for (int s = 0; s < nsteps; ++s) {
-      const int k0 = s * 32 + lq * 8;
-      u32x4 rv = {0, 0, 0, 0};
-      if (k0 < a.rp && nrow < Ncols) rv = *reinterpret_cast<const u32x4*>(a.R + nrc * a.rp + k0);
+    if (lr_lds) {
+      const V8 rv = E::as8(*reinterpret_cast<const u32x4*>(sR + (wn * 64 + ti * 16 + l16) * 64 + lq * 16));
 #pragma unroll
       for (int tj = 0; tj < 8; ++tj) {
-        const int64_t m = m0 + wm * 128 + tj * 16 + l16;
-        u32x4 lv = {0, 0, 0, 0};
-        if (k0 < a.rp && m < M) lv = *reinterpret_cast<const u32x4*>(a.L + m * a.rp + k0);
-        lor[tj] = E::mfma16(E::as8(rv), E::as8(lv), lor[tj]);
+        const V8 lv = E::as8(*reinterpret_cast<const u32x4*>(sL + (wm * 128 + tj * 16 + l16) * 64 + lq * 16));
+        lor[tj] = E::mfma16(rv, lv, lor[tj]);
+      }
+    } else if (lora) {
+      const int64_t nrow = n0 + wn * 64 + ti * 16 + l16;  // A-operand row of this lane
+      const int64_t nrc = nrow < Ncols ? nrow : Ncols - 1;
+      for (int s = 0; s < nsteps; ++s) {
+        const int k0 = s * 32 + lq * 8;
+        u32x4 rv = {0, 0, 0, 0};
+        if (k0 < rp && nrow < Ncols) rv = *reinterpret_cast<const u32x4*>(a.R + nrc * rp + k0);
+#pragma unroll
+        for (int tj = 0; tj < 8; ++tj) {
+          const int64_t m = m0 + wm * 128 + tj * 16 + l16;
+          u32x4 lv = {0, 0, 0, 0};
+          if (k0 < rp && m < M) lv = *reinterpret_cast<const u32x4*>(a.L + m * rp + k0);
+          lor[tj] = E::mfma16(E::as8(rv), E::as8(lv), lor[tj]);
+        }
       }
     }
 #pragma unroll
@@ -785,7 +814,7 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
       for (int v = 0; v < 4; ++v) o[v] = acc[ti][tj][v] + a.c * lor[tj][v] + bs[v];
       const u32x2 pk = {E::pack2(o[0], o[1]), E::pack2(o[2], o[3])};
       const int chunk = (nloc >> 3) ^ (mloc & 31);
-      *reinterpret_cast<u32x2*>(stile + mloc * 512 + chunk * 16 + (nloc & 7) * 2) = pk;
+      *reinterpret_cast<u32x2*>(srow(mloc) + chunk * 16 + (nloc & 7) * 2) = pk;
     }
   }
   __syncthreads();
@@ -794,7 +823,7 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
     const int id = t + 512 * i, row = id >> 5, c = id & 31;
     const int64_t m = m0 + row, n = n0 + c * 8;
     if (m < M && n < Ncols) {
-      const u32x4 v = *reinterpret_cast<const u32x4*>(stile + row * 512 + ((c ^ (row & 31)) << 4));
+      const u32x4 v = *reinterpret_cast<const u32x4*>(srow(row) + ((c ^ (row & 31)) << 4));
       *reinterpret_cast<u32x4*>(a.out + m * Ncols + n) = v;
     }
   }

@@ -94,6 +94,10 @@ def test_reference_gpu_test_shape_ragged(dev):
     (65, 48, 80, 16, False),        # K not a multiple of 64
     (200, 512, 528, 32, True),      # K % 64 == 0, N % 64 != 0: int8 GEMM forward, general dX
     (200, 528, 512, 16, False),     # N % 64 == 0, K % 64 != 0: general forward, int8 GEMM dX
+    (100, 64, 192, 32, True),       # one k-step forward (LoRA operands copied up front), three in dX
+    (260, 128, 64, 16, False),      # two k-steps forward, one in dX
+    (96, 256, 320, 32, True),       # 4 and 5 k-steps: the output staging around the LoRA stage
+    (150, 640, 384, 48, True),      # rank 48: LoRA operands read from global memory
     (50, 256, 256, 0, True),        # base-only linear(::DenseLayer) with bias
     (40, 24, 20, 2, True),          # ragged: generic path with bias
 ])
