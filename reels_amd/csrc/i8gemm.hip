@@ -767,8 +767,18 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
   const int lrs = nk % 3;
   auto srow = [&](int r) { const int q = r >> 6; return smem + (q < lrs ? q : q + 1) * ACT + (r & 63) * 512; };
   const int nsteps = (rp + 31) >> 5;
-  const uint8_t* sL = abase(nk);
-  const uint8_t* sR = sL + 16384;
+  // the LoRA fragments (the same L fragments serve every column tile) are read once
+  V8 lf[8], rf[4];
+  if (lr_lds) {
+    const uint8_t* sL = abase(nk);
+    const uint8_t* sR = sL + 16384;
+#pragma unroll
+    for (int tj = 0; tj < 8; ++tj)
+      lf[tj] = E::as8(*reinterpret_cast<const u32x4*>(sL + (wm * 128 + tj * 16 + l16) * 64 + lq * 16));
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti)
+      rf[ti] = E::as8(*reinterpret_cast<const u32x4*>(sR + (wn * 64 + ti * 16 + l16) * 64 + lq * 16));
+  }
 #pragma unroll
   for (int ti = 0; ti < 4; ++ti) {
     const int nloc = wn * 64 + ti * 16 + lq * 4;  // this lane's four output columns
@@ -784,12 +794,8 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
 #pragma unroll
       for (int v = 0; v < 4; ++v) lor[tj][v] = 0.0f;
     if (lr_lds) {
-      const V8 rv = E::as8(*reinterpret_cast<const u32x4*>(sR + (wn * 64 + ti * 16 + l16) * 64 + lq * 16));
 #pragma unroll
-      for (int tj = 0; tj < 8; ++tj) {
-        const V8 lv = E::as8(*reinterpret_cast<const u32x4*>(sL + (wm * 128 + tj * 16 + l16) * 64 + lq * 16));
-        lor[tj] = E::mfma16(rv, lv, lor[tj]);
-      }
+      for (int tj = 0; tj < 8; ++tj) lor[tj] = E::mfma16(rf[ti], lf[tj], lor[tj]);
     } else if (lora) {
       const int64_t nrow = n0 + wn * 64 + ti * 16 + l16;  // A-operand row of this lane
       const int64_t nrc = nrow < Ncols ? nrow : Ncols - 1;
