@@ -290,39 +290,39 @@ __global__ __launch_bounds__(256) void colgrad_kernel(const uint16_t* __restrict
   }
 }
 
-// out = c * sum_sp part[sp][o][j] in split order; TRANS: out[j][o] (dB [r][N]) else out[o][j]
+// out = c * sum_sp part[sp][o][j] in split order; TRANS: out[j][o] (dB [r][N]) else out[o][j].
+// One sum per thread, j fastest, so the partials are read contiguously; the split loop is
+// unrolled so that each thread has several independent loads in flight.
 template <bool TRANS>
-__global__ void reduce_partials_kernel(const float* __restrict__ part, int splits, int64_t Od,
-                                       int rp, int r, float c, float* __restrict__ out) {
-  if (!TRANS) {  // one output per thread, j fastest: reads and writes are both contiguous
+__global__ __launch_bounds__(256) void reduce_partials_kernel(const float* __restrict__ part, int splits,
+                                                              int64_t Od, int rp, int r, float c,
+                                                              float* __restrict__ out) {
+  if (!TRANS) {
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= Od * r) return;
     const int64_t o = idx / r, j = idx % r;
     float sum = 0.0f;
+#pragma unroll 8
     for (int sp = 0; sp < splits; ++sp) sum += part[((int64_t)sp * Od + o) * rp + j];
     out[idx] = c * sum;
     return;
   }
-  // 32 x 32 tiles of (o, j): the partials are read along j (contiguous) and the [r][Od] output
-  // is written along o through an LDS transpose (same sums, same split order)
-  __shared__ float tile[32][33];
-  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 256 threads: 8 rows of 32
-  const int64_t o0 = (int64_t)blockIdx.x * 32;
-  const int j0 = blockIdx.y * 32;
-  for (int i = ty; i < 32; i += 8) {
-    const int64_t o = o0 + i;
-    const int j = j0 + tx;
-    float sum = 0.0f;
-    if (o < Od && j < r)
-      for (int sp = 0; sp < splits; ++sp) sum += part[((int64_t)sp * Od + o) * rp + j];
-    tile[i][tx] = c * sum;
+  // 8 x 32 tiles of (o, j); the [r][Od] output is written along o through an LDS transpose
+  __shared__ float tile[8][33];
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  const int64_t o = (int64_t)blockIdx.x * 8 + ty;
+  const int j = blockIdx.y * 32 + tx;
+  float sum = 0.0f;
+  if (o < Od && j < r) {
+#pragma unroll 8
+    for (int sp = 0; sp < splits; ++sp) sum += part[((int64_t)sp * Od + o) * rp + j];
   }
+  tile[ty][tx] = c * sum;
   __syncthreads();
-  for (int i = ty; i < 32; i += 8) {
-    const int j = j0 + i;
-    const int64_t o = o0 + tx;
-    if (j < r && o < Od) out[(int64_t)j * Od + o] = tile[tx][i];
-  }
+  const int wo = threadIdx.x & 7, wj = threadIdx.x >> 3;  // 32 rows of 8 outputs
+  const int64_t oo = (int64_t)blockIdx.x * 8 + wo;
+  const int jj = blockIdx.y * 32 + wj;
+  if (jj < r && oo < Od) out[(int64_t)jj * Od + oo] = tile[wo][wj];
 }
 
 __global__ void fill_f32_kernel(float* p, int64_t n, float v) {
@@ -522,7 +522,7 @@ static int launch_colgrad(int elt, const uint16_t* src, int64_t M, int64_t Od, c
   }
   int rc = check_launch("colgrad_kernel");
   if (rc) return rc;
-  if (trans) { TraceScope _ts(st, "reduce_partials_kernel<true>"); reduce_partials_kernel<true><<<dim3((unsigned)ceil_div(Od, 32), (unsigned)ceil_div(r, 32)), 256, 0, st>>>(part, p.splits, Od, rp, r, c, out); }
+  if (trans) { TraceScope _ts(st, "reduce_partials_kernel<true>"); reduce_partials_kernel<true><<<dim3((unsigned)ceil_div(Od, 8), (unsigned)ceil_div(r, 32)), 256, 0, st>>>(part, p.splits, Od, rp, r, c, out); }
   else { TraceScope _ts(st, "reduce_partials_kernel<false>"); reduce_partials_kernel<false><<<grid1(Od * r), 256, 0, st>>>(part, p.splits, Od, rp, r, c, out); }
   return check_launch("reduce_partials_kernel");
 }
