@@ -767,51 +767,18 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
   const int lrs = nk % 3;
   auto srow = [&](int r) { const int q = r >> 6; return smem + (q < lrs ? q : q + 1) * ACT + (r & 63) * 512; };
   const int nsteps = (rp + 31) >> 5;
-  // the LoRA fragments (the same L fragments serve every column tile) are read once
-  V8 lf[8], rf[4];
-  if (lr_lds) {
-    const uint8_t* sL = abase(nk);
-    const uint8_t* sR = sL + 16384;
-#pragma unroll
-    for (int tj = 0; tj < 8; ++tj)
-      lf[tj] = E::as8(*reinterpret_cast<const u32x4*>(sL + (wm * 128 + tj * 16 + l16) * 64 + lq * 16));
-#pragma unroll
-    for (int ti = 0; ti < 4; ++ti)
-      rf[ti] = E::as8(*reinterpret_cast<const u32x4*>(sR + (wn * 64 + ti * 16 + l16) * 64 + lq * 16));
-  }
+  // bias of this lane's four output columns of each 16-column tile, loaded together
+  u32x2 braw[4];
 #pragma unroll
   for (int ti = 0; ti < 4; ++ti) {
+    const int64_t nb = n0 + wn * 64 + ti * 16 + lq * 4;
+    braw[ti] = u32x2{0u, 0u};
+    if (a.bias != nullptr && nb < Ncols) braw[ti] = *reinterpret_cast<const u32x2*>(a.bias + nb);
+  }
+  // acc + c lor + bias, rounded once, into the staging tile
+  auto finish = [&](int ti, const f32x4* lor) {
     const int nloc = wn * 64 + ti * 16 + lq * 4;  // this lane's four output columns
-    const int64_t nb = n0 + nloc;
-    float bs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (a.bias != nullptr && nb < Ncols) {
-      const u32x2 b2 = *reinterpret_cast<const u32x2*>(a.bias + nb);
-      bs[0] = E::lo(b2[0]); bs[1] = E::hi(b2[0]); bs[2] = E::lo(b2[1]); bs[3] = E::hi(b2[1]);
-    }
-    f32x4 lor[8];
-#pragma unroll
-    for (int tj = 0; tj < 8; ++tj)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) lor[tj][v] = 0.0f;
-    if (lr_lds) {
-#pragma unroll
-      for (int tj = 0; tj < 8; ++tj) lor[tj] = E::mfma16(rf[ti], lf[tj], lor[tj]);
-    } else if (lora) {
-      const int64_t nrow = n0 + wn * 64 + ti * 16 + l16;  // A-operand row of this lane
-      const int64_t nrc = nrow < Ncols ? nrow : Ncols - 1;
-      for (int s = 0; s < nsteps; ++s) {
-        const int k0 = s * 32 + lq * 8;
-        u32x4 rv = {0, 0, 0, 0};
-        if (k0 < rp && nrow < Ncols) rv = *reinterpret_cast<const u32x4*>(a.R + nrc * rp + k0);
-#pragma unroll
-        for (int tj = 0; tj < 8; ++tj) {
-          const int64_t m = m0 + wm * 128 + tj * 16 + l16;
-          u32x4 lv = {0, 0, 0, 0};
-          if (k0 < rp && m < M) lv = *reinterpret_cast<const u32x4*>(a.L + m * rp + k0);
-          lor[tj] = E::mfma16(E::as8(rv), E::as8(lv), lor[tj]);
-        }
-      }
-    }
+    const float bs[4] = {E::lo(braw[ti][0]), E::hi(braw[ti][0]), E::lo(braw[ti][1]), E::hi(braw[ti][1])};
 #pragma unroll
     for (int tj = 0; tj < 8; ++tj) {
       const int mloc = wm * 128 + tj * 16 + l16;
@@ -821,6 +788,51 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
       const u32x2 pk = {E::pack2(o[0], o[1]), E::pack2(o[2], o[3])};
       const int chunk = (nloc >> 3) ^ (mloc & 31);
       *reinterpret_cast<u32x2*>(srow(mloc) + chunk * 16 + (nloc & 7) * 2) = pk;
+    }
+  };
+  if (lr_lds) {
+    // the same L fragments serve every column tile: read once
+    const uint8_t* sL = abase(nk);
+    const uint8_t* sR = sL + 16384;
+    V8 lf[8], rf[4];
+#pragma unroll
+    for (int tj = 0; tj < 8; ++tj)
+      lf[tj] = E::as8(*reinterpret_cast<const u32x4*>(sL + (wm * 128 + tj * 16 + l16) * 64 + lq * 16));
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti)
+      rf[ti] = E::as8(*reinterpret_cast<const u32x4*>(sR + (wn * 64 + ti * 16 + l16) * 64 + lq * 16));
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti) {
+      f32x4 lor[8];
+#pragma unroll
+      for (int tj = 0; tj < 8; ++tj) lor[tj] = E::mfma16(rf[ti], lf[tj], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+      finish(ti, lor);
+    }
+  } else {
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti) {
+      f32x4 lor[8];
+#pragma unroll
+      for (int tj = 0; tj < 8; ++tj)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) lor[tj][v] = 0.0f;
+      if (lora) {
+        const int64_t nrow = n0 + wn * 64 + ti * 16 + l16;  // A-operand row of this lane
+        const int64_t nrc = nrow < Ncols ? nrow : Ncols - 1;
+        for (int s = 0; s < nsteps; ++s) {
+          const int k0 = s * 32 + lq * 8;
+          u32x4 rv = {0, 0, 0, 0};
+          if (k0 < rp && nrow < Ncols) rv = *reinterpret_cast<const u32x4*>(a.R + nrc * rp + k0);
+#pragma unroll
+          for (int tj = 0; tj < 8; ++tj) {
+            const int64_t m = m0 + wm * 128 + tj * 16 + l16;
+            u32x4 lv = {0, 0, 0, 0};
+            if (k0 < rp && m < M) lv = *reinterpret_cast<const u32x4*>(a.L + m * rp + k0);
+            lor[tj] = E::mfma16(E::as8(rv), E::as8(lv), lor[tj]);
+          }
+        }
+      }
+      finish(ti, lor);
     }
   }
   __syncthreads();
