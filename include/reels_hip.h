@@ -152,6 +152,32 @@ int reels_hip_gelu_tanh_bwd(const void* x, const void* dy, void* dx, int64_t n, 
 int reels_hip_gelu_tanh_bwd_f16(const void* x, const void* dy, void* dx, int64_t n, void* stream);
 
 /*
+ * fp32 compute, the reference's Float32 path with int8 frozen weights (_dequantize_for_compute
+ * with T = Float32, src/layers/quantization.jl:61-64, and lora_forward / lora_backward in
+ * Float32, src/layers/lora.jl:56-118). Every operand, intermediate and result is f32:
+ *   W = fl32(q[n][k] * s[n])                   materialised in the workspace once per call
+ *   h = x * A                                  [M][r]
+ *   y = (x W^T + bias) + lora_scale * (h B)    (the reference's order: mixed_add, then adapter)
+ *   u = dy B^T;  dx = dy W + lora_scale * u A^T;  dA = lora_scale x^T u;  dB = lora_scale h^T dy
+ * with the layouts of the bf16 entry points (x [M][K], A [K][r], B [r][N], y [M][N], dA [K][r],
+ * dB [r][N]). The sums run in f32 on fp32 MFMA. workspace: reels_hip_i8lora_workspace_bytes_f32.
+ */
+size_t reels_hip_i8lora_workspace_bytes_f32(int64_t M, int64_t K, int64_t N, int64_t r,
+                                            int which);
+int reels_hip_i8lora_fwd_f32(const float* x, const int8_t* q, const float* scales, const float* A,
+                             const float* B, const float* bias, int64_t M, int64_t K, int64_t N,
+                             int64_t r, float lora_scale, float* y, float* h_save, void* workspace,
+                             size_t ws_bytes, void* stream);
+int reels_hip_i8lora_bwd_f32(const float* dy, const float* x, const float* h, const int8_t* q,
+                             const float* scales, const float* A, const float* B, int64_t M,
+                             int64_t K, int64_t N, int64_t r, float lora_scale, float* dx,
+                             float* dA, float* dB, void* workspace, size_t ws_bytes, void* stream);
+/* gelu_tanh and its pullback on f32 x, dy (linear.jl:61-68 with T = Float32: no rounding). */
+int reels_hip_gelu_tanh_f32(const float* x, float* y, int64_t n, void* stream);
+int reels_hip_gelu_tanh_bwd_f32(const float* x, const float* dy, float* dx, int64_t n,
+                                void* stream);
+
+/*
  * Kernel timing instrumentation. No counterpart in the reference (it has no profiler hooks);
  * used by benchmarks to time individual kernels with HIP events on the stream each kernel is
  * launched on. While enabled, every kernel the library enqueues is bracketed by two event

@@ -142,20 +142,23 @@ def dequant(q, s, mode: str = "f32"):
 
 
 # ---- forward / backward -----------------------------------------------------------------------
-_ELT = {"bf16": 0, "f16": 1}
+_ELT = {"bf16": 0, "f16": 1, "f32": 2}
+# storage of activations, adapters and bias: 16-bit codes for bf16 / f16, float32 values for f32
+_STORE = {"bf16": np.uint16, "f16": np.uint16, "f32": np.float32}
 
 
 def lora_forward(x, q, s, A, B, c, bias=None, rows=None, elt="bf16"):
     """f64 restatement of lora_forward (lora.jl:56-95). x, A, B, bias: 16-bit patterns (uint16)
-    of bf16 or, with elt="f16", IEEE binary16. Returns (y [len(rows)][N] f64,
-    h [len(rows)][r] f64)."""
-    x = _c(x, np.uint16); q = _c(q, np.int8); s = _c(s, np.float32)
-    A = _c(A, np.uint16); B = _c(B, np.uint16); bias = _c(bias, np.uint16)
+    of bf16 or, with elt="f16", IEEE binary16, or float32 values with elt="f32". Returns
+    (y [len(rows)][N] f64, h [len(rows)][r] f64)."""
+    st = _STORE[elt]
+    x = _c(x, st); q = _c(q, np.int8); s = _c(s, np.float32)
+    A = _c(A, st); B = _c(B, st); bias = _c(bias, st)
     M, K = x.shape
     N = q.shape[0]
     r = A.shape[1] if A is not None and A.size else 0
     if A is None:
-        A = np.zeros((K, 0), np.uint16); B = np.zeros((0, N), np.uint16)
+        A = np.zeros((K, 0), st); B = np.zeros((0, N), st)
     rws = None if rows is None else np.ascontiguousarray(rows, dtype=np.int64)
     nrows = M if rws is None else len(rws)
     y = np.empty((nrows, N), np.float64)
@@ -169,8 +172,9 @@ def lora_backward(dy, x, q, s, A, B, c, rows=None, kcols=None, ncols=None,
                   want=("dx", "dA", "dB"), elt="bf16"):
     """f64 restatement of lora_backward (lora.jl:106-118). Returns dict of requested grads:
     dx [len(rows)][K], dA [len(kcols)][r], dB [r][len(ncols)]."""
-    dy = _c(dy, np.uint16); x = _c(x, np.uint16); q = _c(q, np.int8); s = _c(s, np.float32)
-    A = _c(A, np.uint16); B = _c(B, np.uint16)
+    st = _STORE[elt]
+    dy = _c(dy, st); x = _c(x, st); q = _c(q, np.int8); s = _c(s, np.float32)
+    A = _c(A, st); B = _c(B, st)
     M, K = x.shape
     N = q.shape[0]
     r = A.shape[1]
@@ -190,14 +194,14 @@ def lora_backward(dy, x, q, s, A, B, c, rows=None, kcols=None, ncols=None,
 
 
 def gelu_tanh(x, elt="bf16"):
-    x = _c(x, np.uint16)
+    x = _c(x, _STORE[elt])
     y = np.empty_like(x)
     lib().oracle_gelu_tanh(_p(x), _p(y), x.size, _ELT[elt])
     return y
 
 
 def gelu_tanh_backward(x, dy, elt="bf16"):
-    x = _c(x, np.uint16); dy = _c(dy, np.uint16)
+    x = _c(x, _STORE[elt]); dy = _c(dy, _STORE[elt])
     dx = np.empty_like(x)
     lib().oracle_gelu_tanh_backward(_p(x), _p(dy), _p(dx), x.size, _ELT[elt])
     return dx

@@ -88,6 +88,14 @@ void oracle_f32_to_f16_array(const float* in, uint16_t* out, int64_t n) {
 /* value of a 16-bit element: elt 0 = bf16 bits, 1 = IEEE binary16 bits (both exact in f32) */
 static float in16(uint16_t h, int elt) { return elt ? f16_to_f32(h) : oracle_bf16_to_f32(h); }
 static uint16_t out16(float f, int elt) { return elt ? f32_to_f16(f) : oracle_f32_to_bf16(f); }
+/* element i of an activation / adapter array: elt 0 = bf16, 1 = f16 (16-bit codes), 2 = f32 */
+static float inel(const void* p, int64_t i, int elt) {
+  return elt == 2 ? ((const float*)p)[i] : in16(((const uint16_t*)p)[i], elt);
+}
+static void outel(void* p, int64_t i, float f, int elt) {
+  if (elt == 2) ((float*)p)[i] = f;
+  else ((uint16_t*)p)[i] = out16(f, elt);
+}
 
 /* ---- quantize_frozen_matrix: src/layers/quantization.jl:35-44 --------------------------- */
 static float load_elem(const void* w, int dtype, int64_t idx) {
@@ -153,15 +161,15 @@ void oracle_dequant(const int8_t* q, const float* s, int64_t N, int64_t K, int m
 }
 
 /* ---- lora_forward: src/layers/lora.jl:56-95 ------------------------------------------- */
-void oracle_lora_forward(const uint16_t* x, const int8_t* q, const float* s, const uint16_t* A,
-                         const uint16_t* B, const uint16_t* bias, int64_t M, int64_t K, int64_t N,
+void oracle_lora_forward(const void* x, const int8_t* q, const float* s, const void* A,
+                         const void* B, const void* bias, int64_t M, int64_t K, int64_t N,
                          int64_t r, float c, const int64_t* rows, int64_t nrows, double* y_out,
                          double* h_out, int elt) {
   if (!rows) nrows = M;
   double* Ad = (double*)malloc(sizeof(double) * (size_t)(K * (r > 0 ? r : 1)));
   double* Bd = (double*)malloc(sizeof(double) * (size_t)((r > 0 ? r : 1) * N));
-  for (int64_t i = 0; i < K * r; ++i) Ad[i] = in16(A[i], elt);
-  for (int64_t i = 0; i < r * N; ++i) Bd[i] = in16(B[i], elt);
+  for (int64_t i = 0; i < K * r; ++i) Ad[i] = inel(A, i, elt);
+  for (int64_t i = 0; i < r * N; ++i) Bd[i] = inel(B, i, elt);
 #pragma omp parallel
   {
     double* xr = (double*)malloc(sizeof(double) * (size_t)K);
@@ -169,7 +177,7 @@ void oracle_lora_forward(const uint16_t* x, const int8_t* q, const float* s, con
 #pragma omp for schedule(dynamic, 4)
     for (int64_t ii = 0; ii < nrows; ++ii) {
       int64_t m = rows ? rows[ii] : ii;
-      for (int64_t k = 0; k < K; ++k) xr[k] = in16(x[m * K + k], elt);
+      for (int64_t k = 0; k < K; ++k) xr[k] = inel(x, m * K + k, elt);
       /* A * z (lora.jl:86) */
       for (int64_t j = 0; j < r; ++j) hr[j] = 0.0;
       for (int64_t k = 0; k < K; ++k)
@@ -184,7 +192,7 @@ void oracle_lora_forward(const uint16_t* x, const int8_t* q, const float* s, con
           for (int64_t k = 0; k < K; ++k) acc += xr[k] * (double)qr[k];
           double y = acc * (double)s[n];
           /* bias: mixed_add(y, bias) (lora.jl:64-67) */
-          if (bias) y += in16(bias[n], elt);
+          if (bias) y += inel(bias, n, elt);
           /* adapter = c * B * (A * z) (lora.jl:86-94) */
           double ad = 0.0;
           for (int64_t j = 0; j < r; ++j) ad += hr[j] * Bd[j * N + n];
@@ -200,8 +208,8 @@ void oracle_lora_forward(const uint16_t* x, const int8_t* q, const float* s, con
 }
 
 /* ---- lora_backward: src/layers/lora.jl:106-118 ------------------------------------------ */
-void oracle_lora_backward(const uint16_t* dy, const uint16_t* x, const int8_t* q, const float* s,
-                          const uint16_t* A, const uint16_t* B, int64_t M, int64_t K, int64_t N,
+void oracle_lora_backward(const void* dy, const void* x, const int8_t* q, const float* s,
+                          const void* A, const void* B, int64_t M, int64_t K, int64_t N,
                           int64_t r, float c, const int64_t* rows, int64_t nrows,
                           const int64_t* kcols, int64_t nk, const int64_t* ncols, int64_t nn,
                           double* dx_out, double* dA_out, double* dB_out, int elt) {
@@ -211,8 +219,8 @@ void oracle_lora_backward(const uint16_t* dy, const uint16_t* x, const int8_t* q
   const int64_t rr = r > 0 ? r : 1;
   double* Ad = (double*)malloc(sizeof(double) * (size_t)(K * rr));
   double* Bd = (double*)malloc(sizeof(double) * (size_t)(rr * N));
-  for (int64_t i = 0; i < K * r; ++i) Ad[i] = in16(A[i], elt);
-  for (int64_t i = 0; i < r * N; ++i) Bd[i] = in16(B[i], elt);
+  for (int64_t i = 0; i < K * r; ++i) Ad[i] = inel(A, i, elt);
+  for (int64_t i = 0; i < r * N; ++i) Bd[i] = inel(B, i, elt);
   /* u = B' * dy and h = A * x for every token (lora.jl:112-113) */
   double* u = (double*)malloc(sizeof(double) * (size_t)(M * rr));
   double* h = (double*)malloc(sizeof(double) * (size_t)(M * rr));
@@ -220,12 +228,12 @@ void oracle_lora_backward(const uint16_t* dy, const uint16_t* x, const int8_t* q
   for (int64_t m = 0; m < M; ++m) {
     for (int64_t j = 0; j < r; ++j) { u[m * r + j] = 0.0; h[m * r + j] = 0.0; }
     for (int64_t n = 0; n < N; ++n) {
-      double d = in16(dy[m * N + n], elt);
+      double d = inel(dy, m * N + n, elt);
       for (int64_t j = 0; j < r; ++j) u[m * r + j] += d * Bd[j * N + n];
     }
     if (dB_out)
       for (int64_t k = 0; k < K; ++k) {
-        double xv = in16(x[m * K + k], elt);
+        double xv = inel(x, m * K + k, elt);
         for (int64_t j = 0; j < r; ++j) h[m * r + j] += xv * Ad[k * r + j];
       }
   }
@@ -239,7 +247,7 @@ void oracle_lora_backward(const uint16_t* dy, const uint16_t* x, const int8_t* q
         int64_t m = rows ? rows[ii] : ii;
         for (int64_t k = 0; k < K; ++k) acc[k] = 0.0;
         for (int64_t n = 0; n < N; ++n) {
-          double d = (double)in16(dy[m * N + n], elt) * (double)s[n];
+          double d = (double)inel(dy, m * N + n, elt) * (double)s[n];
           const int8_t* qr = q + n * K;
           for (int64_t k = 0; k < K; ++k) acc[k] += d * (double)qr[k];
         }
@@ -260,7 +268,7 @@ void oracle_lora_backward(const uint16_t* dy, const uint16_t* x, const int8_t* q
       double accj[256];
       for (int64_t j = 0; j < r; ++j) accj[j] = 0.0;
       for (int64_t m = 0; m < M; ++m) {
-        double xv = in16(x[m * K + k], elt);
+        double xv = inel(x, m * K + k, elt);
         for (int64_t j = 0; j < r; ++j) accj[j] += u[m * r + j] * xv;
       }
       for (int64_t j = 0; j < r; ++j) dA_out[kk * r + j] = (double)c * accj[j];
@@ -274,7 +282,7 @@ void oracle_lora_backward(const uint16_t* dy, const uint16_t* x, const int8_t* q
       double accj[256];
       for (int64_t j = 0; j < r; ++j) accj[j] = 0.0;
       for (int64_t m = 0; m < M; ++m) {
-        double d = in16(dy[m * N + n], elt);
+        double d = inel(dy, m * N + n, elt);
         for (int64_t j = 0; j < r; ++j) accj[j] += h[m * r + j] * d;
       }
       for (int64_t j = 0; j < r; ++j) dB_out[j * nn + nn_i] = (double)c * accj[j];
@@ -295,19 +303,19 @@ static float gelu_f32(float x) {
   return 0.5f * x * (1.0f + activated);
 }
 
-void oracle_gelu_tanh(const uint16_t* x, uint16_t* y, int64_t n, int elt) {
-  for (int64_t i = 0; i < n; ++i) y[i] = out16(gelu_f32(in16(x[i], elt)), elt);
+void oracle_gelu_tanh(const void* x, void* y, int64_t n, int elt) {
+  for (int64_t i = 0; i < n; ++i) outel(y, i, gelu_f32(inel(x, i, elt)), elt);
 }
 
-void oracle_gelu_tanh_backward(const uint16_t* x, const uint16_t* dy, uint16_t* dx, int64_t n,
+void oracle_gelu_tanh_backward(const void* x, const void* dy, void* dx, int64_t n,
                                int elt) {
   /* d/dx 0.5x(1+tanh(k(x+a x^3))) = 0.5(1+t) + 0.5x(1-t^2)k(1+3a x^2) */
   const double k = sqrt(2.0 / 3.14159265358979323846), a = 0.044715;
   for (int64_t i = 0; i < n; ++i) {
-    double xv = in16(x[i], elt);
+    double xv = inel(x, i, elt);
     double t = tanh(k * (xv + a * xv * xv * xv));
     double d = 0.5 * (1.0 + t) + 0.5 * xv * (1.0 - t * t) * k * (1.0 + 3.0 * a * xv * xv);
-    dx[i] = out16((float)(d * (double)in16(dy[i], elt)), elt);
+    outel(dx, i, (float)(d * (double)inel(dy, i, elt)), elt);
   }
 }
 

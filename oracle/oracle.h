@@ -61,8 +61,8 @@ void oracle_f32_to_f16_array(const float* in, uint16_t* out, int64_t n);
  * the order given (y_out [nrows][N], h_out [nrows][r], either may be NULL). bias may be NULL.
  * Pinned by: brute-force small cases with integer-valued inputs (exact in f64), linearity,
  * B = 0 reducing to the base GEMM (test/unit/lora.jl:6), merged-weight identity (lora.jl:8). */
-void oracle_lora_forward(const uint16_t* x, const int8_t* q, const float* s, const uint16_t* A,
-                         const uint16_t* B, const uint16_t* bias, int64_t M, int64_t K, int64_t N,
+void oracle_lora_forward(const void* x, const int8_t* q, const float* s, const void* A,
+                         const void* B, const void* bias, int64_t M, int64_t K, int64_t N,
                          int64_t r, float c, const int64_t* rows, int64_t nrows, double* y_out,
                          double* h_out, int elt);
 
@@ -75,18 +75,18 @@ void oracle_lora_forward(const uint16_t* x, const int8_t* q, const float* s, con
  * with h = x*A in f64. Outputs packed in listed order: dx_out [nrows][K], dA_out [nk][r],
  * dB_out [r][nn]; any may be NULL. Pinned by: central finite differences of
  * oracle_lora_forward (as test/unit/lora.jl:12-21), brute-force integer cases. */
-void oracle_lora_backward(const uint16_t* dy, const uint16_t* x, const int8_t* q, const float* s,
-                          const uint16_t* A, const uint16_t* B, int64_t M, int64_t K, int64_t N,
+void oracle_lora_backward(const void* dy, const void* x, const int8_t* q, const float* s,
+                          const void* A, const void* B, int64_t M, int64_t K, int64_t N,
                           int64_t r, float c, const int64_t* rows, int64_t nrows,
                           const int64_t* kcols, int64_t nk, const int64_t* ncols, int64_t nn,
                           double* dx_out, double* dA_out, double* dB_out, int elt);
 
-/* gelu_tanh, src/layers/linear.jl:61-68, in f32 on 16-bit inputs, result rounded to the input
- * type, and its analytic derivative applied to an upstream gradient (dx = rnd(dy * gelu'(x))).
+/* gelu_tanh, src/layers/linear.jl:61-68, in f32 on bf16 / f16 / f32 inputs, result rounded to
+ * the input type, and its analytic derivative applied to an upstream gradient (dx = rnd(dy * gelu'(x))).
  * Pinned by: closed-form values (gelu(0)=0, odd-part identity gelu(x)-gelu(-x)=x), central
  * finite differences for the derivative. */
-void oracle_gelu_tanh(const uint16_t* x, uint16_t* y, int64_t n, int elt);
-void oracle_gelu_tanh_backward(const uint16_t* x, const uint16_t* dy, uint16_t* dx, int64_t n,
+void oracle_gelu_tanh(const void* x, void* y, int64_t n, int elt);
+void oracle_gelu_tanh_backward(const void* x, const void* dy, void* dx, int64_t n,
                                int elt);
 
 /* Philox4x32-10 (Salmon et al., SC'11) counter-based generator for seeded test inputs.

@@ -32,6 +32,11 @@ EXPORTS = (
     "reels_hip_gelu_tanh_f16",
     "reels_hip_gelu_tanh_bwd",
     "reels_hip_gelu_tanh_bwd_f16",
+    "reels_hip_i8lora_workspace_bytes_f32",
+    "reels_hip_i8lora_fwd_f32",
+    "reels_hip_i8lora_bwd_f32",
+    "reels_hip_gelu_tanh_f32",
+    "reels_hip_gelu_tanh_bwd_f32",
     "reels_hip_trace_start",
     "reels_hip_trace_stop",
     "reels_hip_trace_get",
@@ -75,7 +80,9 @@ def lib():
     L.reels_hip_i8_dequant.restype = ctypes.c_int
     L.reels_hip_i8lora_workspace_bytes.argtypes = [i64, i64, i64, i64, ctypes.c_int]
     L.reels_hip_i8lora_workspace_bytes.restype = sz
-    for sfx in ("", "_f16"):
+    L.reels_hip_i8lora_workspace_bytes_f32.argtypes = [i64, i64, i64, i64, ctypes.c_int]
+    L.reels_hip_i8lora_workspace_bytes_f32.restype = sz
+    for sfx in ("", "_f16", "_f32"):
         fwd, bwd = getattr(L, "reels_hip_i8lora_fwd" + sfx), getattr(L, "reels_hip_i8lora_bwd" + sfx)
         fwd.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, ctypes.c_float, vp, vp, vp, sz, vp]
         fwd.restype = ctypes.c_int

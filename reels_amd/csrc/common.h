@@ -63,6 +63,42 @@ __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast
 // conversion and the dequantized-weight element of the compute type.
 typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
 
+// HBM -> LDS copy of 16 bytes per lane (buffer_load_dwordx4 ... lds): lane i's data lands at
+// LDS byte ldsaddr + 16 i (ldsaddr in M0). Issued through inline asm so the compiler does not
+// order the kernel's LDS reads behind it: the kernel synchronises these copies itself (explicit
+// vmcnt waits followed by a workgroup barrier).
+typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4;
+__device__ __forceinline__ i32x4 buffer_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  i32x4 r;
+  r[0] = (int)(uint32_t)b;
+  r[1] = (int)((b >> 32) & 0xffffu);  // stride 0
+  r[2] = (int)bytes;                  // num_records: reads past it return 0
+  r[3] = 0x00020000;                  // raw buffer, 32-bit data format
+  return r;
+}
+// The compiler writes M0 right before the asm but does not know that the copy reads it: on
+// this GPU generation an LDS-DMA instruction needs one wait state after an SALU write of M0,
+// hence the s_nop.
+__device__ __forceinline__ void dma16(const i32x4& rsrc, uint32_t voff, uint32_t soff,
+                                      const uint8_t* lds) {
+  const uint32_t ldsaddr = (uint32_t)(uintptr_t)LDS_PTR(const uint8_t, lds);
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc),
+               "s"(soff), "{m0}"(ldsaddr)
+               : "memory");
+}
+
+// gelu_tanh, src/layers/linear.jl:61-68, in f32, and its analytic derivative
+__device__ __forceinline__ float gelu_f(float x) {
+  const float k = 0.7978845608028654f;  // sqrt(Float32(2 / pi))
+  const float inner = x + 0.044715f * (x * x * x);
+  return 0.5f * x * (1.0f + tanhf(k * inner));
+}
+__device__ __forceinline__ float gelu_grad_f(float x) {
+  const float k = 0.7978845608028654f, a = 0.044715f;
+  const float t = tanhf(k * (x + a * x * x * x));
+  return 0.5f * (1.0f + t) + 0.5f * x * (1.0f - t * t) * k * (1.0f + 3.0f * a * x * x);
+}
 template <int ELT> struct Elt;
 
 template <> struct Elt<REELS_HIP_BF16> {

@@ -37,4 +37,8 @@ int launch_dequant_rows(int elt, const int8_t* q, int64_t ldq, const float* s, i
 int launch_dequant_transpose(int elt, const int8_t* q, int64_t ldq, const float* s, int64_t N,
                              int64_t K, uint16_t* wt, hipStream_t st);
 
+// out = c * sum over splits of part[sp][o][j] (split order): out[o][j], or out[j][o] with trans
+int launch_reduce_partials(const float* part, int splits, int64_t Od, int rp, int r, float c,
+                           float* out, bool trans, hipStream_t st);
+
 }  // namespace reels

@@ -246,31 +246,6 @@ void i8gemm_kernel(GemmArgs a) {
   }
 }
 
-// HBM -> LDS copy of 16 bytes per lane (buffer_load_dwordx4 ... lds): lane i's data lands at
-// LDS byte ldsaddr + 16 i (ldsaddr in M0). Issued through inline asm so the compiler does not
-// order the kernel's LDS reads behind it: the kernel synchronises these copies itself (explicit
-// vmcnt waits followed by a workgroup barrier).
-typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4;
-__device__ __forceinline__ i32x4 buffer_rsrc(const void* base, uint32_t bytes) {
-  const uint64_t b = reinterpret_cast<uint64_t>(base);
-  i32x4 r;
-  r[0] = (int)(uint32_t)b;
-  r[1] = (int)((b >> 32) & 0xffffu);  // stride 0
-  r[2] = (int)bytes;                  // num_records: reads past it return 0
-  r[3] = 0x00020000;                  // raw buffer, 32-bit data format
-  return r;
-}
-// The compiler writes M0 right before the asm but does not know that the copy reads it: on
-// this GPU generation an LDS-DMA instruction needs one wait state after an SALU write of M0,
-// hence the s_nop.
-__device__ __forceinline__ void dma16(const i32x4& rsrc, uint32_t voff, uint32_t soff,
-                                      const uint8_t* lds) {
-  const uint32_t ldsaddr = (uint32_t)(uintptr_t)LDS_PTR(const uint8_t, lds);
-  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc),
-               "s"(soff), "{m0}"(ldsaddr)
-               : "memory");
-}
-
 // FWD weight tile of the three-stage kernel: [256 n][64 k] int8, 16-byte slots XOR-swizzled
 // within the 64-byte row so 32-row fragment reads (ds_read_b128) hit distinct banks
 __device__ __forceinline__ int wf2_swz(int row) { return ((row >> 1) & 3) ^ ((row >> 3) & 1); }

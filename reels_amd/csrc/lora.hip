@@ -399,17 +399,7 @@ __global__ void g_colgrad_kernel(const uint16_t* __restrict__ src, int64_t M, in
 }
 
 // ---------------------------------------------------------------------------------------------
-// gelu_tanh, src/layers/linear.jl:61-68 (f32 math, bf16 in/out)
-__device__ __forceinline__ float gelu_f(float x) {
-  const float k = 0.7978845608028654f;  // sqrt(Float32(2 / pi))
-  const float inner = x + 0.044715f * (x * x * x);
-  return 0.5f * x * (1.0f + tanhf(k * inner));
-}
-__device__ __forceinline__ float gelu_grad_f(float x) {
-  const float k = 0.7978845608028654f, a = 0.044715f;
-  const float t = tanhf(k * (x + a * x * x * x));
-  return 0.5f * (1.0f + t) + 0.5f * x * (1.0f - t * t) * k * (1.0f + 3.0f * a * x * x);
-}
+// gelu_tanh, src/layers/linear.jl:61-68 (f32 math, 16-bit in/out; gelu_f in common.h)
 template <int ELT>
 __global__ void gelu_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ y, int64_t n) {
   using E = Elt<ELT>;
@@ -522,8 +512,13 @@ static int launch_colgrad(int elt, const uint16_t* src, int64_t M, int64_t Od, c
   }
   int rc = check_launch("colgrad_kernel");
   if (rc) return rc;
-  if (trans) { TraceScope _ts(st, "reduce_partials_kernel<true>"); reduce_partials_kernel<true><<<dim3((unsigned)ceil_div(Od, 8), (unsigned)ceil_div(r, 32)), 256, 0, st>>>(part, p.splits, Od, rp, r, c, out); }
-  else { TraceScope _ts(st, "reduce_partials_kernel<false>"); reduce_partials_kernel<false><<<grid1(Od * r), 256, 0, st>>>(part, p.splits, Od, rp, r, c, out); }
+  return launch_reduce_partials(part, p.splits, Od, rp, r, c, out, trans, st);
+}
+
+int launch_reduce_partials(const float* part, int splits, int64_t Od, int rp, int r, float c,
+                           float* out, bool trans, hipStream_t st) {
+  if (trans) { TraceScope _ts(st, "reduce_partials_kernel<true>"); reduce_partials_kernel<true><<<dim3((unsigned)ceil_div(Od, 8), (unsigned)ceil_div(r, 32)), 256, 0, st>>>(part, splits, Od, rp, r, c, out); }
+  else { TraceScope _ts(st, "reduce_partials_kernel<false>"); reduce_partials_kernel<false><<<(unsigned)ceil_div(Od * r, 256), 256, 0, st>>>(part, splits, Od, rp, r, c, out); }
   return check_launch("reduce_partials_kernel");
 }
 

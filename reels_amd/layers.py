@@ -38,15 +38,16 @@ def _need_device(t: torch.Tensor, name: str) -> None:
                          "runs only on the GPU")
 
 
-# 16-bit activation types of the LoRA linear and the suffix of their C entry points:
-# bfloat16 (this library's default) and float16 (the reference's int8 compute precision)
-_ACT_SUFFIX = {torch.bfloat16: "", torch.float16: "_f16"}
+# activation types of the LoRA linear and the suffix of their C entry points: bfloat16 (this
+# library's default), float16 (the reference's int8 compute precision) and float32 (the
+# reference's Float32 compute, its only CPU precision)
+_ACT_SUFFIX = {torch.bfloat16: "", torch.float16: "_f16", torch.float32: "_f32"}
 
 
 def _act_dtype(t: torch.Tensor, name: str) -> torch.dtype:
     _need_device(t, name)
     if t.dtype not in _ACT_SUFFIX:
-        raise TypeError(f"{name} must be bfloat16 or float16, got {t.dtype}")
+        raise TypeError(f"{name} must be bfloat16, float16 or float32, got {t.dtype}")
     return t.dtype
 
 
@@ -131,8 +132,14 @@ def quantize_frozen_matrix(weight: torch.Tensor, T: Optional[torch.dtype] = None
 
 
 # ---- raw entry points -------------------------------------------------------------------------
-def workspace_bytes(M: int, K: int, N: int, r: int, which: int) -> int:
-    return int(_lib.lib().reels_hip_i8lora_workspace_bytes(M, K, N, r, which))
+def workspace_bytes(M: int, K: int, N: int, r: int, which: int,
+                    dtype: torch.dtype = torch.bfloat16) -> int:
+    """Workspace of reels_hip_i8lora_fwd / _bwd (the 16-bit entry points share one size) or,
+    for float32, of reels_hip_i8lora_fwd_f32 / _bwd_f32."""
+    L = _lib.lib()
+    if dtype == torch.float32:
+        return int(L.reels_hip_i8lora_workspace_bytes_f32(M, K, N, r, which))
+    return int(L.reels_hip_i8lora_workspace_bytes(M, K, N, r, which))
 
 
 def _on_device(weight: QuantizedMatrix, device) -> QuantizedMatrix:
@@ -148,8 +155,9 @@ def i8lora_forward(x, weight: QuantizedMatrix, A=None, B=None, bias=None, lora_s
                    save_h: bool = False):
     """y = rnd(x deq(Wq)^T + lora_scale * rnd(x A) B + bias); returns (y, h or None).
 
-    x [M][K] bfloat16 or float16 (reels_hip_i8lora_fwd / _fwd_f16); A [K][r], B [r][N] and
-    bias [N] of the same dtype (Julia A::(r,K), B::(N,r)); y and h come back in that dtype."""
+    x [M][K] bfloat16, float16 or float32 (reels_hip_i8lora_fwd / _fwd_f16 / _fwd_f32; float32
+    rounds nothing); A [K][r], B [r][N] and bias [N] of the same dtype (Julia A::(r,K),
+    B::(N,r)); y and h come back in that dtype."""
     dt = _act_dtype(x, "x")
     x = x.contiguous()
     weight = _on_device(weight, x.device)
@@ -166,7 +174,7 @@ def i8lora_forward(x, weight: QuantizedMatrix, A=None, B=None, bias=None, lora_s
     dev = x.device
     y = torch.empty((M, N), dtype=dt, device=dev)
     h = torch.empty((M, r), dtype=dt, device=dev) if (save_h and r) else None
-    nbytes = workspace_bytes(M, K, N, r, _lib.WS_FWD)
+    nbytes = workspace_bytes(M, K, N, r, _lib.WS_FWD, dt)
     ws = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
     fn = "reels_hip_i8lora_fwd" + _ACT_SUFFIX[dt]
     _lib.check(fn, getattr(_lib.lib(), fn)(
@@ -178,8 +186,8 @@ def i8lora_forward(x, weight: QuantizedMatrix, A=None, B=None, bias=None, lora_s
 def i8lora_backward(dy, x, weight: QuantizedMatrix, A=None, B=None, lora_scale=1.0, h=None,
                     want_dx=True, want_dA=True, want_dB=True):
     """(dx [M][K], dA f32 [K][r], dB f32 [r][N]) of lora_backward (lora.jl:106-118). dy, x, h,
-    A and B share one dtype, bfloat16 or float16 (reels_hip_i8lora_bwd / _bwd_f16); dx comes
-    back in it."""
+    A and B share one dtype, bfloat16, float16 or float32 (reels_hip_i8lora_bwd / _bwd_f16 /
+    _bwd_f32); dx comes back in it."""
     dt = _act_dtype(dy, "dy")
     dy = dy.contiguous()
     weight = _on_device(weight, dy.device)
@@ -196,7 +204,7 @@ def i8lora_backward(dy, x, weight: QuantizedMatrix, A=None, B=None, lora_scale=1
     dx = torch.empty((M, K), dtype=dt, device=dev) if want_dx else None
     dA = torch.empty((K, r), dtype=torch.float32, device=dev) if (want_dA and r) else None
     dB = torch.empty((r, N), dtype=torch.float32, device=dev) if (want_dB and r) else None
-    nbytes = workspace_bytes(M, K, N, r, _lib.WS_BWD)
+    nbytes = workspace_bytes(M, K, N, r, _lib.WS_BWD, dt)
     ws = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
     fn = "reels_hip_i8lora_bwd" + _ACT_SUFFIX[dt]
     _lib.check(fn, getattr(_lib.lib(), fn)(
@@ -248,7 +256,7 @@ class LoRALinear:
     """LoRALinear (lora.jl:1-35) over a QuantizedMatrix base weight.
 
     A: [K][r] (Julia A::(r, K)), B: [r][N] (Julia B::(N, r)) on the device, in the weight's
-    compute dtype when that is float16, else bfloat16. The constructor initialises
+    compute dtype (bfloat16, float16 or float32). The constructor initialises
     A ~ randn / sqrt(in) and B = 0 like the reference (lora.jl:22-24)."""
 
     def __init__(self, weight: QuantizedMatrix, rank: int, alpha: Optional[float] = None,
@@ -370,7 +378,7 @@ class I8LoRALinearFunction(torch.autograd.Function):
 
 
 def gelu_tanh(x: torch.Tensor) -> torch.Tensor:
-    """gelu_tanh (linear.jl:61-68), bfloat16 or float16 in and out, f32 math."""
+    """gelu_tanh (linear.jl:61-68), bfloat16, float16 or float32 in and out, f32 math."""
     dt = _act_dtype(x, "x")
     x = x.contiguous()
     y = torch.empty_like(x)
@@ -405,10 +413,10 @@ def frozen_weight_transfer(device: str, precision: str, quantization: str = "non
                            cpu_offload: bool = False) -> FrozenWeightTransfer:
     """frozen_weight_transfer (quantization.jl:88-101).
 
-    int8 with fp16 compute is the reference's own low-VRAM mode and runs on the f16 kernels. The
-    reference rejects int8 with bf16 compute because its backward runs through an fp32 shadow
-    model; here bf16 is a compute precision of the HIP kernels, so that combination is accepted
-    on the ROCm device too. fp32 compute with int8 has no kernels here and raises."""
+    int8 with fp16 compute is the reference's own low-VRAM mode and runs on the f16 kernels;
+    int8 with fp32 compute runs on the f32 kernels. The reference rejects int8 with bf16 compute
+    because its backward runs through an fp32 shadow model; here bf16 is a compute precision of
+    the HIP kernels, so that combination is accepted on the ROCm device too."""
     if quantization not in ("none", "int8"):
         raise ValueError("frozen weight quantization must be none or int8")
     if device not in ("cpu", "cuda", "hip"):
@@ -421,16 +429,15 @@ def frozen_weight_transfer(device: str, precision: str, quantization: str = "non
     if quantization == "int8":
         if device == "cpu":
             raise ValueError("the int8 HIP path runs on the GPU only")
-        if precision not in ("bf16", "fp16"):
-            raise NotImplementedError("int8 frozen weights run with bf16 or fp16 compute on "
-                                      f"MI355X; {precision} compute is not implemented")
+        if precision not in ("bf16", "fp16", "fp32"):
+            raise ValueError(f"unknown compute precision {precision!r} (bf16, fp16 or fp32)")
     return FrozenWeightTransfer(device, precision, quantization, cpu_offload)
 
 
 def move_weight(weight, transfer: FrozenWeightTransfer):
     """_move_weight (quantization.jl:111-144): quantize a frozen matrix on the device; an existing
     QuantizedMatrix is kept as is (re-moving keeps identical codes)."""
-    compute = torch.float16 if transfer.precision == "fp16" else torch.bfloat16
+    compute = {"fp16": torch.float16, "fp32": torch.float32}.get(transfer.precision, torch.bfloat16)
     if isinstance(weight, QuantizedMatrix):
         if transfer.quantization == "int8":
             if transfer.cpu_offload and weight.values.is_cuda:

@@ -53,6 +53,13 @@ def test_workspace_sizes():
     # K a multiple of 16 but not of 64: the int8 GEMM path, whose backward holds dy*s [M][N] bf16
     assert L.reels_hip_i8lora_workspace_bytes(4096, 5136, 5120, 32, 1) >= 4096 * 5120 * 2
     assert L.reels_hip_i8lora_workspace_bytes(-1, 5, 5, 1, 0) == 0
+    # f32: the dequantized weight is N x K f32, h / u panels [M][r] f32, dA / dB partials
+    for which in (0, 1):
+        b = L.reels_hip_i8lora_workspace_bytes_f32(32760, 5120, 13824, 32, which)
+        assert b % 256 == 0 and b >= 13824 * 5120 * 4 + 32760 * 32 * 4 * (1 + which)
+    assert L.reels_hip_i8lora_workspace_bytes_f32(4, 5, 7, 3, 1) > 0
+    assert L.reels_hip_i8lora_workspace_bytes_f32(-1, 5, 5, 1, 0) == 0
+    assert L.reels_hip_i8lora_workspace_bytes_f32(4, 5, 5, 1, 7) == 0
 
 
 def _err():
@@ -90,6 +97,23 @@ def test_argument_errors_before_any_gpu_work():
                                       fake, None, None, fake, 1 << 20, None) == -1
     assert "reels_hip_i8lora_bwd_f16" in _err()
     assert L.reels_hip_gelu_tanh_f16(None, None, -1, None) == -1
+    # ... and so do the f32 ones
+    assert L.reels_hip_i8lora_fwd_f32(fake, fake, fake, None, None, None, 8, 16, 16, 0, 1.0, fake,
+                                      None, None, 0, None) == -3
+    assert "reels_hip_i8lora_fwd_f32" in _err() and "_workspace_bytes_f32" in _err()
+    assert L.reels_hip_i8lora_fwd_f32(fake, fake, fake, None, None, None, 8, 0, 16, 0, 1.0, fake,
+                                      None, fake, 1 << 20, None) == -1
+    assert L.reels_hip_i8lora_fwd_f32(fake, fake, fake, None, None, None, 8, 16, 16, 4, 1.0, fake,
+                                      None, fake, 1 << 20, None) == -1  # r > 0 needs A and B
+    assert L.reels_hip_i8lora_fwd_f32(fake, fake, fake, None, None, None, 8, 16, 16, 0,
+                                      float("nan"), fake, None, fake, 1 << 20, None) == -1
+    assert L.reels_hip_i8lora_bwd_f32(fake, fake, None, fake, fake, fake, fake, 8, 16, 16, 16, 1.0,
+                                      fake, None, None, None, 0, None) == -3
+    assert L.reels_hip_i8lora_bwd_f32(None, fake, None, fake, fake, fake, fake, 8, 16, 16, 16, 1.0,
+                                      fake, None, None, fake, 1 << 20, None) == -1
+    assert "reels_hip_i8lora_bwd_f32" in _err()
+    assert L.reels_hip_gelu_tanh_f32(None, None, -1, None) == -1
+    assert L.reels_hip_gelu_tanh_bwd_f32(None, None, None, 5, None) == -1
     # a successful-looking call clears the message of the previous failure
     assert L.reels_hip_gelu_tanh(None, None, 0, None) == 0
     assert _err() == ""
@@ -118,8 +142,10 @@ def test_frozen_weight_transfer_policy():
         frozen_weight_transfer("cpu", "fp32", quantization="int8")
     # fp16 with int8 is the reference's own low-VRAM mode (quantization.jl:96-98 accepts it)
     assert frozen_weight_transfer("hip", "fp16", quantization="int8").precision == "fp16"
-    with pytest.raises(NotImplementedError):
-        frozen_weight_transfer("hip", "fp32", quantization="int8")
+    # fp32 with int8 is the reference's Float32 path (quantization.jl:61-64): the f32 kernels
+    assert frozen_weight_transfer("hip", "fp32", quantization="int8").precision == "fp32"
+    with pytest.raises(ValueError):
+        frozen_weight_transfer("hip", "fp8", quantization="int8")
     assert frozen_weight_transfer("cpu", "fp32").quantization == "none"
 
 

@@ -388,3 +388,45 @@ def test_f16_gelu_closed_forms():
     f = lambda v: 0.5 * v * (1 + np.tanh(k * (v + 0.044715 * v ** 3)))
     fd = (f(gx + 1e-5) - f(gx - 1e-5)) / 2e-5
     assert np.allclose(d, fd, rtol=2 ** -10, atol=2 ** -12)
+
+
+def test_f32_forward_backward_equal_bf16_path_on_shared_values():
+    # bf16-exact values passed as float32: the f32 element path decodes them to the same f64
+    x, q, s, A, B, bias = _small_int_case(seed=9)
+    dy = np.random.default_rng(10).integers(-3, 4, size=(x.shape[0], q.shape[0])).astype(F32)
+    c = 0.75
+    yb, hb = oracle.lora_forward(bf(x), q, s, bf(A), bf(B), c, bias=bf(bias))
+    yf, hf = oracle.lora_forward(x, q, s, A, B, c, bias=bias, elt="f32")
+    assert np.array_equal(yb, yf) and np.array_equal(hb, hf)
+    gb = oracle.lora_backward(bf(dy), bf(x), q, s, bf(A), bf(B), c)
+    gf = oracle.lora_backward(dy, x, q, s, A, B, c, elt="f32")
+    for k in ("dx", "dA", "dB"):
+        assert np.array_equal(gb[k], gf[k]), k
+
+
+def test_f32_forward_uses_the_float32_values():
+    # 24 significant bits survive the f32 decode (bf16 and f16 would round them away)
+    x = np.array([[1 + 2 ** -20, -3 - 2 ** -21]], np.float32)
+    q = np.array([[1, 1]], np.int8)
+    s = np.array([1.0], np.float32)
+    y, _ = oracle.lora_forward(x, q, s, None, None, 0.0, elt="f32")
+    assert y[0, 0] == float(np.float32(1 + 2 ** -20)) + float(np.float32(-3 - 2 ** -21))
+
+
+def test_f32_gelu_is_the_unrounded_bf16_gelu():
+    # the f32 path returns gelu in f32 (linear.jl:61-68 with T = Float32: no cast back); the
+    # bf16 path is the same value rounded to nearest even, and both meet the closed forms
+    xs = np.linspace(-6, 6, 241).astype(F32)
+    xs = oracle.bf16_to_f32(oracle.f32_to_bf16(xs))  # inputs both paths represent exactly
+    yf = oracle.gelu_tanh(xs, elt="f32")
+    assert yf.dtype == np.float32
+    assert np.array_equal(oracle.f32_to_bf16(yf), oracle.gelu_tanh(bf(xs)))
+    k = np.sqrt(2 / np.pi)
+    xb = xs.astype(np.float64)
+    ref = 0.5 * xb * (1 + np.tanh(k * (xb + 0.044715 * xb ** 3)))
+    assert np.allclose(yf, ref, rtol=1e-6, atol=1e-7)
+    assert yf[np.argmin(np.abs(xs))] == 0.0
+    d = oracle.gelu_tanh_backward(xs, np.ones_like(xs), elt="f32").astype(np.float64)
+    f = lambda v: 0.5 * v * (1 + np.tanh(k * (v + 0.044715 * v ** 3)))
+    fd = (f(xb + 1e-6) - f(xb - 1e-6)) / 2e-6
+    assert np.allclose(d, fd, rtol=1e-5, atol=1e-6)
