@@ -28,6 +28,7 @@ import time
 
 METRIC = ("TFLOP/s and % bf16-MFMA peak, int8-W LoRA linear fwd+bwd, Wan-14B shapes, 1 GPU")
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA (published)
+PEAK_TFLOPS = {"bf16": 2500.0, "f16": 2500.0, "f32": 157.3}  # dense MFMA, published
 PEAK_HBM_GBS = 8000.0
 TOKENS = 32760
 RANK = 32
@@ -66,7 +67,7 @@ def parse():
                          "GPU one projection ahead of use on a copy stream (stream: WeightStreamer, "
                          "two slots) or copied right before each use (sync: the reference's "
                          "per-call upload)")
-    ap.add_argument("--dtype", choices=("bf16", "f16"), default="bf16",
+    ap.add_argument("--dtype", choices=("bf16", "f16", "f32"), default="bf16",
                     help="activation / LoRA element type: bf16 (the default workload) or f16 "
                          "(the reference's own int8 compute precision, the _f16 entry points)")
     ap.add_argument("--no-pack", action="store_true", help="skip the pack workload")
@@ -78,8 +79,8 @@ def parse():
 
 
 def vendor_gemm_tflops(dev, M, K, N, seconds=1.5, dtype=None):
-    """16-bit torch.matmul (hipBLASLt; bf16 unless dtype says otherwise) on one Wan-14B
-    projection shape, timed over a
+    """torch.matmul (hipBLASLt; bf16 unless dtype says otherwise, fp32 without TF32) on one
+    Wan-14B projection shape, timed over a
     sustained loop (~seconds, like the timed bench steps: the GPU runs at its power cap, so short
     bursts and sustained loops clock differently): the practical MFMA ceiling for a dense GEMM
     of this size on this GPU, measured in the same run."""
@@ -229,8 +230,8 @@ class Projection:
         self.dx = torch.empty((M, K), dtype=bf, device=dev)
         self.dA = torch.empty((K, r), dtype=torch.float32, device=dev)
         self.dB = torch.empty((r, N), dtype=torch.float32, device=dev)
-        self.wsf_n = workspace_bytes(M, K, N, r, _lib.WS_FWD)
-        self.wsb_n = workspace_bytes(M, K, N, r, _lib.WS_BWD)
+        self.wsf_n = workspace_bytes(M, K, N, r, _lib.WS_FWD, bf)
+        self.wsb_n = workspace_bytes(M, K, N, r, _lib.WS_BWD, bf)
         self.wsf = torch.empty((self.wsf_n,), dtype=torch.uint8, device=dev)
         self.wsb = torch.empty((self.wsb_n,), dtype=torch.uint8, device=dev)
         c = float(torch.tensor(ALPHA, dtype=torch.float32) / torch.tensor(float(r)))
@@ -318,8 +319,8 @@ def main():
         return
     gen = torch.Generator(device=dev).manual_seed(1234)
     M = args.tokens
-    act = torch.float16 if args.dtype == "f16" else torch.bfloat16
-    sfx = "_f16" if args.dtype == "f16" else ""
+    act = {"f16": torch.float16, "f32": torch.float32}.get(args.dtype, torch.bfloat16)
+    sfx = {"f16": "_f16", "f32": "_f32"}.get(args.dtype, "")
     projs = [Projection(n, K, N, M, RANK, dev, gen, act) for (n, K, N) in PROJECTIONS]
     streamer = None
     if args.offload != "none":
@@ -391,17 +392,18 @@ def main():
     achieved = (gemm_fl["fwd"] + gemm_fl["dx"]) / (tot_ms * 1e-3) / 1e12 if tot_ms > 0 else 0.0
     gemm_names = sorted({n for (n, _) in recs if "gemm_kernel" in n})
     vendor = vendor_gemm_tflops(dev, M, 5120, 5120, dtype=act)
-    deq = "bf16(q*s)" if args.dtype == "bf16" else "f16(q*f16(s))"
+    deq = {"bf16": "bf16(q*s)", "f16": "f16(q*f16(s))", "f32": "fl32(q*s)"}[args.dtype]
+    peak = PEAK_TFLOPS[args.dtype]
     roofline = {
         "kernel": " + ".join(gemm_names) + f" (<0> fwd, <1> dX; {args.dtype} MFMA on the "
                                            f"dequantized weight {deq})",
-        "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
-        "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+        "bound": "mfma", "achieved": round(achieved, 2), "peak": peak,
+        "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
         "traffic": GEMM_TRAFFIC_BYTES,
         "traffic_note": GEMM_TRAFFIC_NOTE,
         "avg_launch_ms": {k: round(gemm_ms[k] / max(gemm_n[k], 1), 4) for k in gemm_ms},
         "launches": gemm_n,
-        "vendor_bf16_gemm": {"what": f"torch.matmul {args.dtype} (hipBLASLt), {M}x5120 by 5120x5120, "
+        "vendor_bf16_gemm": {"what": f"torch.matmul {args.dtype} (vendor library), {M}x5120 by 5120x5120, "
                                      "sustained ~1.5 s loop, same run", "tflops": round(vendor, 1),
                              "achieved_over_vendor": round(achieved / vendor, 4)},
     }

@@ -239,7 +239,7 @@ __global__ __launch_bounds__(256) void rowproj_f32_kernel(const float* __restric
   f32x4 acc[JT];
 #pragma unroll
   for (int i = 0; i < JT; ++i) acc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  constexpr int U = 4;
+  constexpr int U = 8;  // 8 k-chunks (8 KiB per wave) in flight
   for (int64_t k0 = 0; k0 < Kd; k0 += 16 * U) {
     f32x4 xv[U];
 #pragma unroll
@@ -289,7 +289,7 @@ __global__ __launch_bounds__(256) void colgrad_f32_kernel(const float* __restric
   using namespace f32c;
   constexpr int JT = 8;
   __shared__ float ss[TM][BO + 1];
-  __shared__ float sl[TM][128 + 1];
+  __shared__ __attribute__((aligned(16))) float sl[TM * 128];  // [tok][j], row stride r
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int l16 = lane & 15, lq = lane >> 4;
   const int64_t o0 = (int64_t)blockIdx.x * BO;
@@ -300,24 +300,52 @@ __global__ __launch_bounds__(256) void colgrad_f32_kernel(const float* __restric
   f32x4 acc[JT];
 #pragma unroll
   for (int i = 0; i < JT; ++i) acc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  for (int64_t mb = mbeg; mb < mend; mb += TM) {
-    // src tile [64 tokens][64 o]: 16 floats per thread in 4 f32x4
+  // the next token tile is loaded into registers while the current one is multiplied: the src
+  // tile [64 tokens][64 o] as 4 f32x4 per thread, the Lm tile [64 tokens][r] (64 r contiguous
+  // floats of Lm) as up to 8 f32x4 per thread
+  f32x4 rs[4], rl[8];
+  const int nl4 = TM * r / 4;
+  auto load = [&](int64_t mb) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int id = t + 256 * i, row = id >> 4, c4 = (id & 15) * 4;
       const int64_t mm = mb + row, o = o0 + c4;
-      f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-      if (mm < mend && o < Od) v = *reinterpret_cast<const f32x4*>(src + mm * Od + o);
+      rs[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      if (mm < mend && o < Od) rs[i] = *reinterpret_cast<const f32x4*>(src + mm * Od + o);
+    }
+    const int64_t lim = (mend - mb) * r;  // floats of the tile that belong to this split
 #pragma unroll
-      for (int e = 0; e < 4; ++e) ss[row][c4 + e] = v[e];
+    for (int i = 0; i < 8; ++i) {
+      const int id = t + 256 * i;
+      rl[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      const int64_t e0 = (int64_t)id * 4;  // whole vectors inside the split; the one across its
+      if (id < nl4 && e0 + 3 < lim) {      // end (r odd) element by element: no read past M r
+        rl[i] = *reinterpret_cast<const f32x4*>(Lm + mb * r + e0);
+      } else if (id < nl4 && e0 < lim) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (e0 + e < lim) rl[i][e] = Lm[mb * r + e0 + e];
+      }
     }
-    // Lm tile [64 tokens][r]
-    for (int id = t; id < TM * r; id += 256) {
-      const int row = id / r, j = id - row * r;
-      const int64_t mm = mb + row;
-      sl[row][j] = mm < mend ? Lm[mm * r + j] : 0.0f;
+  };
+  auto stash = [&]() {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int id = t + 256 * i, row = id >> 4, c4 = (id & 15) * 4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ss[row][c4 + e] = rs[i][e];
     }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int id = t + 256 * i;
+      if (id < nl4) *reinterpret_cast<f32x4*>(&sl[id * 4]) = rl[i];
+    }
+  };
+  if (mbeg < mend) load(mbeg);
+  for (int64_t mb = mbeg; mb < mend; mb += TM) {
+    stash();
     __syncthreads();
+    if (mb + TM < mend) load(mb + TM);
 #pragma unroll 4
     for (int ks = 0; ks < TM / 4; ++ks) {
       const int tok = ks * 4 + lq;
@@ -326,7 +354,7 @@ __global__ __launch_bounds__(256) void colgrad_f32_kernel(const float* __restric
       for (int jt = 0; jt < JT; ++jt) {
         if (jt >= jt_n) break;
         const int j = jt * 16 + l16;
-        const float av = j < r ? sl[tok][j] : 0.0f;
+        const float av = j < r ? sl[tok * r + j] : 0.0f;
         acc[jt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[jt], 0, 0, 0);
       }
     }
@@ -465,7 +493,8 @@ static WsF32 ws_f32(int64_t M, int64_t K, int64_t N, int64_t r, int which, const
   return w;
 }
 
-static int launch_f32gemm(const F32GemmArgs& a, hipStream_t st) {
+// mode 0 = forward, 1 = dX (names the launch in the kernel trace)
+static int launch_f32gemm(int mode, const F32GemmArgs& a, hipStream_t st) {
   using namespace f32g;
   static std::once_flag once;
   static hipError_t attr_err = hipSuccess;
@@ -476,7 +505,7 @@ static int launch_f32gemm(const F32GemmArgs& a, hipStream_t st) {
     return fail(REELS_HIP_EHIP, std::string("f32gemm: hipFuncSetAttribute: ") + hipGetErrorString(attr_err));
   if (a.M == 0 || a.Ncols == 0) return REELS_HIP_OK;
   const int tn = (int)ceil_div(a.Ncols, BN), tm = (int)ceil_div(a.M, BM);
-  { TraceScope _ts(st, "f32gemm_kernel"); f32gemm_kernel<<<tn * tm, NT, LDS, st>>>(a, tn, tm); }
+  { TraceScope _ts(st, mode == 0 ? "f32gemm_kernel<0>" : "f32gemm_kernel<1>"); f32gemm_kernel<<<tn * tm, NT, LDS, st>>>(a, tn, tm); }
   return check_launch("f32gemm_kernel");
 }
 
@@ -550,7 +579,7 @@ static int i8lora_fwd_f32_impl(const float* x, const int8_t* q, const float* sca
   F32GemmArgs g{};
   g.act = x; g.wd = wd; g.L = r > 0 ? h : nullptr; g.R = bt; g.bias = bias; g.out = y;
   g.M = M; g.Ncols = N; g.Kred = K; g.r = (int)r; g.c = c;
-  return launch_f32gemm(g, st);
+  return launch_f32gemm(0, g, st);
 }
 
 static int i8lora_bwd_f32_impl(const float* dy, const float* x, const float* hh, const int8_t* q,
@@ -629,7 +658,7 @@ static int i8lora_bwd_f32_impl(const float* dy, const float* x, const float* hh,
     F32GemmArgs g{};
     g.act = dy; g.wd = wt; g.L = r > 0 ? u : nullptr; g.R = A; g.bias = nullptr; g.out = dx;
     g.M = M; g.Ncols = K; g.Kred = N; g.r = (int)r; g.c = c;
-    if ((rc = launch_f32gemm(g, st))) return rc;
+    if ((rc = launch_f32gemm(1, g, st))) return rc;
   }
   // 3. dA = c x^T u ; dB = c (dy^T h)^T
   if (dA) {
