@@ -7,6 +7,7 @@
 // Fast path: K % 4 == 0, N % 4 == 0, 16-byte aligned pointers, r <= 128. Other shapes take the
 // one-output-per-thread kernels at the end of this file.
 #include <mutex>
+#include <type_traits>
 
 #include "common.h"
 #include "i8gemm.h"
@@ -81,19 +82,22 @@ struct F32GemmArgs {
 };
 
 namespace f32g {
-constexpr int BM = 128, BN = 128, BK = 32, NT = 256;
-constexpr int TILE = 128 * BK * 4;  // 16 KiB: 128 rows of 32 floats
+constexpr int BM = 128, BN = 128, BK = 16, NT = 256;
+constexpr int TILE = 128 * BK * 4;  // 8 KiB: 128 rows of 16 floats
 constexpr int STAGE = 2 * TILE;     // activation tile + weight tile
-constexpr int LDS = 2 * STAGE;      // 64 KiB: two stages, two workgroups per CU
+constexpr int NS = 5;               // ring depth: copies run 3 steps ahead of the MFMAs
+constexpr int LDS = NS * STAGE;     // 80 KiB: two workgroups per CU
 constexpr int GM = 4;
 }  // namespace f32g
 
-// 128 x 128 output tile, reduction step 32, 4 waves of 64 tokens x 64 columns (4 x 4 tiles of
-// v_mfma_f32_16x16x4_f32). Tiles [128][32] fp32 arrive through LDS-DMA copies into a two-stage
-// ring; rows of 128 bytes have their 16-byte chunks XOR-swizzled by row & 7, so a fragment read
-// (16 rows x 4 chunks) hits distinct banks. A lane reads 4 consecutive k of its row with one
-// ds_read_b128 and feeds them to 4 MFMAs, element j to the j-th: every lane of a 16-lane group
-// supplies the same k, so A and B agree on the k order and the sum is the full reduction.
+// 128 x 128 output tile, reduction step 16, 4 waves of 64 tokens x 64 columns (4 x 4 tiles of
+// v_mfma_f32_16x16x4_f32). Tiles [128][16] fp32 arrive through LDS-DMA copies into a five-stage
+// ring, issued three steps before their fragments are read; a wave waits only for the copies of
+// the step it is about to read (vmcnt counts its later copies still in flight). Rows are 64 bytes; the 16-byte chunk c of
+// row i sits in slot c ^ ((i >> 1) & 3), so the 8 rows read together by a fragment load (4 row
+// pairs sharing a 128-byte line) hit distinct banks. A lane reads 4 consecutive k of its row with
+// one ds_read_b128 and feeds them to 4 MFMAs, element j to the j-th: every lane of a 16-lane
+// group supplies the same k, so A and B agree on the k order and the sum is the full reduction.
 // D register v of lane l is output column 4 (l / 16) + v, token l % 16 of the 16 x 16 tile.
 __global__ __launch_bounds__(256, 2) void f32gemm_kernel(F32GemmArgs a, int tiles_n, int tiles_m) {
   using namespace f32g;
@@ -118,29 +122,30 @@ __global__ __launch_bounds__(256, 2) void f32gemm_kernel(F32GemmArgs a, int tile
   const int64_t m0 = (int64_t)(first_m + within % gm) * BM;
   const int64_t n0 = (int64_t)(within / gm) * BN;
 
-  // copies: copy i (0..3) of wave w fills rows (4w + i) * 8 + lane / 8, chunk (lane % 8) ^ row,
-  // 1 KiB of LDS. Rows past M / Ncols and chunks past Kred read beyond the buffer: zeros.
+  // copies: copy i (0..1) of wave w fills rows (2w + i) * 16 + lane / 4, slot lane % 4 (chunk
+  // (lane % 4) ^ ((row >> 1) & 3)), 1 KiB of LDS. Rows past M / Ncols and chunks past Kred read
+  // beyond the buffer: zeros.
   const i32x4 ract = buffer_rsrc(a.act, (uint32_t)(M * Kred * 4));
   const i32x4 rw = buffer_rsrc(a.wd, (uint32_t)(Ncols * Kred * 4));
-  uint32_t voa[4], vow[4];
-  int kc[4];
+  uint32_t voa[2], vow[2];
+  int kc[2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = (w * 4 + i) * 8 + (lane >> 3);
-    const int c = (lane & 7) ^ (row & 7);
+  for (int i = 0; i < 2; ++i) {
+    const int row = (w * 2 + i) * 16 + (lane >> 2);
+    const int c = (lane & 3) ^ ((row >> 1) & 3);
     kc[i] = c * 4;
     voa[i] = (uint32_t)(((m0 + row) * Kred + c * 4) * 4);
     vow[i] = (uint32_t)(((n0 + row) * Kred + c * 4) * 4);
   }
   const int nk = (int)((Kred + BK - 1) / BK);
-  auto issue = [&](int kt, int stage) {
-    uint8_t* base = smem + stage * STAGE;
+  auto issue = [&](int kt) {
+    uint8_t* base = smem + (kt % NS) * STAGE;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 2; ++i) {
       const bool in = (int64_t)kt * BK + kc[i] < Kred;
       const uint32_t adv = (uint32_t)kt * (BK * 4);
-      dma16(ract, in ? voa[i] + adv : 0xFFFFFFF0u, 0u, base + (w * 4 + i) * 1024);
-      dma16(rw, in ? vow[i] + adv : 0xFFFFFFF0u, 0u, base + TILE + (w * 4 + i) * 1024);
+      dma16(ract, in ? voa[i] + adv : 0xFFFFFFF0u, 0u, base + (w * 2 + i) * 1024);
+      dma16(rw, in ? vow[i] + adv : 0xFFFFFFF0u, 0u, base + TILE + (w * 2 + i) * 1024);
     }
   };
 
@@ -150,74 +155,186 @@ __global__ __launch_bounds__(256, 2) void f32gemm_kernel(F32GemmArgs a, int tile
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  const int swz = l16 & 7;  // fragment rows start at multiples of 16
-  issue(0, 0);
-  for (int kt = 0; kt < nk; ++kt) {
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): step kt has landed
-    __syncthreads();                     // ... for every wave; stage (kt + 1) & 1 is free
-    if (kt + 1 < nk) issue(kt + 1, (kt + 1) & 1);
-    const uint8_t* sa = smem + (kt & 1) * STAGE;
-    const uint8_t* sw = sa + TILE;
+  const int off = (lq ^ ((l16 >> 1) & 3)) << 4;  // fragment rows start at multiples of 16
+  const uint32_t frag = (uint32_t)(uintptr_t)LDS_PTR(const uint8_t, smem) + off;
+  const uint32_t fx = frag + (wm * 64 + l16) * 64, fw = frag + TILE + (wn * 64 + l16) * 64;
+  // The fragment reads are inline assembly, invisible to the compiler's wait insertion: the
+  // reads of the next step then overlap this step's MFMAs, and the waits are placed by hand.
+  // A wait names the fragments it releases as operands, so no MFMA moves above it.
+  auto rd = [&](int kt, f32x4(&xf)[4], f32x4(&wf)[4]) {
+    const uint32_t sb = (uint32_t)((kt % NS) * STAGE);
+    asm volatile(
+        "ds_read_b128 %0, %8\n\t"
+        "ds_read_b128 %1, %8 offset:1024\n\t"
+        "ds_read_b128 %2, %8 offset:2048\n\t"
+        "ds_read_b128 %3, %8 offset:3072\n\t"
+        "ds_read_b128 %4, %9\n\t"
+        "ds_read_b128 %5, %9 offset:1024\n\t"
+        "ds_read_b128 %6, %9 offset:2048\n\t"
+        "ds_read_b128 %7, %9 offset:3072"
+        : "=&v"(xf[0]), "=&v"(xf[1]), "=&v"(xf[2]), "=&v"(xf[3]), "=&v"(wf[0]), "=&v"(wf[1]),
+          "=&v"(wf[2]), "=&v"(wf[3])  // early clobber: the data returns while addresses are in use
+        : "v"(fx + sb), "v"(fw + sb)
+        : "memory");
+  };
+  // lgkmcnt(n): at most n of this wave's LDS reads still in flight
+  auto release = [&](f32x4(&xf)[4], f32x4(&wf)[4], auto n) {
+    asm volatile("s_waitcnt lgkmcnt(%8)"
+                 : "+v"(xf[0]), "+v"(xf[1]), "+v"(xf[2]), "+v"(xf[3]), "+v"(wf[0]), "+v"(wf[1]),
+                   "+v"(wf[2]), "+v"(wf[3])
+                 : "n"(decltype(n)::value));
+  };
+  auto mm = [&](const f32x4(&xf)[4], const f32x4(&wf)[4]) {
 #pragma unroll
-    for (int sb = 0; sb < 2; ++sb) {
-      const int off = ((4 * sb + lq) ^ swz) << 4;
-      f32x4 xf[4], wf[4];
-#pragma unroll
-      for (int tj = 0; tj < 4; ++tj)
-        xf[tj] = *reinterpret_cast<const f32x4*>(sa + (wm * 64 + tj * 16 + l16) * 128 + off);
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int ti = 0; ti < 4; ++ti)
-        wf[ti] = *reinterpret_cast<const f32x4*>(sw + (wn * 64 + ti * 16 + l16) * 128 + off);
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+        for (int tj = 0; tj < 4; ++tj)
+          acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x4f32(wf[ti][j], xf[tj][j], acc[ti][tj], 0, 0, 0);
+  };
+  // wait until this wave's copies of step s have landed, given that the copies of every step up
+  // to min(last, nk - 1) were issued after them (4 per step)
+  auto wait_step = [&](int s, int last) {
+    const int later = (last < nk - 1 ? last : nk - 1) - s;
+    if (later >= 3) __builtin_amdgcn_s_waitcnt(0x0F7C);       // vmcnt(12)
+    else if (later == 2) __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8)
+    else if (later == 1) __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4)
+    else __builtin_amdgcn_s_waitcnt(0x0F70);                  // vmcnt(0)
+  };
+  using zero = std::integral_constant<int, 0>;
+  using eight = std::integral_constant<int, 8>;
+  // Fragments are read one step ahead into the second register set. At the barrier of step kt
+  // every wave's copies of step kt + 1 have landed and every wave has consumed its fragments of
+  // step kt - 1, whose stage the copies of step kt + 4 then refill. Scheduling fences keep every
+  // LDS access on its side of the barriers.
+  f32x4 xa[4], wa[4], xb[4], wb[4];
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s)
+    if (s < nk) issue(s);
+  wait_step(0, NS - 2);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  rd(0, xa, wa);
+  release(xa, wa, zero());  // lgkmcnt holds 15: never more than 8 reads in flight
+  __builtin_amdgcn_sched_barrier(0);
+  auto step = [&](int kt, f32x4(&xc)[4], f32x4(&wc)[4], f32x4(&xn)[4], f32x4(&wn_)[4]) {
+    if (kt + 1 < nk) {
+      wait_step(kt + 1, kt + NS - 2);
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      if (kt + NS - 1 < nk) issue(kt + NS - 1);
+      rd(kt + 1, xn, wn_);
+      release(xc, wc, eight());  // the 8 reads just issued may still be in flight
+    } else {
+      release(xc, wc, zero());
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    mm(xc, wc);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // steady state, no branches: the copies of steps kt + 2 and kt + 3 stay in flight
+  int kt = 0;
+  for (; kt + NS < nk; kt += 2) {
+    __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8)
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    issue(kt + NS - 1);
+    rd(kt + 1, xb, wb);
+    release(xa, wa, eight());
+    __builtin_amdgcn_sched_barrier(0);
+    mm(xa, wa);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0x0F78);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    issue(kt + NS);
+    rd(kt + 2, xa, wa);
+    release(xb, wb, eight());
+    __builtin_amdgcn_sched_barrier(0);
+    mm(xb, wb);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // the last steps: fewer copies in flight, nothing to read after the final one
+  for (; kt + 1 < nk; kt += 2) {
+    step(kt, xa, wa, xb, wb);
+    step(kt + 1, xb, wb, xa, wa);
+  }
+  if (kt < nk) step(kt, xa, wa, xb, wb);
+
+  // epilogue: the rank-r term on MFMA from global L and R (k in steps of 16: lane supplies 4
+  // consecutive j, zeros past r), bias, fp32 stores of 4 consecutive columns per lane. With
+  // r % 4 == 0 (rows 16-byte aligned) the 4 j of a lane come in one load.
+  const int r = a.r;
+  // the bias of this lane's 4 x 4 output columns, loaded before any store: a load between the
+  // stores would make each store wait for the previous ones (vmcnt counts both)
+  f32x4 bs[4];
+#pragma unroll
+  for (int ti = 0; ti < 4; ++ti) {
+    const int64_t nb = n0 + wn * 64 + ti * 16 + lq * 4;
+    bs[ti] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (a.bias != nullptr && nb < Ncols) bs[ti] = *reinterpret_cast<const f32x4*>(a.bias + nb);
+  }
+  f32x4 lor[4][4];
+#pragma unroll
+  for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+    for (int tj = 0; tj < 4; ++tj) lor[ti][tj] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  if (a.L != nullptr) {
+    const bool vec = (r & 3) == 0;
+    for (int j0 = 0; j0 < r; j0 += 16) {
+      const int jl = j0 + lq * 4;
+      f32x4 lv[4], rv[4];
+#pragma unroll
+      for (int tj = 0; tj < 4; ++tj) {
+        const int64_t m = m0 + wm * 64 + tj * 16 + l16;
+        lv[tj] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (m < M && jl < r) {
+          if (vec) {
+            lv[tj] = *reinterpret_cast<const f32x4*>(a.L + m * r + jl);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (jl + e < r) lv[tj][e] = a.L[m * r + jl + e];
+          }
+        }
+      }
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti) {
+        const int64_t nrow = n0 + wn * 64 + ti * 16 + l16;  // this lane's R row
+        rv[ti] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (nrow < Ncols && jl < r) {
+          if (vec) {
+            rv[ti] = *reinterpret_cast<const f32x4*>(a.R + nrow * r + jl);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (jl + e < r) rv[ti][e] = a.R[nrow * r + jl + e];
+          }
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
 #pragma unroll
         for (int ti = 0; ti < 4; ++ti)
 #pragma unroll
           for (int tj = 0; tj < 4; ++tj)
-            acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x4f32(wf[ti][j], xf[tj][j], acc[ti][tj], 0, 0, 0);
+            lor[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x4f32(rv[ti][e], lv[tj][e], lor[ti][tj], 0, 0, 0);
     }
   }
-
-  // epilogue: the rank-r term on MFMA from global L and R (k in steps of 16: lane supplies 4
-  // consecutive j, zeros past r), bias, fp32 stores of 4 consecutive columns per lane
-  const int r = a.r;
+  // one wait for every load, outside any branch: the compiler then knows the bias has arrived
+  // on every path and puts no wait (which would include the stores) between the stores
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
 #pragma unroll
   for (int ti = 0; ti < 4; ++ti) {
-    const int64_t nrow = n0 + wn * 64 + ti * 16 + l16;       // this lane's R row
-    const int64_t nb = n0 + wn * 64 + ti * 16 + lq * 4;      // this lane's 4 output columns
-    f32x4 lor[4];
-#pragma unroll
-    for (int tj = 0; tj < 4; ++tj) lor[tj] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    if (a.L != nullptr) {
-      for (int j0 = 0; j0 < r; j0 += 16) {
-        const int jl = j0 + lq * 4;
-        f32x4 rv = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (nrow < Ncols)
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (jl + e < r) rv[e] = a.R[nrow * r + jl + e];
-#pragma unroll
-        for (int tj = 0; tj < 4; ++tj) {
-          const int64_t m = m0 + wm * 64 + tj * 16 + l16;
-          f32x4 lv = {0.0f, 0.0f, 0.0f, 0.0f};
-          if (m < M)
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (jl + e < r) lv[e] = a.L[m * r + jl + e];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) lor[tj] = __builtin_amdgcn_mfma_f32_16x16x4f32(rv[e], lv[e], lor[tj], 0, 0, 0);
-        }
-      }
-    }
-    f32x4 bs = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (a.bias != nullptr && nb < Ncols) bs = *reinterpret_cast<const f32x4*>(a.bias + nb);
+    const int64_t nb = n0 + wn * 64 + ti * 16 + lq * 4;  // this lane's 4 output columns
 #pragma unroll
     for (int tj = 0; tj < 4; ++tj) {
       const int64_t m = m0 + wm * 64 + tj * 16 + l16;
       if (m < M && nb < Ncols) {
         f32x4 o;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) o[v] = (acc[ti][tj][v] + bs[v]) + a.c * lor[tj][v];
+        for (int v = 0; v < 4; ++v) o[v] = (acc[ti][tj][v] + bs[ti][v]) + a.c * lor[ti][tj][v];
         *reinterpret_cast<f32x4*>(a.out + m * Ncols + nb) = o;
       }
     }
