@@ -169,6 +169,9 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(const T* __restrict__ w,
       int64_t c = lane + 64 * (int64_t)i;
       if (c < chunks) Elem<T>::mag(cache[i], mb);
     }
+    // every cached load has been used: saying so outside the branches keeps the compiler from
+    // waiting before each store below (its wait would include the earlier stores)
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   } else {
     for (int64_t c = lane; c < chunks; c += 64) Elem<T>::mag(row[c], mb);
   }
