@@ -71,27 +71,39 @@ __global__ __launch_bounds__(256) void rowproj_kernel(const uint16_t* __restrict
   const int nchunks = (int)((Kd + KC - 1) / KC);
   // loader roles: X chunk = ROWS rows x 32 16-byte chunks, ROWS/8 per thread; P chunk = 32RT
   // rows, 4RT per thread
-  u32x4 rx[ROWS / 8], rpv[4 * RT];
-  auto load = [&](int ck) {
+  // two register stages: the copies of chunks ck + 1 and ck + 2 are in flight while chunk ck is
+  // multiplied
+  typedef u32x4 XS[ROWS / 8];
+  typedef u32x4 PS[4 * RT];
+  XS rx0, rx1;
+  PS rp0, rp1;
+  // Buffer loads: a descriptor over this block's rows of src (and one over P) returns zeros for
+  // offsets past its end, so rows past M, columns past Kd (offset moved out of range) and chunks
+  // past the last need no branch. Branch-free loads keep the compiler's waits exact: a stash
+  // waits only for its own stage.
+  const int64_t rows_here = (M - m0) < ROWS ? (M - m0) : ROWS;
+  const __amdgpu_buffer_rsrc_t rsx = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(src + m0 * Kd), (short)0, (int)(rows_here * Kd * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsp = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(r > 0 ? P : src), (short)0, r > 0 ? (int)(r * Kd * 2) : 0, 0x00020000);
+  auto load = [&](int ck, XS& rx, PS& rpv) {
     const int64_t k0 = (int64_t)ck * KC;
 #pragma unroll
     for (int i = 0; i < ROWS / 8; ++i) {
       const int row = (t >> 5) + 8 * i, c = t & 31;
-      const int64_t m = m0 + row, k = k0 + c * 8;
-      u32x4 v = {0, 0, 0, 0};
-      if (m < M && k < Kd) v = *reinterpret_cast<const u32x4*>(src + m * Kd + k);
-      rx[i] = v;
+      const int64_t k = k0 + c * 8;
+      const uint32_t off = k < Kd ? (uint32_t)((row * Kd + k) * 2) : 0x80000000u;
+      rx[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsx, off, 0, 2));  // nt
     }
 #pragma unroll
     for (int i = 0; i < 4 * RT; ++i) {
       const int row = (t >> 5) + 8 * i, c = t & 31;
       const int64_t k = k0 + c * 8;
-      u32x4 v = {0, 0, 0, 0};
-      if (row < r && k < Kd) v = *reinterpret_cast<const u32x4*>(P + (int64_t)row * Kd + k);
-      rpv[i] = v;
+      const uint32_t off = k < Kd ? (uint32_t)((row * Kd + k) * 2) : 0x80000000u;
+      rpv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsp, off, 0, 0));
     }
   };
-  auto stash = [&](int ck) {
+  auto stash = [&](int ck, const XS& rx, const PS& rpv) {
     const int64_t k0 = (int64_t)ck * KC;
 #pragma unroll
     for (int i = 0; i < ROWS / 8; ++i) {
@@ -125,11 +137,7 @@ __global__ __launch_bounds__(256) void rowproj_kernel(const uint16_t* __restrict
     for (int j = 0; j < RT; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[g][j][v] = 0.0f;
-  load(0);
-  for (int ck = 0; ck < nchunks; ++ck) {
-    stash(ck);
-    __syncthreads();
-    if (ck + 1 < nchunks) load(ck + 1);
+  auto compute = [&]() {
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const int col = wave * 64 + ks * 16 + lhi * 8;
@@ -145,7 +153,24 @@ __global__ __launch_bounds__(256) void rowproj_kernel(const uint16_t* __restrict
           acc[g][j] = E::mfma32(a[g], bv, acc[g][j]);
       }
     }
+  };
+  // chunk ck: its registers to LDS, the copies of chunk ck + 2 into the freed registers, the
+  // MFMAs on chunk ck
+  // (a chunk past the end reads only zeros: its columns are past Kd)
+  auto step = [&](int ck, XS& rx, PS& rpv) {
+    stash(ck, rx, rpv);
     __syncthreads();
+    load(ck + 2, rx, rpv);
+    compute();
+    __syncthreads();
+  };
+  // steps in pairs, the second unconditional (with an odd chunk count the last one is all
+  // zeros): a branch around it would make the compiler's waits drain both stages
+  load(0, rx0, rp0);
+  load(1, rx1, rp1);
+  for (int ck = 0; ck < nchunks; ck += 2) {
+    step(ck, rx0, rp0);
+    step(ck + 1, rx1, rp1);
   }
   if (out == nullptr) return;
   // D lane layout: row (token) = g*32 + (v/4)*8 + lhi*4 + v%4, column (j) = t*32 + l32.
@@ -208,28 +233,38 @@ __global__ __launch_bounds__(256) void colgrad_kernel(const uint16_t* __restrict
 
   const int g = lane >> 4, i16 = lane & 15;
   const int jj = i16 >> 2, qq = i16 & 3;  // providing-lane roles for the transpose reads
-  // register staging of the next token step: src tile [64 tokens][128 o] (4 chunks per thread),
-  // Lm tile [64 tokens][32*RT] (RT chunks per thread)
-  u32x4 rs[4], rl[RT];
-  auto load = [&](int64_t mb) {
+  // register staging, two stages: src tile [64 tokens][128 o] (4 chunks per thread), Lm tile
+  // [64 tokens][32*RT] (RT chunks per thread); the copies of token steps s + 1 and s + 2 are in
+  // flight while step s is multiplied. Buffer loads through descriptors over the step's tokens
+  // return zeros past their end (tokens past the split, a step past the last) and for offsets
+  // moved out of range (columns past Od or rp), so the loads need no branch and the compiler's
+  // waits count only the older stage.
+  typedef u32x4 SS[4];
+  typedef u32x4 LS[RT];
+  SS rs0, rs1;
+  LS rl0, rl1;
+  auto load = [&](int64_t mb, SS& rs, LS& rl) {
+    const int64_t nt = mend - mb < TM ? (mend - mb > 0 ? mend - mb : 0) : TM;
+    const int64_t mc = mb < mend ? mb : mbeg;  // a valid base for an empty descriptor
+    const __amdgpu_buffer_rsrc_t rss = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(src + mc * Od), (short)0, (int)(nt * Od * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsl = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(Lm + mc * rp), (short)0, (int)(nt * rp * 2), 0x00020000);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int id = tid + 256 * i, row = id >> 4, c = id & 15;
-      const int64_t m = mb + row, o = o0 + c * 8;
-      u32x4 v = {0, 0, 0, 0};
-      if (m < mend && o < Od) v = *reinterpret_cast<const u32x4*>(src + m * Od + o);
-      rs[i] = v;
+      const int64_t o = o0 + c * 8;
+      const uint32_t off = o < Od ? (uint32_t)((row * Od + o) * 2) : 0x80000000u;
+      rs[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rss, off, 0, 2));  // nt
     }
 #pragma unroll
     for (int i = 0; i < RT; ++i) {
       const int id = tid + 256 * i, row = id / (RT * 4), c = id % (RT * 4);
-      const int64_t m = mb + row;
-      u32x4 v = {0, 0, 0, 0};
-      if (row < TM && m < mend && c * 8 < rp) v = *reinterpret_cast<const u32x4*>(Lm + m * rp + c * 8);
-      rl[i] = v;
+      const uint32_t off = c * 8 < rp ? (uint32_t)((row * rp + c * 8) * 2) : 0x80000000u;
+      rl[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsl, off, 0, 0));
     }
   };
-  auto stash = [&]() {
+  auto stash = [&](const SS& rs, const LS& rl) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int id = tid + 256 * i, row = id >> 4, c = id & 15;
@@ -241,11 +276,7 @@ __global__ __launch_bounds__(256) void colgrad_kernel(const uint16_t* __restrict
       if (row < TM) *reinterpret_cast<u32x4*>(&slm[row * LROW + c * 8]) = rl[i];
     }
   };
-  if (mbeg < mend) load(mbeg);
-  for (int64_t mb = mbeg; mb < mend; mb += TM) {
-    stash();
-    __syncthreads();
-    if (mb + TM < mend) load(mb + TM);
+  auto compute = [&]() {
 #pragma unroll
     for (int ks = 0; ks < TM / 16; ++ks) {
       // A operand: src^T rows o = wave*32 + (0..31), tokens ks*16 + (lane/32)*8 + (0..7)
@@ -274,7 +305,23 @@ __global__ __launch_bounds__(256) void colgrad_kernel(const uint16_t* __restrict
         acc[t] = E::mfma32(E::as8(av), E::as8(bv), acc[t]);
       }
     }
+  };
+  // token step at mb: its registers to LDS, the copies of step mb + 2 TM into the freed
+  // registers, the MFMAs on step mb
+  auto step = [&](int64_t mb, SS& rs, LS& rl) {
+    stash(rs, rl);
     __syncthreads();
+    load(mb + 2 * TM, rs, rl);
+    compute();
+    __syncthreads();
+  };
+  // steps in pairs, the second unconditional (past the split's end it reads only zeros): a
+  // branch around it would make the compiler's waits drain both stages
+  load(mbeg, rs0, rl0);
+  load(mbeg + TM, rs1, rl1);
+  for (int64_t mb = mbeg; mb < mend; mb += 2 * TM) {
+    step(mb, rs0, rl0);
+    step(mb + TM, rs1, rl1);
   }
   // D lane layout: row (o) = wave*32 + (v/4)*8 + (lane/32)*4 + v%4, column j = t*32 + lane%32
   const int l32 = lane & 31, lhi = lane >> 5;
@@ -416,26 +463,48 @@ __global__ void gelu_bwd_kernel(const uint16_t* __restrict__ x, const uint16_t* 
 
 // ---------------------------------------------------------------------------------------------
 // host side
+// Split-M plan of one gradient pass over a [M][Od] operand: enough token splits that the
+// ceil(Od / 128) column blocks times the splits fill one round of the GPU's workgroup slots
+// (256 CUs x 4 resident gradient workgroups), at most 32 splits (the partials buffer), tokens per
+// split a multiple of 128 (the kernel takes token steps of 64 in pairs).
+struct Split {
+  int splits;
+  int64_t tps;  // tokens per split
+};
+
+static Split split_for(int64_t M, int64_t Od) {
+  constexpr int64_t kSlots = 1024;
+  const int64_t colblocks = (Od + cg::BO - 1) / cg::BO;
+  int64_t s = kSlots / (colblocks > 0 ? colblocks : 1);
+  if (s > 32) s = 32;
+  if (s > (M + 127) / 128) s = (M + 127) / 128;
+  if (s < 1) s = 1;
+  Split sp;
+  sp.tps = ((M + s - 1) / s + 127) / 128 * 128;
+  if (sp.tps < 128) sp.tps = 128;
+  sp.splits = (int)((M + sp.tps - 1) / sp.tps);
+  if (sp.splits < 1) sp.splits = 1;
+  return sp;
+}
+
 struct Plan {
   bool fast;
   bool deq;     // fast and K, N multiples of 64: dequantized weight + bf16 GEMM
   int rp;       // row stride of h/u buffers
-  int splits;   // split-M count for dA/dB
-  int64_t tps;  // tokens per split (multiple of 64)
+  Split sa;     // dA: columns of x (K)
+  Split sb;     // dB: columns of dy (N)
 };
 
 static Plan make_plan(int64_t M, int64_t K, int64_t N, int64_t r, bool ptrs_aligned) {
   Plan p;
-  p.fast = ptrs_aligned && (K % 16 == 0) && (N % 16 == 0) && (r % 16 == 0) && r <= 128;
+  // K, N < 2^22 keeps the projection and gradient kernels' buffer descriptors (64 rows, or the
+  // rank-128 operand, of one row length) below 2^31 bytes
+  p.fast = ptrs_aligned && (K % 16 == 0) && (N % 16 == 0) && (r % 16 == 0) && r <= 128 &&
+           K < ((int64_t)1 << 22) && N < ((int64_t)1 << 22);
   p.deq = p.fast && bfgemm_supported(M, N, K) && bfgemm_supported(M, K, N);
   p.rp = (int)r;
-  int64_t s = (M + 1023) / 1024;
-  if (s < 1) s = 1;
-  if (s > 32) s = 32;
-  p.tps = ((M + s - 1) / s + 63) / 64 * 64;
-  if (p.tps < 64) p.tps = 64;
-  p.splits = (int)((M + p.tps - 1) / p.tps);
-  if (p.splits < 1) p.splits = 1;
+  p.sa = split_for(M, K);
+  p.sb = split_for(M, N);
   return p;
 }
 
@@ -457,8 +526,8 @@ static WsLayout ws_layout(int64_t M, int64_t K, int64_t N, int64_t r, int which,
   } else {
     w.u = take((size_t)M * rp * 2);
     w.dys = take(p.fast && !p.deq ? (size_t)M * N * 2 : 0);
-    w.pa = take(p.fast && r > 0 ? (size_t)p.splits * K * rp * 4 : 0);
-    w.pb = take(p.fast && r > 0 ? (size_t)p.splits * N * rp * 4 : 0);
+    w.pa = take(p.fast && r > 0 ? (size_t)p.sa.splits * K * rp * 4 : 0);
+    w.pb = take(p.fast && r > 0 ? (size_t)p.sb.splits * N * rp * 4 : 0);
   }
   w.total = off == 0 ? 256 : off;
   return w;
@@ -497,7 +566,7 @@ static int launch_rowproj(int elt, const uint16_t* src, int64_t M, int64_t Kd, c
 }
 
 static int launch_colgrad(int elt, const uint16_t* src, int64_t M, int64_t Od, const uint16_t* Lm,
-                          int r, int rp, const Plan& p, float c, float* part, float* out,
+                          int r, int rp, const Split& p, float c, float* part, float* out,
                           bool trans, hipStream_t st) {
   const dim3 grid((unsigned)ceil_div(Od, cg::BO), (unsigned)p.splits);
   const int rt = (rp + 31) / 32;
@@ -705,7 +774,7 @@ static int i8lora_bwd_impl(int elt, const char* fn, const void* dy, const void* 
   }
   // 3. dA = c x^T u ; dB = c (dy^T h)^T
   if (dA) {
-    if ((rc = launch_colgrad(elt, xb, M, K, u, (int)r, p.rp, p, lora_scale,
+    if ((rc = launch_colgrad(elt, xb, M, K, u, (int)r, p.rp, p.sa, lora_scale,
                              reinterpret_cast<float*>(ws + w.pa), dA, false, st))) return rc;
   }
   if (dB) {
@@ -718,7 +787,7 @@ static int i8lora_bwd_impl(int elt, const char* fn, const void* dy, const void* 
       if ((rc = launch_rowproj(elt, xb, M, K, at, (int)r, p.rp, hw, nullptr, nullptr, st))) return rc;
       hh = hw;
     }
-    if ((rc = launch_colgrad(elt, dyb, M, N, hh, (int)r, p.rp, p, lora_scale,
+    if ((rc = launch_colgrad(elt, dyb, M, N, hh, (int)r, p.rp, p.sb, lora_scale,
                              reinterpret_cast<float*>(ws + w.pb), dB, true, st))) return rc;
   }
   return REELS_HIP_OK;
