@@ -54,6 +54,10 @@ def lib():
         L.oracle_gelu_tanh_backward.argtypes = [vp, vp, vp, i64, ci]
         L.oracle_f16_to_f32_array.argtypes = [vp, vp, i64]
         L.oracle_f32_to_f16_array.argtypes = [vp, vp, i64]
+        L.oracle_attention_forward.argtypes = [vp, vp, vp, vp, ci, i64, i64, i64, i64, i64, ci,
+                                               vp, vp]
+        L.oracle_attention_backward.argtypes = [vp, vp, vp, vp, vp, ci, i64, i64, i64, i64, i64,
+                                                ci, vp, vp, vp]
         L.oracle_philox4x32_10.argtypes = [vp, vp, vp]
         L.oracle_normal_bf16.argtypes = [ctypes.c_uint64, ctypes.c_uint32, i64, ctypes.c_double,
                                          ctypes.c_double, ctypes.c_double, vp]
@@ -266,3 +270,40 @@ def reference_fp16_forward(x, q, s, A, B, c, bias=None):
     ad = (h.astype(np.float32) @ B16.astype(np.float32)).astype(f16)
     adapter = np.float32(c) * ad.astype(np.float32)
     return y.astype(np.float32) + adapter
+
+
+def _att_args(q, k, v, mask, elt):
+    st = _STORE[elt]
+    q = _c(q, st); k = _c(k, st); v = _c(v, st)
+    B, Sq, H, D = q.shape
+    Sk = k.shape[1]
+    assert k.shape == (B, Sk, H, D) and v.shape == (B, Sk, H, D)
+    m = None if mask is None else np.ascontiguousarray(mask, dtype=np.uint8)
+    assert m is None or m.shape == (Sq, Sk)
+    return q, k, v, m, B, Sq, Sk, H, D
+
+
+def attention_forward(q, k, v, mask=None, causal=False, elt="bf16"):
+    """f64 restatement of memory_efficient_attention (attention.jl:106-172). q [B][Sq][H][D], k and
+    v [B][Sk][H][D] (16-bit patterns as uint16, or float32 with elt="f32"); mask [Sq][Sk] bool
+    (True = visible) or None. Returns (out [B][Sq][H][D] f64, lse [B][H][Sq] f64)."""
+    q, k, v, m, B, Sq, Sk, H, D = _att_args(q, k, v, mask, elt)
+    out = np.empty((B, Sq, H, D), np.float64)
+    lse = np.empty((B, H, Sq), np.float64)
+    lib().oracle_attention_forward(_p(q), _p(k), _p(v), _p(m), int(bool(causal)), B, Sq, Sk, H, D,
+                                   _ELT[elt], _p(out), _p(lse))
+    return out, lse
+
+
+def attention_backward(q, k, v, dy, mask=None, causal=False, elt="bf16"):
+    """f64 restatement of memory_efficient_attention_backward (attention.jl:174-221): returns
+    (dq, dk, dv) in the q / k / v layouts."""
+    q, k, v, m, B, Sq, Sk, H, D = _att_args(q, k, v, mask, elt)
+    dy = _c(dy, _STORE[elt])
+    assert dy.shape == q.shape
+    dq = np.empty(q.shape, np.float64)
+    dk = np.empty(k.shape, np.float64)
+    dv = np.empty(v.shape, np.float64)
+    lib().oracle_attention_backward(_p(q), _p(k), _p(v), _p(dy), _p(m), int(bool(causal)), B, Sq,
+                                    Sk, H, D, _ELT[elt], _p(dq), _p(dk), _p(dv))
+    return dq, dk, dv

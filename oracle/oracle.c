@@ -320,6 +320,110 @@ void oracle_gelu_tanh_backward(const void* x, const void* dy, void* dx, int64_t 
 }
 
 /* ---- Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11) ------------------------------------ */
+/* ---- attention (attention.jl:106-221) ---------------------------------------------------- */
+static double att_scale(int64_t D) { return (double)(1.0f / sqrtf((float)D)); }
+
+static int att_visible(const uint8_t* mask, int causal, int64_t Sk, int64_t i, int64_t j) {
+  if (mask && !mask[i * Sk + j]) return 0;
+  if (causal && j > i) return 0;
+  return 1;
+}
+
+/* scores and probabilities of query i of head (b, h): p[j] = exp(s_j - m) / l over visible keys,
+ * 0 elsewhere; returns lse (NaN when no key is visible, p then all NaN-free zeros) */
+static double att_row(const void* q, const void* k, const uint8_t* mask, int causal, int64_t b,
+                      int64_t i, int64_t h, int64_t Sq, int64_t Sk, int64_t H, int64_t D, int elt,
+                      double* s, double* p) {
+  const double sc = att_scale(D);
+  const int64_t qo = ((b * Sq + i) * H + h) * D;
+  double m = -INFINITY;
+  int any = 0;
+  for (int64_t j = 0; j < Sk; ++j) {
+    if (!att_visible(mask, causal, Sk, i, j)) { s[j] = -INFINITY; continue; }
+    const int64_t ko = ((b * Sk + j) * H + h) * D;
+    double acc = 0.0;
+    for (int64_t d = 0; d < D; ++d) acc += (double)inel(q, qo + d, elt) * (double)inel(k, ko + d, elt);
+    s[j] = acc * sc;
+    if (s[j] > m) m = s[j];
+    any = 1;
+  }
+  if (!any) {
+    for (int64_t j = 0; j < Sk; ++j) p[j] = 0.0;
+    return NAN;
+  }
+  double l = 0.0;
+  for (int64_t j = 0; j < Sk; ++j) { p[j] = isfinite(s[j]) ? exp(s[j] - m) : 0.0; l += p[j]; }
+  for (int64_t j = 0; j < Sk; ++j) p[j] /= l;
+  return m + log(l);
+}
+
+void oracle_attention_forward(const void* q, const void* k, const void* v, const uint8_t* mask,
+                              int causal, int64_t B, int64_t Sq, int64_t Sk, int64_t H, int64_t D,
+                              int elt, double* out, double* lse) {
+  double* s = (double*)malloc(sizeof(double) * (size_t)(Sk > 0 ? Sk : 1));
+  double* p = (double*)malloc(sizeof(double) * (size_t)(Sk > 0 ? Sk : 1));
+  for (int64_t b = 0; b < B; ++b)
+    for (int64_t h = 0; h < H; ++h)
+      for (int64_t i = 0; i < Sq; ++i) {
+        const double L = att_row(q, k, mask, causal, b, i, h, Sq, Sk, H, D, elt, s, p);
+        if (lse) lse[(b * H + h) * Sq + i] = L;
+        if (!out) continue;
+        double* o = out + ((b * Sq + i) * H + h) * D;
+        for (int64_t d = 0; d < D; ++d) o[d] = isnan(L) ? NAN : 0.0;
+        if (isnan(L)) continue;
+        for (int64_t j = 0; j < Sk; ++j) {
+          if (p[j] == 0.0) continue;
+          const int64_t vo = ((b * Sk + j) * H + h) * D;
+          for (int64_t d = 0; d < D; ++d) o[d] += p[j] * (double)inel(v, vo + d, elt);
+        }
+      }
+  free(s);
+  free(p);
+}
+
+void oracle_attention_backward(const void* q, const void* k, const void* v, const void* dy,
+                               const uint8_t* mask, int causal, int64_t B, int64_t Sq, int64_t Sk,
+                               int64_t H, int64_t D, int elt, double* dq, double* dk, double* dv) {
+  const double sc = att_scale(D);
+  double* s = (double*)malloc(sizeof(double) * (size_t)(Sk > 0 ? Sk : 1));
+  double* p = (double*)malloc(sizeof(double) * (size_t)(Sk > 0 ? Sk : 1));
+  double* o = (double*)malloc(sizeof(double) * (size_t)(D > 0 ? D : 1));
+  if (dq) for (int64_t i = 0; i < B * Sq * H * D; ++i) dq[i] = 0.0;
+  if (dk) for (int64_t i = 0; i < B * Sk * H * D; ++i) dk[i] = 0.0;
+  if (dv) for (int64_t i = 0; i < B * Sk * H * D; ++i) dv[i] = 0.0;
+  for (int64_t b = 0; b < B; ++b)
+    for (int64_t h = 0; h < H; ++h)
+      for (int64_t i = 0; i < Sq; ++i) {
+        const double L = att_row(q, k, mask, causal, b, i, h, Sq, Sk, H, D, elt, s, p);
+        const int64_t qo = ((b * Sq + i) * H + h) * D;
+        /* the output of this query, and the correction sum(dy .* out) (attention.jl:190) */
+        for (int64_t d = 0; d < D; ++d) o[d] = isnan(L) ? NAN : 0.0;
+        if (!isnan(L))
+          for (int64_t j = 0; j < Sk; ++j) {
+            if (p[j] == 0.0) continue;
+            const int64_t vo = ((b * Sk + j) * H + h) * D;
+            for (int64_t d = 0; d < D; ++d) o[d] += p[j] * (double)inel(v, vo + d, elt);
+          }
+        double corr = 0.0;
+        for (int64_t d = 0; d < D; ++d) corr += (double)inel(dy, qo + d, elt) * o[d];
+        for (int64_t j = 0; j < Sk; ++j) {
+          if (!isfinite(s[j])) continue;  /* masked: probability 0, no contribution */
+          const int64_t ko = ((b * Sk + j) * H + h) * D;
+          double dp = 0.0;
+          for (int64_t d = 0; d < D; ++d) dp += (double)inel(dy, qo + d, elt) * (double)inel(v, ko + d, elt);
+          const double ds = p[j] * (dp - corr);
+          for (int64_t d = 0; d < D; ++d) {
+            if (dq) dq[qo + d] += sc * ds * (double)inel(k, ko + d, elt);
+            if (dk) dk[ko + d] += sc * ds * (double)inel(q, qo + d, elt);
+            if (dv) dv[ko + d] += p[j] * (double)inel(dy, qo + d, elt);
+          }
+        }
+      }
+  free(s);
+  free(p);
+  free(o);
+}
+
 void oracle_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]) {
   const uint32_t M0 = 0xD2511F53u, M1 = 0xCD9E8D57u, W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
   uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3];

@@ -89,6 +89,28 @@ void oracle_gelu_tanh(const void* x, void* y, int64_t n, int elt);
 void oracle_gelu_tanh_backward(const void* x, const void* dy, void* dx, int64_t n,
                                int elt);
 
+/* memory_efficient_attention, src/layers/attention.jl:106-172 (and reference_attention 30-63),
+ * as exact scaled dot-product attention in f64 from 16-bit or f32 inputs (elt as above, 2 = f32).
+ * Layouts (row-major; the Julia (D, H, tokens, batch) arrays): q [B][Sq][H][D], k and v
+ * [B][Sk][H][D], mask [Sq][Sk] uint8 (nonzero = visible; Julia's (key_tokens, query_tokens) Bool
+ * array) or NULL, causal: key index <= query index. scale = 1/sqrt(Float32(D)) rounded to f32,
+ * as attention.jl:129. out [B][Sq][H][D] and lse [B][H][Sq] (either may be NULL). A query with no
+ * visible key gets NaN output and NaN lse, as the reference's online softmax gives (its first
+ * rescale is exp(-Inf - -Inf)).
+ * Pinned by: q = 0 (uniform weights: the mean of the visible values, lse = log(count)), causal
+ * row 0 (= v of key 0), an independent numpy restatement, mask/causal equivalences. */
+void oracle_attention_forward(const void* q, const void* k, const void* v, const uint8_t* mask,
+                              int causal, int64_t B, int64_t Sq, int64_t Sk, int64_t H, int64_t D,
+                              int elt, double* out, double* lse);
+/* memory_efficient_attention_backward, attention.jl:174-221, in f64: P from the exact scores,
+ * dP = dy V^T, correction = sum(dy .* out) per query (the reference uses its cached output),
+ * dS = P (dP - correction), dq = scale dS K, dk = scale dS^T Q, dv = P^T dy. Outputs in the q / k
+ * / v layouts, f64 (any may be NULL). Pinned by central finite differences of
+ * oracle_attention_forward (as test/unit/layers.jl:56-71 does for reference_attention). */
+void oracle_attention_backward(const void* q, const void* k, const void* v, const void* dy,
+                               const uint8_t* mask, int causal, int64_t B, int64_t Sq, int64_t Sk,
+                               int64_t H, int64_t D, int elt, double* dq, double* dk, double* dv);
+
 /* Philox4x32-10 (Salmon et al., SC'11) counter-based generator for seeded test inputs.
  * Pinned by the published Random123 known-answer vectors. */
 void oracle_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);

@@ -430,3 +430,122 @@ def test_f32_gelu_is_the_unrounded_bf16_gelu():
     f = lambda v: 0.5 * v * (1 + np.tanh(k * (v + 0.044715 * v ** 3)))
     fd = (f(xb + 1e-6) - f(xb - 1e-6)) / 2e-6
     assert np.allclose(d, fd, rtol=1e-5, atol=1e-6)
+
+
+# ---- attention (src/layers/attention.jl) ------------------------------------------------------
+def _np_attention(q, k, v, mask=None, causal=False):
+    """Second restatement, numpy only: softmax over visible keys per (batch, head, query)."""
+    q, k, v = (a.astype(np.float64) for a in (q, k, v))
+    B, Sq, H, D = q.shape
+    Sk = k.shape[1]
+    sc = float(np.float32(1) / np.sqrt(np.float32(D)))
+    s = np.einsum("bqhd,bkhd->bhqk", q, k) * sc
+    vis = np.ones((Sq, Sk), bool) if mask is None else mask.astype(bool).copy()
+    if causal:
+        vis &= np.arange(Sk)[None, :] <= np.arange(Sq)[:, None]
+    s = np.where(vis[None, None], s, -np.inf)
+    m = s.max(axis=-1, keepdims=True)
+    e = np.exp(s - m)
+    lse = (m + np.log(e.sum(-1, keepdims=True)))[..., 0]
+    p = e / e.sum(-1, keepdims=True)
+    return np.einsum("bhqk,bkhd->bqhd", p, v), lse
+
+
+def _att_inputs(rng, B, Sq, Sk, H, D, scale=1.0):
+    f = lambda *sh: (rng.standard_normal(sh) * scale).astype(np.float32)
+    return f(B, Sq, H, D), f(B, Sk, H, D), f(B, Sk, H, D)
+
+
+def test_attention_zero_queries_average_the_visible_values():
+    # q = 0: every visible score is 0, so the weights are uniform (closed form)
+    rng = np.random.default_rng(1)
+    _, k, v = _att_inputs(rng, 2, 5, 7, 3, 8)
+    q = np.zeros((2, 5, 3, 8), np.float32)
+    mask = rng.random((5, 7)) < 0.6
+    mask[:, 0] = True
+    out, lse = oracle.attention_forward(q, k, v, mask=mask, elt="f32")
+    for i in range(5):
+        vis = mask[i]
+        assert np.allclose(out[:, i], v[:, vis].astype(np.float64).mean(axis=1), rtol=0, atol=1e-12)
+        assert np.allclose(lse[:, :, i], np.log(vis.sum()), rtol=0, atol=1e-12)
+
+
+def test_attention_causal_first_query_is_the_first_value():
+    # causal, query 0 sees key 0 only: output v[0], lse = its score
+    rng = np.random.default_rng(2)
+    q, k, v = _att_inputs(rng, 1, 6, 6, 2, 16)
+    out, lse = oracle.attention_forward(q, k, v, causal=True, elt="f32")
+    assert np.array_equal(out[:, 0], v[:, 0].astype(np.float64))
+    sc = float(np.float32(1) / np.sqrt(np.float32(16)))
+    s00 = (q[0, 0].astype(np.float64) * k[0, 0]).sum(-1) * sc
+    assert np.allclose(lse[0, :, 0], s00, rtol=0, atol=1e-12)
+
+
+def test_attention_matches_numpy_restatement():
+    rng = np.random.default_rng(3)
+    for (B, Sq, Sk, H, D, causal, masked) in [(1, 7, 9, 2, 4, False, True), (2, 9, 9, 3, 8, True, False),
+                                              (1, 5, 3, 1, 16, False, False)]:
+        q, k, v = _att_inputs(rng, B, Sq, Sk, H, D)
+        mask = None
+        if masked:
+            mask = rng.random((Sq, Sk)) < 0.7
+            mask[:, 1] = True
+        out, lse = oracle.attention_forward(q, k, v, mask=mask, causal=causal, elt="f32")
+        ro, rl = _np_attention(q, k, v, mask, causal)
+        assert np.allclose(out, ro, rtol=1e-12, atol=1e-12)
+        assert np.allclose(lse, rl, rtol=1e-12, atol=1e-12)
+
+
+def test_attention_mask_and_causal_equivalences():
+    # an all-visible mask is no mask; the lower-triangular mask is causal (layers.jl:70, 97-100)
+    rng = np.random.default_rng(4)
+    q, k, v = _att_inputs(rng, 1, 6, 6, 2, 8)
+    base = oracle.attention_forward(q, k, v, elt="f32")
+    full = oracle.attention_forward(q, k, v, mask=np.ones((6, 6), bool), elt="f32")
+    assert np.array_equal(base[0], full[0]) and np.array_equal(base[1], full[1])
+    tri = np.tril(np.ones((6, 6), bool))
+    c1 = oracle.attention_forward(q, k, v, causal=True, elt="f32")
+    c2 = oracle.attention_forward(q, k, v, mask=tri, elt="f32")
+    assert np.array_equal(c1[0], c2[0]) and np.array_equal(c1[1], c2[1])
+    # a query with no visible key: NaN output and lse, as the reference's online softmax
+    m = np.ones((6, 6), bool)
+    m[2] = False
+    out, lse = oracle.attention_forward(q, k, v, mask=m, elt="f32")
+    assert np.isnan(out[0, 2]).all() and np.isnan(lse[0, :, 2]).all()
+    assert np.isfinite(out[0, [0, 1, 3, 4, 5]]).all()
+
+
+def test_attention_16bit_inputs_decode_exactly():
+    # bf16 / f16 patterns are decoded exactly: the same values given as f32 give the same result
+    rng = np.random.default_rng(5)
+    q, k, v = _att_inputs(rng, 1, 4, 5, 2, 8)
+    qb, kb, vb = (oracle.f32_to_bf16(a) for a in (q, k, v))
+    ob, lb = oracle.attention_forward(qb, kb, vb, elt="bf16")
+    of, lf = oracle.attention_forward(*(oracle.bf16_to_f32(a) for a in (qb, kb, vb)), elt="f32")
+    assert np.array_equal(ob, of) and np.array_equal(lb, lf)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_backward_matches_finite_differences(causal):
+    # objective sum(out .* dy), central differences of the f64 forward (as layers.jl:62-67)
+    rng = np.random.default_rng(6)
+    B, Sq, Sk, H, D = 1, 4, 5 if not causal else 4, 2, 4
+    q, k, v = _att_inputs(rng, B, Sq, Sk, H, D)
+    dy = rng.standard_normal(q.shape).astype(np.float32)
+    mask = None if causal else (rng.random((Sq, Sk)) < 0.8) | (np.arange(Sk)[None, :] == 0)
+    dq, dk, dv = oracle.attention_backward(q, k, v, dy, mask=mask, causal=causal, elt="f32")
+
+    def objective(qq, kk, vv):
+        o, _ = oracle.attention_forward(qq, kk, vv, mask=mask, causal=causal, elt="f32")
+        return float((o * dy.astype(np.float64)).sum())
+
+    for name, arr, grad in (("q", q, dq), ("k", k, dk), ("v", v, dv)):
+        for idx in [(0, 1, 0, 2), (0, 2, 1, 3), (0, 3, 1, 0)]:
+            hi, lo = arr.copy(), arr.copy()
+            hi[idx] += np.float32(1e-2)
+            lo[idx] -= np.float32(1e-2)
+            step = float(hi[idx]) - float(lo[idx])
+            args_hi = {"q": (hi, k, v), "k": (q, hi, v), "v": (q, k, hi)}[name]
+            args_lo = {"q": (lo, k, v), "k": (q, lo, v), "v": (q, k, lo)}[name]
+            fd = (objective(*args_hi) - objective(*args_lo)) / step
+            assert abs(fd - grad[idx]) <= 1e-4 + 1e-4 * abs(fd), (name, idx, fd, grad[idx])
