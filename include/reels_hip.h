@@ -178,6 +178,37 @@ int reels_hip_gelu_tanh_bwd_f32(const float* x, const float* dy, float* dx, int6
                                 void* stream);
 
 /*
+ * Exact scaled dot-product attention with an online softmax. Replaces
+ * memory_efficient_attention (src/layers/attention.jl:106-172 CPU, 225-304 CUDA) and
+ * memory_efficient_attention_backward (attention.jl:174-221, 306-371), which the Wan model calls
+ * for self- and cross-attention (src/models/wan21/transformer.jl:199, 238-239).
+ * Layouts (row-major, the reference's (head_dim, heads, tokens, batch) arrays):
+ *   q, out, dy, dq [B][Sq][H][D];  k, v, dk, dv [B][Sk][H][D];  lse [B][H][Sq] f32
+ *   mask [Sq][Sk] uint8, nonzero = visible (the reference's (key_tokens, query_tokens) Bool
+ *   array), or NULL; causal != 0: key index <= query index.
+ * dtype REELS_HIP_BF16 or REELS_HIP_F16 for q, k, v, out, dy, dq, dk, dv; head dim D = 64 or 128;
+ * 16-byte aligned tensors; one batch of q or k below 2 GiB. Scores, softmax and sums run in f32
+ * with scale 1/sqrt(Float32(D)) (attention.jl:129); P is rounded to dtype for the P V product.
+ * A query with no visible key gets NaN output and NaN lse (-Inf when Sk = 0), as the reference;
+ * it contributes nothing to dq, dk, dv (in the reference its NaN correction reaches every dk of
+ * the head). The reference's query_block / key_block do not change the result and have no
+ * parameter here.
+ *   reels_hip_attention_fwd: out and (when lse != NULL) lse, the cache the backward needs.
+ *   reels_hip_attention_bwd: dq, dk, dv from dy, the forward's out and lse; workspace of
+ *     reels_hip_attention_workspace_bytes(B, Sq, H) bytes (the per-query sum(dy .* out)).
+ * Deterministic: no atomics, fixed summation order.
+ */
+size_t reels_hip_attention_workspace_bytes(int64_t B, int64_t Sq, int64_t H);
+int reels_hip_attention_fwd(const void* q, const void* k, const void* v, const uint8_t* mask,
+                            int causal, int64_t B, int64_t Sq, int64_t Sk, int64_t H, int64_t D,
+                            int dtype, void* out, float* lse, void* stream);
+int reels_hip_attention_bwd(const void* q, const void* k, const void* v, const void* out,
+                            const void* dy, const float* lse, const uint8_t* mask, int causal,
+                            int64_t B, int64_t Sq, int64_t Sk, int64_t H, int64_t D, int dtype,
+                            void* dq, void* dk, void* dv, void* workspace, size_t ws_bytes,
+                            void* stream);
+
+/*
  * Kernel timing instrumentation. No counterpart in the reference (it has no profiler hooks);
  * used by benchmarks to time individual kernels with HIP events on the stream each kernel is
  * launched on. While enabled, every kernel the library enqueues is bracketed by two event

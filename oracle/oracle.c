@@ -349,7 +349,7 @@ static double att_row(const void* q, const void* k, const uint8_t* mask, int cau
   }
   if (!any) {
     for (int64_t j = 0; j < Sk; ++j) p[j] = 0.0;
-    return NAN;
+    return Sk == 0 ? -INFINITY : NAN;  /* -Inf + log(0) without keys; NaN from exp(-Inf - -Inf) */
   }
   double l = 0.0;
   for (int64_t j = 0; j < Sk; ++j) { p[j] = isfinite(s[j]) ? exp(s[j] - m) : 0.0; l += p[j]; }
@@ -369,8 +369,9 @@ void oracle_attention_forward(const void* q, const void* k, const void* v, const
         if (lse) lse[(b * H + h) * Sq + i] = L;
         if (!out) continue;
         double* o = out + ((b * Sq + i) * H + h) * D;
-        for (int64_t d = 0; d < D; ++d) o[d] = isnan(L) ? NAN : 0.0;
-        if (isnan(L)) continue;
+        const int none = !isfinite(L);
+        for (int64_t d = 0; d < D; ++d) o[d] = none ? NAN : 0.0;
+        if (none) continue;
         for (int64_t j = 0; j < Sk; ++j) {
           if (p[j] == 0.0) continue;
           const int64_t vo = ((b * Sk + j) * H + h) * D;
@@ -397,8 +398,8 @@ void oracle_attention_backward(const void* q, const void* k, const void* v, cons
         const double L = att_row(q, k, mask, causal, b, i, h, Sq, Sk, H, D, elt, s, p);
         const int64_t qo = ((b * Sq + i) * H + h) * D;
         /* the output of this query, and the correction sum(dy .* out) (attention.jl:190) */
-        for (int64_t d = 0; d < D; ++d) o[d] = isnan(L) ? NAN : 0.0;
-        if (!isnan(L))
+        for (int64_t d = 0; d < D; ++d) o[d] = isfinite(L) ? 0.0 : NAN;
+        if (isfinite(L))
           for (int64_t j = 0; j < Sk; ++j) {
             if (p[j] == 0.0) continue;
             const int64_t vo = ((b * Sk + j) * H + h) * D;

@@ -96,7 +96,7 @@ void oracle_gelu_tanh_backward(const void* x, const void* dy, void* dx, int64_t 
  * array) or NULL, causal: key index <= query index. scale = 1/sqrt(Float32(D)) rounded to f32,
  * as attention.jl:129. out [B][Sq][H][D] and lse [B][H][Sq] (either may be NULL). A query with no
  * visible key gets NaN output and NaN lse, as the reference's online softmax gives (its first
- * rescale is exp(-Inf - -Inf)).
+ * rescale is exp(-Inf - -Inf)); with no keys at all (Sk = 0) the lse is -Inf + log(0) = -Inf.
  * Pinned by: q = 0 (uniform weights: the mean of the visible values, lse = log(count)), causal
  * row 0 (= v of key 0), an independent numpy restatement, mask/causal equivalences. */
 void oracle_attention_forward(const void* q, const void* k, const void* v, const uint8_t* mask,

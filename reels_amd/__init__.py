@@ -1,9 +1,14 @@
 """reels_amd: MI355X (gfx950) HIP implementation of Reels.jl's int8 frozen-weight LoRA linear.
 
 The compute lives in libreels_hip.so (C ABI: include/reels_hip.h); this package is the host-side
-mirror of the reference layer API (src/layers/quantization.jl, lora.jl, linear.jl).
+mirror of the reference layer API (src/layers/quantization.jl, lora.jl, linear.jl, attention.jl).
 """
 from ._lib import ReelsHIPError, ReelsHIPUnavailable, library_path  # noqa: F401
+from .attention import (  # noqa: F401
+    TiledAttentionCache,
+    memory_efficient_attention,
+    memory_efficient_attention_backward,
+)
 from .layers import (  # noqa: F401
     DenseLayer,
     FrozenWeightTransfer,

@@ -37,6 +37,9 @@ EXPORTS = (
     "reels_hip_i8lora_bwd_f32",
     "reels_hip_gelu_tanh_f32",
     "reels_hip_gelu_tanh_bwd_f32",
+    "reels_hip_attention_workspace_bytes",
+    "reels_hip_attention_fwd",
+    "reels_hip_attention_bwd",
     "reels_hip_trace_start",
     "reels_hip_trace_stop",
     "reels_hip_trace_get",
@@ -94,6 +97,14 @@ def lib():
         g.restype = ctypes.c_int
         gb.argtypes = [vp, vp, vp, i64, vp]
         gb.restype = ctypes.c_int
+    ci = ctypes.c_int
+    L.reels_hip_attention_workspace_bytes.argtypes = [i64, i64, i64]
+    L.reels_hip_attention_workspace_bytes.restype = sz
+    L.reels_hip_attention_fwd.argtypes = [vp, vp, vp, vp, ci, i64, i64, i64, i64, i64, ci, vp, vp, vp]
+    L.reels_hip_attention_fwd.restype = ci
+    L.reels_hip_attention_bwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, ci, i64, i64, i64, i64, i64, ci,
+                                          vp, vp, vp, vp, sz, vp]
+    L.reels_hip_attention_bwd.restype = ci
     L.reels_hip_trace_start.argtypes = [ctypes.c_int]
     L.reels_hip_trace_start.restype = ctypes.c_int
     L.reels_hip_trace_stop.restype = ctypes.c_int

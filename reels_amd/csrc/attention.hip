@@ -1,0 +1,697 @@
+// Exact scaled dot-product attention with an online softmax: memory_efficient_attention and its
+// backward (src/layers/attention.jl:106-221 CPU, 225-371 CUDA), for bf16 / f16 tensors with f32
+// arithmetic, head_dim 64 or 128.
+//
+// Layouts (row-major; the reference's (head_dim, heads, tokens, batch) arrays): q, out, dq
+// [B][Sq][H][D]; k, v, dk, dv [B][Sk][H][D]; lse [B][H][Sq] f32; mask [Sq][Sk] uint8 (nonzero =
+// visible; the reference's (key_tokens, query_tokens) Bool array), causal: key <= query.
+//
+// Forward: a workgroup takes 128 queries of one (batch, head), 32 per wave as two 16-query MFMA
+// tiles, and streams the keys in tiles of 64 through a two-stage LDS ring (LDS-DMA copies). Per
+// key tile: S^T = K Q^T on v_mfma_f32_16x16x32 (lane l holds keys 4(l/16)+v of a 16-key tile for
+// query l%16), the running maximum and sum in the base-2 domain, P rounded to the element type,
+// O^T += V^T P^T with V^T fragments read transposed from LDS (ds_read_b64_tr_b16). The P operand
+// takes its 8 keys per lane as keys {4g..4g+3} and {16+4g..16+4g+3} of a 32-key block (g = l/16):
+// exactly what the score accumulators hold, so no lane exchange is needed; the V^T reads use the
+// same key order.
+//
+// Backward (deterministic, no atomics): correction[q] = sum(dy .* out) (attention.jl:190); a
+// key-tile kernel accumulates dK and dV over all query tiles; a query-tile kernel accumulates dQ
+// over all key tiles. Both recompute P from lse.
+#include "common.h"
+
+namespace reels {
+
+namespace att {
+constexpr int KT = 64;    // keys per tile
+constexpr int QW = 32;    // queries per wave (forward, dQ)
+constexpr int QB = 128;   // queries per workgroup (forward, dQ)
+constexpr int KW = 16;    // keys per wave (dK / dV)
+constexpr int KB = 64;    // keys per workgroup (dK / dV)
+constexpr int QT = 32;    // queries per step (dK / dV)
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float LN2 = 0.6931471805599453f;
+}  // namespace att
+
+// byte offset of element d of row r in a tile with rows of D elements; 16-byte chunks are
+// XOR-swizzled by the row so that 16 consecutive rows read at one column hit distinct banks
+template <int D>
+__device__ __forceinline__ uint32_t toff(int r, int d) {
+  constexpr int CH = D / 8;
+  return (uint32_t)(r * D * 2 + ((((d >> 3) ^ (r & (CH - 1)))) << 4) + (d & 7) * 2);
+}
+
+__device__ __forceinline__ float wave_max16(float x) {  // over lanes l, l^16, l^32, l^48
+  x = fmaxf(x, __shfl_xor(x, 16));
+  return fmaxf(x, __shfl_xor(x, 32));
+}
+__device__ __forceinline__ float wave_sum16(float x) {
+  x += __shfl_xor(x, 16);
+  return x + __shfl_xor(x, 32);
+}
+
+// A operand of 8 rows-transposed elements from an LDS tile: element e < 4 is row r0 + e,
+// element e >= 4 is row r1 + e - 4, column c (the lane's 4-column piece chosen by the caller's
+// addresses, see ds_read_b64_tr_b16)
+template <int D>
+__device__ __forceinline__ u32x4 read_tr(const uint8_t* tile, int r0, int r1, int c, int i16) {
+  const int rr0 = r0 + (i16 >> 2), rr1 = r1 + (i16 >> 2), cc = c + 4 * (i16 & 3);
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(i16x4, tile + toff<D>(rr0, cc)));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(i16x4, tile + toff<D>(rr1, cc)));
+  u32x4 r;
+  r[0] = (uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16);
+  r[1] = (uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16);
+  r[2] = (uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16);
+  r[3] = (uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16);
+  return r;
+}
+
+struct AttArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const uint16_t* out;   // backward: the forward's output
+  const uint16_t* dy;
+  const float* lse;
+  const float* corr;     // backward: sum(dy .* out) per query, [B][H][Sq]
+  float* corr_out;       // the correction kernel's output (the same buffer)
+  const uint8_t* mask;
+  uint16_t* o;           // forward output / dq
+  uint16_t* dk;
+  uint16_t* dv;
+  float* lse_out;
+  int64_t Sq, Sk, H;
+  int causal;
+  float scale;           // 1 / sqrt(Float32(D)) (attention.jl:129)
+};
+
+__device__ __forceinline__ bool att_visible(const AttArgs& a, int64_t qi, int64_t kj) {
+  if (kj >= a.Sk || qi >= a.Sq) return false;
+  if (a.causal && kj > qi) return false;
+  if (a.mask != nullptr && a.mask[qi * a.Sk + kj] == 0) return false;
+  return true;
+}
+
+// Copies of one 64-row tile of a [B][S][H][D] tensor (rows = tokens of one batch and head) into
+// LDS with the toff swizzle: copy c of the tile covers LDS rows c * (64 / CH) .. + 64 / CH - 1,
+// lane L row c * (64 / CH) + L / CH, LDS slot L % CH holding chunk (L % CH) ^ (row & (CH - 1)).
+// Rows past the tensor's end read zeros (buffer range).
+template <int D>
+__device__ __forceinline__ void copy_tile(const i32x4& rsrc, int64_t row0, int64_t H, int w,
+                                          int lane, uint8_t* dst) {
+  constexpr int CH = D / 8, RPC = 64 / CH, NC = CH / 4;  // chunks per row, rows per copy, copies per wave
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int c = w * NC + i;
+    const int row = c * RPC + lane / CH;
+    const int chunk = (lane % CH) ^ (row & (CH - 1));
+    const uint32_t off = (uint32_t)(((row0 + row) * H * D + chunk * 8) * 2);
+    dma16(rsrc, off, 0u, dst + c * 1024);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// forward
+template <int ELT, int D>
+__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttArgs a) {
+  using E = Elt<ELT>;
+  using namespace att;
+  constexpr int TB = KT * D * 2;  // bytes of one K or V tile
+  constexpr int NKB = D / 32;     // k-blocks of the score MFMA
+  constexpr int NDT = D / 16;     // 16-wide d tiles of the output
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int64_t b = blockIdx.z, h = blockIdx.y;
+  const int64_t q0 = (int64_t)blockIdx.x * QB + w * QW;
+  const int64_t Sq = a.Sq, Sk = a.Sk, H = a.H;
+  const float sl2 = a.scale * LOG2E;
+
+  // this wave's query fragments (B operand of S^T): query q0 + 16 qt + l16, d = 32 kb + 8 g ..
+  u32x4 qf[2][NKB];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int64_t qi = q0 + 16 * qt + l16;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      qf[qt][kb] = u32x4{0, 0, 0, 0};
+      if (qi < Sq) qf[qt][kb] = *reinterpret_cast<const u32x4*>(a.q + ((b * Sq + qi) * H + h) * D + kb * 32 + g * 8);
+    }
+  }
+  const uint16_t* kbase = a.k + (b * Sk * H + h) * D;
+  const uint16_t* vbase = a.v + (b * Sk * H + h) * D;
+  const uint32_t nrec = (uint32_t)(((Sk - 1) * H + 1) * D * 2);
+  const i32x4 rk = buffer_rsrc(kbase, nrec), rv = buffer_rsrc(vbase, nrec);
+  auto issue = [&](int j) {
+    uint8_t* st = smem + (j & 1) * 2 * TB;
+    copy_tile<D>(rk, (int64_t)j * KT, H, w, lane, st);
+    copy_tile<D>(rv, (int64_t)j * KT, H, w, lane, st + TB);
+  };
+
+  f32x4 oacc[NDT][2];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) oacc[dt][qt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float mrun[2] = {-INFINITY, -INFINITY}, lrun[2] = {0.0f, 0.0f};  // lrun: this lane's part
+
+  // keys past the last one any query of this workgroup can see (causal) need no tile
+  int64_t kend = Sk;
+  if (a.causal) {
+    const int64_t qlast = (int64_t)blockIdx.x * QB + QB - 1;
+    kend = qlast + 1 < Sk ? qlast + 1 : Sk;
+  }
+  const int ntiles = (int)((kend + KT - 1) / KT);
+  if (ntiles > 0) issue(0);
+  for (int j = 0; j < ntiles; ++j) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's copies of tile j have landed
+    __syncthreads();                     // every wave's; every wave is done with tile j - 1
+    if (j + 1 < ntiles) issue(j + 1);
+    const uint8_t* sk = smem + (j & 1) * 2 * TB;
+    const uint8_t* sv = sk + TB;
+    const int64_t key0 = (int64_t)j * KT;
+
+    // S^T tiles: s[kt][qt] lane: keys key0 + 16 kt + 4 g + v, query q0 + 16 qt + l16
+    f32x4 s[4][2];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      s[kt][0] = s[kt][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+        const u32x4 kf = *reinterpret_cast<const u32x4*>(sk + toff<D>(16 * kt + l16, kb * 32 + g * 8));
+        s[kt][0] = E::mfma16(E::as8(kf), E::as8(qf[0][kb]), s[kt][0]);
+        s[kt][1] = E::mfma16(E::as8(kf), E::as8(qf[1][kb]), s[kt][1]);
+      }
+    }
+    // online softmax per query (base 2): masked scores are -inf and get probability 0
+    u32x4 pb[2][2];  // P operand: [32-key block][qt]
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      const int64_t qi = q0 + 16 * qt + l16;
+      float mt = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int64_t kj = key0 + 16 * kt + 4 * g + v;
+          const float x = att_visible(a, qi, kj) ? s[kt][qt][v] * sl2 : -INFINITY;
+          s[kt][qt][v] = x;
+          mt = fmaxf(mt, x);
+        }
+      mt = wave_max16(mt);
+      const float mnew = fmaxf(mrun[qt], mt);
+      // no visible key yet: nothing accumulated, keep the factor finite
+      const float alpha = mnew == -INFINITY ? 1.0f : exp2f(mrun[qt] - mnew);
+      mrun[qt] = mnew;
+      float ps = 0.0f;
+      float p[4][4];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float x = s[kt][qt][v];
+          p[kt][v] = x == -INFINITY ? 0.0f : exp2f(x - mnew);
+          ps += p[kt][v];
+        }
+      lrun[qt] = lrun[qt] * alpha + ps;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) oacc[dt][qt][v] *= alpha;
+#pragma unroll
+      for (int kb2 = 0; kb2 < 2; ++kb2) {
+        pb[kb2][qt][0] = E::pack2(p[2 * kb2][0], p[2 * kb2][1]);
+        pb[kb2][qt][1] = E::pack2(p[2 * kb2][2], p[2 * kb2][3]);
+        pb[kb2][qt][2] = E::pack2(p[2 * kb2 + 1][0], p[2 * kb2 + 1][1]);
+        pb[kb2][qt][3] = E::pack2(p[2 * kb2 + 1][2], p[2 * kb2 + 1][3]);
+      }
+    }
+    // O^T += V^T P^T: A = V^T rows d = 16 dt + l16, keys {32 kb2 + 4 g ..} and {32 kb2 + 16 + 4 g ..}
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int kb2 = 0; kb2 < 2; ++kb2) {
+        const u32x4 vf = read_tr<D>(sv, 32 * kb2 + 4 * g, 32 * kb2 + 16 + 4 * g, 16 * dt, l16);
+        oacc[dt][0] = E::mfma16(E::as8(vf), E::as8(pb[kb2][0]), oacc[dt][0]);
+        oacc[dt][1] = E::mfma16(E::as8(vf), E::as8(pb[kb2][1]), oacc[dt][1]);
+      }
+  }
+
+  // out = O / l, lse = (m + log2 l) ln 2; a query with no visible key gets NaN for both, as the
+  // reference's online softmax gives
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int64_t qi = q0 + 16 * qt + l16;
+    const float l = wave_sum16(lrun[qt]);
+    const bool none = !(l > 0.0f);
+    const float inv = none ? __builtin_nanf("") : 1.0f / l;
+    // no keys at all: lse = -Inf + log(0) as the reference computes it; keys, none visible: NaN
+    const float lnone = Sk == 0 ? -INFINITY : __builtin_nanf("");
+    if (qi < Sq) {
+      uint16_t* orow = a.o + ((b * Sq + qi) * H + h) * D;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        const u32x2 pk = {E::pack2(oacc[dt][qt][0] * inv, oacc[dt][qt][1] * inv),
+                          E::pack2(oacc[dt][qt][2] * inv, oacc[dt][qt][3] * inv)};
+        *reinterpret_cast<u32x2*>(orow + 16 * dt + 4 * g) = pk;
+      }
+      if (a.lse_out != nullptr && g == 0)
+        a.lse_out[(b * H + h) * Sq + qi] = none ? lnone : (mrun[qt] + log2f(l)) * LN2;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// backward: correction[b][h][q] = sum_d dy * out (f32), one thread per query row
+template <int ELT, int D>
+__global__ __launch_bounds__(256) void attn_corr_kernel(AttArgs a, int64_t B) {
+  using E = Elt<ELT>;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // ((b * Sq + q) * H + h)
+  if (i >= B * a.Sq * a.H) return;
+  const int64_t h = i % a.H, bq = i / a.H, qi = bq % a.Sq, b = bq / a.Sq;
+  const u32x4* dy = reinterpret_cast<const u32x4*>(a.dy + i * D);
+  const u32x4* o = reinterpret_cast<const u32x4*>(a.out + i * D);
+  float acc = 0.0f;
+#pragma unroll
+  for (int c = 0; c < D / 8; ++c) {
+    const u32x4 x = dy[c], y = o[c];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc += E::lo(x[e]) * E::lo(y[e]) + E::hi(x[e]) * E::hi(y[e]);
+  }
+  a.corr_out[(b * a.H + h) * a.Sq + qi] = acc;
+}
+
+// dK, dV: a workgroup takes 64 keys of one (batch, head), 16 per wave, and streams the queries
+// in steps of 32 (Q and dY tiles through a two-stage LDS ring, lse and correction beside them).
+// Per step: S = Q K^T and dP = dY V^T (lane l: queries 16 qt + 4 g + v, key l16), P from lse,
+// dS = P (dP - correction), dV^T += dY^T P and dK^T += Q^T dS (A operands read transposed, the
+// query order {4g..4g+3, 16+4g..16+4g+3} of the accumulators).
+template <int ELT, int D>
+__global__ __launch_bounds__(256, 2) void attn_dkdv_kernel(AttArgs a) {
+  using E = Elt<ELT>;
+  using namespace att;
+  constexpr int TB = QT * D * 2;  // bytes of one Q or dY step tile
+  constexpr int NKB = D / 32, NDT = D / 16;
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int64_t b = blockIdx.z, h = blockIdx.y;
+  const int64_t k0 = (int64_t)blockIdx.x * KB + w * KW;
+  const int64_t Sq = a.Sq, Sk = a.Sk, H = a.H;
+  const float sl2 = a.scale * LOG2E;
+  const int64_t kj = k0 + l16;  // this lane's key
+
+  // K and V fragments (B operands): key kj, d = 32 kb + 8 g ..
+  u32x4 kf[NKB], vf[NKB];
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) {
+    kf[kb] = vf[kb] = u32x4{0, 0, 0, 0};
+    if (kj < Sk) {
+      kf[kb] = *reinterpret_cast<const u32x4*>(a.k + ((b * Sk + kj) * H + h) * D + kb * 32 + g * 8);
+      vf[kb] = *reinterpret_cast<const u32x4*>(a.v + ((b * Sk + kj) * H + h) * D + kb * 32 + g * 8);
+    }
+  }
+  const uint16_t* qbase = a.q + (b * Sq * H + h) * D;
+  const uint16_t* dbase = a.dy + (b * Sq * H + h) * D;
+  const uint32_t nrec = (uint32_t)(((Sq - 1) * H + 1) * D * 2);
+  const i32x4 rq = buffer_rsrc(qbase, nrec), rd = buffer_rsrc(dbase, nrec);
+  float* sstat = reinterpret_cast<float*>(smem + 4 * TB);  // [2 stages][lse 32, corr 32]
+  auto issue = [&](int j) {
+    uint8_t* st = smem + (j & 1) * 2 * TB;
+    // a 32-row tile: half the copies of copy_tile's 64 rows
+    constexpr int CH = D / 8, RPC = 64 / CH, NCT = 32 * CH / 64;  // copies per tile
+#pragma unroll
+    for (int i = 0; i < (NCT + 3) / 4; ++i) {
+      const int c = w * ((NCT + 3) / 4) + i;
+      if (c < NCT) {
+        const int row = c * RPC + lane / CH;
+        const int chunk = (lane % CH) ^ (row & (CH - 1));
+        const uint32_t off = (uint32_t)((((int64_t)j * QT + row) * H * D + chunk * 8) * 2);
+        dma16(rq, off, 0u, st + c * 1024);
+        dma16(rd, off, 0u, st + TB + c * 1024);
+      }
+    }
+  };
+  // lse and correction of a step's queries (threads 0..63): loaded into a register with the
+  // step's copies and written to LDS after the wait that ends the previous step, so the loads
+  // never make the compiler wait for copies it cannot see
+  float stv = 0.0f;
+  auto stats_load = [&](int j) {
+    if (t < 64) {
+      const int64_t qi = (int64_t)j * QT + (t & 31);
+      stv = 0.0f;
+      if (qi < Sq) stv = (t < 32) ? a.lse[(b * H + h) * Sq + qi] * LOG2E : a.corr[(b * H + h) * Sq + qi];
+    }
+  };
+  auto stats_store = [&](int j) {
+    if (t < 64) sstat[(j & 1) * 64 + t] = stv;
+  };
+
+  f32x4 dvacc[NDT], dkacc[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) dvacc[dt] = dkacc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // causal: queries before the first key of this workgroup see none of its keys
+  int jbeg = 0;
+  if (a.causal) jbeg = (int)(((int64_t)blockIdx.x * KB) / QT);
+  const int nsteps = (int)((Sq + QT - 1) / QT);
+  if (jbeg < nsteps) { stats_load(jbeg); issue(jbeg); }
+  for (int j = jbeg; j < nsteps; ++j) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // this wave's copies and statistics of step j
+    stats_store(j);
+    __syncthreads();
+    if (j + 1 < nsteps) { stats_load(j + 1); issue(j + 1); }
+    const uint8_t* sq = smem + (j & 1) * 2 * TB;
+    const uint8_t* sd = sq + TB;
+    const float* ls = sstat + (j & 1) * 64;
+    // S and dP tiles [qt]: lane queries 16 qt + 4 g + v, key l16
+    f32x4 s[2], dp[2];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      s[qt] = dp[qt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+        const u32x4 qa = *reinterpret_cast<const u32x4*>(sq + toff<D>(16 * qt + l16, kb * 32 + g * 8));
+        const u32x4 da = *reinterpret_cast<const u32x4*>(sd + toff<D>(16 * qt + l16, kb * 32 + g * 8));
+        s[qt] = E::mfma16(E::as8(qa), E::as8(kf[kb]), s[qt]);
+        dp[qt] = E::mfma16(E::as8(da), E::as8(vf[kb]), dp[qt]);
+      }
+    }
+    float p[2][4], ds[2][4];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int ql = 16 * qt + 4 * g + v;
+        const int64_t qi = (int64_t)j * QT + ql;
+        const bool vis = att_visible(a, qi, kj);
+        p[qt][v] = vis ? exp2f(s[qt][v] * sl2 - ls[ql]) : 0.0f;
+        ds[qt][v] = vis ? p[qt][v] * (dp[qt][v] - ls[32 + ql]) : 0.0f;
+      }
+    u32x4 pb, db;  // B operands: key l16, queries {4g..4g+3, 16+4g..16+4g+3}
+    pb[0] = E::pack2(p[0][0], p[0][1]); pb[1] = E::pack2(p[0][2], p[0][3]);
+    pb[2] = E::pack2(p[1][0], p[1][1]); pb[3] = E::pack2(p[1][2], p[1][3]);
+    db[0] = E::pack2(ds[0][0], ds[0][1]); db[1] = E::pack2(ds[0][2], ds[0][3]);
+    db[2] = E::pack2(ds[1][0], ds[1][1]); db[3] = E::pack2(ds[1][2], ds[1][3]);
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      const u32x4 da = read_tr<D>(sd, 4 * g, 16 + 4 * g, 16 * dt, l16);
+      const u32x4 qa = read_tr<D>(sq, 4 * g, 16 + 4 * g, 16 * dt, l16);
+      dvacc[dt] = E::mfma16(E::as8(da), E::as8(pb), dvacc[dt]);
+      dkacc[dt] = E::mfma16(E::as8(qa), E::as8(db), dkacc[dt]);
+    }
+  }
+  // dV[kj][d], dK[kj][d] = scale dK^T: lane holds d = 16 dt + 4 g + v of key kj
+  if (kj < Sk) {
+    uint16_t* dvrow = a.dv + ((b * Sk + kj) * H + h) * D;
+    uint16_t* dkrow = a.dk + ((b * Sk + kj) * H + h) * D;
+    const float sc = a.scale;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      const u32x2 pv = {E::pack2(dvacc[dt][0], dvacc[dt][1]), E::pack2(dvacc[dt][2], dvacc[dt][3])};
+      const u32x2 pk = {E::pack2(dkacc[dt][0] * sc, dkacc[dt][1] * sc), E::pack2(dkacc[dt][2] * sc, dkacc[dt][3] * sc)};
+      *reinterpret_cast<u32x2*>(dvrow + 16 * dt + 4 * g) = pv;
+      *reinterpret_cast<u32x2*>(dkrow + 16 * dt + 4 * g) = pk;
+    }
+  }
+}
+
+// dQ: the forward's structure. Per key tile: S^T = K Q^T and dP^T = V dY^T (A operands K and V
+// rows from LDS, B operands this wave's Q and dY fragments), P from lse, dS = P (dP - corr),
+// dQ^T += K^T dS^T with K^T read transposed in the accumulators' key order.
+template <int ELT, int D>
+__global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttArgs a) {
+  using E = Elt<ELT>;
+  using namespace att;
+  constexpr int TB = KT * D * 2;
+  constexpr int NKB = D / 32, NDT = D / 16;
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int64_t b = blockIdx.z, h = blockIdx.y;
+  const int64_t q0 = (int64_t)blockIdx.x * QB + w * QW;
+  const int64_t Sq = a.Sq, Sk = a.Sk, H = a.H;
+  const float sl2 = a.scale * LOG2E;
+
+  u32x4 qf[2][NKB], df[2][NKB];
+  float lse2[2], cr[2];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int64_t qi = q0 + 16 * qt + l16;
+    lse2[qt] = qi < Sq ? a.lse[(b * H + h) * Sq + qi] * LOG2E : 0.0f;
+    cr[qt] = qi < Sq ? a.corr[(b * H + h) * Sq + qi] : 0.0f;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      qf[qt][kb] = df[qt][kb] = u32x4{0, 0, 0, 0};
+      if (qi < Sq) {
+        qf[qt][kb] = *reinterpret_cast<const u32x4*>(a.q + ((b * Sq + qi) * H + h) * D + kb * 32 + g * 8);
+        df[qt][kb] = *reinterpret_cast<const u32x4*>(a.dy + ((b * Sq + qi) * H + h) * D + kb * 32 + g * 8);
+      }
+    }
+  }
+  const uint16_t* kbase = a.k + (b * Sk * H + h) * D;
+  const uint16_t* vbase = a.v + (b * Sk * H + h) * D;
+  const uint32_t nrec = (uint32_t)(((Sk - 1) * H + 1) * D * 2);
+  const i32x4 rk = buffer_rsrc(kbase, nrec), rv = buffer_rsrc(vbase, nrec);
+  auto issue = [&](int j) {
+    uint8_t* st = smem + (j & 1) * 2 * TB;
+    copy_tile<D>(rk, (int64_t)j * KT, H, w, lane, st);
+    copy_tile<D>(rv, (int64_t)j * KT, H, w, lane, st + TB);
+  };
+  f32x4 qacc[NDT][2];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) qacc[dt][0] = qacc[dt][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  int64_t kend = Sk;
+  if (a.causal) {
+    const int64_t qlast = (int64_t)blockIdx.x * QB + QB - 1;
+    kend = qlast + 1 < Sk ? qlast + 1 : Sk;
+  }
+  const int ntiles = (int)((kend + KT - 1) / KT);
+  if (ntiles > 0) issue(0);
+  for (int j = 0; j < ntiles; ++j) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+    if (j + 1 < ntiles) issue(j + 1);
+    const uint8_t* sk = smem + (j & 1) * 2 * TB;
+    const uint8_t* sv = sk + TB;
+    const int64_t key0 = (int64_t)j * KT;
+    u32x4 db[2][2];  // dS operand [32-key block][qt]
+#pragma unroll
+    for (int kb2 = 0; kb2 < 2; ++kb2) {
+      float dsv[2][2][4];  // [key tile within the block][qt][v]
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int kt = 2 * kb2 + half;
+        f32x4 s[2], dp[2];
+        s[0] = s[1] = dp[0] = dp[1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+          const u32x4 ka = *reinterpret_cast<const u32x4*>(sk + toff<D>(16 * kt + l16, kb * 32 + g * 8));
+          const u32x4 va = *reinterpret_cast<const u32x4*>(sv + toff<D>(16 * kt + l16, kb * 32 + g * 8));
+#pragma unroll
+          for (int qt = 0; qt < 2; ++qt) {
+            s[qt] = E::mfma16(E::as8(ka), E::as8(qf[qt][kb]), s[qt]);
+            dp[qt] = E::mfma16(E::as8(va), E::as8(df[qt][kb]), dp[qt]);
+          }
+        }
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) {
+          const int64_t qi = q0 + 16 * qt + l16;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int64_t kj = key0 + 16 * kt + 4 * g + v;
+            const bool vis = att_visible(a, qi, kj);
+            const float p = vis ? exp2f(s[qt][v] * sl2 - lse2[qt]) : 0.0f;
+            dsv[half][qt][v] = vis ? p * (dp[qt][v] - cr[qt]) : 0.0f;
+          }
+        }
+      }
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+        db[kb2][qt][0] = E::pack2(dsv[0][qt][0], dsv[0][qt][1]);
+        db[kb2][qt][1] = E::pack2(dsv[0][qt][2], dsv[0][qt][3]);
+        db[kb2][qt][2] = E::pack2(dsv[1][qt][0], dsv[1][qt][1]);
+        db[kb2][qt][3] = E::pack2(dsv[1][qt][2], dsv[1][qt][3]);
+      }
+    }
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int kb2 = 0; kb2 < 2; ++kb2) {
+        const u32x4 kt_ = read_tr<D>(sk, 32 * kb2 + 4 * g, 32 * kb2 + 16 + 4 * g, 16 * dt, l16);
+        qacc[dt][0] = E::mfma16(E::as8(kt_), E::as8(db[kb2][0]), qacc[dt][0]);
+        qacc[dt][1] = E::mfma16(E::as8(kt_), E::as8(db[kb2][1]), qacc[dt][1]);
+      }
+  }
+  const float sc = a.scale;
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int64_t qi = q0 + 16 * qt + l16;
+    if (qi >= Sq) continue;
+    uint16_t* row = a.o + ((b * Sq + qi) * H + h) * D;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      const u32x2 pk = {E::pack2(qacc[dt][qt][0] * sc, qacc[dt][qt][1] * sc),
+                        E::pack2(qacc[dt][qt][2] * sc, qacc[dt][qt][3] * sc)};
+      *reinterpret_cast<u32x2*>(row + 16 * dt + 4 * g) = pk;
+    }
+  }
+}
+
+// zero fill of n 16-bit elements (a kernel rather than hipMemsetAsync: callers may capture the
+// backward in a graph)
+__global__ __launch_bounds__(256) void attn_zero_kernel(uint16_t* p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0;
+}
+
+// ---------------------------------------------------------------------------------------------
+// host side
+static int attn_validate(const char* fn, const void* q, const void* k, const void* v, int64_t B,
+                         int64_t Sq, int64_t Sk, int64_t H, int64_t D, int dtype) {
+  if (B < 0 || Sq < 0 || Sk < 0 || H < 0)
+    return fail(REELS_HIP_EINVAL, std::string(fn) + ": need B, Sq, Sk, H >= 0");
+  if (D != 64 && D != 128)
+    return fail(REELS_HIP_EINVAL, std::string(fn) + ": head_dim must be 64 or 128");
+  if (dtype != REELS_HIP_BF16 && dtype != REELS_HIP_F16)
+    return fail(REELS_HIP_EDTYPE, std::string(fn) + ": dtype must be REELS_HIP_BF16 or REELS_HIP_F16");
+  if (H >= 65536 || B >= 65536)
+    return fail(REELS_HIP_EINVAL, std::string(fn) + ": B and H must be below 65536");
+  if (Sq * H * D * 2 >= ((int64_t)1 << 31) || Sk * H * D * 2 >= ((int64_t)1 << 31))
+    return fail(REELS_HIP_EINVAL, std::string(fn) + ": one batch of q or k over 2 GiB");
+  if (B * Sq * H == 0) return 1;  // nothing to compute
+  // k and v may be NULL without keys (empty tensors): nothing reads them then
+  if (!q || (Sk > 0 && (!k || !v))) return fail(REELS_HIP_EINVAL, std::string(fn) + ": NULL q, k or v");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v))
+    return fail(REELS_HIP_EINVAL, std::string(fn) + ": q, k, v must be 16-byte aligned");
+  return 0;
+}
+
+template <typename K>
+static hipError_t set_lds(K kernel, int bytes) {
+  return hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+}
+
+template <int ELT, int D>
+static int launch_attn_fwd(const AttArgs& a, int64_t B, hipStream_t st) {
+  const int lds = 4 * att::KT * D * 2;
+  if (hipError_t e = set_lds(attn_fwd_kernel<ELT, D>, lds))
+    return fail(REELS_HIP_EHIP, std::string("attention fwd: hipFuncSetAttribute: ") + hipGetErrorString(e));
+  const dim3 grid((unsigned)ceil_div(a.Sq, att::QB), (unsigned)a.H, (unsigned)B);
+  { TraceScope _ts(st, "attn_fwd_kernel"); attn_fwd_kernel<ELT, D><<<grid, 256, lds, st>>>(a); }
+  return check_launch("attn_fwd_kernel");
+}
+
+template <int ELT, int D>
+static int launch_attn_bwd(const AttArgs& a, int64_t B, hipStream_t st) {
+  {
+    TraceScope _ts(st, "attn_corr_kernel");
+    attn_corr_kernel<ELT, D><<<(unsigned)ceil_div(B * a.Sq * a.H, 256), 256, 0, st>>>(a, B);
+  }
+  if (int rc = check_launch("attn_corr_kernel")) return rc;
+  if (a.Sk > 0) {
+    const int lds = 4 * att::QT * D * 2 + 512;
+    if (hipError_t e = set_lds(attn_dkdv_kernel<ELT, D>, lds))
+      return fail(REELS_HIP_EHIP, std::string("attention bwd: hipFuncSetAttribute: ") + hipGetErrorString(e));
+    const dim3 grid((unsigned)ceil_div(a.Sk, att::KB), (unsigned)a.H, (unsigned)B);
+    { TraceScope _ts(st, "attn_dkdv_kernel"); attn_dkdv_kernel<ELT, D><<<grid, 256, lds, st>>>(a); }
+    if (int rc = check_launch("attn_dkdv_kernel")) return rc;
+  }
+  const int lds = 4 * att::KT * D * 2;
+  if (hipError_t e = set_lds(attn_dq_kernel<ELT, D>, lds))
+    return fail(REELS_HIP_EHIP, std::string("attention bwd: hipFuncSetAttribute: ") + hipGetErrorString(e));
+  const dim3 grid((unsigned)ceil_div(a.Sq, att::QB), (unsigned)a.H, (unsigned)B);
+  { TraceScope _ts(st, "attn_dq_kernel"); attn_dq_kernel<ELT, D><<<grid, 256, lds, st>>>(a); }
+  return check_launch("attn_dq_kernel");
+}
+
+template <typename F>
+static int with_att(int dtype, int64_t D, F&& f) {
+  if (dtype == REELS_HIP_F16) {
+    if (D == 64) return f(std::integral_constant<int, REELS_HIP_F16>{}, std::integral_constant<int, 64>{});
+    return f(std::integral_constant<int, REELS_HIP_F16>{}, std::integral_constant<int, 128>{});
+  }
+  if (D == 64) return f(std::integral_constant<int, REELS_HIP_BF16>{}, std::integral_constant<int, 64>{});
+  return f(std::integral_constant<int, REELS_HIP_BF16>{}, std::integral_constant<int, 128>{});
+}
+
+}  // namespace reels
+
+using namespace reels;
+
+extern "C" size_t reels_hip_attention_workspace_bytes(int64_t B, int64_t Sq, int64_t H) {
+  if (B < 0 || Sq < 0 || H < 0) return 0;
+  const size_t n = (size_t)B * (size_t)Sq * (size_t)H * 4;
+  return n == 0 ? 256 : (n + 255) / 256 * 256;
+}
+
+extern "C" int reels_hip_attention_fwd(const void* q, const void* k, const void* v,
+                                       const uint8_t* mask, int causal, int64_t B, int64_t Sq,
+                                       int64_t Sk, int64_t H, int64_t D, int dtype, void* out,
+                                       float* lse, void* stream) {
+  clear_error();
+  const char* fn = "reels_hip_attention_fwd";
+  if (int rc = attn_validate(fn, q, k, v, B, Sq, Sk, H, D, dtype)) return rc < 0 ? rc : REELS_HIP_OK;
+  if (!out) return fail(REELS_HIP_EINVAL, std::string(fn) + ": NULL out");
+  if (!aligned16(out)) return fail(REELS_HIP_EINVAL, std::string(fn) + ": out must be 16-byte aligned");
+  AttArgs a{};
+  a.q = static_cast<const uint16_t*>(q);
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.mask = mask;
+  a.o = static_cast<uint16_t*>(out);
+  a.lse_out = lse;
+  a.Sq = Sq; a.Sk = Sk; a.H = H;
+  a.causal = causal ? 1 : 0;
+  a.scale = 1.0f / sqrtf((float)D);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  return with_att(dtype, D, [&](auto e, auto d) { return launch_attn_fwd<decltype(e)::value, decltype(d)::value>(a, B, st); });
+}
+
+extern "C" int reels_hip_attention_bwd(const void* q, const void* k, const void* v,
+                                       const void* out, const void* dy, const float* lse,
+                                       const uint8_t* mask, int causal, int64_t B, int64_t Sq,
+                                       int64_t Sk, int64_t H, int64_t D, int dtype, void* dq,
+                                       void* dk, void* dv, void* workspace, size_t ws_bytes,
+                                       void* stream) {
+  clear_error();
+  const char* fn = "reels_hip_attention_bwd";
+  if (int rc = attn_validate(fn, q, k, v, B, Sq, Sk, H, D, dtype)) {
+    if (rc < 0) return rc;
+    // no queries: dk and dv are zero (the reference's zero(k), zero(v))
+    if (B * Sk * H > 0 && dk && dv) {
+      hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+      const int64_t n = B * Sk * H * D;
+      const unsigned grid = (unsigned)(ceil_div(n, 256) < 4096 ? ceil_div(n, 256) : 4096);
+      { TraceScope _ts(st, "attn_zero_kernel"); attn_zero_kernel<<<grid, 256, 0, st>>>(static_cast<uint16_t*>(dk), n); }
+      { TraceScope _ts(st, "attn_zero_kernel"); attn_zero_kernel<<<grid, 256, 0, st>>>(static_cast<uint16_t*>(dv), n); }
+      return check_launch("attn_zero_kernel");
+    }
+    return REELS_HIP_OK;
+  }
+  if (!out || !dy || !lse || !dq || (Sk > 0 && (!dk || !dv)))
+    return fail(REELS_HIP_EINVAL, std::string(fn) + ": NULL out, dy, lse, dq, dk or dv");
+  if (!aligned16(out) || !aligned16(dy) || !aligned16(dq) || !aligned16(dk) || !aligned16(dv))
+    return fail(REELS_HIP_EINVAL, std::string(fn) + ": out, dy, dq, dk, dv must be 16-byte aligned");
+  if (!workspace || ws_bytes < reels_hip_attention_workspace_bytes(B, Sq, H))
+    return fail(REELS_HIP_EWORKSPACE, std::string(fn) + ": workspace NULL or smaller than "
+                                      "reels_hip_attention_workspace_bytes(B, Sq, H)");
+  AttArgs a{};
+  a.q = static_cast<const uint16_t*>(q);
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.out = static_cast<const uint16_t*>(out);
+  a.dy = static_cast<const uint16_t*>(dy);
+  a.lse = lse;
+  a.corr = static_cast<const float*>(workspace);
+  a.corr_out = static_cast<float*>(workspace);
+  a.mask = mask;
+  a.o = static_cast<uint16_t*>(dq);
+  a.dk = static_cast<uint16_t*>(dk);
+  a.dv = static_cast<uint16_t*>(dv);
+  a.Sq = Sq; a.Sk = Sk; a.H = H;
+  a.causal = causal ? 1 : 0;
+  a.scale = 1.0f / sqrtf((float)D);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  return with_att(dtype, D, [&](auto e, auto d) { return launch_attn_bwd<decltype(e)::value, decltype(d)::value>(a, B, st); });
+}

@@ -186,3 +186,34 @@ def test_dequant_argument_errors():
     assert L.reels_hip_i8_dequant(None, fake, 4, 8, 8, 1, 0, fake, None) == -1
     assert "NULL" in _err()
     assert L.reels_hip_i8_dequant(None, None, 0, 8, 8, 1, 1, None, None) == 0  # empty: no work
+
+
+def test_attention_argument_errors():
+    L = _lib.lib()
+    fake = ctypes.c_void_p(4096)
+    # head dim, dtype, sizes, NULL operands, workspace: all rejected before any GPU work
+    assert L.reels_hip_attention_fwd(fake, fake, fake, None, 0, 1, 4, 4, 2, 96, _lib.BF16, fake,
+                                     None, None) == -1
+    assert "head_dim" in _err()
+    assert L.reels_hip_attention_fwd(fake, fake, fake, None, 0, 1, 4, 4, 2, 64, _lib.F32, fake,
+                                     None, None) == -2
+    assert L.reels_hip_attention_fwd(fake, fake, fake, None, 0, -1, 4, 4, 2, 64, _lib.BF16, fake,
+                                     None, None) == -1
+    assert L.reels_hip_attention_fwd(None, fake, fake, None, 0, 1, 4, 4, 2, 64, _lib.BF16, fake,
+                                     None, None) == -1
+    assert L.reels_hip_attention_fwd(fake, fake, fake, None, 0, 1, 4, 4, 2, 64, _lib.BF16, None,
+                                     None, None) == -1
+    assert L.reels_hip_attention_fwd(ctypes.c_void_p(4098), fake, fake, None, 0, 1, 4, 4, 2, 64,
+                                     _lib.BF16, fake, None, None) == -1  # unaligned
+    assert L.reels_hip_attention_fwd(fake, fake, fake, None, 0, 1, 1 << 24, 4, 64, 128, _lib.BF16,
+                                     fake, None, None) == -1  # one batch of q over 2 GiB
+    assert L.reels_hip_attention_bwd(fake, fake, fake, fake, fake, fake, None, 0, 1, 4, 4, 2, 64,
+                                     _lib.BF16, fake, fake, fake, None, 0, None) == -3
+    assert "workspace" in _err()
+    assert L.reels_hip_attention_bwd(fake, fake, fake, None, fake, fake, None, 0, 1, 4, 4, 2, 64,
+                                     _lib.BF16, fake, fake, fake, fake, 1 << 20, None) == -1
+    # nothing to compute: no queries in the forward
+    assert L.reels_hip_attention_fwd(None, None, None, None, 0, 1, 0, 4, 2, 64, _lib.BF16, None,
+                                     None, None) == 0
+    assert L.reels_hip_attention_workspace_bytes(2, 100, 3) == 2560
+    assert L.reels_hip_attention_workspace_bytes(-1, 1, 1) == 0
