@@ -71,6 +71,9 @@ def parse():
                     help="activation / LoRA element type: bf16 (the default workload) or f16 "
                          "(the reference's own int8 compute precision, the _f16 entry points)")
     ap.add_argument("--no-pack", action="store_true", help="skip the pack workload")
+    ap.add_argument("--no-attention", action="store_true", help="skip the attention workload")
+    ap.add_argument("--attention-only", action="store_true",
+                    help="run only the attention workload")
     ap.add_argument("--pack-only", action="store_true", help="run only the pack workload")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run three 1 GiB device-to-device copies (the reference kernel for "
@@ -169,6 +172,120 @@ def pack_bench(dev, reps=3):
                                                 "same run", "gbs": round(copy, 1),
                                         "achieved_over_copy": round(gbs / copy, 4)}}}
     return out
+
+
+# Wan-2.1-14B self-attention of one block: 32760 tokens (the projection workload's token
+# count), 40 heads of 128, no mask, not causal (src/models/wan21/transformer.jl:199)
+ATT_SHAPE = (1, 32760, 40, 128)
+
+
+def attention_flops(B, Sq, Sk, H, D):
+    """Algorithmic flops of forward (Q K^T and P V: 4 B H Sq Sk D) and backward (2.5 x forward:
+    dV, dP, dQ, dK and the score recomputation counted once, the usual accounting)."""
+    f = 4.0 * B * H * Sq * Sk * D
+    return f, 2.5 * f
+
+
+def attention_bench(dev, reps=3):
+    """Times reels_hip_attention_fwd + _bwd on the Wan-14B self-attention shape; returns the
+    "attention" result object, with torch's fused SDPA (flash / memory-efficient backends only)
+    on the same shape as the vendor reference."""
+    import torch
+    from reels_amd import _lib, memory_efficient_attention, memory_efficient_attention_backward
+    L = _lib.lib()
+    B, S, H, D = ATT_SHAPE
+    gen = torch.Generator(device=dev).manual_seed(5)
+    q, k, v, dy = (torch.randn((B, S, H, D), generator=gen, device=dev).to(torch.bfloat16)
+                   for _ in range(4))
+
+    def step():
+        r = memory_efficient_attention(q, k, v)
+        memory_efficient_attention_backward(q, k, v, dy, r.cache)
+    step()
+    torch.cuda.synchronize()
+    _lib.check("reels_hip_trace_start", L.reels_hip_trace_start(16 * reps))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    kern = {}
+    for n, t in _lib.trace_records():
+        c, tot = kern.get(n, (0, 0.0))
+        kern[n] = (c + 1, tot + t)
+    ff, fb = attention_flops(B, S, S, H, D)
+    fwd_ms = kern.get("attn_fwd_kernel", (1, float("nan")))[1] / reps
+    bwd_ms = sum(t for n, (c, t) in kern.items() if n != "attn_fwd_kernel") / reps
+    tflops = (ff + fb) / (ms * 1e-3) / 1e12
+    vendor = None
+    try:
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        qt, kt, vt, dyt = (x.transpose(1, 2).contiguous() for x in (q, k, v, dy))
+        qt.requires_grad_(); kt.requires_grad_(); vt.requires_grad_()
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            def vstep():
+                o = torch.nn.functional.scaled_dot_product_attention(qt, kt, vt)
+                o.backward(dyt)
+                qt.grad = kt.grad = vt.grad = None
+            vstep()
+            torch.cuda.synchronize()
+            e0.record()
+            for _ in range(reps):
+                vstep()
+            e1.record()
+            torch.cuda.synchronize()
+        vms = e0.elapsed_time(e1) / reps
+        vendor = {"what": "torch.nn.functional.scaled_dot_product_attention, flash / memory-efficient "
+                          "backends only, [B][H][S][D] contiguous bf16, forward + backward, same run",
+                  "ms": round(vms, 3), "tflops": round((ff + fb) / (vms * 1e-3) / 1e12, 1),
+                  "achieved_over_vendor": round(vms / ms, 4)}
+        del qt, kt, vt, dyt
+    except Exception as e:  # backend unavailable on this build: report why
+        vendor = {"what": "torch SDPA fused backends", "error": f"{type(e).__name__}: {e}"[:200]}
+    del q, k, v, dy
+    torch.cuda.empty_cache()
+    return {"metric": "attention TFLOP/s (forward + backward, algorithmic flops)",
+            "value": round(tflops, 1), "unit": "TFLOP/s", "dtype": "bf16",
+            "config": {"workload": "wan2.1-14b self-attention of one block: B=1, 32760 tokens, "
+                                   "40 heads x 128, no mask, not causal", "flops_fwd": ff,
+                       "flops_bwd": fb},
+            "ms": round(ms, 3), "fwd_ms": round(fwd_ms, 3), "bwd_ms": round(bwd_ms, 3),
+            "kernels": {n: {"launches": c // reps, "avg_ms": round(t / c, 4)} for n, (c, t) in kern.items()},
+            "roofline": {"kernel": "attn_fwd_kernel, attn_dkdv_kernel, attn_dq_kernel", "bound": "mfma",
+                         "achieved": round(tflops, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                         "fwd": round(ff / (fwd_ms * 1e-3) / 1e12, 1),
+                         "bwd": round(fb / (bwd_ms * 1e-3) / 1e12, 1)},
+            "vendor_sdpa": vendor}
+
+
+def attention_cpu_baseline(seconds=5.0):
+    """The reference's CPU attention (memory_efficient_attention with its backward,
+    attention.jl:106-221) restated in the oracle (scalar f64), timed on a bounded sample: one head
+    of the Wan-14B shape, all 32760 keys, as many queries as fit the time."""
+    import numpy as np
+    import oracle
+    B, S, H, D = ATT_SHAPE
+    rng = np.random.default_rng(3)
+    k = oracle.f32_to_bf16(rng.standard_normal((1, S, 1, D)).astype(np.float32))
+    v = oracle.f32_to_bf16(rng.standard_normal((1, S, 1, D)).astype(np.float32))
+    nq = 8
+    while True:
+        q = oracle.f32_to_bf16(rng.standard_normal((1, nq, 1, D)).astype(np.float32))
+        dy = oracle.f32_to_bf16(rng.standard_normal((1, nq, 1, D)).astype(np.float32))
+        t0 = time.perf_counter()
+        oracle.attention_forward(q, k, v)
+        oracle.attention_backward(q, k, v, dy)
+        dt = time.perf_counter() - t0
+        if dt > seconds / 4 or nq >= 4096:
+            break
+        nq *= 2
+    ff, fb = attention_flops(1, nq, S, 1, D)
+    return {"value": round((ff + fb) / dt / 1e12, 5), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"one head, {nq} queries x {S} keys x {D}, forward + backward, oracle (scalar "
+                      f"f64 C), {dt:.2f} s"}
 
 
 def copy_gbs(dev, nbytes=4 << 30, reps=5):
@@ -317,6 +434,12 @@ def main():
     if args.pack_only:
         print(json.dumps({"pack": pack_bench(dev)}))
         return
+    if args.attention_only:
+        att = attention_bench(dev)
+        if args.cpu_seconds > 0:
+            att["cpu_baseline"] = attention_cpu_baseline(min(5.0, args.cpu_seconds))
+        print(json.dumps({"attention": att}))
+        return
     gen = torch.Generator(device=dev).manual_seed(1234)
     M = args.tokens
     act = {"f16": torch.float16, "f32": torch.float32}.get(args.dtype, torch.bfloat16)
@@ -420,6 +543,14 @@ def main():
         pack = pack_bench(dev)
         if args.cpu_seconds > 0:
             pack["cpu_baseline"] = pack_cpu_baseline(min(5.0, args.cpu_seconds))
+    att = None
+    if not args.no_attention and args.dtype == "bf16" and args.offload == "none":
+        if args.no_pack:
+            del projs
+            torch.cuda.empty_cache()
+        att = attention_bench(dev)
+        if args.cpu_seconds > 0:
+            att["cpu_baseline"] = attention_cpu_baseline(min(5.0, args.cpu_seconds))
 
     out = {
         "metric": METRIC, "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1,
@@ -439,6 +570,7 @@ def main():
         "cpu_baseline": cpu,
         "kernels": kernels,
         "pack": pack,
+        "attention": att,
         "device": torch.cuda.get_device_name(dev),
     }
     print(json.dumps(out))
