@@ -172,15 +172,20 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttArgs a) {
     const int64_t key0 = (int64_t)j * KT;
 
     // S^T tiles: s[kt][qt] lane: keys key0 + 16 kt + 4 g + v, query q0 + 16 qt + l16
+    // (k-block outer: eight independent accumulators between two MFMAs on the same one)
     f32x4 s[4][2];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      s[kt][0] = s[kt][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int kt = 0; kt < 4; ++kt) s[kt][0] = s[kt][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) {
-        const u32x4 kf = *reinterpret_cast<const u32x4*>(sk + toff<D>(16 * kt + l16, kb * 32 + g * 8));
-        s[kt][0] = E::mfma16(E::as8(kf), E::as8(qf[0][kb]), s[kt][0]);
-        s[kt][1] = E::mfma16(E::as8(kf), E::as8(qf[1][kb]), s[kt][1]);
+    for (int kb = 0; kb < NKB; ++kb) {
+      u32x4 kf[4];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+        kf[kt] = *reinterpret_cast<const u32x4*>(sk + toff<D>(16 * kt + l16, kb * 32 + g * 8));
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        s[kt][0] = E::mfma16(E::as8(kf[kt]), E::as8(qf[0][kb]), s[kt][0]);
+        s[kt][1] = E::mfma16(E::as8(kf[kt]), E::as8(qf[1][kb]), s[kt][1]);
       }
     }
     // online softmax per query (base 2): masked scores are -inf and get probability 0
@@ -228,9 +233,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttArgs a) {
     }
     // O^T += V^T P^T: A = V^T rows d = 16 dt + l16, keys {32 kb2 + 4 g ..} and {32 kb2 + 16 + 4 g ..}
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
+    for (int kb2 = 0; kb2 < 2; ++kb2)
 #pragma unroll
-      for (int kb2 = 0; kb2 < 2; ++kb2) {
+      for (int dt = 0; dt < NDT; ++dt) {
         const u32x4 vf = read_tr<D>(sv, 32 * kb2 + 4 * g, 32 * kb2 + 16 + 4 * g, 16 * dt, l16);
         oacc[dt][0] = E::mfma16(E::as8(vf), E::as8(pb[kb2][0]), oacc[dt][0]);
         oacc[dt][1] = E::mfma16(E::as8(vf), E::as8(pb[kb2][1]), oacc[dt][1]);
@@ -516,9 +521,9 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttArgs a) {
       }
     }
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
+    for (int kb2 = 0; kb2 < 2; ++kb2)
 #pragma unroll
-      for (int kb2 = 0; kb2 < 2; ++kb2) {
+      for (int dt = 0; dt < NDT; ++dt) {
         const u32x4 kt_ = read_tr<D>(sk, 32 * kb2 + 4 * g, 32 * kb2 + 16 + 4 * g, 16 * dt, l16);
         qacc[dt][0] = E::mfma16(E::as8(kt_), E::as8(db[kb2][0]), qacc[dt][0]);
         qacc[dt][1] = E::mfma16(E::as8(kt_), E::as8(db[kb2][1]), qacc[dt][1]);
