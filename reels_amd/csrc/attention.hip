@@ -28,7 +28,7 @@ constexpr int QW = 32;    // queries per wave (forward, dQ)
 constexpr int QB = 128;   // queries per workgroup (forward, dQ)
 constexpr int KW = 16;    // keys per wave (dK / dV)
 constexpr int KB = 64;    // keys per workgroup (dK / dV)
-constexpr int QT = 32;    // queries per step (dK / dV)
+constexpr int QT = 64;    // queries per step (dK / dV)
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.6931471805599453f;
 }  // namespace att
@@ -287,10 +287,10 @@ __global__ __launch_bounds__(256) void attn_corr_kernel(AttArgs a, int64_t B) {
 }
 
 // dK, dV: a workgroup takes 64 keys of one (batch, head), 16 per wave, and streams the queries
-// in steps of 32 (Q and dY tiles through a two-stage LDS ring, lse and correction beside them).
+// in steps of 64 (Q and dY tiles through a two-stage LDS ring, lse and correction beside them).
 // Per step: S = Q K^T and dP = dY V^T (lane l: queries 16 qt + 4 g + v, key l16), P from lse,
 // dS = P (dP - correction), dV^T += dY^T P and dK^T += Q^T dS (A operands read transposed, the
-// query order {4g..4g+3, 16+4g..16+4g+3} of the accumulators).
+// query order {4g..4g+3, 16+4g..16+4g+3} of each 32-query block of the accumulators).
 template <int ELT, int D>
 __global__ __launch_bounds__(256, 2) void attn_dkdv_kernel(AttArgs a) {
   using E = Elt<ELT>;
@@ -320,11 +320,11 @@ __global__ __launch_bounds__(256, 2) void attn_dkdv_kernel(AttArgs a) {
   const uint16_t* dbase = a.dy + (b * Sq * H + h) * D;
   const uint32_t nrec = (uint32_t)(((Sq - 1) * H + 1) * D * 2);
   const i32x4 rq = buffer_rsrc(qbase, nrec), rd = buffer_rsrc(dbase, nrec);
-  float* sstat = reinterpret_cast<float*>(smem + 4 * TB);  // [2 stages][lse 32, corr 32]
+  float* sstat = reinterpret_cast<float*>(smem + 4 * TB);  // [2 stages][lse QT, corr QT]
   auto issue = [&](int j) {
     uint8_t* st = smem + (j & 1) * 2 * TB;
-    // a 32-row tile: half the copies of copy_tile's 64 rows
-    constexpr int CH = D / 8, RPC = 64 / CH, NCT = 32 * CH / 64;  // copies per tile
+    // a QT-row tile (QT = 64: the copies of copy_tile)
+    constexpr int CH = D / 8, RPC = 64 / CH, NCT = QT * CH / 64;  // copies per tile
 #pragma unroll
     for (int i = 0; i < (NCT + 3) / 4; ++i) {
       const int c = w * ((NCT + 3) / 4) + i;
@@ -342,14 +342,14 @@ __global__ __launch_bounds__(256, 2) void attn_dkdv_kernel(AttArgs a) {
   // never make the compiler wait for copies it cannot see
   float stv = 0.0f;
   auto stats_load = [&](int j) {
-    if (t < 64) {
-      const int64_t qi = (int64_t)j * QT + (t & 31);
+    if (t < 2 * QT) {
+      const int64_t qi = (int64_t)j * QT + (t % QT);
       stv = 0.0f;
-      if (qi < Sq) stv = (t < 32) ? a.lse[(b * H + h) * Sq + qi] * LOG2E : a.corr[(b * H + h) * Sq + qi];
+      if (qi < Sq) stv = (t < QT) ? a.lse[(b * H + h) * Sq + qi] * LOG2E : a.corr[(b * H + h) * Sq + qi];
     }
   };
   auto stats_store = [&](int j) {
-    if (t < 64) sstat[(j & 1) * 64 + t] = stv;
+    if (t < 2 * QT) sstat[(j & 1) * 2 * QT + t] = stv;
   };
 
   f32x4 dvacc[NDT], dkacc[NDT];
@@ -368,43 +368,52 @@ __global__ __launch_bounds__(256, 2) void attn_dkdv_kernel(AttArgs a) {
     if (j + 1 < nsteps) { stats_load(j + 1); issue(j + 1); }
     const uint8_t* sq = smem + (j & 1) * 2 * TB;
     const uint8_t* sd = sq + TB;
-    const float* ls = sstat + (j & 1) * 64;
-    // S and dP tiles [qt]: lane queries 16 qt + 4 g + v, key l16
-    f32x4 s[2], dp[2];
+    const float* ls = sstat + (j & 1) * 2 * QT;
+    constexpr int NQT = QT / 16;  // 16-query tiles per step
+    // S and dP tiles [qt]: lane queries 16 qt + 4 g + v, key l16 (k-block outer: independent
+    // accumulators between two MFMAs on the same one)
+    f32x4 s[NQT], dp[NQT];
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-      s[qt] = dp[qt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int qt = 0; qt < NQT; ++qt) s[qt] = dp[qt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) {
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int qt = 0; qt < NQT; ++qt) {
         const u32x4 qa = *reinterpret_cast<const u32x4*>(sq + toff<D>(16 * qt + l16, kb * 32 + g * 8));
         const u32x4 da = *reinterpret_cast<const u32x4*>(sd + toff<D>(16 * qt + l16, kb * 32 + g * 8));
         s[qt] = E::mfma16(E::as8(qa), E::as8(kf[kb]), s[qt]);
         dp[qt] = E::mfma16(E::as8(da), E::as8(vf[kb]), dp[qt]);
       }
+    // B operands per 32-query block kb2: key l16, queries {32 kb2 + 4g ..+3, 32 kb2 + 16 + 4g ..+3}
+    u32x4 pb[NQT / 2], db[NQT / 2];
+#pragma unroll
+    for (int kb2 = 0; kb2 < NQT / 2; ++kb2) {
+      float p[2][4], ds[2][4];
+#pragma unroll
+      for (int hq = 0; hq < 2; ++hq)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int qt = 2 * kb2 + hq;
+          const int ql = 16 * qt + 4 * g + v;
+          const int64_t qi = (int64_t)j * QT + ql;
+          const bool vis = att_visible(a, qi, kj);
+          p[hq][v] = vis ? exp2f(s[qt][v] * sl2 - ls[ql]) : 0.0f;
+          ds[hq][v] = vis ? p[hq][v] * (dp[qt][v] - ls[QT + ql]) : 0.0f;
+        }
+      pb[kb2][0] = E::pack2(p[0][0], p[0][1]); pb[kb2][1] = E::pack2(p[0][2], p[0][3]);
+      pb[kb2][2] = E::pack2(p[1][0], p[1][1]); pb[kb2][3] = E::pack2(p[1][2], p[1][3]);
+      db[kb2][0] = E::pack2(ds[0][0], ds[0][1]); db[kb2][1] = E::pack2(ds[0][2], ds[0][3]);
+      db[kb2][2] = E::pack2(ds[1][0], ds[1][1]); db[kb2][3] = E::pack2(ds[1][2], ds[1][3]);
     }
-    float p[2][4], ds[2][4];
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt)
+    for (int kb2 = 0; kb2 < NQT / 2; ++kb2)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int ql = 16 * qt + 4 * g + v;
-        const int64_t qi = (int64_t)j * QT + ql;
-        const bool vis = att_visible(a, qi, kj);
-        p[qt][v] = vis ? exp2f(s[qt][v] * sl2 - ls[ql]) : 0.0f;
-        ds[qt][v] = vis ? p[qt][v] * (dp[qt][v] - ls[32 + ql]) : 0.0f;
+      for (int dt = 0; dt < NDT; ++dt) {
+        const u32x4 da = read_tr<D>(sd, 32 * kb2 + 4 * g, 32 * kb2 + 16 + 4 * g, 16 * dt, l16);
+        const u32x4 qa = read_tr<D>(sq, 32 * kb2 + 4 * g, 32 * kb2 + 16 + 4 * g, 16 * dt, l16);
+        dvacc[dt] = E::mfma16(E::as8(da), E::as8(pb[kb2]), dvacc[dt]);
+        dkacc[dt] = E::mfma16(E::as8(qa), E::as8(db[kb2]), dkacc[dt]);
       }
-    u32x4 pb, db;  // B operands: key l16, queries {4g..4g+3, 16+4g..16+4g+3}
-    pb[0] = E::pack2(p[0][0], p[0][1]); pb[1] = E::pack2(p[0][2], p[0][3]);
-    pb[2] = E::pack2(p[1][0], p[1][1]); pb[3] = E::pack2(p[1][2], p[1][3]);
-    db[0] = E::pack2(ds[0][0], ds[0][1]); db[1] = E::pack2(ds[0][2], ds[0][3]);
-    db[2] = E::pack2(ds[1][0], ds[1][1]); db[3] = E::pack2(ds[1][2], ds[1][3]);
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      const u32x4 da = read_tr<D>(sd, 4 * g, 16 + 4 * g, 16 * dt, l16);
-      const u32x4 qa = read_tr<D>(sq, 4 * g, 16 + 4 * g, 16 * dt, l16);
-      dvacc[dt] = E::mfma16(E::as8(da), E::as8(pb), dvacc[dt]);
-      dkacc[dt] = E::mfma16(E::as8(qa), E::as8(db), dkacc[dt]);
-    }
   }
   // dV[kj][d], dK[kj][d] = scale dK^T: lane holds d = 16 dt + 4 g + v of key kj
   if (kj < Sk) {
@@ -595,7 +604,7 @@ static int launch_attn_bwd(const AttArgs& a, int64_t B, hipStream_t st) {
   }
   if (int rc = check_launch("attn_corr_kernel")) return rc;
   if (a.Sk > 0) {
-    const int lds = 4 * att::QT * D * 2 + 512;
+    const int lds = 4 * att::QT * D * 2 + 2 * 2 * att::QT * 4;  // Q, dY rings + lse / corr
     if (hipError_t e = set_lds(attn_dkdv_kernel<ELT, D>, lds))
       return fail(REELS_HIP_EHIP, std::string("attention bwd: hipFuncSetAttribute: ") + hipGetErrorString(e));
     const dim3 grid((unsigned)ceil_div(a.Sk, att::KB), (unsigned)a.H, (unsigned)B);
