@@ -85,11 +85,17 @@ struct AttArgs {
   float scale;           // 1 / sqrt(Float32(D)) (attention.jl:129)
 };
 
+// Visibility modes, fixed at compile time so that the common case carries no branch in the
+// kernels' inner loops: VM 0 = no mask, not causal (bounds only); VM 1 = causal; VM 2 = a mask
+// (and causal when a.causal).
+template <int VM>
 __device__ __forceinline__ bool att_visible(const AttArgs& a, int64_t qi, int64_t kj) {
-  if (kj >= a.Sk || qi >= a.Sq) return false;
+  const bool in = (kj < a.Sk) & (qi < a.Sq);
+  if constexpr (VM == 0) return in;
+  if constexpr (VM == 1) return in & (kj <= qi);
+  if (!in) return false;
   if (a.causal && kj > qi) return false;
-  if (a.mask != nullptr && a.mask[qi * a.Sk + kj] == 0) return false;
-  return true;
+  return a.mask[qi * a.Sk + kj] != 0;
 }
 
 // Copies of one 64-row tile of a [B][S][H][D] tensor (rows = tokens of one batch and head) into
@@ -112,7 +118,7 @@ __device__ __forceinline__ void copy_tile(const i32x4& rsrc, int64_t row0, int64
 
 // ---------------------------------------------------------------------------------------------
 // forward
-template <int ELT, int D>
+template <int ELT, int D, int VM>
 __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttArgs a) {
   using E = Elt<ELT>;
   using namespace att;
@@ -199,7 +205,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttArgs a) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int64_t kj = key0 + 16 * kt + 4 * g + v;
-          const float x = att_visible(a, qi, kj) ? s[kt][qt][v] * sl2 : -INFINITY;
+          const float x = att_visible<VM>(a, qi, kj) ? s[kt][qt][v] * sl2 : -INFINITY;
           s[kt][qt][v] = x;
           mt = fmaxf(mt, x);
         }
@@ -291,7 +297,7 @@ __global__ __launch_bounds__(256) void attn_corr_kernel(AttArgs a, int64_t B) {
 // Per step: S = Q K^T and dP = dY V^T (lane l: queries 16 qt + 4 g + v, key l16), P from lse,
 // dS = P (dP - correction), dV^T += dY^T P and dK^T += Q^T dS (A operands read transposed, the
 // query order {4g..4g+3, 16+4g..16+4g+3} of each 32-query block of the accumulators).
-template <int ELT, int D>
+template <int ELT, int D, int VM>
 __global__ __launch_bounds__(256, 2) void attn_dkdv_kernel(AttArgs a) {
   using E = Elt<ELT>;
   using namespace att;
@@ -396,7 +402,7 @@ __global__ __launch_bounds__(256, 2) void attn_dkdv_kernel(AttArgs a) {
           const int qt = 2 * kb2 + hq;
           const int ql = 16 * qt + 4 * g + v;
           const int64_t qi = (int64_t)j * QT + ql;
-          const bool vis = att_visible(a, qi, kj);
+          const bool vis = att_visible<VM>(a, qi, kj);
           p[hq][v] = vis ? exp2f(s[qt][v] * sl2 - ls[ql]) : 0.0f;
           ds[hq][v] = vis ? p[hq][v] * (dp[qt][v] - ls[QT + ql]) : 0.0f;
         }
@@ -433,7 +439,7 @@ __global__ __launch_bounds__(256, 2) void attn_dkdv_kernel(AttArgs a) {
 // dQ: the forward's structure. Per key tile: S^T = K Q^T and dP^T = V dY^T (A operands K and V
 // rows from LDS, B operands this wave's Q and dY fragments), P from lse, dS = P (dP - corr),
 // dQ^T += K^T dS^T with K^T read transposed in the accumulators' key order.
-template <int ELT, int D>
+template <int ELT, int D, int VM>
 __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttArgs a) {
   using E = Elt<ELT>;
   using namespace att;
@@ -515,7 +521,7 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttArgs a) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             const int64_t kj = key0 + 16 * kt + 4 * g + v;
-            const bool vis = att_visible(a, qi, kj);
+            const bool vis = att_visible<VM>(a, qi, kj);
             const float p = vis ? exp2f(s[qt][v] * sl2 - lse2[qt]) : 0.0f;
             dsv[half][qt][v] = vis ? p * (dp[qt][v] - cr[qt]) : 0.0f;
           }
@@ -586,14 +592,25 @@ static hipError_t set_lds(K kernel, int bytes) {
   return hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
 }
 
+// calls f(std::integral_constant<int, VM>) for the arguments' visibility mode
+template <typename F>
+static int with_vm(const AttArgs& a, F&& f) {
+  if (a.mask != nullptr) return f(std::integral_constant<int, 2>{});
+  if (a.causal) return f(std::integral_constant<int, 1>{});
+  return f(std::integral_constant<int, 0>{});
+}
+
 template <int ELT, int D>
 static int launch_attn_fwd(const AttArgs& a, int64_t B, hipStream_t st) {
-  const int lds = 4 * att::KT * D * 2;
-  if (hipError_t e = set_lds(attn_fwd_kernel<ELT, D>, lds))
-    return fail(REELS_HIP_EHIP, std::string("attention fwd: hipFuncSetAttribute: ") + hipGetErrorString(e));
-  const dim3 grid((unsigned)ceil_div(a.Sq, att::QB), (unsigned)a.H, (unsigned)B);
-  { TraceScope _ts(st, "attn_fwd_kernel"); attn_fwd_kernel<ELT, D><<<grid, 256, lds, st>>>(a); }
-  return check_launch("attn_fwd_kernel");
+  return with_vm(a, [&](auto vm) {
+    constexpr int VM = decltype(vm)::value;
+    const int lds = 4 * att::KT * D * 2;
+    if (hipError_t e = set_lds(attn_fwd_kernel<ELT, D, VM>, lds))
+      return fail(REELS_HIP_EHIP, std::string("attention fwd: hipFuncSetAttribute: ") + hipGetErrorString(e));
+    const dim3 grid((unsigned)ceil_div(a.Sq, att::QB), (unsigned)a.H, (unsigned)B);
+    { TraceScope _ts(st, "attn_fwd_kernel"); attn_fwd_kernel<ELT, D, VM><<<grid, 256, lds, st>>>(a); }
+    return check_launch("attn_fwd_kernel");
+  });
 }
 
 template <int ELT, int D>
@@ -603,20 +620,23 @@ static int launch_attn_bwd(const AttArgs& a, int64_t B, hipStream_t st) {
     attn_corr_kernel<ELT, D><<<(unsigned)ceil_div(B * a.Sq * a.H, 256), 256, 0, st>>>(a, B);
   }
   if (int rc = check_launch("attn_corr_kernel")) return rc;
-  if (a.Sk > 0) {
-    const int lds = 4 * att::QT * D * 2 + 2 * 2 * att::QT * 4;  // Q, dY rings + lse / corr
-    if (hipError_t e = set_lds(attn_dkdv_kernel<ELT, D>, lds))
+  return with_vm(a, [&](auto vm) {
+    constexpr int VM = decltype(vm)::value;
+    if (a.Sk > 0) {
+      const int lds = 4 * att::QT * D * 2 + 2 * 2 * att::QT * 4;  // Q, dY rings + lse / corr
+      if (hipError_t e = set_lds(attn_dkdv_kernel<ELT, D, VM>, lds))
+        return fail(REELS_HIP_EHIP, std::string("attention bwd: hipFuncSetAttribute: ") + hipGetErrorString(e));
+      const dim3 grid((unsigned)ceil_div(a.Sk, att::KB), (unsigned)a.H, (unsigned)B);
+      { TraceScope _ts(st, "attn_dkdv_kernel"); attn_dkdv_kernel<ELT, D, VM><<<grid, 256, lds, st>>>(a); }
+      if (int rc = check_launch("attn_dkdv_kernel")) return rc;
+    }
+    const int lds = 4 * att::KT * D * 2;
+    if (hipError_t e = set_lds(attn_dq_kernel<ELT, D, VM>, lds))
       return fail(REELS_HIP_EHIP, std::string("attention bwd: hipFuncSetAttribute: ") + hipGetErrorString(e));
-    const dim3 grid((unsigned)ceil_div(a.Sk, att::KB), (unsigned)a.H, (unsigned)B);
-    { TraceScope _ts(st, "attn_dkdv_kernel"); attn_dkdv_kernel<ELT, D><<<grid, 256, lds, st>>>(a); }
-    if (int rc = check_launch("attn_dkdv_kernel")) return rc;
-  }
-  const int lds = 4 * att::KT * D * 2;
-  if (hipError_t e = set_lds(attn_dq_kernel<ELT, D>, lds))
-    return fail(REELS_HIP_EHIP, std::string("attention bwd: hipFuncSetAttribute: ") + hipGetErrorString(e));
-  const dim3 grid((unsigned)ceil_div(a.Sq, att::QB), (unsigned)a.H, (unsigned)B);
-  { TraceScope _ts(st, "attn_dq_kernel"); attn_dq_kernel<ELT, D><<<grid, 256, lds, st>>>(a); }
-  return check_launch("attn_dq_kernel");
+    const dim3 grid((unsigned)ceil_div(a.Sq, att::QB), (unsigned)a.H, (unsigned)B);
+    { TraceScope _ts(st, "attn_dq_kernel"); attn_dq_kernel<ELT, D, VM><<<grid, 256, lds, st>>>(a); }
+    return check_launch("attn_dq_kernel");
+  });
 }
 
 template <typename F>
