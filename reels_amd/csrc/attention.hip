@@ -211,8 +211,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttArgs a) {
         }
       mt = wave_max16(mt);
       const float mnew = fmaxf(mrun[qt], mt);
-      // no visible key yet: nothing accumulated, keep the factor finite
-      const float alpha = mnew == -INFINITY ? 1.0f : exp2f(mrun[qt] - mnew);
+      // Without a mask every query in range sees key 0 in the first tile, so its maximum is
+      // finite from then on and exp2(-inf - m) is 0: the guards below matter only with a mask
+      // (a query with no visible key yet: nothing accumulated, keep the factor finite)
+      const float alpha = (VM == 2 && mnew == -INFINITY) ? 1.0f : exp2f(mrun[qt] - mnew);
       mrun[qt] = mnew;
       float ps = 0.0f;
       float p[4][4];
@@ -221,7 +223,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttArgs a) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const float x = s[kt][qt][v];
-          p[kt][v] = x == -INFINITY ? 0.0f : exp2f(x - mnew);
+          p[kt][v] = (VM == 2 && x == -INFINITY) ? 0.0f : exp2f(x - mnew);
           ps += p[kt][v];
         }
       lrun[qt] = lrun[qt] * alpha + ps;
