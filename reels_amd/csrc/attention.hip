@@ -9,7 +9,8 @@
 // Forward: a workgroup takes 128 queries of one (batch, head), 32 per wave as two 16-query MFMA
 // tiles, and streams the keys in tiles of 64 through a two-stage LDS ring (LDS-DMA copies). Per
 // key tile: S^T = K Q^T on v_mfma_f32_16x16x32 (lane l holds keys 4(l/16)+v of a 16-key tile for
-// query l%16), the running maximum and sum in the base-2 domain, P rounded to the element type,
+// query l%16), the running maximum and sum in the base-2 domain, P rounded to the element type
+// (v_cvt_pk_bf16_f32 for bf16),
 // O^T += V^T P^T with V^T fragments read transposed from LDS (ds_read_b64_tr_b16). The P operand
 // takes its 8 keys per lane as keys {4g..4g+3} and {16+4g..16+4g+3} of a 32-key block (g = l/16):
 // exactly what the score accumulators hold, so no lane exchange is needed; the V^T reads use the
@@ -233,10 +234,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttArgs a) {
         for (int v = 0; v < 4; ++v) oacc[dt][qt][v] *= alpha;
 #pragma unroll
       for (int kb2 = 0; kb2 < 2; ++kb2) {
-        pb[kb2][qt][0] = E::pack2(p[2 * kb2][0], p[2 * kb2][1]);
-        pb[kb2][qt][1] = E::pack2(p[2 * kb2][2], p[2 * kb2][3]);
-        pb[kb2][qt][2] = E::pack2(p[2 * kb2 + 1][0], p[2 * kb2 + 1][1]);
-        pb[kb2][qt][3] = E::pack2(p[2 * kb2 + 1][2], p[2 * kb2 + 1][3]);
+        pb[kb2][qt][0] = E::pack2_fast(p[2 * kb2][0], p[2 * kb2][1]);
+        pb[kb2][qt][1] = E::pack2_fast(p[2 * kb2][2], p[2 * kb2][3]);
+        pb[kb2][qt][2] = E::pack2_fast(p[2 * kb2 + 1][0], p[2 * kb2 + 1][1]);
+        pb[kb2][qt][3] = E::pack2_fast(p[2 * kb2 + 1][2], p[2 * kb2 + 1][3]);
       }
     }
     // O^T += V^T P^T: A = V^T rows d = 16 dt + l16, keys {32 kb2 + 4 g ..} and {32 kb2 + 16 + 4 g ..}
@@ -408,10 +409,10 @@ __global__ __launch_bounds__(256, 2) void attn_dkdv_kernel(AttArgs a) {
           p[hq][v] = vis ? exp2f(s[qt][v] * sl2 - ls[ql]) : 0.0f;
           ds[hq][v] = vis ? p[hq][v] * (dp[qt][v] - ls[QT + ql]) : 0.0f;
         }
-      pb[kb2][0] = E::pack2(p[0][0], p[0][1]); pb[kb2][1] = E::pack2(p[0][2], p[0][3]);
-      pb[kb2][2] = E::pack2(p[1][0], p[1][1]); pb[kb2][3] = E::pack2(p[1][2], p[1][3]);
-      db[kb2][0] = E::pack2(ds[0][0], ds[0][1]); db[kb2][1] = E::pack2(ds[0][2], ds[0][3]);
-      db[kb2][2] = E::pack2(ds[1][0], ds[1][1]); db[kb2][3] = E::pack2(ds[1][2], ds[1][3]);
+      pb[kb2][0] = E::pack2_fast(p[0][0], p[0][1]); pb[kb2][1] = E::pack2_fast(p[0][2], p[0][3]);
+      pb[kb2][2] = E::pack2_fast(p[1][0], p[1][1]); pb[kb2][3] = E::pack2_fast(p[1][2], p[1][3]);
+      db[kb2][0] = E::pack2_fast(ds[0][0], ds[0][1]); db[kb2][1] = E::pack2_fast(ds[0][2], ds[0][3]);
+      db[kb2][2] = E::pack2_fast(ds[1][0], ds[1][1]); db[kb2][3] = E::pack2_fast(ds[1][2], ds[1][3]);
     }
 #pragma unroll
     for (int kb2 = 0; kb2 < NQT / 2; ++kb2)
@@ -531,10 +532,10 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttArgs a) {
       }
 #pragma unroll
       for (int qt = 0; qt < 2; ++qt) {
-        db[kb2][qt][0] = E::pack2(dsv[0][qt][0], dsv[0][qt][1]);
-        db[kb2][qt][1] = E::pack2(dsv[0][qt][2], dsv[0][qt][3]);
-        db[kb2][qt][2] = E::pack2(dsv[1][qt][0], dsv[1][qt][1]);
-        db[kb2][qt][3] = E::pack2(dsv[1][qt][2], dsv[1][qt][3]);
+        db[kb2][qt][0] = E::pack2_fast(dsv[0][qt][0], dsv[0][qt][1]);
+        db[kb2][qt][1] = E::pack2_fast(dsv[0][qt][2], dsv[0][qt][3]);
+        db[kb2][qt][2] = E::pack2_fast(dsv[1][qt][0], dsv[1][qt][1]);
+        db[kb2][qt][3] = E::pack2_fast(dsv[1][qt][2], dsv[1][qt][3]);
       }
     }
 #pragma unroll

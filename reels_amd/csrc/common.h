@@ -108,6 +108,13 @@ template <> struct Elt<REELS_HIP_BF16> {
   static __device__ __forceinline__ float hi(uint32_t w) { return bf16_hi(w); }
   static __device__ __forceinline__ uint32_t bits(float f) { return f32_to_bf16_bits(f); }
   static __device__ __forceinline__ uint32_t pack2(float a, float b) { return pack_bf16x2(a, b); }
+  // the same rounding for finite values in one v_cvt_pk_bf16_f32 (NaN patterns may differ from
+  // pack2's, and f32 denormals follow the denormal mode): for MFMA operands computed in a kernel
+  static __device__ __forceinline__ uint32_t pack2_fast(float a, float b) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    const bf2 v = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, v);
+  }
   static __device__ __forceinline__ v8 as8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
   static __device__ __forceinline__ v8 from_i8x8(uint32_t l, uint32_t h) { return i8x8_to_bf16x8(l, h); }
   static __device__ __forceinline__ f32x4 mfma16(v8 a, v8 b, f32x4 c) {
@@ -130,6 +137,7 @@ template <> struct Elt<REELS_HIP_F16> {
     return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
   }
   static __device__ __forceinline__ uint32_t pack2(float a, float b) { return bits(a) | (bits(b) << 16); }
+  static __device__ __forceinline__ uint32_t pack2_fast(float a, float b) { return pack2(a, b); }
   static __device__ __forceinline__ v8 as8(u32x4 v) { return __builtin_bit_cast(f16x8, v); }
   // int8 -> binary16 is exact (|q| <= 127 fits the 11-bit significand)
   static __device__ __forceinline__ v8 from_i8x8(uint32_t l, uint32_t h) {
