@@ -216,7 +216,6 @@ __global__ __launch_bounds__(256) void colgrad_kernel(const uint16_t* __restrict
                                                       int rp, int64_t tokens_per_split,
                                                       float* __restrict__ part) {
   using E = Elt<ELT>;
-  typedef typename E::v8 V8;
   using namespace cg;
   __shared__ __attribute__((aligned(16))) uint16_t ssrc[TM * SROW];
   __shared__ __attribute__((aligned(16))) uint16_t slm[TM * LROW];
