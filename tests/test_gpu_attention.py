@@ -98,6 +98,8 @@ CASES = [
     (1, 390, 257, 2, 128, False, False, "bf16"), # image keys (I2V cross-attention, 257 tokens)
     (1, 1, 5, 1, 64, False, False, "bf16"),
     (3, 65, 129, 2, 128, False, True, "f16"),
+    (2, 100, 300, 2, 64, True, False, "f16"),    # causal with more keys than queries, batch 2
+    (2, 129, 129, 3, 128, True, True, "bf16"),   # mask and causal together
 ]
 
 
