@@ -42,6 +42,10 @@ __device__ __forceinline__ uint32_t toff(int r, int d) {
   return (uint32_t)(r * D * 2 + ((((d >> 3) ^ (r & (CH - 1)))) << 4) + (d & 7) * 2);
 }
 
+// 2^x on v_exp_f32 alone: exp2f adds a range scaling for results below 2^-126, probabilities
+// that make no difference to any sum here
+__device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 __device__ __forceinline__ float wave_max16(float x) {  // over lanes l, l^16, l^32, l^48
   x = fmaxf(x, __shfl_xor(x, 16));
   return fmaxf(x, __shfl_xor(x, 32));
@@ -215,7 +219,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttArgs a) {
       // Without a mask every query in range sees key 0 in the first tile, so its maximum is
       // finite from then on and exp2(-inf - m) is 0: the guards below matter only with a mask
       // (a query with no visible key yet: nothing accumulated, keep the factor finite)
-      const float alpha = (VM == 2 && mnew == -INFINITY) ? 1.0f : exp2f(mrun[qt] - mnew);
+      const float alpha = (VM == 2 && mnew == -INFINITY) ? 1.0f : ex2(mrun[qt] - mnew);
       mrun[qt] = mnew;
       float ps = 0.0f;
       float p[4][4];
@@ -224,7 +228,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttArgs a) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const float x = s[kt][qt][v];
-          p[kt][v] = (VM == 2 && x == -INFINITY) ? 0.0f : exp2f(x - mnew);
+          p[kt][v] = (VM == 2 && x == -INFINITY) ? 0.0f : ex2(x - mnew);
           ps += p[kt][v];
         }
       lrun[qt] = lrun[qt] * alpha + ps;
@@ -406,7 +410,7 @@ __global__ __launch_bounds__(256, 2) void attn_dkdv_kernel(AttArgs a) {
           const int ql = 16 * qt + 4 * g + v;
           const int64_t qi = (int64_t)j * QT + ql;
           const bool vis = att_visible<VM>(a, qi, kj);
-          p[hq][v] = vis ? exp2f(s[qt][v] * sl2 - ls[ql]) : 0.0f;
+          p[hq][v] = vis ? ex2(s[qt][v] * sl2 - ls[ql]) : 0.0f;
           ds[hq][v] = vis ? p[hq][v] * (dp[qt][v] - ls[QT + ql]) : 0.0f;
         }
       pb[kb2][0] = E::pack2_fast(p[0][0], p[0][1]); pb[kb2][1] = E::pack2_fast(p[0][2], p[0][3]);
@@ -525,7 +529,7 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttArgs a) {
           for (int v = 0; v < 4; ++v) {
             const int64_t kj = key0 + 16 * kt + 4 * g + v;
             const bool vis = att_visible<VM>(a, qi, kj);
-            const float p = vis ? exp2f(s[qt][v] * sl2 - lse2[qt]) : 0.0f;
+            const float p = vis ? ex2(s[qt][v] * sl2 - lse2[qt]) : 0.0f;
             dsv[half][qt][v] = vis ? p * (dp[qt][v] - cr[qt]) : 0.0f;
           }
         }
