@@ -403,16 +403,20 @@ __global__ __launch_bounds__(256, 2) void attn_dkdv_kernel(AttArgs a) {
     for (int kb2 = 0; kb2 < NQT / 2; ++kb2) {
       float p[2][4], ds[2][4];
 #pragma unroll
-      for (int hq = 0; hq < 2; ++hq)
+      for (int hq = 0; hq < 2; ++hq) {
+        const int qt = 2 * kb2 + hq;
+        // lse and correction of this lane's 4 queries 16 qt + 4 g .. + 3: one read each
+        const f32x4 lq4 = *reinterpret_cast<const f32x4*>(ls + 16 * qt + 4 * g);
+        const f32x4 cq4 = *reinterpret_cast<const f32x4*>(ls + QT + 16 * qt + 4 * g);
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const int qt = 2 * kb2 + hq;
           const int ql = 16 * qt + 4 * g + v;
           const int64_t qi = (int64_t)j * QT + ql;
           const bool vis = att_visible<VM>(a, qi, kj);
-          p[hq][v] = vis ? ex2(s[qt][v] * sl2 - ls[ql]) : 0.0f;
-          ds[hq][v] = vis ? p[hq][v] * (dp[qt][v] - ls[QT + ql]) : 0.0f;
+          p[hq][v] = vis ? ex2(s[qt][v] * sl2 - lq4[v]) : 0.0f;
+          ds[hq][v] = vis ? p[hq][v] * (dp[qt][v] - cq4[v]) : 0.0f;
         }
+      }
       pb[kb2][0] = E::pack2_fast(p[0][0], p[0][1]); pb[kb2][1] = E::pack2_fast(p[0][2], p[0][3]);
       pb[kb2][2] = E::pack2_fast(p[1][0], p[1][1]); pb[kb2][3] = E::pack2_fast(p[1][2], p[1][3]);
       db[kb2][0] = E::pack2_fast(ds[0][0], ds[0][1]); db[kb2][1] = E::pack2_fast(ds[0][2], ds[0][3]);
