@@ -760,7 +760,7 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
       float o[4];
 #pragma unroll
       for (int v = 0; v < 4; ++v) o[v] = acc[ti][tj][v] + a.c * lor[tj][v] + bs[v];
-      const u32x2 pk = {E::pack2(o[0], o[1]), E::pack2(o[2], o[3])};
+      const u32x2 pk = {E::pack2_fast(o[0], o[1]), E::pack2_fast(o[2], o[3])};
       const int chunk = (nloc >> 3) ^ (mloc & 31);
       *reinterpret_cast<u32x2*>(srow(mloc) + chunk * 16 + (nloc & 7) * 2) = pk;
     }
