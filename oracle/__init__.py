@@ -263,11 +263,12 @@ def reference_fp16_forward(x, q, s, A, B, c, bias=None):
     A16 = bf16_to_f32(A).astype(f16)            # [K][r]
     B16 = bf16_to_f32(B).astype(f16)            # [r][N]
     Wd = (q.astype(f16) * np.asarray(s, np.float32).astype(f16)[:, None]).astype(f16)  # [N][K]
-    y = (x16.astype(np.float32) @ Wd.astype(np.float32).T).astype(f16)
-    if bias is not None:
-        y = (y.astype(np.float32) + bf16_to_f32(bias).astype(f16).astype(np.float32)).astype(f16)
-    h = (x16.astype(np.float32) @ A16.astype(np.float32)).astype(f16)
-    ad = (h.astype(np.float32) @ B16.astype(np.float32)).astype(f16)
+    with np.errstate(over="ignore"):  # binary16 overflow to Inf is part of the semantics
+        y = (x16.astype(np.float32) @ Wd.astype(np.float32).T).astype(f16)
+        if bias is not None:
+            y = (y.astype(np.float32) + bf16_to_f32(bias).astype(f16).astype(np.float32)).astype(f16)
+        h = (x16.astype(np.float32) @ A16.astype(np.float32)).astype(f16)
+        ad = (h.astype(np.float32) @ B16.astype(np.float32)).astype(f16)
     adapter = np.float32(c) * ad.astype(np.float32)
     return y.astype(np.float32) + adapter
 

@@ -305,7 +305,85 @@ def test_gelu_closed_forms_and_derivative():
     assert np.allclose(d, fd, rtol=2 ** -7, atol=2 ** -8)
 
 
-def test_reference_fp16_path_is_close_but_not_exact():
+# ---- the reference's own fp16 int8 forward (reported beside ours) --------------------------------
+# Each rounding point of oracle.reference_fp16_forward is pinned by an input whose exact result and
+# rounded result differ, with the expected values worked out by hand (binary16: 11-bit significand,
+# ties to even, largest finite 65504, values >= 65520 round to Inf).
+def _ref16(x, q, s, A, B, c, bias=None):
+    return oracle.reference_fp16_forward(bf(x), np.asarray(q, np.int8), np.asarray(s, F32),
+                                         bf(A), bf(B), c, None if bias is None else bf(bias))
+
+
+def test_reference_fp16_exact_small_integers_equal_brute_force():
+    # every product and sum is exact in binary16 (|y| < 32 on a 1/4 grid), so the restatement must
+    # equal the f64 brute force exactly; M, K, N, r all distinct so a transposed operand fails
+    rng = np.random.default_rng(3)
+    M, K, N, r, c = 5, 7, 3, 2, 0.5
+    x = rng.integers(-2, 3, (M, K)).astype(F32)
+    q = rng.integers(-7, 8, (N, K)).astype(np.int8)
+    s = np.array([0.25, 0.5, 0.125], F32)
+    A = rng.integers(-2, 3, (K, r)).astype(F32)
+    B = rng.integers(-2, 3, (r, N)).astype(F32)
+    want = np.zeros((M, N))
+    for m in range(M):
+        for n in range(N):
+            want[m, n] = sum(float(x[m, k]) * float(q[n, k]) * float(s[n]) for k in range(K))
+            h = [sum(float(x[m, k]) * float(A[k, j]) for k in range(K)) for j in range(r)]
+            want[m, n] += c * sum(h[j] * float(B[j, n]) for j in range(r))
+    got = _ref16(x, q, s, A, B, c)
+    assert got.shape == (M, N)
+    assert np.array_equal(got.astype(np.float64), want)
+
+
+def test_reference_fp16_weight_is_f16_of_q_times_f16_scale():
+    # s = 1/3: Float16(s) = 0.333251953125; Wd = Float16(q * Float16(s)). One-hot x picks out
+    # column k = 1 of Wd for token 0; token 1 picks column 0 (all zero codes).
+    q = np.zeros((5, 3), np.int8)
+    q[:, 1] = [1, 3, 5, 7, -127]
+    s = np.full(5, 1.0 / 3.0, F32)
+    x = np.array([[0, 1, 0], [1, 0, 0]], F32)
+    zA, zB = np.zeros((3, 1), F32), np.zeros((1, 5), F32)
+    got = _ref16(x, q, s, zA, zB, 1.0)
+    # 3 * 0.333251953125 = 1 - 2^-12, a tie between 1 - 2^-11 and 1 -> 1.0 (even);
+    # 5 -> 1706.25 * 2^-10 -> 1.666015625; 7 -> 1194.375 * 2^-9 -> 2.33203125;
+    # -127 -> -1354.34 * 2^-5 -> -42.3125 (rounding 5/3, 7/3, 127/3 directly gives 1.6669921875,
+    # 2.333984375, -42.34375)
+    assert got[0].tolist() == [0.333251953125, 1.0, 1.666015625, 2.33203125, -42.3125]
+    assert got[1].tolist() == [0.0] * 5
+
+
+def test_reference_fp16_output_rounds_ties_to_even_and_overflows():
+    # s = 1, q = 1: Wd = 1. y = x0 + x1 in f32, then rounded to binary16
+    q = np.ones((1, 2), np.int8)
+    s = np.ones(1, F32)
+    x = np.array([[2048, 1], [2048, 3], [2048, 2], [65280, 224], [65280, 240], [65280, 239]], F32)
+    zA, zB = np.zeros((2, 1), F32), np.zeros((1, 1), F32)
+    got = _ref16(x, q, s, zA, zB, 1.0)[:, 0]
+    # 2049 -> 2048 (tie, even), 2051 -> 2052 (tie, even), 2050 exact; 65504 is the largest
+    # finite binary16, 65520 rounds to Inf, 65519 rounds down to 65504
+    assert got.tolist() == [2048.0, 2052.0, 2050.0, 65504.0, np.inf, 65504.0]
+
+
+def test_reference_fp16_lora_roundings_bias_and_final_add():
+    z = np.zeros((1, 2), np.int8)
+    one = np.ones(1, F32)
+    # h = Float16(x A) = Float16(2049) = 2048; Float16(h B) = Float16(3 * 2048) = 6144 exactly;
+    # adapter = 0.25 * 6144. Without the rounding of h: Float16(6147) = 6148 -> 1537
+    got = _ref16([[2048, 1]], z, one, [[1], [1]], [[3]], 0.25)
+    assert got.tolist() == [[1536.0]]
+    # Float16(h B) with h = [2048, 1] exact, B = [1, 1]: 2049 -> 2048
+    got = _ref16([[1]], np.zeros((1, 1), np.int8), one, [[2048, 1]], [[1], [1]], 1.0)
+    assert got.tolist() == [[2048.0]]
+    # the bias is added in binary16 (mixed_add of two Float16 arrays): 2048 + 1 -> 2048;
+    # the scaled adapter is Float32 and its add is not rounded to binary16: 2048 + 1 = 2049
+    q1 = np.ones((1, 1), np.int8)
+    got = _ref16([[2048]], q1, one, [[0]], [[0]], 1.0, bias=[1])
+    assert got.tolist() == [[2048.0]]
+    got = _ref16([[2048]], q1, one, [[1]], [[1]], 1.0 / 2048)
+    assert got.tolist() == [[2049.0]]
+
+
+def test_reference_fp16_path_error_is_small_on_wan_like_inputs():
     x = oracle.normal_bf16(41, (64, 256), 1.0)
     w = oracle.normal_bf16(42, (128, 256), 0.02)
     q, s, _ = oracle.pack(w)
@@ -315,6 +393,30 @@ def test_reference_fp16_path_is_close_but_not_exact():
     y16 = oracle.reference_fp16_forward(x, q, s, A, B, 1.0)
     rel = np.abs(y16 - y).max() / np.abs(y).max()
     assert 1e-6 < rel < 1e-2
+
+
+# ---- the reference's CPU path restated for timing (oracle/cpu_path.py) --------------------------
+def test_cpu_path_matches_the_f64_oracle():
+    # The bench's CPU baseline must compute the reference's Float32 path: compare it with the f64
+    # oracle on the same float32 values (M, K, N, r all distinct so a transposed operand fails)
+    import torch
+    from oracle import cpu_path
+    M, K, N, r, c = 33, 40, 24, 4, 0.75
+    x = oracle.normal_f32(51, (M, K), 1.0)
+    w = oracle.normal_f32(52, (N, K), 0.02)
+    q, s, _ = oracle.pack(w, "f32")
+    A = oracle.normal_f32(53, (K, r), 0.1)
+    B = oracle.normal_f32(54, (r, N), 0.1)
+    dy = oracle.normal_f32(55, (M, N), 1.0)
+    t = torch.from_numpy
+    y = cpu_path.forward(t(x), t(q), t(s), t(A), t(B), c).numpy()
+    dx, dA, dB = (v.numpy() for v in cpu_path.backward(t(x), t(dy), t(q), t(s), t(A), t(B), c))
+    yo, _ = oracle.lora_forward(x, q, s, A, B, c, elt="f32")
+    go = oracle.lora_backward(dy, x, q, s, A, B, c, elt="f32")
+    for got, ref in ((y, yo), (dx, go["dx"]), (dA, go["dA"]), (dB, go["dB"])):
+        assert got.shape == ref.shape
+        assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max()
+    assert cpu_path.flops(M, K, N, r) == 4.0 * M * N * K + 6.0 * M * r * (K + N)
 
 
 # ---- the fp16 element path (the reference's Float16 compute) -----------------------------------
