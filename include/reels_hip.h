@@ -133,7 +133,9 @@ int reels_hip_i8lora_bwd(const void* dy, const void* x, const void* h, const int
                          void* workspace, size_t ws_bytes, void* stream);
 
 /* The same with binary16 dy, x, h, A, B and dx (dA, dB stay f32); roundings and W as in
- * reels_hip_i8lora_fwd_f16. */
+ * reels_hip_i8lora_fwd_f16. On every path dx multiplies the raw dy by the binary16 weight
+ * f16(q * f16(s)) with f32 sums (the reference's Float16 _weight_transpose_mul): dy * s is never
+ * rounded to binary16, whose normal range it can fall below. */
 int reels_hip_i8lora_bwd_f16(const void* dy, const void* x, const void* h, const int8_t* q,
                              const float* scales, const void* A, const void* B, int64_t M,
                              int64_t K, int64_t N, int64_t r, float lora_scale, void* dx, float* dA,

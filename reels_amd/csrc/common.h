@@ -126,6 +126,15 @@ template <> struct Elt<REELS_HIP_BF16> {
   // dequantized weight for bf16 compute: bf16(fl32(q s)) (_host_dequantize with T = BFloat16,
   // src/layers/quantization.jl:25-29)
   static __device__ __forceinline__ uint32_t deq(float q, float s) { return f32_to_bf16_bits(q * s); }
+  // w[i] * s[i] rounded to bf16 (s: 8 bf16 patterns); the int8 dX path scales the activations
+  // instead, so this exists for the generic template only
+  static __device__ __forceinline__ v8 scale8(v8 w, u32x4 s) {
+    const u32x4 wb = __builtin_bit_cast(u32x4, w);
+    u32x4 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = pack2(lo(wb[i]) * lo(s[i]), hi(wb[i]) * hi(s[i]));
+    return as8(o);
+  }
 };
 
 template <> struct Elt<REELS_HIP_F16> {
@@ -162,6 +171,9 @@ template <> struct Elt<REELS_HIP_F16> {
   static __device__ __forceinline__ uint32_t deq(float q, float s) {
     return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)((_Float16)q * (_Float16)s));
   }
+  // w[i] * s[i] in binary16 (one correctly rounded multiply each, v_pk_mul_f16): with w the exact
+  // codes and s = f16(scales) this is Float16(q) * Float16(s) of _dequantize_for_compute
+  static __device__ __forceinline__ v8 scale8(v8 w, u32x4 s) { return w * as8(s); }
 };
 
 // calls f(std::integral_constant<int, ELT>) for the run-time element code (bf16 or f16)

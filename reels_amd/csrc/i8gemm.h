@@ -8,6 +8,8 @@ struct GemmArgs {
   const uint16_t* act;     // [M][Kred] bf16
   const int8_t* q;         // [N][K] int8, row length ldq
   const float* colscale;   // per output column scale (FWD: s) or nullptr (= 1)
+  const float* redscale;   // DX only: per reduction index scale s[n] applied to the weight as
+                           // E::deq(q, s) (the f16 path), or nullptr: act is already scaled
   const uint16_t* L;       // [M][rp] bf16 or nullptr
   const uint16_t* R;       // [Ncols][rp] bf16 or nullptr
   const uint16_t* bias;    // [Ncols] bf16 or nullptr
@@ -17,8 +19,9 @@ struct GemmArgs {
   float c;                 // LoRA scale alpha / r
 };
 
-// mode 0 = FWD (out = s * act q^T + c L R^T + bias), 1 = DX (out = act q + c L R^T); elt is the
-// 16-bit element type of act, L, R, bias and out (REELS_HIP_BF16 or REELS_HIP_F16)
+// mode 0 = FWD (out = s * act q^T + c L R^T + bias), 1 = DX (out = act q + c L R^T, or
+// out = act deq(q, redscale) + c L R^T when redscale is set); elt is the 16-bit element type of
+// act, L, R, bias and out (REELS_HIP_BF16 or REELS_HIP_F16)
 int launch_i8gemm(int mode, int elt, const GemmArgs& a, hipStream_t st);
 
 // 16-bit GEMM with the LoRA epilogue: out = rnd(act wd^T + c L R^T + bias), wd [Ncols][Kred] (a

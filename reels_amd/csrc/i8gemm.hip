@@ -13,7 +13,11 @@
 //   call (transposed for DX, scale folded in), then a bf16 GEMM with the LoRA epilogue.
 // * i8gemm_v3_kernel (reduction a multiple of 64) and i8gemm_kernel (any reduction multiple of
 //   16): the int8 codes themselves are staged in LDS and converted exactly to bf16 in registers;
-//   the FWD scale s[n] is applied to the f32 sum, and DX takes act = bf16(dy * s).
+//   the FWD scale s[n] is applied to the f32 sum. DX in bf16 takes act = bf16(dy * s) (bf16 has
+//   f32's exponent range, so the pre-scaled operand cannot underflow); DX in f16 multiplies the
+//   raw dy by the reference's binary16 weight f16(q * f16(s[n])) (quantization.jl:61-62), built
+//   in registers from the int8 codes and the step's scales staged in LDS (i8gemm_kernel only),
+//   so dy * s never has to fit binary16's exponent range.
 //
 // i8gemm_kernel: block tile 256 output columns (n in FWD, k in DX) x 256 tokens, reduction step
 // 64, 256 threads = 4 waves in a 2 x 2 grid, each wave 128 x 128 = 4 x 4 tiles of
@@ -41,7 +45,8 @@ constexpr int BK = 64;   // reduction per step
 constexpr int NT = 256;
 constexpr int ACT_BYTES = BM * BK * 2;  // 32 KiB
 constexpr int W_BYTES = BN * BK;        // 16 KiB
-constexpr int STAGE_BYTES = ACT_BYTES + W_BYTES;
+constexpr int S_BYTES = BK * 2;          // DX with redscale: f16(s[n]) of the step's 64 n
+constexpr int STAGE_BYTES = ACT_BYTES + W_BYTES + S_BYTES;
 }  // namespace gemm
 
 
@@ -73,8 +78,14 @@ void i8gemm_kernel(GemmArgs a) {
 
   // ---- global -> register staging --------------------------------------------------------
   u32x4 ra[8], rw[4];
+  uint32_t rs = 0;  // DX with redscale: f16(s[n]) for n = r0 + t (threads 0..63)
+  const bool dxs = MODE == 1 && a.redscale != nullptr;
   auto load_tiles = [&](int kt) {
     const int64_t r0 = (int64_t)kt * BK;
+    if (dxs && t < BK) {
+      const int64_t n = r0 + t;
+      rs = n < Kred ? E::bits(a.redscale[n]) : 0u;  // f16(s): E::bits rounds to the element type
+    }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int row = (t >> 3) + 32 * i, c = t & 7;
@@ -110,6 +121,7 @@ void i8gemm_kernel(GemmArgs a) {
   auto store_tiles = [&](int buf) {
     uint8_t* sa = smem + buf * STAGE_BYTES;
     uint8_t* sw = sa + ACT_BYTES;
+    if (dxs && t < BK) reinterpret_cast<uint16_t*>(sw + W_BYTES)[t] = (uint16_t)rs;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int row = (t >> 3) + 32 * i, c = t & 7;
@@ -170,6 +182,14 @@ void i8gemm_kernel(GemmArgs a) {
           raw = u32x2{(uint32_t)v[0], (uint32_t)v[1]};
         }
         afr[ti] = E::from_i8x8(raw[0], raw[1]);
+        if (dxs) {
+          // the 8 bytes this lane received are rows n = kk*16 + (lane/32)*8 + (0..7) of the step
+          // (byte j from providing lane 2j + i/8, whose row is kk*16 + (g/2)*8 + j): multiply each
+          // exact code by its f16 scale, one binary16 rounding, as Float16(q) * Float16(s)
+          const int nrow = kk * 16 + (lane >> 5) * 8;
+          const u32x4 s8 = *reinterpret_cast<const u32x4*>(sw + W_BYTES + nrow * 2);
+          afr[ti] = E::scale8(afr[ti], s8);
+        }
       }
 #pragma unroll
       for (int ti = 0; ti < 4; ++ti)
@@ -863,8 +883,10 @@ int launch_i8gemm(int mode, int elt, const GemmArgs& a, hipStream_t st) {
   using namespace gemm;
   // the main kernel needs a reduction in whole 64-steps and 32-bit buffer offsets
   const int64_t act_bytes = a.M * a.Kred * 2, q_bytes = a.Ncols * a.Kred;
+  // the DX weight scale (f16 path) is applied only by the register-staged kernel
   const bool v3 = (a.Kred % gemm3::BK == 0) && act_bytes < ((int64_t)1 << 31) &&
-                  q_bytes < ((int64_t)1 << 31) && (a.ldq * gemm3::BK) < ((int64_t)1 << 31);
+                  q_bytes < ((int64_t)1 << 31) && (a.ldq * gemm3::BK) < ((int64_t)1 << 31) &&
+                  !(mode == 1 && a.redscale != nullptr);
   static std::once_flag once;
   static hipError_t attr_err = hipSuccess;
   std::call_once(once, [&] {

@@ -9,9 +9,11 @@
 //   2. i8gemm<DX>: dx = bf16(dys q + c * u A^T)                          (MFMA-bound)
 //   3. colgrad: dA = c x^T u, dB = c (dy^T h)^T as split-M partials, then a fixed-order sum
 //      (no float atomics: bitwise reproducible)                          (HBM-bound)
-// Any shape the fast kernels do not take (K, N or r not multiples of 16, r > 128, unaligned
-// pointers) runs through the generic kernels at the bottom, which compute the same formulas with
-// the same bf16 rounding points, one output element per thread.
+// Every rank takes the fast kernels: the LoRA panels h, u and the adapter operands live in the
+// workspace with rp = round_up(r, 16) columns (zeros past r), and the projection and gradient
+// kernels run in rank chunks of up to 128. Shapes the fast kernels do not take (K or N not
+// multiples of 16, unaligned pointers) run through the generic kernels at the bottom, which
+// compute the same formulas with the same bf16 rounding points, one output element per thread.
 #include "i8gemm.h"
 
 namespace reels {
@@ -37,8 +39,9 @@ __global__ void transpose_pad_kernel(const uint16_t* __restrict__ in, int64_t ro
 }
 
 // ---------------------------------------------------------------------------------------------
-// rowproj: out[m][j] = bf16(sum_k src[m][k] * P[j][k]) for j < r, 0 for r <= j < rp.
-// src [M][Kd] bf16 (x or dy), P [r][Kd] bf16 (At or B). When SCALED, also writes
+// rowproj: out[m][j] = bf16(sum_k src[m][k] * P[j][k]) for j < r, 0 for r <= j < rp (rp <= 128;
+// out rows of ld_out elements). src [M][Kd] bf16 (x or dy), P [r][Kd] bf16 (At or B). Ranks above
+// 128 run as launches over rank chunks of 128 (P and out advanced). When SCALED, also writes
 // scaled[m][k] = bf16(src[m][k] * s[k]) (the dy * s operand of the DX GEMM).
 // HBM-bound: a block of 256 threads owns ROWS rows (32 or 64) and streams them in chunks of 256
 // columns. Each wave-instruction loads two contiguous 512-byte row segments; the chunk goes to a
@@ -56,7 +59,7 @@ template <int RT, bool SCALED, int ROWS, int ELT>
 __global__ __launch_bounds__(256) void rowproj_kernel(const uint16_t* __restrict__ src, int64_t M,
                                                       int64_t Kd, const uint16_t* __restrict__ P,
                                                       int r, int rp_, uint16_t* __restrict__ out,
-                                                      const float* __restrict__ s,
+                                                      int ld_out, const float* __restrict__ s,
                                                       uint16_t* __restrict__ scaled) {
   using E = Elt<ELT>;
   typedef typename E::v8 V8;
@@ -194,13 +197,14 @@ __global__ __launch_bounds__(256) void rowproj_kernel(const uint16_t* __restrict
     const float sum = red[g][j0][v][ln];
     const int64_t mm = m0 + g * 32 + row;
     const int j = j0 * 32 + col;
-    if (mm < M && j < rp_) out[mm * rp_ + j] = j < r ? (uint16_t)E::bits(sum) : (uint16_t)0;
+    if (mm < M && j < rp_) out[mm * ld_out + j] = j < r ? (uint16_t)E::bits(sum) : (uint16_t)0;
   }
 }
 
 // ---------------------------------------------------------------------------------------------
 // colgrad partials: part[sp][o][j] = sum over this split's tokens of src[m][o] * Lm[m][j]
-// (o < Od output index, j < rp). D = src^T Lm on MFMA; both operands need 8 consecutive tokens
+// (o < Od output index, j < rp <= 128; Lm rows of ld_lm, part rows of ld_part elements; ranks
+// above 128 run as launches over rank chunks). D = src^T Lm on MFMA; both operands need 8 consecutive tokens
 // per lane, read transposed out of row-major LDS tiles with ds_read_b64_tr_b16 (lane i of a
 // 16-lane group receives element i%4 of the 4 elements addressed by lane 4j + i/4, j = 0..3).
 namespace cg {
@@ -213,8 +217,8 @@ constexpr int LROW = 128 + 16;    // Lm tile row (rp <= 128)
 template <int RT, int ELT>
 __global__ __launch_bounds__(256) void colgrad_kernel(const uint16_t* __restrict__ src, int64_t M,
                                                       int64_t Od, const uint16_t* __restrict__ Lm,
-                                                      int rp, int64_t tokens_per_split,
-                                                      float* __restrict__ part) {
+                                                      int ld_lm, int rp, int64_t tokens_per_split,
+                                                      float* __restrict__ part, int ld_part) {
   using E = Elt<ELT>;
   using namespace cg;
   __shared__ __attribute__((aligned(16))) uint16_t ssrc[TM * SROW];
@@ -248,7 +252,7 @@ __global__ __launch_bounds__(256) void colgrad_kernel(const uint16_t* __restrict
     const __amdgpu_buffer_rsrc_t rss = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(src + mc * Od), (short)0, (int)(nt * Od * 2), 0x00020000);
     const __amdgpu_buffer_rsrc_t rsl = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(Lm + mc * rp), (short)0, (int)(nt * rp * 2), 0x00020000);
+        const_cast<uint16_t*>(Lm + mc * ld_lm), (short)0, (int)(nt * ld_lm * 2), 0x00020000);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int id = tid + 256 * i, row = id >> 4, c = id & 15;
@@ -259,7 +263,7 @@ __global__ __launch_bounds__(256) void colgrad_kernel(const uint16_t* __restrict
 #pragma unroll
     for (int i = 0; i < RT; ++i) {
       const int id = tid + 256 * i, row = id / (RT * 4), c = id % (RT * 4);
-      const uint32_t off = c * 8 < rp ? (uint32_t)((row * rp + c * 8) * 2) : 0x80000000u;
+      const uint32_t off = c * 8 < rp ? (uint32_t)((row * ld_lm + c * 8) * 2) : 0x80000000u;
       rl[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsl, off, 0, 0));
     }
   };
@@ -331,7 +335,7 @@ __global__ __launch_bounds__(256) void colgrad_kernel(const uint16_t* __restrict
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int64_t o = o0 + wave * 32 + (v / 4) * 8 + lhi * 4 + (v % 4);
-      if (o < Od) part[((int64_t)sp * Od + o) * rp + j] = acc[t][v];
+      if (o < Od) part[((int64_t)sp * Od + o) * ld_part + j] = acc[t][v];
     }
   }
 }
@@ -374,6 +378,19 @@ __global__ __launch_bounds__(256) void reduce_partials_kernel(const float* __res
 __global__ void fill_f32_kernel(float* p, int64_t n, float v) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = v;
+}
+
+// dst[i][j] = j < cols ? src[i][j] : 0 for j < cols_dst (16-bit elements; rows of ld_src and
+// ld_dst): widens a [rows][r] LoRA operand to the padded [rows][rp] layout of the fast kernels,
+// or (cols = cols_dst = r) compacts a padded one back to [rows][r]
+__global__ void pad_cols_kernel(const uint16_t* __restrict__ src, int64_t rows, int cols,
+                                int64_t ld_src, uint16_t* __restrict__ dst, int cols_dst,
+                                int64_t ld_dst) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * cols_dst) return;
+  const int64_t row = i / cols_dst;
+  const int j = (int)(i % cols_dst);
+  dst[row * ld_dst + j] = j < cols ? src[row * ld_src + j] : (uint16_t)0;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -420,9 +437,17 @@ __global__ void g_dx_kernel(const uint16_t* __restrict__ dy, const int8_t* __res
   if (idx >= M * K) return;
   const int64_t m = idx / K, k = idx % K;
   float acc = 0.0f;
-  for (int64_t n = 0; n < N; ++n) {
-    const float dys = E::to_f32((uint16_t)E::bits(E::to_f32(dy[m * N + n]) * s[n]));
-    acc += dys * (float)q[n * K + k];
+  if (ELT == REELS_HIP_F16) {
+    // the reference's binary16 weight f16(q * f16(s)) times the raw dy (quantization.jl:61-62):
+    // dy * s itself may lie below binary16's normal range
+    for (int64_t n = 0; n < N; ++n)
+      acc += E::to_f32(dy[m * N + n]) * E::to_f32((uint16_t)E::deq((float)q[n * K + k], s[n]));
+  } else {
+    // bf16 keeps f32's exponent range: bf16(dy * s) times the exact code
+    for (int64_t n = 0; n < N; ++n) {
+      const float dys = E::to_f32((uint16_t)E::bits(E::to_f32(dy[m * N + n]) * s[n]));
+      acc += dys * (float)q[n * K + k];
+    }
   }
   float lo = 0.0f;
   for (int j = 0; j < r; ++j) lo += E::to_f32(u[m * ldu + j]) * E::to_f32(A[k * r + j]);
@@ -489,19 +514,24 @@ static Split split_for(int64_t M, int64_t Od) {
 struct Plan {
   bool fast;
   bool deq;     // fast and K, N multiples of 64: dequantized weight + bf16 GEMM
-  int rp;       // row stride of h/u buffers
+  int rp;       // row stride of the h/u panels and padded adapter operands: round_up(r, 16)
+  bool padded;  // rp != r: h, h_save and A go through padded copies in the workspace
   Split sa;     // dA: columns of x (K)
   Split sb;     // dB: columns of dy (N)
 };
 
+// rank chunk of the projection and gradient kernels (their LDS tiles hold 128 rank columns)
+constexpr int kRankChunk = 128;
+
 static Plan make_plan(int64_t M, int64_t K, int64_t N, int64_t r, bool ptrs_aligned) {
   Plan p;
-  // K, N < 2^22 keeps the projection and gradient kernels' buffer descriptors (64 rows, or the
-  // rank-128 operand, of one row length) below 2^31 bytes
-  p.fast = ptrs_aligned && (K % 16 == 0) && (N % 16 == 0) && (r % 16 == 0) && r <= 128 &&
+  // K, N < 2^22 keeps the projection and gradient kernels' buffer descriptors (64 rows, or a
+  // rank chunk of 128 rows, of one row length) below 2^31 bytes
+  p.fast = ptrs_aligned && (K % 16 == 0) && (N % 16 == 0) &&
            K < ((int64_t)1 << 22) && N < ((int64_t)1 << 22);
   p.deq = p.fast && bfgemm_supported(M, N, K) && bfgemm_supported(M, K, N);
-  p.rp = (int)r;
+  p.rp = (int)((r + 15) / 16 * 16);
+  p.padded = p.fast && p.rp != r;
   p.sa = split_for(M, K);
   p.sb = split_for(M, N);
   return p;
@@ -509,7 +539,7 @@ static Plan make_plan(int64_t M, int64_t K, int64_t N, int64_t r, bool ptrs_alig
 
 // workspace layout (byte offsets, 256-aligned); identical computation for sizing and use
 struct WsLayout {
-  size_t h, u, dys, wd, at, bt, pa, pb, total;
+  size_t h, u, dys, wd, at, bt, ap, pa, pb, total;
 };
 
 static WsLayout ws_layout(int64_t M, int64_t K, int64_t N, int64_t r, int which, const Plan& p) {
@@ -524,6 +554,7 @@ static WsLayout ws_layout(int64_t M, int64_t K, int64_t N, int64_t r, int which,
     w.bt = take(p.fast ? (size_t)N * rp * 2 : 0);
   } else {
     w.u = take((size_t)M * rp * 2);
+    w.ap = take(p.padded ? (size_t)K * rp * 2 : 0);  // A [K][rp], zeros past r
     w.dys = take(p.fast && !p.deq ? (size_t)M * N * 2 : 0);
     w.pa = take(p.fast && r > 0 ? (size_t)p.sa.splits * K * rp * 4 : 0);
     w.pb = take(p.fast && r > 0 ? (size_t)p.sb.splits * N * rp * 4 : 0);
@@ -536,51 +567,75 @@ static int grid1(int64_t n, int bs = 256) { return (int)ceil_div(n, bs); }
 
 template <bool SCALED, int ROWS>
 static void launch_rowproj_t(int elt, int rt, const uint16_t* src, int64_t M, int64_t Kd,
-                             const uint16_t* P, int r, int rp, uint16_t* out, const float* s,
-                             uint16_t* scaled, hipStream_t st) {
+                             const uint16_t* P, int r, int rp, uint16_t* out, int ld_out,
+                             const float* s, uint16_t* scaled, hipStream_t st) {
   const dim3 grid((unsigned)ceil_div(M, ROWS));
   TraceScope _ts(st, SCALED ? (rt <= 1 ? "rowproj_kernel<1,true>" : rt == 2 ? "rowproj_kernel<2,true>" : "rowproj_kernel<4,true>")
                             : (rt <= 1 ? "rowproj_kernel<1,false>" : rt == 2 ? "rowproj_kernel<2,false>" : "rowproj_kernel<4,false>"));
   with_elt(elt, [&](auto e) {
     constexpr int T = decltype(e)::value;
-    if (rt <= 1) rowproj_kernel<1, SCALED, ROWS, T><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, s, scaled);
-    else if (rt == 2) rowproj_kernel<2, SCALED, ROWS, T><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, s, scaled);
-    else rowproj_kernel<4, SCALED, ROWS, T><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, s, scaled);
+    if (rt <= 1) rowproj_kernel<1, SCALED, ROWS, T><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, ld_out, s, scaled);
+    else if (rt == 2) rowproj_kernel<2, SCALED, ROWS, T><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, ld_out, s, scaled);
+    else rowproj_kernel<4, SCALED, ROWS, T><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, ld_out, s, scaled);
   });
 }
 
+// out [M][rp] = bf16(src P^T) (zeros in columns r..rp), P [r][Kd]; one launch per rank chunk of
+// 128 (the scaled copy, when asked for, comes with the first)
 static int launch_rowproj(int elt, const uint16_t* src, int64_t M, int64_t Kd, const uint16_t* P,
                           int r, int rp, uint16_t* out, const float* s, uint16_t* scaled,
                           hipStream_t st) {
-  const int rt = (r + 31) / 32;
   const bool wide = ceil_div(M, 64) >= 256;  // enough tokens for a 64-row block on every CU
-  if (scaled) {
-    if (wide) launch_rowproj_t<true, 64>(elt, rt, src, M, Kd, P, r, rp, out, s, scaled, st);
-    else launch_rowproj_t<true, 32>(elt, rt, src, M, Kd, P, r, rp, out, s, scaled, st);
-  } else {
-    if (wide) launch_rowproj_t<false, 64>(elt, rt, src, M, Kd, P, r, rp, out, s, scaled, st);
-    else launch_rowproj_t<false, 32>(elt, rt, src, M, Kd, P, r, rp, out, s, scaled, st);
+  for (int c0 = 0; c0 < (rp > 0 ? rp : 1); c0 += kRankChunk) {
+    const int rpc = rp - c0 < kRankChunk ? rp - c0 : kRankChunk;     // columns of this chunk
+    const int rc = r - c0 < 0 ? 0 : (r - c0 < rpc ? r - c0 : rpc);  // of them, rows of P
+    const int rt = (rpc + 31) / 32;
+    const uint16_t* Pc = P + (int64_t)c0 * Kd;
+    uint16_t* oc = out ? out + c0 : nullptr;
+    uint16_t* sc = c0 == 0 ? scaled : nullptr;
+    if (sc) {
+      if (wide) launch_rowproj_t<true, 64>(elt, rt, src, M, Kd, Pc, rc, rpc, oc, rp, s, sc, st);
+      else launch_rowproj_t<true, 32>(elt, rt, src, M, Kd, Pc, rc, rpc, oc, rp, s, sc, st);
+    } else {
+      if (wide) launch_rowproj_t<false, 64>(elt, rt, src, M, Kd, Pc, rc, rpc, oc, rp, s, sc, st);
+      else launch_rowproj_t<false, 32>(elt, rt, src, M, Kd, Pc, rc, rpc, oc, rp, s, sc, st);
+    }
+    if (int rcode = check_launch("rowproj_kernel")) return rcode;
   }
-  return check_launch("rowproj_kernel");
+  return REELS_HIP_OK;
 }
 
+// Lm [M][rp]; partials part[sp][Od][rp], one launch per rank chunk of 128, then the fixed-order
+// reduction over the splits
 static int launch_colgrad(int elt, const uint16_t* src, int64_t M, int64_t Od, const uint16_t* Lm,
                           int r, int rp, const Split& p, float c, float* part, float* out,
                           bool trans, hipStream_t st) {
   const dim3 grid((unsigned)ceil_div(Od, cg::BO), (unsigned)p.splits);
-  const int rt = (rp + 31) / 32;
-  {
-    TraceScope _ts(st, rt <= 1 ? "colgrad_kernel<1>" : rt == 2 ? "colgrad_kernel<2>" : "colgrad_kernel<4>");
-    with_elt(elt, [&](auto e) {
-      constexpr int T = decltype(e)::value;
-      if (rt <= 1) colgrad_kernel<1, T><<<grid, 256, 0, st>>>(src, M, Od, Lm, rp, p.tps, part);
-      else if (rt == 2) colgrad_kernel<2, T><<<grid, 256, 0, st>>>(src, M, Od, Lm, rp, p.tps, part);
-      else colgrad_kernel<4, T><<<grid, 256, 0, st>>>(src, M, Od, Lm, rp, p.tps, part);
-    });
+  for (int c0 = 0; c0 < rp; c0 += kRankChunk) {
+    const int rpc = rp - c0 < kRankChunk ? rp - c0 : kRankChunk;
+    const int rt = (rpc + 31) / 32;
+    const uint16_t* Lc = Lm + c0;
+    float* pc = part + c0;
+    {
+      TraceScope _ts(st, rt <= 1 ? "colgrad_kernel<1>" : rt == 2 ? "colgrad_kernel<2>" : "colgrad_kernel<4>");
+      with_elt(elt, [&](auto e) {
+        constexpr int T = decltype(e)::value;
+        if (rt <= 1) colgrad_kernel<1, T><<<grid, 256, 0, st>>>(src, M, Od, Lc, rp, rpc, p.tps, pc, rp);
+        else if (rt == 2) colgrad_kernel<2, T><<<grid, 256, 0, st>>>(src, M, Od, Lc, rp, rpc, p.tps, pc, rp);
+        else colgrad_kernel<4, T><<<grid, 256, 0, st>>>(src, M, Od, Lc, rp, rpc, p.tps, pc, rp);
+      });
+    }
+    if (int rc = check_launch("colgrad_kernel")) return rc;
   }
-  int rc = check_launch("colgrad_kernel");
-  if (rc) return rc;
   return launch_reduce_partials(part, p.splits, Od, rp, r, c, out, trans, st);
+}
+
+// dst [rows][cols_dst] (row stride ld_dst) from src [rows][cols] (row stride ld_src), zeros past cols
+static int launch_pad_cols(const uint16_t* src, int64_t rows, int cols, int64_t ld_src,
+                           uint16_t* dst, int cols_dst, int64_t ld_dst, hipStream_t st) {
+  { TraceScope _ts(st, "pad_cols_kernel");
+    pad_cols_kernel<<<grid1(rows * cols_dst), 256, 0, st>>>(src, rows, cols, ld_src, dst, cols_dst, ld_dst); }
+  return check_launch("pad_cols_kernel");
 }
 
 int launch_reduce_partials(const float* part, int splits, int64_t Od, int rp, int r, float c,
@@ -631,7 +686,10 @@ static int i8lora_fwd_impl(int elt, const char* fn, const void* x, const int8_t*
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   const uint16_t* xb = static_cast<const uint16_t*>(x);
-  uint16_t* h = r > 0 ? (h_save ? static_cast<uint16_t*>(h_save) : reinterpret_cast<uint16_t*>(ws + w.h)) : nullptr;
+  // h [M][rp]: straight into h_save unless padded columns make the layouts differ
+  uint16_t* h = r > 0 ? ((h_save && !p.padded) ? static_cast<uint16_t*>(h_save)
+                                               : reinterpret_cast<uint16_t*>(ws + w.h))
+                      : nullptr;
   int rc;
   if (!p.fast) {
     if (r > 0) {
@@ -656,6 +714,9 @@ static int i8lora_fwd_impl(int elt, const char* fn, const void* x, const int8_t*
         static_cast<const uint16_t*>(B), r, N, p.rp, bt); }
     if ((rc = check_launch("transpose_pad_kernel"))) return rc;
     if ((rc = launch_rowproj(elt, xb, M, K, at, (int)r, p.rp, h, nullptr, nullptr, st))) return rc;
+    if (p.padded && h_save &&
+        (rc = launch_pad_cols(h, M, (int)r, p.rp, static_cast<uint16_t*>(h_save), (int)r, r, st)))
+      return rc;
   }
   GemmArgs g{};
   g.act = xb; g.q = q; g.colscale = scales; g.L = h; g.R = bt;
@@ -740,6 +801,19 @@ static int i8lora_bwd_impl(int elt, const char* fn, const void* dy, const void* 
   }
 
   uint16_t* dys = reinterpret_cast<uint16_t*>(ws + w.dys);
+  const bool f16 = elt == REELS_HIP_F16;
+  // the dX epilogue's A and the dB pass's h in the padded [.][rp] layout
+  const uint16_t* Ar = Ab;
+  if (p.padded && dx) {
+    uint16_t* ap = reinterpret_cast<uint16_t*>(ws + w.ap);
+    if ((rc = launch_pad_cols(Ab, K, (int)r, r, ap, p.rp, p.rp, st))) return rc;
+    Ar = ap;
+  }
+  if (p.padded && need_h && hh) {
+    uint16_t* hw = reinterpret_cast<uint16_t*>(ws + w.h);
+    if ((rc = launch_pad_cols(hh, M, (int)r, r, hw, p.rp, p.rp, st))) return rc;
+    hh = hw;
+  }
   if (p.deq) {
     // 1. u = dy B^T; 2. dx = dy wt^T + c u A^T with wt[k][n] = bf16(q[n][k] s[n])
     if (r > 0 && (dx || dA)) {
@@ -749,24 +823,27 @@ static int i8lora_bwd_impl(int elt, const char* fn, const void* dy, const void* 
       uint16_t* wt = reinterpret_cast<uint16_t*>(ws + w.wd);
       if ((rc = launch_dequant_transpose(elt, q, K, scales, N, K, wt, st))) return rc;
       GemmArgs g{};
-      g.act = dyb; g.q = nullptr; g.colscale = nullptr; g.L = r > 0 ? u : nullptr; g.R = Ab;
+      g.act = dyb; g.q = nullptr; g.colscale = nullptr; g.L = r > 0 ? u : nullptr; g.R = Ar;
       g.bias = nullptr; g.out = static_cast<uint16_t*>(dx);
       g.M = M; g.Ncols = K; g.Kred = N; g.ldq = N; g.rp = r > 0 ? p.rp : 0; g.c = lora_scale;
       if ((rc = launch_bfgemm(1, elt, g, wt, st))) return rc;
     }
-  } else if (r > 0 || dx) {
-    // 1. u = dy B^T and dys = dy * s in one pass over dy (the scaled copy only when dx is wanted)
+  } else if (r > 0 || (dx && !f16)) {
+    // 1. u = dy B^T and (bf16) dys = dy * s in one pass over dy (the scaled copy only when dx is
+    // wanted); f16 keeps dy as it is and scales the weight inside the dX GEMM instead
+    uint16_t* scaled = (dx && !f16) ? dys : nullptr;
     if (r > 0) {
-      if ((rc = launch_rowproj(elt, dyb, M, N, Bb, (int)r, p.rp, u, scales, dx ? dys : nullptr, st))) return rc;
+      if ((rc = launch_rowproj(elt, dyb, M, N, Bb, (int)r, p.rp, u, scales, scaled, st))) return rc;
     } else {
       // r = 0: only the scaled copy is needed (no projection output)
-      if ((rc = launch_rowproj(elt, dyb, M, N, Bb, 0, 0, nullptr, scales, dys, st))) return rc;
+      if ((rc = launch_rowproj(elt, dyb, M, N, Bb, 0, 0, nullptr, scales, scaled, st))) return rc;
     }
   }
-  // 2. dx = dys q + c u A^T
+  // 2. dx = dys q + c u A^T (bf16), dx = dy f16(q f16(s)) + c u A^T (f16)
   if (dx && !p.deq) {
     GemmArgs g{};
-    g.act = dys; g.q = q; g.colscale = nullptr; g.L = r > 0 ? u : nullptr; g.R = Ab; g.bias = nullptr;
+    g.act = f16 ? dyb : dys; g.q = q; g.colscale = nullptr; g.redscale = f16 ? scales : nullptr;
+    g.L = r > 0 ? u : nullptr; g.R = Ar; g.bias = nullptr;
     g.out = static_cast<uint16_t*>(dx);
     g.M = M; g.Ncols = K; g.Kred = N; g.ldq = K; g.rp = r > 0 ? p.rp : 0; g.c = lora_scale;
     if ((rc = launch_i8gemm(1, elt, g, st))) return rc;

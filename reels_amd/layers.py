@@ -109,6 +109,7 @@ def quantize_frozen_matrix(weight: torch.Tensor, T: Optional[torch.dtype] = None
     """quantize_frozen_matrix (quantization.jl:35-44) on the GPU, bit-exact.
 
     weight: [N][K] float32 / bfloat16 / float16 device tensor (rows = output channels).
+    T: the compute dtype tagged on the result, eltype(weight) by default as in the reference.
     Raises ValueError (the reference's InexactError from Int8(NaN)) on non-finite weights."""
     _need_device(weight, "weight")
     if weight.dim() != 2:
@@ -127,11 +128,50 @@ def quantize_frozen_matrix(weight: torch.Tensor, T: Optional[torch.dtype] = None
         _ptr(scales), _ptr(status), st))
     if int(status.item()) != 0:
         raise ValueError("InexactError: Int8(NaN) — weight contains non-finite values")
-    return QuantizedMatrix(values, scales, T or (weight.dtype if weight.dtype != torch.float32
-                                                 else torch.bfloat16))
+    return QuantizedMatrix(values, scales, T or weight.dtype)  # T = eltype(weight) by default
 
 
 # ---- raw entry points -------------------------------------------------------------------------
+# The C ABI sees only pointers, so every shape, dtype and device is checked here before a launch:
+# a mismatched tensor would otherwise be read out of bounds on the device.
+def _check_shape(t: Optional[torch.Tensor], shape, name: str) -> None:
+    if t is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+
+
+def _check_codes(weight: QuantizedMatrix) -> None:
+    q, s = weight.values, weight.scales
+    if q.dtype != torch.int8 or q.dim() != 2:
+        raise ValueError(f"weight values must be an int8 matrix, got {q.dtype} {tuple(q.shape)}")
+    if s.dtype != torch.float32 or tuple(s.shape) != (q.shape[0],) or s.device != q.device:
+        raise ValueError("weight scales must be a float32 vector of length N on the codes' device")
+
+
+def _validate(weight: QuantizedMatrix, M: int, K: int, N: int, A, B, **others) -> int:
+    """Shapes of a forward or backward call: codes [N][K], A [K][r], B [r][N] and every named
+    operand in ``others`` (name -> (tensor, shape)). Returns r."""
+    _check_codes(weight)
+    if (A is None) != (B is None):
+        raise ValueError("A and B must be given together")
+    r = 0 if A is None else int(A.shape[-1])
+    _check_shape(A, (K, r), "A ([K][r])")
+    _check_shape(B, (r, N), "B ([r][N])")
+    for name, (t, shape) in others.items():
+        _check_shape(t, shape, name)
+    return r
+
+
+def _on_activation_device(weight: QuantizedMatrix, device) -> QuantizedMatrix:
+    weight = _on_device(weight, device)
+    if weight.values.device != device:
+        raise ValueError(f"weight is on {weight.values.device}, the activations on {device}")
+    if not (weight.values.is_contiguous() and weight.scales.is_contiguous()):
+        weight = QuantizedMatrix(weight.values.contiguous(), weight.scales.contiguous(),
+                                 weight.compute_dtype)
+    return weight
+
+
+
 def workspace_bytes(M: int, K: int, N: int, r: int, which: int,
                     dtype: torch.dtype = torch.bfloat16) -> int:
     """Workspace of reels_hip_i8lora_fwd / _bwd (the 16-bit entry points share one size) or,
@@ -158,18 +198,18 @@ def i8lora_forward(x, weight: QuantizedMatrix, A=None, B=None, bias=None, lora_s
     x [M][K] bfloat16, float16 or float32 (reels_hip_i8lora_fwd / _fwd_f16 / _fwd_f32; float32
     rounds nothing); A [K][r], B [r][N] and bias [N] of the same dtype (Julia A::(r,K),
     B::(N,r)); y and h come back in that dtype."""
-    dt = _act_dtype(x, "x")
-    x = x.contiguous()
-    weight = _on_device(weight, x.device)
+    if x.dim() != 2:
+        raise ValueError(f"x must be a [M][K] matrix, got shape {tuple(x.shape)}")
     M, K = x.shape
     N, Kw = weight.values.shape
     if Kw != K:
         raise ValueError("DimensionMismatch: LoRA input and weight dimensions differ")
-    r = 0 if A is None else A.shape[1]
+    r = _validate(weight, M, K, N, A, B, bias=(bias, (N,)))
+    dt = _act_dtype(x, "x")
+    x = x.contiguous()
+    weight = _on_activation_device(weight, x.device)
     A = _contig(A, dt, "A")
     B = _contig(B, dt, "B")
-    if r and (tuple(A.shape) != (K, r) or tuple(B.shape) != (r, N)):
-        raise ValueError(f"A must be [K][r] = {(K, r)} and B [r][N] = {(r, N)}")
     bias = _contig(bias, dt, "bias")
     dev = x.device
     y = torch.empty((M, N), dtype=dt, device=dev)
@@ -188,14 +228,19 @@ def i8lora_backward(dy, x, weight: QuantizedMatrix, A=None, B=None, lora_scale=1
     """(dx [M][K], dA f32 [K][r], dB f32 [r][N]) of lora_backward (lora.jl:106-118). dy, x, h,
     A and B share one dtype, bfloat16, float16 or float32 (reels_hip_i8lora_bwd / _bwd_f16 /
     _bwd_f32); dx comes back in it."""
-    dt = _act_dtype(dy, "dy")
-    dy = dy.contiguous()
-    weight = _on_device(weight, dy.device)
+    if dy.dim() != 2:
+        raise ValueError(f"dy must be a [M][N] matrix, got shape {tuple(dy.shape)}")
     M, N = dy.shape
     Nw, K = weight.values.shape
     if Nw != N:
         raise ValueError("DimensionMismatch: dy and weight output dimensions differ")
-    r = 0 if A is None else A.shape[1]
+    r = _validate(weight, M, K, N, A, B, **{"x ([M][K])": (x, (M, K))})
+    _check_shape(h, (M, r), "h ([M][r])")
+    if r and x is None and (want_dA or (want_dB and h is None)):
+        raise ValueError("x is needed for dA and for recomputing h")
+    dt = _act_dtype(dy, "dy")
+    dy = dy.contiguous()
+    weight = _on_activation_device(weight, dy.device)
     A = _contig(A, dt, "A")
     B = _contig(B, dt, "B")
     x = _contig(x, dt, "x") if x is not None else None
@@ -363,18 +408,25 @@ class I8LoRALinearFunction(torch.autograd.Function):
         y, h = i8lora_forward(x, weight, A, B, bias, lora_scale, save_h=True)
         ctx.save_for_backward(x, A, B, values, scales, h)
         ctx.lora_scale = lora_scale
+        ctx.bias_dtype = None if bias is None else bias.dtype
         return y
 
     @staticmethod
     def backward(ctx, dy):
         x, A, B, values, scales, h = ctx.saved_tensors
         weight = QuantizedMatrix(values, scales)
-        dx, dA, dB = i8lora_backward(dy.contiguous(), x, weight, A, B, ctx.lora_scale, h=h,
+        dy = dy.contiguous()
+        dx, dA, dB = i8lora_backward(dy, x, weight, A, B, ctx.lora_scale, h=h,
                                      want_dx=ctx.needs_input_grad[0],
                                      want_dA=ctx.needs_input_grad[1],
                                      want_dB=ctx.needs_input_grad[2])
+        # a trainable bias (LoRALinear train_bias): the pullback of mixed_add (linear.jl:7-13)
+        # sums dy over the tokens; summed in f32
+        dbias = dy.float().sum(0).to(ctx.bias_dtype) if ctx.needs_input_grad[5] else None
+        # dA and dB keep the f32 of the kernels when the adapter parameters are f32 masters (the
+        # reference's AdamW keeps f32 state, optimizer.jl:9-24); otherwise the parameter dtype
         return (dx, None if dA is None else dA.to(A.dtype),
-                None if dB is None else dB.to(B.dtype), None, None, None, None)
+                None if dB is None else dB.to(B.dtype), None, None, dbias, None)
 
 
 def gelu_tanh(x: torch.Tensor) -> torch.Tensor:
@@ -436,10 +488,12 @@ def frozen_weight_transfer(device: str, precision: str, quantization: str = "non
 
 def move_weight(weight, transfer: FrozenWeightTransfer):
     """_move_weight (quantization.jl:111-144): quantize a frozen matrix on the device; an existing
-    QuantizedMatrix is kept as is (re-moving keeps identical codes)."""
+    QuantizedMatrix keeps its codes and scales and takes the transfer's compute type."""
     compute = {"fp16": torch.float16, "fp32": torch.float32}.get(transfer.precision, torch.bfloat16)
     if isinstance(weight, QuantizedMatrix):
         if transfer.quantization == "int8":
+            # the same codes, tagged with the transfer's compute type (lines 131-144)
+            weight = QuantizedMatrix(weight.values, weight.scales, compute)
             if transfer.cpu_offload and weight.values.is_cuda:
                 from .offload import offload_weight
                 return offload_weight(weight)

@@ -176,6 +176,70 @@ def test_cpu_tensors_are_rejected_not_computed():
         quantize_frozen_matrix(torch.zeros((4, 16)))
 
 
+def test_mismatched_operands_raise_before_any_launch():
+    """The C ABI sees only pointers: every shape, dtype and device mismatch must raise ValueError
+    in the Python wrappers (checked before the device checks, so CPU tensors reach them)."""
+    import torch
+    from reels_amd import QuantizedMatrix, i8lora_backward, i8lora_forward
+    bf = torch.bfloat16
+    M, K, N, r = 6, 8, 5, 2
+    W = QuantizedMatrix(torch.zeros((N, K), dtype=torch.int8), torch.ones(N))
+    x, dy = torch.zeros((M, K), dtype=bf), torch.zeros((M, N), dtype=bf)
+    A, B = torch.zeros((K, r), dtype=bf), torch.zeros((r, N), dtype=bf)
+    h = torch.zeros((M, r), dtype=bf)
+    bad_fwd = [
+        dict(x=torch.zeros((M, K + 1), dtype=bf)),                 # K mismatch
+        dict(x=torch.zeros((2, M, K), dtype=bf)),                  # not a matrix
+        dict(A=torch.zeros((K + 1, r), dtype=bf)),                 # A [K][r]
+        dict(A=torch.zeros((r, K), dtype=bf), B=torch.zeros((r, N), dtype=bf)),  # Julia order
+        dict(B=torch.zeros((r, N + 1), dtype=bf)),                 # B [r][N]
+        dict(B=torch.zeros((r + 1, N), dtype=bf)),                 # rank of B differs from A's
+        dict(B=None),                                              # A without B
+        dict(bias=torch.zeros((N + 1,), dtype=bf)),                # bias length
+        dict(weight=QuantizedMatrix(torch.zeros((N, K), dtype=torch.int8), torch.ones(N + 1))),
+        dict(weight=QuantizedMatrix(torch.zeros((N, K), dtype=torch.int8),
+                                    torch.ones(N, dtype=torch.float64))),
+        dict(weight=QuantizedMatrix(torch.zeros((N, K), dtype=torch.int16), torch.ones(N))),
+    ]
+    for case in bad_fwd:
+        a = dict(x=x, weight=W, A=A, B=B, bias=None)
+        a.update(case)
+        with pytest.raises(ValueError):
+            i8lora_forward(a["x"], a["weight"], a["A"], a["B"], a["bias"], 1.0)
+    bad_bwd = [
+        dict(dy=torch.zeros((M, N + 1), dtype=bf)),                # N mismatch
+        dict(x=torch.zeros((M + 1, K), dtype=bf)),                 # x tokens differ from dy's
+        dict(x=torch.zeros((M, K - 1), dtype=bf)),                 # x features
+        dict(h=torch.zeros((M, r + 1), dtype=bf)),                 # h [M][r]
+        dict(h=torch.zeros((M - 1, r), dtype=bf)),
+        dict(A=torch.zeros((K, r + 1), dtype=bf)),                 # A and B ranks differ
+        dict(x=None),                                              # dA needs x
+        dict(weight=QuantizedMatrix(torch.zeros((N, K), dtype=torch.int8), torch.ones(N - 1))),
+    ]
+    for case in bad_bwd:
+        a = dict(dy=dy, x=x, weight=W, A=A, B=B, h=h)
+        a.update(case)
+        with pytest.raises(ValueError):
+            i8lora_backward(a["dy"], a["x"], a["weight"], a["A"], a["B"], 1.0, h=a["h"])
+    # a well-formed call gets past the checks and stops at the device check
+    with pytest.raises(ValueError, match="ROCm device"):
+        i8lora_forward(x, W, A, B, None, 1.0)
+    with pytest.raises(ValueError, match="ROCm device"):
+        i8lora_backward(dy, x, W, A, B, 1.0, h=h)
+
+
+def test_move_weight_tags_the_transfer_precision():
+    """_move_weight(::QuantizedMatrix, transfer) keeps the codes and takes the transfer's compute
+    type (quantization.jl:131-144)."""
+    import torch
+    from reels_amd import QuantizedMatrix, frozen_weight_transfer, move_weight
+    W = QuantizedMatrix(torch.zeros((3, 4), dtype=torch.int8), torch.ones(3), torch.bfloat16)
+    for prec, dt in (("fp16", torch.float16), ("fp32", torch.float32), ("bf16", torch.bfloat16)):
+        moved = move_weight(W, frozen_weight_transfer("hip", prec, quantization="int8"))
+        assert moved.compute_dtype == dt
+        assert moved.values is W.values and moved.scales is W.scales
+
+
 def test_dequant_argument_errors():
     L = _lib.lib()
     fake = ctypes.c_void_p(4096)

@@ -163,3 +163,87 @@ def test_wan13b_chain_with_gelu(dev):
         assert_parity(dA.cpu().numpy(), go["dA"], f"chain {name} dA")
         assert_parity(dB.cpu().numpy(), go["dB"], f"chain {name} dB")
         gd = dx
+
+
+def test_wan13b_30_layer_chain_at_full_tokens(dev):
+    """Config 4 at its configured size: 30 Wan-2.1-1.3B layers, each q -> k -> v -> o -> ffn.0 ->
+    gelu_tanh -> ffn.2 (dim 1536, ffn 8960; src/models/wan21/transformer.jl:289-292,
+    src/layers/linear.jl:61-68), 32760 tokens, LoRA r = 32 on all 180 linears, one forward then
+    one backward (dX chained back through the GELU pullback, dA and dB for every linear).
+    Every linear is checked on the GPU's own inputs: sampled rows of y and of dx (including the
+    last token) against the oracle; dA and dB on sampled columns for all six linears of the first
+    layer (the end of the backward chain); the exact doubling identities y(2x) = 2 y(x) and
+    dx(2dy) = 2 dx(dy), dA(2dy) = 2 dA, dB(2dy) = 2 dB for the first layer's linears."""
+    import time
+
+    import torch
+    from reels_amd import (gelu_tanh, gelu_tanh_backward, i8lora_backward, i8lora_forward,
+                           quantize_frozen_matrix)
+    M, D, F, r, c, layers = 32760, 1536, 8960, 32, 1.0, 30
+    shapes = [("q", D, D), ("k", D, D), ("v", D, D), ("o", D, D), ("ffn0", D, F), ("ffn2", F, D)]
+    g = torch.Generator(device=dev).manual_seed(4321)
+    t0 = time.time()
+    params = []
+    for li in range(layers):
+        for (name, K, N) in shapes:
+            w = (torch.randn((N, K), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+            W = quantize_frozen_matrix(w, torch.bfloat16)
+            A = (torch.randn((K, r), generator=g, device=dev) * 0.01).to(torch.bfloat16)
+            B = (torch.randn((r, N), generator=g, device=dev) * 0.01).to(torch.bfloat16)
+            params.append((f"{li}.{name}", K, N, W, A, B))
+    x0 = torch.randn((M, D), generator=g, device=dev).to(torch.bfloat16)
+    gout = torch.randn((M, D), generator=g, device=dev).to(torch.bfloat16)
+    print(f"[configs] cfg4 chain: {layers} layers x 6 linears, M={M}", flush=True)
+
+    # forward, keeping each linear's input, h and (ffn.0) the pre-GELU output
+    inputs, hs, outs, pre = [], [], [], {}
+    cur = x0
+    for (name, K, N, W, A, B) in params:
+        inputs.append(cur)
+        y, h = i8lora_forward(cur, W, A, B, None, c, save_h=True)
+        hs.append(h)
+        outs.append(y)
+        if name.endswith("ffn0"):
+            pre[name] = y
+            y = gelu_tanh(y)
+        cur = y
+    # backward
+    dys, dxs, grads = [None] * len(params), [None] * len(params), [None] * len(params)
+    gd = gout
+    for i in reversed(range(len(params))):
+        name, K, N, W, A, B = params[i]
+        if name.endswith("ffn0"):
+            gd = gelu_tanh_backward(pre[name], gd)
+        dys[i] = gd
+        dx, dA, dB = i8lora_backward(gd, inputs[i], W, A, B, c, h=hs[i])
+        dxs[i], grads[i] = dx, (dA, dB)
+        gd = dx
+    torch.cuda.synchronize(dev)
+    print(f"[configs] cfg4 chain ran on the GPU ({time.time() - t0:.1f} s with set-up)", flush=True)
+    assert all(torch.isfinite(t).all() for t in (cur, gd))
+
+    rng = np.random.default_rng(44)
+    rows = np.concatenate([rng.choice(M - 1, 7, replace=False), [M - 1]])
+    rt = torch.from_numpy(rows).to(dev)
+    for i, (name, K, N, W, A, B) in enumerate(params):
+        q, s = W.values.cpu().numpy(), W.scales.cpu().numpy()
+        Ah, Bh = bf16_bits(A), bf16_bits(B)
+        xr, dyr = bf16_bits(inputs[i][rt]), bf16_bits(dys[i][rt])
+        yo, _ = oracle.lora_forward(xr, q, s, Ah, Bh, c)
+        assert_parity(bf16_f32(outs[i][rt]), yo, f"cfg4 {name} y (sampled rows)")
+        dxo = oracle.lora_backward(dyr, xr, q, s, Ah, Bh, c, want=("dx",))["dx"]
+        assert_parity(bf16_f32(dxs[i][rt]), dxo, f"cfg4 {name} dx (sampled rows)")
+        if i < len(shapes):  # the first layer: dA, dB over all tokens, and the doubling identities
+            kc = rng.choice(K, 24, replace=False)
+            nc = rng.choice(N, 24, replace=False)
+            go = oracle.lora_backward(bf16_bits(dys[i]), bf16_bits(inputs[i]), q, s, Ah, Bh, c,
+                                      rows=rows[:1], kcols=kc, ncols=nc, want=("dA", "dB"))
+            dA, dB = grads[i]
+            assert_parity(dA.cpu().numpy()[kc], go["dA"], f"cfg4 {name} dA (sampled k)")
+            assert_parity(dB.cpu().numpy()[:, nc], go["dB"], f"cfg4 {name} dB (sampled n)")
+            y2, _ = i8lora_forward(inputs[i] * 2, W, A, B, None, c)
+            dx2, dA2, dB2 = i8lora_backward(dys[i] * 2, inputs[i], W, A, B, c, h=hs[i])
+            torch.cuda.synchronize(dev)
+            assert torch.equal(y2, outs[i] * 2) and torch.equal(dx2, dxs[i] * 2)
+            assert torch.equal(dA2, dA * 2) and torch.equal(dB2, dB * 2)
+    print(f"[configs] cfg4 chain checked ({time.time() - t0:.1f} s)", flush=True)

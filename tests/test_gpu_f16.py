@@ -34,14 +34,14 @@ def f32(bits):
     return oracle.f16_to_f32(bits)
 
 
-def make_case(M, K, N, r, alpha, seed=0, bias=False, w_sigma=0.02, ab_sigma=0.01):
+def make_case(M, K, N, r, alpha, seed=0, bias=False, w_sigma=0.02, ab_sigma=0.01, dy_sigma=1.0):
     x = f16(seed + 1, (M, K), 1.0)
     w = f16(seed + 2, (N, K), w_sigma, outlier_rate=1e-3)
     q, s, st = oracle.pack(f32(w), "f32")
     assert st == 0
     A = f16(seed + 3, (K, r), ab_sigma) if r else None
     B = f16(seed + 4, (r, N), ab_sigma) if r else None
-    dy = f16(seed + 5, (M, N), 1.0)
+    dy = f16(seed + 5, (M, N), dy_sigma)
     b = f16(seed + 6, (N,), 0.1) if bias else None
     c = float(np.float32(alpha) / np.float32(r)) if r else 0.0
     return dict(x=x, q=q, s=s, A=A, B=B, dy=dy, bias=b, c=c, M=M, K=K, N=N, r=r)
@@ -179,3 +179,29 @@ def test_f16_gelu_tanh(dev, n):
         bad = np.flatnonzero(~((d <= 1) | close))
         assert bad.size == 0, (what, [(int(i), hex(got[i]), hex(want[i]), float(f32(xb)[i]),
                                        float(f32(dyb)[i])) for i in bad[:6]])
+
+
+@pytest.mark.parametrize("dy_sigma", [1e-3, 1e-4])
+@pytest.mark.parametrize("M,K,N,r", [
+    (96, 256, 320, 8),     # rank not a multiple of 16
+    (200, 512, 528, 32),   # N % 64 != 0: int8-weight dX GEMM over a reduction of 528
+    (200, 528, 512, 16),   # K % 64 != 0, N % 64 == 0: int8-weight dX GEMM over 512
+    (65, 48, 80, 16),      # K, N not multiples of 64
+    (40, 24, 20, 2),       # ragged: generic kernels
+])
+def test_small_output_gradients_keep_binary16_precision(dev, M, K, N, r, dy_sigma):
+    """Output gradients of 1e-3 and 1e-4 times per-channel scales of ~1e-4 give dy * s far below
+    binary16's normal range (6.1e-5). The reference multiplies dy by its binary16 weight
+    Float16(q) * Float16(s) (quantization.jl:61-62, 75-76) with f32 accumulation, so dx keeps
+    binary16's relative precision; so must every path here (the bar is the usual 1e-2)."""
+    cs = make_case(M, K, N, r, float(r), seed=M + K + N + r + int(1 / dy_sigma), dy_sigma=dy_sigma)
+    print(f"[f16] small dy sigma={dy_sigma:g}: M={M} K={K} N={N} r={r}", flush=True)
+    g = run_gpu(dev, cs)
+    ref = oracle.lora_backward(cs["dy"], cs["x"], cs["q"], cs["s"], cs["A"], cs["B"], cs["c"],
+                               elt="f16")
+    assert_parity(g["dx"], ref["dx"], f"small dy {dy_sigma:g} {M}x{K}x{N}r{r} dx")
+    assert_parity(g["dB"], ref["dB"], f"small dy {dy_sigma:g} {M}x{K}x{N}r{r} dB")
+    if dy_sigma >= 1e-3:
+        # at 1e-4, u = f16(dy B^T) (~4e-6) is itself a binary16 subnormal: the reference's f16
+        # B' * dy (lora.jl:113) rounds it the same way, the f64 oracle does not
+        assert_parity(g["dA"], ref["dA"], f"small dy {dy_sigma:g} {M}x{K}x{N}r{r} dA")

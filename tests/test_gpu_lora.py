@@ -106,6 +106,40 @@ def test_shapes(dev, M, K, N, r, bias):
                               bias=bias), f"shape{M}x{K}x{N}r{r}")
 
 
+@pytest.mark.parametrize("r", [1, 4, 8, 24, 160])
+def test_any_rank_on_a_wan_shape(dev, r):
+    """Any positive rank (the reference accepts any rank and per-layer rank_overrides,
+    src/config/schema.jl:117-123, lora.jl:13-28; its own tests use r = 3) takes the MFMA path:
+    the LoRA panels are zero-padded to a multiple of 16 in the workspace, ranks above 128 run in
+    chunks. 5120 x 5120 at 4096 tokens, alpha = r: sampled rows of y and dx, h in full, sampled
+    dA / dB columns against the oracle, with h saved by the forward and recomputed."""
+    import torch
+    from reels_amd import QuantizedMatrix, i8lora_backward, i8lora_forward
+    M, K, N = 4096, 5120, 5120
+    cs = make_case(M, K, N, r, float(r), seed=800 + r)
+    print(f"[lora] rank {r} on {M}x{K}x{N}", flush=True)
+    W = QuantizedMatrix(to_dev(cs["q"], dev, "raw"), to_dev(cs["s"], dev, "raw"))
+    x, dy = to_dev(cs["x"], dev), to_dev(cs["dy"], dev)
+    A, B = to_dev(cs["A"], dev), to_dev(cs["B"], dev)
+    y, h = i8lora_forward(x, W, A, B, None, cs["c"], save_h=True)
+    dx, dA, dB = i8lora_backward(dy, x, W, A, B, cs["c"], h=h)
+    dx_r, dA_r, dB_r = i8lora_backward(dy, x, W, A, B, cs["c"], h=None)  # h recomputed
+    torch.cuda.synchronize(dev)
+    assert h.shape == (M, r)
+    assert torch.equal(dx, dx_r) and torch.equal(dA, dA_r) and torch.equal(dB, dB_r)
+    rng = np.random.default_rng(r)
+    rows = np.concatenate([rng.choice(M - 8, 24, replace=False), np.arange(M - 8, M)])
+    kc, nc = rng.choice(K, 32, replace=False), rng.choice(N, 32, replace=False)
+    yo, ho = oracle.lora_forward(cs["x"], cs["q"], cs["s"], cs["A"], cs["B"], cs["c"], rows=rows)
+    go = oracle.lora_backward(cs["dy"], cs["x"], cs["q"], cs["s"], cs["A"], cs["B"], cs["c"],
+                              rows=rows, kcols=kc, ncols=nc)
+    assert_parity(bf16_f32(y)[rows], yo, f"rank {r} y")
+    assert_parity(bf16_f32(h)[rows], ho, f"rank {r} h")
+    assert_parity(bf16_f32(dx)[rows], go["dx"], f"rank {r} dx")
+    assert_parity(dA.cpu().numpy()[kc], go["dA"], f"rank {r} dA")
+    assert_parity(dB.cpu().numpy()[:, nc], go["dB"], f"rank {r} dB")
+
+
 def test_recompute_h_equals_saved_h(dev):
     cs = make_case(200, 512, 256, 32, 32.0, seed=7)
     a = run_gpu(dev, cs, h_for_bwd=True)
@@ -122,16 +156,18 @@ def test_backward_bitwise_reproducible(dev):
         assert np.array_equal(a[k], b[k]), k
 
 
-def test_wan14b_qproj_full_size(dev):
-    """Wan-2.1-14B q projection at 32760 tokens (K = N = 5120, r = 32, alpha 32): sampled rows
-    (including the partial last tile) and sampled dA/dB columns against the oracle; exact
-    doubling y(2x) = 2 y(x), dx(2dy) = 2 dx(dy), dA(2dy) = 2 dA, dB(2dy) = 2 dB over the whole
-    output (power-of-two scaling is exact in every f32 sum and bf16 rounding)."""
+@pytest.mark.parametrize("K,N", [(5120, 5120), (5120, 13824), (13824, 5120)])
+def test_wan14b_projection_full_size(dev, K, N):
+    """The Wan-2.1-14B block projections at 32760 tokens (q/k/v/o 5120 -> 5120, ffn.0 5120 ->
+    13824, ffn.2 13824 -> 5120; r = 32, alpha 32): sampled rows (including the partial last tile)
+    and sampled dA/dB columns against the oracle; exact doubling y(2x) = 2 y(x),
+    dx(2dy) = 2 dx(dy), dA(2dy) = 2 dA, dB(2dy) = 2 dB over the whole output (power-of-two
+    scaling is exact in every f32 sum and bf16 rounding)."""
     import torch
     from reels_amd import QuantizedMatrix, i8lora_backward, i8lora_forward
-    M, K, N, r = 32760, 5120, 5120, 32
-    cs = make_case(M, K, N, r, 32.0, seed=500)
-    print("[lora] wan14b q-proj full size", flush=True)
+    M, r = 32760, 32
+    cs = make_case(M, K, N, r, 32.0, seed=500 + K + 2 * N)
+    print(f"[lora] wan14b projection {K}->{N} at {M} tokens", flush=True)
     W = QuantizedMatrix(to_dev(cs["q"], dev, "raw"), to_dev(cs["s"], dev, "raw"))
     x, dy = to_dev(cs["x"], dev), to_dev(cs["dy"], dev)
     A, B = to_dev(cs["A"], dev), to_dev(cs["B"], dev)
@@ -150,10 +186,10 @@ def test_wan14b_qproj_full_size(dev):
     yr, _ = oracle.lora_forward(cs["x"], cs["q"], cs["s"], cs["A"], cs["B"], cs["c"], rows=rows)
     ref = oracle.lora_backward(cs["dy"], cs["x"], cs["q"], cs["s"], cs["A"], cs["B"], cs["c"],
                                rows=rows, kcols=kcols, ncols=ncols)
-    assert_parity(bf16_f32(y)[rows], yr, "wan14b y (sampled rows)")
-    assert_parity(bf16_f32(dx)[rows], ref["dx"], "wan14b dx (sampled rows)")
-    assert_parity(dA.cpu().numpy()[kcols], ref["dA"], "wan14b dA (sampled k)")
-    assert_parity(dB.cpu().numpy()[:, ncols], ref["dB"], "wan14b dB (sampled n)")
+    assert_parity(bf16_f32(y)[rows], yr, f"wan14b {K}->{N} y (sampled rows)")
+    assert_parity(bf16_f32(dx)[rows], ref["dx"], f"wan14b {K}->{N} dx (sampled rows)")
+    assert_parity(dA.cpu().numpy()[kcols], ref["dA"], f"wan14b {K}->{N} dA (sampled k)")
+    assert_parity(dB.cpu().numpy()[:, ncols], ref["dB"], f"wan14b {K}->{N} dB (sampled n)")
 
 
 def test_mirror_api_and_autograd(dev):
@@ -184,6 +220,31 @@ def test_mirror_api_and_autograd(dev):
     assert torch.equal(xa.grad, g["dx"].reshape(-1, 256))
     assert torch.equal(A.grad, g["A"].to(torch.bfloat16))
     assert torch.equal(B.grad, g["B"].to(torch.bfloat16))
+
+
+def test_autograd_trainable_bias_gets_its_gradient(dev):
+    """A trainable bias (LoRALinear train_bias) gets the pullback of mixed_add: dy summed over
+    the tokens (linear.jl:7-13), checked against the f64 column sum; x, A and B get the same
+    gradients as the explicit backward."""
+    import torch
+    from reels_amd import I8LoRALinearFunction, QuantizedMatrix, i8lora_backward
+    M, K, N, r = 300, 256, 384, 16
+    cs = make_case(M, K, N, r, 16.0, seed=640, bias=True)
+    W = QuantizedMatrix(to_dev(cs["q"], dev, "raw"), to_dev(cs["s"], dev, "raw"))
+    x = to_dev(cs["x"], dev).requires_grad_(True)
+    A = to_dev(cs["A"], dev).requires_grad_(True)
+    B = to_dev(cs["B"], dev).requires_grad_(True)
+    bias = to_dev(cs["bias"], dev).requires_grad_(True)
+    dy = to_dev(cs["dy"], dev)
+    y = I8LoRALinearFunction.apply(x, A, B, W.values, W.scales, bias, cs["c"])
+    y.backward(dy)
+    torch.cuda.synchronize(dev)
+    want = oracle.bf16_to_f32(cs["dy"]).astype(np.float64).sum(0)
+    assert bias.grad is not None and bias.grad.dtype == torch.bfloat16
+    assert_parity(bf16_f32(bias.grad), want, "autograd dbias")
+    dx, dA, dB = i8lora_backward(dy, x.detach(), W, A.detach(), B.detach(), cs["c"])
+    assert torch.equal(x.grad, dx)
+    assert torch.equal(A.grad, dA.to(torch.bfloat16)) and torch.equal(B.grad, dB.to(torch.bfloat16))
 
 
 @pytest.mark.parametrize("n", [1, 1000, 8960 * 64 + 3])

@@ -32,8 +32,10 @@ def test_move_weight_offload_keeps_pinned_codes(dev):
     ref = quantize_frozen_matrix(w)
     assert torch.equal(W.values, ref.values.cpu())
     assert torch.equal(W.scales.view(torch.int32), ref.scales.cpu().view(torch.int32))
-    # re-moving an offloaded weight keeps it as it is; moving a resident one offloads it
-    assert move_weight(W, t) is W
+    # re-moving an offloaded weight keeps its pinned codes and scales; moving a resident one
+    # offloads it
+    again = move_weight(W, t)
+    assert again.values is W.values and again.scales is W.scales
     assert not move_weight(ref, t).values.is_cuda
 
 
@@ -90,6 +92,20 @@ def test_streamed_block_fwd_bwd_is_bit_identical(dev, slots):
     for a, b in zip(ref_b, out_b):
         for t1, t2 in zip(a, b):
             assert _same(t1, t2)
+    # one streamed projection (the 512 -> 1536 one) against the oracle: the offloaded codes and
+    # scales multiply exactly as the reference's per-call upload would (quantization.jl:46-59)
+    from tests._util import assert_parity, bf16_bits, bf16_f32
+    i = 2
+    q, s = Hs[i].values.numpy(), Hs[i].scales.numpy()
+    xb, Ab, Bb, dyb = (bf16_bits(t_) for t_ in (xs[i], As[i], Bs[i], dys[i]))
+    yo, ho = oracle.lora_forward(xb, q, s, Ab, Bb, 1.0)
+    go = oracle.lora_backward(dyb, xb, q, s, Ab, Bb, 1.0)
+    dx, dA, dB = out_b[order.index(i)]
+    assert_parity(bf16_f32(out_f[i][0]), yo, "offloaded projection y")
+    assert_parity(bf16_f32(out_f[i][1]), ho, "offloaded projection h")
+    assert_parity(bf16_f32(dx), go["dx"], "offloaded projection dx")
+    assert_parity(dA.cpu().numpy(), go["dA"], "offloaded projection dA")
+    assert_parity(dB.cpu().numpy(), go["dB"], "offloaded projection dB")
     # the weights still held when the backward starts are not uploaded again
     assert st.uploads == 2 * len(Hs) - slots
 
