@@ -116,6 +116,25 @@ int reels_hip_i8lora_fwd_f16(const void* x, const int8_t* q, const float* scales
                              size_t ws_bytes, void* stream);
 
 /*
+ * reels_hip_i8lora_fwd without a workspace argument: it allocates nothing (no hipMalloc, hipFree
+ * or allocating library call), for callers that cannot allocate - code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc. No counterpart in the reference (its
+ * forward allocates per call). Same arguments, results and errors as reels_hip_i8lora_fwd except:
+ *   - the scratch (the h panel and transposed adapter operands) is a 32 MiB device array inside
+ *     the library, one per GPU, held until the process ends; sizes that need more return
+ *     REELS_HIP_EINVAL before any work (M * round_up(r, 16) * 2 + r * K * 2 + N * round_up(r,
+ *     16) * 2 bytes, rounded up to 256 each, must fit);
+ *   - it always multiplies the int8 codes (s applied to the f32 sum), never a dequantized bf16
+ *     copy, so its y can differ from reels_hip_i8lora_fwd's in the last bf16 bit where that entry
+ *     point takes the dequantized-weight path (K and N multiples of 64);
+ *   - calls that overlap on one GPU (other streams or threads) race on the shared scratch.
+ */
+int reels_hip_i8lora_fwd_noalloc(const void* x, const int8_t* q, const float* scales,
+                                 const void* A, const void* B, const void* bias, int64_t M,
+                                 int64_t K, int64_t N, int64_t r, float lora_scale, void* y,
+                                 void* h_save, void* stream);
+
+/*
  * lora_backward(layer, x, dy), src/layers/lora.jl:106-118, with the frozen-weight pullback of
  * src/training/ad_rules.jl:70-80 (_weight_transpose_mul, quantization.jl:75-76):
  *   u  = bf16(dy * B^T)                                                      [M][r]

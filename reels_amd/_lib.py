@@ -25,6 +25,7 @@ EXPORTS = (
     "reels_hip_i8_dequant",
     "reels_hip_i8lora_workspace_bytes",
     "reels_hip_i8lora_fwd",
+    "reels_hip_i8lora_fwd_noalloc",
     "reels_hip_i8lora_fwd_f16",
     "reels_hip_i8lora_bwd",
     "reels_hip_i8lora_bwd_f16",
@@ -97,6 +98,9 @@ def lib():
         g.restype = ctypes.c_int
         gb.argtypes = [vp, vp, vp, i64, vp]
         gb.restype = ctypes.c_int
+    L.reels_hip_i8lora_fwd_noalloc.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64,
+                                               ctypes.c_float, vp, vp, vp]
+    L.reels_hip_i8lora_fwd_noalloc.restype = ctypes.c_int
     ci = ctypes.c_int
     L.reels_hip_attention_workspace_bytes.argtypes = [i64, i64, i64]
     L.reels_hip_attention_workspace_bytes.restype = sz

@@ -16,6 +16,8 @@
 // compute the same formulas with the same bf16 rounding points, one output element per thread.
 #include "i8gemm.h"
 
+#include <mutex>
+
 namespace reels {
 
 
@@ -664,10 +666,43 @@ static bool all_aligned(std::initializer_list<const void*> ps) {
   return true;
 }
 
+// ---- allocation-free forward ----------------------------------------------------------------
+// Scratch of reels_hip_i8lora_fwd_noalloc: one array per GPU, held until the process ends. Host
+// code never uses the array's name as an address (on the host it is a stand-in symbol); the
+// device address comes from hipGetSymbolAddress, once per device, on that device's first call.
+constexpr size_t kScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices] = {};
+
+static int scratch_for_current_device(const char* fn, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return fail(REELS_HIP_EHIP, std::string(fn) + ": hipGetDevice: " + hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(REELS_HIP_EHIP, std::string(fn) + ": device index out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(REELS_HIP_EHIP, std::string(fn) + ": hipGetSymbolAddress(scratch): " +
+                                      hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return REELS_HIP_OK;
+}
+
+// noalloc: never the dequantized-weight plan (its N*K*2-byte copy is what would not fit a modest
+// scratch), the workspace is the device's scratch array
 static int i8lora_fwd_impl(int elt, const char* fn, const void* x, const int8_t* q,
                            const float* scales, const void* A, const void* B, const void* bias,
                            int64_t M, int64_t K, int64_t N, int64_t r, float lora_scale, void* y,
-                           void* h_save, void* workspace, size_t ws_bytes, void* stream) {
+                           void* h_save, void* workspace, size_t ws_bytes, void* stream,
+                           bool noalloc = false) {
   clear_error();
   if (M < 0 || K <= 0 || N <= 0 || r < 0 || r > 4096)
     return fail(REELS_HIP_EINVAL, std::string(fn) + ": " "need M >= 0, K > 0, N > 0, 0 <= r <= 4096");
@@ -679,7 +714,18 @@ static int i8lora_fwd_impl(int elt, const char* fn, const void* x, const int8_t*
   const bool al = all_aligned({x, q, scales, A, B, y, h_save}) &&
                   (bias == nullptr || (reinterpret_cast<uintptr_t>(bias) & 7u) == 0);
   Plan p = make_plan(M, K, N, r, al);
+  if (noalloc) p.deq = false;
   WsLayout w = ws_layout(M, K, N, r, REELS_HIP_WS_FWD, p);
+  if (noalloc) {
+    if (w.total > kScratchBytes)
+      return fail(REELS_HIP_EINVAL,
+                  std::string(fn) + ": these sizes need " + std::to_string(w.total) +
+                      " bytes of scratch, more than the " + std::to_string(kScratchBytes) +
+                      " this entry point holds (use reels_hip_i8lora_fwd with a workspace)");
+    int rc0 = scratch_for_current_device(fn, &workspace);
+    if (rc0) return rc0;
+    ws_bytes = kScratchBytes;
+  }
   if (workspace == nullptr || ws_bytes < w.total)
     return fail(REELS_HIP_EWORKSPACE, std::string(fn) + ": " "workspace NULL or smaller than "
                                       "reels_hip_i8lora_workspace_bytes(..., REELS_HIP_WS_FWD)");
@@ -900,6 +946,14 @@ extern "C" int reels_hip_i8lora_fwd(const void* x, const int8_t* q, const float*
                                     void* h_save, void* workspace, size_t ws_bytes, void* stream) {
   return i8lora_fwd_impl(REELS_HIP_BF16, "reels_hip_i8lora_fwd", x, q, scales, A, B, bias, M, K, N,
                          r, lora_scale, y, h_save, workspace, ws_bytes, stream);
+}
+
+extern "C" int reels_hip_i8lora_fwd_noalloc(const void* x, const int8_t* q, const float* scales,
+                                            const void* A, const void* B, const void* bias,
+                                            int64_t M, int64_t K, int64_t N, int64_t r,
+                                            float lora_scale, void* y, void* h_save, void* stream) {
+  return i8lora_fwd_impl(REELS_HIP_BF16, "reels_hip_i8lora_fwd_noalloc", x, q, scales, A, B, bias,
+                         M, K, N, r, lora_scale, y, h_save, nullptr, 0, stream, true);
 }
 
 extern "C" int reels_hip_i8lora_fwd_f16(const void* x, const int8_t* q, const float* scales,
