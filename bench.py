@@ -71,6 +71,8 @@ def parse():
                     help="activation / LoRA element type: bf16 (the default workload) or f16 "
                          "(the reference's own int8 compute precision, the _f16 entry points)")
     ap.add_argument("--no-pack", action="store_true", help="skip the pack workload")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the config 1 / 2 / 4 / 5a lines")
     ap.add_argument("--no-attention", action="store_true", help="skip the attention workload")
     ap.add_argument("--attention-only", action="store_true",
                     help="run only the attention workload")
@@ -159,6 +161,15 @@ def pack_bench(dev, reps=3):
     kern_ms = sum(ms_ for (_, ms_) in recs) / reps
     gbs = nbytes / (kern_ms * 1e-3) / 1e9
     assert int(status.item()) == 0
+    # sampled rows of each timed launch (input and the GPU's codes and scales) for the bit-exact
+    # comparison in the CPU-baseline leg
+    rng = torch.Generator().manual_seed(5)
+    samples = []
+    for (w, q, sc, rows, K) in mats:
+        idx = torch.cat([torch.randint(0, rows, (62,), generator=rng), torch.tensor([0, rows - 1])])
+        ix = idx.to(dev)
+        samples.append((w[ix].view(torch.int16).cpu().numpy(), q[ix].cpu().numpy(),
+                        sc[ix].cpu().numpy(), rows, K))
     del mats
     torch.cuda.empty_cache()
     copy = copy_gbs(dev)
@@ -171,7 +182,7 @@ def pack_bench(dev, reps=3):
                         "device_copy": {"what": "torch copy_ of a 4 GiB buffer (read + write bytes), "
                                                 "same run", "gbs": round(copy, 1),
                                         "achieved_over_copy": round(gbs / copy, 4)}}}
-    return out
+    return out, samples
 
 
 # Wan-2.1-14B self-attention of one block: 32760 tokens (the projection workload's token
@@ -263,29 +274,32 @@ def attention_bench(dev, reps=3):
 
 def attention_cpu_baseline(seconds=5.0):
     """The reference's CPU attention (memory_efficient_attention with its backward,
-    attention.jl:106-221) restated in the oracle (scalar f64), timed on a bounded sample: one head
-    of the Wan-14B shape, all 32760 keys, as many queries as fit the time."""
-    import numpy as np
-    import oracle
+    attention.jl:106-221: f32 128 x 128 score tiles on BLAS, online softmax) restated in
+    oracle/cpu_path.py on torch's CPU BLAS with every thread this process has, timed on a bounded
+    sample: one head of the Wan-14B shape, all 32760 keys, as many queries as fit the time."""
+    import torch
+    from oracle import cpu_path
     B, S, H, D = ATT_SHAPE
-    rng = np.random.default_rng(3)
-    k = oracle.f32_to_bf16(rng.standard_normal((1, S, 1, D)).astype(np.float32))
-    v = oracle.f32_to_bf16(rng.standard_normal((1, S, 1, D)).astype(np.float32))
-    nq = 8
+    threads = torch.get_num_threads()
+    g = torch.Generator().manual_seed(3)
+    k = torch.randn((S, D), generator=g)
+    v = torch.randn((S, D), generator=g)
+    nq = 128
     while True:
-        q = oracle.f32_to_bf16(rng.standard_normal((1, nq, 1, D)).astype(np.float32))
-        dy = oracle.f32_to_bf16(rng.standard_normal((1, nq, 1, D)).astype(np.float32))
+        q = torch.randn((nq, D), generator=g)
+        dy = torch.randn((nq, D), generator=g)
         t0 = time.perf_counter()
-        oracle.attention_forward(q, k, v)
-        oracle.attention_backward(q, k, v, dy)
+        out, lse = cpu_path.attention_forward(q, k, v)
+        cpu_path.attention_backward(q, k, v, dy, out, lse)
         dt = time.perf_counter() - t0
-        if dt > seconds / 4 or nq >= 4096:
+        if dt > seconds / 3 or nq >= 8192:
             break
         nq *= 2
     ff, fb = attention_flops(1, nq, S, 1, D)
-    return {"value": round((ff + fb) / dt / 1e12, 5), "unit": "TFLOP/s", "cores": 1, "kind": "port",
-            "sample": f"one head, {nq} queries x {S} keys x {D}, forward + backward, oracle (scalar "
-                      f"f64 C), {dt:.2f} s"}
+    return {"value": round((ff + fb) / dt / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port", "host": host_info(),
+            "sample": f"one head, {nq} queries x {S} keys x {D}, forward + backward, the reference's "
+                      f"f32 128x128-tiled algorithm on torch CPU BLAS ({threads} threads), {dt:.2f} s"}
 
 
 def copy_gbs(dev, nbytes=4 << 30, reps=5):
@@ -308,13 +322,32 @@ def copy_gbs(dev, nbytes=4 << 30, reps=5):
     return 2.0 * nbytes / (ms * 1e-3) / 1e9
 
 
-def pack_cpu_baseline(seconds=5.0):
+def host_info():
+    """The host CPU the baselines run on: model, logical CPUs, CPUs this process may use."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "")
+    except OSError:
+        pass
+    return {"cpu_model": model, "nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)),
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
+
+
+def pack_cpu_baseline(samples, seconds=5.0):
     """The reference packs on the host CPU (quantize_frozen_matrix, quantization.jl:35-44 on
-    Float32.(Array(W))); the oracle's C restatement (OpenMP) is timed on a sample of 14B rows."""
+    Float32.(Array(W))); the oracle's C restatement (OpenMP) is timed on a sample of 14B rows.
+    The same leg compares the sampled rows of every timed GPU launch with the oracle bit for bit."""
     import numpy as np
     import oracle
-    import os
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    checked = 0
+    for (wb, qg, sg, rows, K) in samples:
+        qo, so, st = oracle.pack(wb.view(np.uint16), "bf16")
+        if st != 0 or not np.array_equal(qo, qg) or not np.array_equal(so.view(np.uint32),
+                                                                         sg.view(np.uint32)):
+            raise SystemExit(f"pack: sampled rows of the {rows}x{K} launch differ from the oracle")
+        checked += len(qg)
     rows = 2048
     w = oracle.normal_bf16(5, (rows, 5120), 0.02, outlier_rate=1e-3)
     t0 = time.perf_counter(); oracle.pack(w, "bf16"); t1 = time.perf_counter()
@@ -325,12 +358,14 @@ def pack_cpu_baseline(seconds=5.0):
     t1 = time.perf_counter()
     nbytes = 3 * rows * 5120 + 4 * rows
     return {"value": round(nbytes * reps / (t1 - t0) / 1e9, 2), "unit": "GB/s", "cores": threads,
-            "kind": "port", "sample": f"{rows}x5120 bf16 rows x {reps} repetitions, C oracle "
-                                      f"(OpenMP, {threads} threads), {t1 - t0:.2f} s"}
+            "kind": "port", "host": host_info(),
+            "sample": f"{rows}x5120 bf16 rows x {reps} repetitions, C oracle "
+                      f"(OpenMP, {threads} threads), {t1 - t0:.2f} s",
+            "gpu_rows_checked_bit_exact": checked}
 
 
 class Projection:
-    def __init__(self, name, K, N, M, r, dev, gen, act=None):
+    def __init__(self, name, K, N, M, r, dev, gen, act=None, alpha=ALPHA):
         import torch
         from reels_amd import quantize_frozen_matrix, workspace_bytes, _lib
         self.name, self.K, self.N, self.M, self.r = name, K, N, M, r
@@ -351,7 +386,7 @@ class Projection:
         self.wsb_n = workspace_bytes(M, K, N, r, _lib.WS_BWD, bf)
         self.wsf = torch.empty((self.wsf_n,), dtype=torch.uint8, device=dev)
         self.wsb = torch.empty((self.wsb_n,), dtype=torch.uint8, device=dev)
-        c = float(torch.tensor(ALPHA, dtype=torch.float32) / torch.tensor(float(r)))
+        c = float(torch.tensor(alpha, dtype=torch.float32) / torch.tensor(float(r)))
         p = lambda t: ctypes.c_void_p(t.data_ptr())
         st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
         self.fwd_args = (p(self.x), p(self.W.values), p(self.W.scales), p(self.A), p(self.B), None,
@@ -388,6 +423,165 @@ def run_step(L, projs, check, sfx="", streamer=None):
     run_streamed([pr.Wh for pr in rev], b, streamer)
 
 
+PROJECTIONS_13B = [("self_attn.q", 1536, 1536), ("self_attn.k", 1536, 1536),
+                   ("self_attn.v", 1536, 1536), ("self_attn.o", 1536, 1536),
+                   ("ffn.0", 1536, 8960), ("ffn.2", 8960, 1536)]
+
+
+def _time_ms(fn, reps, warmup=2):
+    """Mean ms of fn over reps calls between two events on torch's current stream (the stream the
+    library launches on), after warmup untimed calls."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+class Chain:
+    """Config 4: a stack of Wan-2.1-1.3B layers, each q -> k -> v -> o -> ffn.0 -> gelu_tanh ->
+    ffn.2 (dim 1536, ffn 8960; src/models/wan21/transformer.jl:289-292), LoRA r = 32 (alpha 32)
+    on every linear. One step = the forward through every layer (each linear's input kept, as
+    the backward needs it) and the backward in reverse: dX chained back through the GELU
+    pullback, dA and dB for every linear. Every buffer is allocated up front."""
+
+    def __init__(self, dev, gen, layers=30, M=TOKENS, r=RANK, D=1536, F=8960):
+        import torch
+        from reels_amd import _lib, quantize_frozen_matrix, workspace_bytes
+        bf = torch.bfloat16
+        self.M, self.r, self.layers = M, r, layers
+        p = lambda t: ctypes.c_void_p(t.data_ptr())
+        self.st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        shapes = [(D, D)] * 4 + [(D, F), (F, D)]
+        c = float(torch.tensor(ALPHA, dtype=torch.float32) / torch.tensor(float(r)))
+        wsf = max(workspace_bytes(M, K, N, r, _lib.WS_FWD) for (K, N) in shapes)
+        wsb = max(workspace_bytes(M, K, N, r, _lib.WS_BWD) for (K, N) in shapes)
+        self.wsf = torch.empty((wsf,), dtype=torch.uint8, device=dev)
+        self.wsb = torch.empty((wsb,), dtype=torch.uint8, device=dev)
+        self.x0 = torch.randn((M, D), generator=gen, device=dev).to(bf)
+        self.gout = torch.randn((M, D), generator=gen, device=dev).to(bf)
+        # two gradient buffers per width, used alternately down the chain
+        pool = {D: [torch.empty((M, D), dtype=bf, device=dev) for _ in range(2)],
+                F: [torch.empty((M, F), dtype=bf, device=dev) for _ in range(2)]}
+        self.keep = [pool]
+        self.links = []
+        cur = self.x0
+        for li in range(layers):
+            for j, (K, N) in enumerate(shapes):
+                w = (torch.randn((N, K), generator=gen, device=dev) * 0.02).to(bf)
+                W = quantize_frozen_matrix(w, bf)
+                del w
+                A = (torch.randn((K, r), generator=gen, device=dev) * 0.01).to(bf)
+                B = (torch.randn((r, N), generator=gen, device=dev) * 0.01).to(bf)
+                y = torch.empty((M, N), dtype=bf, device=dev)
+                h = torch.empty((M, r), dtype=bf, device=dev)
+                gl = torch.empty((M, N), dtype=bf, device=dev) if j == 4 else None
+                dA = torch.empty((K, r), dtype=torch.float32, device=dev)
+                dB = torch.empty((r, N), dtype=torch.float32, device=dev)
+                self.keep.append((W, A, B, y, h, gl, dA, dB))
+                self.links.append(dict(
+                    K=K, N=N, gelu=j == 4, x=cur, y=y, gl=gl,
+                    fwd=(p(cur), p(W.values), p(W.scales), p(A), p(B), None, M, K, N, r, c, p(y),
+                         p(h), p(self.wsf), wsf, self.st),
+                    bwd=lambda dy, dx, x=cur, W=W, A=A, B=B, h=h, dA=dA, dB=dB, K=K, N=N: (
+                        p(dy), p(x), p(h), p(W.values), p(W.scales), p(A), p(B), M, K, N, r, c,
+                        p(dx), p(dA), p(dB), p(self.wsb), wsb, self.st)))
+                cur = gl if j == 4 else y
+        # the backward's buffer sequence, fixed once: dy of each link and its dx buffer
+        self.plan = []
+        gd = self.gout
+        for lk in reversed(self.links):
+            pre = None
+            if lk["gelu"]:  # the pullback of gelu_tanh before ffn.0's backward
+                g2 = next(t for t in pool[lk["N"]] if t is not gd)
+                pre = (p(lk["y"]), p(gd), p(g2), M * lk["N"])
+                gd = g2
+            dx = next(t for t in pool[lk["K"]] if t is not gd)
+            self.plan.append((lk, pre, lk["bwd"](gd, dx)))
+            gd = dx
+        self.flops = layers * sum(linear_flops(M, K, N, r) for (K, N) in shapes)
+
+    def step(self, L, check):
+        for lk in self.links:
+            check("reels_hip_i8lora_fwd", L.reels_hip_i8lora_fwd(*lk["fwd"]))
+            if lk["gelu"]:
+                check("reels_hip_gelu_tanh", L.reels_hip_gelu_tanh(
+                    ctypes.c_void_p(lk["y"].data_ptr()), ctypes.c_void_p(lk["gl"].data_ptr()),
+                    self.M * lk["N"], self.st))
+        for (lk, pre, args) in self.plan:
+            if pre is not None:
+                check("reels_hip_gelu_tanh_bwd", L.reels_hip_gelu_tanh_bwd(*pre, self.st))
+            check("reels_hip_i8lora_bwd", L.reels_hip_i8lora_bwd(*args))
+
+
+def configs_bench(dev, L, check):
+    """The other BASELINE workloads on this GPU, each as TFLOP/s of forward + dX + dA + dB
+    (4MNK + 6Mr(K+N) per linear): config 1 (one 1536 x 1536 linear, 1024 tokens, r 16, alpha 16),
+    config 2 (the six Wan-2.1-1.3B block projections at 32760 tokens), config 4 (the 30-layer
+    1.3B chain with GELU), and config 5a (cross-attention K/V 5120 -> 5120 at 77 / 333 / 512 text
+    tokens, forward and backward timed separately, as HBM GB/s of their algorithmic bytes)."""
+    import torch
+    out = {}
+    gen = torch.Generator(device=dev).manual_seed(99)
+    pr = Projection("cfg1", 1536, 1536, 1024, 16, dev, gen, alpha=16.0)
+    ms = _time_ms(lambda: run_step(L, [pr], check), reps=200, warmup=5)
+    f = linear_flops(1024, 1536, 1536, 16)
+    out["cfg1"] = {"what": "one int8 LoRA linear 1536 -> 1536, 1024 tokens, r 16, alpha 16, "
+                           "fwd + dX + dA + dB", "ms": round(ms, 4),
+                   "tflops": round(f / (ms * 1e-3) / 1e12, 1)}
+    del pr
+    projs = [Projection(n, K, N, TOKENS, RANK, dev, gen) for (n, K, N) in PROJECTIONS_13B]
+    ms = _time_ms(lambda: run_step(L, projs, check), reps=10)
+    f = sum(linear_flops(TOKENS, K, N, RANK) for (_, K, N) in PROJECTIONS_13B)
+    out["cfg2"] = {"what": "wan2.1-1.3b block projections q/k/v/o 1536 -> 1536, ffn 1536 -> 8960 "
+                           "-> 1536 at 32760 tokens, r 32, fwd + dX + dA + dB", "ms": round(ms, 3),
+                   "tflops": round(f / (ms * 1e-3) / 1e12, 1),
+                   "frac_of_bf16_peak": round(f / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+    del projs
+    torch.cuda.empty_cache()
+    ch = Chain(dev, gen)
+    ms = _time_ms(lambda: ch.step(L, check), reps=3, warmup=1)
+    out["cfg4"] = {"what": "30 wan2.1-1.3b layers (q -> k -> v -> o -> ffn.0 -> gelu_tanh -> "
+                           "ffn.2) at 32760 tokens, r 32: one forward then one backward through "
+                           "the chain (dX chained, dA and dB per linear)", "ms": round(ms, 2),
+                   "tflops": round(ch.flops / (ms * 1e-3) / 1e12, 1),
+                   "frac_of_bf16_peak": round(ch.flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                   "flops": ch.flops}
+    del ch
+    torch.cuda.empty_cache()
+    sk = {}
+    for M in (77, 333, 512):
+        K = N = 5120
+        pr = Projection("cross_kv", K, N, M, RANK, dev, gen)
+        fms = _time_ms(lambda: check("reels_hip_i8lora_fwd", L.reels_hip_i8lora_fwd(*pr.fwd_args)),
+                       reps=100, warmup=5)
+        bms = _time_ms(lambda: check("reels_hip_i8lora_bwd", L.reels_hip_i8lora_bwd(*pr.bwd_args)),
+                       reps=100, warmup=5)
+        fb = 2 * M * K + N * K + 4 * N + 2 * M * N + 2 * M * RANK
+        bb = 2 * M * N + N * K + 4 * N + 4 * M * K + 2 * M * RANK
+        ff = 2.0 * M * N * K + 2.0 * M * RANK * (K + N)
+        bf_ = 2.0 * M * N * K + 4.0 * M * RANK * (K + N)
+        sk[str(M)] = {"fwd_us": round(fms * 1e3, 2), "bwd_us": round(bms * 1e3, 2),
+                      "fwd_gbs": round(fb / (fms * 1e-3) / 1e9, 1),
+                      "bwd_gbs": round(bb / (bms * 1e-3) / 1e9, 1),
+                      "fwd_frac_of_hbm": round(fb / (fms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                      "fwd_tflops": round(ff / (fms * 1e-3) / 1e12, 1),
+                      "bwd_tflops": round(bf_ / (bms * 1e-3) / 1e12, 1),
+                      "fwd_bytes": fb, "bwd_bytes": bb}
+        del pr
+    out["cfg5a"] = {"what": "cross-attention K/V projection 5120 -> 5120, r 32, at 77 / 333 / 512 "
+                            "text tokens; bytes = 2MK + NK + 4N + 2MN + 2Mr (fwd), 2MN + NK + 4N "
+                            "+ 4MK + 2Mr (bwd); peak 8 TB/s", "tokens": sk}
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(seconds):
     """The reference's CPU path (fp32: dequantize-materialise + BLAS sgemm + rank-r GEMMs, see
     oracle/cpu_path.py) on a bounded sample of the same six projections at fewer tokens."""
@@ -402,7 +596,7 @@ def cpu_baseline(seconds):
     m = max(128, min(m, TOKENS))
     t, f = cpu_path.time_block(shapes, m, RANK, seed=1)
     return {"value": round(f / t / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
-            "kind": "port",
+            "kind": "port", "host": host_info(),
             "sample": (f"Wan-14B block projections (q,k,v,o 5120->5120, ffn 5120->13824->5120), "
                        f"r=32, fwd+dX+dA+dB at {m} tokens (of {TOKENS}), fp32 materialised "
                        f"dequant + torch CPU BLAS, {threads} threads, {t:.2f} s")}
@@ -432,7 +626,7 @@ def main():
         return
     L = _lib.lib()
     if args.pack_only:
-        print(json.dumps({"pack": pack_bench(dev)}))
+        print(json.dumps({"pack": pack_bench(dev)[0]}))
         return
     if args.attention_only:
         att = attention_bench(dev)
@@ -536,18 +730,18 @@ def main():
     cpu = None
     if args.cpu_seconds > 0:
         cpu = cpu_baseline(args.cpu_seconds)
+    del projs
+    torch.cuda.empty_cache()
+    configs = None
+    if not args.no_configs and args.dtype == "bf16" and args.offload == "none":
+        configs = configs_bench(dev, L, _lib.check)
     pack = None
     if not args.no_pack:
-        del projs
-        torch.cuda.empty_cache()
-        pack = pack_bench(dev)
+        pack, samples = pack_bench(dev)
         if args.cpu_seconds > 0:
-            pack["cpu_baseline"] = pack_cpu_baseline(min(5.0, args.cpu_seconds))
+            pack["cpu_baseline"] = pack_cpu_baseline(samples, min(5.0, args.cpu_seconds))
     att = None
     if not args.no_attention and args.dtype == "bf16" and args.offload == "none":
-        if args.no_pack:
-            del projs
-            torch.cuda.empty_cache()
         att = attention_bench(dev)
         if args.cpu_seconds > 0:
             att["cpu_baseline"] = attention_cpu_baseline(min(5.0, args.cpu_seconds))
@@ -569,6 +763,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": kernels,
+        "configs": configs,
         "pack": pack,
         "attention": att,
         "device": torch.cuda.get_device_name(dev),

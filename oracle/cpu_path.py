@@ -70,3 +70,51 @@ def time_block(projections, M: int, r: int, seed: int = 0):
     for (K, N) in projections:
         total += flops(M, K, N, r)
     return t1 - t0, total
+
+
+def attention_forward(q, k, v, query_block: int = 128, key_block: int = 128):
+    """memory_efficient_attention on the CPU (attention.jl:106-172) for one head without a mask:
+    f32 tiles of query_block x key_block scores on BLAS, an online softmax per query block.
+    q [Sq][D], k and v [Sk][D] float32. Returns (out [Sq][D], lse [Sq])."""
+    Sq, D = q.shape
+    scale = 1.0 / float(torch.tensor(float(D), dtype=torch.float32).sqrt())
+    out = torch.empty_like(q)
+    lse = torch.empty((Sq,), dtype=torch.float32)
+    for q0 in range(0, Sq, query_block):
+        qb = q[q0:q0 + query_block]
+        mx = torch.full((qb.shape[0],), float("-inf"))
+        norm = torch.zeros((qb.shape[0],))
+        acc = torch.zeros((qb.shape[0], D))
+        for k0 in range(0, k.shape[0], key_block):
+            s = (qb @ k[k0:k0 + key_block].t()) * scale
+            nm = torch.maximum(mx, s.max(dim=1).values)
+            prev = torch.exp(mx - nm)
+            p = torch.exp(s - nm[:, None])
+            norm = prev * norm + p.sum(dim=1)
+            acc = acc * prev[:, None] + p @ v[k0:k0 + key_block]
+            mx = nm
+        out[q0:q0 + query_block] = acc / norm[:, None]
+        lse[q0:q0 + query_block] = mx + torch.log(norm)
+    return out, lse
+
+
+def attention_backward(q, k, v, dy, out, lse, query_block: int = 128, key_block: int = 128):
+    """memory_efficient_attention_backward on the CPU (attention.jl:174-221), one head, no mask:
+    score tiles recomputed from q, k and the cached lse. Returns (dq, dk, dv)."""
+    Sq, D = q.shape
+    scale = 1.0 / float(torch.tensor(float(D), dtype=torch.float32).sqrt())
+    dq, dk, dv = torch.zeros_like(q), torch.zeros_like(k), torch.zeros_like(v)
+    for q0 in range(0, Sq, query_block):
+        qb, dyb = q[q0:q0 + query_block], dy[q0:q0 + query_block]
+        corr = (dyb * out[q0:q0 + query_block]).sum(dim=1)
+        lb = lse[q0:q0 + query_block]
+        g = torch.zeros_like(qb)
+        for k0 in range(0, k.shape[0], key_block):
+            kb, vb = k[k0:k0 + key_block], v[k0:k0 + key_block]
+            p = torch.exp((qb @ kb.t()) * scale - lb[:, None])
+            ds = p * (dyb @ vb.t() - corr[:, None])
+            g += (ds @ kb) * scale
+            dk[k0:k0 + key_block] += (ds.t() @ qb) * scale
+            dv[k0:k0 + key_block] += p.t() @ dyb
+        dq[q0:q0 + query_block] = g
+    return dq, dk, dv

@@ -653,3 +653,24 @@ def test_attention_backward_matches_finite_differences(causal):
             args_lo = {"q": (lo, k, v), "k": (q, lo, v), "v": (q, k, lo)}[name]
             fd = (objective(*args_hi) - objective(*args_lo)) / step
             assert abs(fd - grad[idx]) <= 1e-4 + 1e-4 * abs(fd), (name, idx, fd, grad[idx])
+
+
+def test_cpu_path_attention_matches_the_f64_oracle():
+    # the attention CPU baseline (the reference's f32 tiled attention, attention.jl:106-221)
+    # against the f64 oracle; tiles smaller than the sizes so several blocks and a ragged last
+    # block are exercised
+    import torch
+    from oracle import cpu_path
+    Sq, Sk, D = 70, 90, 32
+    rng = np.random.default_rng(9)
+    q, k, v, dy = (rng.standard_normal(s).astype(F32) for s in ((Sq, D), (Sk, D), (Sk, D), (Sq, D)))
+    t = torch.from_numpy
+    out, lse = cpu_path.attention_forward(t(q), t(k), t(v), query_block=32, key_block=40)
+    dq, dk, dv = cpu_path.attention_backward(t(q), t(k), t(v), t(dy), out, lse, 32, 40)
+    r4 = lambda a: a.reshape(1, a.shape[0], 1, D)
+    oo, lo = oracle.attention_forward(r4(q), r4(k), r4(v), elt="f32")
+    go = oracle.attention_backward(r4(q), r4(k), r4(v), r4(dy), elt="f32")
+    assert np.abs(out.numpy() - oo[0, :, 0]).max() <= 1e-5 * np.abs(oo).max()
+    assert np.abs(lse.numpy() - lo[0, 0]).max() <= 1e-5
+    for got, ref in zip((dq, dk, dv), go):
+        assert np.abs(got.numpy() - ref[0, :, 0]).max() <= 1e-4 * np.abs(ref).max()
