@@ -516,10 +516,12 @@ static Split split_for(int64_t M, int64_t Od) {
 struct Plan {
   bool fast;
   bool deq;     // fast and K, N multiples of 64: dequantized weight + bf16 GEMM
+  bool skinny;  // few tokens: the int8 codes streamed into registers (skinny.hip), both directions
   int rp;       // row stride of the h/u panels and padded adapter operands: round_up(r, 16)
   bool padded;  // rp != r: h, h_save and A go through padded copies in the workspace
   Split sa;     // dA: columns of x (K)
   Split sb;     // dB: columns of dy (N)
+  SkinnyPlan skf, skb;  // the few-token forward (reduction K) and dX (reduction N)
 };
 
 // rank chunk of the projection and gradient kernels (their LDS tiles hold 128 rank columns)
@@ -534,6 +536,11 @@ static Plan make_plan(int64_t M, int64_t K, int64_t N, int64_t r, bool ptrs_alig
   p.deq = p.fast && bfgemm_supported(M, N, K) && bfgemm_supported(M, K, N);
   p.rp = (int)((r + 15) / 16 * 16);
   p.padded = p.fast && p.rp != r;
+  p.skinny = p.fast && skinny_supported(M, K, N, p.rp);
+  if (p.skinny) {
+    p.skf = skinny_plan(M, K, N, r > 0 ? p.rp : 0);
+    p.skb = skinny_plan(M, N, K, r > 0 ? p.rp : 0);
+  }
   p.sa = split_for(M, K);
   p.sb = split_for(M, N);
   return p;
@@ -549,6 +556,27 @@ static WsLayout ws_layout(int64_t M, int64_t K, int64_t N, int64_t r, int which,
   size_t off = 0;
   auto take = [&](size_t bytes) { size_t o = off; off = align_up(off + bytes, 256); return o; };
   const size_t rp = (size_t)p.rp;
+  const int rpl = r > 0 ? p.rp : 0;
+  if (p.skinny) {
+    // few tokens: the f32 split partials instead of a dequantized weight; A zero-padded to rp for
+    // the forward's adapter blocks; u (and h for the dB pass) as in the other plans
+    if (which == REELS_HIP_WS_FWD) {
+      w.ap = take(p.padded && r > 0 ? (size_t)K * rp * 2 : 0);
+      w.pa = take(skinny_part_bytes(p.skf, M, N, rpl));
+    } else {
+      w.h = take((size_t)M * rp * 2);
+      w.at = take(r > 0 ? (size_t)K * rp * 2 : 0);  // A^T, or A padded to rp for recomputing h
+      w.ap = take(p.padded && r > 0 ? (size_t)K * rp * 2 : 0);  // A [K][rp] for the dX epilogue
+      w.u = take((size_t)M * rp * 2);
+      // dX partials, or the forward's when h is recomputed
+      const size_t pb = skinny_part_bytes(p.skb, M, K, rpl), pf = skinny_part_bytes(p.skf, M, N, rpl);
+      w.wd = take(pb > pf ? pb : pf);
+      w.pa = take(r > 0 ? (size_t)p.sa.splits * K * rp * 4 : 0);
+      w.pb = take(r > 0 ? (size_t)p.sb.splits * N * rp * 4 : 0);
+    }
+    w.total = off == 0 ? 256 : off;
+    return w;
+  }
   w.h = take((size_t)M * rp * 2);
   w.at = take(r > 0 ? (size_t)r * K * 2 : 0);
   w.wd = take(p.deq ? (size_t)N * K * 2 : 0);  // bf16 copy of the dequantized weight
@@ -732,11 +760,25 @@ static int i8lora_fwd_impl(int elt, const char* fn, const void* x, const int8_t*
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   const uint16_t* xb = static_cast<const uint16_t*>(x);
+  int rc;
+  if (p.skinny) {
+    // few tokens: y and h from the int8 codes in one split-K launch plus its epilogue
+    const uint16_t* Ap = static_cast<const uint16_t*>(A);
+    if (r > 0 && p.padded) {
+      uint16_t* ap = reinterpret_cast<uint16_t*>(ws + w.ap);
+      if ((rc = launch_pad_cols(Ap, K, (int)r, r, ap, p.rp, p.rp, st))) return rc;
+      Ap = ap;
+    }
+    return launch_skinny(0, elt, p.skf, xb, q, K, nullptr, r > 0 ? Ap : nullptr,
+                         reinterpret_cast<float*>(ws + w.pa), M, K, N, (int)r, p.rp, scales,
+                         static_cast<const uint16_t*>(B), N, static_cast<const uint16_t*>(bias),
+                         lora_scale, static_cast<uint16_t*>(y), static_cast<uint16_t*>(h_save), r,
+                         (int)r, st);
+  }
   // h [M][rp]: straight into h_save unless padded columns make the layouts differ
   uint16_t* h = r > 0 ? ((h_save && !p.padded) ? static_cast<uint16_t*>(h_save)
                                                : reinterpret_cast<uint16_t*>(ws + w.h))
                       : nullptr;
-  int rc;
   if (!p.fast) {
     if (r > 0) {
       { TraceScope _ts(st, "g_rowproj_kernel"); with_elt(elt, [&](auto e) { g_rowproj_kernel<decltype(e)::value><<<grid1(M * r), 256, 0, st>>>(xb, M, K, static_cast<const uint16_t*>(A), r, 1,
@@ -860,7 +902,19 @@ static int i8lora_bwd_impl(int elt, const char* fn, const void* dy, const void* 
     if ((rc = launch_pad_cols(hh, M, (int)r, r, hw, p.rp, p.rp, st))) return rc;
     hh = hw;
   }
-  if (p.deq) {
+  if (p.skinny && dx) {
+    // few tokens: dx and u = rnd(dy B^T) from one split-K launch over the int8 codes plus its
+    // epilogue (u lands in the workspace for the dA pass)
+    if ((rc = launch_skinny(1, elt, p.skb, dyb, q, K, scales, r > 0 ? Bb : nullptr,
+                            reinterpret_cast<float*>(ws + w.wd), M, N, K, (int)r, p.rp, nullptr,
+                            Ar, p.rp, nullptr, lora_scale, static_cast<uint16_t*>(dx),
+                            r > 0 ? u : nullptr, p.rp, p.rp, st)))
+      return rc;
+  } else if (p.skinny) {
+    if (r > 0 && dA &&
+        (rc = launch_rowproj(elt, dyb, M, N, Bb, (int)r, p.rp, u, nullptr, nullptr, st)))
+      return rc;
+  } else if (p.deq) {
     // 1. u = dy B^T; 2. dx = dy wt^T + c u A^T with wt[k][n] = bf16(q[n][k] s[n])
     if (r > 0 && (dx || dA)) {
       if ((rc = launch_rowproj(elt, dyb, M, N, Bb, (int)r, p.rp, u, nullptr, nullptr, st))) return rc;
@@ -886,7 +940,7 @@ static int i8lora_bwd_impl(int elt, const char* fn, const void* dy, const void* 
     }
   }
   // 2. dx = dys q + c u A^T (bf16), dx = dy f16(q f16(s)) + c u A^T (f16)
-  if (dx && !p.deq) {
+  if (dx && !p.deq && !p.skinny) {
     GemmArgs g{};
     g.act = f16 ? dyb : dys; g.q = q; g.colscale = nullptr; g.redscale = f16 ? scales : nullptr;
     g.L = r > 0 ? u : nullptr; g.R = Ar; g.bias = nullptr;
@@ -900,6 +954,21 @@ static int i8lora_bwd_impl(int elt, const char* fn, const void* dy, const void* 
                              reinterpret_cast<float*>(ws + w.pa), dA, false, st))) return rc;
   }
   if (dB) {
+    if (!hh && p.skinny) {
+      // recompute h exactly as the few-token forward computed it (same blocks, same split order)
+      uint16_t* hw = reinterpret_cast<uint16_t*>(ws + w.h);
+      const uint16_t* Ap = Ab;
+      if (p.padded) {
+        uint16_t* ap = reinterpret_cast<uint16_t*>(ws + w.at);  // A [K][rp] in the A^T slot
+        if ((rc = launch_pad_cols(Ab, K, (int)r, r, ap, p.rp, p.rp, st))) return rc;
+        Ap = ap;
+      }
+      if ((rc = launch_skinny(0, elt, p.skf, xb, q, K, nullptr, Ap, reinterpret_cast<float*>(ws + w.wd),
+                              M, K, N, (int)r, p.rp, nullptr, nullptr, N, nullptr, lora_scale, nullptr,
+                              hw, p.rp, p.rp, st, true)))
+        return rc;
+      hh = hw;
+    }
     if (!hh) {
       uint16_t* at = reinterpret_cast<uint16_t*>(ws + w.at);
       uint16_t* hw = reinterpret_cast<uint16_t*>(ws + w.h);

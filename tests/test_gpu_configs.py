@@ -124,10 +124,12 @@ def test_wan13b_chain_with_gelu(dev):
             assert_parity(oracle.bf16_to_f32(acts[i + 1]), yo, f"chain {name} y")
         xin = acts[i + 1]
 
-    # end-to-end drift against a chain computed in f64 from the weights the path multiplies: the
-    # bf16 dequantization wd = bf16(fl32(q s)) (oracle.dequant "bf16"; K and N are multiples of
-    # 64 here), h = bf16(x A), bf16 between layers. The drift against the exact-weight chain
-    # (f64 q s) is printed beside it; the per-linear checks above bound each layer's error.
+    # end-to-end drift against a chain computed in f64 from the weights the path multiplies. At
+    # 128 tokens the few-token path (at most 512 tokens) multiplies the exact int8 codes and
+    # applies s to the f32 sum, so the model is the exact-weight chain (f64 q s); with more
+    # tokens the path multiplies the bf16 dequantization wd = bf16(fl32(q s)) (oracle.dequant
+    # "bf16"). h = bf16(x A), bf16 between layers in both. The drift against the other model is
+    # printed beside it; the per-linear checks above bound each layer's error.
     def deq_forward(xb, q, s, A, B):
         f64 = lambda bits: oracle.bf16_to_f32(bits).astype(np.float64)
         xf = f64(xb)
@@ -145,7 +147,8 @@ def test_wan13b_chain_with_gelu(dev):
         rf = oracle.bf16_to_f32(ref).astype(np.float64)
         print(f"[configs] chain drift vs the {label} f64 chain: normwise "
               f"{np.abs(got - rf).max() / np.abs(rf).max():.3e}", flush=True)
-    assert_parity(got, oracle.bf16_to_f32(xo), "chain output drift", tol=3e-2)
+    model = xe if M <= 512 else xo
+    assert_parity(got, oracle.bf16_to_f32(model), "chain output drift", tol=3e-2)
 
     # ---- backward on the GPU, layer by layer, each checked against the oracle on its inputs
     g = oracle.normal_bf16(3999, (M, D), 1.0)
