@@ -41,11 +41,12 @@ int launch_dequant_transpose(int elt, const int8_t* q, int64_t ldq, const float*
                              int64_t K, uint16_t* wt, hipStream_t st);
 
 // Few-token path (skinny.hip): int8 codes streamed straight into registers, tokens on the MFMA's
-// 16-wide side, reduction split over blocks with f32 partials summed in split order by an epilogue
-// kernel. mode 0 = FWD (act = x, rows of q are outputs, lw = A [Kred][rp] zero-padded), 1 = DX
-// (act = dy, rows of q are the reduction, lw = B [r][Kred], s = the reduction's scale).
+// 16-wide side, the reduction split over blocks and finished in the same launch by the last block
+// of each tile (split order). mode 0 = FWD (act = x, rows of q are outputs, lw = A [Kred][rp]
+// zero-padded), 1 = DX (act = dy, rows of q are the reduction, lw = B [r][Kred], s = the
+// reduction's scale).
 constexpr int64_t kSkinnyMaxTokens = 512;
-constexpr int64_t kSkinnyTargetBlocks = 512;  // about two resident blocks per CU
+constexpr int64_t kSkinnyTargetBlocks = 256;  // about one block per CU
 struct SkinnyPlan {
   int T;   // token tiles of 16 per block
   int tb;  // token blocks
@@ -53,13 +54,16 @@ struct SkinnyPlan {
 };
 bool skinny_supported(int64_t M, int64_t K, int64_t N, int rp);
 SkinnyPlan skinny_plan(int64_t M, int64_t Kred, int64_t Ncols, int rp);
-size_t skinny_part_bytes(const SkinnyPlan& p, int64_t M, int64_t Ncols, int rp);
+// workspace of one launch: the split partials and l [M][rp]
+size_t skinny_ws_bytes(const SkinnyPlan& p, int64_t M, int64_t Ncols, int rp);
 // out = rnd(colscale * act W + c l R + bias) with l = rnd(act L) (h or u), written to lsave
 // ([M][ld_lsave], lsave_cols columns, zeros past r) when not NULL; R(o, j) = R[j][o] (mode 0,
-// row stride ldr) or R[o][j] (mode 1). adapter_only: l alone, from the same blocks and split
-// order as a full launch (so a recomputed h equals the forward's bit for bit)
+// row stride ldr) or R[o][j] (mode 1, rows of ldr >= rp elements, zeros past r). adapter_only: l
+// alone, from the same blocks and split order as a full launch (so a recomputed h equals the
+// forward's bit for bit). Launches on one stream are ordered; launches on different streams use
+// different counter slots.
 int launch_skinny(int mode, int elt, const SkinnyPlan& p, const uint16_t* act, const int8_t* q,
-                  int64_t ldq, const float* s, const uint16_t* lw, float* part, int64_t M,
+                  int64_t ldq, const float* s, const uint16_t* lw, void* ws, int64_t M,
                   int64_t Kred, int64_t Ncols, int r, int rp, const float* colscale,
                   const uint16_t* R, int64_t ldr, const uint16_t* bias, float c, uint16_t* out,
                   uint16_t* lsave, int64_t ld_lsave, int lsave_cols, hipStream_t st,

@@ -562,14 +562,14 @@ static WsLayout ws_layout(int64_t M, int64_t K, int64_t N, int64_t r, int which,
     // the forward's adapter blocks; u (and h for the dB pass) as in the other plans
     if (which == REELS_HIP_WS_FWD) {
       w.ap = take(p.padded && r > 0 ? (size_t)K * rp * 2 : 0);
-      w.pa = take(skinny_part_bytes(p.skf, M, N, rpl));
+      w.pa = take(skinny_ws_bytes(p.skf, M, N, rpl));
     } else {
       w.h = take((size_t)M * rp * 2);
       w.at = take(r > 0 ? (size_t)K * rp * 2 : 0);  // A^T, or A padded to rp for recomputing h
       w.ap = take(p.padded && r > 0 ? (size_t)K * rp * 2 : 0);  // A [K][rp] for the dX epilogue
       w.u = take((size_t)M * rp * 2);
       // dX partials, or the forward's when h is recomputed
-      const size_t pb = skinny_part_bytes(p.skb, M, K, rpl), pf = skinny_part_bytes(p.skf, M, N, rpl);
+      const size_t pb = skinny_ws_bytes(p.skb, M, K, rpl), pf = skinny_ws_bytes(p.skf, M, N, rpl);
       w.wd = take(pb > pf ? pb : pf);
       w.pa = take(r > 0 ? (size_t)p.sa.splits * K * rp * 4 : 0);
       w.pb = take(r > 0 ? (size_t)p.sb.splits * N * rp * 4 : 0);
@@ -762,7 +762,7 @@ static int i8lora_fwd_impl(int elt, const char* fn, const void* x, const int8_t*
   const uint16_t* xb = static_cast<const uint16_t*>(x);
   int rc;
   if (p.skinny) {
-    // few tokens: y and h from the int8 codes in one split-K launch plus its epilogue
+    // few tokens: y and h from the int8 codes in one launch
     const uint16_t* Ap = static_cast<const uint16_t*>(A);
     if (r > 0 && p.padded) {
       uint16_t* ap = reinterpret_cast<uint16_t*>(ws + w.ap);
@@ -903,8 +903,8 @@ static int i8lora_bwd_impl(int elt, const char* fn, const void* dy, const void* 
     hh = hw;
   }
   if (p.skinny && dx) {
-    // few tokens: dx and u = rnd(dy B^T) from one split-K launch over the int8 codes plus its
-    // epilogue (u lands in the workspace for the dA pass)
+    // few tokens: dx and u = rnd(dy B^T) from one launch over the int8 codes (u lands in the
+    // workspace for the dA pass)
     if ((rc = launch_skinny(1, elt, p.skb, dyb, q, K, scales, r > 0 ? Bb : nullptr,
                             reinterpret_cast<float*>(ws + w.wd), M, N, K, (int)r, p.rp, nullptr,
                             Ar, p.rp, nullptr, lora_scale, static_cast<uint16_t*>(dx),

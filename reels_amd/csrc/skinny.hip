@@ -3,16 +3,25 @@
 // (src/models/wan21/transformer.jl:185-188, I2V 225-235, through quantization.jl:73-76). There
 // the weight stream is the whole cost, so the int8 codes are read once, coalesced, straight from
 // HBM into registers (no bf16 copy of the weight) and converted there; the tokens sit on the
-// 16-wide side of v_mfma_f32_16x16x32 (77 tokens = 2 blocks of 3 tiles of 16).
+// 16-wide side of v_mfma_f32_16x16x32 (77 tokens = 5 tiles of 16).
 //
-//   skinny_kernel      block (o-block of 64 output rows, reduction split sp, token block tb of up
-//                      to 64 tokens): each of its 4 waves takes a quarter of the split's 64-wide
-//                      reduction chunks, accumulating 64 rows x 16T tokens; the 4 wave partials are summed in LDS in
-//                      wave order and written as f32 partials part[sp][m][col]. Blocks past the
-//                      output rows compute the adapter's rank-r projection partials (h = x A in
-//                      the forward, u = dy B^T for dX) into the columns past Ncols.
-//   skinny_epilogue    sums the splits in split order, rounds h (u) once to the element type and
-//                      writes out = rnd(scale * sum + c * h R + bias).
+// One launch does everything. A block is (tile, split): a tile is 64 output rows (or 32 rows of
+// the adapter's rank projection) x up to 16T tokens, a split a contiguous range of 64-wide
+// reduction chunks. The block's 4 waves each take a quarter of the split's chunks; their
+// accumulators are summed in LDS in wave order. With more than one split the block stores that
+// sum as an f32 partial and counts itself in on the tile; the block that arrives last sums the
+// tile's partials in split order (its own from registers) and finishes the tile:
+//   adapter tile: l = rnd(sum) (h = x A in the forward, u = dy B^T for dX) into the workspace
+//                 (and lsave); the last adapter tile to finish raises the launch's ready flag;
+//   output tile:  waits for that flag, then out = rnd(scale * sum + c * l R + bias), the l R
+//                 product on the MFMA.
+// The adapter blocks come first in the grid and wait for nothing, so the flag is normally up long
+// before an output tile looks; the wait is bounded all the same, and an output tile that gives up
+// computes l for its tokens itself with the adapter blocks' code and order (same bits), so the
+// result never depends on how the grid is scheduled.
+// The counters and the flag live in a per-stream slot of static device memory and are put back to
+// zero by the launch that used them, so launches need no clearing pass. Deterministic: fixed wave
+// order, fixed split order; the atomics only count.
 //
 // FWD: out[m][n] = rnd(s[n] sum_k x[m][k] q[n][k] + c sum_j h[m][j] B[j][n] + bias[n]),
 //      h = rnd(x A): the int8 path's formula (the scale on the f32 sum).
@@ -21,67 +30,115 @@
 //      f16(q[n][k] f16(s[n])) for f16 (the reference's binary16 weight, quantization.jl:61-62),
 //      made from the codes in registers; the weight columns of a reduction chunk reach the MFMA
 //      through ds_read_b64_tr_b8 from a per-wave LDS tile.
-// Deterministic: fixed wave order, fixed split order, no atomics.
 #include "i8gemm.h"
 
+#include <cstdlib>
 #include <mutex>
+#include <unordered_map>
 
 namespace reels {
 
 namespace sk {
-constexpr int NB = 64;       // output rows per block: 4 MFMA tiles of 16
-constexpr int NBL = 32;      // adapter rows per adapter block: 2 MFMA tiles of 16
+constexpr int NB = 64;       // output rows per tile: 4 MFMA tiles of 16
+constexpr int NBL = 32;      // adapter rows per tile: 2 MFMA tiles of 16
 constexpr int KC = 64;       // reduction chunk
 constexpr int MAXT = 5;      // token tiles of 16 per block (80 tokens)
+constexpr int MAXS = 8;      // reduction splits
 constexpr int STAGE = 4096;  // per-wave LDS staging (DX weight tile, FWD adapter chunk: 4 KiB each)
+constexpr int kSlots = 64;   // counter slots per device: one per stream, the last one shared
+constexpr int kMaxTiles = 4096;
+constexpr uint32_t kSpinLimit = 1u << 12;  // wait rounds of s_sleep 8 (about 1 ms) before computing l
 }  // namespace sk
+
+// one launch's counters (zero between launches)
+struct SkSlot {
+  uint32_t unused;
+  uint32_t hdone;    // adapter tiles finished
+  uint32_t hready;   // 1: l complete (set by the last adapter tile, cleared by the last tile)
+  uint32_t fin;      // tiles finished (launches with adapter and output tiles)
+  uint32_t pad[28];
+  uint32_t tile[sk::kMaxTiles];  // blocks of the tile that have stored their partial
+};
+static __device__ __align__(256) SkSlot sk_slots[sk::kSlots];
 
 struct SkArgs {
   const uint16_t* act;  // [M][Kred] 16-bit: x (FWD) or dy (DX)
   const int8_t* q;      // codes [N][K], row stride ldq
   const float* s;       // DX: scale of the reduction index n
   const uint16_t* lw;   // adapter operand: FWD A [Kred][rp] (zeros past r), DX B [r][Kred]
-  float* part;          // [S][M][ldp] f32 partials
-  int64_t M, Kred, Ncols, ldq;
-  int r, rp, S, ldp, nblk;  // nblk: output blocks; adapter blocks follow
-  int tb, blocks;           // token blocks; all blocks of the launch
-  int blk0;                 // first block index (nblk: the adapter blocks alone)
+  float* part;          // split partials in MFMA fragment order (output tiles, then adapter tiles)
+  uint16_t* hl;         // [M][rp] l rounded to the element type (zeros past r)
+  const float* colscale;
+  const uint16_t* R;    // FWD B [r][Ncols] (row stride ldr), DX A [Ncols][ldr] (zeros past r)
+  const uint16_t* bias;
+  uint16_t* out;        // [M][Ncols]
+  uint16_t* lsave;      // [M][ld_lsave], lsave_cols columns (or NULL)
+  SkSlot* slot;
+  int64_t M, Kred, Ncols, ldq, ldr, ld_lsave;
+  float c;
+  int r, rp, S, nblk, lblk, tb, lsave_cols;
+  int blocks;  // of the launch
+  int nad;     // adapter blocks: the first blocks of the grid
+  int ntm;     // output tiles (nblk * tb; 0 for an adapter-only launch)
+  uint32_t spin;  // wait rounds before an output tile computes l itself
+  int nta;     // adapter tiles (lblk * tb)
 };
 
-// Block b runs on XCD b % 8. Each XCD takes a contiguous range of the logical order, which walks
-// the token blocks of one (row block, split) first: the blocks that read the same weight rows
-// run on one XCD, close in time, and share them through its L2.
 struct SkBlock {
-  int blk, sp, tb;
+  int blk, sp, tb, tile;  // blk >= nblk: adapter row block blk - nblk
 };
-__device__ __forceinline__ SkBlock skinny_decode(const SkArgs& a) {
-  const int b = blockIdx.x, xcd = b & 7, idx = b >> 3;
-  const int per = a.blocks >> 3, rem = a.blocks & 7;
-  const int logical = xcd * per + (xcd < rem ? xcd : rem) + idx;
-  SkBlock d;
-  d.tb = logical % a.tb;
-  const int rest = logical / a.tb;
-  d.sp = rest % a.S;
-  d.blk = a.blk0 + rest / a.S;
-  return d;
-}
 
+// dynamic LDS: the waves' staging areas during the loop, the 4 wave sums (4 x 4T fragments of 1 KiB)
+// after it; the last 16 bytes hold the block's arrival count and wait result (written and read
+// after the sums are read; for T = 1 they get 16 bytes of their own)
 static constexpr int skinny_lds(int T) {
-  return (4 * 4 * T * 4 * 64 * 4) > 4 * sk::STAGE ? (4 * 4 * T * 4 * 64 * 4) : 4 * sk::STAGE;
+  return (4 * 4 * T * 64 * 16) > 4 * sk::STAGE ? (4 * 4 * T * 64 * 16) : 4 * sk::STAGE + 16;
 }
 
-// One block's work; LORA: an adapter block (rows j of A^T in the forward, of B for dX) rather than
-// an output block of the int8 weight.
+// Data one block hands to another (split partials, l) is stored and loaded with device-scope
+// coherence (sc1: what the compiler emits for agent-scope relaxed atomics), so it never sits in
+// one XCD's L2 where another XCD cannot see it, and no cache-wide write-back or invalidate is
+// needed. Ordering: a block's stores have completed (s_waitcnt vmcnt(0) in every wave, then the
+// barrier) before its thread 0 counts it in; a reader issues its loads only after it has seen the
+// count (or the flag), so the loads reach the device's coherence point after those stores.
+constexpr int kSC1 = 16;  // cache policy bit: device scope
+__device__ __forceinline__ uint32_t sk_add(uint32_t* p, uint32_t v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t sk_load(uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void sk_store(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// every memory operation of this wave complete (and no compiler motion across it)
+__device__ __forceinline__ void sk_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t sk_rsrc(const void* p, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+// A tile of a launch with both adapter and output tiles is finished: the last of them lowers the
+// ready flag for the next launch (thread 0, after the tile no longer reads the flag)
+__device__ __forceinline__ void skinny_finish(const SkArgs& a) {
+  const uint32_t old = sk_add(&a.slot->fin, 1u);
+  if (old == (uint32_t)(a.nta + a.ntm) - 1) {
+    sk_store(&a.slot->hready, 0u);
+    sk_store(&a.slot->fin, 0u);
+  }
+}
+
+// One wave's share of a (row block, split, token block): acc[i][tt] = rows 16 i + (0..15) x tokens
+// 16 tt + (0..15) over the wave's quarter of the split's chunks. LORA: a block of the adapter's
+// rank projection (rows j of A^T in the forward, of B for dX) rather than of the int8 weight.
 template <int T, int MODE, int ELT, bool LORA>
-__device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, uint8_t* smem) {
+__device__ __forceinline__ void skinny_acc(const SkArgs& a, int blk, int sp, int64_t tok0,
+                                           uint8_t* smem, f32x4 (&acc)[LORA ? 2 : 4][T]) {
   using E = Elt<ELT>;
   typedef typename E::v8 V8;
   constexpr bool lora = LORA;
   const int t = threadIdx.x, lane = t & 63;
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);
   const int l16 = lane & 15, g = lane >> 4;
-  const int blk = d.blk, sp = d.sp;
-  const int64_t tok0 = (int64_t)d.tb * (16 * T);
   constexpr int NI = lora ? 2 : 4;  // MFMA row tiles of 16
   const int64_t o0 = lora ? (int64_t)(blk - a.nblk) * sk::NBL : (int64_t)blk * sk::NB;
   const int nc = (int)(a.Kred / sk::KC);
@@ -168,7 +225,6 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
     }
   };
 
-  f32x4 acc[NI][T];
 #pragma unroll
   for (int i = 0; i < NI; ++i)
 #pragma unroll
@@ -281,124 +337,286 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
     load(chunk(i + 3), i + 3 < nw, st1);
     __builtin_amdgcn_sched_barrier(0);
   }
+}
 
-  // the 4 wave partials [i][tt][v][lane] in LDS, summed in wave order
+// The block's sum of its 4 waves' accumulators: the wave sums go to LDS as MFMA fragments (wave w,
+// fragment f = i T + tt, lane) and are summed in wave order by the wave that owns the fragment
+// afterwards: wave w owns f = w, w + 4, ... with the same lane slot (each thread reads and writes
+// 16 consecutive bytes per fragment).
+template <int T, int NI>
+__device__ __forceinline__ void skinny_sum(const f32x4 (&acc)[NI][T], uint8_t* smem,
+                                           f32x4 (&sum)[(NI * T + 3) / 4]) {
+  constexpr int NF = NI * T, FPW = (NF + 3) / 4;
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   __syncthreads();
-  float* red = reinterpret_cast<float*>(smem);
-  constexpr int PER = NI * T * 4 * 64;
+  f32x4* red = reinterpret_cast<f32x4*>(smem);
 #pragma unroll
   for (int i = 0; i < NI; ++i)
 #pragma unroll
-    for (int tt = 0; tt < T; ++tt)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) red[w * PER + ((i * T + tt) * 4 + v) * 64 + lane] = acc[i][tt][v];
+    for (int tt = 0; tt < T; ++tt) red[(w * NF + i * T + tt) * 64 + lane] = acc[i][tt];
   __syncthreads();
-  const int64_t limit = lora ? a.rp : a.Ncols;
-  const int64_t col0 = lora ? a.Ncols : 0;
-  // thread -> (token, 4 consecutive outputs): value (o = 16 i + 4 qd + v, token 16 tt + c) sits at
-  // [i][tt][v][16 qd + c] of each wave's block; the 4 waves summed in wave order, stored as 16
-  // bytes, so a token's NB outputs go out as one contiguous row segment
-  constexpr int QUADS = NI * 4;  // output quads per token
-  for (int idx = t; idx < 16 * T * QUADS; idx += 256) {
-    const int tl = idx / QUADS, n4 = idx % QUADS;
-    const int i = n4 >> 2, qd = n4 & 3, tt = tl >> 4, cc = tl & 15;
-    f32x4 o;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int e = ((i * T + tt) * 4 + v) * 64 + 16 * qd + cc;
-      o[v] = ((red[e] + red[PER + e]) + red[2 * PER + e]) + red[3 * PER + e];
+  for (int k = 0; k < FPW; ++k) {
+    const int f = w + 4 * k;
+    sum[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (f < NF)
+      sum[k] = ((red[f * 64 + lane] + red[(NF + f) * 64 + lane]) + red[(2 * NF + f) * 64 + lane]) +
+               red[(3 * NF + f) * 64 + lane];
+  }
+}
+
+// l = rnd(sum) of an adapter tile (rows j = o0 + 16 i + 4 g + v of fragment (i, tt), token
+// 16 tt + l16) into hl (device scope) and, with lsave set, into lsave
+template <int T, int ELT>
+__device__ __forceinline__ void skinny_put_l(const SkArgs& a, int64_t o0, int64_t tok0,
+                                             const f32x4 (&sum)[(2 * T + 3) / 4], bool lsave) {
+  using E = Elt<ELT>;
+  constexpr int NF = 2 * T, FPW = (NF + 3) / 4;
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l16 = lane & 15, g = lane >> 4;
+  const __amdgpu_buffer_rsrc_t rl = sk_rsrc(a.hl, a.M * a.rp * 2);
+#pragma unroll
+  for (int k = 0; k < FPW; ++k) {
+    const int f = w + 4 * k;
+    if (f >= NF) continue;
+    const int i = f / T, tt = f % T;
+    const int64_t tok = tok0 + 16 * tt + l16, j = o0 + 16 * i + 4 * g;
+    if (tok >= a.M || j >= a.rp) continue;
+    uint32_t b[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) b[v] = j + v < a.r ? E::bits(sum[k][v]) : 0u;
+    typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2;
+    __builtin_amdgcn_raw_buffer_store_b64(u32x2{b[0] | (b[1] << 16), b[2] | (b[3] << 16)}, rl,
+                                          (uint32_t)((tok * a.rp + j) * 2), 0, kSC1);
+    if (lsave && a.lsave != nullptr && a.lsave != a.hl) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (j + v < a.lsave_cols) a.lsave[tok * a.ld_lsave + j + v] = (uint16_t)b[v];
     }
-    const int64_t tok = tok0 + tl, ob = o0 + 4 * n4;
-    if (tok < a.M && ob < limit)
-      *reinterpret_cast<f32x4*>(a.part + ((int64_t)sp * a.M + tok) * a.ldp + col0 + ob) = o;
+  }
+}
+
+// One block: its accumulators, the tile's split reduction when it arrives last, then the tile's
+// results (l for an adapter tile, out for an output tile).
+template <int T, int MODE, int ELT, bool LORA>
+__device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, uint8_t* smem) {
+  using E = Elt<ELT>;
+  constexpr bool lora = LORA;
+  const int t = threadIdx.x, lane = t & 63;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int l16 = lane & 15, g = lane >> 4;
+  const int blk = d.blk, sp = d.sp;
+  const int64_t tok0 = (int64_t)d.tb * (16 * T);
+  constexpr int NI = lora ? 2 : 4;
+  const int64_t o0 = lora ? (int64_t)(blk - a.nblk) * sk::NBL : (int64_t)blk * sk::NB;
+  constexpr int NF = NI * T, FPW = (NF + 3) / 4;
+  f32x4 sum[FPW];
+  {
+    f32x4 acc[NI][T];
+    skinny_acc<T, MODE, ELT, LORA>(a, blk, sp, tok0, smem, acc);
+    skinny_sum<T, NI>(acc, smem, sum);
+  }
+
+  uint32_t& bc = reinterpret_cast<uint32_t*>(smem + skinny_lds(T) - 16)[1];
+  SkSlot* slot = a.slot;
+  if (a.S > 1) {
+    // partial [tile][split][fragment][lane] (16 bytes); output tiles first, then adapter tiles
+    const int64_t tbase = lora ? (int64_t)a.ntm * a.S * (4 * T * 64) + (int64_t)(d.tile - a.ntm) * a.S * (NF * 64)
+                               : (int64_t)d.tile * a.S * (NF * 64);
+    const __amdgpu_buffer_rsrc_t rp_ = sk_rsrc(reinterpret_cast<f32x4*>(a.part) + tbase, (int64_t)a.S * NF * 64 * 16);
+#pragma unroll
+    for (int k = 0; k < FPW; ++k) {
+      const int f = w + 4 * k;
+      if (f < NF)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sum[k]), rp_,
+                                               (uint32_t)((sp * (NF * 64) + f * 64 + lane) * 16), 0, kSC1);
+    }
+    sk_drain();
+    __syncthreads();
+    if (t == 0) {
+      const uint32_t old = sk_add(&slot->tile[d.tile], 1u);
+      if (old == (uint32_t)a.S - 1) sk_store(&slot->tile[d.tile], 0u);
+      bc = old;
+    }
+    __syncthreads();
+    if (bc != (uint32_t)a.S - 1) return;
+    asm volatile("" ::: "memory");
+    // the tile's sum in split order, SB splits' loads in flight at a time
+    f32x4 tot[FPW];
+#pragma unroll
+    for (int k = 0; k < FPW; ++k) tot[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    constexpr int SB = FPW > 3 ? 2 : 4;
+    for (int s0 = 0; s0 < a.S; s0 += SB) {
+      f32x4 v[SB][FPW];
+#pragma unroll
+      for (int u = 0; u < SB; ++u)
+#pragma unroll
+        for (int k = 0; k < FPW; ++k) {
+          const int f = w + 4 * k, s = s0 + u;
+          v[u][k] = sum[k];
+          if (f < NF && s < a.S && s != sp)
+            v[u][k] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                    rp_, (uint32_t)((s * (NF * 64) + f * 64 + lane) * 16), 0, kSC1));
+        }
+#pragma unroll
+      for (int u = 0; u < SB; ++u)
+        if (s0 + u < a.S) {
+#pragma unroll
+          for (int k = 0; k < FPW; ++k) tot[k] += v[u][k];
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < FPW; ++k) sum[k] = tot[k];
+  } else {
+#pragma unroll
+    for (int k = 0; k < FPW; ++k) sum[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f} + sum[k];
+  }
+
+  const __amdgpu_buffer_rsrc_t rl = sk_rsrc(a.hl, a.M * a.rp * 2);
+  if constexpr (lora) {
+    skinny_put_l<T, ELT>(a, o0, tok0, sum, true);
+    sk_drain();
+    __syncthreads();
+    if (t == 0) {
+      const uint32_t old = sk_add(&slot->hdone, 1u);
+      if (old == (uint32_t)a.nta - 1) {
+        sk_store(&slot->hdone, 0u);
+        if (a.ntm > 0) sk_store(&slot->hready, 1u);
+      }
+      if (a.ntm > 0) skinny_finish(a);
+    }
+    return;
+  } else {
+    // l complete: the adapter blocks come first in the grid and wait for nothing, so the flag is
+    // normally up by the time an output tile gets here. Should they not have started after a long
+    // wait (a grid that cannot be resident at once, behind other work), the block computes l for
+    // its tokens itself, with the adapter blocks' code, splits and order, so the values are the
+    // same bits either way.
+    if (a.nad > 0) {
+      uint32_t& up = reinterpret_cast<uint32_t*>(smem + skinny_lds(T) - 16)[2];
+      if (t == 0) {
+        uint32_t n = 0, v;
+        while ((v = sk_load(&slot->hready)) == 0u && ++n <= a.spin) __builtin_amdgcn_s_sleep(8);
+        up = v;
+      }
+      __syncthreads();
+      if (up == 0u) {
+        for (int lb = 0; lb < a.lblk; ++lb) {
+          f32x4 tl[(2 * T + 3) / 4];
+#pragma unroll
+          for (int k = 0; k < (2 * T + 3) / 4; ++k) tl[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+          for (int s = 0; s < a.S; ++s) {
+            f32x4 acc[2][T], ps[(2 * T + 3) / 4];
+            skinny_acc<T, MODE, ELT, true>(a, a.nblk + lb, s, tok0, smem, acc);
+            skinny_sum<T, 2>(acc, smem, ps);
+#pragma unroll
+            for (int k = 0; k < (2 * T + 3) / 4; ++k) tl[k] += ps[k];
+          }
+          skinny_put_l<T, ELT>(a, (int64_t)lb * sk::NBL, tok0, tl, false);
+        }
+        sk_drain();
+        __syncthreads();
+      }
+      asm volatile("" ::: "memory");
+    }
+    // lo = l R for this tile on the MFMA, 32 rank columns per step: A operand rows o = 16 i + l16
+    // with j = 32 jc + 8 g + (0..7), B operand the tokens' l[tok][j .. j + 7]
+    f32x4 lo[FPW];
+#pragma unroll
+    for (int k = 0; k < FPW; ++k) lo[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int njc = a.nad > 0 ? (a.rp + 31) / 32 : 0;
+    uint16_t* rst = reinterpret_cast<uint16_t*>(smem);  // FWD: R rows [32 j][64 o]
+    for (int jc = 0; jc < njc; ++jc) {
+      const int j0 = 32 * jc;
+      if constexpr (MODE == 0) {
+        __syncthreads();
+        {
+          const int row = t >> 3, col = 8 * (t & 7);
+          u32x4 v = u32x4{0u, 0u, 0u, 0u};
+          if (j0 + row < a.r) v = *reinterpret_cast<const u32x4*>(a.R + (int64_t)(j0 + row) * a.ldr + o0 + col);
+          *reinterpret_cast<u32x4*>(rst + row * 64 + col) = v;
+        }
+        __syncthreads();
+      }
+#pragma unroll
+      for (int k = 0; k < FPW; ++k) {
+        const int f = w + 4 * k;
+        if (f >= NF) continue;
+        const int i = f / T, tt = f % T;
+        u32x4 av;
+        if constexpr (MODE == 0) {
+          // transposed 16-bit reads: providing lane p addresses row 8 g + 4 h + p / 4, columns
+          // 16 i + 4 (p % 4) .. +3; lane l16 receives o = 16 i + l16, j = 8 g + 4 h + (0..3)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const uint16_t* p = rst + (8 * g + 4 * h + (l16 >> 2)) * 64 + 16 * i + 4 * (l16 & 3);
+            const i16x4 r4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(i16x4, p));
+            av[2 * h] = (uint16_t)r4[0] | ((uint32_t)(uint16_t)r4[1] << 16);
+            av[2 * h + 1] = (uint16_t)r4[2] | ((uint32_t)(uint16_t)r4[3] << 16);
+          }
+        } else {
+          const int jj = j0 + 8 * g;
+          av = jj < a.rp ? *reinterpret_cast<const u32x4*>(a.R + (o0 + 16 * i + l16) * a.ldr + jj)
+                         : u32x4{0u, 0u, 0u, 0u};
+        }
+        const int64_t tok = tok0 + 16 * tt + l16;
+        const int jj = j0 + 8 * g;
+        const u32x4 bv = (tok < a.M && jj < a.rp)
+                             ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                             rl, (uint32_t)((tok * a.rp + jj) * 2), 0, kSC1))
+                             : u32x4{0u, 0u, 0u, 0u};
+        lo[k] = E::mfma16(E::as8(av), E::as8(bv), lo[k]);
+      }
+    }
+    // out = rnd(scale * sum + c * lo + bias) for rows o = o0 + 16 i + 4 g + v, token 16 tt + l16
+#pragma unroll
+    for (int k = 0; k < FPW; ++k) {
+      const int f = w + 4 * k;
+      if (f >= NF) continue;
+      const int i = f / T, tt = f % T;
+      const int64_t tok = tok0 + 16 * tt + l16, o = o0 + 16 * i + 4 * g;
+      if (tok >= a.M) continue;
+      uint32_t b[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float sc = a.colscale ? a.colscale[o + v] * sum[k][v] : sum[k][v];
+        const float bs = a.bias ? E::to_f32(a.bias[o + v]) : 0.0f;
+        b[v] = E::bits(sc + a.c * lo[k][v] + bs);
+      }
+      *reinterpret_cast<uint2*>(a.out + tok * a.Ncols + o) = uint2{b[0] | (b[1] << 16), b[2] | (b[3] << 16)};
+    }
+    if (a.nad > 0 && t == 0) skinny_finish(a);
   }
 }
 
 template <int T, int MODE, int ELT>
 __global__ __launch_bounds__(256, 2) void skinny_kernel(SkArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const SkBlock d = skinny_decode(a);
-  if (d.blk >= a.nblk) skinny_block<T, MODE, ELT, true>(a, d, smem);
+  // grid order: adapter blocks, then output blocks; within each (row block, split, token block)
+  // with the token block fastest, so blocks that read the same weight rows start together
+  const int tk = (int)blockIdx.x;
+  const bool lora = tk < a.nad;
+  int rest = lora ? tk : tk - a.nad;
+  SkBlock d;
+  d.tb = rest % a.tb;
+  rest /= a.tb;
+  d.sp = rest % a.S;
+  const int rb = rest / a.S;
+  d.blk = lora ? a.nblk + rb : rb;
+  d.tile = lora ? a.ntm + rb * a.tb + d.tb : rb * a.tb + d.tb;
+  if (lora) skinny_block<T, MODE, ELT, true>(a, d, smem);
   else skinny_block<T, MODE, ELT, false>(a, d, smem);
-}
-
-// out[m][o] = rnd(scale[o] * sum_sp part[sp][m][o] + c * sum_j l[m][j] R(o, j) + bias[o]) with
-// l[m][j] = rnd(sum_sp part[sp][m][Ncols + j]) (h in the forward, u for dX); R(o, j) = B[j][o]
-// (MODE 0, row stride ldr) or R[o][j] (MODE 1, rows of ldr >= rp elements, zeros past r). One
-// output per thread; the split partials and the adapter operand are loaded in independent batches
-// (the epilogue is latency-bound: few bytes, many blocks). lsave[m][j] (j < lsave_cols, zeros
-// past r) receives l from the blocks of column block 0.
-template <int MODE, int ELT>
-__global__ __launch_bounds__(256) void skinny_epilogue_kernel(
-    const float* __restrict__ part, int S, int64_t M, int64_t Ncols, int ldp, int r, int rp,
-    const float* __restrict__ colscale, const uint16_t* __restrict__ R, int64_t ldr,
-    const uint16_t* __restrict__ bias, float c, uint16_t* __restrict__ out,
-    uint16_t* __restrict__ lsave, int64_t ld_lsave, int lsave_cols) {
-  using E = Elt<ELT>;
-  extern __shared__ float hl[];  // rp values of l for this token
-  const int t = threadIdx.x;
-  const int64_t m = blockIdx.y;
-  const float* pm = part + m * ldp;
-  const int64_t sstride = M * ldp;
-  auto split_sum = [&](int64_t col) {  // sum over the splits in split order, 8 loads in flight
-    float v = 0.0f;
-    for (int s = 0; s < S; s += 8) {
-      float p[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) p[u] = s + u < S ? pm[(int64_t)(s + u) * sstride + col] : 0.0f;
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (s + u < S) v += p[u];
-    }
-    return v;
-  };
-  for (int j = t; j < rp; j += 256) {
-    const float v = split_sum(Ncols + j);
-    const uint32_t b = j < r ? E::bits(v) : 0u;
-    hl[j] = E::to_f32((uint16_t)b);
-    if (blockIdx.x == 0 && lsave != nullptr && j < lsave_cols) lsave[m * ld_lsave + j] = (uint16_t)b;
-  }
-  __syncthreads();
-  const int64_t o = (int64_t)blockIdx.x * 256 + t;
-  if (out == nullptr || o >= Ncols) return;
-  const float acc = split_sum(o);
-  float lo = 0.0f;
-  if (MODE == 0) {
-    for (int j0 = 0; j0 < r; j0 += 16) {
-      float b[16];
-#pragma unroll
-      for (int u = 0; u < 16; ++u)
-        b[u] = j0 + u < r ? E::to_f32(R[(int64_t)(j0 + u) * ldr + o]) : 0.0f;
-#pragma unroll
-      for (int u = 0; u < 16; ++u) lo += hl[j0 + u < rp ? j0 + u : 0] * b[u];
-    }
-  } else {
-    const uint16_t* ro = R + o * ldr;
-    for (int j0 = 0; j0 < rp; j0 += 32) {
-      u32x4 a4[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-        a4[u] = j0 + 8 * u < rp ? *reinterpret_cast<const u32x4*>(ro + j0 + 8 * u) : u32x4{0, 0, 0, 0};
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int j = j0 + 8 * u + 2 * q;
-          if (j < rp) lo += hl[j] * E::lo(a4[u][q]) + hl[j + 1] * E::hi(a4[u][q]);
-        }
-    }
-  }
-  const float sc = colscale ? colscale[o] * acc : acc;
-  const float bs = bias ? E::to_f32(bias[o]) : 0.0f;
-  out[m * Ncols + o] = (uint16_t)E::bits(sc + c * lo + bs);
 }
 
 bool skinny_supported(int64_t M, int64_t K, int64_t N, int rp) {
   // the reduction in whole 64-chunks, whole 64-row blocks, 32-bit buffer offsets (with room for
-  // the token-block overrun), the epilogue's LDS row of l
+  // the token-block overrun), the tiles within a counter slot
+  const int64_t tb = ceil_div(M, 16 * sk::MAXT);
+  const int64_t mx = K > N ? K : N;
   return M > 0 && M <= kSkinnyMaxTokens && K % 64 == 0 && N % 64 == 0 &&
-         (M + 128) * (K > N ? K : N) * 2 < ((int64_t)1 << 31) && N * K < ((int64_t)1 << 31) &&
-         (int64_t)rp * (K > N ? K : N) * 2 < ((int64_t)1 << 31) && rp <= 4096;
+         (M + 128) * mx * 2 < ((int64_t)1 << 31) && N * K < ((int64_t)1 << 31) &&
+         (int64_t)rp * mx * 2 < ((int64_t)1 << 31) && rp <= 4096 &&
+         (mx / sk::NB + ceil_div(rp, sk::NBL)) * tb <= sk::kMaxTiles;
 }
 
 SkinnyPlan skinny_plan(int64_t M, int64_t Kred, int64_t Ncols, int rp) {
@@ -407,20 +625,35 @@ SkinnyPlan skinny_plan(int64_t M, int64_t Kred, int64_t Ncols, int rp) {
   p.T = (int)ceil_div(ceil_div(M, p.tb), 16);
   const int64_t blocks = (Ncols / sk::NB + ceil_div(rp, sk::NBL)) * p.tb;
   const int64_t nc = Kred / sk::KC;
-  // about two blocks per CU, each wave at least one chunk
+  // about one block per CU, each wave at least one chunk
   int64_t S = (kSkinnyTargetBlocks + blocks / 2) / (blocks > 0 ? blocks : 1);
   if (S > nc / 4) S = nc / 4;
+  if (S > sk::MAXS) S = sk::MAXS;
   if (S < 1) S = 1;
   p.S = (int)S;
   return p;
 }
 
-size_t skinny_part_bytes(const SkinnyPlan& p, int64_t M, int64_t Ncols, int rp) {
-  return (size_t)p.S * (size_t)M * (size_t)(Ncols + rp) * 4;
+size_t skinny_ws_bytes(const SkinnyPlan& p, int64_t M, int64_t Ncols, int rp) {
+  const size_t tiles = (size_t)(Ncols / sk::NB) * p.tb * (4 * p.T) + (size_t)ceil_div(rp, sk::NBL) * p.tb * (2 * p.T);
+  const size_t part = p.S > 1 ? tiles * p.S * 64 * 16 : 0;
+  return align_up(part, 256) + (size_t)M * rp * 2;
 }
 
+// the calling stream's counter slot on the current device; the last slot is shared by streams
+// beyond the first kSlots - 1, whose launches are then ordered through an event
+struct SkSlots {
+  std::mutex mu;
+  SkSlot* base = nullptr;
+  std::unordered_map<hipStream_t, int> map;
+  hipEvent_t shared_ev = nullptr;
+  bool shared_used = false;
+};
+constexpr int kSkMaxDevices = 64;
+static SkSlots g_sk[kSkMaxDevices];
+
 template <int MODE, int ELT, int T>
-static hipError_t launch_skinny_t(const SkArgs& a, dim3 grid, hipStream_t st) {
+static hipError_t launch_skinny_t(const SkArgs& a, hipStream_t st) {
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
   std::call_once(once, [] {
@@ -428,39 +661,85 @@ static hipError_t launch_skinny_t(const SkArgs& a, dim3 grid, hipStream_t st) {
                                hipFuncAttributeMaxDynamicSharedMemorySize, skinny_lds(T));
   });
   if (attr != hipSuccess) return attr;
-  skinny_kernel<T, MODE, ELT><<<grid, 256, skinny_lds(T), st>>>(a);
+  skinny_kernel<T, MODE, ELT><<<dim3((unsigned)a.blocks), 256, skinny_lds(T), st>>>(a);
   return hipSuccess;
 }
 
 int launch_skinny(int mode, int elt, const SkinnyPlan& p, const uint16_t* act, const int8_t* q,
-                  int64_t ldq, const float* s, const uint16_t* lw, float* part, int64_t M,
+                  int64_t ldq, const float* s, const uint16_t* lw, void* ws, int64_t M,
                   int64_t Kred, int64_t Ncols, int r, int rp, const float* colscale,
                   const uint16_t* R, int64_t ldr, const uint16_t* bias, float c, uint16_t* out,
                   uint16_t* lsave, int64_t ld_lsave, int lsave_cols, hipStream_t st,
                   bool adapter_only) {
   SkArgs a;
-  a.act = act; a.q = q; a.s = s; a.lw = lw; a.part = part;
+  a.act = act; a.q = q; a.s = s; a.lw = lw;
   a.M = M; a.Kred = Kred; a.Ncols = Ncols; a.ldq = ldq;
-  a.r = r; a.rp = r > 0 ? rp : 0; a.S = p.S; a.ldp = (int)(Ncols + a.rp);
+  a.r = r; a.rp = r > 0 ? rp : 0; a.S = p.S;
   a.nblk = (int)(Ncols / sk::NB);
-  const int lblk = (int)ceil_div(a.rp, sk::NBL);
+  a.lblk = (int)ceil_div(a.rp, sk::NBL);
   a.tb = p.tb;
-  a.blk0 = adapter_only ? a.nblk : 0;
-  a.blocks = (adapter_only ? lblk : a.nblk + lblk) * p.S * p.tb;
-  const dim3 grid((unsigned)a.blocks);
+  a.colscale = colscale; a.R = R; a.ldr = ldr; a.bias = bias; a.c = c;
+  a.out = out; a.lsave = lsave; a.ld_lsave = ld_lsave; a.lsave_cols = lsave_cols;
+  a.ntm = adapter_only ? 0 : a.nblk * p.tb;
+  a.nta = a.lblk * p.tb;
+  // REELS_HIP_SKINNY_SPIN (tests): wait rounds before an output tile computes l itself; 0 makes
+  // every output tile take that path
+  a.spin = sk::kSpinLimit;
+  if (const char* e = std::getenv("REELS_HIP_SKINNY_SPIN")) a.spin = (uint32_t)std::strtoul(e, nullptr, 10);
+  a.nad = a.nta * p.S;
+  a.blocks = a.nad + a.ntm * p.S;
+  if (a.blocks <= 0) return REELS_HIP_OK;
+  const size_t tiles = (size_t)a.nblk * p.tb * (4 * p.T) + (size_t)a.lblk * p.tb * (2 * p.T);
+  a.part = static_cast<float*>(ws);
+  uint16_t* hl = reinterpret_cast<uint16_t*>(static_cast<uint8_t*>(ws) + align_up(p.S > 1 ? tiles * p.S * 64 * 16 : 0, 256));
+  // l straight into lsave when the layouts agree
+  a.hl = (lsave != nullptr && ld_lsave == a.rp && lsave_cols >= a.rp) ? lsave : hl;
+
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(REELS_HIP_EHIP, std::string("skinny_kernel: hipGetDevice: ") + hipGetErrorString(e));
+  if (dev < 0 || dev >= kSkMaxDevices) return fail(REELS_HIP_EHIP, "skinny_kernel: device index out of range");
+  SkSlots& tab = g_sk[dev];
+  std::lock_guard<std::mutex> lock(tab.mu);
+  if (tab.base == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(sk_slots));
+    if (e != hipSuccess || ptr == nullptr)
+      return fail(REELS_HIP_EHIP, std::string("skinny_kernel: hipGetSymbolAddress(sk_slots): ") + hipGetErrorString(e));
+    tab.base = static_cast<SkSlot*>(ptr);
+  }
+  int idx;
+  auto it = tab.map.find(st);
+  if (it != tab.map.end()) {
+    idx = it->second;
+  } else if ((int)tab.map.size() < sk::kSlots - 1) {
+    idx = (int)tab.map.size();
+    tab.map.emplace(st, idx);
+  } else {
+    idx = sk::kSlots - 1;
+  }
+  const bool shared = idx == sk::kSlots - 1;
+  if (shared) {
+    if (tab.shared_ev == nullptr && (e = hipEventCreateWithFlags(&tab.shared_ev, hipEventDisableTiming)) != hipSuccess)
+      return fail(REELS_HIP_EHIP, std::string("skinny_kernel: hipEventCreateWithFlags: ") + hipGetErrorString(e));
+    if (tab.shared_used && (e = hipStreamWaitEvent(st, tab.shared_ev, 0)) != hipSuccess)
+      return fail(REELS_HIP_EHIP, std::string("skinny_kernel: hipStreamWaitEvent: ") + hipGetErrorString(e));
+  }
+  a.slot = tab.base + idx;
+
   hipError_t attr = hipSuccess;
   {
     TraceScope _ts(st, mode == 0 ? "skinny_kernel<0>" : "skinny_kernel<1>");
-    with_elt(elt, [&](auto e) {
-      constexpr int EL = decltype(e)::value;
+    with_elt(elt, [&](auto el) {
+      constexpr int EL = decltype(el)::value;
       auto go = [&](auto m) {
         constexpr int MD = decltype(m)::value;
         switch (p.T) {
-          case 1: attr = launch_skinny_t<MD, EL, 1>(a, grid, st); break;
-          case 2: attr = launch_skinny_t<MD, EL, 2>(a, grid, st); break;
-          case 3: attr = launch_skinny_t<MD, EL, 3>(a, grid, st); break;
-          case 4: attr = launch_skinny_t<MD, EL, 4>(a, grid, st); break;
-          default: attr = launch_skinny_t<MD, EL, 5>(a, grid, st); break;
+          case 1: attr = launch_skinny_t<MD, EL, 1>(a, st); break;
+          case 2: attr = launch_skinny_t<MD, EL, 2>(a, st); break;
+          case 3: attr = launch_skinny_t<MD, EL, 3>(a, st); break;
+          case 4: attr = launch_skinny_t<MD, EL, 4>(a, st); break;
+          default: attr = launch_skinny_t<MD, EL, 5>(a, st); break;
         }
       };
       if (mode == 0) go(std::integral_constant<int, 0>{});
@@ -470,24 +749,12 @@ int launch_skinny(int mode, int elt, const SkinnyPlan& p, const uint16_t* act, c
   if (attr != hipSuccess)
     return fail(REELS_HIP_EHIP, std::string("skinny_kernel: hipFuncSetAttribute: ") + hipGetErrorString(attr));
   if (int rc = check_launch("skinny_kernel")) return rc;
-  {
-    TraceScope _ts(st, mode == 0 ? "skinny_epilogue_kernel<0>" : "skinny_epilogue_kernel<1>");
-    const dim3 eg(adapter_only ? 1u : (unsigned)ceil_div(Ncols, 256), (unsigned)M);
-    const size_t lds = (size_t)(a.rp > 0 ? a.rp : 1) * 4;
-    with_elt(elt, [&](auto e) {
-      constexpr int EL = decltype(e)::value;
-      if (mode == 0)
-        skinny_epilogue_kernel<0, EL><<<eg, 256, lds, st>>>(part, p.S, M, Ncols, a.ldp, r, a.rp,
-                                                             colscale, R, ldr, bias, c,
-                                                             adapter_only ? nullptr : out, lsave,
-                                                             ld_lsave, lsave_cols);
-      else
-        skinny_epilogue_kernel<1, EL><<<eg, 256, lds, st>>>(part, p.S, M, Ncols, a.ldp, r, a.rp,
-                                                             colscale, R, ldr, bias, c, out, lsave,
-                                                             ld_lsave, lsave_cols);
-    });
+  if (shared) {
+    if ((e = hipEventRecord(tab.shared_ev, st)) != hipSuccess)
+      return fail(REELS_HIP_EHIP, std::string("skinny_kernel: hipEventRecord: ") + hipGetErrorString(e));
+    tab.shared_used = true;
   }
-  return check_launch("skinny_epilogue_kernel");
+  return REELS_HIP_OK;
 }
 
 }  // namespace reels

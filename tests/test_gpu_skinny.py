@@ -1,0 +1,109 @@
+"""The few-token path's single launch (reels_amd/csrc/skinny.hip): output tiles wait for the
+adapter's rank projection l, published by the adapter blocks of the same launch, and a tile that
+stops waiting computes l itself with the adapter blocks' code and order. Its counters live in
+per-stream slots that every launch leaves at zero.
+
+These tests force the fallback from the host (REELS_HIP_SKINNY_SPIN=0: no wait at all) and
+require the same bits as the normal run; run calls concurrently on several streams, more streams
+than there are slots (the shared slot orders its launches with an event), and repeat calls to show
+the counters return to zero. The parity of the values themselves against the oracle is in
+tests/test_gpu_configs.py (cross-attention shapes) and tests/test_gpu_lora.py."""
+import numpy as np
+import pytest
+
+import oracle
+from tests._util import assert_parity, bf16_f32, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(dev, M, K, N, r, seed, elt="bf16"):
+    import torch
+    from reels_amd import QuantizedMatrix
+    w = oracle.normal_bf16(seed, (N, K), 0.02)
+    q, s, st = oracle.pack(w, "bf16")
+    assert st == 0
+    x = oracle.normal_bf16(seed + 1, (M, K), 1.0)
+    A = oracle.normal_bf16(seed + 2, (K, r), 0.01)
+    B = oracle.normal_bf16(seed + 3, (r, N), 0.01)
+    dy = oracle.normal_bf16(seed + 4, (M, N), 1.0)
+    host = dict(x=x, q=q, s=s, A=A, B=B, dy=dy)
+    if elt == "bf16":
+        W = QuantizedMatrix(to_dev(q, dev, "raw"), to_dev(s, dev, "raw"))
+        put = lambda a: to_dev(a, dev)
+    else:
+        W = QuantizedMatrix(to_dev(q, dev, "raw"), to_dev(s, dev, "raw"), torch.float16)
+        put = lambda a: torch.from_numpy(oracle.bf16_to_f32(a)).to(torch.float16).to(dev)
+    devs = dict(x=put(x), A=put(A), B=put(B), dy=put(dy), W=W)
+    return host, devs
+
+
+def _run(d, c):
+    from reels_amd import i8lora_backward, i8lora_forward
+    y, h = i8lora_forward(d["x"], d["W"], d["A"], d["B"], None, c, save_h=True)
+    dx, dA, dB = i8lora_backward(d["dy"], d["x"], d["W"], d["A"], d["B"], c, h=None)
+    return y, h, dx, dA, dB
+
+
+@pytest.mark.parametrize("M,K,N,r", [(77, 5120, 5120, 32), (100, 1536, 1536, 24), (200, 1536, 1024, 8)])
+def test_output_tiles_computing_l_themselves_give_the_same_bits(dev, monkeypatch, M, K, N, r):
+    import torch
+    host, d = _case(dev, M, K, N, r, 4100 + M)
+    c = 2.0
+    print(f"[skinny] fallback M={M} K={K} N={N} r={r}", flush=True)
+    ref = _run(d, c)
+    torch.cuda.synchronize(dev)
+    monkeypatch.setenv("REELS_HIP_SKINNY_SPIN", "0")
+    for _ in range(2):
+        got = _run(d, c)
+        torch.cuda.synchronize(dev)
+        for name, a, b in zip(("y", "h", "dx", "dA", "dB"), ref, got):
+            assert torch.equal(a, b), f"{name} differs when output tiles compute l themselves"
+    monkeypatch.delenv("REELS_HIP_SKINNY_SPIN")
+    again = _run(d, c)
+    torch.cuda.synchronize(dev)
+    assert all(torch.equal(a, b) for a, b in zip(ref, again))
+    rows = np.arange(0, M, 7)
+    yo, ho = oracle.lora_forward(host["x"], host["q"], host["s"], host["A"], host["B"], c, rows=rows)
+    assert_parity(bf16_f32(got[0])[rows], yo, f"fallback M={M} y")
+
+
+def test_concurrent_streams_and_the_shared_slot(dev):
+    """Calls on 70 streams at once (more than the 63 per-stream slots of a device): every result
+    equals the same call made alone on the default stream."""
+    import torch
+    from reels_amd import i8lora_forward
+    M, K, N, r, c = 77, 1536, 1536, 16, 1.0
+    cases = [_case(dev, M, K, N, r, 4300 + 10 * i)[1] for i in range(4)]
+    print("[skinny] 70 streams", flush=True)
+    ref = []
+    for d in cases:
+        y, h = i8lora_forward(d["x"], d["W"], d["A"], d["B"], None, c, save_h=True)
+        ref.append((y, h))
+    torch.cuda.synchronize(dev)
+    streams = [torch.cuda.Stream(device=dev) for _ in range(70)]
+    outs = []
+    for rep in range(2):
+        for i, st in enumerate(streams):
+            d = cases[i % len(cases)]
+            st.wait_stream(torch.cuda.current_stream(dev))
+            with torch.cuda.stream(st):
+                outs.append((i % len(cases), *i8lora_forward(d["x"], d["W"], d["A"], d["B"], None, c,
+                                                            save_h=True)))
+    torch.cuda.synchronize(dev)
+    for k, y, h in outs:
+        assert torch.equal(y, ref[k][0]) and torch.equal(h, ref[k][1])
+
+
+def test_f16_fallback_and_repeat(dev, monkeypatch):
+    import torch
+    host, d = _case(dev, 77, 1536, 1536, 32, 4500, "f16")
+    c = 0.5
+    print("[skinny] f16 fallback", flush=True)
+    ref = _run(d, c)
+    torch.cuda.synchronize(dev)
+    monkeypatch.setenv("REELS_HIP_SKINNY_SPIN", "0")
+    got = _run(d, c)
+    torch.cuda.synchronize(dev)
+    for name, a, b in zip(("y", "h", "dx", "dA", "dB"), ref, got):
+        assert torch.equal(a, b), f"f16 {name} differs when output tiles compute l themselves"
