@@ -89,7 +89,7 @@ struct SkBlock {
 };
 
 // dynamic LDS: the waves' staging areas during the loop, the 4 wave sums (4 x 4T fragments of 1 KiB)
-// after it; the last 16 bytes hold the block's arrival count and wait result (written and read
+// after it; the last 16 bytes hold the block's arrival count and ready flag (written and read
 // after the sums are read; for T = 1 they get 16 bytes of their own)
 static constexpr int skinny_lds(int T) {
   return (4 * 4 * T * 64 * 16) > 4 * sk::STAGE ? (4 * 4 * T * 64 * 16) : 4 * sk::STAGE + 16;
@@ -196,25 +196,29 @@ __device__ __forceinline__ void skinny_acc(const SkArgs& a, int blk, int sp, int
         : MODE == 0            ? (uint32_t)(sk::KC * a.rp * 2)
                                : (uint32_t)(sk::KC * 2);
 
-  struct Stage {
+  struct WStage {
     u32x4 wq[NWL];
-    u32x4 x[T][2];
     f32x4 sc[NSC];  // DX: s[n] for n = 32 e + 8 g + (0..7), [2 e + half]
   };
-  Stage st0, st1;
+  struct XStage {
+    u32x4 x[T][2];
+  };
   // valid = false (a step past the wave's run): every offset of the step moves past its
   // descriptor, so the step reads zeros and adds nothing (no branch around the loads or the
   // multiply, which keeps the compiler's waits exact)
-  auto load = [&](int c, bool valid, Stage& s) {
-    const uint32_t sw = (uint32_t)c * wstep, sx = (uint32_t)c * (uint32_t)(sk::KC * 2);
-#pragma unroll
-    for (int i = 0; i < NWL; ++i)
-      s.wq[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, valid ? vw[i] : OOB, sw, !lora ? 2 : 0));
+  auto load_x = [&](int c, bool valid, XStage& s) {
+    const uint32_t sx = (uint32_t)c * (uint32_t)(sk::KC * 2);
 #pragma unroll
     for (int tt = 0; tt < T; ++tt)
 #pragma unroll
       for (int e = 0; e < 2; ++e)
         s.x[tt][e] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, valid ? vx[tt][e] : OOB, sx, 0));
+  };
+  auto load_w = [&](int c, bool valid, WStage& s) {
+    const uint32_t sw = (uint32_t)c * wstep;
+#pragma unroll
+    for (int i = 0; i < NWL; ++i)
+      s.wq[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, valid ? vw[i] : OOB, sw, !lora ? 2 : 0));
     if constexpr (MODE == 1 && !lora) {  // the scales of a zero step multiply zeros
       const float* sp8 = a.s + (int64_t)c * sk::KC + 8 * g;
 #pragma unroll
@@ -231,7 +235,7 @@ __device__ __forceinline__ void skinny_acc(const SkArgs& a, int blk, int sp, int
     for (int tt = 0; tt < T; ++tt) acc[i][tt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
   uint8_t* wst = smem + w * sk::STAGE;  // this wave's staging area
-  auto compute = [&](const Stage& s) {
+  auto compute = [&](const WStage& s, const XStage& xs) {
     V8 af[NI][2];
     if constexpr (!lora && MODE == 0) {
 #pragma unroll
@@ -301,7 +305,7 @@ __device__ __forceinline__ void skinny_acc(const SkArgs& a, int blk, int sp, int
     for (int e = 0; e < 2; ++e)
 #pragma unroll
       for (int tt = 0; tt < T; ++tt) {
-        const V8 xf = E::as8(s.x[tt][e]);
+        const V8 xf = E::as8(xs.x[tt][e]);
 #pragma unroll
         for (int i = 0; i < NI; ++i) acc[i][tt] = E::mfma16(af[i][e], xf, acc[i][tt]);
       }
@@ -321,21 +325,53 @@ __device__ __forceinline__ void skinny_acc(const SkArgs& a, int blk, int sp, int
     const int p = rot + i;
     return i < nw ? wb + (p < nw ? p : p - nw) : c0;
   };
-  // (scheduling barriers keep each stage's loads together and in program order, so the waits at
-  // the loop head only cover the older stage)
-  load(chunk(0), 0 < nw, st0);
-  __builtin_amdgcn_sched_barrier(0);
-  load(chunk(1), 1 < nw, st1);
-  __builtin_amdgcn_sched_barrier(0);
-  for (int i = 0; i < nw; i += 2) {
-    compute(st0);
+  // (scheduling barriers keep each step's loads together and in program order, so the waits
+  // before a multiply cover exactly its own operands)
+  if constexpr (MODE == 0 && !lora) {
+    // the forward's weight stream runs DW steps ahead; the activations (cache hits) one step
+    // ahead, issued before the weight refill so that waiting for them never waits for it
+    constexpr int DW = 4;
+    WStage ws[DW];
+    XStage xs[2];
+#pragma unroll
+    for (int j = 0; j < DW; ++j) {
+      load_w(chunk(j), j < nw, ws[j]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    load_x(chunk(0), 0 < nw, xs[0]);
     __builtin_amdgcn_sched_barrier(0);
-    load(chunk(i + 2), i + 2 < nw, st0);
+    for (int i = 0; i < nw; i += DW) {
+#pragma unroll
+      for (int j = 0; j < DW; ++j) {
+        load_x(chunk(i + j + 1), i + j + 1 < nw, xs[(j + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(ws[j], xs[j & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+        load_w(chunk(i + j + DW), i + j + DW < nw, ws[j]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  } else {
+    WStage w0, w1;
+    XStage x0, x1;
+    load_w(chunk(0), 0 < nw, w0);
+    load_x(chunk(0), 0 < nw, x0);
     __builtin_amdgcn_sched_barrier(0);
-    compute(st1);
+    load_w(chunk(1), 1 < nw, w1);
+    load_x(chunk(1), 1 < nw, x1);
     __builtin_amdgcn_sched_barrier(0);
-    load(chunk(i + 3), i + 3 < nw, st1);
-    __builtin_amdgcn_sched_barrier(0);
+    for (int i = 0; i < nw; i += 2) {
+      compute(w0, x0);
+      __builtin_amdgcn_sched_barrier(0);
+      load_w(chunk(i + 2), i + 2 < nw, w0);
+      load_x(chunk(i + 2), i + 2 < nw, x0);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(w1, x1);
+      __builtin_amdgcn_sched_barrier(0);
+      load_w(chunk(i + 3), i + 3 < nw, w1);
+      load_x(chunk(i + 3), i + 3 < nw, x1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
 }
 
@@ -363,6 +399,7 @@ __device__ __forceinline__ void skinny_sum(const f32x4 (&acc)[NI][T], uint8_t* s
       sum[k] = ((red[f * 64 + lane] + red[(NF + f) * 64 + lane]) + red[(2 * NF + f) * 64 + lane]) +
                red[(3 * NF + f) * 64 + lane];
   }
+  __syncthreads();  // LDS free again
 }
 
 // l = rnd(sum) of an adapter tile (rows j = o0 + 16 i + 4 g + v of fragment (i, tt), token
@@ -416,9 +453,28 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
     skinny_acc<T, MODE, ELT, LORA>(a, blk, sp, tok0, smem, acc);
     skinny_sum<T, NI>(acc, smem, sum);
   }
-
-  uint32_t& bc = reinterpret_cast<uint32_t*>(smem + skinny_lds(T) - 16)[1];
+  uint32_t* words = reinterpret_cast<uint32_t*>(smem + skinny_lds(T) - 16);  // [1] arrivals, [2] l ready
   SkSlot* slot = a.slot;
+  const __amdgpu_buffer_rsrc_t rl = sk_rsrc(a.hl, a.M * a.rp * 2);
+  // Output tiles of a launch with an adapter look at the ready flag now (each wave reads it; the
+  // flag only goes up during the launch) and, when it is up, load their tokens' l for the first 32
+  // rank columns while the partial is handed over.
+  const bool wants_l = !lora && a.nad > 0;
+  uint32_t up = 0;
+  if (wants_l) up = sk_load(&slot->hready);
+  u32x4 hv[FPW];  // B operand of the l R product: l[tok][j .. j + 7], j = 8 g (first rank chunk)
+  auto load_l = [&](int j0, u32x4 (&dst)[FPW]) {
+#pragma unroll
+    for (int k = 0; k < FPW; ++k) {
+      const int f = w + 4 * k;
+      const int64_t tok = tok0 + 16 * (f % T) + l16;
+      const int jj = j0 + 8 * g;
+      dst[k] = u32x4{0u, 0u, 0u, 0u};
+      if (f < NF && tok < a.M && jj < a.rp)
+        dst[k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                               rl, (uint32_t)((tok * a.rp + jj) * 2), 0, kSC1));
+    }
+  };
   if (a.S > 1) {
     // partial [tile][split][fragment][lane] (16 bytes); output tiles first, then adapter tiles
     const int64_t tbase = lora ? (int64_t)a.ntm * a.S * (4 * T * 64) + (int64_t)(d.tile - a.ntm) * a.S * (NF * 64)
@@ -432,20 +488,21 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
                                                (uint32_t)((sp * (NF * 64) + f * 64 + lane) * 16), 0, kSC1);
     }
     sk_drain();
+    if (wants_l && up) load_l(0, hv);
     __syncthreads();
     if (t == 0) {
       const uint32_t old = sk_add(&slot->tile[d.tile], 1u);
       if (old == (uint32_t)a.S - 1) sk_store(&slot->tile[d.tile], 0u);
-      bc = old;
+      words[1] = old;
     }
     __syncthreads();
-    if (bc != (uint32_t)a.S - 1) return;
+    if (words[1] != (uint32_t)a.S - 1) return;
     asm volatile("" ::: "memory");
-    // the tile's sum in split order, SB splits' loads in flight at a time
+    // the tile's sum in split order: the other splits' partials in one batch (up to SB splits)
+    constexpr int SB = 4;
     f32x4 tot[FPW];
 #pragma unroll
     for (int k = 0; k < FPW; ++k) tot[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    constexpr int SB = FPW > 3 ? 2 : 4;
     for (int s0 = 0; s0 < a.S; s0 += SB) {
       f32x4 v[SB][FPW];
 #pragma unroll
@@ -470,9 +527,9 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
   } else {
 #pragma unroll
     for (int k = 0; k < FPW; ++k) sum[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f} + sum[k];
+    if (wants_l && up) load_l(0, hv);
   }
 
-  const __amdgpu_buffer_rsrc_t rl = sk_rsrc(a.hl, a.M * a.rp * 2);
   if constexpr (lora) {
     skinny_put_l<T, ELT>(a, o0, tok0, sum, true);
     sk_drain();
@@ -492,15 +549,17 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
     // wait (a grid that cannot be resident at once, behind other work), the block computes l for
     // its tokens itself, with the adapter blocks' code, splits and order, so the values are the
     // same bits either way.
-    if (a.nad > 0) {
-      uint32_t& up = reinterpret_cast<uint32_t*>(smem + skinny_lds(T) - 16)[2];
+    if (wants_l) {
       if (t == 0) {
-        uint32_t n = 0, v;
-        while ((v = sk_load(&slot->hready)) == 0u && ++n <= a.spin) __builtin_amdgcn_s_sleep(8);
-        up = v;
+        uint32_t n = 0, v = up;
+        while (v == 0u && ++n <= a.spin) {
+          __builtin_amdgcn_s_sleep(8);
+          v = sk_load(&slot->hready);
+        }
+        words[2] = v;
       }
       __syncthreads();
-      if (up == 0u) {
+      if (words[2] == 0u) {
         for (int lb = 0; lb < a.lblk; ++lb) {
           f32x4 tl[(2 * T + 3) / 4];
 #pragma unroll
@@ -518,16 +577,18 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
         __syncthreads();
       }
       asm volatile("" ::: "memory");
+      if (!up) load_l(0, hv);  // the waves that found the flag down load l now
     }
     // lo = l R for this tile on the MFMA, 32 rank columns per step: A operand rows o = 16 i + l16
     // with j = 32 jc + 8 g + (0..7), B operand the tokens' l[tok][j .. j + 7]
     f32x4 lo[FPW];
 #pragma unroll
     for (int k = 0; k < FPW; ++k) lo[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    const int njc = a.nad > 0 ? (a.rp + 31) / 32 : 0;
+    const int njc = wants_l ? (a.rp + 31) / 32 : 0;
     uint16_t* rst = reinterpret_cast<uint16_t*>(smem);  // FWD: R rows [32 j][64 o]
     for (int jc = 0; jc < njc; ++jc) {
       const int j0 = 32 * jc;
+      if (jc > 0) load_l(j0, hv);
       if constexpr (MODE == 0) {
         __syncthreads();
         {
@@ -542,7 +603,7 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
       for (int k = 0; k < FPW; ++k) {
         const int f = w + 4 * k;
         if (f >= NF) continue;
-        const int i = f / T, tt = f % T;
+        const int i = f / T;
         u32x4 av;
         if constexpr (MODE == 0) {
           // transposed 16-bit reads: providing lane p addresses row 8 g + 4 h + p / 4, columns
@@ -559,13 +620,7 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
           av = jj < a.rp ? *reinterpret_cast<const u32x4*>(a.R + (o0 + 16 * i + l16) * a.ldr + jj)
                          : u32x4{0u, 0u, 0u, 0u};
         }
-        const int64_t tok = tok0 + 16 * tt + l16;
-        const int jj = j0 + 8 * g;
-        const u32x4 bv = (tok < a.M && jj < a.rp)
-                             ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                             rl, (uint32_t)((tok * a.rp + jj) * 2), 0, kSC1))
-                             : u32x4{0u, 0u, 0u, 0u};
-        lo[k] = E::mfma16(E::as8(av), E::as8(bv), lo[k]);
+        lo[k] = E::mfma16(E::as8(av), E::as8(hv[k]), lo[k]);
       }
     }
     // out = rnd(scale * sum + c * lo + bias) for rows o = o0 + 16 i + 4 g + v, token 16 tt + l16
@@ -576,21 +631,22 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
       const int i = f / T, tt = f % T;
       const int64_t tok = tok0 + 16 * tt + l16, o = o0 + 16 * i + 4 * g;
       if (tok >= a.M) continue;
+      const f32x4 cs = a.colscale ? *reinterpret_cast<const f32x4*>(a.colscale + o) : f32x4{1.0f, 1.0f, 1.0f, 1.0f};
       uint32_t b[4];
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const float sc = a.colscale ? a.colscale[o + v] * sum[k][v] : sum[k][v];
+        const float sc = a.colscale ? cs[v] * sum[k][v] : sum[k][v];
         const float bs = a.bias ? E::to_f32(a.bias[o + v]) : 0.0f;
         b[v] = E::bits(sc + a.c * lo[k][v] + bs);
       }
       *reinterpret_cast<uint2*>(a.out + tok * a.Ncols + o) = uint2{b[0] | (b[1] << 16), b[2] | (b[3] << 16)};
     }
-    if (a.nad > 0 && t == 0) skinny_finish(a);
+    if (wants_l && t == 0) skinny_finish(a);
   }
 }
 
 template <int T, int MODE, int ELT>
-__global__ __launch_bounds__(256, 2) void skinny_kernel(SkArgs a) {
+__global__ __launch_bounds__(256, T >= 4 ? 1 : 2) void skinny_kernel(SkArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   // grid order: adapter blocks, then output blocks; within each (row block, split, token block)
   // with the token block fastest, so blocks that read the same weight rows start together
