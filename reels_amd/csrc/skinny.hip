@@ -7,7 +7,7 @@
 //
 // One launch does everything. A block is (tile, split): a tile is 64 output rows (or 32 rows of
 // the adapter's rank projection) x up to 16T tokens, a split a contiguous range of 64-wide
-// reduction chunks. The block's 4 waves each take a quarter of the split's chunks; their
+// reduction chunks. The block's 8 waves each take an eighth of the split's chunks; their
 // accumulators are summed in LDS in wave order. With more than one split the block stores that
 // sum as an f32 partial and counts itself in on the tile; the block that arrives last sums the
 // tile's partials in split order (its own from registers) and finishes the tile:
@@ -45,6 +45,7 @@ constexpr int KC = 64;       // reduction chunk
 constexpr int MAXT = 5;      // token tiles of 16 per block (80 tokens)
 constexpr int MAXS = 8;      // reduction splits
 constexpr int STAGE = 4096;  // per-wave LDS staging (DX weight tile, FWD adapter chunk: 4 KiB each)
+constexpr int NWV = 8;       // waves per block (two per SIMD)
 constexpr int kSlots = 64;   // counter slots per device: one per stream, the last one shared
 constexpr int kMaxTiles = 4096;
 constexpr uint32_t kSpinLimit = 1u << 12;  // wait rounds of s_sleep 8 (about 1 ms) before computing l
@@ -88,11 +89,10 @@ struct SkBlock {
   int blk, sp, tb, tile;  // blk >= nblk: adapter row block blk - nblk
 };
 
-// dynamic LDS: the waves' staging areas during the loop, the 4 wave sums (4 x 4T fragments of 1 KiB)
-// after it; the last 16 bytes hold the block's arrival count and ready flag (written and read
-// after the sums are read; for T = 1 they get 16 bytes of their own)
+// dynamic LDS: the waves' staging areas during the loop, 4 wave sums (4 x 4T fragments of 1 KiB)
+// after it, then 16 bytes for the block's arrival count and ready flag
 static constexpr int skinny_lds(int T) {
-  return (4 * 4 * T * 64 * 16) > 4 * sk::STAGE ? (4 * 4 * T * 64 * 16) : 4 * sk::STAGE + 16;
+  return ((4 * 4 * T * 64 * 16) > sk::NWV * sk::STAGE ? (4 * 4 * T * 64 * 16) : sk::NWV * sk::STAGE) + 16;
 }
 
 // Data one block hands to another (split partials, l) is stored and loaded with device-scope
@@ -128,7 +128,7 @@ __device__ __forceinline__ void skinny_finish(const SkArgs& a) {
 }
 
 // One wave's share of a (row block, split, token block): acc[i][tt] = rows 16 i + (0..15) x tokens
-// 16 tt + (0..15) over the wave's quarter of the split's chunks. LORA: a block of the adapter's
+// 16 tt + (0..15) over the wave's eighth of the split's chunks. LORA: a block of the adapter's
 // rank projection (rows j of A^T in the forward, of B for dX) rather than of the int8 weight.
 template <int T, int MODE, int ELT, bool LORA>
 __device__ __forceinline__ void skinny_acc(const SkArgs& a, int blk, int sp, int64_t tok0,
@@ -311,89 +311,114 @@ __device__ __forceinline__ void skinny_acc(const SkArgs& a, int blk, int sp, int
       }
   };
 
-  // Wave w takes a contiguous quarter of the split's chunks (each weight row read sequentially)
-  // and walks it from a rotation that depends on the logical block: rows of the weight (and of
-  // the activations) lie a multiple of 1 KiB apart, so blocks that walked the same k offsets at
-  // the same time would pile onto a few memory channels. Two register stages: the copies of step
-  // i + 2 are issued while step i is multiplied; steps past the wave's run read zeros (the steps
-  // come in pairs).
-  const int q = (c1 - c0 + 3) / 4;
-  const int wb = c0 + w * q;
-  const int nw = (wb + q < c1 ? wb + q : c1) - wb;
+  // The split's chunks go round by round: in round rr the block's 8 waves take the 8 consecutive
+  // chunks c0 + 8 rr + w, so at any time the block streams one 512-byte stretch of each of its 64
+  // weight rows (DRAM pages stay open) and each wave owns a fixed residue of the chunk index. The
+  // rounds start at a rotation that depends on the block: rows of the weight (and of the
+  // activations) lie a multiple of 1 KiB apart, so blocks that walked the same k offsets at the
+  // same time would pile onto a few memory channels. Slots past the split (the last round) read
+  // zeros and add nothing.
+  const int nk = c1 - c0;
+  const int nw = (nk + sk::NWV - 1) / sk::NWV;  // rounds, the same for every wave
   const int rot = nw > 0 ? (int)(((int64_t)blk * 5 + (int64_t)tok0 / 16 * 3) % nw) : 0;
-  auto chunk = [&](int i) {
+  auto round_of = [&](int i) {
     const int p = rot + i;
-    return i < nw ? wb + (p < nw ? p : p - nw) : c0;
+    return p < nw ? p : p - nw;
   };
+  auto valid = [&](int i) { return i < nw && sk::NWV * round_of(i) + w < nk; };
+  // an empty slot names the split's first chunk: every address formed from it stays in bounds
+  // (dX reads its scales with plain loads; its zero weights then multiply them)
+  auto chunk = [&](int i) { return valid(i) ? c0 + sk::NWV * round_of(i) + w : c0; };
   // (scheduling barriers keep each step's loads together and in program order, so the waits
   // before a multiply cover exactly its own operands)
   if constexpr (MODE == 0 && !lora) {
     // the forward's weight stream runs DW steps ahead; the activations (cache hits) one step
     // ahead, issued before the weight refill so that waiting for them never waits for it
-    constexpr int DW = 4;
+    constexpr int DW = 2;
     WStage ws[DW];
     XStage xs[2];
 #pragma unroll
     for (int j = 0; j < DW; ++j) {
-      load_w(chunk(j), j < nw, ws[j]);
+      load_w(chunk(j), valid(j), ws[j]);
       __builtin_amdgcn_sched_barrier(0);
     }
-    load_x(chunk(0), 0 < nw, xs[0]);
+    load_x(chunk(0), valid(0), xs[0]);
     __builtin_amdgcn_sched_barrier(0);
     for (int i = 0; i < nw; i += DW) {
 #pragma unroll
       for (int j = 0; j < DW; ++j) {
-        load_x(chunk(i + j + 1), i + j + 1 < nw, xs[(j + 1) & 1]);
+        load_x(chunk(i + j + 1), valid(i + j + 1), xs[(j + 1) & 1]);
         __builtin_amdgcn_sched_barrier(0);
         compute(ws[j], xs[j & 1]);
         __builtin_amdgcn_sched_barrier(0);
-        load_w(chunk(i + j + DW), i + j + DW < nw, ws[j]);
+        load_w(chunk(i + j + DW), valid(i + j + DW), ws[j]);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
   } else {
+    // dX and the adapter blocks: the weight (with dX's scales) two steps ahead, the activations
+    // loaded at the start of their step (the other wave of the SIMD covers that wait)
     WStage w0, w1;
-    XStage x0, x1;
-    load_w(chunk(0), 0 < nw, w0);
-    load_x(chunk(0), 0 < nw, x0);
+    XStage x0;
+    load_w(chunk(0), valid(0), w0);
     __builtin_amdgcn_sched_barrier(0);
-    load_w(chunk(1), 1 < nw, w1);
-    load_x(chunk(1), 1 < nw, x1);
+    load_w(chunk(1), valid(1), w1);
     __builtin_amdgcn_sched_barrier(0);
     for (int i = 0; i < nw; i += 2) {
+      load_x(chunk(i), valid(i), x0);
+      __builtin_amdgcn_sched_barrier(0);
       compute(w0, x0);
       __builtin_amdgcn_sched_barrier(0);
-      load_w(chunk(i + 2), i + 2 < nw, w0);
-      load_x(chunk(i + 2), i + 2 < nw, x0);
+      load_w(chunk(i + 2), valid(i + 2), w0);
       __builtin_amdgcn_sched_barrier(0);
-      compute(w1, x1);
+      load_x(chunk(i + 1), valid(i + 1), x0);
       __builtin_amdgcn_sched_barrier(0);
-      load_w(chunk(i + 3), i + 3 < nw, w1);
-      load_x(chunk(i + 3), i + 3 < nw, x1);
+      compute(w1, x0);
+      __builtin_amdgcn_sched_barrier(0);
+      load_w(chunk(i + 3), valid(i + 3), w1);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
 }
 
-// The block's sum of its 4 waves' accumulators: the wave sums go to LDS as MFMA fragments (wave w,
-// fragment f = i T + tt, lane) and are summed in wave order by the wave that owns the fragment
-// afterwards: wave w owns f = w, w + 4, ... with the same lane slot (each thread reads and writes
-// 16 consecutive bytes per fragment).
+// The block's sum of its 8 waves' accumulators, in a fixed order: waves 4-7 hand theirs to waves
+// 0-3 through LDS (p_w = acc_w + acc_{w+4}), then the four p_w go to LDS as MFMA fragments (wave,
+// fragment f = i T + tt, lane) and are summed in wave order, ((p0 + p1) + p2) + p3, by the wave that
+// owns the fragment: wave w owns f = w, w + 8, ... with the same lane slot (each thread reads and
+// writes 16 consecutive bytes per fragment).
+template <int NF> constexpr int sk_fpw() { return (NF + sk::NWV - 1) / sk::NWV; }
+
 template <int T, int NI>
-__device__ __forceinline__ void skinny_sum(const f32x4 (&acc)[NI][T], uint8_t* smem,
-                                           f32x4 (&sum)[(NI * T + 3) / 4]) {
-  constexpr int NF = NI * T, FPW = (NF + 3) / 4;
+__device__ __forceinline__ void skinny_sum(f32x4 (&acc)[NI][T], uint8_t* smem,
+                                           f32x4 (&sum)[sk_fpw<NI * T>()]) {
+  constexpr int NF = NI * T, FPW = sk_fpw<NF>();
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  __syncthreads();
   f32x4* red = reinterpret_cast<f32x4*>(smem);
+  __syncthreads();
+  if (w >= 4) {
 #pragma unroll
-  for (int i = 0; i < NI; ++i)
+    for (int i = 0; i < NI; ++i)
 #pragma unroll
-    for (int tt = 0; tt < T; ++tt) red[(w * NF + i * T + tt) * 64 + lane] = acc[i][tt];
+      for (int tt = 0; tt < T; ++tt) red[((w - 4) * NF + i * T + tt) * 64 + lane] = acc[i][tt];
+  }
+  __syncthreads();
+  if (w < 4) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+      for (int tt = 0; tt < T; ++tt) acc[i][tt] += red[(w * NF + i * T + tt) * 64 + lane];
+  }
+  __syncthreads();
+  if (w < 4) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+      for (int tt = 0; tt < T; ++tt) red[(w * NF + i * T + tt) * 64 + lane] = acc[i][tt];
+  }
   __syncthreads();
 #pragma unroll
   for (int k = 0; k < FPW; ++k) {
-    const int f = w + 4 * k;
+    const int f = w + sk::NWV * k;
     sum[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     if (f < NF)
       sum[k] = ((red[f * 64 + lane] + red[(NF + f) * 64 + lane]) + red[(2 * NF + f) * 64 + lane]) +
@@ -406,15 +431,15 @@ __device__ __forceinline__ void skinny_sum(const f32x4 (&acc)[NI][T], uint8_t* s
 // 16 tt + l16) into hl (device scope) and, with lsave set, into lsave
 template <int T, int ELT>
 __device__ __forceinline__ void skinny_put_l(const SkArgs& a, int64_t o0, int64_t tok0,
-                                             const f32x4 (&sum)[(2 * T + 3) / 4], bool lsave) {
+                                             const f32x4 (&sum)[sk_fpw<2 * T>()], bool lsave) {
   using E = Elt<ELT>;
-  constexpr int NF = 2 * T, FPW = (NF + 3) / 4;
+  constexpr int NF = 2 * T, FPW = sk_fpw<NF>();
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l16 = lane & 15, g = lane >> 4;
   const __amdgpu_buffer_rsrc_t rl = sk_rsrc(a.hl, a.M * a.rp * 2);
 #pragma unroll
   for (int k = 0; k < FPW; ++k) {
-    const int f = w + 4 * k;
+    const int f = w + sk::NWV * k;
     if (f >= NF) continue;
     const int i = f / T, tt = f % T;
     const int64_t tok = tok0 + 16 * tt + l16, j = o0 + 16 * i + 4 * g;
@@ -446,7 +471,7 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
   const int64_t tok0 = (int64_t)d.tb * (16 * T);
   constexpr int NI = lora ? 2 : 4;
   const int64_t o0 = lora ? (int64_t)(blk - a.nblk) * sk::NBL : (int64_t)blk * sk::NB;
-  constexpr int NF = NI * T, FPW = (NF + 3) / 4;
+  constexpr int NF = NI * T, FPW = sk_fpw<NF>();
   f32x4 sum[FPW];
   {
     f32x4 acc[NI][T];
@@ -466,7 +491,7 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
   auto load_l = [&](int j0, u32x4 (&dst)[FPW]) {
 #pragma unroll
     for (int k = 0; k < FPW; ++k) {
-      const int f = w + 4 * k;
+      const int f = w + sk::NWV * k;
       const int64_t tok = tok0 + 16 * (f % T) + l16;
       const int jj = j0 + 8 * g;
       dst[k] = u32x4{0u, 0u, 0u, 0u};
@@ -482,7 +507,7 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
     const __amdgpu_buffer_rsrc_t rp_ = sk_rsrc(reinterpret_cast<f32x4*>(a.part) + tbase, (int64_t)a.S * NF * 64 * 16);
 #pragma unroll
     for (int k = 0; k < FPW; ++k) {
-      const int f = w + 4 * k;
+      const int f = w + sk::NWV * k;
       if (f < NF)
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sum[k]), rp_,
                                                (uint32_t)((sp * (NF * 64) + f * 64 + lane) * 16), 0, kSC1);
@@ -509,7 +534,7 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
       for (int u = 0; u < SB; ++u)
 #pragma unroll
         for (int k = 0; k < FPW; ++k) {
-          const int f = w + 4 * k, s = s0 + u;
+          const int f = w + sk::NWV * k, s = s0 + u;
           v[u][k] = sum[k];
           if (f < NF && s < a.S && s != sp)
             v[u][k] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
@@ -561,15 +586,16 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
       __syncthreads();
       if (words[2] == 0u) {
         for (int lb = 0; lb < a.lblk; ++lb) {
-          f32x4 tl[(2 * T + 3) / 4];
+          constexpr int FA = sk_fpw<2 * T>();
+          f32x4 tl[FA];
 #pragma unroll
-          for (int k = 0; k < (2 * T + 3) / 4; ++k) tl[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+          for (int k = 0; k < FA; ++k) tl[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
           for (int s = 0; s < a.S; ++s) {
-            f32x4 acc[2][T], ps[(2 * T + 3) / 4];
+            f32x4 acc[2][T], ps[FA];
             skinny_acc<T, MODE, ELT, true>(a, a.nblk + lb, s, tok0, smem, acc);
             skinny_sum<T, 2>(acc, smem, ps);
 #pragma unroll
-            for (int k = 0; k < (2 * T + 3) / 4; ++k) tl[k] += ps[k];
+            for (int k = 0; k < FA; ++k) tl[k] += ps[k];
           }
           skinny_put_l<T, ELT>(a, (int64_t)lb * sk::NBL, tok0, tl, false);
         }
@@ -591,7 +617,7 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
       if (jc > 0) load_l(j0, hv);
       if constexpr (MODE == 0) {
         __syncthreads();
-        {
+        if (t < 256) {
           const int row = t >> 3, col = 8 * (t & 7);
           u32x4 v = u32x4{0u, 0u, 0u, 0u};
           if (j0 + row < a.r) v = *reinterpret_cast<const u32x4*>(a.R + (int64_t)(j0 + row) * a.ldr + o0 + col);
@@ -601,7 +627,7 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
       }
 #pragma unroll
       for (int k = 0; k < FPW; ++k) {
-        const int f = w + 4 * k;
+        const int f = w + sk::NWV * k;
         if (f >= NF) continue;
         const int i = f / T;
         u32x4 av;
@@ -626,7 +652,7 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
     // out = rnd(scale * sum + c * lo + bias) for rows o = o0 + 16 i + 4 g + v, token 16 tt + l16
 #pragma unroll
     for (int k = 0; k < FPW; ++k) {
-      const int f = w + 4 * k;
+      const int f = w + sk::NWV * k;
       if (f >= NF) continue;
       const int i = f / T, tt = f % T;
       const int64_t tok = tok0 + 16 * tt + l16, o = o0 + 16 * i + 4 * g;
@@ -646,7 +672,7 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
 }
 
 template <int T, int MODE, int ELT>
-__global__ __launch_bounds__(256, T >= 4 ? 1 : 2) void skinny_kernel(SkArgs a) {
+__global__ __launch_bounds__(64 * sk::NWV, 1) void skinny_kernel(SkArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   // grid order: adapter blocks, then output blocks; within each (row block, split, token block)
   // with the token block fastest, so blocks that read the same weight rows start together
@@ -717,7 +743,7 @@ static hipError_t launch_skinny_t(const SkArgs& a, hipStream_t st) {
                                hipFuncAttributeMaxDynamicSharedMemorySize, skinny_lds(T));
   });
   if (attr != hipSuccess) return attr;
-  skinny_kernel<T, MODE, ELT><<<dim3((unsigned)a.blocks), 256, skinny_lds(T), st>>>(a);
+  skinny_kernel<T, MODE, ELT><<<dim3((unsigned)a.blocks), 64 * sk::NWV, skinny_lds(T), st>>>(a);
   return hipSuccess;
 }
 
