@@ -77,6 +77,12 @@ def parse():
     ap.add_argument("--attention-only", action="store_true",
                     help="run only the attention workload")
     ap.add_argument("--pack-only", action="store_true", help="run only the pack workload")
+    ap.add_argument("--configs-only", default=None,
+                    help="run only these config lines (comma-separated, e.g. cfg5a) and exit")
+    ap.add_argument("--trace", choices=("gemm", "all"), default="gemm",
+                    help="kernels bracketed by HIP events inside the timed steps: the GEMMs only "
+                         "(their durations give roofline.achieved; the per-kernel breakdown comes "
+                         "from one extra untimed step with every kernel traced) or every kernel")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run three 1 GiB device-to-device copies (the reference kernel for "
                          "scaling FETCH_SIZE / WRITE_SIZE counters to bytes) and exit")
@@ -520,7 +526,7 @@ class Chain:
             check("reels_hip_i8lora_bwd", L.reels_hip_i8lora_bwd(*args))
 
 
-def configs_bench(dev, L, check):
+def configs_bench(dev, L, check, which=("cfg1", "cfg2", "cfg4", "cfg5a")):
     """The other BASELINE workloads on this GPU, each as TFLOP/s of forward + dX + dA + dB
     (4MNK + 6Mr(K+N) per linear): config 1 (one 1536 x 1536 linear, 1024 tokens, r 16, alpha 16),
     config 2 (the six Wan-2.1-1.3B block projections at 32760 tokens), config 4 (the 30-layer
@@ -529,13 +535,32 @@ def configs_bench(dev, L, check):
     import torch
     out = {}
     gen = torch.Generator(device=dev).manual_seed(99)
+    if "cfg1" in which:
+        out.update(_cfg1(dev, L, check, gen))
+    if "cfg2" in which:
+        out.update(_cfg2(dev, L, check, gen))
+    if "cfg4" in which:
+        out.update(_cfg4(dev, L, check, gen))
+    if "cfg5a" in which:
+        out.update(_cfg5a(dev, L, check, gen))
+    torch.cuda.empty_cache()
+    return out
+
+
+def _cfg1(dev, L, check, gen):
+    out = {}
     pr = Projection("cfg1", 1536, 1536, 1024, 16, dev, gen, alpha=16.0)
     ms = _time_ms(lambda: run_step(L, [pr], check), reps=200, warmup=5)
     f = linear_flops(1024, 1536, 1536, 16)
     out["cfg1"] = {"what": "one int8 LoRA linear 1536 -> 1536, 1024 tokens, r 16, alpha 16, "
                            "fwd + dX + dA + dB", "ms": round(ms, 4),
                    "tflops": round(f / (ms * 1e-3) / 1e12, 1)}
-    del pr
+    return out
+
+
+def _cfg2(dev, L, check, gen):
+    import torch
+    out = {}
     projs = [Projection(n, K, N, TOKENS, RANK, dev, gen) for (n, K, N) in PROJECTIONS_13B]
     ms = _time_ms(lambda: run_step(L, projs, check), reps=10)
     f = sum(linear_flops(TOKENS, K, N, RANK) for (_, K, N) in PROJECTIONS_13B)
@@ -545,6 +570,12 @@ def configs_bench(dev, L, check):
                    "frac_of_bf16_peak": round(f / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
     del projs
     torch.cuda.empty_cache()
+    return out
+
+
+def _cfg4(dev, L, check, gen):
+    import torch
+    out = {}
     ch = Chain(dev, gen)
     ms = _time_ms(lambda: ch.step(L, check), reps=3, warmup=1)
     out["cfg4"] = {"what": "30 wan2.1-1.3b layers (q -> k -> v -> o -> ffn.0 -> gelu_tanh -> "
@@ -555,6 +586,11 @@ def configs_bench(dev, L, check):
                    "flops": ch.flops}
     del ch
     torch.cuda.empty_cache()
+    return out
+
+
+def _cfg5a(dev, L, check, gen):
+    out = {}
     sk = {}
     for M in (77, 333, 512):
         K = N = 5120
@@ -578,7 +614,6 @@ def configs_bench(dev, L, check):
     out["cfg5a"] = {"what": "cross-attention K/V projection 5120 -> 5120, r 32, at 77 / 333 / 512 "
                             "text tokens; bytes = 2MK + NK + 4N + 2MN + 2Mr (fwd), 2MN + NK + 4N "
                             "+ 4MK + 2Mr (bwd); peak 8 TB/s", "tokens": sk}
-    torch.cuda.empty_cache()
     return out
 
 
@@ -628,6 +663,10 @@ def main():
     if args.pack_only:
         print(json.dumps({"pack": pack_bench(dev)[0]}))
         return
+    if args.configs_only:
+        which = tuple(args.configs_only.split(","))
+        print(json.dumps({"configs": configs_bench(dev, L, _lib.check, which)}))
+        return
     if args.attention_only:
         att = attention_bench(dev)
         if args.cpu_seconds > 0:
@@ -654,6 +693,7 @@ def main():
     torch.cuda.synchronize()
 
     # count one step's launches (an untimed traced step) to size the trace buffer exactly
+    _lib.check("reels_hip_trace_only", L.reels_hip_trace_only(b"gemm_kernel" if args.trace == "gemm" else b""))
     _lib.check("reels_hip_trace_start", L.reels_hip_trace_start(4096))
     run_step(L, projs, _lib.check, sfx, streamer)
     torch.cuda.synchronize()
@@ -667,6 +707,14 @@ def main():
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     recs = _lib.trace_records()
+    all_recs, all_steps = recs, args.steps
+    if args.trace == "gemm":
+        # the per-kernel breakdown: one more (untimed) step with every kernel traced
+        _lib.check("reels_hip_trace_only", L.reels_hip_trace_only(b""))
+        _lib.check("reels_hip_trace_start", L.reels_hip_trace_start(4096))
+        run_step(L, projs, _lib.check, sfx, streamer)
+        torch.cuda.synchronize()
+        all_recs, all_steps = _lib.trace_records(), 1
     offload = None
     if streamer is not None:
         ups = (streamer.uploads - up0) / args.steps
@@ -688,7 +736,7 @@ def main():
     # per-kernel statistics from the event trace (launch order is fixed within a step)
     per_step = len(recs) // max(args.steps, 1)
     kern = {}
-    for name, ms in recs:
+    for name, ms in all_recs:
         d = kern.setdefault(name, [0, 0.0])
         d[0] += 1
         d[1] += ms
@@ -724,7 +772,8 @@ def main():
                                      "sustained ~1.5 s loop, same run", "tflops": round(vendor, 1),
                              "achieved_over_vendor": round(achieved / vendor, 4)},
     }
-    kernels = {n: {"launches": c, "avg_ms": round(t / c, 4), "ms_per_step": round(t / args.steps, 4)}
+    kernels = {n: {"launches_per_step": c // all_steps, "avg_ms": round(t / c, 4),
+                   "ms_per_step": round(t / all_steps, 4)}
                for n, (c, t) in sorted(kern.items(), key=lambda kv: -kv[1][1])}
 
     cpu = None
@@ -763,6 +812,8 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": kernels,
+        "kernels_from": ("one extra untimed step with every kernel traced (the timed steps trace "
+                         "the GEMMs only)") if args.trace == "gemm" else "the timed steps",
         "configs": configs,
         "pack": pack,
         "attention": att,

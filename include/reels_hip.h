@@ -239,8 +239,11 @@ int reels_hip_attention_bwd(const void* q, const void* k, const void* v, const v
  *   reels_hip_trace_stop(): stop recording; returns the number of launches recorded
  *   reels_hip_trace_get(i, &name, &ms): kernel name and duration of launch i; the caller must
  *     have synchronised the streams first. Returns REELS_HIP_EINVAL for a bad index.
+ *   reels_hip_trace_only(name_part): from now on bracket and record only kernels whose name
+ *     contains name_part (NULL or "": every kernel), so the events of a timed loop cost less
  */
 int reels_hip_trace_start(int capacity);
+int reels_hip_trace_only(const char* name_part);
 int reels_hip_trace_stop(void);
 int reels_hip_trace_get(int index, const char** name, float* ms);
 

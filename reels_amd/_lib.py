@@ -42,6 +42,7 @@ EXPORTS = (
     "reels_hip_attention_fwd",
     "reels_hip_attention_bwd",
     "reels_hip_trace_start",
+    "reels_hip_trace_only",
     "reels_hip_trace_stop",
     "reels_hip_trace_get",
 )
@@ -112,6 +113,8 @@ def lib():
     L.reels_hip_trace_start.argtypes = [ctypes.c_int]
     L.reels_hip_trace_start.restype = ctypes.c_int
     L.reels_hip_trace_stop.restype = ctypes.c_int
+    L.reels_hip_trace_only.argtypes = [ctypes.c_char_p]
+    L.reels_hip_trace_only.restype = ctypes.c_int
     L.reels_hip_trace_get.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_char_p),
                                       ctypes.POINTER(ctypes.c_float)]
     L.reels_hip_trace_get.restype = ctypes.c_int

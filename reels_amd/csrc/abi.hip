@@ -4,6 +4,7 @@
 
 #include <atomic>
 #include <mutex>
+#include <string>
 #include <vector>
 
 namespace reels {
@@ -35,12 +36,19 @@ std::mutex g_trace_mu;
 std::vector<TraceRec> g_trace;  // events are created once and reused across trace sessions
 int g_trace_used = 0, g_trace_cap = 0;
 std::atomic<bool> g_trace_on{false};
+std::string g_trace_only;  // record only kernels whose name contains this (empty: all)
+thread_local bool g_trace_skip = false;  // the current launch is not recorded
 }  // namespace
 
 void trace_before(hipStream_t st, const char* name) {
+  g_trace_skip = false;
   if (!g_trace_on) return;
   std::lock_guard<std::mutex> lk(g_trace_mu);
   if (!g_trace_on || g_trace_used >= g_trace_cap) return;
+  if (!g_trace_only.empty() && std::string(name).find(g_trace_only) == std::string::npos) {
+    g_trace_skip = true;
+    return;
+  }
   if (g_trace_used == (int)g_trace.size()) {
     TraceRec r{name, nullptr, nullptr};
     if (hipEventCreate(&r.start) != hipSuccess || hipEventCreate(&r.stop) != hipSuccess) {
@@ -55,7 +63,7 @@ void trace_before(hipStream_t st, const char* name) {
 }
 
 void trace_after(hipStream_t st) {
-  if (!g_trace_on) return;
+  if (!g_trace_on || g_trace_skip) return;
   std::lock_guard<std::mutex> lk(g_trace_mu);
   if (!g_trace_on || g_trace_used >= g_trace_cap) return;
   if (hipEventRecord(g_trace[g_trace_used].stop, st) != hipSuccess) g_trace_on = false;
@@ -72,6 +80,14 @@ extern "C" int reels_hip_trace_start(int capacity) {
   g_trace_used = 0;
   g_trace_cap = capacity;
   g_trace_on = true;
+  return REELS_HIP_OK;
+}
+
+extern "C" int reels_hip_trace_only(const char* name_part) {
+  using namespace reels;
+  clear_error();
+  std::lock_guard<std::mutex> lk(g_trace_mu);
+  g_trace_only = name_part ? name_part : "";
   return REELS_HIP_OK;
 }
 

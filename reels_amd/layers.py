@@ -405,9 +405,14 @@ class I8LoRALinearFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, A, B, values, scales, bias, lora_scale):
         weight = QuantizedMatrix(values, scales)
-        y, h = i8lora_forward(x, weight, A, B, bias, lora_scale, save_h=True)
-        ctx.save_for_backward(x, A, B, values, scales, h)
+        # f32 master parameters with 16-bit activations: the kernels take rounded copies, the
+        # gradients come back in f32 (the reference's AdamW keeps f32 state, optimizer.jl:9-24)
+        Ac = A if A.dtype == x.dtype else A.to(x.dtype)
+        Bc = B if B.dtype == x.dtype else B.to(x.dtype)
+        y, h = i8lora_forward(x, weight, Ac, Bc, bias, lora_scale, save_h=True)
+        ctx.save_for_backward(x, Ac, Bc, values, scales, h)
         ctx.lora_scale = lora_scale
+        ctx.param_dtypes = (A.dtype, B.dtype)
         ctx.bias_dtype = None if bias is None else bias.dtype
         return y
 
@@ -423,10 +428,11 @@ class I8LoRALinearFunction(torch.autograd.Function):
         # a trainable bias (LoRALinear train_bias): the pullback of mixed_add (linear.jl:7-13)
         # sums dy over the tokens; summed in f32
         dbias = dy.float().sum(0).to(ctx.bias_dtype) if ctx.needs_input_grad[5] else None
-        # dA and dB keep the f32 of the kernels when the adapter parameters are f32 masters (the
-        # reference's AdamW keeps f32 state, optimizer.jl:9-24); otherwise the parameter dtype
-        return (dx, None if dA is None else dA.to(A.dtype),
-                None if dB is None else dB.to(B.dtype), None, None, dbias, None)
+        # dA and dB keep the f32 of the kernels when the adapter parameters are f32 masters;
+        # otherwise they take the parameter dtype
+        ad, bd = ctx.param_dtypes
+        return (dx, None if dA is None else dA.to(ad),
+                None if dB is None else dB.to(bd), None, None, dbias, None)
 
 
 def gelu_tanh(x: torch.Tensor) -> torch.Tensor:

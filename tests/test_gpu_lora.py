@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 import oracle
-from tests._util import assert_parity, bf16_f32, rel_errors, to_dev
+from tests._util import assert_parity, bf16_bits, bf16_f32, rel_errors, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -245,6 +245,33 @@ def test_autograd_trainable_bias_gets_its_gradient(dev):
     dx, dA, dB = i8lora_backward(dy, x.detach(), W, A.detach(), B.detach(), cs["c"])
     assert torch.equal(x.grad, dx)
     assert torch.equal(A.grad, dA.to(torch.bfloat16)) and torch.equal(B.grad, dB.to(torch.bfloat16))
+
+
+def test_autograd_f32_master_adapters_get_f32_gradients(dev):
+    """f32 master copies of A and B (the reference's AdamW keeps f32 state, optimizer.jl:9-24)
+    with bf16 activations: the kernels run on bf16 roundings of the masters and the gradients
+    come back as the kernels' f32 values, not rounded to bf16."""
+    import torch
+    from reels_amd import I8LoRALinearFunction, QuantizedMatrix, i8lora_backward, i8lora_forward
+    M, K, N, r = 200, 256, 384, 16
+    cs = make_case(M, K, N, r, 16.0, seed=650)
+    W = QuantizedMatrix(to_dev(cs["q"], dev, "raw"), to_dev(cs["s"], dev, "raw"))
+    x = to_dev(cs["x"], dev).requires_grad_(True)
+    A32 = (to_dev(cs["A"], dev).float() * (1.0 + 2.0 ** -12)).requires_grad_(True)  # not bf16 values
+    B32 = (to_dev(cs["B"], dev).float() * (1.0 - 2.0 ** -12)).requires_grad_(True)
+    dy = to_dev(cs["dy"], dev)
+    y = I8LoRALinearFunction.apply(x, A32, B32, W.values, W.scales, None, cs["c"])
+    y.backward(dy)
+    torch.cuda.synchronize(dev)
+    assert A32.grad.dtype == torch.float32 and B32.grad.dtype == torch.float32
+    Ab, Bb = A32.detach().to(torch.bfloat16), B32.detach().to(torch.bfloat16)
+    y2, _ = i8lora_forward(x.detach(), W, Ab, Bb, None, cs["c"])
+    dx, dA, dB = i8lora_backward(dy, x.detach(), W, Ab, Bb, cs["c"])
+    assert torch.equal(y, y2) and torch.equal(x.grad, dx)
+    assert torch.equal(A32.grad, dA) and torch.equal(B32.grad, dB)
+    ref = oracle.lora_backward(cs["dy"], cs["x"], cs["q"], cs["s"], bf16_bits(Ab), bf16_bits(Bb), cs["c"])
+    assert_parity(A32.grad.cpu().numpy(), ref["dA"], "f32 master dA")
+    assert_parity(B32.grad.cpu().numpy(), ref["dB"], "f32 master dB")
 
 
 @pytest.mark.parametrize("n", [1, 1000, 8960 * 64 + 3])
