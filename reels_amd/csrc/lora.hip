@@ -16,7 +16,6 @@
 // compute the same formulas with the same bf16 rounding points, one output element per thread.
 #include "i8gemm.h"
 
-#include <map>
 #include <mutex>
 
 namespace reels {
@@ -820,38 +819,6 @@ static int i8lora_fwd_impl(int elt, const char* fn, const void* x, const int8_t*
   return launch_i8gemm(0, elt, g, st);
 }
 
-// ---- gradient passes beside the dX GEMM ---------------------------------------------------------
-// dA = c x^T u and dB = c (dy^T h)^T do not feed the dX GEMM; they are HBM-bound while the GEMM is
-// MFMA-bound, so they run on a second stream of the caller's device (one per caller stream,
-// default priority) forked after u and joined before the call returns. The fork and join are
-// event waits, so the pattern is also valid inside a stream capture.
-struct SideStream {
-  hipStream_t side = nullptr;
-  hipEvent_t fork = nullptr, join = nullptr;
-};
-constexpr size_t kMaxSideStreams = 256;
-static std::mutex g_side_mu;
-static std::map<std::pair<int, hipStream_t>, SideStream> g_side;
-
-// the side stream of (current device, st), created on first use; NULL when none can be had (the
-// passes then run on st)
-static SideStream* side_stream_for(hipStream_t st) {
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
-  std::lock_guard<std::mutex> lock(g_side_mu);
-  auto it = g_side.find({dev, st});
-  if (it != g_side.end()) return &it->second;
-  if (g_side.size() >= kMaxSideStreams) return nullptr;
-  SideStream s;
-  if (hipStreamCreateWithFlags(&s.side, hipStreamNonBlocking) != hipSuccess) return nullptr;
-  if (hipEventCreateWithFlags(&s.fork, hipEventDisableTiming) != hipSuccess ||
-      hipEventCreateWithFlags(&s.join, hipEventDisableTiming) != hipSuccess) {
-    (void)hipGetLastError();
-    return nullptr;
-  }
-  return &g_side.emplace(std::make_pair(dev, st), s).first->second;
-}
-
 static int i8lora_bwd_impl(int elt, const char* fn, const void* dy, const void* x, const void* h,
                            const int8_t* q, const float* scales, const void* A, const void* B,
                            int64_t M, int64_t K, int64_t N, int64_t r, float lora_scale, void* dx,
@@ -948,9 +915,18 @@ static int i8lora_bwd_impl(int elt, const char* fn, const void* dy, const void* 
         (rc = launch_rowproj(elt, dyb, M, N, Bb, (int)r, p.rp, u, nullptr, nullptr, st)))
       return rc;
   } else if (p.deq) {
-    // 1. u = dy B^T (the dX GEMM below: dx = dy wt^T + c u A^T with wt[k][n] = bf16(q[n][k] s[n]))
+    // 1. u = dy B^T; 2. dx = dy wt^T + c u A^T with wt[k][n] = bf16(q[n][k] s[n])
     if (r > 0 && (dx || dA)) {
       if ((rc = launch_rowproj(elt, dyb, M, N, Bb, (int)r, p.rp, u, nullptr, nullptr, st))) return rc;
+    }
+    if (dx) {
+      uint16_t* wt = reinterpret_cast<uint16_t*>(ws + w.wd);
+      if ((rc = launch_dequant_transpose(elt, q, K, scales, N, K, wt, st))) return rc;
+      GemmArgs g{};
+      g.act = dyb; g.q = nullptr; g.colscale = nullptr; g.L = r > 0 ? u : nullptr; g.R = Ar;
+      g.bias = nullptr; g.out = static_cast<uint16_t*>(dx);
+      g.M = M; g.Ncols = K; g.Kred = N; g.ldq = N; g.rp = r > 0 ? p.rp : 0; g.c = lora_scale;
+      if ((rc = launch_bfgemm(1, elt, g, wt, st))) return rc;
     }
   } else if (r > 0 || (dx && !f16)) {
     // 1. u = dy B^T and (bf16) dys = dy * s in one pass over dy (the scaled copy only when dx is
@@ -963,29 +939,7 @@ static int i8lora_bwd_impl(int elt, const char* fn, const void* dy, const void* 
       if ((rc = launch_rowproj(elt, dyb, M, N, Bb, 0, 0, nullptr, scales, scaled, st))) return rc;
     }
   }
-  // the gradient passes go beside the dX GEMM (not on the few-token path, whose h recompute shares
-  // the dX launch's workspace)
-  hipStream_t gs = st;
-  SideStream* side = (dx && (dA || dB) && !p.skinny) ? side_stream_for(st) : nullptr;
-  if (side) {
-    hipError_t e = hipEventRecord(side->fork, st);
-    if (e == hipSuccess) e = hipStreamWaitEvent(side->side, side->fork, 0);
-    if (e != hipSuccess) return fail(REELS_HIP_EHIP, std::string(fn) + ": fork to the side stream: " + hipGetErrorString(e));
-    gs = side->side;
-  }
-  // 2. dx = dy wt^T + c u A^T (dequantized weight), dx = dys q + c u A^T (bf16),
-  // dx = dy f16(q f16(s)) + c u A^T (f16)
-  // (exactly one dX path runs: few tokens, else the dequantized weight, else the int8 GEMM; the
-  // few-token plan sizes w.wd for its partials, not for a weight copy)
-  if (dx && p.deq && !p.skinny) {
-    uint16_t* wt = reinterpret_cast<uint16_t*>(ws + w.wd);
-    if ((rc = launch_dequant_transpose(elt, q, K, scales, N, K, wt, st))) return rc;
-    GemmArgs g{};
-    g.act = dyb; g.q = nullptr; g.colscale = nullptr; g.L = r > 0 ? u : nullptr; g.R = Ar;
-    g.bias = nullptr; g.out = static_cast<uint16_t*>(dx);
-    g.M = M; g.Ncols = K; g.Kred = N; g.ldq = N; g.rp = r > 0 ? p.rp : 0; g.c = lora_scale;
-    if ((rc = launch_bfgemm(1, elt, g, wt, st))) return rc;
-  }
+  // 2. dx = dys q + c u A^T (bf16), dx = dy f16(q f16(s)) + c u A^T (f16)
   if (dx && !p.deq && !p.skinny) {
     GemmArgs g{};
     g.act = f16 ? dyb : dys; g.q = q; g.colscale = nullptr; g.redscale = f16 ? scales : nullptr;
@@ -997,7 +951,7 @@ static int i8lora_bwd_impl(int elt, const char* fn, const void* dy, const void* 
   // 3. dA = c x^T u ; dB = c (dy^T h)^T
   if (dA) {
     if ((rc = launch_colgrad(elt, xb, M, K, u, (int)r, p.rp, p.sa, lora_scale,
-                             reinterpret_cast<float*>(ws + w.pa), dA, false, gs))) return rc;
+                             reinterpret_cast<float*>(ws + w.pa), dA, false, st))) return rc;
   }
   if (dB) {
     if (!hh && p.skinny) {
@@ -1018,19 +972,14 @@ static int i8lora_bwd_impl(int elt, const char* fn, const void* dy, const void* 
     if (!hh) {
       uint16_t* at = reinterpret_cast<uint16_t*>(ws + w.at);
       uint16_t* hw = reinterpret_cast<uint16_t*>(ws + w.h);
-      { TraceScope _ts(gs, "transpose_pad_kernel"); transpose_pad_kernel<<<dim3((unsigned)ceil_div(r, 32), (unsigned)ceil_div(K, 32)), 256, 0, gs>>>(
+      { TraceScope _ts(st, "transpose_pad_kernel"); transpose_pad_kernel<<<dim3((unsigned)ceil_div(r, 32), (unsigned)ceil_div(K, 32)), 256, 0, st>>>(
           Ab, K, r, K, at); }
       if ((rc = check_launch("transpose_pad_kernel"))) return rc;
-      if ((rc = launch_rowproj(elt, xb, M, K, at, (int)r, p.rp, hw, nullptr, nullptr, gs))) return rc;
+      if ((rc = launch_rowproj(elt, xb, M, K, at, (int)r, p.rp, hw, nullptr, nullptr, st))) return rc;
       hh = hw;
     }
     if ((rc = launch_colgrad(elt, dyb, M, N, hh, (int)r, p.rp, p.sb, lora_scale,
-                             reinterpret_cast<float*>(ws + w.pb), dB, true, gs))) return rc;
-  }
-  if (side) {
-    hipError_t e = hipEventRecord(side->join, gs);
-    if (e == hipSuccess) e = hipStreamWaitEvent(st, side->join, 0);
-    if (e != hipSuccess) return fail(REELS_HIP_EHIP, std::string(fn) + ": join from the side stream: " + hipGetErrorString(e));
+                             reinterpret_cast<float*>(ws + w.pb), dB, true, st))) return rc;
   }
   return REELS_HIP_OK;
 }

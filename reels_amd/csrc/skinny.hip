@@ -15,8 +15,8 @@
 //                 (and lsave); the last adapter tile to finish raises the launch's ready flag;
 //   output tile:  waits for that flag, then out = rnd(scale * sum + c * l R + bias), the l R
 //                 product on the MFMA.
-// The adapter blocks come first in the grid and wait for nothing, so the flag is normally up long
-// before an output tile looks; the wait is bounded all the same, and an output tile that gives up
+// The adapter blocks come first in the logical order and wait for nothing, so the flag is normally
+// up long before an output tile looks; the wait is bounded all the same, and an output tile that gives up
 // computes l for its tokens itself with the adapter blocks' code and order (same bits), so the
 // result never depends on how the grid is scheduled.
 // The counters and the flag live in a per-stream slot of static device memory and are put back to
@@ -569,7 +569,7 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
     }
     return;
   } else {
-    // l complete: the adapter blocks come first in the grid and wait for nothing, so the flag is
+    // l complete: the adapter blocks come first in the logical order and wait for nothing, so the flag is
     // normally up by the time an output tile gets here. Should they not have started after a long
     // wait (a grid that cannot be resident at once, behind other work), the block computes l for
     // its tokens itself, with the adapter blocks' code, splits and order, so the values are the
@@ -674,9 +674,13 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
 template <int T, int MODE, int ELT>
 __global__ __launch_bounds__(64 * sk::NWV, 1) void skinny_kernel(SkArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  // grid order: adapter blocks, then output blocks; within each (row block, split, token block)
-  // with the token block fastest, so blocks that read the same weight rows start together
-  const int tk = (int)blockIdx.x;
+  // logical order: adapter blocks, then output blocks; within each (row block, split, token
+  // block) with the token block fastest. Block b runs on XCD b % 8, and each XCD takes a
+  // contiguous range of the logical order, so the token blocks that read the same weight rows
+  // run on one XCD, close in time, and share those rows through its L2.
+  const int b = (int)blockIdx.x, xcd = b & 7, idx = b >> 3;
+  const int per = a.blocks >> 3, rem = a.blocks & 7;
+  const int tk = xcd * per + (xcd < rem ? xcd : rem) + idx;
   const bool lora = tk < a.nad;
   int rest = lora ? tk : tk - a.nad;
   SkBlock d;
