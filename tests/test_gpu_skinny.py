@@ -107,3 +107,29 @@ def test_f16_fallback_and_repeat(dev, monkeypatch):
     torch.cuda.synchronize(dev)
     for name, a, b in zip(("y", "h", "dx", "dA", "dB"), ref, got):
         assert torch.equal(a, b), f"f16 {name} differs when output tiles compute l themselves"
+
+
+@pytest.mark.parametrize("r", [3, 160])
+def test_few_tokens_any_rank(dev, r):
+    """Ranks that are not a multiple of 16 and ranks above 128 on the few-token path: several
+    adapter row blocks (160 = 5 of 32) and rank chunks in the epilogue's l R product, padding past
+    the rank. 77 tokens on 5120 x 5120; y, h, dx, dA, dB against the oracle, h recomputed for the
+    backward equal to the saved one."""
+    import torch
+    from reels_amd import i8lora_backward, i8lora_forward
+    M, K, N = 77, 5120, 5120
+    host, d = _case(dev, M, K, N, r, 4600 + r)
+    c = float(np.float32(r) / np.float32(r))
+    print(f"[skinny] rank {r} at {M} tokens", flush=True)
+    y, h = i8lora_forward(d["x"], d["W"], d["A"], d["B"], None, c, save_h=True)
+    dx, dA, dB = i8lora_backward(d["dy"], d["x"], d["W"], d["A"], d["B"], c, h=h)
+    dx2, dA2, dB2 = i8lora_backward(d["dy"], d["x"], d["W"], d["A"], d["B"], c, h=None)
+    torch.cuda.synchronize(dev)
+    assert torch.equal(dx, dx2) and torch.equal(dA, dA2) and torch.equal(dB, dB2)
+    yo, ho = oracle.lora_forward(host["x"], host["q"], host["s"], host["A"], host["B"], c)
+    go = oracle.lora_backward(host["dy"], host["x"], host["q"], host["s"], host["A"], host["B"], c)
+    assert_parity(bf16_f32(y), yo, f"rank {r} y")
+    assert_parity(bf16_f32(h), ho, f"rank {r} h")
+    assert_parity(bf16_f32(dx), go["dx"], f"rank {r} dx")
+    assert_parity(dA.cpu().numpy(), go["dA"], f"rank {r} dA")
+    assert_parity(dB.cpu().numpy(), go["dB"], f"rank {r} dB")
