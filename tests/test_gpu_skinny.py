@@ -133,3 +133,24 @@ def test_few_tokens_any_rank(dev, r):
     assert_parity(bf16_f32(dx), go["dx"], f"rank {r} dx")
     assert_parity(dA.cpu().numpy(), go["dA"], f"rank {r} dA")
     assert_parity(dB.cpu().numpy(), go["dB"], f"rank {r} dB")
+
+
+def test_thousand_tokens_on_a_small_weight(dev):
+    """Config 1's shape (one 1536 x 1536 linear, 1024 tokens, r 16, alpha 16): a small weight takes
+    the few-token path up to 1024 tokens (13 token blocks); y, h, dx, dA, dB against the oracle."""
+    import torch
+    from reels_amd import i8lora_backward, i8lora_forward
+    M, K, N, r = 1024, 1536, 1536, 16
+    host, d = _case(dev, M, K, N, r, 4700)
+    c = 1.0
+    print("[skinny] 1024 tokens on 1536 x 1536", flush=True)
+    y, h = i8lora_forward(d["x"], d["W"], d["A"], d["B"], None, c, save_h=True)
+    dx, dA, dB = i8lora_backward(d["dy"], d["x"], d["W"], d["A"], d["B"], c, h=h)
+    torch.cuda.synchronize(dev)
+    yo, ho = oracle.lora_forward(host["x"], host["q"], host["s"], host["A"], host["B"], c)
+    go = oracle.lora_backward(host["dy"], host["x"], host["q"], host["s"], host["A"], host["B"], c)
+    assert_parity(bf16_f32(y), yo, "1024 tokens y")
+    assert_parity(bf16_f32(h), ho, "1024 tokens h")
+    assert_parity(bf16_f32(dx), go["dx"], "1024 tokens dx")
+    assert_parity(dA.cpu().numpy(), go["dA"], "1024 tokens dA")
+    assert_parity(dB.cpu().numpy(), go["dB"], "1024 tokens dB")
