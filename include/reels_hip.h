@@ -93,8 +93,10 @@ size_t reels_hip_i8lora_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t
  *   h = bf16(x * A)                                    [M][r]
  *   y = bf16(sum_k x[m][k] W[n][k] + lora_scale * sum_j h[m][j] B[j][n] + bias[n])
  * with W = bf16(fl32(q * s)) written into the workspace once per call when K and N are multiples
- * of 64 (the reference's _materialize_weight, quantization.jl:54-64), otherwise W = q * s exact
- * with s[n] applied to the f32 sum. bias may be NULL. r = 0 (A, B NULL) gives the base-only
+ * of 64 and there are many tokens (the reference's _materialize_weight, quantization.jl:54-64);
+ * otherwise W = q * s exact with s[n] applied to the f32 sum: K or N not a multiple of 64, and the
+ * few-token path (M <= 512, or M <= 1024 with N * K <= 2^22; K and N multiples of 64), which
+ * reads the int8 codes without a weight copy. bias may be NULL. r = 0 (A, B NULL) gives the base-only
  * linear(::DenseLayer) of src/layers/linear.jl:38-46. h_save ([M][r] or NULL) receives h for the
  * backward. workspace: device memory of reels_hip_i8lora_workspace_bytes(M, K, N, r,
  * REELS_HIP_WS_FWD).
@@ -140,8 +142,10 @@ int reels_hip_i8lora_fwd_noalloc(const void* x, const int8_t* q, const float* sc
  *   u  = bf16(dy * B^T)                                                      [M][r]
  *   dx = bf16(sum_n dy[m][n] W[n][k] + lora_scale * sum_j u[m][j] A[k][j])
  *   dA = lora_scale * x^T u   (f32 [K][r]);   dB = lora_scale * h^T dy   (f32 [r][N])
- * W as in reels_hip_i8lora_fwd (when K or N is not a multiple of 64, the product is taken as
- * sum_n bf16(dy[m][n] s[n]) q[n][k]). h: the forward's h_save ([M][r]) or NULL to recompute it.
+ * W = bf16(fl32(q * s)) when K and N are multiples of 64 (a transposed copy in the workspace, or,
+ * on the few-token path of reels_hip_i8lora_fwd, built in registers from the codes); when K or N
+ * is not a multiple of 64 the product is taken as sum_n bf16(dy[m][n] s[n]) q[n][k]. h: the
+ * forward's h_save ([M][r]) or NULL to recompute it.
  * dx, dA, dB may each be NULL to skip that output. r = 0 gives dx = deq(W)^T dy alone
  * (_weight_transpose_mul). dA and dB are overwritten (not accumulated) and are bitwise
  * reproducible run to run.
