@@ -7,18 +7,19 @@
 //
 // One launch does everything. A block is (tile, split): a tile is 64 output rows (or 32 rows of
 // the adapter's rank projection) x up to 16T tokens, a split a contiguous range of 64-wide
-// reduction chunks. The block's 8 waves each take an eighth of the split's chunks; their
-// accumulators are summed in LDS in wave order. With more than one split the block stores that
-// sum as an f32 partial and counts itself in on the tile; the block that arrives last sums the
-// tile's partials in split order (its own from registers) and finishes the tile:
+// reduction chunks. The block's 8 waves take the split's chunks round by round (wave w every
+// eighth chunk); their accumulators are summed in LDS in a fixed wave order. With more than one
+// split the block stores that sum as an f32 partial and counts itself in on the tile; the block
+// that arrives last sums the tile's partials in split order (its own from registers) and
+// finishes the tile:
 //   adapter tile: l = rnd(sum) (h = x A in the forward, u = dy B^T for dX) into the workspace
 //                 (and lsave); the last adapter tile to finish raises the launch's ready flag;
 //   output tile:  waits for that flag, then out = rnd(scale * sum + c * l R + bias), the l R
 //                 product on the MFMA.
 // The adapter blocks come first in the logical order and wait for nothing, so the flag is normally
-// up long before an output tile looks; the wait is bounded all the same, and an output tile that gives up
-// computes l for its tokens itself with the adapter blocks' code and order (same bits), so the
-// result never depends on how the grid is scheduled.
+// up long before an output tile looks; the wait is bounded all the same, and an output tile that
+// gives up computes l for its tokens itself with the adapter blocks' code and order (same bits),
+// so the result never depends on how the grid is scheduled.
 // The counters and the flag live in a per-stream slot of static device memory and are put back to
 // zero by the launch that used them, so launches need no clearing pass. Deterministic: fixed wave
 // order, fixed split order; the atomics only count.
@@ -53,11 +54,10 @@ constexpr uint32_t kSpinLimit = 1u << 12;  // wait rounds of s_sleep 8 (about 1 
 
 // one launch's counters (zero between launches)
 struct SkSlot {
-  uint32_t unused;
   uint32_t hdone;    // adapter tiles finished
   uint32_t hready;   // 1: l complete (set by the last adapter tile, cleared by the last tile)
   uint32_t fin;      // tiles finished (launches with adapter and output tiles)
-  uint32_t pad[28];
+  uint32_t pad[29];  // the tile counters start on their own 128-byte line
   uint32_t tile[sk::kMaxTiles];  // blocks of the tile that have stored their partial
 };
 static __device__ __align__(256) SkSlot sk_slots[sk::kSlots];
@@ -79,7 +79,7 @@ struct SkArgs {
   float c;
   int r, rp, S, nblk, lblk, tb, lsave_cols;
   int blocks;  // of the launch
-  int nad;     // adapter blocks: the first blocks of the grid
+  int nad;     // adapter blocks: the first blocks of the logical order
   int ntm;     // output tiles (nblk * tb; 0 for an adapter-only launch)
   uint32_t spin;  // wait rounds before an output tile computes l itself
   int nta;     // adapter tiles (lblk * tb)
@@ -127,9 +127,10 @@ __device__ __forceinline__ void skinny_finish(const SkArgs& a) {
   }
 }
 
-// One wave's share of a (row block, split, token block): acc[i][tt] = rows 16 i + (0..15) x tokens
-// 16 tt + (0..15) over the wave's eighth of the split's chunks. LORA: a block of the adapter's
-// rank projection (rows j of A^T in the forward, of B for dX) rather than of the int8 weight.
+// One wave's share of a (row block, split, token block): acc[i][tt] = rows 16 i + (0..15) x
+// tokens 16 tt + (0..15) over the wave's chunks of the split (every eighth). LORA: a block of the
+// adapter's rank projection (rows j of A^T in the forward, of B for dX) rather than of the int8
+// weight.
 template <int T, int MODE, int ELT, bool LORA>
 __device__ __forceinline__ void skinny_acc(const SkArgs& a, int blk, int sp, int64_t tok0,
                                            uint8_t* smem, f32x4 (&acc)[LORA ? 2 : 4][T]) {
