@@ -34,12 +34,28 @@ constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.6931471805599453f;
 }  // namespace att
 
-// byte offset of element d of row r in a tile with rows of D elements; 16-byte chunks are
-// XOR-swizzled by the row so that 16 consecutive rows read at one column hit distinct banks
+// LDS slot of 16-byte chunk c of row r is c ^ swz<D>(r). The tiles are read in two patterns:
+// - fragment reads (ds_read_b128): 16 rows of an aligned 16-row block, one chunk per 16-lane
+//   group (chunks 4 kb + 0..3);
+// - transposed reads (read_tr, ds_read_b64_tr_b16): 8 rows of an aligned 8-row block per
+//   32-lane pass, 32 bytes of each (chunks 2 i and 2 i + 1).
+// The transposed reads need distinct chunk pairs (swz >> 1) within 8 rows; the fragment reads
+// need the 16-lane passes of ds_read_b128 to meet distinct banks, and that instruction's passes
+// pair 8-lane groups {0, 3}, {1, 2}, {4, 7}, {5, 6} (measured on gfx950 with
+// SQ_LDS_BANK_CONFLICT, like the swizzles themselves). For D = 128 (each row covers all 64
+// banks) swz = 2 (r mod 8) meets both: the row swizzle r mod 16 left the transposed reads
+// two-way conflicted. For D = 64 (two rows per 256 bytes) r mod 8 meets both.
+template <int D>
+__device__ __forceinline__ int swz(int r) {
+  if constexpr (D == 128) return (r & 7) << 1;
+  else return r & 7;
+}
+
+// byte offset of element d of row r in a tile with rows of D elements (16-byte chunks
+// XOR-swizzled by the row, swz above)
 template <int D>
 __device__ __forceinline__ uint32_t toff(int r, int d) {
-  constexpr int CH = D / 8;
-  return (uint32_t)(r * D * 2 + ((((d >> 3) ^ (r & (CH - 1)))) << 4) + (d & 7) * 2);
+  return (uint32_t)(r * D * 2 + (((d >> 3) ^ swz<D>(r)) << 4) + (d & 7) * 2);
 }
 
 // 2^x on v_exp_f32 alone: exp2f adds a range scaling for results below 2^-126, probabilities
@@ -105,7 +121,7 @@ __device__ __forceinline__ bool att_visible(const AttArgs& a, int64_t qi, int64_
 
 // Copies of one 64-row tile of a [B][S][H][D] tensor (rows = tokens of one batch and head) into
 // LDS with the toff swizzle: copy c of the tile covers LDS rows c * (64 / CH) .. + 64 / CH - 1,
-// lane L row c * (64 / CH) + L / CH, LDS slot L % CH holding chunk (L % CH) ^ (row & (CH - 1)).
+// lane L row c * (64 / CH) + L / CH, LDS slot L % CH holding chunk (L % CH) ^ swz<D>(row).
 // Rows past the tensor's end read zeros (buffer range).
 template <int D>
 __device__ __forceinline__ void copy_tile(const i32x4& rsrc, int64_t row0, int64_t H, int w,
@@ -115,7 +131,7 @@ __device__ __forceinline__ void copy_tile(const i32x4& rsrc, int64_t row0, int64
   for (int i = 0; i < NC; ++i) {
     const int c = w * NC + i;
     const int row = c * RPC + lane / CH;
-    const int chunk = (lane % CH) ^ (row & (CH - 1));
+    const int chunk = (lane % CH) ^ swz<D>(row);
     const uint32_t off = (uint32_t)(((row0 + row) * H * D + chunk * 8) * 2);
     dma16(rsrc, off, 0u, dst + c * 1024);
   }
@@ -343,7 +359,7 @@ __global__ __launch_bounds__(256, 2) void attn_dkdv_kernel(AttArgs a) {
       const int c = w * ((NCT + 3) / 4) + i;
       if (c < NCT) {
         const int row = c * RPC + lane / CH;
-        const int chunk = (lane % CH) ^ (row & (CH - 1));
+        const int chunk = (lane % CH) ^ swz<D>(row);
         const uint32_t off = (uint32_t)((((int64_t)j * QT + row) * H * D + chunk * 8) * 2);
         dma16(rq, off, 0u, st + c * 1024);
         dma16(rd, off, 0u, st + TB + c * 1024);
