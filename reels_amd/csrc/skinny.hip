@@ -481,6 +481,29 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
   }
   uint32_t* words = reinterpret_cast<uint32_t*>(smem + skinny_lds(T) - 16);  // [1] arrivals, [2] l ready
   SkSlot* slot = a.slot;
+  // An output tile's epilogue operands: the column scales and bias of this thread's rows and
+  // (forward) the first 32 rank rows of R for the tile's 64 columns, which threads 0-255 stage in
+  // LDS. With split partials they are loaded before the hand-over, whose round trips cover their
+  // latency; with one split just before the epilogue (loaded early there they ran slower).
+  f32x4 cs[FPW];
+  u32x2 bsv[FPW];
+  u32x4 rpre;
+  auto load_epi = [&]() {
+#pragma unroll
+    for (int k = 0; k < FPW; ++k) {
+      const int f = w + sk::NWV * k;
+      const int64_t o = o0 + 16 * (f / T) + 4 * g;
+      cs[k] = f32x4{1.0f, 1.0f, 1.0f, 1.0f};
+      bsv[k] = u32x2{0u, 0u};
+      if (f < NF && a.colscale) cs[k] = *reinterpret_cast<const f32x4*>(a.colscale + o);
+      if (f < NF && a.bias) bsv[k] = *reinterpret_cast<const u32x2*>(a.bias + o);
+    }
+    rpre = u32x4{0u, 0u, 0u, 0u};
+    if (MODE == 0 && a.nad > 0 && t < 256 && (t >> 3) < a.r)
+      rpre = *reinterpret_cast<const u32x4*>(a.R + (int64_t)(t >> 3) * a.ldr + o0 + 8 * (t & 7));
+  };
+  if constexpr (!lora)
+    if (a.S > 1) load_epi();
   const __amdgpu_buffer_rsrc_t rl = sk_rsrc(a.hl, a.M * a.rp * 2);
   // Output tiles of a launch with an adapter look at the ready flag now (each wave reads it; the
   // flag only goes up during the launch) and, when it is up, load their tokens' l for the first 32
@@ -606,6 +629,7 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
       asm volatile("" ::: "memory");
       if (!up) load_l(0, hv);  // the waves that found the flag down load l now
     }
+    if (a.S == 1 || (wants_l && words[2] == 0u)) load_epi();  // (not kept across the path above)
     // lo = l R for this tile on the MFMA, 32 rank columns per step: A operand rows o = 16 i + l16
     // with j = 32 jc + 8 g + (0..7), B operand the tokens' l[tok][j .. j + 7]
     f32x4 lo[FPW];
@@ -620,8 +644,11 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
         __syncthreads();
         if (t < 256) {
           const int row = t >> 3, col = 8 * (t & 7);
-          u32x4 v = u32x4{0u, 0u, 0u, 0u};
-          if (j0 + row < a.r) v = *reinterpret_cast<const u32x4*>(a.R + (int64_t)(j0 + row) * a.ldr + o0 + col);
+          u32x4 v = rpre;
+          if (jc > 0) {
+            v = u32x4{0u, 0u, 0u, 0u};
+            if (j0 + row < a.r) v = *reinterpret_cast<const u32x4*>(a.R + (int64_t)(j0 + row) * a.ldr + o0 + col);
+          }
           *reinterpret_cast<u32x4*>(rst + row * 64 + col) = v;
         }
         __syncthreads();
@@ -658,13 +685,12 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
       const int i = f / T, tt = f % T;
       const int64_t tok = tok0 + 16 * tt + l16, o = o0 + 16 * i + 4 * g;
       if (tok >= a.M) continue;
-      const f32x4 cs = a.colscale ? *reinterpret_cast<const f32x4*>(a.colscale + o) : f32x4{1.0f, 1.0f, 1.0f, 1.0f};
+      const float bv[4] = {E::lo(bsv[k][0]), E::hi(bsv[k][0]), E::lo(bsv[k][1]), E::hi(bsv[k][1])};
       uint32_t b[4];
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const float sc = a.colscale ? cs[v] * sum[k][v] : sum[k][v];
-        const float bs = a.bias ? E::to_f32(a.bias[o + v]) : 0.0f;
-        b[v] = E::bits(sc + a.c * lo[k][v] + bs);
+        const float sc = a.colscale ? cs[k][v] * sum[k][v] : sum[k][v];
+        b[v] = E::bits(sc + a.c * lo[k][v] + bv[v]);
       }
       *reinterpret_cast<uint2*>(a.out + tok * a.Ncols + o) = uint2{b[0] | (b[1] << 16), b[2] | (b[3] << 16)};
     }
