@@ -119,6 +119,15 @@ __device__ __forceinline__ bool att_visible(const AttArgs& a, int64_t qi, int64_
   return a.mask[qi * a.Sk + kj] != 0;
 }
 
+// Visibility of key kj to query qi inside a key tile of the forward or dQ kernel. Without a mask
+// only keys past Sk are invisible (a query past Sq computes values nobody stores), and only the
+// last key tile holds such keys: tiles wholly below Sk (FULL) need no check.
+template <int VM, bool FULL>
+__device__ __forceinline__ bool att_visible_tile(const AttArgs& a, int64_t qi, int64_t kj) {
+  if constexpr (VM == 0) return FULL || kj < a.Sk;
+  return att_visible<VM>(a, qi, kj);
+}
+
 // Copies of one 64-row tile of a [B][S][H][D] tensor (rows = tokens of one batch and head) into
 // LDS with the toff swizzle: copy c of the tile covers LDS rows c * (64 / CH) .. + 64 / CH - 1,
 // lane L row c * (64 / CH) + L / CH, LDS slot L % CH holding chunk (L % CH) ^ swz<D>(row).
@@ -189,8 +198,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttArgs a) {
     kend = qlast + 1 < Sk ? qlast + 1 : Sk;
   }
   const int ntiles = (int)((kend + KT - 1) / KT);
+  // tiles wholly below Sk (checked per score only with a mask or causal)
+  const int nfull = VM == 0 ? (int)(kend / KT) : 0;
   if (ntiles > 0) issue(0);
-  for (int j = 0; j < ntiles; ++j) {
+  auto step = [&](int j, auto full) {
+    constexpr bool FULL = decltype(full)::value;
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's copies of tile j have landed
     __syncthreads();                     // every wave's; every wave is done with tile j - 1
     if (j + 1 < ntiles) issue(j + 1);
@@ -226,7 +238,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttArgs a) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int64_t kj = key0 + 16 * kt + 4 * g + v;
-          const float x = att_visible<VM>(a, qi, kj) ? s[kt][qt][v] * sl2 : -INFINITY;
+          const float x = att_visible_tile<VM, FULL>(a, qi, kj) ? s[kt][qt][v] * sl2 : -INFINITY;
           s[kt][qt][v] = x;
           mt = fmaxf(mt, x);
         }
@@ -269,7 +281,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttArgs a) {
         oacc[dt][0] = E::mfma16(E::as8(vf), E::as8(pb[kb2][0]), oacc[dt][0]);
         oacc[dt][1] = E::mfma16(E::as8(vf), E::as8(pb[kb2][1]), oacc[dt][1]);
       }
-  }
+  };
+  int j = 0;
+  for (; j < nfull; ++j) step(j, std::true_type{});
+  for (; j < ntiles; ++j) step(j, std::false_type{});
 
   // out = O / l, lse = (m + log2 l) ln 2; a query with no visible key gets NaN for both, as the
   // reference's online softmax gives
@@ -428,7 +443,10 @@ __global__ __launch_bounds__(256, 2) void attn_dkdv_kernel(AttArgs a) {
         for (int v = 0; v < 4; ++v) {
           const int ql = 16 * qt + 4 * g + v;
           const int64_t qi = (int64_t)j * QT + ql;
-          const bool vis = att_visible<VM>(a, qi, kj);
+          // without a mask nothing needs hiding here: a query past Sq has zero Q and dY rows
+          // (and zero statistics), so its P is 1 and its dS 0 and both products add zeros; a
+          // key past Sk only affects its own, unstored, dK and dV column
+          const bool vis = VM == 0 || att_visible<VM>(a, qi, kj);
           p[hq][v] = vis ? ex2(s[qt][v] * sl2 - lq4[v]) : 0.0f;
           ds[hq][v] = vis ? p[hq][v] * (dp[qt][v] - cq4[v]) : 0.0f;
         }
@@ -515,8 +533,12 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttArgs a) {
     kend = qlast + 1 < Sk ? qlast + 1 : Sk;
   }
   const int ntiles = (int)((kend + KT - 1) / KT);
+  // tiles wholly below Sk (keys past Sk must get P = 0 here: their zero K rows would not cancel
+  // an overflowing P)
+  const int nfull = VM == 0 ? (int)(kend / KT) : 0;
   if (ntiles > 0) issue(0);
-  for (int j = 0; j < ntiles; ++j) {
+  auto step = [&](int j, auto full) {
+    constexpr bool FULL = decltype(full)::value;
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
     if (j + 1 < ntiles) issue(j + 1);
@@ -548,7 +570,7 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttArgs a) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             const int64_t kj = key0 + 16 * kt + 4 * g + v;
-            const bool vis = att_visible<VM>(a, qi, kj);
+            const bool vis = att_visible_tile<VM, FULL>(a, qi, kj);
             const float p = vis ? ex2(s[qt][v] * sl2 - lse2[qt]) : 0.0f;
             dsv[half][qt][v] = vis ? p * (dp[qt][v] - cr[qt]) : 0.0f;
           }
@@ -570,7 +592,10 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttArgs a) {
         qacc[dt][0] = E::mfma16(E::as8(kt_), E::as8(db[kb2][0]), qacc[dt][0]);
         qacc[dt][1] = E::mfma16(E::as8(kt_), E::as8(db[kb2][1]), qacc[dt][1]);
       }
-  }
+  };
+  int j = 0;
+  for (; j < nfull; ++j) step(j, std::true_type{});
+  for (; j < ntiles; ++j) step(j, std::false_type{});
   const float sc = a.scale;
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
