@@ -178,8 +178,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttArgs a) {
   const uint16_t* vbase = a.v + (b * Sk * H + h) * D;
   const uint32_t nrec = (uint32_t)(((Sk - 1) * H + 1) * D * 2);
   const i32x4 rk = buffer_rsrc(kbase, nrec), rv = buffer_rsrc(vbase, nrec);
-  auto issue = [&](int j) {
-    uint8_t* st = smem + (j & 1) * 2 * TB;
+  auto issue = [&](int j, int stg) {
+    uint8_t* st = smem + stg * 2 * TB;
     copy_tile<D>(rk, (int64_t)j * KT, H, w, lane, st);
     copy_tile<D>(rv, (int64_t)j * KT, H, w, lane, st + TB);
   };
@@ -200,13 +200,17 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttArgs a) {
   const int ntiles = (int)((kend + KT - 1) / KT);
   // tiles wholly below Sk (checked per score only with a mask or causal)
   const int nfull = VM == 0 ? (int)(kend / KT) : 0;
-  if (ntiles > 0) issue(0);
-  auto step = [&](int j, auto full) {
+  if (ntiles > 0) issue(0, 0);
+  // step j uses ring stage j % 2: STG 0 or 1 when the caller knows it (the LDS addresses are then
+  // constant offsets of the lane's base), -1 to compute it
+  auto step = [&](int j, auto full, auto stage) {
     constexpr bool FULL = decltype(full)::value;
+    constexpr int STG = decltype(stage)::value;
+    const int stg = STG >= 0 ? STG : (j & 1);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's copies of tile j have landed
     __syncthreads();                     // every wave's; every wave is done with tile j - 1
-    if (j + 1 < ntiles) issue(j + 1);
-    const uint8_t* sk = smem + (j & 1) * 2 * TB;
+    if (j + 1 < ntiles) issue(j + 1, stg ^ 1);
+    const uint8_t* sk = smem + stg * 2 * TB;
     const uint8_t* sv = sk + TB;
     const int64_t key0 = (int64_t)j * KT;
 
@@ -227,7 +231,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttArgs a) {
         s[kt][1] = E::mfma16(E::as8(kf[kt]), E::as8(qf[1][kb]), s[kt][1]);
       }
     }
-    // online softmax per query (base 2): masked scores are -inf and get probability 0
+    // online softmax per query (base 2): masked scores are -inf and get probability 0. The
+    // maximum is taken on the raw scores (the scale sl2 is positive) and each exponent is one
+    // fma, s sl2 - m.
     u32x4 pb[2][2];  // P operand: [32-key block][qt]
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
@@ -238,11 +244,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttArgs a) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int64_t kj = key0 + 16 * kt + 4 * g + v;
-          const float x = att_visible_tile<VM, FULL>(a, qi, kj) ? s[kt][qt][v] * sl2 : -INFINITY;
+          const float x = att_visible_tile<VM, FULL>(a, qi, kj) ? s[kt][qt][v] : -INFINITY;
           s[kt][qt][v] = x;
           mt = fmaxf(mt, x);
         }
-      mt = wave_max16(mt);
+      mt = wave_max16(mt) * sl2;
       const float mnew = fmaxf(mrun[qt], mt);
       // Without a mask every query in range sees key 0 in the first tile, so its maximum is
       // finite from then on and exp2(-inf - m) is 0: the guards below matter only with a mask
@@ -256,7 +262,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttArgs a) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const float x = s[kt][qt][v];
-          p[kt][v] = (VM == 2 && x == -INFINITY) ? 0.0f : ex2(x - mnew);
+          p[kt][v] = (VM == 2 && x == -INFINITY) ? 0.0f : ex2(__builtin_fmaf(x, sl2, -mnew));
           ps += p[kt][v];
         }
       lrun[qt] = lrun[qt] * alpha + ps;
@@ -282,9 +288,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttArgs a) {
         oacc[dt][1] = E::mfma16(E::as8(vf), E::as8(pb[kb2][1]), oacc[dt][1]);
       }
   };
+  // (run-time stage: with constant stages this kernel spills and runs slower)
+  using SR = std::integral_constant<int, -1>;
   int j = 0;
-  for (; j < nfull; ++j) step(j, std::true_type{});
-  for (; j < ntiles; ++j) step(j, std::false_type{});
+  for (; j < nfull; ++j) step(j, std::true_type{}, SR{});
+  for (; j < ntiles; ++j) step(j, std::false_type{}, SR{});
 
   // out = O / l, lse = (m + log2 l) ln 2; a query with no visible key gets NaN for both, as the
   // reference's online softmax gives
@@ -518,8 +526,8 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttArgs a) {
   const uint16_t* vbase = a.v + (b * Sk * H + h) * D;
   const uint32_t nrec = (uint32_t)(((Sk - 1) * H + 1) * D * 2);
   const i32x4 rk = buffer_rsrc(kbase, nrec), rv = buffer_rsrc(vbase, nrec);
-  auto issue = [&](int j) {
-    uint8_t* st = smem + (j & 1) * 2 * TB;
+  auto issue = [&](int j, int stg) {
+    uint8_t* st = smem + stg * 2 * TB;
     copy_tile<D>(rk, (int64_t)j * KT, H, w, lane, st);
     copy_tile<D>(rv, (int64_t)j * KT, H, w, lane, st + TB);
   };
@@ -536,13 +544,15 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttArgs a) {
   // tiles wholly below Sk (keys past Sk must get P = 0 here: their zero K rows would not cancel
   // an overflowing P)
   const int nfull = VM == 0 ? (int)(kend / KT) : 0;
-  if (ntiles > 0) issue(0);
-  auto step = [&](int j, auto full) {
+  if (ntiles > 0) issue(0, 0);
+  auto step = [&](int j, auto full, auto stage) {  // stage as in the forward
     constexpr bool FULL = decltype(full)::value;
+    constexpr int STG = decltype(stage)::value;
+    const int stg = STG >= 0 ? STG : (j & 1);
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
-    if (j + 1 < ntiles) issue(j + 1);
-    const uint8_t* sk = smem + (j & 1) * 2 * TB;
+    if (j + 1 < ntiles) issue(j + 1, stg ^ 1);
+    const uint8_t* sk = smem + stg * 2 * TB;
     const uint8_t* sv = sk + TB;
     const int64_t key0 = (int64_t)j * KT;
     u32x4 db[2][2];  // dS operand [32-key block][qt]
@@ -593,9 +603,16 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttArgs a) {
         qacc[dt][1] = E::mfma16(E::as8(kt_), E::as8(db[kb2][1]), qacc[dt][1]);
       }
   };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using SR = std::integral_constant<int, -1>;
   int j = 0;
-  for (; j < nfull; ++j) step(j, std::true_type{});
-  for (; j < ntiles; ++j) step(j, std::false_type{});
+  for (; j + 1 < nfull; j += 2) {
+    step(j, std::true_type{}, S0{});
+    step(j + 1, std::true_type{}, S1{});
+  }
+  for (; j < nfull; ++j) step(j, std::true_type{}, SR{});
+  for (; j < ntiles; ++j) step(j, std::false_type{}, SR{});
   const float sc = a.scale;
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
