@@ -473,18 +473,44 @@ __global__ void g_colgrad_kernel(const uint16_t* __restrict__ src, int64_t M, in
 
 // ---------------------------------------------------------------------------------------------
 // gelu_tanh, src/layers/linear.jl:61-68 (f32 math, 16-bit in/out; gelu_f in common.h)
+// Streaming passes: with 16-byte aligned operands a thread takes 8 elements per 16-byte load
+// (nontemporal, grid-stride), the rest (n mod 8, or unaligned operands) one element per thread.
 template <int ELT>
-__global__ void gelu_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ y, int64_t n) {
+__global__ __launch_bounds__(256) void gelu_kernel(const uint16_t* __restrict__ x,
+                                                   uint16_t* __restrict__ y, int64_t n, int vec) {
   using E = Elt<ELT>;
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) y[i] = (uint16_t)E::bits(gelu_f(E::to_f32(x[i])));
+  const int64_t nv = vec ? n / 8 : 0;
+  const int64_t step = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nv; i += step) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x) + i);
+    u32x4 o;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      o[k] = E::bits(gelu_f(E::lo(v[k]))) | (E::bits(gelu_f(E::hi(v[k]))) << 16);
+    __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(y) + i);
+  }
+  for (int64_t i = nv * 8 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step)
+    y[i] = (uint16_t)E::bits(gelu_f(E::to_f32(x[i])));
 }
 template <int ELT>
-__global__ void gelu_bwd_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ dy,
-                                uint16_t* __restrict__ dx, int64_t n) {
+__global__ __launch_bounds__(256) void gelu_bwd_kernel(const uint16_t* __restrict__ x,
+                                                       const uint16_t* __restrict__ dy,
+                                                       uint16_t* __restrict__ dx, int64_t n, int vec) {
   using E = Elt<ELT>;
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) dx[i] = (uint16_t)E::bits(E::to_f32(dy[i]) * gelu_grad_f(E::to_f32(x[i])));
+  const int64_t nv = vec ? n / 8 : 0;
+  const int64_t step = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nv; i += step) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x) + i);
+    const u32x4 d = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(dy) + i);
+    u32x4 o;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      o[k] = E::bits(E::lo(d[k]) * gelu_grad_f(E::lo(v[k]))) |
+             (E::bits(E::hi(d[k]) * gelu_grad_f(E::hi(v[k]))) << 16);
+    __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(dx) + i);
+  }
+  for (int64_t i = nv * 8 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step)
+    dx[i] = (uint16_t)E::bits(E::to_f32(dy[i]) * gelu_grad_f(E::to_f32(x[i])));
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -594,6 +620,12 @@ static WsLayout ws_layout(int64_t M, int64_t K, int64_t N, int64_t r, int which,
 }
 
 static int grid1(int64_t n, int bs = 256) { return (int)ceil_div(n, bs); }
+// grid of a grid-stride streaming pass over n 16-bit elements (8 per thread and step): enough
+// blocks to fill the GPU several times over, fewer for small n
+static int grid_stream(int64_t n) {
+  const int64_t b = ceil_div(ceil_div(n, 8), 256);
+  return (int)(b < 8192 ? (b > 0 ? b : 1) : 8192);
+}
 
 template <bool SCALED, int ROWS>
 static void launch_rowproj_t(int elt, int rt, const uint16_t* src, int64_t M, int64_t Kd,
@@ -990,8 +1022,9 @@ static int gelu_impl(int elt, const char* fn, const void* x, void* y, int64_t n,
   if (n == 0) return REELS_HIP_OK;
   if (!x || !y) return fail(REELS_HIP_EINVAL, std::string(fn) + ": " "NULL pointer");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int vec = aligned16(x) && aligned16(y);
   { TraceScope _ts(st, "gelu_kernel");
-    with_elt(elt, [&](auto e) { gelu_kernel<decltype(e)::value><<<grid1(n), 256, 0, st>>>(static_cast<const uint16_t*>(x), static_cast<uint16_t*>(y), n); }); }
+    with_elt(elt, [&](auto e) { gelu_kernel<decltype(e)::value><<<grid_stream(n), 256, 0, st>>>(static_cast<const uint16_t*>(x), static_cast<uint16_t*>(y), n, vec); }); }
   return check_launch("gelu_kernel");
 }
 
@@ -1002,10 +1035,11 @@ static int gelu_bwd_impl(int elt, const char* fn, const void* x, const void* dy,
   if (n == 0) return REELS_HIP_OK;
   if (!x || !dy || !dx) return fail(REELS_HIP_EINVAL, std::string(fn) + ": " "NULL pointer");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int vec = aligned16(x) && aligned16(dy) && aligned16(dx);
   { TraceScope _ts(st, "gelu_bwd_kernel");
-    with_elt(elt, [&](auto e) { gelu_bwd_kernel<decltype(e)::value><<<grid1(n), 256, 0, st>>>(static_cast<const uint16_t*>(x),
+    with_elt(elt, [&](auto e) { gelu_bwd_kernel<decltype(e)::value><<<grid_stream(n), 256, 0, st>>>(static_cast<const uint16_t*>(x),
                                               static_cast<const uint16_t*>(dy),
-                                              static_cast<uint16_t*>(dx), n); }); }
+                                              static_cast<uint16_t*>(dx), n, vec); }); }
   return check_launch("gelu_bwd_kernel");
 }
 

@@ -292,6 +292,22 @@ def test_gelu_tanh(dev, n):
     assert np.mean(dx == dxo) > 0.95
 
 
+def test_gelu_tanh_unaligned_operands(dev):
+    """Operands that are not 16-byte aligned take the one-element-per-thread path: the same bits
+    as the 16-byte path on aligned copies."""
+    import torch
+    from reels_amd import gelu_tanh, gelu_tanh_backward
+    n = 4099
+    xb = oracle.normal_bf16(711, (n + 1,), 2.0)
+    dyb = oracle.normal_bf16(712, (n + 1,), 1.0)
+    x, dy = to_dev(xb, dev), to_dev(dyb, dev)
+    xu, dyu = x[1:], dy[1:]
+    assert xu.data_ptr() % 16 != 0
+    xa, dya = xu.clone(), dyu.clone()
+    assert torch.equal(gelu_tanh(xu), gelu_tanh(xa))
+    assert torch.equal(gelu_tanh_backward(xu, dyu), gelu_tanh_backward(xa, dya))
+
+
 @pytest.mark.parametrize("K,N", [(8960, 1536), (1536, 8960)])
 def test_tokens_beyond_2gib_of_activations(dev, K, N):
     # 120000 tokens x 8960 bf16 is 2.15 GB: the GEMM whose reduction is 8960 wide (forward for
