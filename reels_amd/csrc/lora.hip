@@ -220,7 +220,9 @@ template <int RT, int ELT>
 __global__ __launch_bounds__(256) void colgrad_kernel(const uint16_t* __restrict__ src, int64_t M,
                                                       int64_t Od, const uint16_t* __restrict__ Lm,
                                                       int ld_lm, int rp, int64_t tokens_per_split,
-                                                      float* __restrict__ part, int ld_part) {
+                                                      float* __restrict__ part, int ld_part,
+                                                      float c, float* __restrict__ out, int r,
+                                                      int trans) {
   using E = Elt<ELT>;
   using namespace cg;
   __shared__ __attribute__((aligned(16))) uint16_t ssrc[TM * SROW];
@@ -337,7 +339,15 @@ __global__ __launch_bounds__(256) void colgrad_kernel(const uint16_t* __restrict
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int64_t o = o0 + wave * 32 + (v / 4) * 8 + lhi * 4 + (v % 4);
-      if (o < Od) part[((int64_t)sp * Od + o) * ld_part + j] = acc[t][v];
+      if (o >= Od) continue;
+      if (out == nullptr) {
+        part[((int64_t)sp * Od + o) * ld_part + j] = acc[t][v];
+      } else if (j < r) {
+        // one split: the result itself, as the reduction pass would write it (c (0 + sum))
+        const float val = c * (0.0f + acc[t][v]);
+        if (trans) out[(int64_t)j * Od + o] = val;
+        else out[o * r + j] = val;
+      }
     }
   }
 }
@@ -673,22 +683,27 @@ static int launch_colgrad(int elt, const uint16_t* src, int64_t M, int64_t Od, c
                           int r, int rp, const Split& p, float c, float* part, float* out,
                           bool trans, hipStream_t st) {
   const dim3 grid((unsigned)ceil_div(Od, cg::BO), (unsigned)p.splits);
+  // one split and one rank chunk: the kernel writes the result (no reduction pass)
+  const bool direct = p.splits == 1 && rp <= kRankChunk;
   for (int c0 = 0; c0 < rp; c0 += kRankChunk) {
     const int rpc = rp - c0 < kRankChunk ? rp - c0 : kRankChunk;
     const int rt = (rpc + 31) / 32;
     const uint16_t* Lc = Lm + c0;
     float* pc = part + c0;
+    float* oc = direct ? out : nullptr;
+    const int tr = trans ? 1 : 0;
     {
       TraceScope _ts(st, rt <= 1 ? "colgrad_kernel<1>" : rt == 2 ? "colgrad_kernel<2>" : "colgrad_kernel<4>");
       with_elt(elt, [&](auto e) {
         constexpr int T = decltype(e)::value;
-        if (rt <= 1) colgrad_kernel<1, T><<<grid, 256, 0, st>>>(src, M, Od, Lc, rp, rpc, p.tps, pc, rp);
-        else if (rt == 2) colgrad_kernel<2, T><<<grid, 256, 0, st>>>(src, M, Od, Lc, rp, rpc, p.tps, pc, rp);
-        else colgrad_kernel<4, T><<<grid, 256, 0, st>>>(src, M, Od, Lc, rp, rpc, p.tps, pc, rp);
+        if (rt <= 1) colgrad_kernel<1, T><<<grid, 256, 0, st>>>(src, M, Od, Lc, rp, rpc, p.tps, pc, rp, c, oc, r, tr);
+        else if (rt == 2) colgrad_kernel<2, T><<<grid, 256, 0, st>>>(src, M, Od, Lc, rp, rpc, p.tps, pc, rp, c, oc, r, tr);
+        else colgrad_kernel<4, T><<<grid, 256, 0, st>>>(src, M, Od, Lc, rp, rpc, p.tps, pc, rp, c, oc, r, tr);
       });
     }
     if (int rc = check_launch("colgrad_kernel")) return rc;
   }
+  if (direct) return REELS_HIP_OK;
   return launch_reduce_partials(part, p.splits, Od, rp, r, c, out, trans, st);
 }
 
