@@ -216,20 +216,38 @@ constexpr int SROW = BO + 16;     // padded LDS row (elements)
 constexpr int LROW = 128 + 16;    // Lm tile row (rp <= 128)
 }  // namespace cg
 
+// One launch runs up to two such passes (dA over x with u, dB over dy with h): job 0 takes the
+// first nb0 blocks. A job's blocks are (column block, split), column block fastest.
+struct CgJob {
+  const uint16_t* src;  // [M][Od]
+  const uint16_t* Lm;   // [M][ld_lm]
+  float* part;          // partials, or NULL with out set
+  float* out;           // one split: c * sum written here ([Od][r], or [r][Od] with trans)
+  int64_t Od, tps;      // output rows; tokens per split
+  int nbx, trans;       // column blocks
+};
+
 template <int RT, int ELT>
-__global__ __launch_bounds__(256) void colgrad_kernel(const uint16_t* __restrict__ src, int64_t M,
-                                                      int64_t Od, const uint16_t* __restrict__ Lm,
-                                                      int ld_lm, int rp, int64_t tokens_per_split,
-                                                      float* __restrict__ part, int ld_part,
-                                                      float c, float* __restrict__ out, int r,
-                                                      int trans) {
+__global__ __launch_bounds__(256) void colgrad_kernel(CgJob j0, CgJob j1, int nb0, int64_t M,
+                                                      int ld_lm, int rp, int ld_part, float c,
+                                                      int r) {
   using E = Elt<ELT>;
   using namespace cg;
   __shared__ __attribute__((aligned(16))) uint16_t ssrc[TM * SROW];
   __shared__ __attribute__((aligned(16))) uint16_t slm[TM * LROW];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t o0 = (int64_t)blockIdx.x * BO;
-  const int sp = blockIdx.y;
+  const bool second = (int)blockIdx.x >= nb0;
+  const int bj = second ? (int)blockIdx.x - nb0 : (int)blockIdx.x;
+  const uint16_t* __restrict__ src = second ? j1.src : j0.src;
+  const uint16_t* __restrict__ Lm = second ? j1.Lm : j0.Lm;
+  float* __restrict__ part = second ? j1.part : j0.part;
+  float* __restrict__ out = second ? j1.out : j0.out;
+  const int64_t Od = second ? j1.Od : j0.Od;
+  const int64_t tokens_per_split = second ? j1.tps : j0.tps;
+  const int nbx = second ? j1.nbx : j0.nbx;
+  const int trans = second ? j1.trans : j0.trans;
+  const int64_t o0 = (int64_t)(bj % nbx) * BO;
+  const int sp = bj / nbx;
   const int64_t mbeg = (int64_t)sp * tokens_per_split;
   const int64_t mend = (mbeg + tokens_per_split < M) ? mbeg + tokens_per_split : M;
   f32x16 acc[RT];
@@ -679,32 +697,59 @@ static int launch_rowproj(int elt, const uint16_t* src, int64_t M, int64_t Kd, c
 
 // Lm [M][rp]; partials part[sp][Od][rp], one launch per rank chunk of 128, then the fixed-order
 // reduction over the splits
-static int launch_colgrad(int elt, const uint16_t* src, int64_t M, int64_t Od, const uint16_t* Lm,
-                          int r, int rp, const Split& p, float c, float* part, float* out,
-                          bool trans, hipStream_t st) {
-  const dim3 grid((unsigned)ceil_div(Od, cg::BO), (unsigned)p.splits);
-  // one split and one rank chunk: the kernel writes the result (no reduction pass)
-  const bool direct = p.splits == 1 && rp <= kRankChunk;
+// One gradient pass over [M][Od] operands: out = c * src^T Lm (trans: its transpose), through
+// split partials and the reduction pass, or written directly with one split.
+struct CgPass {
+  const uint16_t* src;
+  int64_t Od;
+  const uint16_t* Lm;
+  Split sp;
+  float* part;
+  float* out;
+  bool trans;
+};
+
+// dA and dB passes (either may be absent: src NULL) in one colgrad launch per rank chunk, then
+// the reduction passes of those that need one
+static int launch_colgrad2(int elt, int64_t M, int r, int rp, float c, const CgPass& pa,
+                           const CgPass& pb, hipStream_t st) {
+  const CgPass* ps[2] = {pa.src ? &pa : nullptr, pb.src ? &pb : nullptr};
+  if (!ps[0] && !ps[1]) return REELS_HIP_OK;
+  if (!ps[0]) { ps[0] = ps[1]; ps[1] = nullptr; }
+  bool direct[2];
+  for (int i = 0; i < 2; ++i) direct[i] = ps[i] && ps[i]->sp.splits == 1 && rp <= kRankChunk;
   for (int c0 = 0; c0 < rp; c0 += kRankChunk) {
     const int rpc = rp - c0 < kRankChunk ? rp - c0 : kRankChunk;
     const int rt = (rpc + 31) / 32;
-    const uint16_t* Lc = Lm + c0;
-    float* pc = part + c0;
-    float* oc = direct ? out : nullptr;
-    const int tr = trans ? 1 : 0;
+    CgJob j[2] = {};
+    int nb[2] = {0, 0};
+    for (int i = 0; i < 2; ++i) {
+      if (!ps[i]) continue;
+      const CgPass& q = *ps[i];
+      j[i].src = q.src; j[i].Lm = q.Lm + c0; j[i].part = q.part + c0;
+      j[i].out = direct[i] ? q.out : nullptr;
+      j[i].Od = q.Od; j[i].tps = q.sp.tps; j[i].trans = q.trans ? 1 : 0;
+      j[i].nbx = (int)ceil_div(q.Od, cg::BO);
+      nb[i] = j[i].nbx * q.sp.splits;
+    }
+    const unsigned grid = (unsigned)(nb[0] + nb[1]);
     {
       TraceScope _ts(st, rt <= 1 ? "colgrad_kernel<1>" : rt == 2 ? "colgrad_kernel<2>" : "colgrad_kernel<4>");
       with_elt(elt, [&](auto e) {
         constexpr int T = decltype(e)::value;
-        if (rt <= 1) colgrad_kernel<1, T><<<grid, 256, 0, st>>>(src, M, Od, Lc, rp, rpc, p.tps, pc, rp, c, oc, r, tr);
-        else if (rt == 2) colgrad_kernel<2, T><<<grid, 256, 0, st>>>(src, M, Od, Lc, rp, rpc, p.tps, pc, rp, c, oc, r, tr);
-        else colgrad_kernel<4, T><<<grid, 256, 0, st>>>(src, M, Od, Lc, rp, rpc, p.tps, pc, rp, c, oc, r, tr);
+        if (rt <= 1) colgrad_kernel<1, T><<<grid, 256, 0, st>>>(j[0], j[1], nb[0], M, rp, rpc, rp, c, r);
+        else if (rt == 2) colgrad_kernel<2, T><<<grid, 256, 0, st>>>(j[0], j[1], nb[0], M, rp, rpc, rp, c, r);
+        else colgrad_kernel<4, T><<<grid, 256, 0, st>>>(j[0], j[1], nb[0], M, rp, rpc, rp, c, r);
       });
     }
     if (int rc = check_launch("colgrad_kernel")) return rc;
   }
-  if (direct) return REELS_HIP_OK;
-  return launch_reduce_partials(part, p.splits, Od, rp, r, c, out, trans, st);
+  for (int i = 0; i < 2; ++i) {
+    if (!ps[i] || direct[i]) continue;
+    const CgPass& q = *ps[i];
+    if (int rc = launch_reduce_partials(q.part, q.sp.splits, q.Od, rp, r, c, q.out, q.trans, st)) return rc;
+  }
+  return REELS_HIP_OK;
 }
 
 // dst [rows][cols_dst] (row stride ld_dst) from src [rows][cols] (row stride ld_src), zeros past cols
@@ -995,11 +1040,7 @@ static int i8lora_bwd_impl(int elt, const char* fn, const void* dy, const void* 
     g.M = M; g.Ncols = K; g.Kred = N; g.ldq = K; g.rp = r > 0 ? p.rp : 0; g.c = lora_scale;
     if ((rc = launch_i8gemm(1, elt, g, st))) return rc;
   }
-  // 3. dA = c x^T u ; dB = c (dy^T h)^T
-  if (dA) {
-    if ((rc = launch_colgrad(elt, xb, M, K, u, (int)r, p.rp, p.sa, lora_scale,
-                             reinterpret_cast<float*>(ws + w.pa), dA, false, st))) return rc;
-  }
+  // 3. dA = c x^T u ; dB = c (dy^T h)^T, in one launch (h recomputed first when not given)
   if (dB) {
     if (!hh && p.skinny) {
       // recompute h exactly as the few-token forward computed it (same blocks, same split order)
@@ -1025,8 +1066,12 @@ static int i8lora_bwd_impl(int elt, const char* fn, const void* dy, const void* 
       if ((rc = launch_rowproj(elt, xb, M, K, at, (int)r, p.rp, hw, nullptr, nullptr, st))) return rc;
       hh = hw;
     }
-    if ((rc = launch_colgrad(elt, dyb, M, N, hh, (int)r, p.rp, p.sb, lora_scale,
-                             reinterpret_cast<float*>(ws + w.pb), dB, true, st))) return rc;
+  }
+  {
+    CgPass ga{}, gb{};
+    if (dA) ga = CgPass{xb, K, u, p.sa, reinterpret_cast<float*>(ws + w.pa), dA, false};
+    if (dB) gb = CgPass{dyb, N, hh, p.sb, reinterpret_cast<float*>(ws + w.pb), dB, true};
+    if ((rc = launch_colgrad2(elt, M, (int)r, p.rp, lora_scale, ga, gb, st))) return rc;
   }
   return REELS_HIP_OK;
 }
