@@ -233,12 +233,16 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttArgs a) {
     }
     // online softmax per query (base 2): masked scores are -inf and get probability 0. The
     // maximum is taken on the raw scores (the scale sl2 is positive) and each exponent is one
-    // fma, s sl2 - m.
-    u32x4 pb[2][2];  // P operand: [32-key block][qt]
+    // fma, s sl2 - m. The running maximum m is only moved (and O and l rescaled) when a query's
+    // tile maximum exceeds it by more than TAU = 8 somewhere in the wave (one wave-uniform
+    // branch); otherwise P = 2^(s sl2 - m) <= 2^8, exact in the sums and in the lse, and the
+    // rounding of P to the element type is relative as before.
+    constexpr float TAU = 8.0f;
+    float mt[2];
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
       const int64_t qi = q0 + 16 * qt + l16;
-      float mt = -INFINITY;
+      float m = -INFINITY;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
@@ -246,15 +250,29 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttArgs a) {
           const int64_t kj = key0 + 16 * kt + 4 * g + v;
           const float x = att_visible_tile<VM, FULL>(a, qi, kj) ? s[kt][qt][v] : -INFINITY;
           s[kt][qt][v] = x;
-          mt = fmaxf(mt, x);
+          m = fmaxf(m, x);
         }
-      mt = wave_max16(mt) * sl2;
-      const float mnew = fmaxf(mrun[qt], mt);
-      // Without a mask every query in range sees key 0 in the first tile, so its maximum is
-      // finite from then on and exp2(-inf - m) is 0: the guards below matter only with a mask
-      // (a query with no visible key yet: nothing accumulated, keep the factor finite)
-      const float alpha = (VM == 2 && mnew == -INFINITY) ? 1.0f : ex2(mrun[qt] - mnew);
-      mrun[qt] = mnew;
+      mt[qt] = wave_max16(m) * sl2;
+    }
+    // a query with no visible key so far keeps m = -inf (nothing accumulated); the first tile
+    // always moves m (-inf + TAU < any finite maximum)
+    if (__builtin_amdgcn_ballot_w64((mt[0] > mrun[0] + TAU) || (mt[1] > mrun[1] + TAU))) {
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+        const float mnew = fmaxf(mrun[qt], mt[qt]);
+        const float alpha = (VM == 2 && mnew == -INFINITY) ? 1.0f : ex2(mrun[qt] - mnew);
+        mrun[qt] = mnew;
+        lrun[qt] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) oacc[dt][qt][v] *= alpha;
+      }
+    }
+    u32x4 pb[2][2];  // P operand: [32-key block][qt]
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      const float mu = mrun[qt];
       float ps = 0.0f;
       float p[4][4];
 #pragma unroll
@@ -262,14 +280,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttArgs a) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const float x = s[kt][qt][v];
-          p[kt][v] = (VM == 2 && x == -INFINITY) ? 0.0f : ex2(__builtin_fmaf(x, sl2, -mnew));
+          p[kt][v] = (VM == 2 && x == -INFINITY) ? 0.0f : ex2(__builtin_fmaf(x, sl2, -mu));
           ps += p[kt][v];
         }
-      lrun[qt] = lrun[qt] * alpha + ps;
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) oacc[dt][qt][v] *= alpha;
+      lrun[qt] += ps;
 #pragma unroll
       for (int kb2 = 0; kb2 < 2; ++kb2) {
         pb[kb2][qt][0] = E::pack2_fast(p[2 * kb2][0], p[2 * kb2][1]);
