@@ -17,6 +17,11 @@ struct GemmArgs {
   int64_t M, Ncols, Kred, ldq;
   int rp;                  // LoRA rank (multiple of 16, 0 = none)
   float c;                 // LoRA scale alpha / r
+  // bfgemm only: the reduction split over ksplit workgroups per tile (0 or 1 = none); each writes
+  // its f32 partial to part [ksplit][M][Ncols] (the first split's with c L R^T added) and a
+  // reduction pass sums them in split order, adds the bias and rounds once
+  int ksplit;
+  float* part;
 };
 
 // mode 0 = FWD (out = s * act q^T + c L R^T + bias), 1 = DX (out = act q + c L R^T, or
@@ -29,6 +34,9 @@ int launch_i8gemm(int mode, int elt, const GemmArgs& a, hipStream_t st);
 // unused. Needs Kred % 64 == 0, 16-byte aligned operands and a weight below 2^31 bytes
 // (bfgemm_supported); any token count (split into chunks of activations below 2^31 bytes).
 bool bfgemm_supported(int64_t M, int64_t Ncols, int64_t Kred);
+// reduction splits for token counts whose 256 x 256 tiles leave most CUs idle (1 = none): about
+// one round of 256 workgroups, at least 4 reduction steps of 64 per split
+int bfgemm_splits(int64_t M, int64_t Ncols, int64_t Kred);
 // mode only labels the trace record ("bfgemm_kernel<0>" forward, "<1>" dX)
 int launch_bfgemm(int mode, int elt, const GemmArgs& a, const uint16_t* wd, hipStream_t st);
 
@@ -45,7 +53,11 @@ int launch_dequant_transpose(int elt, const int8_t* q, int64_t ldq, const float*
 // of each tile (split order). mode 0 = FWD (act = x, rows of q are outputs, lw = A [Kred][rp]
 // zero-padded), 1 = DX (act = dy, rows of q are the reduction, lw = B [r][Kred], s = the
 // reduction's scale).
-constexpr int64_t kSkinnyMaxTokens = 512;
+// up to 320 tokens (four 80-token blocks), or 1024 on weights of at most 4M elements; above,
+// the dequantized-weight GEMM with split reductions is faster (512 tokens on 5120 x 5120: 86
+// against 120 us)
+constexpr int64_t kSkinnyMaxTokens = 320;
+constexpr int64_t kSkinnySmallWeightTokens = 1024;
 constexpr int64_t kSkinnyTargetBlocks = 256;  // about one block per CU
 struct SkinnyPlan {
   int T;   // token tiles of 16 per block

@@ -564,7 +564,9 @@ constexpr int GM = 4;
 // (this GEMM: +3.5% over the same kernel on 32 x 32 tiles). Lane l supplies row l % 16 of both
 // operands with k = 8 (l / 16) + (0..7) (any k order shared by the two operands gives the same
 // sum); D register v of lane l is output column 4 (l / 16) + v, token l % 16 of the tile.
-template <int ELT>
+// SPLIT: the workgroup takes one of a.ksplit reduction ranges of its tile and writes an f32
+// partial (a separate instantiation, so the unsplit kernel's registers stay as they are)
+template <int ELT, bool SPLIT>
 __global__ __launch_bounds__(512)
 void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int tiles_m) {
   using E = Elt<ELT>;
@@ -578,10 +580,12 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
   const int64_t M = a.M, Ncols = a.Ncols, Kred = a.Kred;
 
   const int nt = tiles_n * tiles_m;
+  const int ks = SPLIT ? a.ksplit : 1;  // reduction splits: a tile's are consecutive
   const int b = blockIdx.x;
   const int xcd = b & 7, idx = b >> 3;
-  const int lo = nt >> 3, rem = nt & 7;
-  const int logical = xcd * lo + (xcd < rem ? xcd : rem) + idx;
+  const int lo = (nt * ks) >> 3, rem = (nt * ks) & 7;
+  const int lall = xcd * lo + (xcd < rem ? xcd : rem) + idx;
+  const int logical = lall / ks, split = lall - logical * ks;
   const int group = GM * tiles_n;
   const int g = logical / group;
   const int first_m = g * GM;
@@ -590,6 +594,10 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
   const int64_t m0 = (int64_t)(first_m + within % gm) * BM;
   const int64_t n0 = (int64_t)(within / gm) * BN;
 
+  // this workgroup's reduction steps [kb, kb + nk) of 64
+  const int nkt = (int)(Kred / BK);
+  const int kb = (int)((int64_t)split * nkt / ks);
+  const int nk = (int)((int64_t)(split + 1) * nkt / ks) - kb;
   const i32x4 ract = buffer_rsrc(a.act, (uint32_t)(M * Kred * 2));
   const i32x4 rw = buffer_rsrc(wd, (uint32_t)(Ncols * Kred * 2));
   uint32_t voa[4], vow[4];  // copies i: rows (w*4+i)*8 + lane/8 of each tile, 16 bytes per lane
@@ -599,11 +607,10 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
     const int c = (lane & 7) ^ bf_swz(row);
     const int64_t m = (m0 + row < M) ? m0 + row : M - 1;
     const int64_t n = (n0 + row < Ncols) ? n0 + row : Ncols - 1;
-    voa[i] = (uint32_t)((m * Kred + c * 8) * 2);
-    vow[i] = (uint32_t)((n * Kred + c * 8) * 2);
+    voa[i] = (uint32_t)((m * Kred + (int64_t)kb * BK + c * 8) * 2);
+    vow[i] = (uint32_t)((n * Kred + (int64_t)kb * BK + c * 8) * 2);
   }
   const i32x4 rnone = buffer_rsrc(a.act, 0u);  // zero records: a copy through it reads nothing
-  const int nk = (int)(Kred / BK);
   // LDS: activation ring of 3 stages [0, 96 KiB), weight ring of 2 stages [96, 160 KiB); step kt
   // uses activation stage kt % 3 and weight stage kt % 2
   auto abase = [&](int kt) { return smem + (kt % 3) * ACT; };
@@ -621,7 +628,7 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
   // 2-3 R; copy i of wave w fills 1 KiB = 16 rows). A 16 x 32 fragment is then 1 KiB of
   // contiguous LDS. Higher ranks read L and R from global memory in the epilogue.
   const int rp = a.rp;
-  const bool lora = rp > 0 && a.L != nullptr;
+  const bool lora = rp > 0 && a.L != nullptr && split == 0;  // split 0 carries the LoRA term
   const bool lr_lds = lora && rp <= 32;
   auto issue_lr = [&](int kt, int k) {  // copy k (0..3) into activation stage kt
     const bool isr = k >= 2;
@@ -773,6 +780,20 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
   // acc + c lor + bias, rounded once, into the staging tile
   auto finish = [&](int ti, const f32x4* lor) {
     const int nloc = wn * 64 + ti * 16 + lq * 4;  // this lane's four output columns
+    if constexpr (SPLIT) {
+      // split partial: acc (+ c lor in split 0), f32, 16 bytes per lane and token
+#pragma unroll
+      for (int tj = 0; tj < 8; ++tj) {
+        const int64_t m = m0 + wm * 128 + tj * 16 + l16, n = n0 + nloc;
+        f32x4 o = acc[ti][tj];
+        if (lora) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) o[v] += a.c * lor[tj][v];
+        }
+        if (m < M && n < Ncols) *reinterpret_cast<f32x4*>(a.part + ((int64_t)split * M + m) * Ncols + n) = o;
+      }
+      return;
+    }
     const float bs[4] = {E::lo(braw[ti][0]), E::hi(braw[ti][0]), E::lo(braw[ti][1]), E::hi(braw[ti][1])};
 #pragma unroll
     for (int tj = 0; tj < 8; ++tj) {
@@ -830,6 +851,7 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
       finish(ti, lor);
     }
   }
+  if constexpr (SPLIT) return;  // the partials went straight to global memory
   __syncthreads();
 #pragma unroll 4
   for (int i = 0; i < 16; ++i) {
@@ -840,6 +862,39 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
       *reinterpret_cast<u32x4*>(a.out + m * Ncols + n) = v;
     }
   }
+}
+
+// out = rnd(sum over splits of part[sp][m][n] (split order) + bias[n]) for the split bf16 GEMM;
+// four outputs per thread and step, grid-stride
+template <int ELT>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, int ks,
+                                                            int64_t M, int64_t Ncols,
+                                                            const uint16_t* __restrict__ bias,
+                                                            uint16_t* __restrict__ out) {
+  using E = Elt<ELT>;
+  const int64_t n4 = Ncols / 4, total = M * n4, plane = M * Ncols;
+  const int64_t step = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += step) {
+    const int64_t m = i / n4, n = (i - m * n4) * 4;
+    const float* p = part + m * Ncols + n;
+    f32x4 sum = *reinterpret_cast<const f32x4*>(p);
+    for (int sp = 1; sp < ks; ++sp) sum += *reinterpret_cast<const f32x4*>(p + sp * plane);
+    if (bias != nullptr) {
+      const u32x2 b = *reinterpret_cast<const u32x2*>(bias + n);
+      sum[0] += E::lo(b[0]); sum[1] += E::hi(b[0]); sum[2] += E::lo(b[1]); sum[3] += E::hi(b[1]);
+    }
+    *reinterpret_cast<u32x2*>(out + m * Ncols + n) = u32x2{E::pack2_fast(sum[0], sum[1]), E::pack2_fast(sum[2], sum[3])};
+  }
+}
+
+int bfgemm_splits(int64_t M, int64_t Ncols, int64_t Kred) {
+  const int64_t tiles = ceil_div(M, bfg::BM) * ceil_div(Ncols, bfg::BN);
+  if (tiles <= 0 || tiles >= 128) return 1;
+  int64_t s = (256 + tiles / 2) / tiles;
+  const int64_t nk = Kred / bfg::BK;
+  if (s > nk / 4) s = nk / 4;
+  if (s > 16) s = 16;
+  return s < 2 ? 1 : (int)s;
 }
 
 bool bfgemm_supported(int64_t M, int64_t Ncols, int64_t Kred) {
@@ -853,9 +908,10 @@ int launch_bfgemm(int mode, int elt, const GemmArgs& a, const uint16_t* wd, hipS
   static std::once_flag once;
   static hipError_t attr_err = hipSuccess;
   std::call_once(once, [&] {
-    attr_err = hipFuncSetAttribute((const void*)bfgemm_kernel<REELS_HIP_BF16>, hipFuncAttributeMaxDynamicSharedMemorySize, bfg::LDS);
-    if (attr_err == hipSuccess)
-      attr_err = hipFuncSetAttribute((const void*)bfgemm_kernel<REELS_HIP_F16>, hipFuncAttributeMaxDynamicSharedMemorySize, bfg::LDS);
+    const void* ks[] = {(const void*)bfgemm_kernel<REELS_HIP_BF16, false>, (const void*)bfgemm_kernel<REELS_HIP_F16, false>,
+                        (const void*)bfgemm_kernel<REELS_HIP_BF16, true>, (const void*)bfgemm_kernel<REELS_HIP_F16, true>};
+    for (const void* k : ks)
+      if (attr_err == hipSuccess) attr_err = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, bfg::LDS);
   });
   if (attr_err != hipSuccess)
     return fail(REELS_HIP_EHIP, std::string("bfgemm: hipFuncSetAttribute: ") + hipGetErrorString(attr_err));
@@ -863,6 +919,24 @@ int launch_bfgemm(int mode, int elt, const GemmArgs& a, const uint16_t* wd, hipS
   // activations reach 2 GiB run as consecutive launches over token chunks (multiples of the
   // 256-token tile) with the activation, output and L pointers advanced.
   const int64_t chunk = ((((int64_t)1 << 31) - 1) / (a.Kred * 2)) / bfg::BM * bfg::BM;
+  if (a.ksplit > 1) {
+    // split reduction: few tiles (one chunk of tokens), partials in a.part, then the reduction pass
+    if (a.M > chunk || a.part == nullptr || a.Ncols % 4 != 0)
+      return fail(REELS_HIP_EINVAL, "bfgemm: split reduction needs one token chunk, a partials buffer and Ncols % 4 == 0");
+    const int tn = (int)ceil_div(a.Ncols, bfg::BN), tm = (int)ceil_div(a.M, bfg::BM);
+    { TraceScope _ts(st, mode == 0 ? "bfgemm_kernel<0>" : "bfgemm_kernel<1>");
+      with_elt(elt, [&](auto e) {
+        bfgemm_kernel<decltype(e)::value, true><<<tn * tm * a.ksplit, bfg::NT, bfg::LDS, st>>>(a, wd, tn, tm);
+      }); }
+    if (int rc = check_launch("bfgemm_kernel")) return rc;
+    const int64_t n4 = a.M * (a.Ncols / 4);
+    const unsigned grid = (unsigned)(ceil_div(n4, 256) < 4096 ? ceil_div(n4, 256) : 4096);
+    { TraceScope _ts(st, "splitk_reduce_kernel");
+      with_elt(elt, [&](auto e) {
+        splitk_reduce_kernel<decltype(e)::value><<<grid, 256, 0, st>>>(a.part, a.ksplit, a.M, a.Ncols, a.bias, a.out);
+      }); }
+    return check_launch("splitk_reduce_kernel");
+  }
   for (int64_t m0 = 0; m0 < a.M; m0 += chunk) {
     GemmArgs c = a;
     c.M = (a.M - m0 < chunk) ? a.M - m0 : chunk;
@@ -872,7 +946,7 @@ int launch_bfgemm(int mode, int elt, const GemmArgs& a, const uint16_t* wd, hipS
     const int tn = (int)ceil_div(c.Ncols, bfg::BN), tm = (int)ceil_div(c.M, bfg::BM);
     { TraceScope _ts(st, mode == 0 ? "bfgemm_kernel<0>" : "bfgemm_kernel<1>");
       with_elt(elt, [&](auto e) {
-        bfgemm_kernel<decltype(e)::value><<<tn * tm, bfg::NT, bfg::LDS, st>>>(c, wd, tn, tm);
+        bfgemm_kernel<decltype(e)::value, false><<<tn * tm, bfg::NT, bfg::LDS, st>>>(c, wd, tn, tm);
       }); }
     if (int rc = check_launch("bfgemm_kernel")) return rc;
   }

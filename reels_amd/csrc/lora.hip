@@ -576,6 +576,7 @@ struct Plan {
   Split sa;     // dA: columns of x (K)
   Split sb;     // dB: columns of dy (N)
   SkinnyPlan skf, skb;  // the few-token forward (reduction K) and dX (reduction N)
+  int ksf, ksb;  // deq: reduction splits of the forward and dX GEMMs (1 = none)
 };
 
 // rank chunk of the projection and gradient kernels (their LDS tiles hold 128 rank columns)
@@ -597,12 +598,14 @@ static Plan make_plan(int64_t M, int64_t K, int64_t N, int64_t r, bool ptrs_alig
   }
   p.sa = split_for(M, K);
   p.sb = split_for(M, N);
+  p.ksf = p.deq && !p.skinny ? bfgemm_splits(M, N, K) : 1;
+  p.ksb = p.deq && !p.skinny ? bfgemm_splits(M, K, N) : 1;
   return p;
 }
 
 // workspace layout (byte offsets, 256-aligned); identical computation for sizing and use
 struct WsLayout {
-  size_t h, u, dys, wd, at, bt, ap, pa, pb, total;
+  size_t h, u, dys, wd, at, bt, ap, pa, pb, kp, total;
 };
 
 static WsLayout ws_layout(int64_t M, int64_t K, int64_t N, int64_t r, int which, const Plan& p) {
@@ -636,7 +639,9 @@ static WsLayout ws_layout(int64_t M, int64_t K, int64_t N, int64_t r, int which,
   w.wd = take(p.deq ? (size_t)N * K * 2 : 0);  // bf16 copy of the dequantized weight
   if (which == REELS_HIP_WS_FWD) {
     w.bt = take(p.fast ? (size_t)N * rp * 2 : 0);
+    w.kp = take(p.ksf > 1 ? (size_t)p.ksf * M * N * 4 : 0);  // split GEMM partials
   } else {
+    w.kp = take(p.ksb > 1 ? (size_t)p.ksb * M * K * 4 : 0);
     w.u = take((size_t)M * rp * 2);
     w.ap = take(p.padded ? (size_t)K * rp * 2 : 0);  // A [K][rp], zeros past r
     w.dys = take(p.fast && !p.deq ? (size_t)M * N * 2 : 0);
@@ -834,7 +839,7 @@ static int i8lora_fwd_impl(int elt, const char* fn, const void* x, const int8_t*
   const bool al = all_aligned({x, q, scales, A, B, y, h_save}) &&
                   (bias == nullptr || (reinterpret_cast<uintptr_t>(bias) & 7u) == 0);
   Plan p = make_plan(M, K, N, r, al);
-  if (noalloc) p.deq = false;
+  if (noalloc) { p.deq = false; p.ksf = p.ksb = 1; }
   WsLayout w = ws_layout(M, K, N, r, REELS_HIP_WS_FWD, p);
   if (noalloc) {
     if (w.total > kScratchBytes)
@@ -906,6 +911,7 @@ static int i8lora_fwd_impl(int elt, const char* fn, const void* x, const int8_t*
     uint16_t* wd = reinterpret_cast<uint16_t*>(ws + w.wd);
     if ((rc = launch_dequant_rows(elt, q, K, scales, N, K, wd, st))) return rc;
     g.q = nullptr; g.colscale = nullptr;
+    g.ksplit = p.ksf; g.part = reinterpret_cast<float*>(ws + w.kp);
     return launch_bfgemm(0, elt, g, wd, st);
   }
   return launch_i8gemm(0, elt, g, st);
@@ -1018,6 +1024,7 @@ static int i8lora_bwd_impl(int elt, const char* fn, const void* dy, const void* 
       g.act = dyb; g.q = nullptr; g.colscale = nullptr; g.L = r > 0 ? u : nullptr; g.R = Ar;
       g.bias = nullptr; g.out = static_cast<uint16_t*>(dx);
       g.M = M; g.Ncols = K; g.Kred = N; g.ldq = N; g.rp = r > 0 ? p.rp : 0; g.c = lora_scale;
+      g.ksplit = p.ksb; g.part = reinterpret_cast<float*>(ws + w.kp);
       if ((rc = launch_bfgemm(1, elt, g, wt, st))) return rc;
     }
   } else if (r > 0 || (dx && !f16)) {

@@ -98,6 +98,7 @@ def check(dev, cs, label):
     (65, 48, 80, 16, False),        # K not a multiple of 64
     (50, 256, 256, 0, True),        # base-only linear with bias
     (40, 24, 20, 5, True),          # rank 5: generic kernels
+    (400, 2048, 2560, 32, True),    # split reductions in both GEMMs
 ])
 def test_f16_shapes(dev, M, K, N, r, bias):
     check(dev, make_case(M, K, N, r, float(r) if r else 1.0, seed=900 + M + K + N + r, bias=bias),

@@ -100,6 +100,8 @@ def test_reference_gpu_test_shape_ragged(dev):
     (150, 640, 384, 48, True),      # rank 48: LoRA operands read from global memory
     (50, 256, 256, 0, True),        # base-only linear(::DenseLayer) with bias
     (40, 24, 20, 2, True),          # ragged: generic path with bias
+    (400, 2048, 2560, 32, True),    # 20 tiles: reduction split over 8 (forward) and 10 (dX) workgroups
+    (352, 1024, 4608, 24, False),   # split reduction with a padded rank, 36 / 8 tiles
 ])
 def test_shapes(dev, M, K, N, r, bias):
     check_full(dev, make_case(M, K, N, r, float(r) if r else 1.0, seed=M + K + N + r,
