@@ -95,10 +95,11 @@ size_t reels_hip_i8lora_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t
  * with W = bf16(fl32(q * s)) written into the workspace once per call when K and N are multiples
  * of 64 and there are many tokens (the reference's _materialize_weight, quantization.jl:54-64);
  * otherwise W = q * s exact with s[n] applied to the f32 sum: K or N not a multiple of 64, and the
- * few-token path (M <= 320, or M <= 1024 with N * K <= 2^22; K and N multiples of 64), which
- * reads the int8 codes without a weight copy. With few 256 x 256 output tiles the GEMM splits its
- * reduction over several workgroups and sums their f32 partials in a fixed order before the one
- * rounding (the workspace holds them). bias may be NULL. r = 0 (A, B NULL) gives the base-only
+ * few-token path (M <= 240, or M <= 1024 with N * K <= 2^22; K and N multiples of 64), which
+ * reads the int8 codes without a weight copy. With few 256 x 256 output tiles (a few hundred
+ * tokens) the GEMM splits its reduction over several workgroups and sums their f32 partials in a
+ * fixed order before the one rounding (the workspace holds them); the forward then multiplies the
+ * int8 codes with s on the f32 sum, no weight copy. bias may be NULL. r = 0 (A, B NULL) gives the base-only
  * linear(::DenseLayer) of src/layers/linear.jl:38-46. h_save ([M][r] or NULL) receives h for the
  * backward. workspace: device memory of reels_hip_i8lora_workspace_bytes(M, K, N, r,
  * REELS_HIP_WS_FWD).

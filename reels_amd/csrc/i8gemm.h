@@ -53,10 +53,10 @@ int launch_dequant_transpose(int elt, const int8_t* q, int64_t ldq, const float*
 // of each tile (split order). mode 0 = FWD (act = x, rows of q are outputs, lw = A [Kred][rp]
 // zero-padded), 1 = DX (act = dy, rows of q are the reduction, lw = B [r][Kred], s = the
 // reduction's scale).
-// up to 320 tokens (four 80-token blocks), or 1024 on weights of at most 4M elements; above,
-// the dequantized-weight GEMM with split reductions is faster (512 tokens on 5120 x 5120: 86
-// against 120 us)
-constexpr int64_t kSkinnyMaxTokens = 320;
+// up to 240 tokens (three 80-token blocks), or 1024 on weights of at most 4M elements; above,
+// the GEMMs with split reductions are faster (5120 x 5120 forward: 256 tokens 78 us few-token,
+// 333 tokens 65 us split; 512 tokens 70 us split against 120 us few-token)
+constexpr int64_t kSkinnyMaxTokens = 240;
 constexpr int64_t kSkinnySmallWeightTokens = 1024;
 constexpr int64_t kSkinnyTargetBlocks = 256;  // about one block per CU
 struct SkinnyPlan {

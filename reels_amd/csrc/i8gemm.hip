@@ -299,7 +299,9 @@ constexpr int NSTAGE = 3;
 constexpr int GM = 4;
 }  // namespace gemm3
 
-template <int MODE, int ELT>
+// SPLIT: one of a.ksplit reduction ranges of the tile, written as an f32 partial (colscale
+// applied, LoRA term in split 0, no bias), as in the bf16 GEMM below
+template <int MODE, int ELT, bool SPLIT>
 __global__ __launch_bounds__(512)
 void i8gemm_v3_kernel(GemmArgs a, int tiles_n, int tiles_m) {
   using E = Elt<ELT>;
@@ -314,10 +316,12 @@ void i8gemm_v3_kernel(GemmArgs a, int tiles_n, int tiles_m) {
   const int64_t M = a.M, Ncols = a.Ncols, Kred = a.Kred;
 
   const int nt = tiles_n * tiles_m;
+  const int ks = SPLIT ? a.ksplit : 1;  // reduction splits: a tile's are consecutive
   const int b = blockIdx.x;
   const int xcd = b & 7, idx = b >> 3;
-  const int lo = nt >> 3, rem = nt & 7;
-  const int logical = xcd * lo + (xcd < rem ? xcd : rem) + idx;
+  const int lo = (nt * ks) >> 3, rem = (nt * ks) & 7;
+  const int lall = xcd * lo + (xcd < rem ? xcd : rem) + idx;
+  const int logical = lall / ks, split = lall - logical * ks;
   const int group = GM * tiles_n;
   const int g = logical / group;
   const int first_m = g * GM;
@@ -326,6 +330,10 @@ void i8gemm_v3_kernel(GemmArgs a, int tiles_n, int tiles_m) {
   const int64_t m0 = (int64_t)(first_m + within % gm) * BM;
   const int64_t n0 = (int64_t)(within / gm) * BN;
 
+  // this workgroup's reduction steps [kb, kb + nk) of 64
+  const int nkt = (int)(Kred / BK);
+  const int kb = (int)((int64_t)split * nkt / ks);
+  const int nk = (int)((int64_t)(split + 1) * nkt / ks) - kb;
   const i32x4 ract = buffer_rsrc(a.act, (uint32_t)(M * Kred * 2));
   const i32x4 rq = buffer_rsrc(a.q, (uint32_t)(Ncols * Kred));
   uint32_t voa[4], vow[2];
@@ -334,7 +342,7 @@ void i8gemm_v3_kernel(GemmArgs a, int tiles_n, int tiles_m) {
     const int row = (w * 4 + i) * 8 + (lane >> 3);
     const int c = (lane & 7) ^ act_swz(row);
     const int64_t m = (m0 + row < M) ? m0 + row : M - 1;
-    voa[i] = (uint32_t)((m * Kred + c * 8) * 2);
+    voa[i] = (uint32_t)((m * Kred + (int64_t)kb * BK + c * 8) * 2);
   }
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
@@ -342,16 +350,15 @@ void i8gemm_v3_kernel(GemmArgs a, int tiles_n, int tiles_m) {
       const int row = (w * 2 + i) * 16 + (lane >> 2);
       const int j = (lane & 3) ^ wf2_swz(row);
       const int64_t n = (n0 + row < Ncols) ? n0 + row : Ncols - 1;
-      vow[i] = (uint32_t)(n * Kred + j * 16);
+      vow[i] = (uint32_t)(n * Kred + (int64_t)kb * BK + j * 16);
     } else {
       const int row = (w * 2 + i) * 4 + (lane >> 4);
       const int c = (lane & 15) ^ wd_swz(row);
       int64_t kc = n0 + c * 16;
       if (kc >= Ncols) kc = Ncols - 16;
-      vow[i] = (uint32_t)(row * a.ldq + kc);
+      vow[i] = (uint32_t)(((int64_t)kb * BK + row) * a.ldq + kc);
     }
   }
-  const int nk = (int)(Kred / BK);
   auto issue = [&](int kt, int stage) {
     uint8_t* base = smem + stage * STAGE;
     const uint32_t sa = (uint32_t)kt * (BK * 2);
@@ -468,7 +475,7 @@ void i8gemm_v3_kernel(GemmArgs a, int tiles_n, int tiles_m) {
   // and written to HBM as whole 512-byte row segments.
   __syncthreads();  // every wave is done reading the last stage
   uint8_t* stile = smem;
-  const int nsteps = a.rp >> 4;
+  const int nsteps = split == 0 ? a.rp >> 4 : 0;  // the LoRA term: in split 0 only
 #pragma unroll
   for (int ti = 0; ti < 2; ++ti) {
     const int64_t nrow = n0 + wn * 64 + ti * 32 + l32;
@@ -504,6 +511,20 @@ void i8gemm_v3_kernel(GemmArgs a, int tiles_n, int tiles_m) {
         if (m >= M) lv = u32x4{0, 0, 0, 0};
         lo = E::mfma32(E::as8(rv), E::as8(lv), lo);
       }
+      if constexpr (SPLIT) {
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int64_t n = nbase + g4 * 8;
+          f32x4 o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int v = g4 * 4 + e;
+            o[e] = sc[v] * acc[ti][tj][v] + (split == 0 ? a.c * lo[v] : 0.0f);
+          }
+          if (m < M && n < Ncols) *reinterpret_cast<f32x4*>(a.part + ((int64_t)split * M + m) * Ncols + n) = o;
+        }
+        continue;
+      }
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
         float o[4];
@@ -519,6 +540,7 @@ void i8gemm_v3_kernel(GemmArgs a, int tiles_n, int tiles_m) {
       }
     }
   }
+  if constexpr (SPLIT) return;  // the partials went straight to global memory
   __syncthreads();
   // 256 rows x 32 chunks of 16 bytes; a wave stores two whole 512-byte row segments per instruction
 #pragma unroll 4
@@ -887,6 +909,16 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   }
 }
 
+static int launch_splitk_reduce(int elt, const GemmArgs& a, hipStream_t st) {
+  const int64_t n4 = a.M * (a.Ncols / 4);
+  const unsigned grid = (unsigned)(ceil_div(n4, 256) < 4096 ? ceil_div(n4, 256) : 4096);
+  { TraceScope _ts(st, "splitk_reduce_kernel");
+    with_elt(elt, [&](auto e) {
+      splitk_reduce_kernel<decltype(e)::value><<<grid, 256, 0, st>>>(a.part, a.ksplit, a.M, a.Ncols, a.bias, a.out);
+    }); }
+  return check_launch("splitk_reduce_kernel");
+}
+
 int bfgemm_splits(int64_t M, int64_t Ncols, int64_t Kred) {
   const int64_t tiles = ceil_div(M, bfg::BM) * ceil_div(Ncols, bfg::BN);
   if (tiles <= 0 || tiles >= 128) return 1;
@@ -929,13 +961,7 @@ int launch_bfgemm(int mode, int elt, const GemmArgs& a, const uint16_t* wd, hipS
         bfgemm_kernel<decltype(e)::value, true><<<tn * tm * a.ksplit, bfg::NT, bfg::LDS, st>>>(a, wd, tn, tm);
       }); }
     if (int rc = check_launch("bfgemm_kernel")) return rc;
-    const int64_t n4 = a.M * (a.Ncols / 4);
-    const unsigned grid = (unsigned)(ceil_div(n4, 256) < 4096 ? ceil_div(n4, 256) : 4096);
-    { TraceScope _ts(st, "splitk_reduce_kernel");
-      with_elt(elt, [&](auto e) {
-        splitk_reduce_kernel<decltype(e)::value><<<grid, 256, 0, st>>>(a.part, a.ksplit, a.M, a.Ncols, a.bias, a.out);
-      }); }
-    return check_launch("splitk_reduce_kernel");
+    return launch_splitk_reduce(elt, a, st);
   }
   for (int64_t m0 = 0; m0 < a.M; m0 += chunk) {
     GemmArgs c = a;
@@ -967,8 +993,10 @@ int launch_i8gemm(int mode, int elt, const GemmArgs& a, hipStream_t st) {
     const int l1 = 2 * STAGE_BYTES, l2 = gemm3::NSTAGE * gemm3::STAGE;
     const void* k1[] = {(const void*)i8gemm_kernel<0, REELS_HIP_BF16>, (const void*)i8gemm_kernel<1, REELS_HIP_BF16>,
                         (const void*)i8gemm_kernel<0, REELS_HIP_F16>, (const void*)i8gemm_kernel<1, REELS_HIP_F16>};
-    const void* k3[] = {(const void*)i8gemm_v3_kernel<0, REELS_HIP_BF16>, (const void*)i8gemm_v3_kernel<1, REELS_HIP_BF16>,
-                        (const void*)i8gemm_v3_kernel<0, REELS_HIP_F16>, (const void*)i8gemm_v3_kernel<1, REELS_HIP_F16>};
+    const void* k3[] = {(const void*)i8gemm_v3_kernel<0, REELS_HIP_BF16, false>, (const void*)i8gemm_v3_kernel<1, REELS_HIP_BF16, false>,
+                        (const void*)i8gemm_v3_kernel<0, REELS_HIP_F16, false>, (const void*)i8gemm_v3_kernel<1, REELS_HIP_F16, false>,
+                        (const void*)i8gemm_v3_kernel<0, REELS_HIP_BF16, true>, (const void*)i8gemm_v3_kernel<1, REELS_HIP_BF16, true>,
+                        (const void*)i8gemm_v3_kernel<0, REELS_HIP_F16, true>, (const void*)i8gemm_v3_kernel<1, REELS_HIP_F16, true>};
     for (const void* k : k1)
       if (attr_err == hipSuccess) attr_err = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, l1);
     for (const void* k : k3)
@@ -976,14 +1004,31 @@ int launch_i8gemm(int mode, int elt, const GemmArgs& a, hipStream_t st) {
   });
   if (attr_err != hipSuccess)
     return fail(REELS_HIP_EHIP, std::string("i8gemm: hipFuncSetAttribute: ") + hipGetErrorString(attr_err));
+  if (v3 && a.ksplit > 1) {
+    // split reduction (few tiles): partials in a.part, then the reduction pass of the bf16 GEMM
+    if (a.part == nullptr || a.Ncols % 4 != 0)
+      return fail(REELS_HIP_EINVAL, "i8gemm: split reduction needs a partials buffer and Ncols % 4 == 0");
+    const int tn = (int)ceil_div(a.Ncols, gemm3::BN), tm = (int)ceil_div(a.M, gemm3::BM);
+    const size_t lds = gemm3::NSTAGE * gemm3::STAGE;
+    {
+      TraceScope _ts(st, mode == 0 ? "i8gemm_v3_kernel<0>" : "i8gemm_v3_kernel<1>");
+      with_elt(elt, [&](auto e) {
+        constexpr int T = decltype(e)::value;
+        if (mode == 0) i8gemm_v3_kernel<0, T, true><<<tn * tm * a.ksplit, gemm3::NT, lds, st>>>(a, tn, tm);
+        else i8gemm_v3_kernel<1, T, true><<<tn * tm * a.ksplit, gemm3::NT, lds, st>>>(a, tn, tm);
+      });
+    }
+    if (int rc = check_launch(mode == 0 ? "i8gemm_v3_kernel<FWD>" : "i8gemm_v3_kernel<DX>")) return rc;
+    return launch_splitk_reduce(elt, a, st);
+  }
   if (v3) {
     const int tn = (int)ceil_div(a.Ncols, gemm3::BN), tm = (int)ceil_div(a.M, gemm3::BM);
     const size_t lds = gemm3::NSTAGE * gemm3::STAGE;
     TraceScope _ts(st, mode == 0 ? "i8gemm_v3_kernel<0>" : "i8gemm_v3_kernel<1>");
     with_elt(elt, [&](auto e) {
       constexpr int T = decltype(e)::value;
-      if (mode == 0) i8gemm_v3_kernel<0, T><<<tn * tm, gemm3::NT, lds, st>>>(a, tn, tm);
-      else i8gemm_v3_kernel<1, T><<<tn * tm, gemm3::NT, lds, st>>>(a, tn, tm);
+      if (mode == 0) i8gemm_v3_kernel<0, T, false><<<tn * tm, gemm3::NT, lds, st>>>(a, tn, tm);
+      else i8gemm_v3_kernel<1, T, false><<<tn * tm, gemm3::NT, lds, st>>>(a, tn, tm);
     });
   } else {
     dim3 grid((unsigned)ceil_div(a.Ncols, BN), (unsigned)ceil_div(a.M, BM));

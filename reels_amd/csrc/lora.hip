@@ -576,7 +576,9 @@ struct Plan {
   Split sa;     // dA: columns of x (K)
   Split sb;     // dB: columns of dy (N)
   SkinnyPlan skf, skb;  // the few-token forward (reduction K) and dX (reduction N)
-  int ksf, ksb;  // deq: reduction splits of the forward and dX GEMMs (1 = none)
+  int ksf, ksb;  // reduction splits of the forward and dX GEMMs (1 = none)
+  bool i8f;      // deq shapes with a split forward: the forward multiplies the int8 codes (no
+                 // weight copy; faster there), dX keeps the dequantized weight (faster there)
 };
 
 // rank chunk of the projection and gradient kernels (their LDS tiles hold 128 rank columns)
@@ -598,8 +600,9 @@ static Plan make_plan(int64_t M, int64_t K, int64_t N, int64_t r, bool ptrs_alig
   }
   p.sa = split_for(M, K);
   p.sb = split_for(M, N);
-  p.ksf = p.deq && !p.skinny ? bfgemm_splits(M, N, K) : 1;
-  p.ksb = p.deq && !p.skinny ? bfgemm_splits(M, K, N) : 1;
+  p.ksf = p.fast && !p.skinny ? bfgemm_splits(M, N, K) : 1;
+  p.ksb = p.fast && !p.skinny ? bfgemm_splits(M, K, N) : 1;
+  p.i8f = p.deq && p.ksf > 1;
   return p;
 }
 
@@ -636,7 +639,8 @@ static WsLayout ws_layout(int64_t M, int64_t K, int64_t N, int64_t r, int which,
   }
   w.h = take((size_t)M * rp * 2);
   w.at = take(r > 0 ? (size_t)r * K * 2 : 0);
-  w.wd = take(p.deq ? (size_t)N * K * 2 : 0);  // bf16 copy of the dequantized weight
+  // bf16 copy of the dequantized weight (dX, and the forward unless it multiplies the codes)
+  w.wd = take(p.deq && !(which == REELS_HIP_WS_FWD && p.i8f) ? (size_t)N * K * 2 : 0);
   if (which == REELS_HIP_WS_FWD) {
     w.bt = take(p.fast ? (size_t)N * rp * 2 : 0);
     w.kp = take(p.ksf > 1 ? (size_t)p.ksf * M * N * 4 : 0);  // split GEMM partials
@@ -839,7 +843,7 @@ static int i8lora_fwd_impl(int elt, const char* fn, const void* x, const int8_t*
   const bool al = all_aligned({x, q, scales, A, B, y, h_save}) &&
                   (bias == nullptr || (reinterpret_cast<uintptr_t>(bias) & 7u) == 0);
   Plan p = make_plan(M, K, N, r, al);
-  if (noalloc) { p.deq = false; p.ksf = p.ksb = 1; }
+  if (noalloc) { p.deq = false; p.i8f = false; p.ksf = p.ksb = 1; }
   WsLayout w = ws_layout(M, K, N, r, REELS_HIP_WS_FWD, p);
   if (noalloc) {
     if (w.total > kScratchBytes)
@@ -907,11 +911,11 @@ static int i8lora_fwd_impl(int elt, const char* fn, const void* x, const int8_t*
   g.act = xb; g.q = q; g.colscale = scales; g.L = h; g.R = bt;
   g.bias = static_cast<const uint16_t*>(bias); g.out = static_cast<uint16_t*>(y);
   g.M = M; g.Ncols = N; g.Kred = K; g.ldq = K; g.rp = r > 0 ? p.rp : 0; g.c = lora_scale;
-  if (p.deq) {
+  g.ksplit = p.ksf; g.part = reinterpret_cast<float*>(ws + w.kp);
+  if (p.deq && !p.i8f) {
     uint16_t* wd = reinterpret_cast<uint16_t*>(ws + w.wd);
     if ((rc = launch_dequant_rows(elt, q, K, scales, N, K, wd, st))) return rc;
     g.q = nullptr; g.colscale = nullptr;
-    g.ksplit = p.ksf; g.part = reinterpret_cast<float*>(ws + w.kp);
     return launch_bfgemm(0, elt, g, wd, st);
   }
   return launch_i8gemm(0, elt, g, st);
@@ -1045,6 +1049,7 @@ static int i8lora_bwd_impl(int elt, const char* fn, const void* dy, const void* 
     g.L = r > 0 ? u : nullptr; g.R = Ar; g.bias = nullptr;
     g.out = static_cast<uint16_t*>(dx);
     g.M = M; g.Ncols = K; g.Kred = N; g.ldq = K; g.rp = r > 0 ? p.rp : 0; g.c = lora_scale;
+    g.ksplit = p.ksb; g.part = reinterpret_cast<float*>(ws + w.kp);
     if ((rc = launch_i8gemm(1, elt, g, st))) return rc;
   }
   // 3. dA = c x^T u ; dB = c (dy^T h)^T, in one launch (h recomputed first when not given)

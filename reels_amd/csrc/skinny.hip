@@ -726,7 +726,7 @@ bool skinny_supported(int64_t M, int64_t K, int64_t N, int rp) {
   // the token-block overrun), the tiles within a counter slot
   const int64_t tb = ceil_div(M, 16 * sk::MAXT);
   const int64_t mx = K > N ? K : N;
-  // up to 320 tokens, or up to 1024 on a small weight (at most 4M elements, which stays in L2
+  // up to 240 tokens, or up to 1024 on a small weight (at most 4M elements, which stays in L2
   // across the token blocks): there one launch beats the 256 x 256-tile GEMM's few tiles
   const bool few = M <= kSkinnyMaxTokens || (M <= kSkinnySmallWeightTokens && N * K <= ((int64_t)1 << 22));
   return M > 0 && few && K % 64 == 0 && N % 64 == 0 &&
