@@ -57,12 +57,16 @@ namespace rowp {
 constexpr int KC = 256, LROW = KC + 8;  // LDS row: 264 bf16 = 528 bytes
 }  // namespace rowp
 
+// With part set (few tokens), blockIdx.y splits the columns: the block streams chunks
+// [c0, c1) of its rows and writes its f32 sums to part[split][m][rp_]; rowproj_reduce_kernel then
+// sums the splits in order and rounds once.
 template <int RT, bool SCALED, int ROWS, int ELT>
 __global__ __launch_bounds__(256) void rowproj_kernel(const uint16_t* __restrict__ src, int64_t M,
                                                       int64_t Kd, const uint16_t* __restrict__ P,
                                                       int r, int rp_, uint16_t* __restrict__ out,
                                                       int ld_out, const float* __restrict__ s,
-                                                      uint16_t* __restrict__ scaled) {
+                                                      uint16_t* __restrict__ scaled,
+                                                      float* __restrict__ part) {
   using E = Elt<ELT>;
   typedef typename E::v8 V8;
   using namespace rowp;
@@ -74,6 +78,8 @@ __global__ __launch_bounds__(256) void rowproj_kernel(const uint16_t* __restrict
   const int l32 = lane & 31, lhi = lane >> 5;
   const int64_t m0 = (int64_t)blockIdx.x * ROWS;
   const int nchunks = (int)((Kd + KC - 1) / KC);
+  const int ks = (int)gridDim.y, sp = (int)blockIdx.y;
+  const int cbeg = (int)((int64_t)sp * nchunks / ks), cend = (int)((int64_t)(sp + 1) * nchunks / ks);
   // loader roles: X chunk = ROWS rows x 32 16-byte chunks, ROWS/8 per thread; P chunk = 32RT
   // rows, 4RT per thread
   // two register stages: the copies of chunks ck + 1 and ck + 2 are in flight while chunk ck is
@@ -93,18 +99,19 @@ __global__ __launch_bounds__(256) void rowproj_kernel(const uint16_t* __restrict
       const_cast<uint16_t*>(r > 0 ? P : src), (short)0, r > 0 ? (int)(r * Kd * 2) : 0, 0x00020000);
   auto load = [&](int ck, XS& rx, PS& rpv) {
     const int64_t k0 = (int64_t)ck * KC;
+    const bool in = ck < cend;  // chunks of the next split read zeros
 #pragma unroll
     for (int i = 0; i < ROWS / 8; ++i) {
       const int row = (t >> 5) + 8 * i, c = t & 31;
       const int64_t k = k0 + c * 8;
-      const uint32_t off = k < Kd ? (uint32_t)((row * Kd + k) * 2) : 0x80000000u;
+      const uint32_t off = (in && k < Kd) ? (uint32_t)((row * Kd + k) * 2) : 0x80000000u;
       rx[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsx, off, 0, 2));  // nt
     }
 #pragma unroll
     for (int i = 0; i < 4 * RT; ++i) {
       const int row = (t >> 5) + 8 * i, c = t & 31;
       const int64_t k = k0 + c * 8;
-      const uint32_t off = k < Kd ? (uint32_t)((row * Kd + k) * 2) : 0x80000000u;
+      const uint32_t off = (in && k < Kd) ? (uint32_t)((row * Kd + k) * 2) : 0x80000000u;
       rpv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsp, off, 0, 0));
     }
   };
@@ -116,7 +123,7 @@ __global__ __launch_bounds__(256) void rowproj_kernel(const uint16_t* __restrict
       *reinterpret_cast<u32x4*>(&xs[row * LROW + c * 8]) = rx[i];
       if (SCALED) {
         const int64_t m = m0 + row, k = k0 + c * 8;
-        if (m < M && k < Kd) {
+        if (m < M && k < Kd && ck < cend) {
           const f32x4 sa = *reinterpret_cast<const f32x4*>(s + k);
           const f32x4 sb = *reinterpret_cast<const f32x4*>(s + k + 4);
           const u32x4 x = rx[i];
@@ -171,9 +178,9 @@ __global__ __launch_bounds__(256) void rowproj_kernel(const uint16_t* __restrict
   };
   // steps in pairs, the second unconditional (with an odd chunk count the last one is all
   // zeros): a branch around it would make the compiler's waits drain both stages
-  load(0, rx0, rp0);
-  load(1, rx1, rp1);
-  for (int ck = 0; ck < nchunks; ck += 2) {
+  load(cbeg, rx0, rp0);
+  load(cbeg + 1, rx1, rp1);
+  for (int ck = cbeg; ck < cend; ck += 2) {
     step(ck, rx0, rp0);
     step(ck + 1, rx1, rp1);
   }
@@ -199,8 +206,27 @@ __global__ __launch_bounds__(256) void rowproj_kernel(const uint16_t* __restrict
     const float sum = red[g][j0][v][ln];
     const int64_t mm = m0 + g * 32 + row;
     const int j = j0 * 32 + col;
-    if (mm < M && j < rp_) out[mm * ld_out + j] = j < r ? (uint16_t)E::bits(sum) : (uint16_t)0;
+    if (part != nullptr) {
+      if (mm < M && j < rp_) part[((int64_t)sp * M + mm) * rp_ + j] = sum;
+    } else {
+      if (mm < M && j < rp_) out[mm * ld_out + j] = j < r ? (uint16_t)E::bits(sum) : (uint16_t)0;
+    }
   }
+}
+
+// out[m][j] = rnd(sum over splits of part[sp][m][j]) in split order (j < r; zeros up to rp)
+template <int ELT>
+__global__ __launch_bounds__(256) void rowproj_reduce_kernel(const float* __restrict__ part, int ks,
+                                                             int64_t M, int r, int rp,
+                                                             uint16_t* __restrict__ out, int ld_out) {
+  using E = Elt<ELT>;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= M * rp) return;
+  const int64_t m = i / rp;
+  const int j = (int)(i - m * rp);
+  float sum = 0.0f;
+  for (int sp = 0; sp < ks; ++sp) sum += part[((int64_t)sp * M + m) * rp + j];
+  out[m * ld_out + j] = j < r ? (uint16_t)E::bits(sum) : (uint16_t)0;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -584,6 +610,19 @@ struct Plan {
 // rank chunk of the projection and gradient kernels (their LDS tiles hold 128 rank columns)
 constexpr int kRankChunk = 128;
 
+// Column splits of a rank projection over few tokens (32-row blocks that leave most CUs idle):
+// about 256 blocks, at most 16 splits, one rank chunk (rp <= 128); 1 = none
+static int rowproj_splits(int64_t M, int64_t Kd, int rp) {
+  const int64_t blocks = ceil_div(M, 32);
+  if (blocks >= 128 || rp > kRankChunk || rp <= 0) return 1;
+  int64_t s = ceil_div(256, blocks);
+  const int64_t nch = ceil_div(Kd, rowp::KC);
+  if (s > nch) s = nch;
+  if (s > 16) s = 16;
+  return s < 2 ? 1 : (int)s;
+}
+
+
 static Plan make_plan(int64_t M, int64_t K, int64_t N, int64_t r, bool ptrs_aligned) {
   Plan p;
   // K, N < 2^22 keeps the projection and gradient kernels' buffer descriptors (64 rows, or a
@@ -608,7 +647,7 @@ static Plan make_plan(int64_t M, int64_t K, int64_t N, int64_t r, bool ptrs_alig
 
 // workspace layout (byte offsets, 256-aligned); identical computation for sizing and use
 struct WsLayout {
-  size_t h, u, dys, wd, at, bt, ap, pa, pb, kp, total;
+  size_t h, u, dys, wd, at, bt, ap, pa, pb, kp, rq, total;
 };
 
 static WsLayout ws_layout(int64_t M, int64_t K, int64_t N, int64_t r, int which, const Plan& p) {
@@ -639,6 +678,10 @@ static WsLayout ws_layout(int64_t M, int64_t K, int64_t N, int64_t r, int which,
   }
   w.h = take((size_t)M * rp * 2);
   w.at = take(r > 0 ? (size_t)r * K * 2 : 0);
+  {  // column-split partials of the rank projections over few tokens (h over K, u over N)
+    const int rs = r > 0 && p.fast ? std::max(rowproj_splits(M, K, p.rp), rowproj_splits(M, N, p.rp)) : 1;
+    w.rq = take(rs > 1 ? (size_t)rs * M * rp * 4 : 0);
+  }
   // bf16 copy of the dequantized weight (dX, and the forward unless it multiplies the codes)
   w.wd = take(p.deq && !(which == REELS_HIP_WS_FWD && p.i8f) ? (size_t)N * K * 2 : 0);
   if (which == REELS_HIP_WS_FWD) {
@@ -667,24 +710,39 @@ static int grid_stream(int64_t n) {
 template <bool SCALED, int ROWS>
 static void launch_rowproj_t(int elt, int rt, const uint16_t* src, int64_t M, int64_t Kd,
                              const uint16_t* P, int r, int rp, uint16_t* out, int ld_out,
-                             const float* s, uint16_t* scaled, hipStream_t st) {
-  const dim3 grid((unsigned)ceil_div(M, ROWS));
+                             const float* s, uint16_t* scaled, hipStream_t st,
+                             float* part = nullptr, int ks = 1) {
+  const dim3 grid((unsigned)ceil_div(M, ROWS), (unsigned)ks);
   TraceScope _ts(st, SCALED ? (rt <= 1 ? "rowproj_kernel<1,true>" : rt == 2 ? "rowproj_kernel<2,true>" : "rowproj_kernel<4,true>")
                             : (rt <= 1 ? "rowproj_kernel<1,false>" : rt == 2 ? "rowproj_kernel<2,false>" : "rowproj_kernel<4,false>"));
   with_elt(elt, [&](auto e) {
     constexpr int T = decltype(e)::value;
-    if (rt <= 1) rowproj_kernel<1, SCALED, ROWS, T><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, ld_out, s, scaled);
-    else if (rt == 2) rowproj_kernel<2, SCALED, ROWS, T><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, ld_out, s, scaled);
-    else rowproj_kernel<4, SCALED, ROWS, T><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, ld_out, s, scaled);
+    float* pt = ks > 1 ? part : nullptr;
+    if (rt <= 1) rowproj_kernel<1, SCALED, ROWS, T><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, ld_out, s, scaled, pt);
+    else if (rt == 2) rowproj_kernel<2, SCALED, ROWS, T><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, ld_out, s, scaled, pt);
+    else rowproj_kernel<4, SCALED, ROWS, T><<<grid, 256, 0, st>>>(src, M, Kd, P, r, rp, out, ld_out, s, scaled, pt);
   });
 }
 
 // out [M][rp] = bf16(src P^T) (zeros in columns r..rp), P [r][Kd]; one launch per rank chunk of
-// 128 (the scaled copy, when asked for, comes with the first)
+// 128 (the scaled copy, when asked for, comes with the first). part (rowproj_splits(M, Kd, rp)
+// x M x rp f32, or NULL): with few tokens the columns are split and a second pass sums them.
 static int launch_rowproj(int elt, const uint16_t* src, int64_t M, int64_t Kd, const uint16_t* P,
                           int r, int rp, uint16_t* out, const float* s, uint16_t* scaled,
-                          hipStream_t st) {
+                          hipStream_t st, float* part = nullptr) {
   const bool wide = ceil_div(M, 64) >= 256;  // enough tokens for a 64-row block on every CU
+  const int ks = (part != nullptr && out != nullptr) ? rowproj_splits(M, Kd, rp) : 1;
+  if (ks > 1) {
+    const int rt = (rp + 31) / 32;
+    if (scaled) launch_rowproj_t<true, 32>(elt, rt, src, M, Kd, P, r, rp, out, rp, s, scaled, st, part, ks);
+    else launch_rowproj_t<false, 32>(elt, rt, src, M, Kd, P, r, rp, out, rp, s, scaled, st, part, ks);
+    if (int rcode = check_launch("rowproj_kernel")) return rcode;
+    { TraceScope _ts(st, "rowproj_reduce_kernel");
+      with_elt(elt, [&](auto e) {
+        rowproj_reduce_kernel<decltype(e)::value><<<grid1(M * rp), 256, 0, st>>>(part, ks, M, r, rp, out, rp);
+      }); }
+    return check_launch("rowproj_reduce_kernel");
+  }
   for (int c0 = 0; c0 < (rp > 0 ? rp : 1); c0 += kRankChunk) {
     const int rpc = rp - c0 < kRankChunk ? rp - c0 : kRankChunk;     // columns of this chunk
     const int rc = r - c0 < 0 ? 0 : (r - c0 < rpc ? r - c0 : rpc);  // of them, rows of P
@@ -902,7 +960,8 @@ static int i8lora_fwd_impl(int elt, const char* fn, const void* x, const int8_t*
     { TraceScope _ts(st, "transpose_pad_kernel"); transpose_pad_kernel<<<dim3((unsigned)ceil_div(N, 32), (unsigned)ceil_div(r, 32)), 256, 0, st>>>(
         static_cast<const uint16_t*>(B), r, N, p.rp, bt); }
     if ((rc = check_launch("transpose_pad_kernel"))) return rc;
-    if ((rc = launch_rowproj(elt, xb, M, K, at, (int)r, p.rp, h, nullptr, nullptr, st))) return rc;
+    if ((rc = launch_rowproj(elt, xb, M, K, at, (int)r, p.rp, h, nullptr, nullptr, st,
+                             reinterpret_cast<float*>(ws + w.rq)))) return rc;
     if (p.padded && h_save &&
         (rc = launch_pad_cols(h, M, (int)r, p.rp, static_cast<uint16_t*>(h_save), (int)r, r, st)))
       return rc;
@@ -1019,7 +1078,8 @@ static int i8lora_bwd_impl(int elt, const char* fn, const void* dy, const void* 
   } else if (p.deq) {
     // 1. u = dy B^T; 2. dx = dy wt^T + c u A^T with wt[k][n] = bf16(q[n][k] s[n])
     if (r > 0 && (dx || dA)) {
-      if ((rc = launch_rowproj(elt, dyb, M, N, Bb, (int)r, p.rp, u, nullptr, nullptr, st))) return rc;
+      if ((rc = launch_rowproj(elt, dyb, M, N, Bb, (int)r, p.rp, u, nullptr, nullptr, st,
+                               reinterpret_cast<float*>(ws + w.rq)))) return rc;
     }
     if (dx) {
       uint16_t* wt = reinterpret_cast<uint16_t*>(ws + w.wd);
@@ -1036,7 +1096,8 @@ static int i8lora_bwd_impl(int elt, const char* fn, const void* dy, const void* 
     // wanted); f16 keeps dy as it is and scales the weight inside the dX GEMM instead
     uint16_t* scaled = (dx && !f16) ? dys : nullptr;
     if (r > 0) {
-      if ((rc = launch_rowproj(elt, dyb, M, N, Bb, (int)r, p.rp, u, scales, scaled, st))) return rc;
+      if ((rc = launch_rowproj(elt, dyb, M, N, Bb, (int)r, p.rp, u, scales, scaled, st,
+                               reinterpret_cast<float*>(ws + w.rq)))) return rc;
     } else {
       // r = 0: only the scaled copy is needed (no projection output)
       if ((rc = launch_rowproj(elt, dyb, M, N, Bb, 0, 0, nullptr, scales, scaled, st))) return rc;
@@ -1075,7 +1136,8 @@ static int i8lora_bwd_impl(int elt, const char* fn, const void* dy, const void* 
       { TraceScope _ts(st, "transpose_pad_kernel"); transpose_pad_kernel<<<dim3((unsigned)ceil_div(r, 32), (unsigned)ceil_div(K, 32)), 256, 0, st>>>(
           Ab, K, r, K, at); }
       if ((rc = check_launch("transpose_pad_kernel"))) return rc;
-      if ((rc = launch_rowproj(elt, xb, M, K, at, (int)r, p.rp, hw, nullptr, nullptr, st))) return rc;
+      if ((rc = launch_rowproj(elt, xb, M, K, at, (int)r, p.rp, hw, nullptr, nullptr, st,
+                               reinterpret_cast<float*>(ws + w.rq)))) return rc;
       hh = hw;
     }
   }
