@@ -24,10 +24,24 @@ namespace reels {
 
 // ---------------------------------------------------------------------------------------------
 // transpose: out[c][r] = in[r][c] for r < rows, zero for rows <= r < rows_pad (bf16)
-__global__ void transpose_pad_kernel(const uint16_t* __restrict__ in, int64_t rows, int64_t cols,
-                                     int64_t rows_pad, uint16_t* __restrict__ out) {
+// up to two transposes in one launch: job 0 takes the first nb0 blocks; a job's blocks are 32 x 32
+// tiles, column tile fastest
+struct TpJob {
+  const uint16_t* in;
+  uint16_t* out;
+  int64_t rows, cols, rows_pad;
+  int gx;  // column tiles
+};
+__global__ void transpose_pad_kernel(TpJob j0, TpJob j1, int nb0) {
   __shared__ uint16_t tile[32][33];
-  const int64_t r0 = (int64_t)blockIdx.y * 32, c0 = (int64_t)blockIdx.x * 32;
+  const bool second = (int)blockIdx.x >= nb0;
+  const int b = second ? (int)blockIdx.x - nb0 : (int)blockIdx.x;
+  const uint16_t* __restrict__ in = second ? j1.in : j0.in;
+  uint16_t* __restrict__ out = second ? j1.out : j0.out;
+  const int64_t rows = second ? j1.rows : j0.rows, cols = second ? j1.cols : j0.cols;
+  const int64_t rows_pad = second ? j1.rows_pad : j0.rows_pad;
+  const int gx = second ? j1.gx : j0.gx;
+  const int64_t r0 = (int64_t)(b / gx) * 32, c0 = (int64_t)(b % gx) * 32;
   const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 256 threads: 32 x 8
   for (int i = ty; i < 32; i += 8) {
     const int64_t r = r0 + i, c = c0 + tx;
@@ -700,6 +714,22 @@ static WsLayout ws_layout(int64_t M, int64_t K, int64_t N, int64_t r, int which,
 }
 
 static int grid1(int64_t n, int bs = 256) { return (int)ceil_div(n, bs); }
+
+// out[c][r] = in[r][c] (rows_pad >= rows output rows, zeros past rows) for one or two matrices
+// in one launch (in1 NULL: one)
+static TpJob tp_job(const uint16_t* in, int64_t rows, int64_t cols, int64_t rows_pad, uint16_t* out) {
+  TpJob j{};
+  j.in = in; j.out = out; j.rows = rows; j.cols = cols; j.rows_pad = rows_pad;
+  j.gx = (int)ceil_div(cols, 32);
+  return j;
+}
+static int launch_transpose_pad(const TpJob& a, const TpJob* b, hipStream_t st) {
+  const int nb0 = a.gx * (int)ceil_div(a.rows_pad, 32);
+  const int nb1 = b ? b->gx * (int)ceil_div(b->rows_pad, 32) : 0;
+  { TraceScope _ts(st, "transpose_pad_kernel");
+    transpose_pad_kernel<<<(unsigned)(nb0 + nb1), 256, 0, st>>>(a, b ? *b : a, nb0); }
+  return check_launch("transpose_pad_kernel");
+}
 // grid of a grid-stride streaming pass over n 16-bit elements (8 per thread and step): enough
 // blocks to fill the GPU several times over, fewer for small n
 static int grid_stream(int64_t n) {
@@ -953,13 +983,10 @@ static int i8lora_fwd_impl(int elt, const char* fn, const void* x, const int8_t*
   if (r > 0) {
     uint16_t* at = reinterpret_cast<uint16_t*>(ws + w.at);
     bt = reinterpret_cast<uint16_t*>(ws + w.bt);
-    // At [r][K] from A [K][r]; Bt [N][rp] from B [r][N]
-    { TraceScope _ts(st, "transpose_pad_kernel"); transpose_pad_kernel<<<dim3((unsigned)ceil_div(r, 32), (unsigned)ceil_div(K, 32)), 256, 0, st>>>(
-        static_cast<const uint16_t*>(A), K, r, K, at); }
-    if ((rc = check_launch("transpose_pad_kernel"))) return rc;
-    { TraceScope _ts(st, "transpose_pad_kernel"); transpose_pad_kernel<<<dim3((unsigned)ceil_div(N, 32), (unsigned)ceil_div(r, 32)), 256, 0, st>>>(
-        static_cast<const uint16_t*>(B), r, N, p.rp, bt); }
-    if ((rc = check_launch("transpose_pad_kernel"))) return rc;
+    // At [r][K] from A [K][r]; Bt [N][rp] from B [r][N] (one launch)
+    const TpJob ja = tp_job(static_cast<const uint16_t*>(A), K, r, K, at);
+    const TpJob jb = tp_job(static_cast<const uint16_t*>(B), r, N, p.rp, bt);
+    if ((rc = launch_transpose_pad(ja, &jb, st))) return rc;
     if ((rc = launch_rowproj(elt, xb, M, K, at, (int)r, p.rp, h, nullptr, nullptr, st,
                              reinterpret_cast<float*>(ws + w.rq)))) return rc;
     if (p.padded && h_save &&
@@ -1133,9 +1160,7 @@ static int i8lora_bwd_impl(int elt, const char* fn, const void* dy, const void* 
     if (!hh) {
       uint16_t* at = reinterpret_cast<uint16_t*>(ws + w.at);
       uint16_t* hw = reinterpret_cast<uint16_t*>(ws + w.h);
-      { TraceScope _ts(st, "transpose_pad_kernel"); transpose_pad_kernel<<<dim3((unsigned)ceil_div(r, 32), (unsigned)ceil_div(K, 32)), 256, 0, st>>>(
-          Ab, K, r, K, at); }
-      if ((rc = check_launch("transpose_pad_kernel"))) return rc;
+      if ((rc = launch_transpose_pad(tp_job(Ab, K, r, K, at), nullptr, st))) return rc;
       if ((rc = launch_rowproj(elt, xb, M, K, at, (int)r, p.rp, hw, nullptr, nullptr, st,
                                reinterpret_cast<float*>(ws + w.rq)))) return rc;
       hh = hw;
