@@ -445,6 +445,47 @@ __global__ __launch_bounds__(256) void reduce_partials_kernel(const float* __res
   if (jj < r && oo < Od) out[(int64_t)jj * Od + oo] = tile[wo][wj];
 }
 
+// The dA (out[o][j]) and dB (out[j][o]) reductions of one backward in one launch: blocks
+// [0, nb0) reduce dA as reduce_partials_kernel<false> (256 outputs per block), the rest dB as
+// <true> (8 x 32 tiles, row of tiles fastest); same sums in the same order
+struct RpJob {
+  const float* part;
+  float* out;
+  int64_t Od;
+  int splits;
+};
+__global__ __launch_bounds__(256) void reduce_partials2_kernel(RpJob ja, RpJob jb, int nb0, int rp,
+                                                               int r, float c) {
+  __shared__ float tile[8][33];
+  if ((int)blockIdx.x < nb0) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= ja.Od * r) return;
+    const int64_t o = idx / r, j = idx % r;
+    float sum = 0.0f;
+#pragma unroll 8
+    for (int sp = 0; sp < ja.splits; ++sp) sum += ja.part[((int64_t)sp * ja.Od + o) * rp + j];
+    ja.out[idx] = c * sum;
+    return;
+  }
+  const int b = (int)blockIdx.x - nb0;
+  const int gx = (int)((jb.Od + 7) / 8);
+  const int bx = b % gx, by = b / gx;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  const int64_t o = (int64_t)bx * 8 + ty;
+  const int j = by * 32 + tx;
+  float sum = 0.0f;
+  if (o < jb.Od && j < r) {
+#pragma unroll 8
+    for (int sp = 0; sp < jb.splits; ++sp) sum += jb.part[((int64_t)sp * jb.Od + o) * rp + j];
+  }
+  tile[ty][tx] = c * sum;
+  __syncthreads();
+  const int wo = threadIdx.x & 7, wj = threadIdx.x >> 3;
+  const int64_t oo = (int64_t)bx * 8 + wo;
+  const int jj = by * 32 + wj;
+  if (jj < r && oo < jb.Od) jb.out[(int64_t)jj * jb.Od + oo] = tile[wo][wj];
+}
+
 __global__ void fill_f32_kernel(float* p, int64_t n, float v) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = v;
@@ -841,9 +882,22 @@ static int launch_colgrad2(int elt, int64_t M, int r, int rp, float c, const CgP
     }
     if (int rc = check_launch("colgrad_kernel")) return rc;
   }
-  for (int i = 0; i < 2; ++i) {
-    if (!ps[i] || direct[i]) continue;
-    const CgPass& q = *ps[i];
+  // the reductions: dA and dB together in one launch when both need one
+  const CgPass* need[2] = {nullptr, nullptr};
+  int nn = 0;
+  for (int i = 0; i < 2; ++i)
+    if (ps[i] && !direct[i]) need[nn++] = ps[i];
+  if (nn == 2 && !need[0]->trans && need[1]->trans) {
+    const RpJob ja{need[0]->part, need[0]->out, need[0]->Od, need[0]->sp.splits};
+    const RpJob jb{need[1]->part, need[1]->out, need[1]->Od, need[1]->sp.splits};
+    const int nb0 = (int)ceil_div(ja.Od * r, 256);
+    const int nb1 = (int)(ceil_div(jb.Od, 8) * ceil_div(r, 32));
+    { TraceScope _ts(st, "reduce_partials2_kernel");
+      reduce_partials2_kernel<<<(unsigned)(nb0 + nb1), 256, 0, st>>>(ja, jb, nb0, rp, r, c); }
+    return check_launch("reduce_partials2_kernel");
+  }
+  for (int i = 0; i < nn; ++i) {
+    const CgPass& q = *need[i];
     if (int rc = launch_reduce_partials(q.part, q.sp.splits, q.Od, rp, r, c, q.out, q.trans, st)) return rc;
   }
   return REELS_HIP_OK;
