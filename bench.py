@@ -603,7 +603,14 @@ def _cfg5a(dev, L, check, gen):
         bb = 2 * M * N + N * K + 4 * N + 4 * M * K + 2 * M * RANK
         ff = 2.0 * M * N * K + 2.0 * M * RANK * (K + N)
         bf_ = 2.0 * M * N * K + 4.0 * M * RANK * (K + N)
+        # the vendor library's plain bf16 GEMM on the same shape (bf16 weight, no scales, no LoRA)
+        import torch
+        xv = torch.randn((M, K), device=dev, dtype=torch.bfloat16)
+        wv = torch.randn((N, K), device=dev, dtype=torch.bfloat16)
+        vms = _time_ms(lambda: torch.matmul(xv, wv.t()), reps=100, warmup=5)
+        del xv, wv
         sk[str(M)] = {"fwd_us": round(fms * 1e3, 2), "bwd_us": round(bms * 1e3, 2),
+                      "vendor_bf16_gemm_us": round(vms * 1e3, 2),
                       "fwd_gbs": round(fb / (fms * 1e-3) / 1e9, 1),
                       "bwd_gbs": round(bb / (bms * 1e-3) / 1e9, 1),
                       "fwd_frac_of_hbm": round(fb / (fms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
@@ -613,7 +620,9 @@ def _cfg5a(dev, L, check, gen):
         del pr
     out["cfg5a"] = {"what": "cross-attention K/V projection 5120 -> 5120, r 32, at 77 / 333 / 512 "
                             "text tokens; bytes = 2MK + NK + 4N + 2MN + 2Mr (fwd), 2MN + NK + 4N "
-                            "+ 4MK + 2Mr (bwd); peak 8 TB/s", "tokens": sk}
+                            "+ 4MK + 2Mr (bwd); peak 8 TB/s; vendor_bf16_gemm_us: torch.matmul of "
+                            "the same x by a bf16 weight (twice the weight bytes, no scales or LoRA)",
+                    "tokens": sk}
     return out
 
 
