@@ -100,6 +100,8 @@ CASES = [
     (3, 65, 129, 2, 128, False, True, "f16"),
     (2, 100, 300, 2, 64, True, False, "f16"),    # causal with more keys than queries, batch 2
     (2, 129, 129, 3, 128, True, True, "bf16"),   # mask and causal together
+    (1, 40, 200, 2, 128, False, False, "bf16"),  # one query step (dK / dV ring prologue only)
+    (2, 192, 385, 1, 128, False, False, "f16"),  # whole query steps, keys one past 3 x 128
 ]
 
 
