@@ -626,6 +626,42 @@ def _cfg5a(dev, L, check, gen):
     return out
 
 
+def configs_cpu_baseline(configs):
+    """The reference's CPU path (oracle/cpu_path.py: fp32 materialised dequant + torch CPU BLAS)
+    on the smaller configurations, beside their GPU figures: config 1 in full, one linear of each
+    config-2 shape at 32760 tokens, config 5a in full (forward and backward timed apart)."""
+    import torch
+    from oracle import cpu_path
+    threads = torch.get_num_threads()
+    out = {"kind": "port", "cores": threads, "host": host_info(),
+           "what": "fp32 materialised dequant + torch CPU BLAS, all host threads; configs 1 and "
+                   "5a: best of three runs after an untimed one, config 2: one run per shape"}
+    if "cfg1" in configs:
+        tf, tb = cpu_path.time_linear(1536, 1536, 1024, 16, reps=3)
+        ms = (tf + tb) * 1e3
+        f = linear_flops(1024, 1536, 1536, 16)
+        out["cfg1"] = {"ms": round(ms, 3), "tflops": round(f / (ms * 1e-3) / 1e12, 4),
+                       "gpu_speedup": round(ms / configs["cfg1"]["ms"], 1)}
+    if "cfg2" in configs:
+        shapes = {}
+        for (name, K, N) in (("q", 1536, 1536), ("ffn.0", 1536, 8960), ("ffn.2", 8960, 1536)):
+            tf, tb = cpu_path.time_linear(K, N, TOKENS, RANK, warm=0)  # one timed run
+            f = linear_flops(TOKENS, K, N, RANK)
+            shapes[name] = {"ms": round((tf + tb) * 1e3, 1),
+                            "tflops": round(f / (tf + tb) / 1e12, 4)}
+        out["cfg2_one_linear_per_shape"] = shapes
+    if "cfg5a" in configs:
+        tok = {}
+        for M in (77, 333, 512):
+            tf, tb = cpu_path.time_linear(5120, 5120, M, RANK, reps=3)
+            g = configs["cfg5a"]["tokens"][str(M)]
+            tok[str(M)] = {"fwd_us": round(tf * 1e6, 1), "bwd_us": round(tb * 1e6, 1),
+                           "gpu_speedup_fwd": round(tf * 1e6 / g["fwd_us"], 1),
+                           "gpu_speedup_bwd": round(tb * 1e6 / g["bwd_us"], 1)}
+        out["cfg5a"] = tok
+    return out
+
+
 def cpu_baseline(seconds):
     """The reference's CPU path (fp32: dequantize-materialise + BLAS sgemm + rank-r GEMMs, see
     oracle/cpu_path.py) on a bounded sample of the same six projections at fewer tokens."""
@@ -793,6 +829,8 @@ def main():
     configs = None
     if not args.no_configs and args.dtype == "bf16" and args.offload == "none":
         configs = configs_bench(dev, L, _lib.check)
+        if args.cpu_seconds > 0:
+            configs["cpu_baseline"] = configs_cpu_baseline(configs)
     pack = None
     if not args.no_pack:
         pack, samples = pack_bench(dev)

@@ -72,6 +72,29 @@ def time_block(projections, M: int, r: int, seed: int = 0):
     return t1 - t0, total
 
 
+def time_linear(K: int, N: int, M: int, r: int, seed: int = 0, reps: int = 1, warm: int = 1):
+    """Times the forward and, separately, the backward of one (K, N) linear at M tokens (the best
+    of reps runs each, after warm untimed runs). Returns (forward seconds, backward seconds)."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn((M, K), generator=g)
+    dy = torch.randn((M, N), generator=g)
+    q = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    s = torch.rand((N,), generator=g) * 1e-3 + 1e-4
+    A = torch.randn((K, r), generator=g) * 0.01
+    B = torch.randn((r, N), generator=g) * 0.01
+    c = 1.0
+    tf = tb = float("inf")
+    for i in range(warm + reps):
+        t0 = time.perf_counter()
+        forward(x, q, s, A, B, c)
+        t1 = time.perf_counter()
+        backward(x, dy, q, s, A, B, c)
+        t2 = time.perf_counter()
+        if i >= warm:
+            tf, tb = min(tf, t1 - t0), min(tb, t2 - t1)
+    return tf, tb
+
+
 def attention_forward(q, k, v, query_block: int = 128, key_block: int = 128):
     """memory_efficient_attention on the CPU (attention.jl:106-172) for one head without a mask:
     f32 tiles of query_block x key_block scores on BLAS, an online softmax per query block.

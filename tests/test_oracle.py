@@ -419,6 +419,15 @@ def test_cpu_path_matches_the_f64_oracle():
     assert cpu_path.flops(M, K, N, r) == 4.0 * M * N * K + 6.0 * M * r * (K + N)
 
 
+def test_cpu_path_time_linear():
+    # the per-linear timing behind the configs' CPU baselines: both legs timed, finite, positive
+    from oracle import cpu_path
+    tf, tb = cpu_path.time_linear(64, 48, 40, 4, reps=2)
+    assert 0.0 < tf < 60.0 and 0.0 < tb < 60.0
+    tf, tb = cpu_path.time_linear(64, 48, 40, 4, warm=0)
+    assert 0.0 < tf < 60.0 and 0.0 < tb < 60.0
+
+
 # ---- the fp16 element path (the reference's Float16 compute) -----------------------------------
 def h16(a):
     """IEEE binary16 patterns of the values a (numpy's rounding)."""
