@@ -340,6 +340,29 @@ def host_info():
             "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
 
 
+def device_info(dev, sclk=None):
+    """The GPU: name, compute units, architecture, and (when the driver's sysfs file is readable)
+    the shader clock level it sat at when sampled (right after the timed steps)."""
+    import torch
+    p = torch.cuda.get_device_properties(dev)
+    return {"name": p.name, "compute_units": p.multi_processor_count, "arch": p.gcnArchName,
+            "sclk_after_timed_steps": sclk}
+
+
+def read_sclk(dev):
+    """The current shader clock level from /sys/bus/pci/devices/<this GPU>/pp_dpm_sclk (the line
+    marked '*'), or None where the file is missing or unreadable."""
+    import torch
+    try:
+        p = torch.cuda.get_device_properties(dev)
+        path = f"/sys/bus/pci/devices/{p.pci_domain_id:04x}:{p.pci_bus_id:02x}:{p.pci_device_id:02x}.0/pp_dpm_sclk"
+        with open(path) as f:
+            cur = [l.split(":", 1)[1].replace("*", "").strip() for l in f if "*" in l]
+        return cur[0] if cur else None
+    except (OSError, IndexError, AttributeError, RuntimeError):
+        return None
+
+
 def pack_cpu_baseline(samples, seconds=5.0):
     """The reference packs on the host CPU (quantize_frozen_matrix, quantization.jl:35-44 on
     Float32.(Array(W))); the oracle's C restatement (OpenMP) is timed on a sample of 14B rows.
@@ -751,6 +774,7 @@ def main():
         run_step(L, projs, _lib.check, sfx, streamer)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
+    sclk = read_sclk(dev)
     recs = _lib.trace_records()
     all_recs, all_steps = recs, args.steps
     if args.trace == "gemm":
@@ -864,7 +888,7 @@ def main():
         "configs": configs,
         "pack": pack,
         "attention": att,
-        "device": torch.cuda.get_device_name(dev),
+        "device": device_info(dev, sclk),
     }
     print(json.dumps(out))
 
