@@ -345,7 +345,7 @@ def device_info(dev, sclk=None):
     the shader clock level it sat at when sampled (right after the timed steps)."""
     import torch
     p = torch.cuda.get_device_properties(dev)
-    return {"name": p.name, "compute_units": p.multi_processor_count, "arch": p.gcnArchName,
+    return {"name": torch.cuda.get_device_name(dev), "compute_units": p.multi_processor_count, "arch": p.gcnArchName,
             "sclk_after_timed_steps": sclk}
 
 
