@@ -62,13 +62,21 @@ __device__ __forceinline__ uint32_t toff(int r, int d) {
 // that make no difference to any sum here
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-__device__ __forceinline__ float wave_max16(float x) {  // over lanes l, l^16, l^32, l^48
-  x = fmaxf(x, __shfl_xor(x, 16));
-  return fmaxf(x, __shfl_xor(x, 32));
+// Reductions over lanes l, l^16, l^32, l^48. v_permlane16_swap (v_permlane32_swap) with x as both
+// operands hands every lane the values of lanes l and l^16 (l^32), in an order that depends on
+// the lane: a VALU exchange instead of an LDS round trip (ds_bpermute). The sums are the same
+// bits as (x_l + x_l^16) + (x_l^32 + x_l^48) in any lane order, since a + b == b + a.
+__device__ __forceinline__ float wave_max16(float x) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
 }
 __device__ __forceinline__ float wave_sum16(float x) {
-  x += __shfl_xor(x, 16);
-  return x + __shfl_xor(x, 32);
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(q[0]) + __uint_as_float(q[1]);
 }
 
 // A operand of 8 rows-transposed elements from an LDS tile: element e < 4 is row r0 + e,
