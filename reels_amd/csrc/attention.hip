@@ -246,7 +246,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttArgs a) {
     // branch); otherwise P = 2^(s sl2 - m) <= 2^8, exact in the sums and in the lse, and the
     // rounding of P to the element type is relative as before.
     constexpr float TAU = 8.0f;
-    float mt[2];
+    float ml[2];  // this lane's maximum raw score per query tile
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
       const int64_t qi = q0 + 16 * qt + l16;
@@ -260,14 +260,16 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttArgs a) {
           s[kt][qt][v] = x;
           m = fmaxf(m, x);
         }
-      mt[qt] = wave_max16(m) * sl2;
+      ml[qt] = m;
     }
     // a query with no visible key so far keeps m = -inf (nothing accumulated); the first tile
-    // always moves m (-inf + TAU < any finite maximum)
-    if (__builtin_amdgcn_ballot_w64((mt[0] > mrun[0] + TAU) || (mt[1] > mrun[1] + TAU))) {
+    // always moves m (-inf + TAU < any finite maximum). The test needs no exchange between lanes:
+    // some lane's own maximum exceeds its row's running maximum + TAU exactly when the row's
+    // maximum does (scaling by sl2 > 0 keeps the order), and the ballot asks for any row
+    if (__builtin_amdgcn_ballot_w64((ml[0] * sl2 > mrun[0] + TAU) || (ml[1] * sl2 > mrun[1] + TAU))) {
 #pragma unroll
       for (int qt = 0; qt < 2; ++qt) {
-        const float mnew = fmaxf(mrun[qt], mt[qt]);
+        const float mnew = fmaxf(mrun[qt], wave_max16(ml[qt]) * sl2);
         const float alpha = (VM == 2 && mnew == -INFINITY) ? 1.0f : ex2(mrun[qt] - mnew);
         mrun[qt] = mnew;
         lrun[qt] *= alpha;
