@@ -141,17 +141,34 @@ __device__ __forceinline__ bool att_visible_tile(const AttArgs& a, int64_t qi, i
 // lane L row c * (64 / CH) + L / CH, LDS slot L % CH holding chunk (L % CH) ^ swz<D>(row).
 // Rows past the tensor's end read zeros (buffer range).
 template <int D>
-__device__ __forceinline__ void copy_tile(const i32x4& rsrc, int64_t row0, int64_t H, int w,
-                                          int lane, uint8_t* dst) {
-  constexpr int CH = D / 8, RPC = 64 / CH, NC = CH / 4;  // chunks per row, rows per copy, copies per wave
+struct TileCopy {
+  static constexpr int CH = D / 8, RPC = 64 / CH, NC = CH / 4;  // chunks per row, rows per copy, copies per wave
+  uint32_t off[NC];  // this lane's byte offset of copy i within a tile that starts at row 0
+  uint32_t lds0;     // LDS byte address of this wave's first copy in a tile (scalar)
+};
+template <int D>
+__device__ __forceinline__ TileCopy<D> tile_copy(int64_t H, int w, int lane, const uint8_t* smem) {
+  TileCopy<D> tc;
 #pragma unroll
-  for (int i = 0; i < NC; ++i) {
-    const int c = w * NC + i;
-    const int row = c * RPC + lane / CH;
-    const int chunk = (lane % CH) ^ swz<D>(row);
-    const uint32_t off = (uint32_t)(((row0 + row) * H * D + chunk * 8) * 2);
-    dma16(rsrc, off, 0u, dst + c * 1024);
+  for (int i = 0; i < TileCopy<D>::NC; ++i) {
+    const int c = w * TileCopy<D>::NC + i;
+    const int row = c * TileCopy<D>::RPC + lane / TileCopy<D>::CH;
+    const int chunk = (lane % TileCopy<D>::CH) ^ swz<D>(row);
+    tc.off[i] = (uint32_t)((row * H * D + chunk * 8) * 2);
   }
+  tc.lds0 = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)LDS_PTR(const uint8_t, smem) + (uint32_t)(w * TileCopy<D>::NC * 1024));
+  return tc;
+}
+// one wave's copies of the tile at rows row0 .. into the LDS tile at byte offset dst (scalar).
+// The row offset is added to the per-lane offsets (one add per copy): the buffer's range check,
+// which turns rows past the tensor's end into zeros, covers the vector offset only.
+template <int D>
+__device__ __forceinline__ void copy_tile(const i32x4& rsrc, const TileCopy<D>& tc, int64_t row0,
+                                          int64_t H, uint32_t dst) {
+  const uint32_t roff = (uint32_t)(row0 * H * D * 2);
+#pragma unroll
+  for (int i = 0; i < TileCopy<D>::NC; ++i) dma16_at(rsrc, tc.off[i] + roff, 0u, tc.lds0 + dst + i * 1024);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -186,10 +203,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttArgs a) {
   const uint16_t* vbase = a.v + (b * Sk * H + h) * D;
   const uint32_t nrec = (uint32_t)(((Sk - 1) * H + 1) * D * 2);
   const i32x4 rk = buffer_rsrc(kbase, nrec), rv = buffer_rsrc(vbase, nrec);
+  const TileCopy<D> tc = tile_copy<D>(H, w, lane, smem);
   auto issue = [&](int j, int stg) {
-    uint8_t* st = smem + stg * 2 * TB;
-    copy_tile<D>(rk, (int64_t)j * KT, H, w, lane, st);
-    copy_tile<D>(rv, (int64_t)j * KT, H, w, lane, st + TB);
+    const uint32_t st = (uint32_t)(stg * 2 * TB);
+    copy_tile<D>(rk, tc, (int64_t)j * KT, H, st);
+    copy_tile<D>(rv, tc, (int64_t)j * KT, H, st + TB);
   };
 
   f32x4 oacc[NDT][2];
@@ -550,10 +568,11 @@ __global__ __launch_bounds__(256, 2) void attn_dq_kernel(AttArgs a) {
   const uint16_t* vbase = a.v + (b * Sk * H + h) * D;
   const uint32_t nrec = (uint32_t)(((Sk - 1) * H + 1) * D * 2);
   const i32x4 rk = buffer_rsrc(kbase, nrec), rv = buffer_rsrc(vbase, nrec);
+  const TileCopy<D> tc = tile_copy<D>(H, w, lane, smem);
   auto issue = [&](int j, int stg) {
-    uint8_t* st = smem + stg * 2 * TB;
-    copy_tile<D>(rk, (int64_t)j * KT, H, w, lane, st);
-    copy_tile<D>(rv, (int64_t)j * KT, H, w, lane, st + TB);
+    const uint32_t st = (uint32_t)(stg * 2 * TB);
+    copy_tile<D>(rk, tc, (int64_t)j * KT, H, st);
+    copy_tile<D>(rv, tc, (int64_t)j * KT, H, st + TB);
   };
   f32x4 qacc[NDT][2];
 #pragma unroll

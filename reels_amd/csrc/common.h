@@ -88,6 +88,14 @@ __device__ __forceinline__ void dma16(const i32x4& rsrc, uint32_t voff, uint32_t
                : "memory");
 }
 
+// the same with the LDS byte address given as a (wave-uniform) integer
+__device__ __forceinline__ void dma16_at(const i32x4& rsrc, uint32_t voff, uint32_t soff,
+                                         uint32_t ldsaddr) {
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc),
+               "s"(soff), "{m0}"(ldsaddr)
+               : "memory");
+}
+
 // gelu_tanh, src/layers/linear.jl:61-68, in f32, and its analytic derivative
 __device__ __forceinline__ float gelu_f(float x) {
   const float k = 0.7978845608028654f;  // sqrt(Float32(2 / pi))
