@@ -415,21 +415,12 @@ __global__ __launch_bounds__(256, 2) void attn_dkdv_kernel(AttArgs a) {
   const uint32_t nrec = (uint32_t)(((Sq - 1) * H + 1) * D * 2);
   const i32x4 rq = buffer_rsrc(qbase, nrec), rd = buffer_rsrc(dbase, nrec);
   float* sstat = reinterpret_cast<float*>(smem + 4 * TB);  // [2 stages][lse QT, corr QT]
+  static_assert(QT == 64, "the step tiles are the 64-row tiles of copy_tile");
+  const TileCopy<D> tc = tile_copy<D>(H, w, lane, smem);
   auto issue = [&](int j) {
-    uint8_t* st = smem + (j & 1) * 2 * TB;
-    // a QT-row tile (QT = 64: the copies of copy_tile)
-    constexpr int CH = D / 8, RPC = 64 / CH, NCT = QT * CH / 64;  // copies per tile
-#pragma unroll
-    for (int i = 0; i < (NCT + 3) / 4; ++i) {
-      const int c = w * ((NCT + 3) / 4) + i;
-      if (c < NCT) {
-        const int row = c * RPC + lane / CH;
-        const int chunk = (lane % CH) ^ swz<D>(row);
-        const uint32_t off = (uint32_t)((((int64_t)j * QT + row) * H * D + chunk * 8) * 2);
-        dma16(rq, off, 0u, st + c * 1024);
-        dma16(rd, off, 0u, st + TB + c * 1024);
-      }
-    }
+    const uint32_t st = (uint32_t)((j & 1) * 2 * TB);
+    copy_tile<D>(rq, tc, (int64_t)j * QT, H, st);
+    copy_tile<D>(rd, tc, (int64_t)j * QT, H, st + TB);
   };
   // lse and correction of a step's queries (threads 0..63): loaded into a register with the
   // step's copies and written to LDS after the wait that ends the previous step, so the loads
