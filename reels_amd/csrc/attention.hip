@@ -161,8 +161,8 @@ __device__ __forceinline__ TileCopy<D> tile_copy(int64_t H, int w, int lane, con
   return tc;
 }
 // one wave's copies of the tile at rows row0 .. into the LDS tile at byte offset dst (scalar).
-// The row offset is added to the per-lane offsets (one add per copy): the buffer's range check,
-// which turns rows past the tensor's end into zeros, covers the vector offset only.
+// The row offset goes into the per-lane (vector) offsets, one add per copy, where the buffer's
+// range check that turns rows past the tensor's end into zeros applies to it.
 template <int D>
 __device__ __forceinline__ void copy_tile(const i32x4& rsrc, const TileCopy<D>& tc, int64_t row0,
                                           int64_t H, uint32_t dst) {
