@@ -874,10 +874,12 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
     }
   }
   if constexpr (SPLIT) return;  // the partials went straight to global memory
-  __syncthreads();
+  // each wave stores the region it staged itself (128 rows x 64 columns: 128-byte row segments,
+  // whole cache lines), so no barrier waits for the other waves
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's staging writes are done
 #pragma unroll 4
   for (int i = 0; i < 16; ++i) {
-    const int id = t + 512 * i, row = id >> 5, c = id & 31;
+    const int row = wm * 128 + 8 * i + (lane >> 3), c = wn * 8 + (lane & 7);
     const int64_t m = m0 + row, n = n0 + c * 8;
     if (m < M && n < Ncols) {
       const u32x4 v = *reinterpret_cast<const u32x4*>(srow(row) + ((c ^ (row & 31)) << 4));
