@@ -783,10 +783,10 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
   __builtin_amdgcn_s_waitcnt(0x0F70);  // the L and R copies have landed
 
   // epilogue: LoRA up-projection on MFMA (k = 32 per instruction, lanes past the rank supply
-  // zeros), bias, one rounding per output (acc + c lor + bias); the tile is staged in LDS and
-  // stored as whole rows. The staging tile's rows of 512 bytes (16-byte chunks XOR-swizzled by
-  // row) fill, 64 rows at a time, the four stages other than activation stage nk, which holds L
-  // and R until every wave has read them.
+  // zeros), bias, one rounding per output (acc + c lor + bias); each wave stages its 128 x 64
+  // outputs in LDS and stores them as 128-byte row segments. The staging tile's rows of 512 bytes
+  // (16-byte chunks XOR-swizzled by row) fill, 64 rows at a time, the four stages other than
+  // activation stage nk, which holds L and R until every wave has read them.
   __syncthreads();
   const int lrs = nk % 3;
   auto srow = [&](int r) { const int q = r >> 6; return smem + (q < lrs ? q : q + 1) * ACT + (r & 63) * 512; };
