@@ -550,7 +550,7 @@ class Chain:
 
 
 def configs_bench(dev, L, check, which=("cfg1", "cfg2", "cfg4", "cfg5a")):
-    """The other BASELINE workloads on this GPU, each as TFLOP/s of forward + dX + dA + dB
+    """The smaller int8 LoRA workloads on this GPU, each as TFLOP/s of forward + dX + dA + dB
     (4MNK + 6Mr(K+N) per linear): config 1 (one 1536 x 1536 linear, 1024 tokens, r 16, alpha 16),
     config 2 (the six Wan-2.1-1.3B block projections at 32760 tokens), config 4 (the 30-layer
     1.3B chain with GELU), and config 5a (cross-attention K/V 5120 -> 5120 at 77 / 333 / 512 text

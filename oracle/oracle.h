@@ -3,8 +3,8 @@
  * Reels.jl's algorithm (file:line citations are relative to the Reels.jl repository).
  *
  * TEST INFRASTRUCTURE ONLY. The only callers are tests/, __graft_entry__.smoke() and the
- * cpu_baseline leg of bench.py, and only as the checker. The product path (reels_amd/) never
- * links, loads or calls anything here.
+ * cpu_baseline leg of bench.py, and only as the reference results to compare with. The product
+ * path (reels_amd/) never links, loads or calls anything here.
  *
  * Physical layouts (row-major, "[a][b]" = a rows of b contiguous elements), identical to the
  * Julia column-major arrays they restate:

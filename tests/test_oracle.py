@@ -1,5 +1,5 @@
-"""Pins the oracle (CPU restatement of Reels.jl's int8 LoRA linear) before it is trusted as the
-checker: known-answer vectors, a second independent restatement, closed forms and invariants
+"""Pins the oracle (CPU restatement of Reels.jl's int8 LoRA linear) before the GPU results are
+compared with it: known-answer vectors, a second independent restatement, closed forms and invariants
 chosen so that a dropped term, wrong sign, wrong index or transposed operand fails a test.
 CPU only."""
 import os
