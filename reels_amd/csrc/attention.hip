@@ -451,6 +451,7 @@ __global__ __launch_bounds__(256, 2) void attn_dkdv_kernel(AttArgs a) {
     stats_store(j);
     __syncthreads();
     if (j + 1 < nsteps) { stats_load(j + 1); issue(j + 1); }
+    __builtin_amdgcn_s_setprio(0);
     const uint8_t* sq = smem + (j & 1) * 2 * TB;
     const uint8_t* sd = sq + TB;
     const float* ls = sstat + (j & 1) * 2 * QT;
@@ -497,10 +498,12 @@ __global__ __launch_bounds__(256, 2) void attn_dkdv_kernel(AttArgs a) {
       db[kb2][0] = E::pack2_fast(ds[0][0], ds[0][1]); db[kb2][1] = E::pack2_fast(ds[0][2], ds[0][3]);
       db[kb2][2] = E::pack2_fast(ds[1][0], ds[1][1]); db[kb2][3] = E::pack2_fast(ds[1][2], ds[1][3]);
     }
-    // The gradient MFMAs run at raised wave priority: a wave in this phase issues ahead of the
-    // other wave on its SIMD (which is in its score reads or softmax), so the matrix core gets
-    // one wave's dense MFMA run while the other's LDS reads and VALU work proceed beside it
-    // (dK/dV 41.9 -> 40.1 ms; the same around the score MFMAs, or in dQ and the forward, is slower)
+    // The gradient MFMAs run at raised wave priority, kept through the next step's wait, barrier
+    // and copy issue and dropped before its score reads: a wave in this phase issues ahead of
+    // the other wave on its SIMD (which is in its score reads or softmax), so the matrix core
+    // gets one wave's dense MFMA run while the other's LDS reads and VALU work proceed beside it
+    // (dK/dV 41.9 -> 39.6 ms; the same around the score MFMAs or the softmax, or in dQ and the
+    // forward, is slower)
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int kb2 = 0; kb2 < NQT / 2; ++kb2)
@@ -511,8 +514,8 @@ __global__ __launch_bounds__(256, 2) void attn_dkdv_kernel(AttArgs a) {
         dvacc[dt] = E::mfma16(E::as8(da), E::as8(pb[kb2]), dvacc[dt]);
         dkacc[dt] = E::mfma16(E::as8(qa), E::as8(db[kb2]), dkacc[dt]);
       }
-    __builtin_amdgcn_s_setprio(0);
   }
+  __builtin_amdgcn_s_setprio(0);
   // dV[kj][d], dK[kj][d] = scale dK^T: lane holds d = 16 dt + 4 g + v of key kj
   if (kj < Sk) {
     uint16_t* dvrow = a.dv + ((b * Sk + kj) * H + h) * D;
