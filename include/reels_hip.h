@@ -167,6 +167,30 @@ int reels_hip_i8lora_bwd_f16(const void* dy, const void* x, const void* h, const
                              int64_t K, int64_t N, int64_t r, float lora_scale, void* dx, float* dA,
                              float* dB, void* workspace, size_t ws_bytes, void* stream);
 
+/*
+ * lora_backward with the gradient of a trainable bias: LoRALinear's bias when train_bias is set
+ * (src/layers/lora.jl:37-38, lora_parameters, and 64-67, where the forward adds it with
+ * mixed_add, src/layers/linear.jl:7-13). The reference lets Zygote differentiate that add, which
+ * gives dbias[n] = sum over tokens m of dy[m][n]; here it is
+ *   dbias [N] f32 = sum_m dy[m][n]   (f32 sums in a fixed order: bitwise reproducible)
+ * beside the outputs of reels_hip_i8lora_bwd (same arguments, same meaning, same workspace size:
+ * reels_hip_i8lora_workspace_bytes(..., REELS_HIP_WS_BWD)). When dB is computed, the column sums
+ * come from the dB gradient pass's own read of dy; otherwise (dB NULL, r = 0) from a pass of
+ * their own with the same summation order, so dbias does not depend on which outputs are asked
+ * for. dbias NULL gives exactly reels_hip_i8lora_bwd.
+ */
+int reels_hip_i8lora_bwd_bias(const void* dy, const void* x, const void* h, const int8_t* q,
+                              const float* scales, const void* A, const void* B, int64_t M,
+                              int64_t K, int64_t N, int64_t r, float lora_scale, void* dx,
+                              float* dA, float* dB, float* dbias, void* workspace,
+                              size_t ws_bytes, void* stream);
+/* The same with binary16 dy, x, h, A, B and dx (reels_hip_i8lora_bwd_f16); dbias stays f32. */
+int reels_hip_i8lora_bwd_bias_f16(const void* dy, const void* x, const void* h, const int8_t* q,
+                                  const float* scales, const void* A, const void* B, int64_t M,
+                                  int64_t K, int64_t N, int64_t r, float lora_scale, void* dx,
+                                  float* dA, float* dB, float* dbias, void* workspace,
+                                  size_t ws_bytes, void* stream);
+
 /* gelu_tanh, src/layers/linear.jl:61-68: y = bf16(0.5x(1 + tanh(sqrt(2/pi)(x + 0.044715x^3))))
  * computed in f32 on bf16 x[n]. */
 int reels_hip_gelu_tanh(const void* x, void* y, int64_t n, void* stream);
@@ -200,6 +224,13 @@ int reels_hip_i8lora_bwd_f32(const float* dy, const float* x, const float* h, co
                              const float* scales, const float* A, const float* B, int64_t M,
                              int64_t K, int64_t N, int64_t r, float lora_scale, float* dx,
                              float* dA, float* dB, void* workspace, size_t ws_bytes, void* stream);
+/* reels_hip_i8lora_bwd_f32 with the trainable bias's gradient dbias [N] = sum_m dy[m][n] (f32,
+ * fixed order), as reels_hip_i8lora_bwd_bias; same workspace as reels_hip_i8lora_bwd_f32. */
+int reels_hip_i8lora_bwd_bias_f32(const float* dy, const float* x, const float* h,
+                                  const int8_t* q, const float* scales, const float* A,
+                                  const float* B, int64_t M, int64_t K, int64_t N, int64_t r,
+                                  float lora_scale, float* dx, float* dA, float* dB, float* dbias,
+                                  void* workspace, size_t ws_bytes, void* stream);
 /* gelu_tanh and its pullback on f32 x, dy (linear.jl:61-68 with T = Float32: no rounding). */
 int reels_hip_gelu_tanh_f32(const float* x, float* y, int64_t n, void* stream);
 int reels_hip_gelu_tanh_bwd_f32(const float* x, const float* dy, float* dx, int64_t n,

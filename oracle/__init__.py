@@ -197,6 +197,23 @@ def lora_backward(dy, x, q, s, A, B, c, rows=None, kcols=None, ncols=None,
     return {"dx": dx, "dA": dA, "dB": dB}
 
 
+def bias_gradient(dy, cols=None, elt="bf16"):
+    """f64 gradient of a trainable bias (LoRALinear with train_bias, lora.jl:37-38): the forward
+    adds it per output channel with mixed_add (lora.jl:64-67, linear.jl:7-13), so its cotangent
+    is dy summed over the tokens, dbias[n] = sum_m dy[m][n]. dy: [M][N] 16-bit patterns (bf16 or,
+    with elt="f16", binary16) or float32 values (elt="f32"). Returns [len(cols)] f64."""
+    dy = np.ascontiguousarray(dy)
+    if elt == "bf16":
+        d = bf16_to_f32(dy.astype(np.uint16))
+    elif elt == "f16":
+        d = f16_to_f32(dy.astype(np.uint16))
+    else:
+        d = dy.astype(np.float32)
+    if cols is not None:
+        d = d[:, np.asarray(cols, dtype=np.int64)]
+    return d.astype(np.float64).sum(axis=0)
+
+
 def gelu_tanh(x, elt="bf16"):
     x = _c(x, _STORE[elt])
     y = np.empty_like(x)
@@ -308,3 +325,63 @@ def attention_backward(q, k, v, dy, mask=None, causal=False, elt="bf16"):
     lib().oracle_attention_backward(_p(q), _p(k), _p(v), _p(dy), _p(m), int(bool(causal)), B, Sq,
                                     Sk, H, D, _ELT[elt], _p(dq), _p(dk), _p(dv))
     return dq, dk, dv
+
+
+def attention_sampled(q, k, v, dy, b, h, qrows=(), kcols=(), elt="bf16", block=1024):
+    """f64 attention without mask or causal order (attention.jl:106-221, the Wan self-attention
+    case) of one (batch b, head h), for sizes where the whole score matrix does not fit:
+    out, lse and dq for the query rows ``qrows``, and dk, dv for the key columns ``kcols``.
+    q, dy [B][Sq][H][D], k, v [B][Sk][H][D] as 16-bit patterns (bf16 or f16) or float32 values
+    (elt="f32"). dk and dv need every query's softmax and correction sum(dy .* out)
+    (attention.jl:190), so the queries are streamed in blocks of ``block`` rows through torch's
+    CPU f64 matrix products (all host threads). Returns a dict with "out" [nq][D], "lse" [nq],
+    "dq" [nq][D], "dk" [nk][D], "dv" [nk][D] (f64 numpy)."""
+    import torch
+
+    def dec(a, S):
+        a = np.ascontiguousarray(a[b, :, h, :])
+        if elt == "bf16":
+            f = bf16_to_f32(a.astype(np.uint16))
+        elif elt == "f16":
+            f = f16_to_f32(a.astype(np.uint16))
+        else:
+            f = a.astype(np.float32)
+        return torch.from_numpy(f.astype(np.float64))
+
+    Sq, Sk, D = q.shape[1], k.shape[1], q.shape[3]
+    Q, Kt, V, dY = dec(q, Sq), dec(k, Sk), dec(v, Sk), dec(dy, Sq)
+    sc = float(np.float32(1.0) / np.sqrt(np.float32(D)))  # 1 / sqrt(Float32(D)), attention.jl:129
+    res = {}
+
+    def rows_of(Qb, dYb):
+        S = (Qb @ Kt.T) * sc
+        m = S.max(dim=1, keepdim=True).values
+        E = torch.exp(S - m)
+        l = E.sum(dim=1, keepdim=True)
+        P = E / l
+        out = P @ V
+        corr = (dYb * out).sum(dim=1, keepdim=True)
+        return P, out, (m + torch.log(l)).squeeze(1), corr
+
+    qrows = np.asarray(qrows, dtype=np.int64)
+    if qrows.size:
+        ix = torch.from_numpy(qrows)
+        P, out, lse, corr = rows_of(Q[ix], dY[ix])
+        dS = P * (dY[ix] @ V.T - corr)
+        res["out"], res["lse"] = out.numpy(), lse.numpy()
+        res["dq"] = (sc * (dS @ Kt)).numpy()
+    kcols = np.asarray(kcols, dtype=np.int64)
+    if kcols.size:
+        kx = torch.from_numpy(kcols)
+        Vc = V[kx]
+        dk = torch.zeros((kcols.size, D), dtype=torch.float64)
+        dv = torch.zeros((kcols.size, D), dtype=torch.float64)
+        for i0 in range(0, Sq, block):
+            Qb, dYb = Q[i0:i0 + block], dY[i0:i0 + block]
+            P, _, _, corr = rows_of(Qb, dYb)
+            Pc = P[:, kx]
+            dSc = Pc * (dYb @ Vc.T - corr)
+            dv += Pc.T @ dYb
+            dk += sc * (dSc.T @ Qb)
+        res["dk"], res["dv"] = dk.numpy(), dv.numpy()
+    return res

@@ -29,6 +29,8 @@ EXPORTS = (
     "reels_hip_i8lora_fwd_f16",
     "reels_hip_i8lora_bwd",
     "reels_hip_i8lora_bwd_f16",
+    "reels_hip_i8lora_bwd_bias",
+    "reels_hip_i8lora_bwd_bias_f16",
     "reels_hip_gelu_tanh",
     "reels_hip_gelu_tanh_f16",
     "reels_hip_gelu_tanh_bwd",
@@ -36,6 +38,7 @@ EXPORTS = (
     "reels_hip_i8lora_workspace_bytes_f32",
     "reels_hip_i8lora_fwd_f32",
     "reels_hip_i8lora_bwd_f32",
+    "reels_hip_i8lora_bwd_bias_f32",
     "reels_hip_gelu_tanh_f32",
     "reels_hip_gelu_tanh_bwd_f32",
     "reels_hip_attention_workspace_bytes",
@@ -94,6 +97,10 @@ def lib():
         bwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, ctypes.c_float, vp, vp, vp,
                         vp, sz, vp]
         bwd.restype = ctypes.c_int
+        bwb = getattr(L, "reels_hip_i8lora_bwd_bias" + sfx)
+        bwb.argtypes = [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, ctypes.c_float, vp, vp, vp,
+                        vp, vp, sz, vp]
+        bwb.restype = ctypes.c_int
         g, gb = getattr(L, "reels_hip_gelu_tanh" + sfx), getattr(L, "reels_hip_gelu_tanh_bwd" + sfx)
         g.argtypes = [vp, vp, i64, vp]
         g.restype = ctypes.c_int

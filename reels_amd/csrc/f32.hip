@@ -589,7 +589,7 @@ static PlanF32 plan_f32(int64_t M, int64_t K, int64_t N, int64_t r, bool aligned
 }
 
 struct WsF32 {
-  size_t at, bt, h, wd, u, pa, pb, total;
+  size_t at, bt, h, wd, u, pa, pb, pbias, total;
 };
 
 static WsF32 ws_f32(int64_t M, int64_t K, int64_t N, int64_t r, int which, const PlanF32& p) {
@@ -605,6 +605,7 @@ static WsF32 ws_f32(int64_t M, int64_t K, int64_t N, int64_t r, int which, const
     w.u = take((size_t)M * r * 4);
     w.pa = take(p.fast && r > 0 ? (size_t)p.splits * K * r * 4 : 0);
     w.pb = take(p.fast && r > 0 ? (size_t)p.splits * N * r * 4 : 0);
+    w.pbias = take(colsum_partial_bytes(M, N));  // the bias gradient's split partials
   }
   w.total = off == 0 ? 256 : off;
   return w;
@@ -699,11 +700,11 @@ static int i8lora_fwd_f32_impl(const float* x, const int8_t* q, const float* sca
   return launch_f32gemm(0, g, st);
 }
 
-static int i8lora_bwd_f32_impl(const float* dy, const float* x, const float* hh, const int8_t* q,
-                               const float* scales, const float* A, const float* B, int64_t M,
-                               int64_t K, int64_t N, int64_t r, float c, float* dx, float* dA,
-                               float* dB, void* workspace, size_t ws_bytes, hipStream_t st) {
-  const char* fn = "reels_hip_i8lora_bwd_f32";
+static int i8lora_bwd_f32_impl(const char* fn, const float* dy, const float* x, const float* hh,
+                               const int8_t* q, const float* scales, const float* A,
+                               const float* B, int64_t M, int64_t K, int64_t N, int64_t r, float c,
+                               float* dx, float* dA, float* dB, float* dbias, void* workspace,
+                               size_t ws_bytes, hipStream_t st) {
   if (M < 0 || K <= 0 || N <= 0 || r < 0 || r > 4096)
     return fail(REELS_HIP_EINVAL, std::string(fn) + ": need M >= 0, K > 0, N > 0, 0 <= r <= 4096");
   if (!(c == c)) return fail(REELS_HIP_EINVAL, std::string(fn) + ": lora_scale is NaN");
@@ -718,12 +719,16 @@ static int i8lora_bwd_f32_impl(const float* dy, const float* x, const float* hh,
       { TraceScope _ts(st, "zero_f32_kernel"); zero_f32_kernel<<<g1(N * r), 256, 0, st>>>(dB, N * r); }
       if ((rc = check_launch("zero_f32_kernel"))) return rc;
     }
+    if (dbias) {
+      { TraceScope _ts(st, "zero_f32_kernel"); zero_f32_kernel<<<g1(N), 256, 0, st>>>(dbias, N); }
+      if ((rc = check_launch("zero_f32_kernel"))) return rc;
+    }
     return REELS_HIP_OK;
   }
   if (!dy || !q || !scales || (r > 0 && (!A || !B)) || ((dA || (dB && !hh)) && !x))
     return fail(REELS_HIP_EINVAL, std::string(fn) + ": NULL dy, q, scales, A/B with r > 0, or x "
                                   "needed for dA / recomputing h");
-  if (!dx && !dA && !dB) return REELS_HIP_OK;
+  if (!dx && !dA && !dB && !dbias) return REELS_HIP_OK;
   const bool aligned = aligned16(dy) && aligned16(x) && aligned16(hh) && aligned16(q) &&
                        aligned16(scales) && aligned16(A) && aligned16(B) && aligned16(dx) &&
                        aligned16(dA) && aligned16(dB) && aligned16(workspace);
@@ -759,6 +764,8 @@ static int i8lora_bwd_f32_impl(const float* dy, const float* x, const float* hh,
       { TraceScope _ts(st, "gf_colgrad_kernel<true>"); gf_colgrad_kernel<true><<<g1(N * r), 256, 0, st>>>(dy, M, N, hp, (int)r, c, dB); }
       if ((rc = check_launch("gf_colgrad_kernel"))) return rc;
     }
+    if (dbias)
+      return launch_colsum(REELS_HIP_F32, dy, M, N, reinterpret_cast<float*>(ws + w.pbias), dbias, st);
     return REELS_HIP_OK;
   }
   // 1. u = dy B^T (B [r][N] rows are the projection rows); 2. dx = dy wt^T + c u A^T
@@ -792,6 +799,8 @@ static int i8lora_bwd_f32_impl(const float* dy, const float* x, const float* hh,
     }
     if ((rc = launch_colgrad_f32(dy, M, N, hp, (int)r, p, c, reinterpret_cast<float*>(ws + w.pb), dB, true, st))) return rc;
   }
+  if (dbias)
+    return launch_colsum(REELS_HIP_F32, dy, M, N, reinterpret_cast<float*>(ws + w.pbias), dbias, st);
   return REELS_HIP_OK;
 }
 
@@ -823,8 +832,21 @@ extern "C" int reels_hip_i8lora_bwd_f32(const float* dy, const float* x, const f
                                         float lora_scale, float* dx, float* dA, float* dB,
                                         void* workspace, size_t ws_bytes, void* stream) {
   clear_error();
-  return i8lora_bwd_f32_impl(dy, x, h, q, scales, A, B, M, K, N, r, lora_scale, dx, dA, dB,
-                             workspace, ws_bytes, reinterpret_cast<hipStream_t>(stream));
+  return i8lora_bwd_f32_impl("reels_hip_i8lora_bwd_f32", dy, x, h, q, scales, A, B, M, K, N, r,
+                             lora_scale, dx, dA, dB, nullptr, workspace, ws_bytes,
+                             reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int reels_hip_i8lora_bwd_bias_f32(const float* dy, const float* x, const float* h,
+                                             const int8_t* q, const float* scales, const float* A,
+                                             const float* B, int64_t M, int64_t K, int64_t N,
+                                             int64_t r, float lora_scale, float* dx, float* dA,
+                                             float* dB, float* dbias, void* workspace,
+                                             size_t ws_bytes, void* stream) {
+  clear_error();
+  return i8lora_bwd_f32_impl("reels_hip_i8lora_bwd_bias_f32", dy, x, h, q, scales, A, B, M, K, N,
+                             r, lora_scale, dx, dA, dB, dbias, workspace, ws_bytes,
+                             reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int reels_hip_gelu_tanh_f32(const float* x, float* y, int64_t n, void* stream) {

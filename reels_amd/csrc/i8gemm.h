@@ -85,4 +85,11 @@ int launch_skinny(int mode, int elt, const SkinnyPlan& p, const uint16_t* act, c
 int launch_reduce_partials(const float* part, int splits, int64_t Od, int rp, int r, float c,
                            float* out, bool trans, hipStream_t st);
 
+// out[o] = sum_m src[m][o] in f32 (src [M][Od] of element type elt: REELS_HIP_F32, _BF16 or
+// _F16): the bias gradient. Split-M partials in part (colsum_partial_bytes(M, Od) bytes), summed
+// in split order; the same splits and order as the dB gradient pass's fused column sums.
+int launch_colsum(int elt, const void* src, int64_t M, int64_t Od, float* part, float* out,
+                  hipStream_t st);
+size_t colsum_partial_bytes(int64_t M, int64_t Od);
+
 }  // namespace reels

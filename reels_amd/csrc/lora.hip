@@ -263,11 +263,17 @@ struct CgJob {
   const uint16_t* Lm;   // [M][ld_lm]
   float* part;          // partials, or NULL with out set
   float* out;           // one split: c * sum written here ([Od][r], or [r][Od] with trans)
+  float* bpart;         // column sums of src (the bias gradient): split partials [splits][Od],
+  float* bout;          // or with one split the sums themselves [Od]; both NULL: none
   int64_t Od, tps;      // output rows; tokens per split
   int nbx, trans;       // column blocks
 };
 
-template <int RT, int ELT>
+// BS: jobs with bpart or bout set also sum the columns of src (sum_m src[m][o], unscaled) from
+// the registers the tile copies pass through, in the order of colsum_kernel: per 64-token step
+// thread (c = tid % 16, g = tid / 16) adds rows g, g + 16, g + 32, g + 48 of columns 8c..8c+7,
+// steps in token order, then the 16 row groups are added in order g = 0..15
+template <int RT, int ELT, bool BS>
 __global__ __launch_bounds__(256) void colgrad_kernel(CgJob j0, CgJob j1, int nb0, int64_t M,
                                                       int ld_lm, int rp, int ld_part, float c,
                                                       int r) {
@@ -286,6 +292,12 @@ __global__ __launch_bounds__(256) void colgrad_kernel(CgJob j0, CgJob j1, int nb
   const int64_t tokens_per_split = second ? j1.tps : j0.tps;
   const int nbx = second ? j1.nbx : j0.nbx;
   const int trans = second ? j1.trans : j0.trans;
+  float* __restrict__ bpart = second ? j1.bpart : j0.bpart;
+  float* __restrict__ bout = second ? j1.bout : j0.bout;
+  const bool bsum = BS && (bpart != nullptr || bout != nullptr);  // uniform over the block
+  float csum[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) csum[e] = 0.0f;
   const int64_t o0 = (int64_t)(bj % nbx) * BO;
   const int sp = bj / nbx;
   const int64_t mbeg = (int64_t)sp * tokens_per_split;
@@ -334,6 +346,16 @@ __global__ __launch_bounds__(256) void colgrad_kernel(CgJob j0, CgJob j1, int nb
     for (int i = 0; i < 4; ++i) {
       const int id = tid + 256 * i, row = id >> 4, c = id & 15;
       *reinterpret_cast<u32x4*>(&ssrc[row * SROW + c * 8]) = rs[i];
+    }
+    if (BS && bsum) {
+      // rows past the split or M arrive as zeros, which leave the sums unchanged
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          csum[2 * e] += E::lo(rs[i][e]);
+          csum[2 * e + 1] += E::hi(rs[i][e]);
+        }
     }
 #pragma unroll
     for (int i = 0; i < RT; ++i) {
@@ -388,6 +410,24 @@ __global__ __launch_bounds__(256) void colgrad_kernel(CgJob j0, CgJob j1, int nb
     step(mb, rs0, rl0);
     step(mb + TM, rs1, rl1);
   }
+  if (BS && bsum) {
+    // the 16 row groups' sums through LDS (the step loop ended with a barrier: ssrc is free)
+    float* red = reinterpret_cast<float*>(ssrc);  // [16][BO]
+    const int cc = tid & 15, gg = tid >> 4;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) red[gg * BO + cc * 8 + e] = csum[e];
+    __syncthreads();
+    if (tid < BO) {
+      float sum = 0.0f;
+#pragma unroll
+      for (int q = 0; q < 16; ++q) sum += red[q * BO + tid];
+      const int64_t o = o0 + tid;
+      if (o < Od) {
+        if (bout != nullptr) bout[o] = sum;
+        else bpart[(int64_t)sp * Od + o] = sum;
+      }
+    }
+  }
   // D lane layout: row (o) = wave*32 + (v/4)*8 + (lane/32)*4 + v%4, column j = t*32 + lane%32
   const int l32 = lane & 31, lhi = lane >> 5;
 #pragma unroll
@@ -408,6 +448,144 @@ __global__ __launch_bounds__(256) void colgrad_kernel(CgJob j0, CgJob j1, int nb
       }
     }
   }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Column sums sum_m src[m][o] of a [M][Od] operand: the gradient of a trainable bias, the
+// pullback of mixed_add (src/layers/linear.jl:7-13) for LoRALinear's bias when train_bias is set
+// (src/layers/lora.jl:37-38, 64-67), dbias[n] = sum over tokens of dy[m][n], in f32.
+// Split-M partials part[sp][o] (or, with one split, the sums written to out), then
+// colsum_reduce_kernel adds the splits in order. The block and thread order is the one the dB
+// gradient pass uses when it sums dy's columns beside its MFMAs (colgrad_kernel with BS): blocks
+// are (column block of 128, split), column block fastest; per 64-token step thread
+// (c = tid % 16, g = tid / 16) adds rows g, g + 16, g + 32, g + 48 of columns 8c..8c+7, steps in
+// token order; then the 16 row groups are added in order. Same splits, same bits.
+// VEC: 16-byte loads (16-byte aligned rows, Od a multiple of 8), else one element at a time.
+template <int ELT, bool VEC>
+__global__ __launch_bounds__(256) void colsum_kernel(const uint16_t* __restrict__ src, int64_t M,
+                                                     int64_t Od, int64_t tps,
+                                                     float* __restrict__ part,
+                                                     float* __restrict__ out) {
+  using E = Elt<ELT>;
+  constexpr int BO = cg::BO, TM = cg::TM;
+  __shared__ float red[16 * BO];
+  const int tid = threadIdx.x, cc = tid & 15, gg = tid >> 4;
+  const int nbx = (int)((Od + BO - 1) / BO);
+  const int64_t o0 = (int64_t)(blockIdx.x % nbx) * BO;
+  const int sp = (int)(blockIdx.x / nbx);
+  const int64_t mbeg = (int64_t)sp * tps;
+  const int64_t mend = mbeg + tps < M ? mbeg + tps : M;
+  const int64_t oc = o0 + cc * 8;
+  float csum[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) csum[e] = 0.0f;
+  auto add_row = [&](int64_t m) {
+    const uint16_t* row = src + m * Od;
+    if (VEC) {
+      if (oc < Od) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(row + oc);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          csum[2 * e] += E::lo(v[e]);
+          csum[2 * e + 1] += E::hi(v[e]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (oc + e < Od) csum[e] += E::to_f32(row[oc + e]);
+    }
+  };
+  int64_t mb = mbeg;
+  for (; mb + TM <= mend; mb += TM) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) add_row(mb + gg + 16 * i);
+  }
+  if (mb < mend) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (mb + gg + 16 * i < mend) add_row(mb + gg + 16 * i);
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) red[gg * BO + cc * 8 + e] = csum[e];
+  __syncthreads();
+  if (tid < BO) {
+    float sum = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) sum += red[q * BO + tid];
+    const int64_t o = o0 + tid;
+    if (o < Od) {
+      if (part == nullptr) out[o] = sum;
+      else part[(int64_t)sp * Od + o] = sum;
+    }
+  }
+}
+
+// The same over f32 src (the fp32 path): per 64-token step thread (c = tid % 32, g = tid / 32)
+// adds rows g, g + 8, ..., g + 56 of columns 4c..4c+3; then the 8 row groups in order.
+template <bool VEC>
+__global__ __launch_bounds__(256) void colsum_f32_kernel(const float* __restrict__ src, int64_t M,
+                                                         int64_t Od, int64_t tps,
+                                                         float* __restrict__ part,
+                                                         float* __restrict__ out) {
+  constexpr int BO = cg::BO, TM = cg::TM;
+  __shared__ float red[8 * BO];
+  const int tid = threadIdx.x, cc = tid & 31, gg = tid >> 5;
+  const int nbx = (int)((Od + BO - 1) / BO);
+  const int64_t o0 = (int64_t)(blockIdx.x % nbx) * BO;
+  const int sp = (int)(blockIdx.x / nbx);
+  const int64_t mbeg = (int64_t)sp * tps;
+  const int64_t mend = mbeg + tps < M ? mbeg + tps : M;
+  const int64_t oc = o0 + cc * 4;
+  float csum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  auto add_row = [&](int64_t m) {
+    const float* row = src + m * Od;
+    if (VEC) {
+      if (oc < Od) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(row + oc);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) csum[e] += v[e];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (oc + e < Od) csum[e] += row[oc + e];
+    }
+  };
+  int64_t mb = mbeg;
+  for (; mb + TM <= mend; mb += TM) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) add_row(mb + gg + 8 * i);
+  }
+  if (mb < mend) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (mb + gg + 8 * i < mend) add_row(mb + gg + 8 * i);
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) red[gg * BO + cc * 4 + e] = csum[e];
+  __syncthreads();
+  if (tid < BO) {
+    float sum = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) sum += red[q * BO + tid];
+    const int64_t o = o0 + tid;
+    if (o < Od) {
+      if (part == nullptr) out[o] = sum;
+      else part[(int64_t)sp * Od + o] = sum;
+    }
+  }
+}
+
+// out[o] = sum_sp part[sp][o] in split order
+__global__ __launch_bounds__(256) void colsum_reduce_kernel(const float* __restrict__ part,
+                                                            int splits, int64_t Od,
+                                                            float* __restrict__ out) {
+  const int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (o >= Od) return;
+  float sum = 0.0f;
+  for (int sp = 0; sp < splits; ++sp) sum += part[(int64_t)sp * Od + o];
+  out[o] = sum;
 }
 
 // out = c * sum_sp part[sp][o][j] in split order; TRANS: out[j][o] (dB [r][N]) else out[o][j].
@@ -454,9 +632,19 @@ struct RpJob {
   int64_t Od;
   int splits;
 };
+// blocks from nbs on sum the column-sum partials bj.part [splits][Od] into bj.out (as
+// colsum_reduce_kernel; nbs = gridDim.x: none)
 __global__ __launch_bounds__(256) void reduce_partials2_kernel(RpJob ja, RpJob jb, int nb0, int rp,
-                                                               int r, float c) {
+                                                               int r, float c, RpJob bj, int nbs) {
   __shared__ float tile[8][33];
+  if ((int)blockIdx.x >= nbs) {
+    const int64_t o = (int64_t)((int)blockIdx.x - nbs) * blockDim.x + threadIdx.x;
+    if (o >= bj.Od) return;
+    float sum = 0.0f;
+    for (int sp = 0; sp < bj.splits; ++sp) sum += bj.part[(int64_t)sp * bj.Od + o];
+    bj.out[o] = sum;
+    return;
+  }
   if ((int)blockIdx.x < nb0) {
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= ja.Od * r) return;
@@ -702,7 +890,7 @@ static Plan make_plan(int64_t M, int64_t K, int64_t N, int64_t r, bool ptrs_alig
 
 // workspace layout (byte offsets, 256-aligned); identical computation for sizing and use
 struct WsLayout {
-  size_t h, u, dys, wd, at, bt, ap, pa, pb, kp, rq, total;
+  size_t h, u, dys, wd, at, bt, ap, pa, pb, pbias, kp, rq, total;
 };
 
 static WsLayout ws_layout(int64_t M, int64_t K, int64_t N, int64_t r, int which, const Plan& p) {
@@ -727,6 +915,7 @@ static WsLayout ws_layout(int64_t M, int64_t K, int64_t N, int64_t r, int which,
       w.wd = take(pb > pf ? pb : pf);
       w.pa = take(r > 0 ? (size_t)p.sa.splits * K * rp * 4 : 0);
       w.pb = take(r > 0 ? (size_t)p.sb.splits * N * rp * 4 : 0);
+      w.pbias = take(colsum_partial_bytes(M, N));
     }
     w.total = off == 0 ? 256 : off;
     return w;
@@ -749,6 +938,7 @@ static WsLayout ws_layout(int64_t M, int64_t K, int64_t N, int64_t r, int which,
     w.dys = take(p.fast && !p.deq ? (size_t)M * N * 2 : 0);
     w.pa = take(p.fast && r > 0 ? (size_t)p.sa.splits * K * rp * 4 : 0);
     w.pb = take(p.fast && r > 0 ? (size_t)p.sb.splits * N * rp * 4 : 0);
+    w.pbias = take(colsum_partial_bytes(M, N));  // the bias gradient's split partials
   }
   w.total = off == 0 ? 256 : off;
   return w;
@@ -845,6 +1035,8 @@ struct CgPass {
   float* part;
   float* out;
   bool trans;
+  float* bpart = nullptr;  // column sums of src too (the bias gradient): split partials
+  float* bout = nullptr;   // [sp.splits][Od] and the result [Od]; NULL bout: none
 };
 
 // dA and dB passes (either may be absent: src NULL) in one colgrad launch per rank chunk, then
@@ -861,27 +1053,45 @@ static int launch_colgrad2(int elt, int64_t M, int r, int rp, float c, const CgP
     const int rt = (rpc + 31) / 32;
     CgJob j[2] = {};
     int nb[2] = {0, 0};
+    bool bs = false;
     for (int i = 0; i < 2; ++i) {
       if (!ps[i]) continue;
       const CgPass& q = *ps[i];
       j[i].src = q.src; j[i].Lm = q.Lm + c0; j[i].part = q.part + c0;
       j[i].out = direct[i] ? q.out : nullptr;
+      if (q.bout && c0 == 0) {  // the column sums ride on the first rank chunk's launch
+        if (q.sp.splits == 1) j[i].bout = q.bout;
+        else j[i].bpart = q.bpart;
+        bs = true;
+      }
       j[i].Od = q.Od; j[i].tps = q.sp.tps; j[i].trans = q.trans ? 1 : 0;
       j[i].nbx = (int)ceil_div(q.Od, cg::BO);
       nb[i] = j[i].nbx * q.sp.splits;
     }
     const unsigned grid = (unsigned)(nb[0] + nb[1]);
     {
-      TraceScope _ts(st, rt <= 1 ? "colgrad_kernel<1>" : rt == 2 ? "colgrad_kernel<2>" : "colgrad_kernel<4>");
+      TraceScope _ts(st, rt <= 1 ? (bs ? "colgrad_kernel<1,bias>" : "colgrad_kernel<1>")
+                         : rt == 2 ? (bs ? "colgrad_kernel<2,bias>" : "colgrad_kernel<2>")
+                                   : (bs ? "colgrad_kernel<4,bias>" : "colgrad_kernel<4>"));
       with_elt(elt, [&](auto e) {
         constexpr int T = decltype(e)::value;
-        if (rt <= 1) colgrad_kernel<1, T><<<grid, 256, 0, st>>>(j[0], j[1], nb[0], M, rp, rpc, rp, c, r);
-        else if (rt == 2) colgrad_kernel<2, T><<<grid, 256, 0, st>>>(j[0], j[1], nb[0], M, rp, rpc, rp, c, r);
-        else colgrad_kernel<4, T><<<grid, 256, 0, st>>>(j[0], j[1], nb[0], M, rp, rpc, rp, c, r);
+        if (bs) {
+          if (rt <= 1) colgrad_kernel<1, T, true><<<grid, 256, 0, st>>>(j[0], j[1], nb[0], M, rp, rpc, rp, c, r);
+          else if (rt == 2) colgrad_kernel<2, T, true><<<grid, 256, 0, st>>>(j[0], j[1], nb[0], M, rp, rpc, rp, c, r);
+          else colgrad_kernel<4, T, true><<<grid, 256, 0, st>>>(j[0], j[1], nb[0], M, rp, rpc, rp, c, r);
+        } else {
+          if (rt <= 1) colgrad_kernel<1, T, false><<<grid, 256, 0, st>>>(j[0], j[1], nb[0], M, rp, rpc, rp, c, r);
+          else if (rt == 2) colgrad_kernel<2, T, false><<<grid, 256, 0, st>>>(j[0], j[1], nb[0], M, rp, rpc, rp, c, r);
+          else colgrad_kernel<4, T, false><<<grid, 256, 0, st>>>(j[0], j[1], nb[0], M, rp, rpc, rp, c, r);
+        }
       });
     }
     if (int rc = check_launch("colgrad_kernel")) return rc;
   }
+  // the column-sum partials still to be added up (at most one pass carries them)
+  const CgPass* bias_red = nullptr;
+  for (int i = 0; i < 2; ++i)
+    if (ps[i] && ps[i]->bout && ps[i]->sp.splits > 1) bias_red = ps[i];
   // the reductions: dA and dB together in one launch when both need one
   const CgPass* need[2] = {nullptr, nullptr};
   int nn = 0;
@@ -892,15 +1102,70 @@ static int launch_colgrad2(int elt, int64_t M, int r, int rp, float c, const CgP
     const RpJob jb{need[1]->part, need[1]->out, need[1]->Od, need[1]->sp.splits};
     const int nb0 = (int)ceil_div(ja.Od * r, 256);
     const int nb1 = (int)(ceil_div(jb.Od, 8) * ceil_div(r, 32));
+    RpJob bj{};
+    int nb2 = 0;
+    if (bias_red) {
+      bj = RpJob{bias_red->bpart, bias_red->bout, bias_red->Od, bias_red->sp.splits};
+      nb2 = (int)ceil_div(bj.Od, 256);
+      bias_red = nullptr;
+    }
     { TraceScope _ts(st, "reduce_partials2_kernel");
-      reduce_partials2_kernel<<<(unsigned)(nb0 + nb1), 256, 0, st>>>(ja, jb, nb0, rp, r, c); }
+      reduce_partials2_kernel<<<(unsigned)(nb0 + nb1 + nb2), 256, 0, st>>>(ja, jb, nb0, rp, r, c, bj, nb0 + nb1); }
     return check_launch("reduce_partials2_kernel");
   }
   for (int i = 0; i < nn; ++i) {
     const CgPass& q = *need[i];
     if (int rc = launch_reduce_partials(q.part, q.sp.splits, q.Od, rp, r, c, q.out, q.trans, st)) return rc;
   }
+  if (bias_red) {
+    { TraceScope _ts(st, "colsum_reduce_kernel");
+      colsum_reduce_kernel<<<(unsigned)ceil_div(bias_red->Od, 256), 256, 0, st>>>(
+          bias_red->bpart, bias_red->sp.splits, bias_red->Od, bias_red->bout); }
+    return check_launch("colsum_reduce_kernel");
+  }
   return REELS_HIP_OK;
+}
+
+// Column sums out[o] = sum_m src[m][o] of a [M][Od] operand of element type elt (F32, BF16 or
+// F16), in the split plan of the dB gradient pass (split_for(M, Od)): partials in part
+// (colsum_partial_bytes(M, Od) bytes), then the ordered sum over the splits
+int launch_colsum(int elt, const void* src, int64_t M, int64_t Od, float* part, float* out,
+                  hipStream_t st) {
+  if (Od <= 0) return REELS_HIP_OK;
+  if (M == 0) {
+    { TraceScope _ts(st, "fill_f32_kernel"); fill_f32_kernel<<<grid1(Od), 256, 0, st>>>(out, Od, 0.0f); }
+    return check_launch("fill_f32_kernel");
+  }
+  const Split sp = split_for(M, Od);
+  const unsigned grid = (unsigned)(ceil_div(Od, cg::BO) * sp.splits);
+  float* pt = sp.splits > 1 ? part : nullptr;
+  const size_t esz = elt == REELS_HIP_F32 ? 4 : 2;
+  const bool vec = aligned16(src) && (Od * (int64_t)esz) % 16 == 0;
+  {
+    TraceScope _ts(st, "colsum_kernel");
+    if (elt == REELS_HIP_F32) {
+      const float* f = static_cast<const float*>(src);
+      if (vec) colsum_f32_kernel<true><<<grid, 256, 0, st>>>(f, M, Od, sp.tps, pt, out);
+      else colsum_f32_kernel<false><<<grid, 256, 0, st>>>(f, M, Od, sp.tps, pt, out);
+    } else {
+      const uint16_t* h = static_cast<const uint16_t*>(src);
+      with_elt(elt, [&](auto e) {
+        constexpr int T = decltype(e)::value;
+        if (vec) colsum_kernel<T, true><<<grid, 256, 0, st>>>(h, M, Od, sp.tps, pt, out);
+        else colsum_kernel<T, false><<<grid, 256, 0, st>>>(h, M, Od, sp.tps, pt, out);
+      });
+    }
+  }
+  if (int rc = check_launch("colsum_kernel")) return rc;
+  if (sp.splits == 1) return REELS_HIP_OK;
+  { TraceScope _ts(st, "colsum_reduce_kernel");
+    colsum_reduce_kernel<<<(unsigned)ceil_div(Od, 256), 256, 0, st>>>(part, sp.splits, Od, out); }
+  return check_launch("colsum_reduce_kernel");
+}
+
+size_t colsum_partial_bytes(int64_t M, int64_t Od) {
+  const Split sp = split_for(M, Od);
+  return sp.splits > 1 ? (size_t)sp.splits * (size_t)Od * 4 : 0;
 }
 
 // dst [rows][cols_dst] (row stride ld_dst) from src [rows][cols] (row stride ld_src), zeros past cols
@@ -1064,7 +1329,8 @@ static int i8lora_fwd_impl(int elt, const char* fn, const void* x, const int8_t*
 static int i8lora_bwd_impl(int elt, const char* fn, const void* dy, const void* x, const void* h,
                            const int8_t* q, const float* scales, const void* A, const void* B,
                            int64_t M, int64_t K, int64_t N, int64_t r, float lora_scale, void* dx,
-                           float* dA, float* dB, void* workspace, size_t ws_bytes, void* stream) {
+                           float* dA, float* dB, float* dbias, void* workspace, size_t ws_bytes,
+                           void* stream) {
   clear_error();
   if (M < 0 || K <= 0 || N <= 0 || r < 0 || r > 4096)
     return fail(REELS_HIP_EINVAL, std::string(fn) + ": " "need M >= 0, K > 0, N > 0, 0 <= r <= 4096");
@@ -1082,13 +1348,17 @@ static int i8lora_bwd_impl(int elt, const char* fn, const void* dy, const void* 
       { TraceScope _ts(st, "fill_f32_kernel"); fill_f32_kernel<<<grid1(N * r), 256, 0, st>>>(dB, N * r, 0.0f); }
       if ((rc = check_launch("fill_f32_kernel"))) return rc;
     }
+    if (dbias) {
+      { TraceScope _ts(st, "fill_f32_kernel"); fill_f32_kernel<<<grid1(N), 256, 0, st>>>(dbias, N, 0.0f); }
+      if ((rc = check_launch("fill_f32_kernel"))) return rc;
+    }
     return REELS_HIP_OK;
   }
   if (!dy || !q || !scales || (r > 0 && (!A || !B)) || ((dA || (dB && !h)) && !x))
     return fail(REELS_HIP_EINVAL, std::string(fn) + ": " "NULL dy, q, scales, A/B with r > 0, or x "
                                   "needed for dA / recomputing h");
-  if (!dx && !dA && !dB) return REELS_HIP_OK;
-  const bool al = all_aligned({dy, x, h, q, scales, A, B, dx, dA, dB});
+  if (!dx && !dA && !dB && !dbias) return REELS_HIP_OK;
+  const bool al = all_aligned({dy, x, h, q, scales, A, B, dx, dA, dB, dbias});
   Plan p = make_plan(M, K, N, r, al);
   WsLayout w = ws_layout(M, K, N, r, REELS_HIP_WS_BWD, p);
   if (workspace == nullptr || ws_bytes < w.total)
@@ -1127,6 +1397,8 @@ static int i8lora_bwd_impl(int elt, const char* fn, const void* dy, const void* 
       { TraceScope _ts(st, "g_colgrad_kernel<true>"); with_elt(elt, [&](auto e) { g_colgrad_kernel<true, decltype(e)::value><<<grid1(N * r), 256, 0, st>>>(dyb, M, N, hh, r, (int)r, lora_scale, dB); }); }
       if ((rc = check_launch("g_colgrad_kernel"))) return rc;
     }
+    if (dbias)
+      return launch_colsum(elt, dyb, M, N, reinterpret_cast<float*>(ws + w.pbias), dbias, st);
     return REELS_HIP_OK;
   }
 
@@ -1223,9 +1495,16 @@ static int i8lora_bwd_impl(int elt, const char* fn, const void* dy, const void* 
   {
     CgPass ga{}, gb{};
     if (dA) ga = CgPass{xb, K, u, p.sa, reinterpret_cast<float*>(ws + w.pa), dA, false};
-    if (dB) gb = CgPass{dyb, N, hh, p.sb, reinterpret_cast<float*>(ws + w.pb), dB, true};
+    if (dB) {
+      gb = CgPass{dyb, N, hh, p.sb, reinterpret_cast<float*>(ws + w.pb), dB, true};
+      // the bias gradient from the same pass over dy
+      gb.bpart = reinterpret_cast<float*>(ws + w.pbias);
+      gb.bout = dbias;
+    }
     if ((rc = launch_colgrad2(elt, M, (int)r, p.rp, lora_scale, ga, gb, st))) return rc;
   }
+  if (dbias && !dB)
+    return launch_colsum(elt, dyb, M, N, reinterpret_cast<float*>(ws + w.pbias), dbias, st);
   return REELS_HIP_OK;
 }
 
@@ -1287,7 +1566,27 @@ extern "C" int reels_hip_i8lora_bwd(const void* dy, const void* x, const void* h
                                     float* dA, float* dB, void* workspace, size_t ws_bytes,
                                     void* stream) {
   return i8lora_bwd_impl(REELS_HIP_BF16, "reels_hip_i8lora_bwd", dy, x, h, q, scales, A, B, M, K, N,
-                         r, lora_scale, dx, dA, dB, workspace, ws_bytes, stream);
+                         r, lora_scale, dx, dA, dB, nullptr, workspace, ws_bytes, stream);
+}
+
+extern "C" int reels_hip_i8lora_bwd_bias(const void* dy, const void* x, const void* h,
+                                         const int8_t* q, const float* scales, const void* A,
+                                         const void* B, int64_t M, int64_t K, int64_t N,
+                                         int64_t r, float lora_scale, void* dx, float* dA,
+                                         float* dB, float* dbias, void* workspace,
+                                         size_t ws_bytes, void* stream) {
+  return i8lora_bwd_impl(REELS_HIP_BF16, "reels_hip_i8lora_bwd_bias", dy, x, h, q, scales, A, B, M,
+                         K, N, r, lora_scale, dx, dA, dB, dbias, workspace, ws_bytes, stream);
+}
+
+extern "C" int reels_hip_i8lora_bwd_bias_f16(const void* dy, const void* x, const void* h,
+                                             const int8_t* q, const float* scales, const void* A,
+                                             const void* B, int64_t M, int64_t K, int64_t N,
+                                             int64_t r, float lora_scale, void* dx, float* dA,
+                                             float* dB, float* dbias, void* workspace,
+                                             size_t ws_bytes, void* stream) {
+  return i8lora_bwd_impl(REELS_HIP_F16, "reels_hip_i8lora_bwd_bias_f16", dy, x, h, q, scales, A, B,
+                         M, K, N, r, lora_scale, dx, dA, dB, dbias, workspace, ws_bytes, stream);
 }
 
 extern "C" int reels_hip_i8lora_bwd_f16(const void* dy, const void* x, const void* h,
@@ -1296,7 +1595,7 @@ extern "C" int reels_hip_i8lora_bwd_f16(const void* dy, const void* x, const voi
                                         float lora_scale, void* dx, float* dA, float* dB,
                                         void* workspace, size_t ws_bytes, void* stream) {
   return i8lora_bwd_impl(REELS_HIP_F16, "reels_hip_i8lora_bwd_f16", dy, x, h, q, scales, A, B, M, K,
-                         N, r, lora_scale, dx, dA, dB, workspace, ws_bytes, stream);
+                         N, r, lora_scale, dx, dA, dB, nullptr, workspace, ws_bytes, stream);
 }
 
 extern "C" int reels_hip_gelu_tanh(const void* x, void* y, int64_t n, void* stream) {

@@ -224,10 +224,12 @@ def i8lora_forward(x, weight: QuantizedMatrix, A=None, B=None, bias=None, lora_s
 
 
 def i8lora_backward(dy, x, weight: QuantizedMatrix, A=None, B=None, lora_scale=1.0, h=None,
-                    want_dx=True, want_dA=True, want_dB=True):
+                    want_dx=True, want_dA=True, want_dB=True, want_dbias=False):
     """(dx [M][K], dA f32 [K][r], dB f32 [r][N]) of lora_backward (lora.jl:106-118). dy, x, h,
     A and B share one dtype, bfloat16, float16 or float32 (reels_hip_i8lora_bwd / _bwd_f16 /
-    _bwd_f32); dx comes back in it."""
+    _bwd_f32); dx comes back in it. With want_dbias, a fourth result: the gradient of a trainable
+    bias, dbias f32 [N] = sum over tokens of dy (reels_hip_i8lora_bwd_bias*), the pullback of the
+    forward's mixed_add (linear.jl:7-13; lora.jl:37-38, 64-67)."""
     if dy.dim() != 2:
         raise ValueError(f"dy must be a [M][N] matrix, got shape {tuple(dy.shape)}")
     M, N = dy.shape
@@ -251,6 +253,14 @@ def i8lora_backward(dy, x, weight: QuantizedMatrix, A=None, B=None, lora_scale=1
     dB = torch.empty((r, N), dtype=torch.float32, device=dev) if (want_dB and r) else None
     nbytes = workspace_bytes(M, K, N, r, _lib.WS_BWD, dt)
     ws = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
+    if want_dbias:
+        dbias = torch.empty((N,), dtype=torch.float32, device=dev)
+        fn = "reels_hip_i8lora_bwd_bias" + _ACT_SUFFIX[dt]
+        _lib.check(fn, getattr(_lib.lib(), fn)(
+            _ptr(dy), _ptr(x), _ptr(h), _ptr(weight.values), _ptr(weight.scales), _ptr(A),
+            _ptr(B), M, K, N, r, float(lora_scale), _ptr(dx), _ptr(dA), _ptr(dB), _ptr(dbias),
+            _ptr(ws), nbytes, _stream(dev)))
+        return dx, dA, dB, dbias
     fn = "reels_hip_i8lora_bwd" + _ACT_SUFFIX[dt]
     _lib.check(fn, getattr(_lib.lib(), fn)(
         _ptr(dy), _ptr(x), _ptr(h), _ptr(weight.values), _ptr(weight.scales), _ptr(A), _ptr(B),
@@ -421,13 +431,15 @@ class I8LoRALinearFunction(torch.autograd.Function):
         x, A, B, values, scales, h = ctx.saved_tensors
         weight = QuantizedMatrix(values, scales)
         dy = dy.contiguous()
-        dx, dA, dB = i8lora_backward(dy, x, weight, A, B, ctx.lora_scale, h=h,
-                                     want_dx=ctx.needs_input_grad[0],
-                                     want_dA=ctx.needs_input_grad[1],
-                                     want_dB=ctx.needs_input_grad[2])
         # a trainable bias (LoRALinear train_bias): the pullback of mixed_add (linear.jl:7-13)
-        # sums dy over the tokens; summed in f32
-        dbias = dy.float().sum(0).to(ctx.bias_dtype) if ctx.needs_input_grad[5] else None
+        # sums dy over the tokens, in f32 inside the library (the dB pass's read of dy)
+        want_bias = ctx.needs_input_grad[5]
+        res = i8lora_backward(dy, x, weight, A, B, ctx.lora_scale, h=h,
+                              want_dx=ctx.needs_input_grad[0],
+                              want_dA=ctx.needs_input_grad[1],
+                              want_dB=ctx.needs_input_grad[2], want_dbias=want_bias)
+        dx, dA, dB = res[:3]
+        dbias = res[3].to(ctx.bias_dtype) if want_bias else None
         # dA and dB keep the f32 of the kernels when the adapter parameters are f32 masters;
         # otherwise they take the parameter dtype
         ad, bd = ctx.param_dtypes

@@ -198,3 +198,51 @@ def test_attention_argument_errors(dev):
     with pytest.raises(ValueError, match="head_dim must be 64 or 128"):
         x = torch.zeros(1, 4, 2, 32, device=dev, dtype=torch.bfloat16)
         memory_efficient_attention(x, x, x)
+
+
+def test_attention_wan14b_self_attention_full_size(dev):
+    """The benchmarked shape: Wan-2.1-14B self-attention of one block, 1 x 32760 tokens x 40 heads
+    x 128 (src/models/wan21/transformer.jl:199), bf16 ~N(0, 1). Against the f64 oracle: out, lse
+    and dq of 6 sampled queries (the first and the last among them) in every head; dk and dv of
+    6 sampled keys (the first and the last among them) in heads 0 and 39, whose oracle streams
+    all 32760 queries (the dK / dV kernel accumulates over 512 query steps). Every gradient
+    element: the exact identities dq, dk, dv (2 dy) = 2 (dq, dk, dv) (dy enters linearly and
+    scaling by 2 commutes with every rounding)."""
+    import torch
+    from reels_amd import memory_efficient_attention, memory_efficient_attention_backward
+    B, S, H, D = 1, 32760, 40, 128
+    print(f"[case] attention full size B={B} S={S} H={H} D={D} bf16", flush=True)
+    g = torch.Generator(device=dev).manual_seed(32760)
+    q, k, v, dy = (torch.randn((B, S, H, D), generator=g, device=dev).to(torch.bfloat16)
+                   for _ in range(4))
+    res = memory_efficient_attention(q, k, v)
+    gr = memory_efficient_attention_backward(q, k, v, dy, res.cache)
+    gr2 = memory_efficient_attention_backward(q, k, v, dy * 2, res.cache)
+    torch.cuda.synchronize()
+    for a, b2, name in zip(gr, gr2, ("dq", "dk", "dv")):
+        assert torch.equal((a * 2).view(torch.int16), b2.view(torch.int16)), f"{name}(2dy) != 2 {name}"
+    del gr2
+    host = [bf16_bits(t) for t in (q, k, v, dy)]
+    out = oracle.bf16_to_f32(bf16_bits(res.output))
+    lse = res.cache.logsumexp.cpu().numpy()
+    dq, dk, dv = (oracle.bf16_to_f32(bf16_bits(t)) for t in gr)
+    rng = np.random.default_rng(5)
+    qr = np.unique(np.concatenate([[0, S - 1], rng.integers(1, S - 1, 4)]))
+    got = {n: [] for n in ("out", "lse", "dq", "dk", "dv")}
+    ref = {n: [] for n in got}
+    for h in range(H):
+        r = oracle.attention_sampled(*host, 0, h, qrows=qr)
+        got["out"].append(out[0, qr, h]); ref["out"].append(r["out"])
+        got["lse"].append(lse[0, h, qr]); ref["lse"].append(r["lse"])
+        got["dq"].append(dq[0, qr, h]); ref["dq"].append(r["dq"])
+    kc = np.unique(np.concatenate([[0, S - 1], rng.integers(1, S - 1, 4)]))
+    for h in (0, H - 1):
+        print(f"[case] attention full size: oracle dk/dv of head {h}", flush=True)
+        r = oracle.attention_sampled(*host, 0, h, kcols=kc)
+        got["dk"].append(dk[0, kc, h]); ref["dk"].append(r["dk"])
+        got["dv"].append(dv[0, kc, h]); ref["dv"].append(r["dv"])
+    cat = lambda xs: np.concatenate([np.ravel(x) for x in xs])
+    assert_parity(cat(got["out"]), cat(ref["out"]), "full-size out")
+    assert np.max(np.abs(cat(got["lse"]) - cat(ref["lse"]))) <= 1e-4
+    for n in ("dq", "dk", "dv"):
+        assert_parity(cat(got[n]), cat(ref[n]), f"full-size {n}", tol=GTOL)

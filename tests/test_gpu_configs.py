@@ -175,8 +175,9 @@ def test_wan13b_30_layer_chain_at_full_tokens(dev):
     one backward (dX chained back through the GELU pullback, dA and dB for every linear).
     Every linear is checked on the GPU's own inputs: sampled rows of y and of dx (including the
     last token) against the oracle; dA and dB on sampled columns for all six linears of the first
-    layer (the end of the backward chain); the exact doubling identities y(2x) = 2 y(x) and
-    dx(2dy) = 2 dx(dy), dA(2dy) = 2 dA, dB(2dy) = 2 dB for the first layer's linears."""
+    layer (the end of the backward chain) and of the last layer (its start); the exact doubling
+    identities y(2x) = 2 y(x) and dx(2dy) = 2 dx(dy), dA(2dy) = 2 dA, dB(2dy) = 2 dB for those
+    twelve linears."""
     import time
 
     import torch
@@ -236,7 +237,9 @@ def test_wan13b_30_layer_chain_at_full_tokens(dev):
         assert_parity(bf16_f32(outs[i][rt]), yo, f"cfg4 {name} y (sampled rows)")
         dxo = oracle.lora_backward(dyr, xr, q, s, Ah, Bh, c, want=("dx",))["dx"]
         assert_parity(bf16_f32(dxs[i][rt]), dxo, f"cfg4 {name} dx (sampled rows)")
-        if i < len(shapes):  # the first layer: dA, dB over all tokens, and the doubling identities
+        if i < len(shapes) or i >= len(params) - len(shapes):
+            # the first layer (end of the backward chain) and the last (its start): dA, dB over
+            # all tokens on sampled columns, and the doubling identities
             kc = rng.choice(K, 24, replace=False)
             nc = rng.choice(N, 24, replace=False)
             go = oracle.lora_backward(bf16_bits(dys[i]), bf16_bits(inputs[i]), q, s, Ah, Bh, c,

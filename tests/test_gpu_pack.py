@@ -144,3 +144,45 @@ def test_pack_near_ties_take_exact_division(dev):
     w = np.stack(rows)
     check(dev, w, "f32")
     check(dev, oracle.f32_to_bf16(w), "bf16")
+
+
+def test_pack_one_launch_beyond_2_32_elements(dev):
+    """One pack launch over 860160 rows x 5120 (4.4e9 elements, above 2^32; the 40-layer
+    14B weight set is packed in launches of this order), bf16 ~N(0, 0.02) with 0.1% outliers at
+    +-20 sigma: the first and last 64 rows and 192 random rows bit-exact against the oracle."""
+    import torch
+    from reels_amd import _lib
+    rows, K = 860160, 5120
+    assert rows * K > 2 ** 32
+    print(f"[pack] one launch {rows} x {K} = {rows * K} elements", flush=True)
+    gen = torch.Generator(device=dev).manual_seed(91)
+    w = torch.empty((rows, K), dtype=torch.bfloat16, device=dev)
+    step = 32768
+    for r0 in range(0, rows, step):
+        r1 = min(rows, r0 + step)
+        c = torch.randn((r1 - r0, K), generator=gen, device=dev).mul_(0.02)
+        u = torch.rand((r1 - r0, K), generator=gen, device=dev)
+        c = torch.where(u < 0.001, torch.where(u < 0.0005, -0.4, 0.4), c)
+        w[r0:r1] = c.to(torch.bfloat16)
+        del c, u
+    q = torch.empty((rows, K), dtype=torch.int8, device=dev)
+    s = torch.empty((rows,), dtype=torch.float32, device=dev)
+    st = torch.full((1,), 7, dtype=torch.int32, device=dev)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    rc = _lib.lib().reels_hip_i8_pack(p(w), _lib.BF16, rows, K, K, p(q), p(s), p(st),
+                                      ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
+    _lib.check("reels_hip_i8_pack", rc)
+    torch.cuda.synchronize(dev)
+    assert int(st.item()) == 0
+    rng = np.random.default_rng(92)
+    idx = np.unique(np.concatenate([np.arange(64), np.arange(rows - 64, rows),
+                                    rng.integers(0, rows, 192)]))
+    ix = torch.as_tensor(idx, device=dev)
+    wb = w[ix].view(torch.int16).cpu().numpy().view(np.uint16)
+    qg, sg = q[ix].cpu().numpy(), s[ix].cpu().numpy()
+    del w, q, s
+    torch.cuda.empty_cache()
+    qo, so, sto = oracle.pack(wb, "bf16")
+    assert sto == 0
+    assert np.array_equal(qg, qo), f"codes differ in rows {idx[np.unique(np.argwhere(qg != qo)[:, 0])][:5]}"
+    assert np.array_equal(sg.view(np.uint32), so.view(np.uint32))

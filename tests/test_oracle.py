@@ -269,6 +269,42 @@ def test_backward_matches_finite_differences():
     assert np.array_equal(g2["dB"], g["dB"][:, [4, 2]])
 
 
+def test_bias_gradient_is_the_difference_quotient_of_the_forward():
+    # The forward adds the bias per output channel (lora.jl:64-67 via mixed_add, linear.jl:7-13),
+    # so sum(y .* dy) is affine in the bias: a difference quotient in bias[n] is exact and equals
+    # the oracle's bias gradient. A gradient summed over the wrong axis (over n instead of m) or
+    # with the LoRA scale applied would fail it.
+    M, K, N, r, c = 7, 8, 5, 3, 1.5
+    x = oracle.normal_bf16(41, (M, K), 1.0)
+    w = oracle.normal_bf16(42, (N, K), 0.1)
+    q, s, _ = oracle.pack(w)
+    A = oracle.normal_bf16(43, (K, r), 0.3)
+    B = oracle.normal_bf16(44, (r, N), 0.3)
+    dy = oracle.normal_bf16(45, (M, N), 1.0)
+    bias = oracle.normal_bf16(46, (N,), 0.5)
+    d = oracle.bf16_to_f32(dy).astype(np.float64)
+
+    def loss(b):
+        y, _ = oracle.lora_forward(x, q, s, A, B, c, b)
+        return float(np.sum(y * d))
+
+    base = loss(bias)
+    g = oracle.bias_gradient(dy)
+    assert g.shape == (N,)
+    for n in range(N):
+        b2 = bias.copy()
+        old = float(oracle.bf16_to_f32(bias[n:n + 1])[0])
+        b2[n] = bf([old + 0.5])[0]
+        step = float(oracle.bf16_to_f32(b2[n:n + 1])[0]) - old
+        assert np.isclose((loss(b2) - base) / step, g[n], rtol=1e-9, atol=1e-9)
+    # column selection, and the binary16 / float32 decodes of the same values
+    assert np.array_equal(oracle.bias_gradient(dy, cols=[4, 0]), g[[4, 0]])
+    vals = oracle.bf16_to_f32(dy)
+    assert np.array_equal(oracle.bias_gradient(vals, elt="f32"), g)
+    assert np.array_equal(oracle.bias_gradient(oracle.f32_to_f16(vals), elt="f16"),
+                          oracle.f16_to_f32(oracle.f32_to_f16(vals)).astype(np.float64).sum(0))
+
+
 def test_backward_brute_force_integers():
     x, q, s, A, B, _ = _small_int_case(seed=3)
     dy = np.random.default_rng(4).integers(-3, 4, size=(x.shape[0], q.shape[0])).astype(F32)
@@ -683,3 +719,26 @@ def test_cpu_path_attention_matches_the_f64_oracle():
     assert np.abs(lse.numpy() - lo[0, 0]).max() <= 1e-5
     for got, ref in zip((dq, dk, dv), go):
         assert np.abs(got.numpy() - ref[0, :, 0]).max() <= 1e-4 * np.abs(ref).max()
+
+
+def test_attention_sampled_equals_the_full_oracle():
+    # the blockwise f64 restatement used at full size agrees with the loop oracle on every query
+    # and key it is asked for, in several blocks (block smaller than Sq), bf16 and f32 inputs
+    rng = np.random.default_rng(77)
+    B, Sq, Sk, H, D = 2, 70, 53, 3, 16
+    f = lambda *sh: rng.standard_normal(sh).astype(F32)
+    q, k, v, dy = (oracle.f32_to_bf16(a) for a in (f(B, Sq, H, D), f(B, Sk, H, D),
+                                                   f(B, Sk, H, D), f(B, Sq, H, D)))
+    out, lse = oracle.attention_forward(q, k, v)
+    dq, dk, dv = oracle.attention_backward(q, k, v, dy)
+    qr, kc = [0, 17, 69], [0, 30, 52]
+    for (b, h) in [(0, 0), (1, 2)]:
+        r = oracle.attention_sampled(q, k, v, dy, b, h, qr, kc, block=16)
+        np.testing.assert_allclose(r["out"], out[b, qr, h], rtol=1e-10, atol=1e-12)
+        np.testing.assert_allclose(r["lse"], lse[b, h, qr], rtol=1e-12, atol=1e-12)
+        np.testing.assert_allclose(r["dq"], dq[b, qr, h], rtol=1e-9, atol=1e-12)
+        np.testing.assert_allclose(r["dk"], dk[b, kc, h], rtol=1e-9, atol=1e-12)
+        np.testing.assert_allclose(r["dv"], dv[b, kc, h], rtol=1e-9, atol=1e-12)
+    qf, kf, vf, dyf = (oracle.bf16_to_f32(a) for a in (q, k, v, dy))
+    r = oracle.attention_sampled(qf, kf, vf, dyf, 1, 1, [5], [7], elt="f32")
+    np.testing.assert_allclose(r["dv"], dv[1, [7], 1], rtol=1e-9, atol=1e-12)
