@@ -46,6 +46,7 @@ extern "C" {
 /* workspace selectors for reels_hip_i8lora_workspace_bytes */
 #define REELS_HIP_WS_FWD 0
 #define REELS_HIP_WS_BWD 1
+#define REELS_HIP_WS_FWD_NOALLOC 2 /* the scratch reels_hip_i8lora_fwd_noalloc needs */
 
 /* ABI version of the loaded library; compare with REELS_HIP_ABI_VERSION. No reference
  * counterpart (the reference has no native library for this path). */
@@ -84,7 +85,9 @@ int reels_hip_i8_dequant(const int8_t* q, const float* scales, int64_t N, int64_
                          int dtype, int transpose, void* out, void* stream);
 
 /* Bytes of device workspace needed by reels_hip_i8lora_fwd (which = REELS_HIP_WS_FWD) or
- * reels_hip_i8lora_bwd (REELS_HIP_WS_BWD) for these sizes. Always a multiple of 256. */
+ * reels_hip_i8lora_bwd (REELS_HIP_WS_BWD) for these sizes, or of the library's scratch that
+ * reels_hip_i8lora_fwd_noalloc would use (REELS_HIP_WS_FWD_NOALLOC). Always a multiple of 256;
+ * 0 for negative sizes or another selector. */
 size_t reels_hip_i8lora_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t r, int which);
 
 /*
@@ -112,8 +115,13 @@ int reels_hip_i8lora_fwd(const void* x, const int8_t* q, const float* scales, co
 /*
  * The same with binary16 x, A, B, bias, y and h_save: the reference's own int8 compute
  * precision (Float16, quantization.jl:61-62 and lora.jl:56-95 with T = Float16). Every bf16
- * rounding above becomes an f16 rounding (nearest even), and the dequantized weight is
- * W = f16(q * f16(s)) as _dequantize_for_compute computes it. Same workspace size.
+ * rounding above becomes an f16 rounding (nearest even). The weight is the one the bf16 entry
+ * point's shape rules pick, in binary16: where that entry point multiplies a dequantized copy
+ * (K and N multiples of 64, many tokens), W = f16(q * f16(s)) as _dequantize_for_compute
+ * computes it; where it multiplies the int8 codes (the few-token path, the split-reduction
+ * forward over a few hundred tokens, K or N not a multiple of 64), s[n] is applied to the f32
+ * sum of x * q, so y can differ from the f16(q * f16(s)) product in the last f16 bit. The
+ * backward (reels_hip_i8lora_bwd_f16) always multiplies f16(q * f16(s)). Same workspace size.
  */
 int reels_hip_i8lora_fwd_f16(const void* x, const int8_t* q, const float* scales, const void* A,
                              const void* B, const void* bias, int64_t M, int64_t K, int64_t N,
@@ -125,10 +133,11 @@ int reels_hip_i8lora_fwd_f16(const void* x, const int8_t* q, const float* scales
  * or allocating library call), for callers that cannot allocate - code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc. No counterpart in the reference (its
  * forward allocates per call). Same arguments, results and errors as reels_hip_i8lora_fwd except:
- *   - the scratch (the h panel and transposed adapter operands) is a 32 MiB device array inside
- *     the library, one per GPU, held until the process ends; sizes that need more return
- *     REELS_HIP_EINVAL before any work (M * round_up(r, 16) * 2 + r * K * 2 + N * round_up(r,
- *     16) * 2 bytes, rounded up to 256 each, must fit);
+ *   - the scratch (the h panel, transposed adapter operands, the few-token kernel's split
+ *     partials and counters, the rank projection's split partials) is a 32 MiB device array
+ *     inside the library, one per GPU, held until the process ends; sizes for which
+ *     reels_hip_i8lora_workspace_bytes(M, K, N, r, REELS_HIP_WS_FWD_NOALLOC) exceeds 32 MiB
+ *     return REELS_HIP_EINVAL before any work;
  *   - it always multiplies the int8 codes (s applied to the f32 sum), never a dequantized bf16
  *     copy, so its y can differ from reels_hip_i8lora_fwd's in the last bf16 bit where that entry
  *     point takes the dequantized-weight path (K and N multiples of 64);

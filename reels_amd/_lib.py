@@ -15,7 +15,7 @@ DEFAULT_LIB = os.path.join(HERE, "lib", "libreels_hip.so")
 
 ABI_VERSION = 1
 F32, BF16, F16 = 0, 1, 2
-WS_FWD, WS_BWD = 0, 1
+WS_FWD, WS_BWD, WS_FWD_NOALLOC = 0, 1, 2
 
 # every symbol include/reels_hip.h declares
 EXPORTS = (

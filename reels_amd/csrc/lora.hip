@@ -866,6 +866,14 @@ static int rowproj_splits(int64_t M, int64_t Kd, int rp) {
 }
 
 
+// The plan of reels_hip_i8lora_fwd_noalloc: never the dequantized-weight copy (its N*K*2 bytes
+// are what would not fit a modest scratch) and no split-reduction partials
+static void noalloc_plan(Plan& p) {
+  p.deq = false;
+  p.i8f = false;
+  p.ksf = p.ksb = 1;
+}
+
 static Plan make_plan(int64_t M, int64_t K, int64_t N, int64_t r, bool ptrs_aligned) {
   Plan p;
   // K, N < 2^22 keeps the projection and gradient kernels' buffer descriptors (64 rows, or a
@@ -1190,9 +1198,15 @@ using namespace reels;
 extern "C" size_t reels_hip_i8lora_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t r,
                                                    int which) {
   if (M < 0 || K < 0 || N < 0 || r < 0) return 0;
+  if (which != REELS_HIP_WS_FWD && which != REELS_HIP_WS_BWD && which != REELS_HIP_WS_FWD_NOALLOC)
+    return 0;
   // sized for the fast layout when the shape allows it (pointer alignment cannot be known here;
   // the fast layout is never smaller than the generic one)
   Plan p = make_plan(M, K, N, r, true);
+  if (which == REELS_HIP_WS_FWD_NOALLOC) {
+    noalloc_plan(p);
+    which = REELS_HIP_WS_FWD;
+  }
   return ws_layout(M, K, N, r, which, p).total;
 }
 
@@ -1250,7 +1264,7 @@ static int i8lora_fwd_impl(int elt, const char* fn, const void* x, const int8_t*
   const bool al = all_aligned({x, q, scales, A, B, y, h_save}) &&
                   (bias == nullptr || (reinterpret_cast<uintptr_t>(bias) & 7u) == 0);
   Plan p = make_plan(M, K, N, r, al);
-  if (noalloc) { p.deq = false; p.i8f = false; p.ksf = p.ksb = 1; }
+  if (noalloc) noalloc_plan(p);
   WsLayout w = ws_layout(M, K, N, r, REELS_HIP_WS_FWD, p);
   if (noalloc) {
     if (w.total > kScratchBytes)

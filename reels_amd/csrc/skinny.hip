@@ -20,9 +20,10 @@
 // up long before an output tile looks; the wait is bounded all the same, and an output tile that
 // gives up computes l for its tokens itself with the adapter blocks' code and order (same bits),
 // so the result never depends on how the grid is scheduled.
-// The counters and the flag live in a per-stream slot of static device memory and are put back to
-// zero by the launch that used them, so launches need no clearing pass. Deterministic: fixed wave
-// order, fixed split order; the atomics only count.
+// The counters and the flag live in the call's own workspace, after the partials and l, and a
+// one-block kernel clears them just before the launch: nothing is shared between calls, so calls
+// on any streams, and HIP graphs that capture them, may run at the same time. Deterministic:
+// fixed wave order, fixed split order; the atomics only count.
 //
 // FWD: out[m][n] = rnd(s[n] sum_k x[m][k] q[n][k] + c sum_j h[m][j] B[j][n] + bias[n]),
 //      h = rnd(x A): the int8 path's formula (the scale on the f32 sum).
@@ -35,7 +36,6 @@
 
 #include <cstdlib>
 #include <mutex>
-#include <unordered_map>
 
 namespace reels {
 
@@ -47,20 +47,18 @@ constexpr int MAXT = 5;      // token tiles of 16 per block (80 tokens)
 constexpr int MAXS = 8;      // reduction splits
 constexpr int STAGE = 4096;  // per-wave LDS staging (DX weight tile, FWD adapter chunk: 4 KiB each)
 constexpr int NWV = 8;       // waves per block (two per SIMD)
-constexpr int kSlots = 64;   // counter slots per device: one per stream, the last one shared
 constexpr int kMaxTiles = 4096;
 constexpr uint32_t kSpinLimit = 1u << 12;  // wait rounds of s_sleep 8 (about 1 ms) before computing l
 }  // namespace sk
 
-// one launch's counters (zero between launches)
-struct SkSlot {
+// one launch's counters, zero when it starts: this header, then one word per tile (the blocks of
+// the tile that have stored their partial)
+struct SkCounters {
   uint32_t hdone;    // adapter tiles finished
-  uint32_t hready;   // 1: l complete (set by the last adapter tile, cleared by the last tile)
-  uint32_t fin;      // tiles finished (launches with adapter and output tiles)
-  uint32_t pad[29];  // the tile counters start on their own 128-byte line
-  uint32_t tile[sk::kMaxTiles];  // blocks of the tile that have stored their partial
+  uint32_t hready;   // 1: l complete (set by the last adapter tile)
+  uint32_t pad[30];  // the tile counters start on their own 128-byte line
 };
-static __device__ __align__(256) SkSlot sk_slots[sk::kSlots];
+constexpr int kSkCounterHeaderWords = (int)(sizeof(SkCounters) / 4);
 
 struct SkArgs {
   const uint16_t* act;  // [M][Kred] 16-bit: x (FWD) or dy (DX)
@@ -74,7 +72,8 @@ struct SkArgs {
   const uint16_t* bias;
   uint16_t* out;        // [M][Ncols]
   uint16_t* lsave;      // [M][ld_lsave], lsave_cols columns (or NULL)
-  SkSlot* slot;
+  SkCounters* ctr;
+  uint32_t* tiles;      // [nblk * tb + lblk * tb], right after *ctr
   int64_t M, Kred, Ncols, ldq, ldr, ld_lsave;
   float c;
   int r, rp, S, nblk, lblk, tb, lsave_cols;
@@ -115,16 +114,6 @@ __device__ __forceinline__ void sk_store(uint32_t* p, uint32_t v) {
 __device__ __forceinline__ void sk_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t sk_rsrc(const void* p, int64_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
-}
-
-// A tile of a launch with both adapter and output tiles is finished: the last of them lowers the
-// ready flag for the next launch (thread 0, after the tile no longer reads the flag)
-__device__ __forceinline__ void skinny_finish(const SkArgs& a) {
-  const uint32_t old = sk_add(&a.slot->fin, 1u);
-  if (old == (uint32_t)(a.nta + a.ntm) - 1) {
-    sk_store(&a.slot->hready, 0u);
-    sk_store(&a.slot->fin, 0u);
-  }
 }
 
 // One wave's share of a (row block, split, token block): acc[i][tt] = rows 16 i + (0..15) x
@@ -480,7 +469,7 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
     skinny_sum<T, NI>(acc, smem, sum);
   }
   uint32_t* words = reinterpret_cast<uint32_t*>(smem + skinny_lds(T) - 16);  // [1] arrivals, [2] l ready
-  SkSlot* slot = a.slot;
+  SkCounters* ctr = a.ctr;
   // An output tile's epilogue operands: the column scales and bias of this thread's rows and
   // (forward) the first 32 rank rows of R for the tile's 64 columns, which threads 0-255 stage in
   // LDS. With split partials they are loaded before the hand-over, whose round trips cover their
@@ -510,7 +499,7 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
   // rank columns while the partial is handed over.
   const bool wants_l = !lora && a.nad > 0;
   uint32_t up = 0;
-  if (wants_l) up = sk_load(&slot->hready);
+  if (wants_l) up = sk_load(&ctr->hready);
   u32x4 hv[FPW];  // B operand of the l R product: l[tok][j .. j + 7], j = 8 g (first rank chunk)
   auto load_l = [&](int j0, u32x4 (&dst)[FPW]) {
 #pragma unroll
@@ -540,9 +529,7 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
     if (wants_l && up) load_l(0, hv);
     __syncthreads();
     if (t == 0) {
-      const uint32_t old = sk_add(&slot->tile[d.tile], 1u);
-      if (old == (uint32_t)a.S - 1) sk_store(&slot->tile[d.tile], 0u);
-      words[1] = old;
+      words[1] = sk_add(&a.tiles[d.tile], 1u);
     }
     __syncthreads();
     if (words[1] != (uint32_t)a.S - 1) return;
@@ -584,12 +571,8 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
     sk_drain();
     __syncthreads();
     if (t == 0) {
-      const uint32_t old = sk_add(&slot->hdone, 1u);
-      if (old == (uint32_t)a.nta - 1) {
-        sk_store(&slot->hdone, 0u);
-        if (a.ntm > 0) sk_store(&slot->hready, 1u);
-      }
-      if (a.ntm > 0) skinny_finish(a);
+      const uint32_t old = sk_add(&ctr->hdone, 1u);
+      if (old == (uint32_t)a.nta - 1 && a.ntm > 0) sk_store(&ctr->hready, 1u);
     }
     return;
   } else {
@@ -603,7 +586,7 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
         uint32_t n = 0, v = up;
         while (v == 0u && ++n <= a.spin) {
           __builtin_amdgcn_s_sleep(8);
-          v = sk_load(&slot->hready);
+          v = sk_load(&ctr->hready);
         }
         words[2] = v;
       }
@@ -694,8 +677,12 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
       }
       *reinterpret_cast<uint2*>(a.out + tok * a.Ncols + o) = uint2{b[0] | (b[1] << 16), b[2] | (b[3] << 16)};
     }
-    if (wants_l && t == 0) skinny_finish(a);
   }
+}
+
+// clears one launch's counters (n words)
+__global__ __launch_bounds__(256) void skinny_clear_kernel(uint32_t* p, int n) {
+  for (int i = (int)threadIdx.x; i < n; i += 256) p[i] = 0u;
 }
 
 template <int T, int MODE, int ELT>
@@ -750,23 +737,26 @@ SkinnyPlan skinny_plan(int64_t M, int64_t Kred, int64_t Ncols, int rp) {
   return p;
 }
 
-size_t skinny_ws_bytes(const SkinnyPlan& p, int64_t M, int64_t Ncols, int rp) {
-  const size_t tiles = (size_t)(Ncols / sk::NB) * p.tb * (4 * p.T) + (size_t)ceil_div(rp, sk::NBL) * p.tb * (2 * p.T);
-  const size_t part = p.S > 1 ? tiles * p.S * 64 * 16 : 0;
-  return align_up(part, 256) + (size_t)M * rp * 2;
+// workspace of one launch: split partials, l [M][rp], then the counters (header + one word per
+// tile); the offsets are the same in sizing and use
+struct SkWs {
+  size_t part, hl, ctr, total;
+  int ntiles;
+};
+static SkWs skinny_ws(const SkinnyPlan& p, int64_t M, int64_t Ncols, int rp) {
+  SkWs w;
+  const size_t frags = (size_t)(Ncols / sk::NB) * p.tb * (4 * p.T) + (size_t)ceil_div(rp, sk::NBL) * p.tb * (2 * p.T);
+  w.ntiles = (int)((Ncols / sk::NB + ceil_div(rp, sk::NBL)) * p.tb);
+  w.part = 0;
+  w.hl = align_up(p.S > 1 ? frags * p.S * 64 * 16 : 0, 256);
+  w.ctr = align_up(w.hl + (size_t)M * rp * 2, 256);
+  w.total = align_up(w.ctr + (size_t)(kSkCounterHeaderWords + w.ntiles) * 4, 256);
+  return w;
 }
 
-// the calling stream's counter slot on the current device; the last slot is shared by streams
-// beyond the first kSlots - 1, whose launches are then ordered through an event
-struct SkSlots {
-  std::mutex mu;
-  SkSlot* base = nullptr;
-  std::unordered_map<hipStream_t, int> map;
-  hipEvent_t shared_ev = nullptr;
-  bool shared_used = false;
-};
-constexpr int kSkMaxDevices = 64;
-static SkSlots g_sk[kSkMaxDevices];
+size_t skinny_ws_bytes(const SkinnyPlan& p, int64_t M, int64_t Ncols, int rp) {
+  return skinny_ws(p, M, Ncols, rp).total;
+}
 
 template <int MODE, int ELT, int T>
 static hipError_t launch_skinny_t(const SkArgs& a, hipStream_t st) {
@@ -805,43 +795,19 @@ int launch_skinny(int mode, int elt, const SkinnyPlan& p, const uint16_t* act, c
   a.nad = a.nta * p.S;
   a.blocks = a.nad + a.ntm * p.S;
   if (a.blocks <= 0) return REELS_HIP_OK;
-  const size_t tiles = (size_t)a.nblk * p.tb * (4 * p.T) + (size_t)a.lblk * p.tb * (2 * p.T);
-  a.part = static_cast<float*>(ws);
-  uint16_t* hl = reinterpret_cast<uint16_t*>(static_cast<uint8_t*>(ws) + align_up(p.S > 1 ? tiles * p.S * 64 * 16 : 0, 256));
+  const SkWs w = skinny_ws(p, M, Ncols, a.rp);
+  uint8_t* wb = static_cast<uint8_t*>(ws);
+  a.part = reinterpret_cast<float*>(wb + w.part);
+  uint16_t* hl = reinterpret_cast<uint16_t*>(wb + w.hl);
   // l straight into lsave when the layouts agree
   a.hl = (lsave != nullptr && ld_lsave == a.rp && lsave_cols >= a.rp) ? lsave : hl;
-
-  int dev = -1;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return fail(REELS_HIP_EHIP, std::string("skinny_kernel: hipGetDevice: ") + hipGetErrorString(e));
-  if (dev < 0 || dev >= kSkMaxDevices) return fail(REELS_HIP_EHIP, "skinny_kernel: device index out of range");
-  SkSlots& tab = g_sk[dev];
-  std::lock_guard<std::mutex> lock(tab.mu);
-  if (tab.base == nullptr) {
-    void* ptr = nullptr;
-    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(sk_slots));
-    if (e != hipSuccess || ptr == nullptr)
-      return fail(REELS_HIP_EHIP, std::string("skinny_kernel: hipGetSymbolAddress(sk_slots): ") + hipGetErrorString(e));
-    tab.base = static_cast<SkSlot*>(ptr);
+  a.ctr = reinterpret_cast<SkCounters*>(wb + w.ctr);
+  a.tiles = reinterpret_cast<uint32_t*>(wb + w.ctr) + kSkCounterHeaderWords;
+  {
+    TraceScope _ts(st, "skinny_clear_kernel");
+    skinny_clear_kernel<<<1, 256, 0, st>>>(reinterpret_cast<uint32_t*>(a.ctr), kSkCounterHeaderWords + w.ntiles);
   }
-  int idx;
-  auto it = tab.map.find(st);
-  if (it != tab.map.end()) {
-    idx = it->second;
-  } else if ((int)tab.map.size() < sk::kSlots - 1) {
-    idx = (int)tab.map.size();
-    tab.map.emplace(st, idx);
-  } else {
-    idx = sk::kSlots - 1;
-  }
-  const bool shared = idx == sk::kSlots - 1;
-  if (shared) {
-    if (tab.shared_ev == nullptr && (e = hipEventCreateWithFlags(&tab.shared_ev, hipEventDisableTiming)) != hipSuccess)
-      return fail(REELS_HIP_EHIP, std::string("skinny_kernel: hipEventCreateWithFlags: ") + hipGetErrorString(e));
-    if (tab.shared_used && (e = hipStreamWaitEvent(st, tab.shared_ev, 0)) != hipSuccess)
-      return fail(REELS_HIP_EHIP, std::string("skinny_kernel: hipStreamWaitEvent: ") + hipGetErrorString(e));
-  }
-  a.slot = tab.base + idx;
+  if (int rc = check_launch("skinny_clear_kernel")) return rc;
 
   hipError_t attr = hipSuccess;
   {
@@ -864,13 +830,7 @@ int launch_skinny(int mode, int elt, const SkinnyPlan& p, const uint16_t* act, c
   }
   if (attr != hipSuccess)
     return fail(REELS_HIP_EHIP, std::string("skinny_kernel: hipFuncSetAttribute: ") + hipGetErrorString(attr));
-  if (int rc = check_launch("skinny_kernel")) return rc;
-  if (shared) {
-    if ((e = hipEventRecord(tab.shared_ev, st)) != hipSuccess)
-      return fail(REELS_HIP_EHIP, std::string("skinny_kernel: hipEventRecord: ") + hipGetErrorString(e));
-    tab.shared_used = true;
-  }
-  return REELS_HIP_OK;
+  return check_launch("skinny_kernel");
 }
 
 }  // namespace reels

@@ -34,8 +34,9 @@ def test_header_constants_match_binding():
     assert int(consts["REELS_HIP_ABI_VERSION"]) == _lib.ABI_VERSION
     assert (int(consts["REELS_HIP_F32"]), int(consts["REELS_HIP_BF16"]),
             int(consts["REELS_HIP_F16"])) == (_lib.F32, _lib.BF16, _lib.F16)
-    assert (int(consts["REELS_HIP_WS_FWD"]), int(consts["REELS_HIP_WS_BWD"])) == (_lib.WS_FWD,
-                                                                               _lib.WS_BWD)
+    assert (int(consts["REELS_HIP_WS_FWD"]), int(consts["REELS_HIP_WS_BWD"]),
+            int(consts["REELS_HIP_WS_FWD_NOALLOC"])) == (_lib.WS_FWD, _lib.WS_BWD,
+                                                         _lib.WS_FWD_NOALLOC)
 
 
 def test_workspace_sizes():
@@ -53,6 +54,14 @@ def test_workspace_sizes():
     # K a multiple of 16 but not of 64: the int8 GEMM path, whose backward holds dy*s [M][N] bf16
     assert L.reels_hip_i8lora_workspace_bytes(4096, 5136, 5120, 32, 1) >= 4096 * 5120 * 2
     assert L.reels_hip_i8lora_workspace_bytes(-1, 5, 5, 1, 0) == 0
+    assert L.reels_hip_i8lora_workspace_bytes(4, 5, 5, 1, 7) == 0
+    # the no-allocation forward's scratch: no dequantized weight copy, so far below the
+    # workspace forward's on a Wan shape; the few-token kernel's partials, l and counters fit
+    nw = L.reels_hip_i8lora_workspace_bytes(32760, 5120, 5120, 32, _lib.WS_FWD_NOALLOC)
+    assert 0 < nw < L.reels_hip_i8lora_workspace_bytes(32760, 5120, 5120, 32, _lib.WS_FWD)
+    assert nw >= 32760 * 32 * 2 and nw % 256 == 0
+    few = L.reels_hip_i8lora_workspace_bytes(77, 5120, 5120, 32, _lib.WS_FWD_NOALLOC)
+    assert 0 < few <= 32 << 20 and few >= 77 * 32 * 2 + 128
     # f32: the dequantized weight is N x K f32, h / u panels [M][r] f32, dA / dB partials
     for which in (0, 1):
         b = L.reels_hip_i8lora_workspace_bytes_f32(32760, 5120, 13824, 32, which)

@@ -1,12 +1,12 @@
 """The few-token path's single launch (reels_amd/csrc/skinny.hip): output tiles wait for the
 adapter's rank projection l, published by the adapter blocks of the same launch, and a tile that
 stops waiting computes l itself with the adapter blocks' code and order. Its counters live in
-per-stream slots that every launch leaves at zero.
+the call's own workspace, cleared by a one-block kernel just before the launch.
 
 These tests force the fallback from the host (REELS_HIP_SKINNY_SPIN=0: no wait at all) and
-require the same bits as the normal run; run calls concurrently on several streams, more streams
-than there are slots (the shared slot orders its launches with an event), and repeat calls to show
-the counters return to zero. The parity of the values themselves against the oracle is in
+require the same bits as the normal run; run calls concurrently on many streams, and HIP graphs
+of few-token calls captured on one stream and replayed at the same time on two streams, and
+repeat calls. The parity of the values themselves against the oracle is in
 tests/test_gpu_configs.py (cross-attention shapes) and tests/test_gpu_lora.py."""
 import numpy as np
 import pytest
@@ -68,9 +68,9 @@ def test_output_tiles_computing_l_themselves_give_the_same_bits(dev, monkeypatch
     assert_parity(bf16_f32(got[0])[rows], yo, f"fallback M={M} y")
 
 
-def test_concurrent_streams_and_the_shared_slot(dev):
-    """Calls on 70 streams at once (more than the 63 per-stream slots of a device): every result
-    equals the same call made alone on the default stream."""
+def test_concurrent_streams(dev):
+    """Calls on 70 streams at once: every result equals the same call made alone on the default
+    stream."""
     import torch
     from reels_amd import i8lora_forward
     M, K, N, r, c = 77, 1536, 1536, 16, 1.0
@@ -93,6 +93,48 @@ def test_concurrent_streams_and_the_shared_slot(dev):
     torch.cuda.synchronize(dev)
     for k, y, h in outs:
         assert torch.equal(y, ref[k][0]) and torch.equal(h, ref[k][1])
+
+
+def test_graphs_captured_on_one_stream_replayed_concurrently(dev):
+    """Few-token forwards and backwards captured into two HIP graphs on the same capture stream
+    (torch.cuda.graph uses one side stream for every capture), then replayed at the same time on
+    two streams, several rounds with eager work and synchronisations between them: each replay
+    equals the eager call bit for bit. Counters kept per caller stream would be shared by the two
+    graphs here."""
+    import torch
+    M, K, N, r, c = 77, 5120, 5120, 32, 1.0
+    cases = [_case(dev, M, K, N, r, 4700 + 10 * i)[1] for i in range(2)]
+    print("[skinny] two graphs replayed concurrently", flush=True)
+    eager = [_run(d, c) for d in cases]
+    torch.cuda.synchronize(dev)
+    for d in cases:  # warm-up on a side stream (first-call set-up stays out of the captures)
+        s = torch.cuda.Stream(device=dev)
+        s.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(s):
+            _run(d, c)
+        torch.cuda.current_stream(dev).wait_stream(s)
+    torch.cuda.synchronize(dev)
+    graphs, outs = [], []
+    for d in cases:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            outs.append(_run(d, c))
+        graphs.append(g)
+    torch.cuda.synchronize(dev)
+    streams = [torch.cuda.Stream(device=dev) for _ in graphs]
+    for rnd in range(4):
+        for g, st in zip(graphs, streams):
+            st.wait_stream(torch.cuda.current_stream(dev))
+            with torch.cuda.stream(st):
+                g.replay()
+        for st in streams:
+            torch.cuda.current_stream(dev).wait_stream(st)
+        torch.cuda.synchronize(dev)
+        for i, (got, ref) in enumerate(zip(outs, eager)):
+            for name, a, b in zip(("y", "h", "dx", "dA", "dB"), got, ref):
+                assert torch.equal(a, b), f"round {rnd}: graph {i} {name} differs from eager"
+        _run(cases[rnd % 2], c)  # eager work between the rounds
+        torch.cuda.synchronize(dev)
 
 
 def test_f16_fallback_and_repeat(dev, monkeypatch):

@@ -84,6 +84,7 @@ def test_noalloc_rejects_sizes_beyond_its_scratch(dev):
     M, K, N, r = 300000, 64, 64, 64
     buf = torch.zeros((1024,), dtype=torch.uint8, device=dev)
     p = ctypes.c_void_p(buf.data_ptr())
+    assert L.reels_hip_i8lora_workspace_bytes(M, K, N, r, _lib.WS_FWD_NOALLOC) > 32 << 20
     rc = L.reels_hip_i8lora_fwd_noalloc(p, p, p, p, p, None, M, K, N, r, 1.0, p, p, None)
     assert rc == -1
     assert b"scratch" in L.reels_hip_last_error()
@@ -93,3 +94,51 @@ def test_noalloc_rejects_sizes_beyond_its_scratch(dev):
     y1, _ = _run(dev, L, "workspace", x, q, s, A, B, bias, 64, 64, 64, 16, 1.0)
     assert_parity(oracle.bf16_to_f32(y0), oracle.bf16_to_f32(y1).astype(np.float64),
                   "noalloc y after a rejected call")
+
+
+@pytest.mark.parametrize("M,K,N,r", [(77, 5120, 5120, 32), (2048, 1536, 1536, 32)])
+def test_noalloc_forward_under_graph_capture(dev, M, K, N, r):
+    """The caller this entry point is for: warmed up once, then captured with torch.cuda.graph
+    (global capture mode, under which an allocation on the capturing thread fails the capture)
+    and replayed several times with eager work and synchronisations between the replays; every
+    replay equals the eager call bit for bit. 77 tokens take the few-token kernel, 2048 the
+    int8 GEMM."""
+    import torch
+    from reels_amd import _lib
+    L = _lib.lib()
+    x, q, s, A, B, bias = _case(M, K, N, r, 40 + M)
+    c = 1.0
+    t = {k: to_dev(v, dev) for k, v in dict(x=x, A=A, B=B, bias=bias).items()}
+    qd, sd = to_dev(q, dev, "raw"), to_dev(s, dev, "raw")
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    h = torch.empty((M, r), dtype=torch.bfloat16, device=dev)
+    p = lambda a: ctypes.c_void_p(a.data_ptr())
+
+    def call():
+        st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        rc = L.reels_hip_i8lora_fwd_noalloc(p(t["x"]), p(qd), p(sd), p(t["A"]), p(t["B"]),
+                                            p(t["bias"]), M, K, N, r, c, p(y), p(h), st)
+        _lib.check("reels_hip_i8lora_fwd_noalloc", rc)
+
+    print(f"[noalloc] graph capture M={M} K={K} N={N} r={r}", flush=True)
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        call()
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize(dev)
+    y_ref, h_ref = y.clone(), h.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call()
+    for i in range(3):
+        y.zero_()
+        h.zero_()
+        torch.cuda.synchronize(dev)
+        g.replay()
+        torch.cuda.synchronize(dev)
+        assert torch.equal(y, y_ref), f"replay {i}: y differs from the eager call"
+        assert torch.equal(h, h_ref), f"replay {i}: h differs from the eager call"
+        call()  # eager work between the replays
+        torch.cuda.synchronize(dev)
+        assert torch.equal(y, y_ref)
