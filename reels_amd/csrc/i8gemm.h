@@ -53,27 +53,31 @@ int launch_dequant_transpose(int elt, const int8_t* q, int64_t ldq, const float*
 // of each tile (split order). mode 0 = FWD (act = x, rows of q are outputs, lw = A [Kred][rp]
 // zero-padded), 1 = DX (act = dy, rows of q are the reduction, lw = B [r][Kred], s = the
 // reduction's scale).
-// up to 240 tokens (three 80-token blocks), or 1024 on weights of at most 4M elements; above,
-// the GEMMs with split reductions are faster (5120 x 5120 forward: 256 tokens 78 us few-token,
-// 333 tokens 65 us split; 512 tokens 70 us split against 120 us few-token)
+// up to 240 tokens (three 80-token blocks), or 1024 on weights of at most 4M elements; beyond,
+// and wherever they fill the GPU, the row-wave output tiles (skinny_rw_kernel) run instead
 constexpr int64_t kSkinnyMaxTokens = 240;
 constexpr int64_t kSkinnySmallWeightTokens = 1024;
 constexpr int64_t kSkinnyTargetBlocks = 256;  // about one block per CU
 struct SkinnyPlan {
-  int T;   // token tiles of 16 per block
-  int tb;  // token blocks
-  int S;   // reduction splits
+  int T;   // token tiles of 16 per block (the adapter blocks; also the output blocks unless rw)
+  int tb;  // token blocks (ditto)
+  int S;   // reduction splits (ditto)
+  // row-wave output tiles: 64 NI rows x 16 To tokens over the whole reduction in one block,
+  // orb x otb of them; the adapter blocks keep T, tb and S
+  bool rw = false;
+  int NI = 0, To = 0, orb = 0, otb = 0;
 };
 bool skinny_supported(int64_t M, int64_t K, int64_t N, int rp);
-SkinnyPlan skinny_plan(int64_t M, int64_t Kred, int64_t Ncols, int rp);
+// mode 0: the forward (Kred = K, Ncols = N); 1: dX (Kred = N, Ncols = K)
+SkinnyPlan skinny_plan(int64_t M, int64_t Kred, int64_t Ncols, int rp, int mode);
 // workspace of one launch: the split partials and l [M][rp]
 size_t skinny_ws_bytes(const SkinnyPlan& p, int64_t M, int64_t Ncols, int rp);
 // out = rnd(colscale * act W + c l R + bias) with l = rnd(act L) (h or u), written to lsave
 // ([M][ld_lsave], lsave_cols columns, zeros past r) when not NULL; R(o, j) = R[j][o] (mode 0,
 // row stride ldr) or R[o][j] (mode 1, rows of ldr >= rp elements, zeros past r). adapter_only: l
 // alone, from the same blocks and split order as a full launch (so a recomputed h equals the
-// forward's bit for bit). Launches on one stream are ordered; launches on different streams use
-// different counter slots.
+// forward's bit for bit). The launch's counters live in ws (cleared by a kernel before it), so
+// launches with their own workspaces may run concurrently.
 int launch_skinny(int mode, int elt, const SkinnyPlan& p, const uint16_t* act, const int8_t* q,
                   int64_t ldq, const float* s, const uint16_t* lw, void* ws, int64_t M,
                   int64_t Kred, int64_t Ncols, int r, int rp, const float* colscale,

@@ -885,8 +885,8 @@ static Plan make_plan(int64_t M, int64_t K, int64_t N, int64_t r, bool ptrs_alig
   p.padded = p.fast && p.rp != r;
   p.skinny = p.fast && skinny_supported(M, K, N, p.rp);
   if (p.skinny) {
-    p.skf = skinny_plan(M, K, N, r > 0 ? p.rp : 0);
-    p.skb = skinny_plan(M, N, K, r > 0 ? p.rp : 0);
+    p.skf = skinny_plan(M, K, N, r > 0 ? p.rp : 0, 0);
+    p.skb = skinny_plan(M, N, K, r > 0 ? p.rp : 0, 1);
   }
   p.sa = split_for(M, K);
   p.sb = split_for(M, N);

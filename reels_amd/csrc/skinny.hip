@@ -82,6 +82,8 @@ struct SkArgs {
   int ntm;     // output tiles (nblk * tb; 0 for an adapter-only launch)
   uint32_t spin;  // wait rounds before an output tile computes l itself
   int nta;     // adapter tiles (lblk * tb)
+  int64_t lpart0;  // first partial fragment of the adapter tiles (after the output tiles')
+  int otb;     // row-wave output tiles: token tiles (the output tile is ti / otb, ti % otb)
 };
 
 struct SkBlock {
@@ -515,7 +517,7 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
   };
   if (a.S > 1) {
     // partial [tile][split][fragment][lane] (16 bytes); output tiles first, then adapter tiles
-    const int64_t tbase = lora ? (int64_t)a.ntm * a.S * (4 * T * 64) + (int64_t)(d.tile - a.ntm) * a.S * (NF * 64)
+    const int64_t tbase = lora ? a.lpart0 + (int64_t)(d.tile - a.ntm) * a.S * (NF * 64)
                                : (int64_t)d.tile * a.S * (NF * 64);
     const __amdgpu_buffer_rsrc_t rp_ = sk_rsrc(reinterpret_cast<f32x4*>(a.part) + tbase, (int64_t)a.S * NF * 64 * 16);
 #pragma unroll
@@ -685,6 +687,450 @@ __global__ __launch_bounds__(256) void skinny_clear_kernel(uint32_t* p, int n) {
   for (int i = (int)threadIdx.x; i < n; i += 256) p[i] = 0u;
 }
 
+// ---- row-wave output tiles: a few hundred tokens on a large weight ------------------------------
+// With more tokens than one 80-token block the tiles above re-read the activations once per
+// 64-row block and hand split partials between blocks. A row-wave tile instead covers 64 NI
+// output rows x 16 To tokens and the whole reduction in one block, so no partial leaves it: wave
+// w takes rows 16 NI (w & 3) .. + 16 NI of the tile and, in step s, the 64-wide reduction chunk
+// 2 s + (w >> 2); waves w and w + 4 meet once at the end. The step's activations (two chunks of
+// 16 To tokens) are loaded by all 8 waves into registers rw_depth steps ahead and written to an LDS
+// double buffer one step ahead, where every wave of the block reads them; each wave's weight
+// goes straight from memory into its registers, also rw_depth steps ahead.
+//   FWD: the lane holds 16 code bytes of one weight row (k = 16 g .. 16 g + 15 of the chunk) and
+//        feeds MFMA step e with k = 16 g + 8 e + (0..7); the activations use the same k.
+//   DX:  the wave's [64 n][16 NI k] code tile goes through a per-wave LDS tile and
+//        ds_read_b64_tr_b8 (lane: k = 16 i + l16, n = 32 e + 8 g + (0..7)), each code scaled by
+//        s[n] from a table of the block's scales in LDS: bf16(fl32(q s[n])) (f16: f16(q f16(s))),
+//        the dequantized weight of the large-token dX.
+// LDS rows of the activations are 128 bytes (64 bf16), their 16-byte units swizzled per row
+// (rw_swz) so that the fragment reads hit distinct banks.
+// Steps per barrier (G) and steps whose loads are in flight (D, a multiple of G above it): the
+// activations ring in LDS holds 2 G steps, so a group of G steps reads one half while the other
+// half is written for the next group, and the waves meet at one barrier per group.
+// (measured: dX, whose loop is heavier on the VALU, runs best with four steps in flight and a
+// barrier every step or two)
+constexpr int rw_group(int To, int MODE) { return MODE == 1 ? (To <= 2 ? 2 : 1) : (To <= 2 ? 4 : 2); }
+constexpr int rw_depth(int To, int MODE) { return MODE == 1 ? 4 : 2 * rw_group(To, MODE); }
+constexpr int align16(int v) { return (v + 15) & ~15; }
+
+// The 16-byte unit u of activation row r sits at u ^ rw_swz<MODE>(r). A fragment read takes
+// unit 2 g + e (FWD) or 4 e + g (DX) of rows r .. r + 15 in each 16-lane group g, and
+// ds_read_b128 serves two 8-lane groups per pass; with these swizzles any two groups that may
+// share a pass (lanes 0-7 with 16-23 or with 24-31, and so on) hit distinct banks: bits 1-2 of
+// the row pick the swizzle from {0, 1, 4, 5} (FWD, never flipping unit bit 1, which separates
+// g from g ^ 1) or {0, 2, 4, 6} (DX, never flipping bit 0), and bit 0 of the row already picks
+// the other half of the 64 banks.
+template <int MODE> __device__ __forceinline__ int rw_swz(int row) {
+  return MODE == 0 ? ((row >> 1) & 1) | (((row >> 2) & 1) << 2) : ((row >> 1) & 3) << 1;
+}
+
+template <int To, int NI, int MODE, int ELT>
+__device__ __forceinline__ void rw_acc(const SkArgs& a, int64_t r0, int64_t tok0, int rot,
+                                       uint8_t* smem, f32x4 (&acc)[NI][To]) {
+  using E = Elt<ELT>;
+  typedef typename E::v8 V8;
+  constexpr int BN = 16 * To, XL = To / 2, SLOT = 2 * BN * 128, G = rw_group(To, MODE), D = rw_depth(To, MODE);
+  constexpr uint32_t OOB = 0x80000000u;
+  const int t = threadIdx.x, lane = t & 63;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wr = w & 3, par = w >> 2;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int nsteps = (int)(a.Kred / 128);
+  const __amdgpu_buffer_rsrc_t rx = sk_rsrc(a.act, a.M * a.Kred * 2);
+  const int64_t wbytes = MODE == 0 ? a.Ncols * a.ldq : a.Kred * a.ldq;
+  const __amdgpu_buffer_rsrc_t rq = sk_rsrc(a.q, wbytes);
+  // activations: the lane's load j fills LDS unit (8 j + w) 64 + lane of the step's slot
+  uint32_t vx[XL], lx[XL];
+#pragma unroll
+  for (int j = 0; j < XL; ++j) {
+    const int u = (8 * j + w) * 64 + lane;
+    const int p = u / (BN * 8), rem = u % (BN * 8), row = rem >> 3;
+    const int col = (rem & 7) ^ rw_swz<MODE>(row);
+    const int64_t tok = tok0 + row;
+    vx[j] = tok < a.M ? (uint32_t)(tok * a.Kred * 2 + p * 128 + col * 16) : OOB;
+    lx[j] = (uint32_t)u * 16u;
+  }
+  // weight: FWD row r0 + 16 NI wr + 16 i + l16, bytes 16 g of the chunk; DX row n = lane of the
+  // chunk, bytes r0 + 16 NI wr + 16 i (16 output columns k)
+  uint32_t vw[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    if (MODE == 0) {
+      const int64_t row = r0 + 16 * NI * wr + 16 * i + l16;
+      vw[i] = row < a.Ncols ? (uint32_t)(row * a.ldq + 16 * g + 64 * par) : OOB;
+    } else {
+      const int64_t col = r0 + 16 * NI * wr + 16 * i;
+      vw[i] = col < a.Ncols ? (uint32_t)((64 * par + lane) * a.ldq + col) : OOB;
+    }
+  }
+  const uint32_t wstep = MODE == 0 ? 128u : (uint32_t)(128 * a.ldq);
+  // DX: the block's scales s[0 .. Kred) in LDS after the activation slots, and this wave's
+  // [64 n][16 NI] code tile after them
+  float* stab = reinterpret_cast<float*>(smem + 2 * G * SLOT);
+  uint8_t* wt = smem + 2 * G * SLOT + align16((int)a.Kred * 4) + w * (1024 * NI);
+  if constexpr (MODE == 1) {
+    for (int i = t; i < (int)a.Kred / 4; i += 64 * sk::NWV)
+      reinterpret_cast<f32x4*>(stab)[i] = reinterpret_cast<const f32x4*>(a.s)[i];
+  }
+
+  u32x4 xr[D][XL], wq[D][NI];
+  // Steps past the operands read zeros: their scalar offset alone moves every lane past the
+  // descriptor (the planner keeps the operands below 2^30 bytes, so no offset wraps).
+  constexpr uint32_t PAST = 0x40000000u;
+  // The walk over the reduction starts at step rot (then wraps): weight rows lie a multiple of
+  // 1 KiB apart, so row blocks that walked the same offsets together would pile onto a few
+  // memory channels. Step s of the walk is reduction step at(s).
+  auto at = [&](int s) { const int v = s + rot; return v >= nsteps ? v - nsteps : v; };
+  auto issue = [&](int s, u32x4 (&xd)[XL], u32x4 (&wd)[NI]) {
+    const bool ok = s < nsteps;
+    const int sr = at(s);
+    const uint32_t sx = ok ? (uint32_t)sr * 256u : PAST, sw = ok ? (uint32_t)sr * wstep : PAST;
+#pragma unroll
+    for (int j = 0; j < XL; ++j)
+      xd[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, vx[j], sx, 0));
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+      wd[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, vw[i], sw, 0));
+  };
+  // the wave's DX code tile: with an even NI, rows r and r + 8 (read in one pass of the
+  // transposed read) would share banks, so the 16-byte units of a row are flipped by its bit 3
+  auto wt_swz = [&](int row) { return (NI % 2 == 0) ? ((row >> 3) & 1) : 0; };
+  auto put_x = [&](const u32x4 (&xd)[XL], int slot) {
+#pragma unroll
+    for (int j = 0; j < XL; ++j) *reinterpret_cast<u32x4*>(smem + slot * SLOT + lx[j]) = xd[j];
+  };
+#pragma unroll
+  for (int i = 0; i < NI; ++i)
+#pragma unroll
+    for (int tt = 0; tt < To; ++tt) acc[i][tt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // the MFMA A operands of step s from its codes: FWD exact int8 -> bf16 (f16); DX through the
+  // wave's LDS tile, each code scaled by s[n]
+  auto convert = [&](const u32x4 (&wv)[NI], int s, V8 (&af)[NI][2]) {
+    if constexpr (MODE == 0) {
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        af[i][0] = E::from_i8x8(wv[i][0], wv[i][1]);
+        af[i][1] = E::from_i8x8(wv[i][2], wv[i][3]);
+      }
+    } else {
+      // the code tile [64 n][16 NI k] to this wave's LDS tile, then per 16-k tile i and step e the
+      // transposed read: providing lane p of a 16-lane group addresses row 32 e + 8 g + p / 2,
+      // columns 16 i + 8 (p % 2) .. +7; lane l16 receives k = 16 i + l16, n = 32 e + 8 g + (0..7)
+#pragma unroll
+      for (int i = 0; i < NI; ++i) *reinterpret_cast<u32x4*>(wt + lane * (16 * NI) + 16 * (i ^ wt_swz(lane))) = wv[i];
+      // the zero codes of a step past the operands may take any scale
+      const int64_t nb = s < nsteps ? (int64_t)(2 * at(s) + par) * 64 : 0;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const f32x4 s0 = *reinterpret_cast<const f32x4*>(stab + nb + 32 * e + 8 * g);
+        const f32x4 s1 = *reinterpret_cast<const f32x4*>(stab + nb + 32 * e + 8 * g + 4);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          const int row = 32 * e + 8 * g + (l16 >> 1);
+          const uint8_t* p = wt + row * (16 * NI) + 16 * (i ^ wt_swz(row)) + 8 * (l16 & 1);
+          const i32x2 v = __builtin_amdgcn_ds_read_tr8_b64_v2i32(LDS_PTR(i32x2, p));
+          if constexpr (ELT == REELS_HIP_F16) {  // Float16(q) * Float16(s[n])
+            const u32x4 s16 = {E::pack2(s0[0], s0[1]), E::pack2(s0[2], s0[3]),
+                               E::pack2(s1[0], s1[1]), E::pack2(s1[2], s1[3])};
+            af[i][e] = E::scale8(E::from_i8x8((uint32_t)v[0], (uint32_t)v[1]), s16);
+          } else {  // bf16(fl32(q * s[n]))
+            const uint32_t lo = (uint32_t)v[0], hi = (uint32_t)v[1];
+            const u32x4 o = {E::pack2_fast((float)(int8_t)(lo & 0xffu) * s0[0], (float)(int8_t)((lo >> 8) & 0xffu) * s0[1]),
+                             E::pack2_fast((float)(int8_t)((lo >> 16) & 0xffu) * s0[2], (float)((int32_t)lo >> 24) * s0[3]),
+                             E::pack2_fast((float)(int8_t)(hi & 0xffu) * s1[0], (float)(int8_t)((hi >> 8) & 0xffu) * s1[1]),
+                             E::pack2_fast((float)(int8_t)((hi >> 16) & 0xffu) * s1[2], (float)((int32_t)hi >> 24) * s1[3])};
+            af[i][e] = E::as8(o);
+          }
+        }
+      }
+    }
+  };
+
+  // Step s: its activation fragments from LDS, then its MFMAs (k step outermost, so the two
+  // products into one accumulator lie NI To MFMAs apart) interleaved with the conversion of step
+  // s + 1's codes, so the matrix cores and the VALU work side by side in each wave.
+  auto mma_convert = [&](int s, const V8 (&afc)[NI][2], const u32x4 (&wn)[NI], V8 (&afn)[NI][2]) {
+    const uint8_t* xs = smem + (s % (2 * G)) * SLOT + par * (BN * 128);
+    const int sw = rw_swz<MODE>(l16);  // the same for every 16-row token tile
+    u32x4 xv[2][To];
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+#pragma unroll
+      for (int tt = 0; tt < To; ++tt) {
+        // FWD: k = 16 g + 8 e + (0..7) (unit 2 g + e); DX: n = 32 e + 8 g + (0..7) (unit 4 e + g)
+        const int unit = MODE == 0 ? 2 * g + e : 4 * e + g;
+        xv[e][tt] = *reinterpret_cast<const u32x4*>(xs + (16 * tt + l16) * 128 + ((unit ^ sw) << 4));
+      }
+    convert(wn, s + 1, afn);
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+#pragma unroll
+      for (int tt = 0; tt < To; ++tt)
+#pragma unroll
+        for (int i = 0; i < NI; ++i) acc[i][tt] = E::mfma16(afc[i][e], E::as8(xv[e][tt]), acc[i][tt]);
+    // schedule: the fragment reads, then one MFMA and a few VALU (and for dX LDS) ops in turn
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * To, 0);
+#pragma unroll
+    for (int k = 0; k < 2 * NI * To; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, MODE == 0 ? 3 : 6, 0);
+      if constexpr (MODE == 1) __builtin_amdgcn_sched_group_barrier(0x080, 1, 0);
+    }
+  };
+
+  // Step s reads ring slot s % 2G and writes the activations of step s + G (loaded G steps
+  // earlier) into slot (s + G) % 2G, which the group before last read; register slot j takes
+  // step s + D (zeros when s + D >= nsteps). Steps past nsteps write zeros nobody reads.
+  V8 afa[NI][2], afb[NI][2];
+  auto step = [&](int s, int j, V8 (&afc)[NI][2], V8 (&afn)[NI][2]) {
+    mma_convert(s, afc, wq[(j + 1) % D], afn);
+    put_x(xr[(j + G) % D], (s + G) % (2 * G));
+    issue(s + D, xr[j], wq[j]);
+  };
+  // A group's barrier: every wave's writes of the next group's activations are done, and every
+  // wave has finished reading the slots the group after writes. It waits for LDS operations
+  // only: the loads in flight stay in flight (a __syncthreads() would wait for vmcnt(0) in its
+  // release fence).
+  auto group_barrier = [&]() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  // prologue: steps 0 .. D-1 in flight, the first group's activations in slots 0 .. G-1, then
+  // (after the barrier) the first step's codes converted
+#pragma unroll
+  for (int d = 0; d < D; ++d) issue(d, xr[d], wq[d]);
+#pragma unroll
+  for (int d = 0; d < G; ++d) put_x(xr[d], d);
+  group_barrier();  // also publishes the DX scale table, which convert reads
+  convert(wq[0], 0, afa);
+  // whole units of D steps without a branch inside (a conditional step in the unrolled body
+  // makes the compiler drain every load at the loop head), then the last steps
+  static_assert(D % G == 0 && D > G && D % 2 == 0, "a unit of D steps holds whole groups");
+  const int nfull = nsteps / D * D;
+  for (int s0 = 0; s0 < nfull; s0 += D) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      if (j & 1) step(s0 + j, j, afb, afa);
+      else step(s0 + j, j, afa, afb);
+      if ((j + 1) % G == 0) group_barrier();
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < D; ++j) {
+    if (nfull + j < nsteps) {
+      if (j & 1) step(nfull + j, j, afb, afa);
+      else step(nfull + j, j, afa, afb);
+      if ((j + 1) % G == 0 && nfull + j + 1 < nsteps) group_barrier();
+    }
+  }
+}
+
+// lo[i][tt] (rows 16 i + 4 g + v of the wave's 16 NI, tokens of the wave's token tiles) += the
+// adapter term l R over rank columns [0, rp): FWD R(o, j) = B[j][o] staged per wave in LDS and
+// read transposed, DX R(k, j) = A[k][j] read straight from memory; l = h or u from the workspace
+template <int NI, int TH, int MODE, int ELT>
+__device__ __forceinline__ void rw_lora(const SkArgs& a, int64_t ob, int64_t tok0, uint8_t* wst,
+                                        f32x4 (&lo)[NI][TH]) {
+  using E = Elt<ELT>;
+  const int lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
+  const __amdgpu_buffer_rsrc_t rl = sk_rsrc(a.hl, a.M * a.rp * 2);
+  const int njc = (a.rp + 31) / 32;
+  for (int jc = 0; jc < njc; ++jc) {
+    const int j0 = 32 * jc;
+    u32x4 hv[TH];
+#pragma unroll
+    for (int tt = 0; tt < TH; ++tt) {
+      const int64_t tok = tok0 + 16 * tt + l16;
+      const int jj = j0 + 8 * g;
+      hv[tt] = u32x4{0u, 0u, 0u, 0u};
+      if (tok < a.M && jj < a.rp)
+        hv[tt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rl, (uint32_t)((tok * a.rp + jj) * 2), 0, kSC1));
+    }
+    u32x4 av[NI];
+    if constexpr (MODE == 0) {
+      // rows j0 .. j0 + 31 of B, columns ob .. ob + 16 NI, into the wave's tile [32 j][16 NI o]
+      // (2 NI lanes per row, 16 bytes each), then transposed 16-bit reads: providing lane p
+      // addresses row 8 g + 4 h + p / 4, columns 16 i + 4 (p % 4) .. +3; lane l16 receives
+      // o = 16 i + l16, j = 8 g + 4 h + (0..3)
+      uint16_t* rst = reinterpret_cast<uint16_t*>(wst);
+#pragma unroll
+      for (int k = 0; k < NI; ++k) {
+        const int idx = lane + 64 * k, row = idx / (2 * NI), c8 = 8 * (idx % (2 * NI));
+        u32x4 v = u32x4{0u, 0u, 0u, 0u};
+        if (j0 + row < a.r && ob + c8 < a.Ncols)
+          v = *reinterpret_cast<const u32x4*>(a.R + (int64_t)(j0 + row) * a.ldr + ob + c8);
+        *reinterpret_cast<u32x4*>(rst + row * (16 * NI) + c8) = v;
+      }
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint16_t* p = rst + (8 * g + 4 * h + (l16 >> 2)) * (16 * NI) + 16 * i + 4 * (l16 & 3);
+          const i16x4 r4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(i16x4, p));
+          av[i][2 * h] = (uint16_t)r4[0] | ((uint32_t)(uint16_t)r4[1] << 16);
+          av[i][2 * h + 1] = (uint16_t)r4[2] | ((uint32_t)(uint16_t)r4[3] << 16);
+        }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int64_t k = ob + 16 * i + l16;
+        const int jj = j0 + 8 * g;
+        av[i] = (k < a.Ncols && jj < a.rp) ? *reinterpret_cast<const u32x4*>(a.R + k * a.ldr + jj)
+                                           : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+      for (int tt = 0; tt < TH; ++tt) lo[i][tt] = E::mfma16(E::as8(av[i]), E::as8(hv[tt]), lo[i][tt]);
+  }
+}
+
+// One row-wave output tile: the wave's accumulators, the pair sum of waves w and w + 4 (each
+// keeps half the token tiles), l when the adapter blocks have published it (or computed here with
+// their code, splits and order when they have not), then out = rnd(scale sum + c l R + bias).
+template <int To, int NI, int Ta, int MODE, int ELT>
+__device__ __forceinline__ void rw_block(const SkArgs& a, int rb, int tbo, uint8_t* smem,
+                                         int lds_bytes) {
+  using E = Elt<ELT>;
+  constexpr int TH = To / 2;
+  const int t = threadIdx.x, lane = t & 63;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wr = w & 3, par = w >> 2;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int64_t r0 = (int64_t)rb * (64 * NI), tok0 = (int64_t)tbo * (16 * To);
+  const int64_t ob = r0 + 16 * NI * wr;          // the wave's first output row
+  const int64_t tw0 = tok0 + (int64_t)par * (16 * TH);  // the wave's first token after the pair sum
+  uint32_t* words = reinterpret_cast<uint32_t*>(smem + lds_bytes - 16);
+  SkCounters* ctr = a.ctr;
+  const bool wants_l = a.nad > 0;
+  uint32_t up = 0;
+  if (wants_l) up = sk_load(&ctr->hready);
+
+  f32x4 sum[NI][TH];
+  {
+    f32x4 acc[NI][To];
+    // a rotation per row block (the token tiles of one row block read its weight rows together)
+    const int nsteps = (int)(a.Kred / 128);
+    rw_acc<To, NI, MODE, ELT>(a, r0, tok0, (int)(((int64_t)rb * 7) % nsteps), smem, acc);
+    // waves 4-7 give their first half of the token tiles, waves 0-3 their second, through LDS;
+    // each then adds (partner + own, wave w's value first: the same sum for both halves)
+    f32x4* ex = reinterpret_cast<f32x4*>(smem);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+      for (int tt = 0; tt < TH; ++tt)
+        ex[((w * NI + i) * TH + tt) * 64 + lane] = acc[i][par == 0 ? TH + tt : tt];
+    __syncthreads();
+    const int pw = w ^ 4;
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+      for (int tt = 0; tt < TH; ++tt) {
+        const f32x4 other = ex[((pw * NI + i) * TH + tt) * 64 + lane];
+        const f32x4 own = acc[i][par == 0 ? tt : TH + tt];
+        sum[i][tt] = par == 0 ? own + other : other + own;
+      }
+    __syncthreads();  // LDS free again
+  }
+
+  if (wants_l) {
+    // the adapter blocks come first in the logical order and wait for nothing, so the flag is
+    // normally up; after a bounded wait the block computes l for its tokens itself, with the
+    // adapter blocks' code, splits and order (the same bits)
+    if (t == 0) {
+      uint32_t n = 0, v = up;
+      while (v == 0u && ++n <= a.spin) {
+        __builtin_amdgcn_s_sleep(8);
+        v = sk_load(&ctr->hready);
+      }
+      words[2] = v;
+    }
+    __syncthreads();
+    if (words[2] == 0u) {
+      const int tb_lo = (int)(tok0 / (16 * Ta));
+      const int tb_hi = (int)((tok0 + 16 * To + 16 * Ta - 1) / (16 * Ta));
+      for (int tba = tb_lo; tba < tb_hi && tba < a.tb; ++tba)
+        for (int lb = 0; lb < a.lblk; ++lb) {
+          constexpr int FA = sk_fpw<2 * Ta>();
+          f32x4 tl[FA];
+#pragma unroll
+          for (int k = 0; k < FA; ++k) tl[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+          for (int s = 0; s < a.S; ++s) {
+            f32x4 acc[2][Ta], ps[FA];
+            skinny_acc<Ta, MODE, ELT, true>(a, a.nblk + lb, s, (int64_t)tba * (16 * Ta), smem, acc);
+            skinny_sum<Ta, 2>(acc, smem, ps);
+#pragma unroll
+            for (int k = 0; k < FA; ++k) tl[k] += ps[k];
+          }
+          skinny_put_l<Ta, ELT>(a, (int64_t)lb * sk::NBL, (int64_t)tba * (16 * Ta), tl, false);
+        }
+      sk_drain();
+      __syncthreads();
+    }
+    asm volatile("" ::: "memory");
+  }
+
+  f32x4 lo[NI][TH];
+#pragma unroll
+  for (int i = 0; i < NI; ++i)
+#pragma unroll
+    for (int tt = 0; tt < TH; ++tt) lo[i][tt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  if (wants_l) rw_lora<NI, TH, MODE, ELT>(a, ob, tw0, smem + w * (1024 * NI), lo);
+
+  // out = rnd(scale * sum + c * lo + bias), rows o = ob + 16 i + 4 g + v, token 16 tt + l16
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int64_t o = ob + 16 * i + 4 * g;
+    if (o >= a.Ncols) continue;
+    f32x4 cs = f32x4{1.0f, 1.0f, 1.0f, 1.0f};
+    if (a.colscale) cs = *reinterpret_cast<const f32x4*>(a.colscale + o);
+    u32x2 bsv = u32x2{0u, 0u};
+    if (a.bias) bsv = *reinterpret_cast<const u32x2*>(a.bias + o);
+    const float bv[4] = {E::lo(bsv[0]), E::hi(bsv[0]), E::lo(bsv[1]), E::hi(bsv[1])};
+#pragma unroll
+    for (int tt = 0; tt < TH; ++tt) {
+      const int64_t tok = tw0 + 16 * tt + l16;
+      if (tok >= a.M) continue;
+      uint32_t b[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float sc = a.colscale ? cs[v] * sum[i][tt][v] : sum[i][tt][v];
+        b[v] = E::bits(sc + a.c * lo[i][tt][v] + bv[v]);
+      }
+      *reinterpret_cast<uint2*>(a.out + tok * a.Ncols + o) = uint2{b[0] | (b[1] << 16), b[2] | (b[3] << 16)};
+    }
+  }
+}
+
+template <int To, int NI, int Ta, int MODE, int ELT>
+__global__ __launch_bounds__(64 * sk::NWV, 1) void skinny_rw_kernel(SkArgs a, int lds_bytes) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  // the logical order and XCD mapping of skinny_kernel: adapter blocks first, then the output
+  // tiles with the token tile fastest, so the tiles that read the same weight rows run on one
+  // XCD, close in time
+  const int b = (int)blockIdx.x, xcd = b & 7, idx = b >> 3;
+  const int per = a.blocks >> 3, rem = a.blocks & 7;
+  const int tk = xcd * per + (xcd < rem ? xcd : rem) + idx;
+  if (tk < a.nad) {
+    int rest = tk;
+    SkBlock d;
+    d.tb = rest % a.tb;
+    rest /= a.tb;
+    d.sp = rest % a.S;
+    const int rb = rest / a.S;
+    d.blk = a.nblk + rb;
+    d.tile = a.ntm + rb * a.tb + d.tb;
+    skinny_block<Ta, MODE, ELT, true>(a, d, smem);
+  } else {
+    const int ti = tk - a.nad;
+    rw_block<To, NI, Ta, MODE, ELT>(a, ti / a.otb, ti % a.otb, smem, lds_bytes);
+  }
+}
+
 template <int T, int MODE, int ELT>
 __global__ __launch_bounds__(64 * sk::NWV, 1) void skinny_kernel(SkArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -708,22 +1154,89 @@ __global__ __launch_bounds__(64 * sk::NWV, 1) void skinny_kernel(SkArgs a) {
   else skinny_block<T, MODE, ELT, false>(a, d, smem);
 }
 
-bool skinny_supported(int64_t M, int64_t K, int64_t N, int rp) {
+// Row-wave tiles (NI, To) for a launch: the candidates whose output tiles and adapter blocks fit
+// one round of the 256 CUs and fill most of it; among them the least estimated clocks per
+// 128-deep step on a CU (the largest of the matrix cores, the LDS reads, the vector memory and,
+// for dX, the VALU scaling of the codes), then the least padded work.
+struct RwCand { int NI, To; };
+constexpr RwCand kRwCands[] = {{1, 2}, {2, 4}, {3, 4}, {2, 6}};
+constexpr int kRwLdsMax = 160 * 1024;
+
+static int rw_lds_bytes(int NI, int To, int mode, int64_t Kred) {
+  const int slot = 2 * 16 * To * 128, ta = To <= 4 ? To : To / 2;
+  int v = 2 * rw_group(To, mode) * slot + (mode == 1 ? align16((int)Kred * 4) + 8 * 1024 * NI : 0);
+  v = std::max(v, 8 * NI * (To / 2) * 1024);
+  v = std::max(v, skinny_lds(ta));
+  v = std::max(v, 8 * 1024 * NI);
+  return v + 16;
+}
+
+static bool rw_choose(int64_t M, int64_t Kred, int64_t Ncols, int rp, int mode, SkinnyPlan& out) {
+  if (M <= 0 || Kred % 128 != 0 || Ncols % 64 != 0 || Kred > 16384) return false;
+  // the kernel moves steps past the operands with a scalar offset of 2^30 bytes
+  if (M * Kred * 2 > ((int64_t)1 << 30) || Ncols * Kred > ((int64_t)1 << 30)) return false;
+  bool found = false;
+  int64_t best_cost = 0, best_work = 0;
+  for (const RwCand& c : kRwCands) {
+    const int64_t orb = ceil_div(Ncols, 64 * c.NI), otb = ceil_div(M, 16 * c.To);
+    const int ta = c.To <= 4 ? c.To : c.To / 2;
+    const int64_t tba = ceil_div(M, 16 * ta), lblk = ceil_div(rp, sk::NBL);
+    const int64_t tiles = orb * otb, nad = rp > 0 ? lblk * tba : 0;
+    if (tiles + nad > kSkinnyTargetBlocks || tiles < kSkinnyTargetBlocks / 2) continue;
+    if (rw_lds_bytes(c.NI, c.To, mode, Kred) > kRwLdsMax) continue;
+    const int64_t mf = 64 * c.NI * c.To, lds = 128 * c.To, vm = 128 * c.NI + 64 * c.To;
+    const int64_t valu = (mode == 1 ? 384 : 192) * c.NI;
+    const int64_t cost = std::max(std::max(mf, lds), std::max(vm, valu));
+    const int64_t work = orb * 64 * c.NI * otb * 16 * c.To;
+    if (!found || cost < best_cost || (cost == best_cost && work < best_work)) {
+      found = true;
+      best_cost = cost;
+      best_work = work;
+      out.rw = true;
+      out.NI = c.NI; out.To = c.To;
+      out.orb = (int)orb; out.otb = (int)otb;
+      out.T = ta; out.tb = (int)tba;
+      // adapter splits: as many as the round leaves room for (shorter adapter blocks publish l
+      // sooner), each wave at least one chunk
+      int64_t S = nad > 0 ? (kSkinnyTargetBlocks - tiles) / nad : 1;
+      if (S > Kred / sk::KC / 4) S = Kred / sk::KC / 4;
+      if (S > sk::MAXS) S = sk::MAXS;
+      if (S < 1) S = 1;
+      out.S = (int)S;
+    }
+  }
+  return found;
+}
+
+static bool skinny_limits(int64_t M, int64_t K, int64_t N, int rp) {
   // the reduction in whole 64-chunks, whole 64-row blocks, 32-bit buffer offsets (with room for
-  // the token-block overrun), the tiles within a counter slot
+  // the token-block overrun), the tiles within the counter array
   const int64_t tb = ceil_div(M, 16 * sk::MAXT);
   const int64_t mx = K > N ? K : N;
-  // up to 240 tokens, or up to 1024 on a small weight (at most 4M elements, which stays in L2
-  // across the token blocks): there one launch beats the 256 x 256-tile GEMM's few tiles
-  const bool few = M <= kSkinnyMaxTokens || (M <= kSkinnySmallWeightTokens && N * K <= ((int64_t)1 << 22));
-  return M > 0 && few && K % 64 == 0 && N % 64 == 0 &&
+  return M > 0 && K % 64 == 0 && N % 64 == 0 &&
          (M + 128) * mx * 2 < ((int64_t)1 << 31) && N * K < ((int64_t)1 << 31) &&
          (int64_t)rp * mx * 2 < ((int64_t)1 << 31) && rp <= 4096 &&
          (mx / sk::NB + ceil_div(rp, sk::NBL)) * tb <= sk::kMaxTiles;
 }
 
-SkinnyPlan skinny_plan(int64_t M, int64_t Kred, int64_t Ncols, int rp) {
+bool skinny_supported(int64_t M, int64_t K, int64_t N, int rp) {
+  if (!skinny_limits(M, K, N, rp)) return false;
+  // up to 240 tokens, or up to 1024 on a small weight (at most 4M elements, which stays in L2
+  // across the token blocks): there one launch beats the 256 x 256-tile GEMM's few tiles
+  if (M <= kSkinnyMaxTokens || (M <= kSkinnySmallWeightTokens && N * K <= ((int64_t)1 << 22)))
+    return true;
+  // a few hundred tokens on a large weight: row-wave tiles in both directions
+  SkinnyPlan f, d;
+  return M <= kSkinnySmallWeightTokens && rw_choose(M, K, N, rp, 0, f) && rw_choose(M, N, K, rp, 1, d);
+}
+
+SkinnyPlan skinny_plan(int64_t M, int64_t Kred, int64_t Ncols, int rp, int mode) {
   SkinnyPlan p;
+  // the forward takes row-wave tiles wherever they fill the GPU; dX up to 240 tokens keeps the
+  // split tiles (its weight scaling costs the row-wave loop more: 77 tokens on 5120 x 5120,
+  // 26 against 30 us)
+  const bool few = M <= kSkinnyMaxTokens || (M <= kSkinnySmallWeightTokens && Ncols * Kred <= ((int64_t)1 << 22));
+  if ((mode == 0 || !few) && rw_choose(M, Kred, Ncols, rp, mode, p)) return p;
   p.tb = (int)ceil_div(M, 16 * sk::MAXT);
   p.T = (int)ceil_div(ceil_div(M, p.tb), 16);
   const int64_t blocks = (Ncols / sk::NB + ceil_div(rp, sk::NBL)) * p.tb;
@@ -745,8 +1258,12 @@ struct SkWs {
 };
 static SkWs skinny_ws(const SkinnyPlan& p, int64_t M, int64_t Ncols, int rp) {
   SkWs w;
-  const size_t frags = (size_t)(Ncols / sk::NB) * p.tb * (4 * p.T) + (size_t)ceil_div(rp, sk::NBL) * p.tb * (2 * p.T);
-  w.ntiles = (int)((Ncols / sk::NB + ceil_div(rp, sk::NBL)) * p.tb);
+  // split partials in MFMA fragments: the output tiles' (none for row-wave tiles), then the
+  // adapter tiles'
+  const size_t ofrags = p.rw ? 0 : (size_t)(Ncols / sk::NB) * p.tb * (4 * p.T);
+  const size_t frags = ofrags + (size_t)ceil_div(rp, sk::NBL) * p.tb * (2 * p.T);
+  const int64_t otiles = p.rw ? (int64_t)p.orb * p.otb : (Ncols / sk::NB) * p.tb;
+  w.ntiles = (int)(otiles + ceil_div(rp, sk::NBL) * p.tb);
   w.part = 0;
   w.hl = align_up(p.S > 1 ? frags * p.S * 64 * 16 : 0, 256);
   w.ctr = align_up(w.hl + (size_t)M * rp * 2, 256);
@@ -771,6 +1288,19 @@ static hipError_t launch_skinny_t(const SkArgs& a, hipStream_t st) {
   return hipSuccess;
 }
 
+template <int To, int NI, int Ta, int MODE, int ELT>
+static hipError_t launch_rw_t(const SkArgs& a, int lds, hipStream_t st) {
+  static std::once_flag once;
+  static hipError_t attr = hipSuccess;
+  std::call_once(once, [] {
+    attr = hipFuncSetAttribute((const void*)skinny_rw_kernel<To, NI, Ta, MODE, ELT>,
+                               hipFuncAttributeMaxDynamicSharedMemorySize, kRwLdsMax);
+  });
+  if (attr != hipSuccess) return attr;
+  skinny_rw_kernel<To, NI, Ta, MODE, ELT><<<dim3((unsigned)a.blocks), 64 * sk::NWV, lds, st>>>(a, lds);
+  return hipSuccess;
+}
+
 int launch_skinny(int mode, int elt, const SkinnyPlan& p, const uint16_t* act, const int8_t* q,
                   int64_t ldq, const float* s, const uint16_t* lw, void* ws, int64_t M,
                   int64_t Kred, int64_t Ncols, int r, int rp, const float* colscale,
@@ -786,14 +1316,16 @@ int launch_skinny(int mode, int elt, const SkinnyPlan& p, const uint16_t* act, c
   a.tb = p.tb;
   a.colscale = colscale; a.R = R; a.ldr = ldr; a.bias = bias; a.c = c;
   a.out = out; a.lsave = lsave; a.ld_lsave = ld_lsave; a.lsave_cols = lsave_cols;
-  a.ntm = adapter_only ? 0 : a.nblk * p.tb;
+  a.ntm = adapter_only ? 0 : (p.rw ? p.orb * p.otb : a.nblk * p.tb);
   a.nta = a.lblk * p.tb;
+  a.otb = p.otb;
+  a.lpart0 = p.rw ? 0 : (int64_t)a.ntm * p.S * (4 * p.T * 64);
   // REELS_HIP_SKINNY_SPIN (tests): wait rounds before an output tile computes l itself; 0 makes
   // every output tile take that path
   a.spin = sk::kSpinLimit;
   if (const char* e = std::getenv("REELS_HIP_SKINNY_SPIN")) a.spin = (uint32_t)std::strtoul(e, nullptr, 10);
   a.nad = a.nta * p.S;
-  a.blocks = a.nad + a.ntm * p.S;
+  a.blocks = a.nad + a.ntm * (p.rw ? 1 : p.S);
   if (a.blocks <= 0) return REELS_HIP_OK;
   const SkWs w = skinny_ws(p, M, Ncols, a.rp);
   uint8_t* wb = static_cast<uint8_t*>(ws);
@@ -810,7 +1342,22 @@ int launch_skinny(int mode, int elt, const SkinnyPlan& p, const uint16_t* act, c
   if (int rc = check_launch("skinny_clear_kernel")) return rc;
 
   hipError_t attr = hipSuccess;
-  {
+  if (p.rw) {
+    TraceScope _ts(st, mode == 0 ? "skinny_rw_kernel<0>" : "skinny_rw_kernel<1>");
+    const int lds = rw_lds_bytes(p.NI, p.To, mode, Kred);
+    with_elt(elt, [&](auto el) {
+      constexpr int EL = decltype(el)::value;
+      auto go = [&](auto m) {
+        constexpr int MD = decltype(m)::value;
+        if (p.NI == 1 && p.To == 2) attr = launch_rw_t<2, 1, 2, MD, EL>(a, lds, st);
+        else if (p.NI == 2 && p.To == 4) attr = launch_rw_t<4, 2, 4, MD, EL>(a, lds, st);
+        else if (p.NI == 3 && p.To == 4) attr = launch_rw_t<4, 3, 4, MD, EL>(a, lds, st);
+        else attr = launch_rw_t<6, 2, 3, MD, EL>(a, lds, st);
+      };
+      if (mode == 0) go(std::integral_constant<int, 0>{});
+      else go(std::integral_constant<int, 1>{});
+    });
+  } else {
     TraceScope _ts(st, mode == 0 ? "skinny_kernel<0>" : "skinny_kernel<1>");
     with_elt(elt, [&](auto el) {
       constexpr int EL = decltype(el)::value;
