@@ -254,9 +254,11 @@ int reels_hip_gelu_tanh_bwd_f32(const float* x, const float* dy, float* dx, int6
  *   q, out, dy, dq [B][Sq][H][D];  k, v, dk, dv [B][Sk][H][D];  lse [B][H][Sq] f32
  *   mask [Sq][Sk] uint8, nonzero = visible (the reference's (key_tokens, query_tokens) Bool
  *   array), or NULL; causal != 0: key index <= query index.
- * dtype REELS_HIP_BF16 or REELS_HIP_F16 for q, k, v, out, dy, dq, dk, dv; head dim D = 64 or 128;
- * 16-byte aligned tensors; one batch of q or k below 2 GiB. Scores, softmax and sums run in f32
- * with scale 1/sqrt(Float32(D)) (attention.jl:129); P is rounded to dtype for the P V product.
+ * dtype REELS_HIP_BF16, REELS_HIP_F16 or REELS_HIP_F32 for q, k, v, out, dy, dq, dk, dv; head
+ * dim 1 <= D <= 128; 16-byte aligned tensors; one batch of q or k below 2 GiB. Scores, softmax
+ * and sums run in f32 with scale 1/sqrt(Float32(D)) (attention.jl:129). bf16 / f16 with D = 64
+ * or 128 take the tuned kernels, which round P to dtype for the P V product; f32 and other head
+ * dims take kernels that keep P in f32 (the reference's order) at a lower rate.
  * A query with no visible key gets NaN output and NaN lse (-Inf when Sk = 0), as the reference;
  * it contributes nothing to dq, dk, dv (in the reference its NaN correction reaches every dk of
  * the head). The reference's query_block / key_block do not change the result and have no

@@ -5,8 +5,9 @@
 Tensors are torch tensors in the row-major form of the reference's ``(head_dim, heads, tokens,
 batch)`` arrays: ``q`` ``[B][Sq][H][D]``, ``k`` and ``v`` ``[B][Sk][H][D]``; ``mask`` is the
 reference's ``(key_tokens, query_tokens)`` Bool array as a ``[Sq][Sk]`` bool tensor (True =
-visible). bfloat16 or float16, head dim 64 or 128, on the ROCm device; the output has the
-input dtype (``promote_type`` of equal types) and the cache keeps the f32 log-sum-exp.
+visible). bfloat16, float16 or float32, any head dim up to 128, on the ROCm device (bfloat16 and
+float16 with head dim 64 or 128 take the tuned kernels, the rest the generic ones); the output
+has the input dtype (``promote_type`` of equal types) and the cache keeps the f32 log-sum-exp.
 """
 from __future__ import annotations
 
@@ -20,7 +21,7 @@ import torch
 from . import _lib
 from .layers import _need_device, _ptr, _stream
 
-_DT = {torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
+_DT = {torch.bfloat16: _lib.BF16, torch.float16: _lib.F16, torch.float32: _lib.F32}
 
 
 @dataclass
@@ -61,10 +62,10 @@ def _check(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
     if not (q.shape[0] == k.shape[0] == v.shape[0]):
         raise ValueError("q, k, and v batch counts differ")
     if not (q.dtype == k.dtype == v.dtype) or q.dtype not in _DT:
-        raise TypeError(f"q, k, v must share one dtype, bfloat16 or float16 (got {q.dtype}, "
-                        f"{k.dtype}, {v.dtype})")
-    if q.shape[3] not in (64, 128):
-        raise ValueError(f"head_dim must be 64 or 128 on this path, got {q.shape[3]}")
+        raise TypeError(f"q, k, v must share one dtype, bfloat16, float16 or float32 (got "
+                        f"{q.dtype}, {k.dtype}, {v.dtype})")
+    if not 1 <= q.shape[3] <= 128:
+        raise ValueError(f"head_dim must be between 1 and 128 on this path, got {q.shape[3]}")
     return q.contiguous(), k.contiguous(), v.contiguous()
 
 

@@ -1,6 +1,7 @@
 // Exact scaled dot-product attention with an online softmax: memory_efficient_attention and its
 // backward (src/layers/attention.jl:106-221 CPU, 225-371 CUDA), for bf16 / f16 tensors with f32
-// arithmetic, head_dim 64 or 128.
+// arithmetic, head_dim 64 or 128 (f32 tensors and the other head dims up to 128 go to the
+// generic kernels of attention_g.hip).
 //
 // Layouts (row-major; the reference's (head_dim, heads, tokens, batch) arrays): q, out, dq
 // [B][Sq][H][D]; k, v, dk, dv [B][Sk][H][D]; lse [B][H][Sq] f32; mask [Sq][Sk] uint8 (nonzero =
@@ -19,7 +20,7 @@
 // Backward (deterministic, no atomics): correction[q] = sum(dy .* out) (attention.jl:190); a
 // key-tile kernel accumulates dK and dV over all query tiles; a query-tile kernel accumulates dQ
 // over all key tiles. Both recompute P from lse.
-#include "common.h"
+#include "attention_g.h"
 
 namespace reels {
 
@@ -62,22 +63,6 @@ __device__ __forceinline__ uint32_t toff(int r, int d) {
 // that make no difference to any sum here
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Reductions over lanes l, l^16, l^32, l^48. v_permlane16_swap (v_permlane32_swap) with x as both
-// operands hands every lane the values of lanes l and l^16 (l^32), in an order that depends on
-// the lane: a VALU exchange instead of an LDS round trip (ds_bpermute). The sums are the same
-// bits as (x_l + x_l^16) + (x_l^32 + x_l^48) in any lane order, since a + b == b + a.
-__device__ __forceinline__ float wave_max16(float x) {
-  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
-  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
-}
-__device__ __forceinline__ float wave_sum16(float x) {
-  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = __uint_as_float(p[0]) + __uint_as_float(p[1]);
-  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(q[0]) + __uint_as_float(q[1]);
-}
 
 // A operand of 8 rows-transposed elements from an LDS tile: element e < 4 is row r0 + e,
 // element e >= 4 is row r1 + e - 4, column c (the lane's 4-column piece chosen by the caller's
@@ -683,17 +668,24 @@ __global__ __launch_bounds__(256) void attn_zero_kernel(uint16_t* p, int64_t n) 
 
 // ---------------------------------------------------------------------------------------------
 // host side
+// bf16 / f16 with head dim 64 or 128 take the tuned kernels above; f32 and the other head dims
+// up to 128 the generic kernels of attention_g.hip
+static bool attn_tuned(int dtype, int64_t D) {
+  return (dtype == REELS_HIP_BF16 || dtype == REELS_HIP_F16) && (D == 64 || D == 128);
+}
+
 static int attn_validate(const char* fn, const void* q, const void* k, const void* v, int64_t B,
                          int64_t Sq, int64_t Sk, int64_t H, int64_t D, int dtype) {
   if (B < 0 || Sq < 0 || Sk < 0 || H < 0)
     return fail(REELS_HIP_EINVAL, std::string(fn) + ": need B, Sq, Sk, H >= 0");
-  if (D != 64 && D != 128)
-    return fail(REELS_HIP_EINVAL, std::string(fn) + ": head_dim must be 64 or 128");
-  if (dtype != REELS_HIP_BF16 && dtype != REELS_HIP_F16)
-    return fail(REELS_HIP_EDTYPE, std::string(fn) + ": dtype must be REELS_HIP_BF16 or REELS_HIP_F16");
+  if (dtype != REELS_HIP_BF16 && dtype != REELS_HIP_F16 && dtype != REELS_HIP_F32)
+    return fail(REELS_HIP_EDTYPE, std::string(fn) + ": dtype must be REELS_HIP_BF16, REELS_HIP_F16 or REELS_HIP_F32");
+  if (D < 1 || D > 128)
+    return fail(REELS_HIP_EINVAL, std::string(fn) + ": head_dim must be between 1 and 128");
   if (H >= 65536 || B >= 65536)
     return fail(REELS_HIP_EINVAL, std::string(fn) + ": B and H must be below 65536");
-  if (Sq * H * D * 2 >= ((int64_t)1 << 31) || Sk * H * D * 2 >= ((int64_t)1 << 31))
+  const int64_t es = dtype == REELS_HIP_F32 ? 4 : 2;
+  if (Sq * H * D * es >= ((int64_t)1 << 31) || Sk * H * D * es >= ((int64_t)1 << 31))
     return fail(REELS_HIP_EINVAL, std::string(fn) + ": one batch of q or k over 2 GiB");
   if (B * Sq * H == 0) return 1;  // nothing to compute
   // k and v may be NULL without keys (empty tensors): nothing reads them then
@@ -784,6 +776,15 @@ extern "C" int reels_hip_attention_fwd(const void* q, const void* k, const void*
   if (int rc = attn_validate(fn, q, k, v, B, Sq, Sk, H, D, dtype)) return rc < 0 ? rc : REELS_HIP_OK;
   if (!out) return fail(REELS_HIP_EINVAL, std::string(fn) + ": NULL out");
   if (!aligned16(out)) return fail(REELS_HIP_EINVAL, std::string(fn) + ": out must be 16-byte aligned");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (!attn_tuned(dtype, D)) {
+    AttgArgs g{};
+    g.q = q; g.k = k; g.v = v; g.mask = mask; g.o = out; g.lse_out = lse;
+    g.Sq = Sq; g.Sk = Sk; g.H = H; g.D = D;
+    g.causal = causal ? 1 : 0;
+    g.scale = 1.0f / sqrtf((float)D);
+    return attn_generic_fwd(g, dtype, B, st);
+  }
   AttArgs a{};
   a.q = static_cast<const uint16_t*>(q);
   a.k = static_cast<const uint16_t*>(k);
@@ -794,7 +795,6 @@ extern "C" int reels_hip_attention_fwd(const void* q, const void* k, const void*
   a.Sq = Sq; a.Sk = Sk; a.H = H;
   a.causal = causal ? 1 : 0;
   a.scale = 1.0f / sqrtf((float)D);
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   return with_att(dtype, D, [&](auto e, auto d) { return launch_attn_fwd<decltype(e)::value, decltype(d)::value>(a, B, st); });
 }
 
@@ -811,7 +811,7 @@ extern "C" int reels_hip_attention_bwd(const void* q, const void* k, const void*
     // no queries: dk and dv are zero (the reference's zero(k), zero(v))
     if (B * Sk * H > 0 && dk && dv) {
       hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-      const int64_t n = B * Sk * H * D;
+      const int64_t n = B * Sk * H * D * (dtype == REELS_HIP_F32 ? 2 : 1);  // 16-bit words
       const unsigned grid = (unsigned)(ceil_div(n, 256) < 4096 ? ceil_div(n, 256) : 4096);
       { TraceScope _ts(st, "attn_zero_kernel"); attn_zero_kernel<<<grid, 256, 0, st>>>(static_cast<uint16_t*>(dk), n); }
       { TraceScope _ts(st, "attn_zero_kernel"); attn_zero_kernel<<<grid, 256, 0, st>>>(static_cast<uint16_t*>(dv), n); }
@@ -826,6 +826,17 @@ extern "C" int reels_hip_attention_bwd(const void* q, const void* k, const void*
   if (!workspace || ws_bytes < reels_hip_attention_workspace_bytes(B, Sq, H))
     return fail(REELS_HIP_EWORKSPACE, std::string(fn) + ": workspace NULL or smaller than "
                                       "reels_hip_attention_workspace_bytes(B, Sq, H)");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (!attn_tuned(dtype, D)) {
+    AttgArgs g{};
+    g.q = q; g.k = k; g.v = v; g.out = out; g.dy = dy; g.lse = lse;
+    g.corr = static_cast<float*>(workspace);
+    g.mask = mask; g.o = dq; g.dk = dk; g.dv = dv;
+    g.Sq = Sq; g.Sk = Sk; g.H = H; g.D = D;
+    g.causal = causal ? 1 : 0;
+    g.scale = 1.0f / sqrtf((float)D);
+    return attn_generic_bwd(g, dtype, B, st);
+  }
   AttArgs a{};
   a.q = static_cast<const uint16_t*>(q);
   a.k = static_cast<const uint16_t*>(k);
@@ -842,6 +853,5 @@ extern "C" int reels_hip_attention_bwd(const void* q, const void* k, const void*
   a.Sq = Sq; a.Sk = Sk; a.H = H;
   a.causal = causal ? 1 : 0;
   a.scale = 1.0f / sqrtf((float)D);
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   return with_att(dtype, D, [&](auto e, auto d) { return launch_attn_bwd<decltype(e)::value, decltype(d)::value>(a, B, st); });
 }

@@ -96,6 +96,23 @@ __device__ __forceinline__ void dma16_at(const i32x4& rsrc, uint32_t voff, uint3
                : "memory");
 }
 
+// Reductions over lanes l, l^16, l^32, l^48. v_permlane16_swap (v_permlane32_swap) with x as both
+// operands hands every lane the values of lanes l and l^16 (l^32), in an order that depends on
+// the lane: a VALU exchange instead of an LDS round trip (ds_bpermute). The sums are the same
+// bits as (x_l + x_l^16) + (x_l^32 + x_l^48) in any lane order, since a + b == b + a.
+__device__ __forceinline__ float wave_max16(float x) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+}
+__device__ __forceinline__ float wave_sum16(float x) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+
 // gelu_tanh, src/layers/linear.jl:61-68, in f32, and its analytic derivative
 __device__ __forceinline__ float gelu_f(float x) {
   const float k = 0.7978845608028654f;  // sqrt(Float32(2 / pi))

@@ -265,11 +265,16 @@ def test_attention_argument_errors():
     L = _lib.lib()
     fake = ctypes.c_void_p(4096)
     # head dim, dtype, sizes, NULL operands, workspace: all rejected before any GPU work
-    assert L.reels_hip_attention_fwd(fake, fake, fake, None, 0, 1, 4, 4, 2, 96, _lib.BF16, fake,
-                                     None, None) == -1
-    assert "head_dim" in _err()
-    assert L.reels_hip_attention_fwd(fake, fake, fake, None, 0, 1, 4, 4, 2, 64, _lib.F32, fake,
+    for D in (0, 129, 256):
+        assert L.reels_hip_attention_fwd(fake, fake, fake, None, 0, 1, 4, 4, 2, D, _lib.BF16, fake,
+                                         None, None) == -1
+        assert "head_dim" in _err()
+    assert L.reels_hip_attention_fwd(fake, fake, fake, None, 0, 1, 4, 4, 2, 64, 7, fake,
                                      None, None) == -2
+    # f32 counts 4 bytes an element in the 2 GiB bound: 2^23 x 2 x 32 x 4 = 2^31
+    assert L.reels_hip_attention_fwd(fake, fake, fake, None, 0, 1, 1 << 23, 4, 2, 32, _lib.F32,
+                                     fake, None, None) == -1
+    assert "2 GiB" in _err()
     assert L.reels_hip_attention_fwd(fake, fake, fake, None, 0, -1, 4, 4, 2, 64, _lib.BF16, fake,
                                      None, None) == -1
     assert L.reels_hip_attention_fwd(None, fake, fake, None, 0, 1, 4, 4, 2, 64, _lib.BF16, fake,

@@ -30,21 +30,29 @@ def _inputs(B, Sq, Sk, H, D, seed, dt="bf16"):
     q, k, v, dy = f(B, Sq, H, D), f(B, Sk, H, D), f(B, Sk, H, D), f(B, Sq, H, D)
     if dt == "bf16":
         return tuple(oracle.f32_to_bf16(a) for a in (q, k, v, dy))
+    if dt == "f32":
+        return q, k, v, dy
     return tuple(a.astype(np.float16).view(np.uint16) for a in (q, k, v, dy))
 
 
 def _dev(a, d, dt):
     import torch
+    if dt == "f32":
+        return torch.from_numpy(a).to(d)
     t = to_dev(a, d)  # bf16 view of the bits
     return t if dt == "bf16" else t.view(torch.float16)
 
 
 def _bits(t):
     import torch
+    if t.dtype == torch.float32:
+        return t.cpu().numpy()
     return bf16_bits(t.view(torch.bfloat16) if t.dtype == torch.float16 else t)
 
 
 def _vals(bits, dt):
+    if dt == "f32":
+        return bits
     return oracle.bf16_to_f32(bits) if dt == "bf16" else bits.view(np.float16).astype(np.float32)
 
 
@@ -61,7 +69,7 @@ def _run(B, Sq, Sk, H, D, causal=False, mask=None, dt="bf16", seed=0, backward=T
     torch.cuda.synchronize()
     out = _vals(_bits(res.output), dt)
     lse = res.cache.logsumexp.cpu().numpy()
-    elt = "bf16" if dt == "bf16" else "f16"
+    elt = dt
     ro, rl = oracle.attention_forward(q, k, v, mask=mask, causal=causal, elt=elt)
     grads = None
     if backward:
@@ -195,8 +203,11 @@ def test_attention_argument_errors(dev):
         memory_efficient_attention(q, q, q, query_block=0)
     with pytest.raises(ValueError, match="mask shape differs"):
         memory_efficient_attention(q, q, q, mask=torch.ones(3, 4, dtype=torch.bool))
-    with pytest.raises(ValueError, match="head_dim must be 64 or 128"):
-        x = torch.zeros(1, 4, 2, 32, device=dev, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="head_dim must be between 1 and 128"):
+        x = torch.zeros(1, 4, 2, 160, device=dev, dtype=torch.bfloat16)
+        memory_efficient_attention(x, x, x)
+    with pytest.raises(TypeError, match="share one dtype"):
+        x = torch.zeros(1, 4, 2, 64, device=dev, dtype=torch.float64)
         memory_efficient_attention(x, x, x)
 
 
@@ -246,3 +257,62 @@ def test_attention_wan14b_self_attention_full_size(dev):
     assert np.max(np.abs(cat(got["lse"]) - cat(ref["lse"]))) <= 1e-4
     for n in ("dq", "dk", "dv"):
         assert_parity(cat(got[n]), cat(ref[n]), f"full-size {n}", tol=GTOL)
+
+
+# f32 tensors and head dims other than 64 / 128 run on the generic kernels (attention_g.hip):
+# every product and sum in f32 with the probabilities unrounded, so f32 results meet an f32 bar
+# (normwise 1e-5 against the f64 oracle, lse 1e-5) and 16-bit results the bars of the tuned
+# kernels above (the correction sum(dy .* out) reads the rounded output, as the reference's).
+GENERIC = [
+    # B, Sq, Sk, H, D, causal, masked, dtype
+    (1, 200, 300, 2, 128, False, False, "f32"),
+    (2, 130, 70, 3, 64, True, True, "f32"),
+    (1, 77, 512, 2, 40, False, False, "f32"),    # UMT5-like head dim, text keys
+    (1, 97, 129, 2, 80, True, False, "bf16"),
+    (2, 65, 100, 1, 100, False, True, "f16"),
+    (1, 33, 47, 3, 32, False, False, "bf16"),
+    (1, 1, 5, 1, 7, False, False, "f32"),        # odd head dim, one query
+]
+
+
+@pytest.mark.parametrize("B,Sq,Sk,H,D,causal,masked,dt", GENERIC)
+def test_attention_generic_parity(dev, B, Sq, Sk, H, D, causal, masked, dt):
+    mask = None
+    if masked:
+        rng = np.random.default_rng(200 + Sq)
+        mask = rng.random((Sq, Sk)) < 0.7
+        mask[:, 0] = True
+    out, lse, ro, rl, grads = _run(B, Sq, Sk, H, D, causal, mask, dt, seed=Sq * 3 + Sk)
+    what = f"generic {B}x{Sq}x{Sk}x{H}x{D} causal={causal} masked={masked} {dt}"
+    if dt == "f32":
+        assert_parity(out, ro, f"{what} out", tol=1e-5)
+        assert np.max(np.abs(lse - rl)) <= 1e-5, f"{what} lse: {np.max(np.abs(lse - rl)):.3e}"
+        (dq, dk, dv), (rq, rk, rv) = grads
+        for name, a, r in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+            assert_parity(a, r, f"{what} {name}", tol=1e-5)
+    else:
+        _check_fwd(out, lse, ro, rl, what)
+        _check_bwd(grads, what)
+
+
+def test_attention_generic_no_visible_key_and_no_keys(dev):
+    """The generic kernels' edge cases: a query that sees no key gets NaN output and lse and adds
+    nothing to the gradients; without keys the output is NaN, lse -Inf and dk, dv are empty."""
+    import torch
+    from reels_amd import memory_efficient_attention, memory_efficient_attention_backward
+    Sq, Sk = 20, 33
+    mask = np.ones((Sq, Sk), bool)
+    mask[5] = False
+    out, lse, ro, rl, grads = _run(1, Sq, Sk, 2, 48, mask=mask, dt="f32", seed=9)
+    assert np.isnan(out[0, 5]).all() and np.isnan(lse[0, :, 5]).all()
+    keep = np.arange(Sq) != 5
+    assert_parity(out[:, keep], ro[:, keep], "no-key query: other outputs", tol=1e-5)
+    (dq, dk, dv), (rq, rk, rv) = grads
+    assert np.all(dq[0, 5] == 0)
+    assert_parity(dk, rk, "no-key query: dk", tol=1e-5)
+    d = torch.device("cuda:0")
+    q = torch.randn(1, 4, 1, 24, device=d)
+    kk = torch.zeros(1, 0, 1, 24, device=d)
+    res = memory_efficient_attention(q, kk, kk)
+    torch.cuda.synchronize()
+    assert torch.isnan(res.output).all() and torch.isneginf(res.cache.logsumexp).all()
