@@ -590,10 +590,49 @@ def _cfg2(dev, L, check, gen):
     out["cfg2"] = {"what": "wan2.1-1.3b block projections q/k/v/o 1536 -> 1536, ffn 1536 -> 8960 "
                            "-> 1536 at 32760 tokens, r 32, fwd + dX + dA + dB", "ms": round(ms, 3),
                    "tflops": round(f / (ms * 1e-3) / 1e12, 1),
-                   "frac_of_bf16_peak": round(f / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+                   "frac_of_bf16_peak": round(f / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                   "gemm_vs_vendor": _cfg2_gemms(dev, L, check, projs)}
     del projs
     torch.cuda.empty_cache()
     return out
+
+
+def _cfg2_gemms(dev, L, check, projs, reps=20):
+    """Per config-2 shape: the library's GEMM launches alone (HIP events around each launch,
+    forward and dX) against torch.matmul's bf16 GEMM (the vendor library) on the same operand
+    shapes and layouts: x [M][K] by a [N][K] weight transposed (forward), dy [M][N] by the
+    [N][K] weight (dX). us per launch; ratio = vendor time / ours (above 1: ours faster)."""
+    import torch
+    from reels_amd import _lib
+    res = {}
+    for name in ("self_attn.q", "ffn.0", "ffn.2"):
+        pr = next(p for p in projs if p.name == name)
+        t = {}
+        for mode, fn, args in (("fwd", L.reels_hip_i8lora_fwd, pr.fwd_args),
+                               ("dx", L.reels_hip_i8lora_bwd, pr.bwd_args)):
+            call = lambda: check("reels_hip_i8lora_" + ("fwd" if mode == "fwd" else "bwd"), fn(*args))
+            call()
+            torch.cuda.synchronize()
+            _lib.check("reels_hip_trace_only", L.reels_hip_trace_only(b"gemm_kernel"))
+            _lib.check("reels_hip_trace_start", L.reels_hip_trace_start(8 * reps))
+            for _ in range(reps):
+                call()
+            torch.cuda.synchronize()
+            recs = [ms for (n, ms) in _lib.trace_records() if n.endswith("<0>" if mode == "fwd" else "<1>")]
+            t[mode] = sum(recs) / max(len(recs), 1) * 1e3
+        _lib.check("reels_hip_trace_only", L.reels_hip_trace_only(b""))
+        w = torch.randn((pr.N, pr.K), device=dev).to(torch.bfloat16)
+        vf = _time_ms(lambda: torch.matmul(pr.x, w.t()), reps=reps) * 1e3
+        vd = _time_ms(lambda: torch.matmul(pr.dy, w), reps=reps) * 1e3
+        del w
+        fl = 2.0 * pr.M * pr.K * pr.N
+        res[f"{pr.K}x{pr.N}"] = {
+            "fwd_us": round(t["fwd"], 1), "vendor_fwd_us": round(vf, 1),
+            "fwd_ratio": round(vf / t["fwd"], 3), "dx_us": round(t["dx"], 1),
+            "vendor_dx_us": round(vd, 1), "dx_ratio": round(vd / t["dx"], 3),
+            "fwd_tflops": round(fl / (t["fwd"] * 1e-6) / 1e12, 1),
+            "vendor_fwd_tflops": round(fl / (vf * 1e-6) / 1e12, 1)}
+    return res
 
 
 def _cfg4(dev, L, check, gen):
@@ -640,6 +679,7 @@ def _cfg5a(dev, L, check, gen):
                       "fwd_tflops": round(ff / (fms * 1e-3) / 1e12, 1),
                       "bwd_tflops": round(bf_ / (bms * 1e-3) / 1e12, 1),
                       "fwd_bytes": fb, "bwd_bytes": bb}
+        sk[str(M)].update(_cfg5a_rotating(dev, L, check, gen, M, K, N, fb))
         del pr
     out["cfg5a"] = {"what": "cross-attention K/V projection 5120 -> 5120, r 32, at 77 / 333 / 512 "
                             "text tokens; bytes = 2MK + NK + 4N + 2MN + 2Mr (fwd), 2MN + NK + 4N "
@@ -647,6 +687,33 @@ def _cfg5a(dev, L, check, gen):
                             "the same x by a bf16 weight (twice the weight bytes, no scales or LoRA)",
                     "tokens": sk}
     return out
+
+
+def _cfg5a_rotating(dev, L, check, gen, M, K, N, fb, nw=12, reps=48):
+    """The forward over a rotating set of nw weights (12 x 26 MB int8 = 315 MB, above the 256 MB
+    last-level cache, so each call reads its weight from HBM), against torch.matmul over 12 bf16
+    weights (629 MB) of the same shape."""
+    import torch
+    prs = [Projection("cross_kv", K, N, M, RANK, dev, gen) for _ in range(nw)]
+    i = [0]
+
+    def ours():
+        check("reels_hip_i8lora_fwd", L.reels_hip_i8lora_fwd(*prs[i[0] % nw].fwd_args))
+        i[0] += 1
+    fms = _time_ms(ours, reps=reps, warmup=nw)
+    x = prs[0].x
+    ws = [torch.randn((N, K), device=dev).to(torch.bfloat16) for _ in range(nw)]
+
+    def vend():
+        torch.matmul(x, ws[i[0] % nw].t())
+        i[0] += 1
+    vms = _time_ms(vend, reps=reps, warmup=nw)
+    del prs, ws
+    torch.cuda.empty_cache()
+    return {"rotating_fwd_us": round(fms * 1e3, 2), "rotating_vendor_us": round(vms * 1e3, 2),
+            "rotating_fwd_gbs": round(fb / (fms * 1e-3) / 1e9, 1),
+            "rotating_note": f"{nw} weights in turn (int8 {nw * N * K / 1e6:.0f} MB, vendor bf16 "
+                             f"{2 * nw * N * K / 1e6:.0f} MB): weight reads from HBM"}
 
 
 def configs_cpu_baseline(configs):

@@ -113,15 +113,27 @@ __device__ __forceinline__ float wave_sum16(float x) {
   return __uint_as_float(q[0]) + __uint_as_float(q[1]);
 }
 
+// tanh(u) from one exponential and one reciprocal: |t| = 1 - 2 / (1 + 2^(2 |u| log2 e)) with the
+// sign of u (v_exp_f32 and v_rcp_f32, each within 1 ulp; no overflow path: a huge |u| gives
+// 2 / inf = 0, |t| = 1; NaN stays NaN). Within 2^-23 of tanh(u) absolute, so 1 + t and 1 - t^2
+// below carry the same cancellation as with a correctly rounded tanh (for u << 0, 1 + t is
+// rounded near -1 in both). About 6 VALU operations against ~25 for the libm tanhf, whose range
+// reduction made the GELU passes VALU-bound.
+__device__ __forceinline__ float tanh_f(float u) {
+  const float e = __builtin_amdgcn_exp2f(fabsf(u) * 2.8853900817779268f);  // 2 log2(e)
+  const float m = fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + e), 1.0f);
+  return copysignf(m, u);
+}
+
 // gelu_tanh, src/layers/linear.jl:61-68, in f32, and its analytic derivative
 __device__ __forceinline__ float gelu_f(float x) {
   const float k = 0.7978845608028654f;  // sqrt(Float32(2 / pi))
   const float inner = x + 0.044715f * (x * x * x);
-  return 0.5f * x * (1.0f + tanhf(k * inner));
+  return 0.5f * x * (1.0f + tanh_f(k * inner));
 }
 __device__ __forceinline__ float gelu_grad_f(float x) {
   const float k = 0.7978845608028654f, a = 0.044715f;
-  const float t = tanhf(k * (x + a * x * x * x));
+  const float t = tanh_f(k * (x + a * x * x * x));
   return 0.5f * (1.0f + t) + 0.5f * x * (1.0f - t * t) * k * (1.0f + 3.0f * a * x * x);
 }
 template <int ELT> struct Elt;
