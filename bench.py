@@ -514,16 +514,21 @@ class Chain:
                 dA = torch.empty((K, r), dtype=torch.float32, device=dev)
                 dB = torch.empty((r, N), dtype=torch.float32, device=dev)
                 self.keep.append((W, A, B, y, h, gl, dA, dB))
+                gx = self.links[-1]["y"] if j == 5 else None  # ffn.2's input is gelu(ffn.0's y)
                 self.links.append(dict(
-                    K=K, N=N, gelu=j == 4, x=cur, y=y, gl=gl,
+                    K=K, N=N, gelu=j == 4, after_gelu=j == 5, x=cur, y=y, gl=gl,
                     fwd=(p(cur), p(W.values), p(W.scales), p(A), p(B), None, M, K, N, r, c, p(y),
                          p(h), p(self.wsf), wsf, self.st),
                     bwd=lambda dy, dx, x=cur, W=W, A=A, B=B, h=h, dA=dA, dB=dB, K=K, N=N: (
                         p(dy), p(x), p(h), p(W.values), p(W.scales), p(A), p(B), M, K, N, r, c,
-                        p(dx), p(dA), p(dB), p(self.wsb), wsb, self.st)))
+                        p(dx), p(dA), p(dB), p(self.wsb), wsb, self.st),
+                    bwd_gelu=lambda dy, dx, x=cur, W=W, A=A, B=B, h=h, dA=dA, dB=dB, K=K, N=N, gx=gx: (
+                        p(dy), p(x), p(h), p(W.values), p(W.scales), p(A), p(B), p(gx), M, K, N,
+                        r, c, p(dx), p(dA), p(dB), None, p(self.wsb), wsb, self.st)))
                 cur = gl if j == 4 else y
-        # the backward's buffer sequence, fixed once: dy of each link and its dx buffer
-        self.plan = []
+        # the backward's buffer sequence, fixed once: dy of each link and its dx buffer; with the
+        # GELU's pullback as a separate call (plan_sep) or fused into ffn.2's dX (plan)
+        self.plan_sep, self.plan = [], []
         gd = self.gout
         for lk in reversed(self.links):
             pre = None
@@ -532,18 +537,30 @@ class Chain:
                 pre = (p(lk["y"]), p(gd), p(g2), M * lk["N"])
                 gd = g2
             dx = next(t for t in pool[lk["K"]] if t is not gd)
-            self.plan.append((lk, pre, lk["bwd"](gd, dx)))
+            self.plan_sep.append((lk, pre, lk["bwd"](gd, dx)))
+            gd = dx
+        gd = self.gout
+        for lk in reversed(self.links):
+            dx = next(t for t in pool[lk["K"]] if t is not gd)
+            self.plan.append((lk, lk["bwd_gelu"](gd, dx) if lk["after_gelu"] else lk["bwd"](gd, dx)))
             gd = dx
         self.flops = layers * sum(linear_flops(M, K, N, r) for (K, N) in shapes)
 
-    def step(self, L, check):
+    def step(self, L, check, fused=True):
         for lk in self.links:
             check("reels_hip_i8lora_fwd", L.reels_hip_i8lora_fwd(*lk["fwd"]))
             if lk["gelu"]:
                 check("reels_hip_gelu_tanh", L.reels_hip_gelu_tanh(
                     ctypes.c_void_p(lk["y"].data_ptr()), ctypes.c_void_p(lk["gl"].data_ptr()),
                     self.M * lk["N"], self.st))
-        for (lk, pre, args) in self.plan:
+        if fused:
+            for (lk, args) in self.plan:
+                if lk["after_gelu"]:
+                    check("reels_hip_i8lora_bwd_gelu", L.reels_hip_i8lora_bwd_gelu(*args))
+                else:
+                    check("reels_hip_i8lora_bwd", L.reels_hip_i8lora_bwd(*args))
+            return
+        for (lk, pre, args) in self.plan_sep:
             if pre is not None:
                 check("reels_hip_gelu_tanh_bwd", L.reels_hip_gelu_tanh_bwd(*pre, self.st))
             check("reels_hip_i8lora_bwd", L.reels_hip_i8lora_bwd(*args))
@@ -640,9 +657,12 @@ def _cfg4(dev, L, check, gen):
     out = {}
     ch = Chain(dev, gen)
     ms = _time_ms(lambda: ch.step(L, check), reps=3, warmup=1)
+    ms_sep = _time_ms(lambda: ch.step(L, check, fused=False), reps=3, warmup=1)
     out["cfg4"] = {"what": "30 wan2.1-1.3b layers (q -> k -> v -> o -> ffn.0 -> gelu_tanh -> "
                            "ffn.2) at 32760 tokens, r 32: one forward then one backward through "
-                           "the chain (dX chained, dA and dB per linear)", "ms": round(ms, 2),
+                           "the chain (dX chained, dA and dB per linear); the GELU's pullback "
+                           "fused into ffn.2's dX (reels_hip_i8lora_bwd_gelu)", "ms": round(ms, 2),
+                   "ms_separate_gelu_pullback": round(ms_sep, 2),
                    "tflops": round(ch.flops / (ms * 1e-3) / 1e12, 1),
                    "frac_of_bf16_peak": round(ch.flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
                    "flops": ch.flops}

@@ -213,6 +213,29 @@ int reels_hip_gelu_tanh_bwd(const void* x, const void* dy, void* dx, int64_t n, 
 int reels_hip_gelu_tanh_bwd_f16(const void* x, const void* dy, void* dx, int64_t n, void* stream);
 
 /*
+ * The backward of the Wan FFN's second projection with the GELU's pullback before it,
+ * transformer.jl:289-292 (ffn.0 -> gelu_tanh -> ffn.2), in one call. No single counterpart in the
+ * reference (its FFN pullback calls the linear's, then gelu_tanh's, linear.jl:61-68, in turn);
+ * the results are those of the two calls, bit for bit: reels_hip_i8lora_bwd_bias for the second
+ * projection (dbias may be NULL) with dx replaced by gelu_tanh_bwd(gx, dx), gx [M][K] the
+ * GELU's input (the first projection's y). Where dX runs on the dequantized-weight GEMM without
+ * a split reduction (many tokens, K and N multiples of 64, 16-byte aligned buffers) the pullback
+ * runs in the GEMM's epilogue (the product is neither stored nor read back);
+ * elsewhere that pass runs after it. Workspace as for reels_hip_i8lora_bwd. _f16: binary16
+ * operands, as reels_hip_i8lora_bwd_f16.
+ */
+int reels_hip_i8lora_bwd_gelu(const void* dy, const void* x, const void* h, const int8_t* q,
+                              const float* scales, const void* A, const void* B, const void* gx,
+                              int64_t M, int64_t K, int64_t N, int64_t r, float lora_scale,
+                              void* dx, float* dA, float* dB, float* dbias, void* workspace,
+                              size_t ws_bytes, void* stream);
+int reels_hip_i8lora_bwd_gelu_f16(const void* dy, const void* x, const void* h, const int8_t* q,
+                                  const float* scales, const void* A, const void* B,
+                                  const void* gx, int64_t M, int64_t K, int64_t N, int64_t r,
+                                  float lora_scale, void* dx, float* dA, float* dB, float* dbias,
+                                  void* workspace, size_t ws_bytes, void* stream);
+
+/*
  * fp32 compute, the reference's Float32 path with int8 frozen weights (_dequantize_for_compute
  * with T = Float32, src/layers/quantization.jl:61-64, and lora_forward / lora_backward in
  * Float32, src/layers/lora.jl:56-118). Every operand, intermediate and result is f32:

@@ -21,6 +21,7 @@ from .layers import (  # noqa: F401
     gelu_tanh,
     gelu_tanh_backward,
     i8lora_backward,
+    i8lora_backward_gelu,
     i8lora_forward,
     linear,
     lora_backward,

@@ -22,6 +22,10 @@ struct GemmArgs {
   // reduction pass sums them in split order, adds the bias and rounds once
   int ksplit;
   float* part;
+  // bfgemm only, without a split reduction: the GELU's pullback fused into the epilogue,
+  // out = rnd(rnd(sum) * gelu_tanh'(gx)) with gx [M][Ncols] the GELU's input (the same bits as
+  // gelu_bwd_kernel on the stored product), when gx != nullptr
+  const uint16_t* gx;
 };
 
 // mode 0 = FWD (out = s * act q^T + c L R^T + bias), 1 = DX (out = act q + c L R^T, or
@@ -37,8 +41,10 @@ bool bfgemm_supported(int64_t M, int64_t Ncols, int64_t Kred);
 // reduction splits for token counts whose 256 x 256 tiles leave most CUs idle (1 = none): about
 // one round of 256 workgroups, at least 4 reduction steps of 64 per split
 int bfgemm_splits(int64_t M, int64_t Ncols, int64_t Kred);
-// mode only labels the trace record ("bfgemm_kernel<0>" forward, "<1>" dX)
+// mode only labels the trace record ("bfgemm_kernel<0>" forward, "<1>" dX). a.gx needs
+// a.ksplit <= 1 and 16-byte aligned buffers (bfgemm_fuses_gelu)
 int launch_bfgemm(int mode, int elt, const GemmArgs& a, const uint16_t* wd, hipStream_t st);
+bool bfgemm_fuses_gelu(const GemmArgs& a);
 
 // wd[n][k] = deq(q[n][k], s[n]) in element type elt (bf16: bf16(fl32(q s)); f16: f16(q f16(s))),
 // q [N][K] row stride ldq (K % 16 == 0)

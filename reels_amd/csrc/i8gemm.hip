@@ -587,10 +587,15 @@ constexpr int GM = 4;
 // operands with k = 8 (l / 16) + (0..7) (any k order shared by the two operands gives the same
 // sum); D register v of lane l is output column 4 (l / 16) + v, token l % 16 of the tile.
 // SPLIT: the workgroup takes one of a.ksplit reduction ranges of its tile and writes an f32
-// partial (a separate instantiation, so the unsplit kernel's registers stay as they are)
-template <int ELT, bool SPLIT>
+// partial (a separate instantiation, so the unsplit kernel's registers stay as they are).
+// EPI (unsplit only): 0 plain; 2 writes out = rnd(rnd(sum) * gelu_tanh'(gx)), the GELU's pullback
+// of the product, from the rounded 16-bit values the plain kernel would store, so the bits equal
+// the separate pass. (A forward epilogue writing gelu(out) as well measured slower than the
+// separate GELU pass: its VALU work runs while the matrix cores idle, the pass's overlaps HBM.)
+template <int ELT, bool SPLIT, int EPI = 0>
 __global__ __launch_bounds__(512)
 void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int tiles_m) {
+  static_assert(EPI == 0 || !SPLIT, "the GELU epilogues run on the unsplit kernel");
   using E = Elt<ELT>;
   typedef typename E::v8 V8;
   using namespace bfg;
@@ -799,6 +804,7 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
     braw[ti] = u32x2{0u, 0u};
     if (a.bias != nullptr && nb < Ncols) braw[ti] = *reinterpret_cast<const u32x2*>(a.bias + nb);
   }
+
   // acc + c lor + bias, rounded once, into the staging tile
   auto finish = [&](int ti, const f32x4* lor) {
     const int nloc = wn * 64 + ti * 16 + lq * 4;  // this lane's four output columns
@@ -876,6 +882,34 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
   if constexpr (SPLIT) return;  // the partials went straight to global memory
   // each wave stores the region it staged itself (128 rows x 64 columns: 128-byte row segments,
   // whole cache lines), so no barrier waits for the other waves
+  if constexpr (EPI == 2) {
+    // the GELU inputs of the 16 row segments this lane stores, all loaded at once once the
+    // accumulators are dead (earlier, with them live, the registers spill), then the products
+    u32x4 gv[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int row = wm * 128 + 8 * i + (lane >> 3), c = wn * 8 + (lane & 7);
+      const int64_t m = m0 + row, n = n0 + c * 8;
+      gv[i] = u32x4{0u, 0u, 0u, 0u};
+      if (m < M && n < Ncols) gv[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.gx + m * Ncols + n));
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's staging writes are done
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int row = wm * 128 + 8 * i + (lane >> 3), c = wn * 8 + (lane & 7);
+      const int64_t m = m0 + row, n = n0 + c * 8;
+      if (m < M && n < Ncols) {
+        const u32x4 d = *reinterpret_cast<const u32x4*>(srow(row) + ((c ^ (row & 31)) << 4));
+        u32x4 o;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          o[k] = E::bits(E::lo(d[k]) * gelu_grad_f(E::lo(gv[i][k]))) |
+                 (E::bits(E::hi(d[k]) * gelu_grad_f(E::hi(gv[i][k]))) << 16);
+        *reinterpret_cast<u32x4*>(a.out + m * Ncols + n) = o;
+      }
+    }
+    return;
+  }
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's staging writes are done
 #pragma unroll 4
   for (int i = 0; i < 16; ++i) {
@@ -931,6 +965,11 @@ int bfgemm_splits(int64_t M, int64_t Ncols, int64_t Kred) {
   return s < 2 ? 1 : (int)s;
 }
 
+bool bfgemm_fuses_gelu(const GemmArgs& a) {
+  const auto al = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  return a.ksplit <= 1 && a.Ncols % 8 == 0 && al(a.out) && al(a.gx);
+}
+
 bool bfgemm_supported(int64_t M, int64_t Ncols, int64_t Kred) {
   (void)M;  // any token count: launch_bfgemm splits the tokens into chunks (below)
   return Kred % bfg::BK == 0 && Ncols % 16 == 0 && Ncols * Kred * 2 < ((int64_t)1 << 31);
@@ -943,7 +982,8 @@ int launch_bfgemm(int mode, int elt, const GemmArgs& a, const uint16_t* wd, hipS
   static hipError_t attr_err = hipSuccess;
   std::call_once(once, [&] {
     const void* ks[] = {(const void*)bfgemm_kernel<REELS_HIP_BF16, false>, (const void*)bfgemm_kernel<REELS_HIP_F16, false>,
-                        (const void*)bfgemm_kernel<REELS_HIP_BF16, true>, (const void*)bfgemm_kernel<REELS_HIP_F16, true>};
+                        (const void*)bfgemm_kernel<REELS_HIP_BF16, true>, (const void*)bfgemm_kernel<REELS_HIP_F16, true>,
+                        (const void*)bfgemm_kernel<REELS_HIP_BF16, false, 2>, (const void*)bfgemm_kernel<REELS_HIP_F16, false, 2>};
     for (const void* k : ks)
       if (attr_err == hipSuccess) attr_err = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, bfg::LDS);
   });
@@ -953,6 +993,8 @@ int launch_bfgemm(int mode, int elt, const GemmArgs& a, const uint16_t* wd, hipS
   // activations reach 2 GiB run as consecutive launches over token chunks (multiples of the
   // 256-token tile) with the activation, output and L pointers advanced.
   const int64_t chunk = ((((int64_t)1 << 31) - 1) / (a.Kred * 2)) / bfg::BM * bfg::BM;
+  if (a.gx && !bfgemm_fuses_gelu(a))
+    return fail(REELS_HIP_EINVAL, "bfgemm: the GELU epilogue needs the unsplit kernel and 16-byte aligned buffers");
   if (a.ksplit > 1) {
     // split reduction: few tiles (one chunk of tokens), partials in a.part, then the reduction pass
     if (a.M > chunk || a.part == nullptr || a.Ncols % 4 != 0)
@@ -971,10 +1013,13 @@ int launch_bfgemm(int mode, int elt, const GemmArgs& a, const uint16_t* wd, hipS
     c.act = a.act + m0 * a.Kred;
     c.out = a.out + m0 * a.Ncols;
     if (a.L) c.L = a.L + m0 * a.rp;
+    if (a.gx) c.gx = a.gx + m0 * a.Ncols;
     const int tn = (int)ceil_div(c.Ncols, bfg::BN), tm = (int)ceil_div(c.M, bfg::BM);
     { TraceScope _ts(st, mode == 0 ? "bfgemm_kernel<0>" : "bfgemm_kernel<1>");
       with_elt(elt, [&](auto e) {
-        bfgemm_kernel<decltype(e)::value, false><<<tn * tm, bfg::NT, bfg::LDS, st>>>(c, wd, tn, tm);
+        constexpr int EL = decltype(e)::value;
+        if (c.gx) bfgemm_kernel<EL, false, 2><<<tn * tm, bfg::NT, bfg::LDS, st>>>(c, wd, tn, tm);
+        else bfgemm_kernel<EL, false><<<tn * tm, bfg::NT, bfg::LDS, st>>>(c, wd, tn, tm);
       }); }
     if (int rc = check_launch("bfgemm_kernel")) return rc;
   }

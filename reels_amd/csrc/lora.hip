@@ -790,9 +790,10 @@ __global__ __launch_bounds__(256) void gelu_kernel(const uint16_t* __restrict__ 
     y[i] = (uint16_t)E::bits(gelu_f(E::to_f32(x[i])));
 }
 template <int ELT>
+// (dx may be dy: each element is read before the same thread writes it)
 __global__ __launch_bounds__(256) void gelu_bwd_kernel(const uint16_t* __restrict__ x,
-                                                       const uint16_t* __restrict__ dy,
-                                                       uint16_t* __restrict__ dx, int64_t n, int vec) {
+                                                       const uint16_t* dy, uint16_t* dx, int64_t n,
+                                                       int vec) {
   using E = Elt<ELT>;
   const int64_t nv = vec ? n / 8 : 0;
   const int64_t step = (int64_t)gridDim.x * blockDim.x;
@@ -1344,7 +1345,7 @@ static int i8lora_bwd_impl(int elt, const char* fn, const void* dy, const void* 
                            const int8_t* q, const float* scales, const void* A, const void* B,
                            int64_t M, int64_t K, int64_t N, int64_t r, float lora_scale, void* dx,
                            float* dA, float* dB, float* dbias, void* workspace, size_t ws_bytes,
-                           void* stream) {
+                           void* stream, const void* gx = nullptr, bool* gelu_fused = nullptr) {
   clear_error();
   if (M < 0 || K <= 0 || N <= 0 || r < 0 || r > 4096)
     return fail(REELS_HIP_EINVAL, std::string(fn) + ": " "need M >= 0, K > 0, N > 0, 0 <= r <= 4096");
@@ -1456,6 +1457,9 @@ static int i8lora_bwd_impl(int elt, const char* fn, const void* dy, const void* 
       g.bias = nullptr; g.out = static_cast<uint16_t*>(dx);
       g.M = M; g.Ncols = K; g.Kred = N; g.ldq = N; g.rp = r > 0 ? p.rp : 0; g.c = lora_scale;
       g.ksplit = p.ksb; g.part = reinterpret_cast<float*>(ws + w.kp);
+      g.gx = static_cast<const uint16_t*>(gx);
+      if (g.gx && !bfgemm_fuses_gelu(g)) g.gx = nullptr;
+      if (g.gx && gelu_fused) *gelu_fused = true;
       if ((rc = launch_bfgemm(1, elt, g, wt, st))) return rc;
     }
   } else if (r > 0 || (dx && !f16)) {
@@ -1610,6 +1614,48 @@ extern "C" int reels_hip_i8lora_bwd_f16(const void* dy, const void* x, const voi
                                         void* workspace, size_t ws_bytes, void* stream) {
   return i8lora_bwd_impl(REELS_HIP_F16, "reels_hip_i8lora_bwd_f16", dy, x, h, q, scales, A, B, M, K,
                          N, r, lora_scale, dx, dA, dB, nullptr, workspace, ws_bytes, stream);
+}
+
+// The second FFN projection's backward with the GELU's pullback (transformer.jl:289-292,
+// linear.jl:61-68): fused into the dX GEMM's epilogue where dX runs on the unsplit
+// dequantized-weight GEMM, otherwise the separate pass after it (the same bits either way).
+static int i8lora_bwd_gelu_impl(int elt, const char* fn, const void* dy, const void* x,
+                                const void* h, const int8_t* q, const float* scales, const void* A,
+                                const void* B, const void* gx, int64_t M, int64_t K, int64_t N,
+                                int64_t r, float lora_scale, void* dx, float* dA, float* dB,
+                                float* dbias, void* workspace, size_t ws_bytes, void* stream) {
+  if (M > 0 && dx && !gx) {
+    clear_error();
+    return fail(REELS_HIP_EINVAL, std::string(fn) + ": NULL gx with dx");
+  }
+  bool fused = false;
+  if (int rc = i8lora_bwd_impl(elt, fn, dy, x, h, q, scales, A, B, M, K, N, r, lora_scale, dx, dA,
+                               dB, dbias, workspace, ws_bytes, stream, dx ? gx : nullptr, &fused))
+    return rc;
+  if (fused || M == 0 || !dx) return REELS_HIP_OK;
+  return gelu_bwd_impl(elt, fn, gx, dx, dx, M * K, stream);
+}
+
+extern "C" int reels_hip_i8lora_bwd_gelu(const void* dy, const void* x, const void* h,
+                                         const int8_t* q, const float* scales, const void* A,
+                                         const void* B, const void* gx, int64_t M, int64_t K,
+                                         int64_t N, int64_t r, float lora_scale, void* dx,
+                                         float* dA, float* dB, float* dbias, void* workspace,
+                                         size_t ws_bytes, void* stream) {
+  return i8lora_bwd_gelu_impl(REELS_HIP_BF16, "reels_hip_i8lora_bwd_gelu", dy, x, h, q, scales, A,
+                              B, gx, M, K, N, r, lora_scale, dx, dA, dB, dbias, workspace,
+                              ws_bytes, stream);
+}
+
+extern "C" int reels_hip_i8lora_bwd_gelu_f16(const void* dy, const void* x, const void* h,
+                                             const int8_t* q, const float* scales, const void* A,
+                                             const void* B, const void* gx, int64_t M, int64_t K,
+                                             int64_t N, int64_t r, float lora_scale, void* dx,
+                                             float* dA, float* dB, float* dbias, void* workspace,
+                                             size_t ws_bytes, void* stream) {
+  return i8lora_bwd_gelu_impl(REELS_HIP_F16, "reels_hip_i8lora_bwd_gelu_f16", dy, x, h, q, scales,
+                              A, B, gx, M, K, N, r, lora_scale, dx, dA, dB, dbias, workspace,
+                              ws_bytes, stream);
 }
 
 extern "C" int reels_hip_gelu_tanh(const void* x, void* y, int64_t n, void* stream) {

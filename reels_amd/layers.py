@@ -269,6 +269,48 @@ def i8lora_backward(dy, x, weight: QuantizedMatrix, A=None, B=None, lora_scale=1
     return dx, dA, dB
 
 
+def i8lora_backward_gelu(dy, x, gx, weight: QuantizedMatrix, A=None, B=None, lora_scale=1.0,
+                         h=None, want_dA=True, want_dB=True, want_dbias=False):
+    """i8lora_backward of the projection after a GELU, with dx replaced by the GELU's pullback
+    gelu_tanh_backward(gx, dx), gx [M][K] the GELU's input (reels_hip_i8lora_bwd_gelu*: in the
+    dX GEMM's epilogue where that GEMM is unsplit, bit-identical to the two calls). Returns
+    (dgx, dA, dB), and dbias with want_dbias. float32 runs the two calls."""
+    if dy.dim() == 2 and dy.dtype == torch.float32:
+        res = i8lora_backward(dy, x, weight, A, B, lora_scale, h, True, want_dA, want_dB, want_dbias)
+        return (gelu_tanh_backward(gx, res[0]),) + tuple(res[1:])
+    if dy.dim() != 2:
+        raise ValueError(f"dy must be a [M][N] matrix, got shape {tuple(dy.shape)}")
+    M, N = dy.shape
+    Nw, K = weight.values.shape
+    if Nw != N:
+        raise ValueError("DimensionMismatch: dy and weight output dimensions differ")
+    r = _validate(weight, M, K, N, A, B, **{"x ([M][K])": (x, (M, K))})
+    _check_shape(h, (M, r), "h ([M][r])")
+    _check_shape(gx, (M, K), "gx ([M][K])")
+    if gx is None:
+        raise ValueError("gx (the GELU's input) is required")
+    if r and x is None and (want_dA or (want_dB and h is None)):
+        raise ValueError("x is needed for dA and for recomputing h")
+    dt = _act_dtype(dy, "dy")
+    dy = dy.contiguous()
+    weight = _on_activation_device(weight, dy.device)
+    A, B, h, gx = _contig(A, dt, "A"), _contig(B, dt, "B"), _contig(h, dt, "h"), _contig(gx, dt, "gx")
+    x = _contig(x, dt, "x") if x is not None else None
+    dev = dy.device
+    dx = torch.empty((M, K), dtype=dt, device=dev)
+    dA = torch.empty((K, r), dtype=torch.float32, device=dev) if (want_dA and r) else None
+    dB = torch.empty((r, N), dtype=torch.float32, device=dev) if (want_dB and r) else None
+    dbias = torch.empty((N,), dtype=torch.float32, device=dev) if want_dbias else None
+    nbytes = workspace_bytes(M, K, N, r, _lib.WS_BWD, dt)
+    ws = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
+    fn = "reels_hip_i8lora_bwd_gelu" + _ACT_SUFFIX[dt]
+    _lib.check(fn, getattr(_lib.lib(), fn)(
+        _ptr(dy), _ptr(x), _ptr(h), _ptr(weight.values), _ptr(weight.scales), _ptr(A), _ptr(B),
+        _ptr(gx), M, K, N, r, float(lora_scale), _ptr(dx), _ptr(dA), _ptr(dB), _ptr(dbias),
+        _ptr(ws), nbytes, _stream(dev)))
+    return (dx, dA, dB, dbias) if want_dbias else (dx, dA, dB)
+
+
 # ---- reference-named layer API ----------------------------------------------------------------
 def _weight_mul(weight: QuantizedMatrix, x: torch.Tensor) -> torch.Tensor:
     """_weight_mul (quantization.jl:73-74): x deq(W)^T (deq(W) lives only in the call's
