@@ -186,14 +186,19 @@ template <> struct Elt<REELS_HIP_F16> {
   static __device__ __forceinline__ uint32_t pack2_fast(float a, float b) { return pack2(a, b); }
   static __device__ __forceinline__ v8 as8(u32x4 v) { return __builtin_bit_cast(f16x8, v); }
   // int8 -> binary16 is exact (|q| <= 127 fits the 11-bit significand)
+  // exact: 1024 + (q + 128) is a binary16 value (ulp 1 on [1024, 2048)). Each code byte with its
+  // sign bit flipped (q + 128) becomes the low mantissa byte under the exponent byte of 1024
+  // (0x64), then one packed binary16 subtraction of 1152 per two codes leaves q
   static __device__ __forceinline__ v8 from_i8x8(uint32_t l, uint32_t h) {
-    v8 r;
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const uint32_t e = 0x64646464u, ul = l ^ 0x80808080u, uh = h ^ 0x80808080u;
+    const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const uint32_t w[4] = {__builtin_amdgcn_perm(e, ul, 0x04010400u), __builtin_amdgcn_perm(e, ul, 0x04030402u),
+                           __builtin_amdgcn_perm(e, uh, 0x04010400u), __builtin_amdgcn_perm(e, uh, 0x04030402u)};
+    u32x4 r;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      r[i] = (_Float16)(float)(int8_t)((l >> (8 * i)) & 0xffu);
-      r[4 + i] = (_Float16)(float)(int8_t)((h >> (8 * i)) & 0xffu);
-    }
-    return r;
+    for (int i = 0; i < 4; ++i) r[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, w[i]) - bias);
+    return __builtin_bit_cast(v8, r);
   }
   static __device__ __forceinline__ f32x4 mfma16(v8 a, v8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);

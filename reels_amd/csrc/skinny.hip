@@ -696,8 +696,13 @@ __global__ __launch_bounds__(256) void skinny_clear_kernel(uint32_t* p, int n) {
 // 16 To tokens) are loaded by all 8 waves into registers rw_depth steps ahead and written to an LDS
 // double buffer one step ahead, where every wave of the block reads them; each wave's weight
 // goes straight from memory into its registers, also rw_depth steps ahead.
-//   FWD: the lane holds 16 code bytes of one weight row (k = 16 g .. 16 g + 15 of the chunk) and
-//        feeds MFMA step e with k = 16 g + 8 e + (0..7); the activations use the same k.
+//   FWD: the block's codes of a step (64 NI rows x 128 bytes) are loaded as whole 128-byte row
+//        segments, 8 rows per wave instruction (waves w and w + 4 load alternate 8-row groups of
+//        their 16 NI rows), and written to an LDS ring G + 1 steps ahead of their conversion
+//        (rows' 16-byte units XOR-swizzled by row); a lane then reads 8 codes of row 16 i + l16
+//        at k = 64 par + 16 g + 8 e + (0..7) for MFMA step e, the activations using the same k.
+//        (Loaded straight in that layout, each instruction touched 16 rows' half lines: 15-18%
+//        slower.)
 //   DX:  the wave's [64 n][16 NI k] code tile goes through a per-wave LDS tile and
 //        ds_read_b64_tr_b8 (lane: k = 16 i + l16, n = 32 e + 8 g + (0..7)), each code scaled by
 //        s[n] from a table of the block's scales in LDS: bf16(fl32(q s[n])) (f16: f16(q f16(s))),
@@ -708,9 +713,24 @@ __global__ __launch_bounds__(256) void skinny_clear_kernel(uint32_t* p, int n) {
 // activations ring in LDS holds 2 G steps, so a group of G steps reads one half while the other
 // half is written for the next group, and the waves meet at one barrier per group.
 // (measured: dX, whose loop is heavier on the VALU, runs best with four steps in flight and a
-// barrier every step or two)
-constexpr int rw_group(int To, int MODE) { return MODE == 1 ? (To <= 2 ? 2 : 1) : (To <= 2 ? 4 : 2); }
-constexpr int rw_depth(int To, int MODE) { return MODE == 1 ? 4 : 2 * rw_group(To, MODE); }
+// barrier every step or two). The FWD tile of 12 MFMA tiles per wave (2 x 6) meets every step:
+// its code ring of 2 G slots then fits the LDS beside the activations (and 3 x 4 does not fit
+// the registers at G = 1 nor the LDS at G = 2: not a FWD candidate).
+constexpr int rw_group(int To, int MODE, int NI) {
+  return MODE == 1 ? (To <= 2 ? 2 : 1) : (To <= 2 ? 4 : (NI * To >= 12 ? 1 : 2));
+}
+constexpr int rw_depth(int To, int MODE) { return MODE == 1 ? 4 : (To <= 2 ? 8 : 4); }
+// FWD weight ring slot: the block's 64 NI rows x 128 code bytes of one step. A wave's load puts 8
+// lanes on each of 8 rows; rw_wrow gives the 8-lane groups that may share a pass of the LDS
+// write (0-7 with 16-23 or 24-31, and so on) rows of different parity, which start in the
+// other half of the banks. The 16-byte unit u of ring row r sits at u ^ rw_wswz(r): the code
+// reads (rows l16 of a 16-row tile, unit 4 par + g) then meet distinct banks in such a pass too.
+constexpr int rw_wslot(int NI) { return 64 * NI * 128; }
+__device__ __forceinline__ int rw_wrow(int lane) {
+  const int q = lane >> 3;
+  return ((q & 1) << 1) | ((q >> 1) & 1) | (q & 4);
+}
+__device__ __forceinline__ int rw_wswz(int row) { return ((row >> 1) & 3) << 1; }
 constexpr int align16(int v) { return (v + 15) & ~15; }
 
 // The 16-byte unit u of activation row r sits at u ^ rw_swz<MODE>(r). A fragment read takes
@@ -729,7 +749,7 @@ __device__ __forceinline__ void rw_acc(const SkArgs& a, int64_t r0, int64_t tok0
                                        uint8_t* smem, f32x4 (&acc)[NI][To]) {
   using E = Elt<ELT>;
   typedef typename E::v8 V8;
-  constexpr int BN = 16 * To, XL = To / 2, SLOT = 2 * BN * 128, G = rw_group(To, MODE), D = rw_depth(To, MODE);
+  constexpr int BN = 16 * To, XL = To / 2, SLOT = 2 * BN * 128, G = rw_group(To, MODE, NI), D = rw_depth(To, MODE);
   constexpr uint32_t OOB = 0x80000000u;
   const int t = threadIdx.x, lane = t & 63;
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -750,14 +770,14 @@ __device__ __forceinline__ void rw_acc(const SkArgs& a, int64_t r0, int64_t tok0
     vx[j] = tok < a.M ? (uint32_t)(tok * a.Kred * 2 + p * 128 + col * 16) : OOB;
     lx[j] = (uint32_t)u * 16u;
   }
-  // weight: FWD row r0 + 16 NI wr + 16 i + l16, bytes 16 g of the chunk; DX row n = lane of the
-  // chunk, bytes r0 + 16 NI wr + 16 i (16 output columns k)
+  // weight: FWD row r0 + 16 NI wr + 8 (2 i + par) + lane / 8, bytes 16 (lane % 8) of the step's
+  // 128; DX row n = lane of the chunk, bytes r0 + 16 NI wr + 16 i (16 output columns k)
   uint32_t vw[NI];
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
     if (MODE == 0) {
-      const int64_t row = r0 + 16 * NI * wr + 16 * i + l16;
-      vw[i] = row < a.Ncols ? (uint32_t)(row * a.ldq + 16 * g + 64 * par) : OOB;
+      const int64_t row = r0 + 16 * NI * wr + 8 * (2 * i + par) + rw_wrow(lane);
+      vw[i] = row < a.Ncols ? (uint32_t)(row * a.ldq + 16 * (lane & 7)) : OOB;
     } else {
       const int64_t col = r0 + 16 * NI * wr + 16 * i;
       vw[i] = col < a.Ncols ? (uint32_t)((64 * par + lane) * a.ldq + col) : OOB;
@@ -768,6 +788,20 @@ __device__ __forceinline__ void rw_acc(const SkArgs& a, int64_t r0, int64_t tok0
   // [64 n][16 NI] code tile after them
   float* stab = reinterpret_cast<float*>(smem + 2 * G * SLOT);
   uint8_t* wt = smem + 2 * G * SLOT + align16((int)a.Kred * 4) + w * (1024 * NI);
+  // FWD: the weight ring of 2 G slots after the activation slots. Step t's codes are written
+  // in step t - G - 1 and read in step t - 1 (converted for the next step's MFMAs), so a group
+  // barrier lies between the writes and the reads, and between the last read of a slot and its
+  // next writes (G steps apart).
+  static_assert(MODE == 1 || D >= G + 2, "the codes of step t arrive before step t - G - 1");
+  uint8_t* wring = smem + 2 * G * SLOT;
+  constexpr int WSLOT = rw_wslot(NI);
+  auto put_w = [&](const u32x4 (&wd)[NI], int slot) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int row = 16 * NI * wr + 16 * i + 8 * par + rw_wrow(lane);
+      *reinterpret_cast<u32x4*>(wring + slot * WSLOT + row * 128 + (((lane & 7) ^ rw_wswz(row)) << 4)) = wd[i];
+    }
+  };
   if constexpr (MODE == 1) {
     for (int i = t; i < (int)a.Kred / 4; i += 64 * sk::NWV)
       reinterpret_cast<f32x4*>(stab)[i] = reinterpret_cast<const f32x4*>(a.s)[i];
@@ -808,11 +842,11 @@ __device__ __forceinline__ void rw_acc(const SkArgs& a, int64_t r0, int64_t tok0
   // wave's LDS tile, each code scaled by s[n]
   auto convert = [&](const u32x4 (&wv)[NI], int s, V8 (&af)[NI][2]) {
     if constexpr (MODE == 0) {
+      // the codes read by read_codes
 #pragma unroll
-      for (int i = 0; i < NI; ++i) {
-        af[i][0] = E::from_i8x8(wv[i][0], wv[i][1]);
-        af[i][1] = E::from_i8x8(wv[i][2], wv[i][3]);
-      }
+      for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) af[i][e] = E::from_i8x8(wv[i][2 * e], wv[i][2 * e + 1]);
     } else {
       // the code tile [64 n][16 NI k] to this wave's LDS tile, then per 16-k tile i and step e the
       // transposed read: providing lane p of a 16-lane group addresses row 32 e + 8 g + p / 2,
@@ -847,10 +881,24 @@ __device__ __forceinline__ void rw_acc(const SkArgs& a, int64_t r0, int64_t tok0
     }
   };
 
+  // FWD: 8 codes of row 16 i + l16 at k = 64 par + 16 g + 8 e (e = 0, 1) of step s from its ring
+  // slot, read before the step's activation fragments (LDS answers in order, and the conversions
+  // interleaved with the first MFMAs wait only for these)
+  auto read_codes = [&](int s, u32x4 (&cv)[NI]) {
+    const uint8_t* ws = wring + (s % (2 * G)) * WSLOT;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int row = 16 * NI * wr + 16 * i + l16;
+      cv[i] = *reinterpret_cast<const u32x4*>(ws + row * 128 + (((4 * par + g) ^ rw_wswz(row)) << 4));
+    }
+  };
+
   // Step s: its activation fragments from LDS, then its MFMAs (k step outermost, so the two
   // products into one accumulator lie NI To MFMAs apart) interleaved with the conversion of step
   // s + 1's codes, so the matrix cores and the VALU work side by side in each wave.
   auto mma_convert = [&](int s, const V8 (&afc)[NI][2], const u32x4 (&wn)[NI], V8 (&afn)[NI][2]) {
+    u32x4 cv[NI];
+    if constexpr (MODE == 0) read_codes(s + 1, cv);
     const uint8_t* xs = smem + (s % (2 * G)) * SLOT + par * (BN * 128);
     const int sw = rw_swz<MODE>(l16);  // the same for every 16-row token tile
     u32x4 xv[2][To];
@@ -862,15 +910,17 @@ __device__ __forceinline__ void rw_acc(const SkArgs& a, int64_t r0, int64_t tok0
         const int unit = MODE == 0 ? 2 * g + e : 4 * e + g;
         xv[e][tt] = *reinterpret_cast<const u32x4*>(xs + (16 * tt + l16) * 128 + ((unit ^ sw) << 4));
       }
-    convert(wn, s + 1, afn);
+    if constexpr (MODE == 0) convert(cv, s + 1, afn);
+    else convert(wn, s + 1, afn);
 #pragma unroll
     for (int e = 0; e < 2; ++e)
 #pragma unroll
       for (int tt = 0; tt < To; ++tt)
 #pragma unroll
         for (int i = 0; i < NI; ++i) acc[i][tt] = E::mfma16(afc[i][e], E::as8(xv[e][tt]), acc[i][tt]);
-    // schedule: the fragment reads, then one MFMA and a few VALU (and for dX LDS) ops in turn
-    __builtin_amdgcn_sched_group_barrier(0x100, 2 * To, 0);
+    // schedule: the fragment reads (and the FWD codes), then one MFMA and a few VALU (and for dX
+    // LDS) ops in turn
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * To + (MODE == 0 ? NI : 0), 0);
 #pragma unroll
     for (int k = 0; k < 2 * NI * To; ++k) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -886,6 +936,7 @@ __device__ __forceinline__ void rw_acc(const SkArgs& a, int64_t r0, int64_t tok0
   auto step = [&](int s, int j, V8 (&afc)[NI][2], V8 (&afn)[NI][2]) {
     mma_convert(s, afc, wq[(j + 1) % D], afn);
     put_x(xr[(j + G) % D], (s + G) % (2 * G));
+    if constexpr (MODE == 0) put_w(wq[(j + G + 1) % D], (s + G + 1) % (2 * G));
     issue(s + D, xr[j], wq[j]);
   };
   // A group's barrier: every wave's writes of the next group's activations are done, and every
@@ -903,8 +954,18 @@ __device__ __forceinline__ void rw_acc(const SkArgs& a, int64_t r0, int64_t tok0
   for (int d = 0; d < D; ++d) issue(d, xr[d], wq[d]);
 #pragma unroll
   for (int d = 0; d < G; ++d) put_x(xr[d], d);
-  group_barrier();  // also publishes the DX scale table, which convert reads
-  convert(wq[0], 0, afa);
+  if constexpr (MODE == 0) {
+#pragma unroll
+    for (int d = 0; d <= G; ++d) put_w(wq[d], d);
+  }
+  group_barrier();  // also publishes the DX scale table (and the FWD codes), which convert reads
+  if constexpr (MODE == 0) {
+    u32x4 cv[NI];
+    read_codes(0, cv);
+    convert(cv, 0, afa);
+  } else {
+    convert(wq[0], 0, afa);
+  }
   // whole units of D steps without a branch inside (a conditional step in the unrolled body
   // makes the compiler drain every load at the loop head), then the last steps
   static_assert(D % G == 0 && D > G && D % 2 == 0, "a unit of D steps holds whole groups");
@@ -1164,7 +1225,8 @@ constexpr int kRwLdsMax = 160 * 1024;
 
 static int rw_lds_bytes(int NI, int To, int mode, int64_t Kred) {
   const int slot = 2 * 16 * To * 128, ta = To <= 4 ? To : To / 2;
-  int v = 2 * rw_group(To, mode) * slot + (mode == 1 ? align16((int)Kred * 4) + 8 * 1024 * NI : 0);
+  const int G = rw_group(To, mode, NI);
+  int v = 2 * G * slot + (mode == 1 ? align16((int)Kred * 4) + 8 * 1024 * NI : 2 * G * rw_wslot(NI));
   v = std::max(v, 8 * NI * (To / 2) * 1024);
   v = std::max(v, skinny_lds(ta));
   v = std::max(v, 8 * 1024 * NI);
@@ -1184,6 +1246,7 @@ static bool rw_choose(int64_t M, int64_t Kred, int64_t Ncols, int rp, int mode, 
     const int64_t tiles = orb * otb, nad = rp > 0 ? lblk * tba : 0;
     if (tiles + nad > kSkinnyTargetBlocks || tiles < kSkinnyTargetBlocks / 2) continue;
     if (rw_lds_bytes(c.NI, c.To, mode, Kred) > kRwLdsMax) continue;
+    if (mode == 0 && c.NI == 3) continue;  // see rw_group
     const int64_t mf = 64 * c.NI * c.To, lds = 128 * c.To, vm = 128 * c.NI + 64 * c.To;
     const int64_t valu = (mode == 1 ? 384 : 192) * c.NI;
     const int64_t cost = std::max(std::max(mf, lds), std::max(vm, valu));
@@ -1351,8 +1414,9 @@ int launch_skinny(int mode, int elt, const SkinnyPlan& p, const uint16_t* act, c
         constexpr int MD = decltype(m)::value;
         if (p.NI == 1 && p.To == 2) attr = launch_rw_t<2, 1, 2, MD, EL>(a, lds, st);
         else if (p.NI == 2 && p.To == 4) attr = launch_rw_t<4, 2, 4, MD, EL>(a, lds, st);
-        else if (p.NI == 3 && p.To == 4) attr = launch_rw_t<4, 3, 4, MD, EL>(a, lds, st);
-        else attr = launch_rw_t<6, 2, 3, MD, EL>(a, lds, st);
+        else if (p.NI == 2 && p.To == 6) attr = launch_rw_t<6, 2, 3, MD, EL>(a, lds, st);
+        else if constexpr (MD == 1) attr = launch_rw_t<4, 3, 4, MD, EL>(a, lds, st);  // 3 x 4: dX only
+        else attr = hipErrorInvalidConfiguration;  // no FWD 3 x 4 plan (rw_choose)
       };
       if (mode == 0) go(std::integral_constant<int, 0>{});
       else go(std::integral_constant<int, 1>{});
