@@ -703,10 +703,13 @@ __global__ __launch_bounds__(256) void skinny_clear_kernel(uint32_t* p, int n) {
 //        at k = 64 par + 16 g + 8 e + (0..7) for MFMA step e, the activations using the same k.
 //        (Loaded straight in that layout, each instruction touched 16 rows' half lines: 15-18%
 //        slower.)
-//   DX:  the wave's [64 n][16 NI k] code tile goes through a per-wave LDS tile and
-//        ds_read_b64_tr_b8 (lane: k = 16 i + l16, n = 32 e + 8 g + (0..7)), each code scaled by
-//        s[n] from a table of the block's scales in LDS: bf16(fl32(q s[n])) (f16: f16(q f16(s))),
-//        the dequantized weight of the large-token dX.
+//   DX:  the block's codes of a step (128 rows n x 64 NI bytes k) are loaded as whole row
+//        segments (flat 16-byte units in order, so each instruction covers 64 NI-byte pieces of
+//        consecutive rows) into the same kind of ring, G + 1 steps ahead; a wave's
+//        [64 n][16 NI k] share reaches the MFMA through ds_read_b64_tr_b8 (lane: k = 16 i + l16,
+//        n = 32 e + 8 g + (0..7)), each code scaled by s[n] from a table of the block's scales in
+//        LDS: bf16(fl32(q s[n])) (f16: f16(q f16(s))), the dequantized weight of the large-token
+//        dX. (Loaded per wave, each instruction took 16 bytes from each of 64 rows.)
 // LDS rows of the activations are 128 bytes (64 bf16), their 16-byte units swizzled per row
 // (rw_swz) so that the fragment reads hit distinct banks.
 // Steps per barrier (G) and steps whose loads are in flight (D, a multiple of G above it): the
@@ -714,8 +717,8 @@ __global__ __launch_bounds__(256) void skinny_clear_kernel(uint32_t* p, int n) {
 // half is written for the next group, and the waves meet at one barrier per group.
 // (measured: dX, whose loop is heavier on the VALU, runs best with four steps in flight and a
 // barrier every step or two). The FWD tile of 12 MFMA tiles per wave (2 x 6) meets every step:
-// its code ring of 2 G slots then fits the LDS beside the activations (and 3 x 4 does not fit
-// the registers at G = 1 nor the LDS at G = 2: not a FWD candidate).
+// its code ring of 2 G slots then fits the LDS beside the activations. (A 3 x 4 tile fits
+// neither the registers at G = 1 nor the LDS at G = 2 with the code ring: not a candidate.)
 constexpr int rw_group(int To, int MODE, int NI) {
   return MODE == 1 ? (To <= 2 ? 2 : 1) : (To <= 2 ? 4 : (NI * To >= 12 ? 1 : 2));
 }
@@ -731,6 +734,11 @@ __device__ __forceinline__ int rw_wrow(int lane) {
   return ((q & 1) << 1) | ((q >> 1) & 1) | (q & 4);
 }
 __device__ __forceinline__ int rw_wswz(int row) { return ((row >> 1) & 3) << 1; }
+// DX ring rows (64 NI bytes, 4 NI units of 16 bytes): unit u of row n sits at u ^ rw_dswz(n), so
+// that the 16 rows of a transposed read's 32-lane pass (one unit each) meet distinct banks
+template <int NI> __device__ __forceinline__ int rw_dswz(int row) {
+  return NI == 2 ? ((row >> 1) & 7) : ((row >> 2) & 3);
+}
 constexpr int align16(int v) { return (v + 15) & ~15; }
 
 // The 16-byte unit u of activation row r sits at u ^ rw_swz<MODE>(r). A fragment read takes
@@ -771,36 +779,36 @@ __device__ __forceinline__ void rw_acc(const SkArgs& a, int64_t r0, int64_t tok0
     lx[j] = (uint32_t)u * 16u;
   }
   // weight: FWD row r0 + 16 NI wr + 8 (2 i + par) + lane / 8, bytes 16 (lane % 8) of the step's
-  // 128; DX row n = lane of the chunk, bytes r0 + 16 NI wr + 16 i (16 output columns k)
-  uint32_t vw[NI];
+  // 128; DX flat unit (NI w + i) 64 + lane of the step's [128 n][4 NI units] (16 output columns
+  // k each), stored at lw[i] in the ring slot
+  uint32_t vw[NI], lw[NI];
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
     if (MODE == 0) {
       const int64_t row = r0 + 16 * NI * wr + 8 * (2 * i + par) + rw_wrow(lane);
       vw[i] = row < a.Ncols ? (uint32_t)(row * a.ldq + 16 * (lane & 7)) : OOB;
+      const int rr = 16 * NI * wr + 16 * i + 8 * par + rw_wrow(lane);
+      lw[i] = (uint32_t)(rr * 128 + (((lane & 7) ^ rw_wswz(rr)) << 4));
     } else {
-      const int64_t col = r0 + 16 * NI * wr + 16 * i;
-      vw[i] = col < a.Ncols ? (uint32_t)((64 * par + lane) * a.ldq + col) : OOB;
+      const int idx = (NI * w + i) * 64 + lane, n = idx / (4 * NI), u = idx % (4 * NI);
+      const int64_t col = r0 + 16 * u;
+      vw[i] = col < a.Ncols ? (uint32_t)(n * a.ldq + col) : OOB;
+      lw[i] = (uint32_t)(n * (64 * NI) + ((u ^ rw_dswz<NI>(n)) << 4));
     }
   }
   const uint32_t wstep = MODE == 0 ? 128u : (uint32_t)(128 * a.ldq);
-  // DX: the block's scales s[0 .. Kred) in LDS after the activation slots, and this wave's
-  // [64 n][16 NI] code tile after them
+  // DX: the block's scales s[0 .. Kred) in LDS after the activation slots
   float* stab = reinterpret_cast<float*>(smem + 2 * G * SLOT);
-  uint8_t* wt = smem + 2 * G * SLOT + align16((int)a.Kred * 4) + w * (1024 * NI);
-  // FWD: the weight ring of 2 G slots after the activation slots. Step t's codes are written
-  // in step t - G - 1 and read in step t - 1 (converted for the next step's MFMAs), so a group
-  // barrier lies between the writes and the reads, and between the last read of a slot and its
-  // next writes (G steps apart).
-  static_assert(MODE == 1 || D >= G + 2, "the codes of step t arrive before step t - G - 1");
-  uint8_t* wring = smem + 2 * G * SLOT;
+  // The code ring of 2 G slots (after the activation slots, and for DX the scales). Step t's
+  // codes are written in step t - G - 1 and read in step t - 1 (converted for the next step's
+  // MFMAs), so a group barrier lies between the writes and the reads, and between the last read
+  // of a slot and its next writes (G steps apart).
+  static_assert(D >= G + 2, "the codes of step t arrive before step t - G - 1");
+  uint8_t* wring = smem + 2 * G * SLOT + (MODE == 1 ? align16((int)a.Kred * 4) : 0);
   constexpr int WSLOT = rw_wslot(NI);
   auto put_w = [&](const u32x4 (&wd)[NI], int slot) {
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int row = 16 * NI * wr + 16 * i + 8 * par + rw_wrow(lane);
-      *reinterpret_cast<u32x4*>(wring + slot * WSLOT + row * 128 + (((lane & 7) ^ rw_wswz(row)) << 4)) = wd[i];
-    }
+    for (int i = 0; i < NI; ++i) *reinterpret_cast<u32x4*>(wring + slot * WSLOT + lw[i]) = wd[i];
   };
   if constexpr (MODE == 1) {
     for (int i = t; i < (int)a.Kred / 4; i += 64 * sk::NWV)
@@ -826,9 +834,6 @@ __device__ __forceinline__ void rw_acc(const SkArgs& a, int64_t r0, int64_t tok0
     for (int i = 0; i < NI; ++i)
       wd[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, vw[i], sw, 0));
   };
-  // the wave's DX code tile: with an even NI, rows r and r + 8 (read in one pass of the
-  // transposed read) would share banks, so the 16-byte units of a row are flipped by its bit 3
-  auto wt_swz = [&](int row) { return (NI % 2 == 0) ? ((row >> 3) & 1) : 0; };
   auto put_x = [&](const u32x4 (&xd)[XL], int slot) {
 #pragma unroll
     for (int j = 0; j < XL; ++j) *reinterpret_cast<u32x4*>(smem + slot * SLOT + lx[j]) = xd[j];
@@ -848,11 +853,10 @@ __device__ __forceinline__ void rw_acc(const SkArgs& a, int64_t r0, int64_t tok0
 #pragma unroll
         for (int e = 0; e < 2; ++e) af[i][e] = E::from_i8x8(wv[i][2 * e], wv[i][2 * e + 1]);
     } else {
-      // the code tile [64 n][16 NI k] to this wave's LDS tile, then per 16-k tile i and step e the
-      // transposed read: providing lane p of a 16-lane group addresses row 32 e + 8 g + p / 2,
-      // columns 16 i + 8 (p % 2) .. +7; lane l16 receives k = 16 i + l16, n = 32 e + 8 g + (0..7)
-#pragma unroll
-      for (int i = 0; i < NI; ++i) *reinterpret_cast<u32x4*>(wt + lane * (16 * NI) + 16 * (i ^ wt_swz(lane))) = wv[i];
+      // per 16-k tile i and step e the transposed read from the step's ring slot: providing lane
+      // p of a 16-lane group addresses row n = 64 par + 32 e + 8 g + p / 2, unit NI wr + i, bytes
+      // 8 (p % 2) .. +7; lane l16 receives k = 16 (NI wr + i) + l16, n = 64 par + 32 e + 8 g + (0..7)
+      const uint8_t* ws = wring + (s % (2 * G)) * WSLOT;
       // the zero codes of a step past the operands may take any scale
       const int64_t nb = s < nsteps ? (int64_t)(2 * at(s) + par) * 64 : 0;
 #pragma unroll
@@ -861,8 +865,8 @@ __device__ __forceinline__ void rw_acc(const SkArgs& a, int64_t r0, int64_t tok0
         const f32x4 s1 = *reinterpret_cast<const f32x4*>(stab + nb + 32 * e + 8 * g + 4);
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
-          const int row = 32 * e + 8 * g + (l16 >> 1);
-          const uint8_t* p = wt + row * (16 * NI) + 16 * (i ^ wt_swz(row)) + 8 * (l16 & 1);
+          const int row = 64 * par + 32 * e + 8 * g + (l16 >> 1);
+          const uint8_t* p = ws + row * (64 * NI) + (((NI * wr + i) ^ rw_dswz<NI>(row)) << 4) + 8 * (l16 & 1);
           const i32x2 v = __builtin_amdgcn_ds_read_tr8_b64_v2i32(LDS_PTR(i32x2, p));
           if constexpr (ELT == REELS_HIP_F16) {  // Float16(q) * Float16(s[n])
             const u32x4 s16 = {E::pack2(s0[0], s0[1]), E::pack2(s0[2], s0[3]),
@@ -936,7 +940,7 @@ __device__ __forceinline__ void rw_acc(const SkArgs& a, int64_t r0, int64_t tok0
   auto step = [&](int s, int j, V8 (&afc)[NI][2], V8 (&afn)[NI][2]) {
     mma_convert(s, afc, wq[(j + 1) % D], afn);
     put_x(xr[(j + G) % D], (s + G) % (2 * G));
-    if constexpr (MODE == 0) put_w(wq[(j + G + 1) % D], (s + G + 1) % (2 * G));
+    put_w(wq[(j + G + 1) % D], (s + G + 1) % (2 * G));
     issue(s + D, xr[j], wq[j]);
   };
   // A group's barrier: every wave's writes of the next group's activations are done, and every
@@ -954,10 +958,8 @@ __device__ __forceinline__ void rw_acc(const SkArgs& a, int64_t r0, int64_t tok0
   for (int d = 0; d < D; ++d) issue(d, xr[d], wq[d]);
 #pragma unroll
   for (int d = 0; d < G; ++d) put_x(xr[d], d);
-  if constexpr (MODE == 0) {
 #pragma unroll
-    for (int d = 0; d <= G; ++d) put_w(wq[d], d);
-  }
+  for (int d = 0; d <= G; ++d) put_w(wq[d], d);
   group_barrier();  // also publishes the DX scale table (and the FWD codes), which convert reads
   if constexpr (MODE == 0) {
     u32x4 cv[NI];
@@ -1220,13 +1222,13 @@ __global__ __launch_bounds__(64 * sk::NWV, 1) void skinny_kernel(SkArgs a) {
 // 128-deep step on a CU (the largest of the matrix cores, the LDS reads, the vector memory and,
 // for dX, the VALU scaling of the codes), then the least padded work.
 struct RwCand { int NI, To; };
-constexpr RwCand kRwCands[] = {{1, 2}, {2, 4}, {3, 4}, {2, 6}};
+constexpr RwCand kRwCands[] = {{1, 2}, {2, 4}, {2, 6}};
 constexpr int kRwLdsMax = 160 * 1024;
 
 static int rw_lds_bytes(int NI, int To, int mode, int64_t Kred) {
   const int slot = 2 * 16 * To * 128, ta = To <= 4 ? To : To / 2;
   const int G = rw_group(To, mode, NI);
-  int v = 2 * G * slot + (mode == 1 ? align16((int)Kred * 4) + 8 * 1024 * NI : 2 * G * rw_wslot(NI));
+  int v = 2 * G * slot + (mode == 1 ? align16((int)Kred * 4) : 0) + 2 * G * rw_wslot(NI);
   v = std::max(v, 8 * NI * (To / 2) * 1024);
   v = std::max(v, skinny_lds(ta));
   v = std::max(v, 8 * 1024 * NI);
@@ -1246,7 +1248,6 @@ static bool rw_choose(int64_t M, int64_t Kred, int64_t Ncols, int rp, int mode, 
     const int64_t tiles = orb * otb, nad = rp > 0 ? lblk * tba : 0;
     if (tiles + nad > kSkinnyTargetBlocks || tiles < kSkinnyTargetBlocks / 2) continue;
     if (rw_lds_bytes(c.NI, c.To, mode, Kred) > kRwLdsMax) continue;
-    if (mode == 0 && c.NI == 3) continue;  // see rw_group
     const int64_t mf = 64 * c.NI * c.To, lds = 128 * c.To, vm = 128 * c.NI + 64 * c.To;
     const int64_t valu = (mode == 1 ? 384 : 192) * c.NI;
     const int64_t cost = std::max(std::max(mf, lds), std::max(vm, valu));
@@ -1295,11 +1296,10 @@ bool skinny_supported(int64_t M, int64_t K, int64_t N, int rp) {
 
 SkinnyPlan skinny_plan(int64_t M, int64_t Kred, int64_t Ncols, int rp, int mode) {
   SkinnyPlan p;
-  // the forward takes row-wave tiles wherever they fill the GPU; dX up to 240 tokens keeps the
-  // split tiles (its weight scaling costs the row-wave loop more: 77 tokens on 5120 x 5120,
-  // 26 against 30 us)
-  const bool few = M <= kSkinnyMaxTokens || (M <= kSkinnySmallWeightTokens && Ncols * Kred <= ((int64_t)1 << 22));
-  if ((mode == 0 || !few) && rw_choose(M, Kred, Ncols, rp, mode, p)) return p;
+  // row-wave tiles wherever they fill the GPU (with the codes loaded as whole row segments they
+  // beat the split tiles in both directions: 77 tokens on 5120 x 5120, dX + dA + dB 29.5 against
+  // 32.0 us), split tiles elsewhere
+  if (rw_choose(M, Kred, Ncols, rp, mode, p)) return p;
   p.tb = (int)ceil_div(M, 16 * sk::MAXT);
   p.T = (int)ceil_div(ceil_div(M, p.tb), 16);
   const int64_t blocks = (Ncols / sk::NB + ceil_div(rp, sk::NBL)) * p.tb;
@@ -1414,9 +1414,7 @@ int launch_skinny(int mode, int elt, const SkinnyPlan& p, const uint16_t* act, c
         constexpr int MD = decltype(m)::value;
         if (p.NI == 1 && p.To == 2) attr = launch_rw_t<2, 1, 2, MD, EL>(a, lds, st);
         else if (p.NI == 2 && p.To == 4) attr = launch_rw_t<4, 2, 4, MD, EL>(a, lds, st);
-        else if (p.NI == 2 && p.To == 6) attr = launch_rw_t<6, 2, 3, MD, EL>(a, lds, st);
-        else if constexpr (MD == 1) attr = launch_rw_t<4, 3, 4, MD, EL>(a, lds, st);  // 3 x 4: dX only
-        else attr = hipErrorInvalidConfiguration;  // no FWD 3 x 4 plan (rw_choose)
+        else attr = launch_rw_t<6, 2, 3, MD, EL>(a, lds, st);
       };
       if (mode == 0) go(std::integral_constant<int, 0>{});
       else go(std::integral_constant<int, 1>{});
