@@ -990,6 +990,123 @@ __device__ __forceinline__ void rw_acc(const SkArgs& a, int64_t r0, int64_t tok0
   }
 }
 
+// FWD: the same products with both operands copied from memory straight into LDS by the buffer
+// unit (buffer_load ... lds), no register staging: a ring of RS step slots (activations
+// [2 par][16 To tokens][128 bytes] as above, then the codes [64 NI rows][128 bytes] with their
+// 16-byte units XOR-swizzled by rw_wswz), the copies of step s + L = s + RS - 1 issued right after
+// the barrier that opens step s. At that barrier every wave has finished reading the previous
+// step's slot (lgkmcnt(0)) and waited for its own copies of step s (the copies of the L - 1 later
+// steps may stay in flight), so the barrier publishes step s and frees slot (s - 1) % RS, which
+// the new copies fill. Copies past the reduction read zeros (a 2^30-byte offset past the
+// descriptor) into slots nobody reads; the last of them are drained before returning.
+constexpr int rw_fslots(int To, int NI) {
+  return ((160 * 1024 - 16) / (2 * 16 * To * 128 + rw_wslot(NI))) > 8
+             ? 8
+             : ((160 * 1024 - 16) / (2 * 16 * To * 128 + rw_wslot(NI)));
+}
+
+template <int To, int NI, int ELT>
+__device__ __forceinline__ void rw_acc_dma(const SkArgs& a, int64_t r0, int64_t tok0, int rot,
+                                           uint8_t* smem, f32x4 (&acc)[NI][To]) {
+  using E = Elt<ELT>;
+  typedef typename E::v8 V8;
+  constexpr int BN = 16 * To, XL = To / 2, SLOT = 2 * BN * 128, WSLOT = rw_wslot(NI);
+  constexpr int RS = rw_fslots(To, NI), L = RS - 1, STEP = SLOT + WSLOT;
+  static_assert(RS >= 3, "at least two steps in flight");
+  constexpr uint32_t OOB = 0x80000000u, PAST = 0x40000000u;
+  const int t = threadIdx.x, lane = t & 63;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wr = w & 3, par = w >> 2;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int nsteps = (int)(a.Kred / 128);
+  const i32x4 rx = buffer_rsrc(a.act, (uint32_t)(a.M * a.Kred * 2));
+  const i32x4 rq = buffer_rsrc(a.q, (uint32_t)(a.Ncols * a.ldq));
+  // activations: copy j of wave w fills LDS unit (8 j + w) 64 + lane of the slot (as rw_acc)
+  uint32_t vx[XL];
+#pragma unroll
+  for (int j = 0; j < XL; ++j) {
+    const int u = (8 * j + w) * 64 + lane;
+    const int p = u / (BN * 8), rem = u % (BN * 8), row = rem >> 3;
+    const int col = (rem & 7) ^ rw_swz<0>(row);
+    const int64_t tok = tok0 + row;
+    vx[j] = tok < a.M ? (uint32_t)(tok * a.Kred * 2 + p * 128 + col * 16) : OOB;
+  }
+  // codes: copy i of wave w fills ring rows 8 (NI w + i) .. + 7, lane at unit lane % 8 of row
+  // lane / 8, which holds the row's unit (lane % 8) ^ rw_wswz(row)
+  uint32_t vw[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int R = (NI * w + i) * 8 + (lane >> 3);
+    const int64_t grow = r0 + R;
+    vw[i] = grow < a.Ncols ? (uint32_t)(grow * a.ldq + 16 * ((lane & 7) ^ rw_wswz(R))) : OOB;
+  }
+  auto at = [&](int s) { const int v = s + rot; return v >= nsteps ? v - nsteps : v; };
+  auto issue = [&](int s, int slot) {
+    const bool ok = s < nsteps;
+    const int sr = at(s);
+    const uint32_t sx = ok ? (uint32_t)sr * 256u : PAST, sw = ok ? (uint32_t)sr * 128u : PAST;
+    uint8_t* base = smem + slot * STEP;
+#pragma unroll
+    for (int j = 0; j < XL; ++j) dma16(rx, vx[j], sx, base + (8 * j + w) * 1024);
+#pragma unroll
+    for (int i = 0; i < NI; ++i) dma16(rq, vw[i], sw, base + SLOT + (NI * w + i) * 1024);
+  };
+#pragma unroll
+  for (int i = 0; i < NI; ++i)
+#pragma unroll
+    for (int tt = 0; tt < To; ++tt) acc[i][tt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  // the wait that opens a step: this wave's LDS reads done, its copies of the step landed (the
+  // copies of the L - 1 steps after it may stay in flight)
+  constexpr int NV = (L - 1) * (XL + NI);
+  static_assert(NV < 64, "vmcnt field");
+  constexpr int WAIT = (NV & 15) | ((NV >> 4) << 14) | (7 << 4);  // lgkmcnt(0), vmcnt(NV)
+  auto step = [&](int s, int slot) {
+    __builtin_amdgcn_s_waitcnt(WAIT);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    issue(s + L, (slot + L) % RS);
+    const uint8_t* base = smem + slot * STEP;
+    // codes of rows 16 i + l16 (unit 4 par + g: k = 64 par + 16 g + (0..15)), then the
+    // activations (unit 2 g + e of the par half: k = 64 par + 16 g + 8 e + (0..7))
+    u32x4 cv[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int row = 16 * NI * wr + 16 * i + l16;
+      cv[i] = *reinterpret_cast<const u32x4*>(base + SLOT + row * 128 + (((4 * par + g) ^ rw_wswz(row)) << 4));
+    }
+    const uint8_t* xs = base + par * (BN * 128);
+    const int sw = rw_swz<0>(l16);
+    u32x4 xv[2][To];
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+#pragma unroll
+      for (int tt = 0; tt < To; ++tt)
+        xv[e][tt] = *reinterpret_cast<const u32x4*>(xs + (16 * tt + l16) * 128 + (((2 * g + e) ^ sw) << 4));
+    V8 af[NI][2];
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) af[i][e] = E::from_i8x8(cv[i][2 * e], cv[i][2 * e + 1]);
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+#pragma unroll
+      for (int tt = 0; tt < To; ++tt)
+#pragma unroll
+        for (int i = 0; i < NI; ++i) acc[i][tt] = E::mfma16(af[i][e], E::as8(xv[e][tt]), acc[i][tt]);
+  };
+#pragma unroll
+  for (int d = 0; d < L; ++d) issue(d, d);
+  const int nfull = nsteps / RS * RS;
+  for (int s0 = 0; s0 < nfull; s0 += RS) {
+#pragma unroll
+    for (int j = 0; j < RS; ++j) step(s0 + j, j);
+  }
+#pragma unroll
+  for (int j = 0; j < RS; ++j)
+    if (nfull + j < nsteps) step(nfull + j, j);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the copies past the reduction have landed
+}
+
 // lo[i][tt] (rows 16 i + 4 g + v of the wave's 16 NI, tokens of the wave's token tiles) += the
 // adapter term l R over rank columns [0, rp): FWD R(o, j) = B[j][o] staged per wave in LDS and
 // read transposed, DX R(k, j) = A[k][j] read straight from memory; l = h or u from the workspace
@@ -1077,7 +1194,9 @@ __device__ __forceinline__ void rw_block(const SkArgs& a, int rb, int tbo, uint8
     f32x4 acc[NI][To];
     // a rotation per row block (the token tiles of one row block read its weight rows together)
     const int nsteps = (int)(a.Kred / 128);
-    rw_acc<To, NI, MODE, ELT>(a, r0, tok0, (int)(((int64_t)rb * 7) % nsteps), smem, acc);
+    const int rot = (int)(((int64_t)rb * 7) % nsteps);
+    if constexpr (MODE == 0) rw_acc_dma<To, NI, ELT>(a, r0, tok0, rot, smem, acc);
+    else rw_acc<To, NI, MODE, ELT>(a, r0, tok0, rot, smem, acc);
     // waves 4-7 give their first half of the token tiles, waves 0-3 their second, through LDS;
     // each then adds (partner + own, wave w's value first: the same sum for both halves)
     f32x4* ex = reinterpret_cast<f32x4*>(smem);
@@ -1228,7 +1347,8 @@ constexpr int kRwLdsMax = 160 * 1024;
 static int rw_lds_bytes(int NI, int To, int mode, int64_t Kred) {
   const int slot = 2 * 16 * To * 128, ta = To <= 4 ? To : To / 2;
   const int G = rw_group(To, mode, NI);
-  int v = 2 * G * slot + (mode == 1 ? align16((int)Kred * 4) : 0) + 2 * G * rw_wslot(NI);
+  int v = mode == 0 ? rw_fslots(To, NI) * (slot + rw_wslot(NI))
+                    : 2 * G * slot + align16((int)Kred * 4) + 2 * G * rw_wslot(NI);
   v = std::max(v, 8 * NI * (To / 2) * 1024);
   v = std::max(v, skinny_lds(ta));
   v = std::max(v, 8 * 1024 * NI);
