@@ -692,53 +692,27 @@ __global__ __launch_bounds__(256) void skinny_clear_kernel(uint32_t* p, int n) {
 // 64-row block and hand split partials between blocks. A row-wave tile instead covers 64 NI
 // output rows x 16 To tokens and the whole reduction in one block, so no partial leaves it: wave
 // w takes rows 16 NI (w & 3) .. + 16 NI of the tile and, in step s, the 64-wide reduction chunk
-// 2 s + (w >> 2); waves w and w + 4 meet once at the end. The step's activations (two chunks of
-// 16 To tokens) are loaded by all 8 waves into registers rw_depth steps ahead and written to an LDS
-// double buffer one step ahead, where every wave of the block reads them; each wave's weight
-// goes straight from memory into its registers, also rw_depth steps ahead.
-//   FWD: the block's codes of a step (64 NI rows x 128 bytes) are loaded as whole 128-byte row
-//        segments, 8 rows per wave instruction (waves w and w + 4 load alternate 8-row groups of
-//        their 16 NI rows), and written to an LDS ring G + 1 steps ahead of their conversion
-//        (rows' 16-byte units XOR-swizzled by row); a lane then reads 8 codes of row 16 i + l16
-//        at k = 64 par + 16 g + 8 e + (0..7) for MFMA step e, the activations using the same k.
-//        (Loaded straight in that layout, each instruction touched 16 rows' half lines: 15-18%
-//        slower.)
-//   DX:  the block's codes of a step (128 rows n x 64 NI bytes k) are loaded as whole row
-//        segments (flat 16-byte units in order, so each instruction covers 64 NI-byte pieces of
-//        consecutive rows) into the same kind of ring, G + 1 steps ahead; a wave's
-//        [64 n][16 NI k] share reaches the MFMA through ds_read_b64_tr_b8 (lane: k = 16 i + l16,
-//        n = 32 e + 8 g + (0..7)), each code scaled by s[n] from a table of the block's scales in
-//        LDS: bf16(fl32(q s[n])) (f16: f16(q f16(s))), the dequantized weight of the large-token
-//        dX. (Loaded per wave, each instruction took 16 bytes from each of 64 rows.)
+// 2 s + (w >> 2); waves w and w + 4 meet once at the end. A step's operands (the activations of
+// two chunks x 16 To tokens, and the block's codes) are copied from memory straight into an LDS
+// ring by the buffer unit, several steps ahead (rw_acc_dma), and every wave reads its fragments
+// there:
+//   FWD: the codes of a step, 64 NI rows x 128 bytes, are copied as whole 128-byte row segments
+//        (8 rows per copy instruction); a lane reads 16 codes of row 16 i + l16 at
+//        k = 64 par + 16 g + (0..15) and feeds MFMA step e with k = 64 par + 16 g + 8 e + (0..7),
+//        the activations using the same k. Converted exactly to bf16 (f16); the row scale
+//        multiplies the f32 sum at the end.
+//   DX:  the codes of a step, 128 rows n x 64 NI bytes k, are copied as whole row segments too;
+//        a wave's [64 n][16 NI k] share reaches the MFMA through ds_read_b64_tr_b8 (lane:
+//        k = 16 i + l16, n = 32 e + 8 g + (0..7)), each code scaled by s[n] from a table of the
+//        block's scales in LDS: bf16(fl32(q s[n])) (f16: f16(q f16(s))), the dequantized weight
+//        of the large-token dX.
+// (Measured against register-staged loads: codes loaded straight in the MFMA layout touched 16
+// rows' half lines per instruction (FWD) or 16 bytes of each of 64 rows (DX); whole row segments
+// through LDS, then copies that bypass the registers, took 77 / 333 / 512 tokens on 5120 x 5120
+// from 20.1 / 34.4 / 46.6 to 17.3 / 30.0 / 40.6 us forward and 32.0 / 56.7 / 73.0 to
+// 29.1 / 43.7 / 54.2 us backward.)
 // LDS rows of the activations are 128 bytes (64 bf16), their 16-byte units swizzled per row
 // (rw_swz) so that the fragment reads hit distinct banks.
-// Steps per barrier (G) and steps whose loads are in flight (D, a multiple of G above it): the
-// activations ring in LDS holds 2 G steps, so a group of G steps reads one half while the other
-// half is written for the next group, and the waves meet at one barrier per group.
-// (measured: dX, whose loop is heavier on the VALU, runs best with four steps in flight and a
-// barrier every step or two). The FWD tile of 12 MFMA tiles per wave (2 x 6) meets every step:
-// its code ring of 2 G slots then fits the LDS beside the activations. (A 3 x 4 tile fits
-// neither the registers at G = 1 nor the LDS at G = 2 with the code ring: not a candidate.)
-constexpr int rw_group(int To, int MODE, int NI) {
-  return MODE == 1 ? (To <= 2 ? 2 : 1) : (To <= 2 ? 4 : (NI * To >= 12 ? 1 : 2));
-}
-constexpr int rw_depth(int To, int MODE) { return MODE == 1 ? 4 : (To <= 2 ? 8 : 4); }
-// FWD weight ring slot: the block's 64 NI rows x 128 code bytes of one step. A wave's load puts 8
-// lanes on each of 8 rows; rw_wrow gives the 8-lane groups that may share a pass of the LDS
-// write (0-7 with 16-23 or 24-31, and so on) rows of different parity, which start in the
-// other half of the banks. The 16-byte unit u of ring row r sits at u ^ rw_wswz(r): the code
-// reads (rows l16 of a 16-row tile, unit 4 par + g) then meet distinct banks in such a pass too.
-constexpr int rw_wslot(int NI) { return 64 * NI * 128; }
-__device__ __forceinline__ int rw_wrow(int lane) {
-  const int q = lane >> 3;
-  return ((q & 1) << 1) | ((q >> 1) & 1) | (q & 4);
-}
-__device__ __forceinline__ int rw_wswz(int row) { return ((row >> 1) & 3) << 1; }
-// DX ring rows (64 NI bytes, 4 NI units of 16 bytes): unit u of row n sits at u ^ rw_dswz(n), so
-// that the 16 rows of a transposed read's 32-lane pass (one unit each) meet distinct banks
-template <int NI> __device__ __forceinline__ int rw_dswz(int row) {
-  return NI == 2 ? ((row >> 1) & 7) : ((row >> 2) & 3);
-}
 constexpr int align16(int v) { return (v + 15) & ~15; }
 
 // The 16-byte unit u of activation row r sits at u ^ rw_swz<MODE>(r). A fragment read takes
@@ -751,267 +725,40 @@ constexpr int align16(int v) { return (v + 15) & ~15; }
 template <int MODE> __device__ __forceinline__ int rw_swz(int row) {
   return MODE == 0 ? ((row >> 1) & 1) | (((row >> 2) & 1) << 2) : ((row >> 1) & 3) << 1;
 }
-
-template <int To, int NI, int MODE, int ELT>
-__device__ __forceinline__ void rw_acc(const SkArgs& a, int64_t r0, int64_t tok0, int rot,
-                                       uint8_t* smem, f32x4 (&acc)[NI][To]) {
-  using E = Elt<ELT>;
-  typedef typename E::v8 V8;
-  constexpr int BN = 16 * To, XL = To / 2, SLOT = 2 * BN * 128, G = rw_group(To, MODE, NI), D = rw_depth(To, MODE);
-  constexpr uint32_t OOB = 0x80000000u;
-  const int t = threadIdx.x, lane = t & 63;
-  const int w = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int wr = w & 3, par = w >> 2;
-  const int l16 = lane & 15, g = lane >> 4;
-  const int nsteps = (int)(a.Kred / 128);
-  const __amdgpu_buffer_rsrc_t rx = sk_rsrc(a.act, a.M * a.Kred * 2);
-  const int64_t wbytes = MODE == 0 ? a.Ncols * a.ldq : a.Kred * a.ldq;
-  const __amdgpu_buffer_rsrc_t rq = sk_rsrc(a.q, wbytes);
-  // activations: the lane's load j fills LDS unit (8 j + w) 64 + lane of the step's slot
-  uint32_t vx[XL], lx[XL];
-#pragma unroll
-  for (int j = 0; j < XL; ++j) {
-    const int u = (8 * j + w) * 64 + lane;
-    const int p = u / (BN * 8), rem = u % (BN * 8), row = rem >> 3;
-    const int col = (rem & 7) ^ rw_swz<MODE>(row);
-    const int64_t tok = tok0 + row;
-    vx[j] = tok < a.M ? (uint32_t)(tok * a.Kred * 2 + p * 128 + col * 16) : OOB;
-    lx[j] = (uint32_t)u * 16u;
-  }
-  // weight: FWD row r0 + 16 NI wr + 8 (2 i + par) + lane / 8, bytes 16 (lane % 8) of the step's
-  // 128; DX flat unit (NI w + i) 64 + lane of the step's [128 n][4 NI units] (16 output columns
-  // k each), stored at lw[i] in the ring slot
-  uint32_t vw[NI], lw[NI];
-#pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    if (MODE == 0) {
-      const int64_t row = r0 + 16 * NI * wr + 8 * (2 * i + par) + rw_wrow(lane);
-      vw[i] = row < a.Ncols ? (uint32_t)(row * a.ldq + 16 * (lane & 7)) : OOB;
-      const int rr = 16 * NI * wr + 16 * i + 8 * par + rw_wrow(lane);
-      lw[i] = (uint32_t)(rr * 128 + (((lane & 7) ^ rw_wswz(rr)) << 4));
-    } else {
-      const int idx = (NI * w + i) * 64 + lane, n = idx / (4 * NI), u = idx % (4 * NI);
-      const int64_t col = r0 + 16 * u;
-      vw[i] = col < a.Ncols ? (uint32_t)(n * a.ldq + col) : OOB;
-      lw[i] = (uint32_t)(n * (64 * NI) + ((u ^ rw_dswz<NI>(n)) << 4));
-    }
-  }
-  const uint32_t wstep = MODE == 0 ? 128u : (uint32_t)(128 * a.ldq);
-  // DX: the block's scales s[0 .. Kred) in LDS after the activation slots
-  float* stab = reinterpret_cast<float*>(smem + 2 * G * SLOT);
-  // The code ring of 2 G slots (after the activation slots, and for DX the scales). Step t's
-  // codes are written in step t - G - 1 and read in step t - 1 (converted for the next step's
-  // MFMAs), so a group barrier lies between the writes and the reads, and between the last read
-  // of a slot and its next writes (G steps apart).
-  static_assert(D >= G + 2, "the codes of step t arrive before step t - G - 1");
-  uint8_t* wring = smem + 2 * G * SLOT + (MODE == 1 ? align16((int)a.Kred * 4) : 0);
-  constexpr int WSLOT = rw_wslot(NI);
-  auto put_w = [&](const u32x4 (&wd)[NI], int slot) {
-#pragma unroll
-    for (int i = 0; i < NI; ++i) *reinterpret_cast<u32x4*>(wring + slot * WSLOT + lw[i]) = wd[i];
-  };
-  if constexpr (MODE == 1) {
-    for (int i = t; i < (int)a.Kred / 4; i += 64 * sk::NWV)
-      reinterpret_cast<f32x4*>(stab)[i] = reinterpret_cast<const f32x4*>(a.s)[i];
-  }
-
-  u32x4 xr[D][XL], wq[D][NI];
-  // Steps past the operands read zeros: their scalar offset alone moves every lane past the
-  // descriptor (the planner keeps the operands below 2^30 bytes, so no offset wraps).
-  constexpr uint32_t PAST = 0x40000000u;
-  // The walk over the reduction starts at step rot (then wraps): weight rows lie a multiple of
-  // 1 KiB apart, so row blocks that walked the same offsets together would pile onto a few
-  // memory channels. Step s of the walk is reduction step at(s).
-  auto at = [&](int s) { const int v = s + rot; return v >= nsteps ? v - nsteps : v; };
-  auto issue = [&](int s, u32x4 (&xd)[XL], u32x4 (&wd)[NI]) {
-    const bool ok = s < nsteps;
-    const int sr = at(s);
-    const uint32_t sx = ok ? (uint32_t)sr * 256u : PAST, sw = ok ? (uint32_t)sr * wstep : PAST;
-#pragma unroll
-    for (int j = 0; j < XL; ++j)
-      xd[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, vx[j], sx, 0));
-#pragma unroll
-    for (int i = 0; i < NI; ++i)
-      wd[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, vw[i], sw, 0));
-  };
-  auto put_x = [&](const u32x4 (&xd)[XL], int slot) {
-#pragma unroll
-    for (int j = 0; j < XL; ++j) *reinterpret_cast<u32x4*>(smem + slot * SLOT + lx[j]) = xd[j];
-  };
-#pragma unroll
-  for (int i = 0; i < NI; ++i)
-#pragma unroll
-    for (int tt = 0; tt < To; ++tt) acc[i][tt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-
-  // the MFMA A operands of step s from its codes: FWD exact int8 -> bf16 (f16); DX through the
-  // wave's LDS tile, each code scaled by s[n]
-  auto convert = [&](const u32x4 (&wv)[NI], int s, V8 (&af)[NI][2]) {
-    if constexpr (MODE == 0) {
-      // the codes read by read_codes
-#pragma unroll
-      for (int i = 0; i < NI; ++i)
-#pragma unroll
-        for (int e = 0; e < 2; ++e) af[i][e] = E::from_i8x8(wv[i][2 * e], wv[i][2 * e + 1]);
-    } else {
-      // per 16-k tile i and step e the transposed read from the step's ring slot: providing lane
-      // p of a 16-lane group addresses row n = 64 par + 32 e + 8 g + p / 2, unit NI wr + i, bytes
-      // 8 (p % 2) .. +7; lane l16 receives k = 16 (NI wr + i) + l16, n = 64 par + 32 e + 8 g + (0..7)
-      const uint8_t* ws = wring + (s % (2 * G)) * WSLOT;
-      // the zero codes of a step past the operands may take any scale
-      const int64_t nb = s < nsteps ? (int64_t)(2 * at(s) + par) * 64 : 0;
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const f32x4 s0 = *reinterpret_cast<const f32x4*>(stab + nb + 32 * e + 8 * g);
-        const f32x4 s1 = *reinterpret_cast<const f32x4*>(stab + nb + 32 * e + 8 * g + 4);
-#pragma unroll
-        for (int i = 0; i < NI; ++i) {
-          const int row = 64 * par + 32 * e + 8 * g + (l16 >> 1);
-          const uint8_t* p = ws + row * (64 * NI) + (((NI * wr + i) ^ rw_dswz<NI>(row)) << 4) + 8 * (l16 & 1);
-          const i32x2 v = __builtin_amdgcn_ds_read_tr8_b64_v2i32(LDS_PTR(i32x2, p));
-          if constexpr (ELT == REELS_HIP_F16) {  // Float16(q) * Float16(s[n])
-            const u32x4 s16 = {E::pack2(s0[0], s0[1]), E::pack2(s0[2], s0[3]),
-                               E::pack2(s1[0], s1[1]), E::pack2(s1[2], s1[3])};
-            af[i][e] = E::scale8(E::from_i8x8((uint32_t)v[0], (uint32_t)v[1]), s16);
-          } else {  // bf16(fl32(q * s[n]))
-            const uint32_t lo = (uint32_t)v[0], hi = (uint32_t)v[1];
-            const u32x4 o = {E::pack2_fast((float)(int8_t)(lo & 0xffu) * s0[0], (float)(int8_t)((lo >> 8) & 0xffu) * s0[1]),
-                             E::pack2_fast((float)(int8_t)((lo >> 16) & 0xffu) * s0[2], (float)((int32_t)lo >> 24) * s0[3]),
-                             E::pack2_fast((float)(int8_t)(hi & 0xffu) * s1[0], (float)(int8_t)((hi >> 8) & 0xffu) * s1[1]),
-                             E::pack2_fast((float)(int8_t)((hi >> 16) & 0xffu) * s1[2], (float)((int32_t)hi >> 24) * s1[3])};
-            af[i][e] = E::as8(o);
-          }
-        }
-      }
-    }
-  };
-
-  // FWD: 8 codes of row 16 i + l16 at k = 64 par + 16 g + 8 e (e = 0, 1) of step s from its ring
-  // slot, read before the step's activation fragments (LDS answers in order, and the conversions
-  // interleaved with the first MFMAs wait only for these)
-  auto read_codes = [&](int s, u32x4 (&cv)[NI]) {
-    const uint8_t* ws = wring + (s % (2 * G)) * WSLOT;
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int row = 16 * NI * wr + 16 * i + l16;
-      cv[i] = *reinterpret_cast<const u32x4*>(ws + row * 128 + (((4 * par + g) ^ rw_wswz(row)) << 4));
-    }
-  };
-
-  // Step s: its activation fragments from LDS, then its MFMAs (k step outermost, so the two
-  // products into one accumulator lie NI To MFMAs apart) interleaved with the conversion of step
-  // s + 1's codes, so the matrix cores and the VALU work side by side in each wave.
-  auto mma_convert = [&](int s, const V8 (&afc)[NI][2], const u32x4 (&wn)[NI], V8 (&afn)[NI][2]) {
-    u32x4 cv[NI];
-    if constexpr (MODE == 0) read_codes(s + 1, cv);
-    const uint8_t* xs = smem + (s % (2 * G)) * SLOT + par * (BN * 128);
-    const int sw = rw_swz<MODE>(l16);  // the same for every 16-row token tile
-    u32x4 xv[2][To];
-#pragma unroll
-    for (int e = 0; e < 2; ++e)
-#pragma unroll
-      for (int tt = 0; tt < To; ++tt) {
-        // FWD: k = 16 g + 8 e + (0..7) (unit 2 g + e); DX: n = 32 e + 8 g + (0..7) (unit 4 e + g)
-        const int unit = MODE == 0 ? 2 * g + e : 4 * e + g;
-        xv[e][tt] = *reinterpret_cast<const u32x4*>(xs + (16 * tt + l16) * 128 + ((unit ^ sw) << 4));
-      }
-    if constexpr (MODE == 0) convert(cv, s + 1, afn);
-    else convert(wn, s + 1, afn);
-#pragma unroll
-    for (int e = 0; e < 2; ++e)
-#pragma unroll
-      for (int tt = 0; tt < To; ++tt)
-#pragma unroll
-        for (int i = 0; i < NI; ++i) acc[i][tt] = E::mfma16(afc[i][e], E::as8(xv[e][tt]), acc[i][tt]);
-    // schedule: the fragment reads (and the FWD codes), then one MFMA and a few VALU (and for dX
-    // LDS) ops in turn
-    __builtin_amdgcn_sched_group_barrier(0x100, 2 * To + (MODE == 0 ? NI : 0), 0);
-#pragma unroll
-    for (int k = 0; k < 2 * NI * To; ++k) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, MODE == 0 ? 3 : 6, 0);
-      if constexpr (MODE == 1) __builtin_amdgcn_sched_group_barrier(0x080, 1, 0);
-    }
-  };
-
-  // Step s reads ring slot s % 2G and writes the activations of step s + G (loaded G steps
-  // earlier) into slot (s + G) % 2G, which the group before last read; register slot j takes
-  // step s + D (zeros when s + D >= nsteps). Steps past nsteps write zeros nobody reads.
-  V8 afa[NI][2], afb[NI][2];
-  auto step = [&](int s, int j, V8 (&afc)[NI][2], V8 (&afn)[NI][2]) {
-    mma_convert(s, afc, wq[(j + 1) % D], afn);
-    put_x(xr[(j + G) % D], (s + G) % (2 * G));
-    put_w(wq[(j + G + 1) % D], (s + G + 1) % (2 * G));
-    issue(s + D, xr[j], wq[j]);
-  };
-  // A group's barrier: every wave's writes of the next group's activations are done, and every
-  // wave has finished reading the slots the group after writes. It waits for LDS operations
-  // only: the loads in flight stay in flight (a __syncthreads() would wait for vmcnt(0) in its
-  // release fence).
-  auto group_barrier = [&]() {
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-  };
-  // prologue: steps 0 .. D-1 in flight, the first group's activations in slots 0 .. G-1, then
-  // (after the barrier) the first step's codes converted
-#pragma unroll
-  for (int d = 0; d < D; ++d) issue(d, xr[d], wq[d]);
-#pragma unroll
-  for (int d = 0; d < G; ++d) put_x(xr[d], d);
-#pragma unroll
-  for (int d = 0; d <= G; ++d) put_w(wq[d], d);
-  group_barrier();  // also publishes the DX scale table (and the FWD codes), which convert reads
-  if constexpr (MODE == 0) {
-    u32x4 cv[NI];
-    read_codes(0, cv);
-    convert(cv, 0, afa);
-  } else {
-    convert(wq[0], 0, afa);
-  }
-  // whole units of D steps without a branch inside (a conditional step in the unrolled body
-  // makes the compiler drain every load at the loop head), then the last steps
-  static_assert(D % G == 0 && D > G && D % 2 == 0, "a unit of D steps holds whole groups");
-  const int nfull = nsteps / D * D;
-  for (int s0 = 0; s0 < nfull; s0 += D) {
-#pragma unroll
-    for (int j = 0; j < D; ++j) {
-      if (j & 1) step(s0 + j, j, afb, afa);
-      else step(s0 + j, j, afa, afb);
-      if ((j + 1) % G == 0) group_barrier();
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < D; ++j) {
-    if (nfull + j < nsteps) {
-      if (j & 1) step(nfull + j, j, afb, afa);
-      else step(nfull + j, j, afa, afb);
-      if ((j + 1) % G == 0 && nfull + j + 1 < nsteps) group_barrier();
-    }
-  }
+// Code slot of a step: FWD 64 NI rows x 128 bytes, DX 128 rows x 64 NI bytes. FWD row r's unit
+// u sits at u ^ rw_wswz(r): the code reads (rows l16 of a 16-row tile, unit 4 par + g) meet
+// distinct banks in a pass. DX row n's unit u sits at u ^ rw_dswz(n), so that the 16 rows of a
+// transposed read's 32-lane pass (one unit each) meet distinct banks.
+constexpr int rw_wslot(int NI) { return 64 * NI * 128; }
+__device__ __forceinline__ int rw_wswz(int row) { return ((row >> 1) & 3) << 1; }
+template <int NI> __device__ __forceinline__ int rw_dswz(int row) {
+  return NI == 2 ? ((row >> 1) & 7) : ((row >> 2) & 3);
 }
 
-// FWD: the same products with both operands copied from memory straight into LDS by the buffer
-// unit (buffer_load ... lds), no register staging: a ring of RS step slots (activations
-// [2 par][16 To tokens][128 bytes] as above, then the codes [64 NI rows][128 bytes] with their
-// 16-byte units XOR-swizzled by rw_wswz), the copies of step s + L = s + RS - 1 issued right after
-// the barrier that opens step s. At that barrier every wave has finished reading the previous
+// The same products with both operands copied from memory straight into LDS by the buffer unit
+// (buffer_load ... lds), no register staging: a ring of RS step slots (activations
+// [2 par][16 To tokens][128 bytes] as above, then the codes: FWD [64 NI rows][128 bytes], units
+// XOR-swizzled by rw_wswz; DX [128 n][64 NI bytes], units swizzled by rw_dswz), the copies of
+// step s + L = s + RS - 1 issued right after the barrier that opens step s. At that barrier every wave has finished reading the previous
 // step's slot (lgkmcnt(0)) and waited for its own copies of step s (the copies of the L - 1 later
 // steps may stay in flight), so the barrier publishes step s and frees slot (s - 1) % RS, which
 // the new copies fill. Copies past the reduction read zeros (a 2^30-byte offset past the
 // descriptor) into slots nobody reads; the last of them are drained before returning.
-constexpr int rw_fslots(int To, int NI) {
-  return ((160 * 1024 - 16) / (2 * 16 * To * 128 + rw_wslot(NI))) > 8
+// DX keeps the block's scales s[0 .. Kred) beside the ring: Kred up to kRwDxMaxRed
+constexpr int kRwDxMaxRed = 8192;
+constexpr int rw_fslots(int To, int NI, int MODE) {
+  return ((160 * 1024 - 16 - (MODE == 1 ? 4 * kRwDxMaxRed : 0)) / (2 * 16 * To * 128 + rw_wslot(NI))) > 8
              ? 8
-             : ((160 * 1024 - 16) / (2 * 16 * To * 128 + rw_wslot(NI)));
+             : ((160 * 1024 - 16 - (MODE == 1 ? 4 * kRwDxMaxRed : 0)) / (2 * 16 * To * 128 + rw_wslot(NI)));
 }
 
-template <int To, int NI, int ELT>
+template <int To, int NI, int MODE, int ELT>
 __device__ __forceinline__ void rw_acc_dma(const SkArgs& a, int64_t r0, int64_t tok0, int rot,
                                            uint8_t* smem, f32x4 (&acc)[NI][To]) {
   using E = Elt<ELT>;
   typedef typename E::v8 V8;
   constexpr int BN = 16 * To, XL = To / 2, SLOT = 2 * BN * 128, WSLOT = rw_wslot(NI);
-  constexpr int RS = rw_fslots(To, NI), L = RS - 1, STEP = SLOT + WSLOT;
+  constexpr int RS = rw_fslots(To, NI, MODE), L = RS - 1, STEP = SLOT + WSLOT;
   static_assert(RS >= 3, "at least two steps in flight");
   constexpr uint32_t OOB = 0x80000000u, PAST = 0x40000000u;
   const int t = threadIdx.x, lane = t & 63;
@@ -1020,31 +767,45 @@ __device__ __forceinline__ void rw_acc_dma(const SkArgs& a, int64_t r0, int64_t 
   const int l16 = lane & 15, g = lane >> 4;
   const int nsteps = (int)(a.Kred / 128);
   const i32x4 rx = buffer_rsrc(a.act, (uint32_t)(a.M * a.Kred * 2));
-  const i32x4 rq = buffer_rsrc(a.q, (uint32_t)(a.Ncols * a.ldq));
+  const i32x4 rq = buffer_rsrc(a.q, (uint32_t)((MODE == 0 ? a.Ncols : a.Kred) * a.ldq));
+  // DX: the block's scales after the ring, published by the barrier that opens step 0
+  float* stab = reinterpret_cast<float*>(smem + RS * STEP);
+  if constexpr (MODE == 1) {
+    for (int i = t; i < (int)a.Kred / 4; i += 64 * sk::NWV)
+      reinterpret_cast<f32x4*>(stab)[i] = reinterpret_cast<const f32x4*>(a.s)[i];
+  }
   // activations: copy j of wave w fills LDS unit (8 j + w) 64 + lane of the slot (as rw_acc)
   uint32_t vx[XL];
 #pragma unroll
   for (int j = 0; j < XL; ++j) {
     const int u = (8 * j + w) * 64 + lane;
     const int p = u / (BN * 8), rem = u % (BN * 8), row = rem >> 3;
-    const int col = (rem & 7) ^ rw_swz<0>(row);
+    const int col = (rem & 7) ^ rw_swz<MODE>(row);
     const int64_t tok = tok0 + row;
     vx[j] = tok < a.M ? (uint32_t)(tok * a.Kred * 2 + p * 128 + col * 16) : OOB;
   }
-  // codes: copy i of wave w fills ring rows 8 (NI w + i) .. + 7, lane at unit lane % 8 of row
-  // lane / 8, which holds the row's unit (lane % 8) ^ rw_wswz(row)
+  // codes: copy i of wave w fills the slot's 16-byte units (NI w + i) 64 + lane. FWD: ring row
+  // 8 (NI w + i) + lane / 8, unit lane % 8, which holds the row's unit (lane % 8) ^ rw_wswz(row);
+  // DX: flat unit idx of [128 n][4 NI], holding unit (idx % 4 NI) ^ rw_dswz(n) of row n
   uint32_t vw[NI];
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
-    const int R = (NI * w + i) * 8 + (lane >> 3);
-    const int64_t grow = r0 + R;
-    vw[i] = grow < a.Ncols ? (uint32_t)(grow * a.ldq + 16 * ((lane & 7) ^ rw_wswz(R))) : OOB;
+    if constexpr (MODE == 0) {
+      const int R = (NI * w + i) * 8 + (lane >> 3);
+      const int64_t grow = r0 + R;
+      vw[i] = grow < a.Ncols ? (uint32_t)(grow * a.ldq + 16 * ((lane & 7) ^ rw_wswz(R))) : OOB;
+    } else {
+      const int idx = (NI * w + i) * 64 + lane, n = idx / (4 * NI);
+      const int64_t col = r0 + 16 * ((idx % (4 * NI)) ^ rw_dswz<NI>(n));
+      vw[i] = col < a.Ncols ? (uint32_t)(n * a.ldq + col) : OOB;
+    }
   }
+  const uint32_t wstep = MODE == 0 ? 128u : (uint32_t)(128 * a.ldq);
   auto at = [&](int s) { const int v = s + rot; return v >= nsteps ? v - nsteps : v; };
   auto issue = [&](int s, int slot) {
     const bool ok = s < nsteps;
     const int sr = at(s);
-    const uint32_t sx = ok ? (uint32_t)sr * 256u : PAST, sw = ok ? (uint32_t)sr * 128u : PAST;
+    const uint32_t sx = ok ? (uint32_t)sr * 256u : PAST, sw = ok ? (uint32_t)sr * wstep : PAST;
     uint8_t* base = smem + slot * STEP;
 #pragma unroll
     for (int j = 0; j < XL; ++j) dma16(rx, vx[j], sx, base + (8 * j + w) * 1024);
@@ -1066,27 +827,63 @@ __device__ __forceinline__ void rw_acc_dma(const SkArgs& a, int64_t r0, int64_t 
     asm volatile("" ::: "memory");
     issue(s + L, (slot + L) % RS);
     const uint8_t* base = smem + slot * STEP;
-    // codes of rows 16 i + l16 (unit 4 par + g: k = 64 par + 16 g + (0..15)), then the
-    // activations (unit 2 g + e of the par half: k = 64 par + 16 g + 8 e + (0..7))
+    V8 af[NI][2];
     u32x4 cv[NI];
+    if constexpr (MODE == 0) {
+      // codes of rows 16 i + l16 (unit 4 par + g: k = 64 par + 16 g + (0..15)), read before the
+      // activations (unit 2 g + e of the par half: k = 64 par + 16 g + 8 e + (0..7))
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int row = 16 * NI * wr + 16 * i + l16;
-      cv[i] = *reinterpret_cast<const u32x4*>(base + SLOT + row * 128 + (((4 * par + g) ^ rw_wswz(row)) << 4));
+      for (int i = 0; i < NI; ++i) {
+        const int row = 16 * NI * wr + 16 * i + l16;
+        cv[i] = *reinterpret_cast<const u32x4*>(base + SLOT + row * 128 + (((4 * par + g) ^ rw_wswz(row)) << 4));
+      }
     }
     const uint8_t* xs = base + par * (BN * 128);
-    const int sw = rw_swz<0>(l16);
+    const int sw = rw_swz<MODE>(l16);
     u32x4 xv[2][To];
 #pragma unroll
     for (int e = 0; e < 2; ++e)
 #pragma unroll
-      for (int tt = 0; tt < To; ++tt)
-        xv[e][tt] = *reinterpret_cast<const u32x4*>(xs + (16 * tt + l16) * 128 + (((2 * g + e) ^ sw) << 4));
-    V8 af[NI][2];
+      for (int tt = 0; tt < To; ++tt) {
+        // FWD: k = 16 g + 8 e + (0..7) (unit 2 g + e); DX: n = 32 e + 8 g + (0..7) (unit 4 e + g)
+        const int unit = MODE == 0 ? 2 * g + e : 4 * e + g;
+        xv[e][tt] = *reinterpret_cast<const u32x4*>(xs + (16 * tt + l16) * 128 + ((unit ^ sw) << 4));
+      }
+    if constexpr (MODE == 0) {
 #pragma unroll
-    for (int i = 0; i < NI; ++i)
+      for (int i = 0; i < NI; ++i)
 #pragma unroll
-      for (int e = 0; e < 2; ++e) af[i][e] = E::from_i8x8(cv[i][2 * e], cv[i][2 * e + 1]);
+        for (int e = 0; e < 2; ++e) af[i][e] = E::from_i8x8(cv[i][2 * e], cv[i][2 * e + 1]);
+    } else {
+      // per 16-k tile i and half e the transposed read: providing lane p of a 16-lane group
+      // addresses row n = 64 par + 32 e + 8 g + p / 2, unit NI wr + i, bytes 8 (p % 2) .. +7;
+      // lane l16 receives k = 16 (NI wr + i) + l16, n = 64 par + 32 e + 8 g + (0..7), each code
+      // scaled by s[n] (the zero codes of a step past the operands may take any scale)
+      const int64_t nb = s < nsteps ? (int64_t)(2 * at(s) + par) * 64 : 0;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const f32x4 s0 = *reinterpret_cast<const f32x4*>(stab + nb + 32 * e + 8 * g);
+        const f32x4 s1 = *reinterpret_cast<const f32x4*>(stab + nb + 32 * e + 8 * g + 4);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          const int row = 64 * par + 32 * e + 8 * g + (l16 >> 1);
+          const uint8_t* p = base + SLOT + row * (64 * NI) + (((NI * wr + i) ^ rw_dswz<NI>(row)) << 4) + 8 * (l16 & 1);
+          const i32x2 v = __builtin_amdgcn_ds_read_tr8_b64_v2i32(LDS_PTR(i32x2, p));
+          if constexpr (ELT == REELS_HIP_F16) {  // Float16(q) * Float16(s[n])
+            const u32x4 s16 = {E::pack2(s0[0], s0[1]), E::pack2(s0[2], s0[3]),
+                               E::pack2(s1[0], s1[1]), E::pack2(s1[2], s1[3])};
+            af[i][e] = E::scale8(E::from_i8x8((uint32_t)v[0], (uint32_t)v[1]), s16);
+          } else {  // bf16(fl32(q * s[n]))
+            const uint32_t lo = (uint32_t)v[0], hi = (uint32_t)v[1];
+            const u32x4 o = {E::pack2_fast((float)(int8_t)(lo & 0xffu) * s0[0], (float)(int8_t)((lo >> 8) & 0xffu) * s0[1]),
+                             E::pack2_fast((float)(int8_t)((lo >> 16) & 0xffu) * s0[2], (float)((int32_t)lo >> 24) * s0[3]),
+                             E::pack2_fast((float)(int8_t)(hi & 0xffu) * s1[0], (float)(int8_t)((hi >> 8) & 0xffu) * s1[1]),
+                             E::pack2_fast((float)(int8_t)((hi >> 16) & 0xffu) * s1[2], (float)((int32_t)hi >> 24) * s1[3])};
+            af[i][e] = E::as8(o);
+          }
+        }
+      }
+    }
 #pragma unroll
     for (int e = 0; e < 2; ++e)
 #pragma unroll
@@ -1195,8 +992,7 @@ __device__ __forceinline__ void rw_block(const SkArgs& a, int rb, int tbo, uint8
     // a rotation per row block (the token tiles of one row block read its weight rows together)
     const int nsteps = (int)(a.Kred / 128);
     const int rot = (int)(((int64_t)rb * 7) % nsteps);
-    if constexpr (MODE == 0) rw_acc_dma<To, NI, ELT>(a, r0, tok0, rot, smem, acc);
-    else rw_acc<To, NI, MODE, ELT>(a, r0, tok0, rot, smem, acc);
+    rw_acc_dma<To, NI, MODE, ELT>(a, r0, tok0, rot, smem, acc);
     // waves 4-7 give their first half of the token tiles, waves 0-3 their second, through LDS;
     // each then adds (partner + own, wave w's value first: the same sum for both halves)
     f32x4* ex = reinterpret_cast<f32x4*>(smem);
@@ -1346,9 +1142,7 @@ constexpr int kRwLdsMax = 160 * 1024;
 
 static int rw_lds_bytes(int NI, int To, int mode, int64_t Kred) {
   const int slot = 2 * 16 * To * 128, ta = To <= 4 ? To : To / 2;
-  const int G = rw_group(To, mode, NI);
-  int v = mode == 0 ? rw_fslots(To, NI) * (slot + rw_wslot(NI))
-                    : 2 * G * slot + align16((int)Kred * 4) + 2 * G * rw_wslot(NI);
+  int v = rw_fslots(To, NI, mode) * (slot + rw_wslot(NI)) + (mode == 1 ? align16((int)Kred * 4) : 0);
   v = std::max(v, 8 * NI * (To / 2) * 1024);
   v = std::max(v, skinny_lds(ta));
   v = std::max(v, 8 * 1024 * NI);
@@ -1356,7 +1150,7 @@ static int rw_lds_bytes(int NI, int To, int mode, int64_t Kred) {
 }
 
 static bool rw_choose(int64_t M, int64_t Kred, int64_t Ncols, int rp, int mode, SkinnyPlan& out) {
-  if (M <= 0 || Kred % 128 != 0 || Ncols % 64 != 0 || Kred > 16384) return false;
+  if (M <= 0 || Kred % 128 != 0 || Ncols % 64 != 0 || Kred > (mode == 1 ? kRwDxMaxRed : 16384)) return false;
   // the kernel moves steps past the operands with a scalar offset of 2^30 bytes
   if (M * Kred * 2 > ((int64_t)1 << 30) || Ncols * Kred > ((int64_t)1 << 30)) return false;
   bool found = false;
