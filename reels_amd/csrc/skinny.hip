@@ -738,18 +738,17 @@ template <int NI> __device__ __forceinline__ int rw_dswz(int row) {
 // The same products with both operands copied from memory straight into LDS by the buffer unit
 // (buffer_load ... lds), no register staging: a ring of RS step slots (activations
 // [2 par][16 To tokens][128 bytes] as above, then the codes: FWD [64 NI rows][128 bytes], units
-// XOR-swizzled by rw_wswz; DX [128 n][64 NI bytes], units swizzled by rw_dswz), the copies of
-// step s + L = s + RS - 1 issued right after the barrier that opens step s. At that barrier every wave has finished reading the previous
-// step's slot (lgkmcnt(0)) and waited for its own copies of step s (the copies of the L - 1 later
-// steps may stay in flight), so the barrier publishes step s and frees slot (s - 1) % RS, which
-// the new copies fill. Copies past the reduction read zeros (a 2^30-byte offset past the
-// descriptor) into slots nobody reads; the last of them are drained before returning.
-// DX keeps the block's scales s[0 .. Kred) beside the ring: Kred up to kRwDxMaxRed
-constexpr int kRwDxMaxRed = 8192;
+// XOR-swizzled by rw_wswz; DX [128 n][64 NI bytes], units swizzled by rw_dswz, then the step's
+// 128 scales s[n] in a 1 KiB tail, copied by wave 0), the copies of step s + L = s + RS - 1
+// issued right after the barrier that opens step s. At that barrier every wave has finished
+// reading the previous step's slot (lgkmcnt(0)) and waited for its own copies of step s (the
+// copies of the L - 1 later steps may stay in flight), so the barrier publishes step s and frees
+// slot (s - 1) % RS, which the new copies fill. Copies past the reduction read zeros (a
+// 2^30-byte offset past the descriptor) into slots nobody reads; the last of them are drained
+// before returning.
+constexpr int rw_fstep(int To, int NI, int MODE) { return 2 * 16 * To * 128 + rw_wslot(NI) + (MODE == 1 ? 1024 : 0); }
 constexpr int rw_fslots(int To, int NI, int MODE) {
-  return ((160 * 1024 - 16 - (MODE == 1 ? 4 * kRwDxMaxRed : 0)) / (2 * 16 * To * 128 + rw_wslot(NI))) > 8
-             ? 8
-             : ((160 * 1024 - 16 - (MODE == 1 ? 4 * kRwDxMaxRed : 0)) / (2 * 16 * To * 128 + rw_wslot(NI)));
+  return (160 * 1024 - 16) / rw_fstep(To, NI, MODE) > 8 ? 8 : (160 * 1024 - 16) / rw_fstep(To, NI, MODE);
 }
 
 template <int To, int NI, int MODE, int ELT>
@@ -758,7 +757,7 @@ __device__ __forceinline__ void rw_acc_dma(const SkArgs& a, int64_t r0, int64_t 
   using E = Elt<ELT>;
   typedef typename E::v8 V8;
   constexpr int BN = 16 * To, XL = To / 2, SLOT = 2 * BN * 128, WSLOT = rw_wslot(NI);
-  constexpr int RS = rw_fslots(To, NI, MODE), L = RS - 1, STEP = SLOT + WSLOT;
+  constexpr int RS = rw_fslots(To, NI, MODE), L = RS - 1, STEP = rw_fstep(To, NI, MODE);
   static_assert(RS >= 3, "at least two steps in flight");
   constexpr uint32_t OOB = 0x80000000u, PAST = 0x40000000u;
   const int t = threadIdx.x, lane = t & 63;
@@ -768,12 +767,9 @@ __device__ __forceinline__ void rw_acc_dma(const SkArgs& a, int64_t r0, int64_t 
   const int nsteps = (int)(a.Kred / 128);
   const i32x4 rx = buffer_rsrc(a.act, (uint32_t)(a.M * a.Kred * 2));
   const i32x4 rq = buffer_rsrc(a.q, (uint32_t)((MODE == 0 ? a.Ncols : a.Kred) * a.ldq));
-  // DX: the block's scales after the ring, published by the barrier that opens step 0
-  float* stab = reinterpret_cast<float*>(smem + RS * STEP);
-  if constexpr (MODE == 1) {
-    for (int i = t; i < (int)a.Kred / 4; i += 64 * sk::NWV)
-      reinterpret_cast<f32x4*>(stab)[i] = reinterpret_cast<const f32x4*>(a.s)[i];
-  }
+  // DX: wave 0's lanes 0-31 copy a step's 128 scales (lanes 32-63 read zeros past the descriptor)
+  const i32x4 rs = buffer_rsrc(a.s, (uint32_t)(MODE == 1 ? a.Kred * 4 : 0));
+  const uint32_t vsc = lane < 32 ? (uint32_t)lane * 16u : OOB;
   // activations: copy j of wave w fills LDS unit (8 j + w) 64 + lane of the slot (as rw_acc)
   uint32_t vx[XL];
 #pragma unroll
@@ -811,6 +807,7 @@ __device__ __forceinline__ void rw_acc_dma(const SkArgs& a, int64_t r0, int64_t 
     for (int j = 0; j < XL; ++j) dma16(rx, vx[j], sx, base + (8 * j + w) * 1024);
 #pragma unroll
     for (int i = 0; i < NI; ++i) dma16(rq, vw[i], sw, base + SLOT + (NI * w + i) * 1024);
+    if (MODE == 1 && w == 0) dma16(rs, vsc, ok ? (uint32_t)sr * 512u : PAST, base + SLOT + WSLOT);
   };
 #pragma unroll
   for (int i = 0; i < NI; ++i)
@@ -818,11 +815,13 @@ __device__ __forceinline__ void rw_acc_dma(const SkArgs& a, int64_t r0, int64_t 
     for (int tt = 0; tt < To; ++tt) acc[i][tt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   // the wait that opens a step: this wave's LDS reads done, its copies of the step landed (the
   // copies of the L - 1 steps after it may stay in flight)
-  constexpr int NV = (L - 1) * (XL + NI);
-  static_assert(NV < 64, "vmcnt field");
+  constexpr int NV = (L - 1) * (XL + NI), NV0 = (L - 1) * (XL + NI + (MODE == 1 ? 1 : 0));
+  static_assert(NV0 < 64, "vmcnt field");
   constexpr int WAIT = (NV & 15) | ((NV >> 4) << 14) | (7 << 4);  // lgkmcnt(0), vmcnt(NV)
+  constexpr int WAIT0 = (NV0 & 15) | ((NV0 >> 4) << 14) | (7 << 4);  // wave 0 (DX: the scales)
   auto step = [&](int s, int slot) {
-    __builtin_amdgcn_s_waitcnt(WAIT);
+    if (w == 0) __builtin_amdgcn_s_waitcnt(WAIT0);
+    else __builtin_amdgcn_s_waitcnt(WAIT);
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     issue(s + L, (slot + L) % RS);
@@ -858,12 +857,12 @@ __device__ __forceinline__ void rw_acc_dma(const SkArgs& a, int64_t r0, int64_t 
       // per 16-k tile i and half e the transposed read: providing lane p of a 16-lane group
       // addresses row n = 64 par + 32 e + 8 g + p / 2, unit NI wr + i, bytes 8 (p % 2) .. +7;
       // lane l16 receives k = 16 (NI wr + i) + l16, n = 64 par + 32 e + 8 g + (0..7), each code
-      // scaled by s[n] (the zero codes of a step past the operands may take any scale)
-      const int64_t nb = s < nsteps ? (int64_t)(2 * at(s) + par) * 64 : 0;
+      // scaled by s[n] from the slot's scales
+      const float* sc = reinterpret_cast<const float*>(base + SLOT + WSLOT) + 64 * par;
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
-        const f32x4 s0 = *reinterpret_cast<const f32x4*>(stab + nb + 32 * e + 8 * g);
-        const f32x4 s1 = *reinterpret_cast<const f32x4*>(stab + nb + 32 * e + 8 * g + 4);
+        const f32x4 s0 = *reinterpret_cast<const f32x4*>(sc + 32 * e + 8 * g);
+        const f32x4 s1 = *reinterpret_cast<const f32x4*>(sc + 32 * e + 8 * g + 4);
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
           const int row = 64 * par + 32 * e + 8 * g + (l16 >> 1);
@@ -1142,7 +1141,8 @@ constexpr int kRwLdsMax = 160 * 1024;
 
 static int rw_lds_bytes(int NI, int To, int mode, int64_t Kred) {
   const int slot = 2 * 16 * To * 128, ta = To <= 4 ? To : To / 2;
-  int v = rw_fslots(To, NI, mode) * (slot + rw_wslot(NI)) + (mode == 1 ? align16((int)Kred * 4) : 0);
+  (void)Kred;
+  int v = rw_fslots(To, NI, mode) * rw_fstep(To, NI, mode);
   v = std::max(v, 8 * NI * (To / 2) * 1024);
   v = std::max(v, skinny_lds(ta));
   v = std::max(v, 8 * 1024 * NI);
@@ -1150,7 +1150,7 @@ static int rw_lds_bytes(int NI, int To, int mode, int64_t Kred) {
 }
 
 static bool rw_choose(int64_t M, int64_t Kred, int64_t Ncols, int rp, int mode, SkinnyPlan& out) {
-  if (M <= 0 || Kred % 128 != 0 || Ncols % 64 != 0 || Kred > (mode == 1 ? kRwDxMaxRed : 16384)) return false;
+  if (M <= 0 || Kred % 128 != 0 || Ncols % 64 != 0 || Kred > 16384) return false;
   // the kernel moves steps past the operands with a scalar offset of 2^30 bytes
   if (M * Kred * 2 > ((int64_t)1 << 30) || Ncols * Kred > ((int64_t)1 << 30)) return false;
   bool found = false;

@@ -196,3 +196,28 @@ def test_thousand_tokens_on_a_small_weight(dev):
     assert_parity(bf16_f32(dx), go["dx"], "1024 tokens dx")
     assert_parity(dA.cpu().numpy(), go["dA"], "1024 tokens dA")
     assert_parity(dB.cpu().numpy(), go["dB"], "1024 tokens dB")
+
+
+def test_row_wave_dx_over_a_long_reduction(dev):
+    """dX on row-wave tiles over a reduction longer than the split tiles' scale table held: 200
+    tokens on a 1536 -> 8960 weight (dX reduces over the 8960 outputs; the row-wave dX copies
+    each step's 128 scales with its codes). y, h, dx, dA, dB against the oracle, and the same
+    bits when repeated."""
+    import torch
+    from reels_amd import i8lora_backward, i8lora_forward
+    M, K, N, r = 200, 1536, 8960, 32
+    host, d = _case(dev, M, K, N, r, 4800)
+    c = 1.0
+    print("[skinny] row-wave dX, 200 tokens on 1536 -> 8960", flush=True)
+    y, h = i8lora_forward(d["x"], d["W"], d["A"], d["B"], None, c, save_h=True)
+    dx, dA, dB = i8lora_backward(d["dy"], d["x"], d["W"], d["A"], d["B"], c, h=h)
+    dx2, _, _ = i8lora_backward(d["dy"], d["x"], d["W"], d["A"], d["B"], c, h=h)
+    torch.cuda.synchronize()
+    assert torch.equal(dx, dx2)
+    yo, ho = oracle.lora_forward(host["x"], host["q"], host["s"], host["A"], host["B"], c)
+    go = oracle.lora_backward(host["dy"], host["x"], host["q"], host["s"], host["A"], host["B"], c)
+    assert_parity(bf16_f32(y), yo, "long-reduction y")
+    assert_parity(bf16_f32(h), ho, "long-reduction h")
+    assert_parity(bf16_f32(dx), go["dx"], "long-reduction dx")
+    assert_parity(dA.cpu().numpy(), go["dA"], "long-reduction dA")
+    assert_parity(dB.cpu().numpy(), go["dB"], "long-reduction dB")
