@@ -988,9 +988,13 @@ __device__ __forceinline__ void rw_block(const SkArgs& a, int rb, int tbo, uint8
   f32x4 sum[NI][TH];
   {
     f32x4 acc[NI][To];
-    // a rotation per row block (the token tiles of one row block read its weight rows together)
+    // The walk over the reduction starts at a rotation per XCD (block b runs on XCD b % 8): the
+    // blocks of one XCD walk together, so the activations of a token tile that several row
+    // blocks read meet in that XCD's L2, and the 8 XCDs' weight reads spread over the channels.
+    // (A rotation per row block spread the channels as well but re-fetched the activations per
+    // row block: 512 tokens on 5120 x 5120 40.4 against 35.1 us forward.)
     const int nsteps = (int)(a.Kred / 128);
-    const int rot = (int)(((int64_t)rb * 7) % nsteps);
+    const int rot = (int)(((int64_t)(blockIdx.x & 7) * nsteps) / 8);
     rw_acc_dma<To, NI, MODE, ELT>(a, r0, tok0, rot, smem, acc);
     // waves 4-7 give their first half of the token tiles, waves 0-3 their second, through LDS;
     // each then adds (partner + own, wave w's value first: the same sum for both halves)
