@@ -34,8 +34,11 @@
 //      through ds_read_b64_tr_b8 from a per-wave LDS tile.
 #include "i8gemm.h"
 
+#include <atomic>
+#include <chrono>
 #include <cstdlib>
 #include <mutex>
+#include <random>
 
 namespace reels {
 
@@ -51,8 +54,8 @@ constexpr int kMaxTiles = 4096;
 constexpr uint32_t kSpinLimit = 1u << 12;  // wait rounds of s_sleep 8 (about 1 ms) before computing l
 }  // namespace sk
 
-// one launch's counters, zero when it starts: this header, then one word per tile (the blocks of
-// the tile that have stored their partial)
+// one split-tile launch's counters, zero when it starts: this header, then one word per tile (the
+// blocks of the tile that have stored their partial). Row-wave launches use keys instead.
 struct SkCounters {
   uint32_t hdone;    // adapter tiles finished
   uint32_t hready;   // 1: l complete (set by the last adapter tile)
@@ -74,6 +77,8 @@ struct SkArgs {
   uint16_t* lsave;      // [M][ld_lsave], lsave_cols columns (or NULL)
   SkCounters* ctr;
   uint32_t* tiles;      // [nblk * tb + lblk * tb], right after *ctr
+  uint32_t* keys;       // row-wave launches: [nta] l ready, then [nta][S] split partial stored
+  uint32_t nonce_lo, nonce_hi;  // row-wave launches: the host call's nonce (first key words)
   int64_t M, Kred, Ncols, ldq, ldr, ld_lsave;
   float c;
   int r, rp, S, nblk, lblk, tb, lsave_cols;
@@ -116,6 +121,47 @@ __device__ __forceinline__ void sk_store(uint32_t* p, uint32_t v) {
 __device__ __forceinline__ void sk_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t sk_rsrc(const void* p, int64_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+// Row-wave launches hand l and the adapter tiles' split partials over under a key rather than
+// counters, so nothing has to zero memory before the launch (a zeroing launch in front cost about
+// 4 us per call, a tenth of a 512-token forward). A key is 16 bytes: the host call's nonce (two
+// words), the dispatch's packet index in its queue and the queue's address. A (queue, packet
+// index) pair names one dispatch for the queue's life, graph replays included, and the nonce
+// differs between host calls and between processes, so whatever an earlier launch (or anything
+// else) left in the workspace does not hold this launch's key. A block stores its data, waits for
+// those stores (vmcnt 0 in every wave, then the barrier), and then thread 0 stores the key with
+// one 16-byte device-scope store; a reader loads the key with device-scope loads and issues its
+// data loads after seeing it.
+extern "C" __device__ uint64_t reels_dispatch_id() __asm("llvm.amdgcn.dispatch.id");
+__device__ __forceinline__ u32x4 sk_key(const SkArgs& a) {
+  const uint64_t did = reels_dispatch_id();
+  const uint64_t q = (uint64_t)__builtin_amdgcn_queue_ptr();
+  return u32x4{a.nonce_lo, a.nonce_hi, (uint32_t)did, (uint32_t)(q >> 6) ^ (uint32_t)(did >> 32)};
+}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t sk_keys_rsrc(const SkArgs& a) {
+  return sk_rsrc(a.keys, (int64_t)a.nta * (1 + a.S) * 16);
+}
+__device__ __forceinline__ void sk_put_key(const SkArgs& a, int idx, u32x4 key) {
+  __builtin_amdgcn_raw_buffer_store_b128(key, sk_keys_rsrc(a), (uint32_t)idx * 16u, 0, kSC1);
+}
+// whether entry idx holds the key (reloaded on every call: the clobber keeps the compiler from
+// reusing an earlier load)
+__device__ __forceinline__ bool sk_has_key(const SkArgs& a, int idx, u32x4 key) {
+  asm volatile("" ::: "memory");
+  const u32x4 v = __builtin_bit_cast(
+      u32x4, __builtin_amdgcn_raw_buffer_load_b128(sk_keys_rsrc(a), (uint32_t)idx * 16u, 0, kSC1));
+  return v[0] == key[0] && v[1] == key[1] && v[2] == key[2] && v[3] == key[3];
+}
+// waits for the key at entry idx, spending the shared budget of wait rounds (s_sleep 8 each);
+// false once the budget is spent without it. A budget of 0 (tests) looks at nothing.
+__device__ __forceinline__ bool sk_wait_key(const SkArgs& a, int idx, u32x4 key, uint32_t& rounds) {
+  if (a.spin == 0u) return false;
+  while (!sk_has_key(a, idx, key)) {
+    if (++rounds > a.spin) return false;
+    __builtin_amdgcn_s_sleep(8);
+  }
+  return true;
 }
 
 // One wave's share of a (row block, split, token block): acc[i][tt] = rows 16 i + (0..15) x
@@ -451,9 +497,13 @@ __device__ __forceinline__ void skinny_put_l(const SkArgs& a, int64_t o0, int64_
 }
 
 // One block: its accumulators, the tile's split reduction when it arrives last, then the tile's
-// results (l for an adapter tile, out for an output tile).
-template <int T, int MODE, int ELT, bool LORA>
+// results (l for an adapter tile, out for an output tile). KEYED (the adapter tiles of a row-wave
+// launch): split 0 of a tile reduces it, after the other splits have stored their partials under
+// the launch's key (a split that has not after a bounded wait it computes itself, with that
+// split's code: the same bits), and the tile's l is announced under the key too.
+template <int T, int MODE, int ELT, bool LORA, bool KEYED = false>
 __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, uint8_t* smem) {
+  static_assert(!KEYED || LORA, "keyed hand-over: adapter tiles only");
   using E = Elt<ELT>;
   constexpr bool lora = LORA;
   const int t = threadIdx.x, lane = t & 63;
@@ -520,21 +570,40 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
     const int64_t tbase = lora ? a.lpart0 + (int64_t)(d.tile - a.ntm) * a.S * (NF * 64)
                                : (int64_t)d.tile * a.S * (NF * 64);
     const __amdgpu_buffer_rsrc_t rp_ = sk_rsrc(reinterpret_cast<f32x4*>(a.part) + tbase, (int64_t)a.S * NF * 64 * 16);
+    if (KEYED && sp == 0) {
+      // split 0 keeps its partial in registers and waits for the others'
+      if (t == 0) {
+        const u32x4 key = sk_key(a);
+        const int k0 = a.nta + (d.tile - a.ntm) * a.S;
+        uint32_t seen = 0, rounds = 0;
+        for (int s = 1; s < a.S; ++s)
+          if (sk_wait_key(a, k0 + s, key, rounds)) seen |= 1u << s;
+        words[1] = seen;
+      }
+      __syncthreads();
+    } else {
 #pragma unroll
-    for (int k = 0; k < FPW; ++k) {
-      const int f = w + sk::NWV * k;
-      if (f < NF)
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sum[k]), rp_,
-                                               (uint32_t)((sp * (NF * 64) + f * 64 + lane) * 16), 0, kSC1);
+      for (int k = 0; k < FPW; ++k) {
+        const int f = w + sk::NWV * k;
+        if (f < NF)
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sum[k]), rp_,
+                                                 (uint32_t)((sp * (NF * 64) + f * 64 + lane) * 16), 0, kSC1);
+      }
+      sk_drain();
+      if (wants_l && up) load_l(0, hv);
+      __syncthreads();
+      if constexpr (KEYED) {
+        if (t == 0) sk_put_key(a, a.nta + (d.tile - a.ntm) * a.S + sp, sk_key(a));
+        return;
+      }
+      if (t == 0) {
+        words[1] = sk_add(&a.tiles[d.tile], 1u);
+      }
+      __syncthreads();
+      if (words[1] != (uint32_t)a.S - 1) return;
     }
-    sk_drain();
-    if (wants_l && up) load_l(0, hv);
-    __syncthreads();
-    if (t == 0) {
-      words[1] = sk_add(&a.tiles[d.tile], 1u);
-    }
-    __syncthreads();
-    if (words[1] != (uint32_t)a.S - 1) return;
+    // the splits whose partial is loaded: all but this block's (keyed: those seen under the key)
+    const uint32_t have = KEYED ? words[1] : ~(1u << sp);
     asm volatile("" ::: "memory");
     // the tile's sum in split order: the other splits' partials in one batch (up to SB splits)
     constexpr int SB = 4;
@@ -549,10 +618,22 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
         for (int k = 0; k < FPW; ++k) {
           const int f = w + sk::NWV * k, s = s0 + u;
           v[u][k] = sum[k];
-          if (f < NF && s < a.S && s != sp)
+          if (f < NF && s < a.S && s != sp && ((have >> s) & 1u))
             v[u][k] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                                     rp_, (uint32_t)((s * (NF * 64) + f * 64 + lane) * 16), 0, kSC1));
         }
+      if constexpr (KEYED) {
+        // (block-uniform) the splits not seen: their partials computed here
+#pragma unroll
+        for (int u = 0; u < SB; ++u) {
+          const int s = s0 + u;
+          if (s < a.S && s != sp && !((have >> s) & 1u)) {
+            f32x4 acc[NI][T];
+            skinny_acc<T, MODE, ELT, LORA>(a, blk, s, tok0, smem, acc);
+            skinny_sum<T, NI>(acc, smem, v[u]);
+          }
+        }
+      }
 #pragma unroll
       for (int u = 0; u < SB; ++u)
         if (s0 + u < a.S) {
@@ -572,7 +653,9 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
     skinny_put_l<T, ELT>(a, o0, tok0, sum, true);
     sk_drain();
     __syncthreads();
-    if (t == 0) {
+    if constexpr (KEYED) {
+      if (t == 0) sk_put_key(a, d.tile - a.ntm, sk_key(a));
+    } else if (t == 0) {
       const uint32_t old = sk_add(&ctr->hdone, 1u);
       if (old == (uint32_t)a.nta - 1 && a.ntm > 0) sk_store(&ctr->hready, 1u);
     }
@@ -980,10 +1063,7 @@ __device__ __forceinline__ void rw_block(const SkArgs& a, int rb, int tbo, uint8
   const int64_t ob = r0 + 16 * NI * wr;          // the wave's first output row
   const int64_t tw0 = tok0 + (int64_t)par * (16 * TH);  // the wave's first token after the pair sum
   uint32_t* words = reinterpret_cast<uint32_t*>(smem + lds_bytes - 16);
-  SkCounters* ctr = a.ctr;
   const bool wants_l = a.nad > 0;
-  uint32_t up = 0;
-  if (wants_l) up = sk_load(&ctr->hready);
 
   f32x4 sum[NI][TH];
   {
@@ -1019,22 +1099,22 @@ __device__ __forceinline__ void rw_block(const SkArgs& a, int rb, int tbo, uint8
   }
 
   if (wants_l) {
-    // the adapter blocks come first in the logical order and wait for nothing, so the flag is
-    // normally up; after a bounded wait the block computes l for its tokens itself, with the
-    // adapter blocks' code, splits and order (the same bits)
+    // the adapter tiles of this tile's tokens: they come first in the logical order and wait for
+    // nothing but their splits, so their keys are normally there; after a bounded wait the block
+    // computes l for its tokens itself, with the adapter blocks' code, splits and order (the same
+    // bits)
+    const int tb_lo = (int)(tok0 / (16 * Ta));
+    const int tb_hi = std::min((int)((tok0 + 16 * To + 16 * Ta - 1) / (16 * Ta)), a.tb);
     if (t == 0) {
-      uint32_t n = 0, v = up;
-      while (v == 0u && ++n <= a.spin) {
-        __builtin_amdgcn_s_sleep(8);
-        v = sk_load(&ctr->hready);
-      }
-      words[2] = v;
+      const u32x4 key = sk_key(a);
+      uint32_t rounds = 0, ok = 1;
+      for (int lb = 0; lb < a.lblk && ok; ++lb)
+        for (int tba = tb_lo; tba < tb_hi && ok; ++tba) ok = sk_wait_key(a, lb * a.tb + tba, key, rounds);
+      words[2] = ok;
     }
     __syncthreads();
     if (words[2] == 0u) {
-      const int tb_lo = (int)(tok0 / (16 * Ta));
-      const int tb_hi = (int)((tok0 + 16 * To + 16 * Ta - 1) / (16 * Ta));
-      for (int tba = tb_lo; tba < tb_hi && tba < a.tb; ++tba)
+      for (int tba = tb_lo; tba < tb_hi; ++tba)
         for (int lb = 0; lb < a.lblk; ++lb) {
           constexpr int FA = sk_fpw<2 * Ta>();
           f32x4 tl[FA];
@@ -1105,7 +1185,7 @@ __global__ __launch_bounds__(64 * sk::NWV, 1) void skinny_rw_kernel(SkArgs a, in
     const int rb = rest / a.S;
     d.blk = a.nblk + rb;
     d.tile = a.ntm + rb * a.tb + d.tb;
-    skinny_block<Ta, MODE, ELT, true>(a, d, smem);
+    skinny_block<Ta, MODE, ELT, true, true>(a, d, smem);
   } else {
     const int ti = tk - a.nad;
     rw_block<To, NI, Ta, MODE, ELT>(a, ti / a.otb, ti % a.otb, smem, lds_bytes);
@@ -1248,7 +1328,9 @@ static SkWs skinny_ws(const SkinnyPlan& p, int64_t M, int64_t Ncols, int rp) {
   w.part = 0;
   w.hl = align_up(p.S > 1 ? frags * p.S * 64 * 16 : 0, 256);
   w.ctr = align_up(w.hl + (size_t)M * rp * 2, 256);
-  w.total = align_up(w.ctr + (size_t)(kSkCounterHeaderWords + w.ntiles) * 4, 256);
+  // split tiles: the counters; row-wave tiles: the adapter tiles' keys (l ready, then per split)
+  const size_t nta = (size_t)ceil_div(rp, sk::NBL) * p.tb;
+  w.total = align_up(w.ctr + (p.rw ? nta * (1 + p.S) * 16 : (size_t)(kSkCounterHeaderWords + w.ntiles) * 4), 256);
   return w;
 }
 
@@ -1280,6 +1362,17 @@ static hipError_t launch_rw_t(const SkArgs& a, int lds, hipStream_t st) {
   if (attr != hipSuccess) return attr;
   skinny_rw_kernel<To, NI, Ta, MODE, ELT><<<dim3((unsigned)a.blocks), 64 * sk::NWV, lds, st>>>(a, lds);
   return hipSuccess;
+}
+
+// the nonce of a row-wave launch's keys: a process-wide count from a random start (so two
+// processes, or two calls, do not share one)
+static uint64_t sk_next_nonce() {
+  static std::atomic<uint64_t> next{[] {
+    std::random_device rd;
+    const uint64_t t = (uint64_t)std::chrono::steady_clock::now().time_since_epoch().count();
+    return (((uint64_t)rd() << 32) ^ (uint64_t)rd() ^ (t * 0x9E3779B97F4A7C15ull));
+  }()};
+  return next.fetch_add(1, std::memory_order_relaxed);
 }
 
 int launch_skinny(int mode, int elt, const SkinnyPlan& p, const uint16_t* act, const int8_t* q,
@@ -1316,11 +1409,19 @@ int launch_skinny(int mode, int elt, const SkinnyPlan& p, const uint16_t* act, c
   a.hl = (lsave != nullptr && ld_lsave == a.rp && lsave_cols >= a.rp) ? lsave : hl;
   a.ctr = reinterpret_cast<SkCounters*>(wb + w.ctr);
   a.tiles = reinterpret_cast<uint32_t*>(wb + w.ctr) + kSkCounterHeaderWords;
-  {
-    TraceScope _ts(st, "skinny_clear_kernel");
-    skinny_clear_kernel<<<1, 256, 0, st>>>(reinterpret_cast<uint32_t*>(a.ctr), kSkCounterHeaderWords + w.ntiles);
+  a.keys = reinterpret_cast<uint32_t*>(wb + w.ctr);
+  if (p.rw) {
+    const uint64_t nonce = sk_next_nonce();
+    a.nonce_lo = (uint32_t)nonce;
+    a.nonce_hi = (uint32_t)(nonce >> 32);
+  } else {
+    a.nonce_lo = a.nonce_hi = 0u;
+    {
+      TraceScope _ts(st, "skinny_clear_kernel");
+      skinny_clear_kernel<<<1, 256, 0, st>>>(reinterpret_cast<uint32_t*>(a.ctr), kSkCounterHeaderWords + w.ntiles);
+    }
+    if (int rc = check_launch("skinny_clear_kernel")) return rc;
   }
-  if (int rc = check_launch("skinny_clear_kernel")) return rc;
 
   hipError_t attr = hipSuccess;
   if (p.rw) {

@@ -1,12 +1,16 @@
 """The few-token path's single launch (reels_amd/csrc/skinny.hip): output tiles wait for the
 adapter's rank projection l, published by the adapter blocks of the same launch, and a tile that
-stops waiting computes l itself with the adapter blocks' code and order. Its counters live in
-the call's own workspace, cleared by a one-block kernel just before the launch.
+stops waiting computes l itself with the adapter blocks' code and order. With split tiles the
+counters live in the call's own workspace, cleared by a one-block kernel just before the launch;
+row-wave launches (a few hundred tokens on a large weight) hand l and the adapter tiles' split
+partials over under a key of the launch (its dispatch in its queue and the host call's nonce)
+and clear nothing.
 
-These tests force the fallback from the host (REELS_HIP_SKINNY_SPIN=0: no wait at all) and
-require the same bits as the normal run; run calls concurrently on many streams, and HIP graphs
-of few-token calls captured on one stream and replayed at the same time on two streams, and
-repeat calls. The parity of the values themselves against the oracle is in
+These tests force the fallback from the host (REELS_HIP_SKINNY_SPIN=0: no wait at all, so
+split-0 adapter blocks also compute the other splits' partials) and require the same bits as
+the normal run; run calls concurrently on many streams, HIP graphs of few-token calls captured
+on one stream and replayed at the same time on two streams, graphs replayed on changing inputs,
+row-wave calls on workspaces of any contents, and repeat calls. The parity of the values themselves against the oracle is in
 tests/test_gpu_configs.py (cross-attention shapes) and tests/test_gpu_lora.py."""
 import numpy as np
 import pytest
@@ -221,3 +225,94 @@ def test_row_wave_dx_over_a_long_reduction(dev):
     assert_parity(bf16_f32(dx), go["dx"], "long-reduction dx")
     assert_parity(dA.cpu().numpy(), go["dA"], "long-reduction dA")
     assert_parity(dB.cpu().numpy(), go["dB"], "long-reduction dB")
+
+
+def _abi_calls(dev, M, K, N, r, c, ws):
+    """Forward and backward through the C-ABI on an explicit workspace ws (uint8, large enough
+    for both)."""
+    import ctypes
+    import torch
+    from reels_amd import _lib
+    L = _lib.lib()
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+    def run(d):
+        bf = torch.bfloat16
+        y, h = torch.empty((M, N), dtype=bf, device=dev), torch.empty((M, r), dtype=bf, device=dev)
+        dx = torch.empty((M, K), dtype=bf, device=dev)
+        dA = torch.empty((K, r), dtype=torch.float32, device=dev)
+        dB = torch.empty((r, N), dtype=torch.float32, device=dev)
+        q, s = p(d["W"].values), p(d["W"].scales)
+        _lib.check("fwd", L.reels_hip_i8lora_fwd(p(d["x"]), q, s, p(d["A"]), p(d["B"]), None, M, K, N,
+                                                 r, c, p(y), p(h), p(ws), ws.numel(), st))
+        _lib.check("bwd", L.reels_hip_i8lora_bwd(p(d["dy"]), p(d["x"]), p(h), q, s, p(d["A"]), p(d["B"]),
+                                                 M, K, N, r, c, p(dx), p(dA), p(dB), p(ws), ws.numel(), st))
+        return y, h, dx, dA, dB
+    return run
+
+
+@pytest.mark.parametrize("M", [77, 333, 512])
+def test_row_wave_results_do_not_depend_on_the_workspace_contents(dev, M):
+    """5120 x 5120 at 77 / 333 / 512 tokens (row-wave forward and dX, adapter tiles split 5 / 2 /
+    1 ways): the same bits on a workspace of zeros, of 0xff bytes, of random bytes, and on the
+    workspace a call on other inputs has just used (its keys and l still there)."""
+    import torch
+    from reels_amd import _lib, workspace_bytes
+    K = N = 5120
+    r, c = 32, 1.0
+    print(f"[skinny] workspace contents M={M}", flush=True)
+    _, a = _case(dev, M, K, N, r, 5100 + M)
+    _, b = _case(dev, M, K, N, r, 5200 + M)
+    wsn = max(workspace_bytes(M, K, N, r, _lib.WS_FWD, torch.bfloat16),
+              workspace_bytes(M, K, N, r, _lib.WS_BWD, torch.bfloat16))
+    ws = torch.zeros(wsn, dtype=torch.uint8, device=dev)
+    run = _abi_calls(dev, M, K, N, r, c, ws)
+    ref = run(a)
+    torch.cuda.synchronize(dev)
+    gen = torch.Generator(device=dev).manual_seed(M)
+    fills = [("0xff", lambda: ws.fill_(255)),
+             ("random", lambda: ws.random_(0, 256, generator=gen)),
+             ("another call's", lambda: run(b)),
+             ("zeros", lambda: ws.zero_())]
+    for name, fill in fills:
+        fill()
+        got = run(a)
+        torch.cuda.synchronize(dev)
+        for t, x, y in zip(("y", "h", "dx", "dA", "dB"), ref, got):
+            assert torch.equal(x, y), f"{t} differs on a workspace of {name} bytes"
+
+
+def test_graph_replays_on_changing_inputs(dev):
+    """A captured few-token forward + backward (77 tokens, 5120 x 5120) replayed with other
+    activations and output gradients copied into its inputs between replays: every replay
+    equals the eager call on those inputs (l and the split partials of one replay are never
+    taken for another's)."""
+    import torch
+    M, K, N, r, c = 77, 5120, 5120, 32, 1.0
+    _, d = _case(dev, M, K, N, r, 5300)
+    _, e = _case(dev, M, K, N, r, 5400)
+    print("[skinny] graph replays on changing inputs", flush=True)
+    inputs = [(d["x"], d["dy"]), (e["x"], e["dy"])]
+    refs = [_run(dict(d, x=x, dy=dy), c) for x, dy in inputs]
+    torch.cuda.synchronize(dev)
+    xs, dys = d["x"].clone(), d["dy"].clone()
+    stat = dict(d, x=xs, dy=dys)
+    s = torch.cuda.Stream(device=dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        _run(stat, c)
+    torch.cuda.current_stream(dev).wait_stream(s)
+    torch.cuda.synchronize(dev)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = _run(stat, c)
+    torch.cuda.synchronize(dev)
+    for rnd in range(6):
+        k = rnd % 2
+        xs.copy_(inputs[k][0])
+        dys.copy_(inputs[k][1])
+        g.replay()
+        torch.cuda.synchronize(dev)
+        for name, a, b in zip(("y", "h", "dx", "dA", "dB"), out, refs[k]):
+            assert torch.equal(a, b), f"replay {rnd} (inputs {k}): {name} differs from eager"
