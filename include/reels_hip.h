@@ -134,7 +134,7 @@ int reels_hip_i8lora_fwd_f16(const void* x, const int8_t* q, const float* scales
  * tight serving loops, harnesses that forbid hipMalloc. No counterpart in the reference (its
  * forward allocates per call). Same arguments, results and errors as reels_hip_i8lora_fwd except:
  *   - the scratch (the h panel, transposed adapter operands, the few-token kernel's split
- *     partials and counters, the rank projection's split partials) is a 32 MiB device array
+ *     partials and keys, the rank projection's split partials) is a 32 MiB device array
  *     inside the library, one per GPU, held until the process ends; sizes for which
  *     reels_hip_i8lora_workspace_bytes(M, K, N, r, REELS_HIP_WS_FWD_NOALLOC) exceeds 32 MiB
  *     return REELS_HIP_EINVAL before any work;

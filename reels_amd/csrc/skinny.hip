@@ -9,21 +9,21 @@
 // the adapter's rank projection) x up to 16T tokens, a split a contiguous range of 64-wide
 // reduction chunks. The block's 8 waves take the split's chunks round by round (wave w every
 // eighth chunk); their accumulators are summed in LDS in a fixed wave order. With more than one
-// split the block stores that sum as an f32 partial and counts itself in on the tile; the block
-// that arrives last sums the tile's partials in split order (its own from registers) and
-// finishes the tile:
+// split the other splits store that sum as an f32 partial and announce it under the launch's
+// key; split 0 waits for those keys, sums the tile's partials in split order (its own from
+// registers) and finishes the tile:
 //   adapter tile: l = rnd(sum) (h = x A in the forward, u = dy B^T for dX) into the workspace
-//                 (and lsave); the last adapter tile to finish raises the launch's ready flag;
-//   output tile:  waits for that flag, then out = rnd(scale * sum + c * l R + bias), the l R
-//                 product on the MFMA.
-// The adapter blocks come first in the logical order and wait for nothing, so the flag is normally
-// up long before an output tile looks; the wait is bounded all the same, and an output tile that
-// gives up computes l for its tokens itself with the adapter blocks' code and order (same bits),
-// so the result never depends on how the grid is scheduled.
-// The counters and the flag live in the call's own workspace, after the partials and l, and a
-// one-block kernel clears them just before the launch: nothing is shared between calls, so calls
-// on any streams, and HIP graphs that capture them, may run at the same time. Deterministic:
-// fixed wave order, fixed split order; the atomics only count.
+//                 (and lsave), announced under the key;
+//   output tile:  waits for its tokens' adapter tiles' keys, then
+//                 out = rnd(scale * sum + c * l R + bias), the l R product on the MFMA.
+// The adapter blocks come first in the logical order and wait for nothing but their splits, so
+// their keys are normally there long before an output tile looks; every wait is bounded all the
+// same, and a block that gives up computes what it waited for itself with the same code and
+// order (same bits), so the result never depends on how the grid is scheduled.
+// The keys, partials and l live in the call's own workspace and a key names one launch (its
+// dispatch in its queue and the host call's nonce), so nothing needs clearing before a launch and
+// nothing is shared between calls: calls on any streams, and HIP graphs that capture them, may
+// run at the same time. Deterministic: fixed wave order, fixed split order.
 //
 // FWD: out[m][n] = rnd(s[n] sum_k x[m][k] q[n][k] + c sum_j h[m][j] B[j][n] + bias[n]),
 //      h = rnd(x A): the int8 path's formula (the scale on the f32 sum).
@@ -54,15 +54,6 @@ constexpr int kMaxTiles = 4096;
 constexpr uint32_t kSpinLimit = 1u << 12;  // wait rounds of s_sleep 8 (about 1 ms) before computing l
 }  // namespace sk
 
-// one split-tile launch's counters, zero when it starts: this header, then one word per tile (the
-// blocks of the tile that have stored their partial). Row-wave launches use keys instead.
-struct SkCounters {
-  uint32_t hdone;    // adapter tiles finished
-  uint32_t hready;   // 1: l complete (set by the last adapter tile)
-  uint32_t pad[30];  // the tile counters start on their own 128-byte line
-};
-constexpr int kSkCounterHeaderWords = (int)(sizeof(SkCounters) / 4);
-
 struct SkArgs {
   const uint16_t* act;  // [M][Kred] 16-bit: x (FWD) or dy (DX)
   const int8_t* q;      // codes [N][K], row stride ldq
@@ -75,10 +66,8 @@ struct SkArgs {
   const uint16_t* bias;
   uint16_t* out;        // [M][Ncols]
   uint16_t* lsave;      // [M][ld_lsave], lsave_cols columns (or NULL)
-  SkCounters* ctr;
-  uint32_t* tiles;      // [nblk * tb + lblk * tb], right after *ctr
-  uint32_t* keys;       // row-wave launches: [nta] l ready, then [nta][S] split partial stored
-  uint32_t nonce_lo, nonce_hi;  // row-wave launches: the host call's nonce (first key words)
+  uint32_t* keys;       // [nta] adapter tile's l stored, then [tiles][S] split partial stored
+  uint32_t nonce_lo, nonce_hi;  // the host call's nonce (the keys' first words)
   int64_t M, Kred, Ncols, ldq, ldr, ld_lsave;
   float c;
   int r, rp, S, nblk, lblk, tb, lsave_cols;
@@ -101,31 +90,20 @@ static constexpr int skinny_lds(int T) {
   return ((4 * 4 * T * 64 * 16) > sk::NWV * sk::STAGE ? (4 * 4 * T * 64 * 16) : sk::NWV * sk::STAGE) + 16;
 }
 
-// Data one block hands to another (split partials, l) is stored and loaded with device-scope
-// coherence (sc1: what the compiler emits for agent-scope relaxed atomics), so it never sits in
-// one XCD's L2 where another XCD cannot see it, and no cache-wide write-back or invalidate is
-// needed. Ordering: a block's stores have completed (s_waitcnt vmcnt(0) in every wave, then the
-// barrier) before its thread 0 counts it in; a reader issues its loads only after it has seen the
-// count (or the flag), so the loads reach the device's coherence point after those stores.
+// Data one block hands to another (split partials, l, and the keys that announce them) is
+// stored and loaded with device-scope coherence (sc1: what the compiler emits for agent-scope
+// relaxed atomics), so it never sits in one XCD's L2 where another XCD cannot see it, and no
+// cache-wide write-back or invalidate is needed.
 constexpr int kSC1 = 16;  // cache policy bit: device scope
-__device__ __forceinline__ uint32_t sk_add(uint32_t* p, uint32_t v) {
-  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint32_t sk_load(uint32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void sk_store(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 // every memory operation of this wave complete (and no compiler motion across it)
 __device__ __forceinline__ void sk_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t sk_rsrc(const void* p, int64_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
 }
 
-// Row-wave launches hand l and the adapter tiles' split partials over under a key rather than
-// counters, so nothing has to zero memory before the launch (a zeroing launch in front cost about
-// 4 us per call, a tenth of a 512-token forward). A key is 16 bytes: the host call's nonce (two
+// A launch hands l and the split partials over under a key rather than counters, so nothing has
+// to zero memory before the launch (a zeroing launch in front cost about 4 us per call, a tenth
+// of a 512-token forward). A key is 16 bytes: the host call's nonce (two
 // words), the dispatch's packet index in its queue and the queue's address. A (queue, packet
 // index) pair names one dispatch for the queue's life, graph replays included, and the nonce
 // differs between host calls and between processes, so whatever an earlier launch (or anything
@@ -134,13 +112,22 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t sk_rsrc(const void* p, int64_t
 // one 16-byte device-scope store; a reader loads the key with device-scope loads and issues its
 // data loads after seeing it.
 extern "C" __device__ uint64_t reels_dispatch_id() __asm("llvm.amdgcn.dispatch.id");
-__device__ __forceinline__ u32x4 sk_key(const SkArgs& a) {
-  const uint64_t did = reels_dispatch_id();
-  const uint64_t q = (uint64_t)__builtin_amdgcn_queue_ptr();
-  return u32x4{a.nonce_lo, a.nonce_hi, (uint32_t)did, (uint32_t)(q >> 6) ^ (uint32_t)(did >> 32)};
+// The dispatch's two key words go to the block's words [0] and [3] in LDS as the block starts
+// (so the registers that bring them in are free for the rest of the block), and the key is read
+// back after a barrier.
+__device__ __forceinline__ void sk_stash_key(uint32_t* words) {
+  if (threadIdx.x == 0) {
+    const uint64_t did = reels_dispatch_id();
+    const uint64_t q = (uint64_t)__builtin_amdgcn_queue_ptr();
+    words[0] = (uint32_t)did;
+    words[3] = (uint32_t)(q >> 6) ^ (uint32_t)(did >> 32);
+  }
+}
+__device__ __forceinline__ u32x4 sk_key(const SkArgs& a, const uint32_t* words) {
+  return u32x4{a.nonce_lo, a.nonce_hi, words[0], words[3]};
 }
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t sk_keys_rsrc(const SkArgs& a) {
-  return sk_rsrc(a.keys, (int64_t)a.nta * (1 + a.S) * 16);
+  return sk_rsrc(a.keys, ((int64_t)a.nta + (int64_t)(a.ntm + a.nta) * a.S) * 16);
 }
 __device__ __forceinline__ void sk_put_key(const SkArgs& a, int idx, u32x4 key) {
   __builtin_amdgcn_raw_buffer_store_b128(key, sk_keys_rsrc(a), (uint32_t)idx * 16u, 0, kSC1);
@@ -496,14 +483,13 @@ __device__ __forceinline__ void skinny_put_l(const SkArgs& a, int64_t o0, int64_
   }
 }
 
-// One block: its accumulators, the tile's split reduction when it arrives last, then the tile's
-// results (l for an adapter tile, out for an output tile). KEYED (the adapter tiles of a row-wave
-// launch): split 0 of a tile reduces it, after the other splits have stored their partials under
-// the launch's key (a split that has not after a bounded wait it computes itself, with that
-// split's code: the same bits), and the tile's l is announced under the key too.
-template <int T, int MODE, int ELT, bool LORA, bool KEYED = false>
+// One block: its accumulators, the tile's split reduction, then the tile's results (l for an
+// adapter tile, out for an output tile). Split 0 of a tile reduces it, after the other splits
+// have stored their partials under the launch's key; a split whose key has not come after a
+// bounded wait it computes itself, with that split's code (the same bits). An adapter tile
+// announces its l under the key.
+template <int T, int MODE, int ELT, bool LORA>
 __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, uint8_t* smem) {
-  static_assert(!KEYED || LORA, "keyed hand-over: adapter tiles only");
   using E = Elt<ELT>;
   constexpr bool lora = LORA;
   const int t = threadIdx.x, lane = t & 63;
@@ -514,14 +500,16 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
   constexpr int NI = lora ? 2 : 4;
   const int64_t o0 = lora ? (int64_t)(blk - a.nblk) * sk::NBL : (int64_t)blk * sk::NB;
   constexpr int NF = NI * T, FPW = sk_fpw<NF>();
+  // [0], [3] the dispatch's key words, [1] splits seen, [2] l ready
+  uint32_t* words = reinterpret_cast<uint32_t*>(smem + skinny_lds(T) - 16);
+  sk_stash_key(words);
   f32x4 sum[FPW];
   {
     f32x4 acc[NI][T];
     skinny_acc<T, MODE, ELT, LORA>(a, blk, sp, tok0, smem, acc);
     skinny_sum<T, NI>(acc, smem, sum);
   }
-  uint32_t* words = reinterpret_cast<uint32_t*>(smem + skinny_lds(T) - 16);  // [1] arrivals, [2] l ready
-  SkCounters* ctr = a.ctr;
+  const u32x4 key = sk_key(a, words);
   // An output tile's epilogue operands: the column scales and bias of this thread's rows and
   // (forward) the first 32 rank rows of R for the tile's 64 columns, which threads 0-255 stage in
   // LDS. With split partials they are loaded before the hand-over, whose round trips cover their
@@ -546,18 +534,25 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
   if constexpr (!lora)
     if (a.S > 1) load_epi();
   const __amdgpu_buffer_rsrc_t rl = sk_rsrc(a.hl, a.M * a.rp * 2);
-  // Output tiles of a launch with an adapter look at the ready flag now (each wave reads it; the
-  // flag only goes up during the launch) and, when it is up, load their tokens' l for the first 32
-  // rank columns while the partial is handed over.
+  // Output tiles of a launch with an adapter look for the keys of their tokens' adapter tiles now
+  // (each wave looks; a key once there stays) and, when all are there, load their tokens' l for
+  // the first 32 rank columns while the partial is handed over.
   const bool wants_l = !lora && a.nad > 0;
   uint32_t up = 0;
-  if (wants_l) up = sk_load(&ctr->hready);
+  if (wants_l) {
+    up = 1;
+    for (int lb = 0; lb < a.lblk && up; ++lb) up = sk_has_key(a, lb * a.tb + d.tb, key);
+  }
   u32x4 hv[FPW];  // B operand of the l R product: l[tok][j .. j + 7], j = 8 g (first rank chunk)
   auto load_l = [&](int j0, u32x4 (&dst)[FPW]) {
+    // (the lane index through an empty asm: the offsets are computed here, not kept in
+    // registers across the main loop)
+    int l16v = l16;
+    asm volatile("" : "+v"(l16v));
 #pragma unroll
     for (int k = 0; k < FPW; ++k) {
       const int f = w + sk::NWV * k;
-      const int64_t tok = tok0 + 16 * (f % T) + l16;
+      const int64_t tok = tok0 + 16 * (f % T) + l16v;
       const int jj = j0 + 8 * g;
       dst[k] = u32x4{0u, 0u, 0u, 0u};
       if (f < NF && tok < a.M && jj < a.rp)
@@ -570,42 +565,54 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
     const int64_t tbase = lora ? a.lpart0 + (int64_t)(d.tile - a.ntm) * a.S * (NF * 64)
                                : (int64_t)d.tile * a.S * (NF * 64);
     const __amdgpu_buffer_rsrc_t rp_ = sk_rsrc(reinterpret_cast<f32x4*>(a.part) + tbase, (int64_t)a.S * NF * 64 * 16);
-    if (KEYED && sp == 0) {
-      // split 0 keeps its partial in registers and waits for the others'
-      if (t == 0) {
-        const u32x4 key = sk_key(a);
-        const int k0 = a.nta + (d.tile - a.ntm) * a.S;
-        uint32_t seen = 0, rounds = 0;
-        for (int s = 1; s < a.S; ++s)
-          if (sk_wait_key(a, k0 + s, key, rounds)) seen |= 1u << s;
-        words[1] = seen;
-      }
-      __syncthreads();
-    } else {
+    // every split stores its partial (split 0's is loaded back with the others', so no value of
+    // it stays in registers across a wait or a recomputation)
+    auto put_part = [&](int s, const f32x4 (&v)[FPW]) {
 #pragma unroll
       for (int k = 0; k < FPW; ++k) {
         const int f = w + sk::NWV * k;
         if (f < NF)
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sum[k]), rp_,
-                                                 (uint32_t)((sp * (NF * 64) + f * 64 + lane) * 16), 0, kSC1);
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[k]), rp_,
+                                                 (uint32_t)((s * (NF * 64) + f * 64 + lane) * 16), 0, kSC1);
+      }
+    };
+    put_part(sp, sum);
+    sk_drain();
+    __syncthreads();
+    if (sp != 0) {
+      if (t == 0) sk_put_key(a, a.nta + d.tile * a.S + sp, key);
+      return;
+    }
+    // split 0: the other splits' keys
+    if (t == 0) {
+      const int k0 = a.nta + d.tile * a.S;
+      uint32_t seen = 0, rounds = 0;
+      for (int s = 1; s < a.S; ++s)
+        if (sk_wait_key(a, k0 + s, key, rounds)) seen |= 1u << s;
+      words[1] = seen;
+    }
+    __syncthreads();
+    const uint32_t seen = words[1], others = ((1u << a.S) - 1u) & ~1u;
+    if ((seen & others) != others) {
+      // (block-uniform) the splits not seen: their partials computed here with their code and
+      // stored in their place; the epilogue operands loaded again after
+      for (int s = 1; s < a.S; ++s) {
+        if ((seen >> s) & 1u) continue;
+        f32x4 ps[FPW];
+        {
+          f32x4 acc[NI][T];
+          skinny_acc<T, MODE, ELT, LORA>(a, blk, s, tok0, smem, acc);
+          skinny_sum<T, NI>(acc, smem, ps);
+        }
+        put_part(s, ps);
       }
       sk_drain();
-      if (wants_l && up) load_l(0, hv);
       __syncthreads();
-      if constexpr (KEYED) {
-        if (t == 0) sk_put_key(a, a.nta + (d.tile - a.ntm) * a.S + sp, sk_key(a));
-        return;
-      }
-      if (t == 0) {
-        words[1] = sk_add(&a.tiles[d.tile], 1u);
-      }
-      __syncthreads();
-      if (words[1] != (uint32_t)a.S - 1) return;
+      if constexpr (!lora) load_epi();
     }
-    // the splits whose partial is loaded: all but this block's (keyed: those seen under the key)
-    const uint32_t have = KEYED ? words[1] : ~(1u << sp);
+    if (wants_l && up) load_l(0, hv);
     asm volatile("" ::: "memory");
-    // the tile's sum in split order: the other splits' partials in one batch (up to SB splits)
+    // the tile's sum in split order, the partials loaded in batches of SB splits
     constexpr int SB = 4;
     f32x4 tot[FPW];
 #pragma unroll
@@ -617,23 +624,11 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
 #pragma unroll
         for (int k = 0; k < FPW; ++k) {
           const int f = w + sk::NWV * k, s = s0 + u;
-          v[u][k] = sum[k];
-          if (f < NF && s < a.S && s != sp && ((have >> s) & 1u))
+          v[u][k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+          if (f < NF && s < a.S)
             v[u][k] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                                     rp_, (uint32_t)((s * (NF * 64) + f * 64 + lane) * 16), 0, kSC1));
         }
-      if constexpr (KEYED) {
-        // (block-uniform) the splits not seen: their partials computed here
-#pragma unroll
-        for (int u = 0; u < SB; ++u) {
-          const int s = s0 + u;
-          if (s < a.S && s != sp && !((have >> s) & 1u)) {
-            f32x4 acc[NI][T];
-            skinny_acc<T, MODE, ELT, LORA>(a, blk, s, tok0, smem, acc);
-            skinny_sum<T, NI>(acc, smem, v[u]);
-          }
-        }
-      }
 #pragma unroll
       for (int u = 0; u < SB; ++u)
         if (s0 + u < a.S) {
@@ -653,27 +648,19 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
     skinny_put_l<T, ELT>(a, o0, tok0, sum, true);
     sk_drain();
     __syncthreads();
-    if constexpr (KEYED) {
-      if (t == 0) sk_put_key(a, d.tile - a.ntm, sk_key(a));
-    } else if (t == 0) {
-      const uint32_t old = sk_add(&ctr->hdone, 1u);
-      if (old == (uint32_t)a.nta - 1 && a.ntm > 0) sk_store(&ctr->hready, 1u);
-    }
+    if (t == 0) sk_put_key(a, d.tile - a.ntm, key);
     return;
   } else {
-    // l complete: the adapter blocks come first in the logical order and wait for nothing, so the flag is
-    // normally up by the time an output tile gets here. Should they not have started after a long
-    // wait (a grid that cannot be resident at once, behind other work), the block computes l for
-    // its tokens itself, with the adapter blocks' code, splits and order, so the values are the
-    // same bits either way.
+    // l complete: the adapter blocks come first in the logical order and wait for nothing but
+    // their splits, so their keys are normally there by the time an output tile gets here. Should
+    // they not have come after a bounded wait (a grid that cannot be resident at once, behind
+    // other work), the block computes l for its tokens itself, with the adapter blocks' code,
+    // splits and order, so the values are the same bits either way.
     if (wants_l) {
       if (t == 0) {
-        uint32_t n = 0, v = up;
-        while (v == 0u && ++n <= a.spin) {
-          __builtin_amdgcn_s_sleep(8);
-          v = sk_load(&ctr->hready);
-        }
-        words[2] = v;
+        uint32_t rounds = 0, ok = 1;
+        for (int lb = 0; lb < a.lblk && ok; ++lb) ok = sk_wait_key(a, lb * a.tb + d.tb, key, rounds);
+        words[2] = ok;
       }
       __syncthreads();
       if (words[2] == 0u) {
@@ -763,11 +750,6 @@ __device__ __forceinline__ void skinny_block(const SkArgs& a, const SkBlock& d, 
       *reinterpret_cast<uint2*>(a.out + tok * a.Ncols + o) = uint2{b[0] | (b[1] << 16), b[2] | (b[3] << 16)};
     }
   }
-}
-
-// clears one launch's counters (n words)
-__global__ __launch_bounds__(256) void skinny_clear_kernel(uint32_t* p, int n) {
-  for (int i = (int)threadIdx.x; i < n; i += 256) p[i] = 0u;
 }
 
 // ---- row-wave output tiles: a few hundred tokens on a large weight ------------------------------
@@ -1062,8 +1044,9 @@ __device__ __forceinline__ void rw_block(const SkArgs& a, int rb, int tbo, uint8
   const int64_t r0 = (int64_t)rb * (64 * NI), tok0 = (int64_t)tbo * (16 * To);
   const int64_t ob = r0 + 16 * NI * wr;          // the wave's first output row
   const int64_t tw0 = tok0 + (int64_t)par * (16 * TH);  // the wave's first token after the pair sum
-  uint32_t* words = reinterpret_cast<uint32_t*>(smem + lds_bytes - 16);
+  uint32_t* words = reinterpret_cast<uint32_t*>(smem + lds_bytes - 16);  // [0], [3] key, [2] l ready
   const bool wants_l = a.nad > 0;
+  sk_stash_key(words);
 
   f32x4 sum[NI][TH];
   {
@@ -1106,7 +1089,7 @@ __device__ __forceinline__ void rw_block(const SkArgs& a, int rb, int tbo, uint8
     const int tb_lo = (int)(tok0 / (16 * Ta));
     const int tb_hi = std::min((int)((tok0 + 16 * To + 16 * Ta - 1) / (16 * Ta)), a.tb);
     if (t == 0) {
-      const u32x4 key = sk_key(a);
+      const u32x4 key = sk_key(a, words);
       uint32_t rounds = 0, ok = 1;
       for (int lb = 0; lb < a.lblk && ok; ++lb)
         for (int tba = tb_lo; tba < tb_hi && ok; ++tba) ok = sk_wait_key(a, lb * a.tb + tba, key, rounds);
@@ -1185,7 +1168,7 @@ __global__ __launch_bounds__(64 * sk::NWV, 1) void skinny_rw_kernel(SkArgs a, in
     const int rb = rest / a.S;
     d.blk = a.nblk + rb;
     d.tile = a.ntm + rb * a.tb + d.tb;
-    skinny_block<Ta, MODE, ELT, true, true>(a, d, smem);
+    skinny_block<Ta, MODE, ELT, true>(a, d, smem);
   } else {
     const int ti = tk - a.nad;
     rw_block<To, NI, Ta, MODE, ELT>(a, ti / a.otb, ti % a.otb, smem, lds_bytes);
@@ -1272,7 +1255,7 @@ static bool rw_choose(int64_t M, int64_t Kred, int64_t Ncols, int rp, int mode, 
 
 static bool skinny_limits(int64_t M, int64_t K, int64_t N, int rp) {
   // the reduction in whole 64-chunks, whole 64-row blocks, 32-bit buffer offsets (with room for
-  // the token-block overrun), the tiles within the counter array
+  // the token-block overrun), a bounded tile count
   const int64_t tb = ceil_div(M, 16 * sk::MAXT);
   const int64_t mx = K > N ? K : N;
   return M > 0 && K % 64 == 0 && N % 64 == 0 &&
@@ -1311,10 +1294,10 @@ SkinnyPlan skinny_plan(int64_t M, int64_t Kred, int64_t Ncols, int rp, int mode)
   return p;
 }
 
-// workspace of one launch: split partials, l [M][rp], then the counters (header + one word per
-// tile); the offsets are the same in sizing and use
+// workspace of one launch: split partials, l [M][rp], then the keys; the offsets are the same in
+// sizing and use
 struct SkWs {
-  size_t part, hl, ctr, total;
+  size_t part, hl, keys, total;
   int ntiles;
 };
 static SkWs skinny_ws(const SkinnyPlan& p, int64_t M, int64_t Ncols, int rp) {
@@ -1327,10 +1310,10 @@ static SkWs skinny_ws(const SkinnyPlan& p, int64_t M, int64_t Ncols, int rp) {
   w.ntiles = (int)(otiles + ceil_div(rp, sk::NBL) * p.tb);
   w.part = 0;
   w.hl = align_up(p.S > 1 ? frags * p.S * 64 * 16 : 0, 256);
-  w.ctr = align_up(w.hl + (size_t)M * rp * 2, 256);
-  // split tiles: the counters; row-wave tiles: the adapter tiles' keys (l ready, then per split)
+  w.keys = align_up(w.hl + (size_t)M * rp * 2, 256);
+  // 16-byte keys: one per adapter tile (l stored), then one per tile and split (partial stored)
   const size_t nta = (size_t)ceil_div(rp, sk::NBL) * p.tb;
-  w.total = align_up(w.ctr + (p.rw ? nta * (1 + p.S) * 16 : (size_t)(kSkCounterHeaderWords + w.ntiles) * 4), 256);
+  w.total = align_up(w.keys + (nta + (size_t)w.ntiles * p.S) * 16, 256);
   return w;
 }
 
@@ -1407,21 +1390,10 @@ int launch_skinny(int mode, int elt, const SkinnyPlan& p, const uint16_t* act, c
   uint16_t* hl = reinterpret_cast<uint16_t*>(wb + w.hl);
   // l straight into lsave when the layouts agree
   a.hl = (lsave != nullptr && ld_lsave == a.rp && lsave_cols >= a.rp) ? lsave : hl;
-  a.ctr = reinterpret_cast<SkCounters*>(wb + w.ctr);
-  a.tiles = reinterpret_cast<uint32_t*>(wb + w.ctr) + kSkCounterHeaderWords;
-  a.keys = reinterpret_cast<uint32_t*>(wb + w.ctr);
-  if (p.rw) {
-    const uint64_t nonce = sk_next_nonce();
-    a.nonce_lo = (uint32_t)nonce;
-    a.nonce_hi = (uint32_t)(nonce >> 32);
-  } else {
-    a.nonce_lo = a.nonce_hi = 0u;
-    {
-      TraceScope _ts(st, "skinny_clear_kernel");
-      skinny_clear_kernel<<<1, 256, 0, st>>>(reinterpret_cast<uint32_t*>(a.ctr), kSkCounterHeaderWords + w.ntiles);
-    }
-    if (int rc = check_launch("skinny_clear_kernel")) return rc;
-  }
+  a.keys = reinterpret_cast<uint32_t*>(wb + w.keys);
+  const uint64_t nonce = sk_next_nonce();
+  a.nonce_lo = (uint32_t)nonce;
+  a.nonce_hi = (uint32_t)(nonce >> 32);
 
   hipError_t attr = hipSuccess;
   if (p.rw) {
