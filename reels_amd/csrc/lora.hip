@@ -816,7 +816,10 @@ __global__ __launch_bounds__(256) void gelu_bwd_kernel(const uint16_t* __restric
 // Split-M plan of one gradient pass over a [M][Od] operand: enough token splits that the
 // ceil(Od / 128) column blocks times the splits fill one round of the GPU's workgroup slots
 // (256 CUs x 4 resident gradient workgroups), at most 32 splits (the partials buffer), tokens per
-// split a multiple of 128 (the kernel takes token steps of 64 in pairs).
+// split a multiple of 128 (the kernel takes token steps of 64 in pairs). Up to 512 tokens one
+// split: the pass writes its result itself and no reduction launch follows (5120 x 5120 backward
+// at 333 / 512 tokens 42.2 -> 40.6 and 51.5 -> 49.6 us; capping the splits at 2 or 4 up to 1024
+// tokens slowed 1536 x 1536 at 1024 tokens, 21.5 -> 22.7-23.6 us).
 struct Split {
   int splits;
   int64_t tps;  // tokens per split
@@ -828,6 +831,7 @@ static Split split_for(int64_t M, int64_t Od) {
   int64_t s = kSlots / (colblocks > 0 ? colblocks : 1);
   if (s > 32) s = 32;
   if (s > (M + 127) / 128) s = (M + 127) / 128;
+  if (M <= 512) s = 1;
   if (s < 1) s = 1;
   Split sp;
   sp.tps = ((M + s - 1) / s + 127) / 128 * 128;

@@ -1203,7 +1203,7 @@ __global__ __launch_bounds__(64 * sk::NWV, 1) void skinny_kernel(SkArgs a) {
 // 128-deep step on a CU (the largest of the matrix cores, the LDS reads, the vector memory and,
 // for dX, the VALU scaling of the codes), then the least padded work.
 struct RwCand { int NI, To; };
-constexpr RwCand kRwCands[] = {{1, 2}, {2, 4}, {2, 6}};
+constexpr RwCand kRwCands[] = {{1, 2}, {1, 4}, {2, 4}, {2, 6}};
 constexpr int kRwLdsMax = 160 * 1024;
 
 static int rw_lds_bytes(int NI, int To, int mode, int64_t Kred) {
@@ -1404,6 +1404,7 @@ int launch_skinny(int mode, int elt, const SkinnyPlan& p, const uint16_t* act, c
       auto go = [&](auto m) {
         constexpr int MD = decltype(m)::value;
         if (p.NI == 1 && p.To == 2) attr = launch_rw_t<2, 1, 2, MD, EL>(a, lds, st);
+        else if (p.NI == 1 && p.To == 4) attr = launch_rw_t<4, 1, 4, MD, EL>(a, lds, st);
         else if (p.NI == 2 && p.To == 4) attr = launch_rw_t<4, 2, 4, MD, EL>(a, lds, st);
         else attr = launch_rw_t<6, 2, 3, MD, EL>(a, lds, st);
       };
