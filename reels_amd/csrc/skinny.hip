@@ -1199,7 +1199,8 @@ __global__ __launch_bounds__(64 * sk::NWV, 1) void skinny_kernel(SkArgs a) {
 }
 
 // Row-wave tiles (NI, To) for a launch: the candidates whose output tiles and adapter blocks fit
-// one round of the 256 CUs and fill most of it; among them the least estimated clocks per
+// one round of the 256 CUs and fill most of it (or, on short reductions, some of it); among them
+// the least estimated clocks per
 // 128-deep step on a CU (the largest of the matrix cores, the LDS reads, the vector memory and,
 // for dX, the VALU scaling of the codes), then the least padded work.
 struct RwCand { int NI, To; };
@@ -1220,6 +1221,13 @@ static bool rw_choose(int64_t M, int64_t Kred, int64_t Ncols, int rp, int mode, 
   if (M <= 0 || Kred % 128 != 0 || Ncols % 64 != 0 || Kred > 16384) return false;
   // the kernel moves steps past the operands with a scalar offset of 2^30 bytes
   if (M * Kred * 2 > ((int64_t)1 << 30) || Ncols * Kred > ((int64_t)1 << 30)) return false;
+  // Tiles that fill most of the GPU; on reductions up to 4096 deep also fewer (down to 32): a
+  // whole-reduction tile there is short, and beats split tiles that hand partials over (77 tokens
+  // on 1536 x 1536 forward 15.7 -> 10.4 us, backward 20.7 -> 15.2 us; the 4096-deep dX of 160
+  // tokens on 1024 -> 4096 backward 34.8 -> 25.9 us), while on longer ones the split tiles win
+  // (3 tokens on 5120 x 5120 forward 11.6 against 13.9 us; the 8960-deep dX of 77 tokens on
+  // 1536 -> 8960 backward 28.3 against 36.6 us)
+  const int64_t min_tiles = Kred <= 4096 ? 32 : kSkinnyTargetBlocks / 2;
   bool found = false;
   int64_t best_cost = 0, best_work = 0;
   for (const RwCand& c : kRwCands) {
@@ -1227,7 +1235,7 @@ static bool rw_choose(int64_t M, int64_t Kred, int64_t Ncols, int rp, int mode, 
     const int ta = c.To <= 4 ? c.To : c.To / 2;
     const int64_t tba = ceil_div(M, 16 * ta), lblk = ceil_div(rp, sk::NBL);
     const int64_t tiles = orb * otb, nad = rp > 0 ? lblk * tba : 0;
-    if (tiles + nad > kSkinnyTargetBlocks || tiles < kSkinnyTargetBlocks / 2) continue;
+    if (tiles + nad > kSkinnyTargetBlocks || tiles < min_tiles) continue;
     if (rw_lds_bytes(c.NI, c.To, mode, Kred) > kRwLdsMax) continue;
     const int64_t mf = 64 * c.NI * c.To, lds = 128 * c.To, vm = 128 * c.NI + 64 * c.To;
     const int64_t valu = (mode == 1 ? 384 : 192) * c.NI;

@@ -227,13 +227,15 @@ def test_row_wave_dx_over_a_long_reduction(dev):
     assert_parity(dB.cpu().numpy(), go["dB"], "long-reduction dB")
 
 
-@pytest.mark.parametrize("M,K,N,r", [(512, 1536, 1536, 32), (400, 1536, 1536, 16), (160, 1024, 4096, 8)])
-def test_row_wave_tiles_of_64_rows_by_64_tokens(dev, M, K, N, r):
-    """Row-wave tiles of 64 weight rows x 64 tokens: a few hundred tokens on a weight too narrow
-    for 128-row tiles to fill the GPU (the 1.3B model's 1536 x 1536 cross-attention K/V at 512
-    text tokens) runs them in both directions; 160 tokens on 1024 -> 4096 in the forward only
-    (its dX on split tiles). y, h, dx, dA, dB against the oracle, and the same bits when
-    repeated."""
+@pytest.mark.parametrize("M,K,N,r", [(512, 1536, 1536, 32), (400, 1536, 1536, 16), (160, 1024, 4096, 8),
+                                     (77, 1536, 1536, 32), (40, 1536, 1536, 32)])
+def test_row_wave_tiles_on_narrow_weights(dev, M, K, N, r):
+    """Row-wave tiles where 128-row tiles cannot fill the GPU. Tiles of 64 weight rows x 64
+    tokens: a few hundred tokens on 1536 x 1536 (the 1.3B model's cross-attention K/V at 512
+    text tokens) in both directions, 160 tokens on 1024 -> 4096 in the forward. Fewer tiles than
+    CUs on reductions up to 4096 deep: the 4096-deep dX of that shape (80 tiles), 77 and 40
+    tokens on 1536 x 1536 (72 and 48 tiles). y, h, dx, dA, dB against the oracle, and the same
+    bits when repeated."""
     import torch
     from reels_amd import i8lora_backward, i8lora_forward
     host, d = _case(dev, M, K, N, r, 4900 + M)
