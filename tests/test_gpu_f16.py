@@ -98,7 +98,9 @@ def check(dev, cs, label):
     (65, 48, 80, 16, False),        # K not a multiple of 64
     (50, 256, 256, 0, True),        # base-only linear with bias
     (40, 24, 20, 5, True),          # rank 5: generic kernels
-    (400, 2048, 2560, 32, True),    # split reductions in both GEMMs
+    (1100, 2048, 2560, 32, True),   # split reductions in both GEMMs
+    (512, 1536, 1536, 32, False),   # row-wave tiles of 64 rows x 64 tokens in both directions
+    (77, 1536, 1536, 16, True),     # row-wave tiles on part of the GPU (72 tiles)
 ])
 def test_f16_shapes(dev, M, K, N, r, bias):
     check(dev, make_case(M, K, N, r, float(r) if r else 1.0, seed=900 + M + K + N + r, bias=bias),

@@ -100,8 +100,9 @@ def test_reference_gpu_test_shape_ragged(dev):
     (150, 640, 384, 48, True),      # rank 48: LoRA operands read from global memory
     (50, 256, 256, 0, True),        # base-only linear(::DenseLayer) with bias
     (40, 24, 20, 2, True),          # ragged: generic path with bias
-    (400, 2048, 2560, 32, True),    # 20 tiles: reduction split over 8 (forward) and 10 (dX) workgroups
-    (352, 1024, 4608, 24, False),   # split reduction with a padded rank, 36 / 8 tiles
+    (1100, 2048, 2560, 32, True),   # 50 / 40 tiles of 256 x 256: reductions split in both GEMMs
+    (400, 2048, 2560, 32, True),    # row-wave tiles: 128 rows x 64 tokens forward, 64 x 64 dX
+    (352, 1024, 4608, 24, False),   # row-wave tiles with a padded rank
 ])
 def test_shapes(dev, M, K, N, r, bias):
     check_full(dev, make_case(M, K, N, r, float(r) if r else 1.0, seed=M + K + N + r,
