@@ -49,8 +49,9 @@ def _check(dev, q, s, mode, transpose, ld=None):
 
 
 # (N, K): fast bf16 row kernel (K % 16 == 0), fast transpose (N, K % 64 == 0), generic paths
+# (192, 320): five 64-column tiles, so the transpose's second block holds one tile of its four
 @pytest.mark.parametrize("N,K", [(256, 1536), (1024, 5120), (128, 64), (333, 1536), (7, 5),
-                                 (65, 48), (40, 8960)])
+                                 (65, 48), (40, 8960), (192, 320)])
 @pytest.mark.parametrize("mode", ["bf16", "f16", "f32"])
 @pytest.mark.parametrize("transpose", [False, True])
 def test_dequant_bit_exact(dev, N, K, mode, transpose):
