@@ -648,12 +648,13 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
   auto issue_w = [&](int kt, int i) {
     dma16(rw, vow[i], (uint32_t)kt * (BK * 2), wbase(kt) + (w * 4 + i) * 1024);
   };
-  // LoRA operands of the epilogue (rank up to 32): the L tile [256 tokens][32] and the R tile
-  // [256 columns][32], rows of 64 bytes, zeros past the rank, share activation stage nk (free
-  // during the last step) as bytes [0, 16) and [16, 32) KiB. Step nk-2 copies them with the four
-  // activation copies it would otherwise issue for a step nk that does not exist (copies 0-1 L,
-  // 2-3 R; copy i of wave w fills 1 KiB = 16 rows). A 16 x 32 fragment is then 1 KiB of
-  // contiguous LDS. Higher ranks read L and R from global memory in the epilogue.
+  // LoRA operands (rank up to 32): the L tile [256 tokens][32] and the R tile [256 columns][32],
+  // rows of 64 bytes, zeros past the rank, copied before the first steps' copies into activation
+  // stage 2 (free until step 0 issues step 2's copies, after the prologue's barrier) as bytes
+  // [0, 16) and [16, 32) KiB (copies 0-1 L, 2-3 R; copy i of wave w fills 1 KiB = 16 rows). A
+  // 16 x 32 fragment is then 1 KiB of contiguous LDS. The accumulators start at c L R^T, computed
+  // while the first steps' copies land, so the epilogue adds only the bias and rounds. Higher
+  // ranks read L and R from global memory in the epilogue.
   const int rp = a.rp;
   const bool lora = rp > 0 && a.L != nullptr && split == 0;  // split 0 carries the LoRA term
   const bool lr_lds = lora && rp <= 32;
@@ -695,17 +696,52 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
   };
 
   V8 w0[4], w1[4], x[8];
+  // L and R first (through the zero-record descriptor when they stay in global memory: the copy
+  // counts of the waits below are the same either way), then steps 0 and 1
+#pragma unroll
+  for (int k = 0; k < 4; ++k) issue_lr(2, k);
 #pragma unroll
   for (int i = 0; i < 4; ++i) { issue_act(0, i); issue_w(0, i); }
   if (nk > 1) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) { issue_act(1, i); issue_w(1, i); }
-    __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8): step 1 may stay in flight
-  } else {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) issue_lr(1, k);
-    __builtin_amdgcn_s_waitcnt(0x0F70);
   }
+  if (lr_lds) {
+    // acc = c L R^T: the same L fragments serve every column tile
+    if (nk > 1) __builtin_amdgcn_s_waitcnt(0x4F70);  // vmcnt(16): L and R have landed
+    else __builtin_amdgcn_s_waitcnt(0x0F78);         // vmcnt(8)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");  // the L and R reads stay after the barrier
+    __builtin_amdgcn_sched_barrier(0);
+    const uint8_t* sL = abase(2);
+    const uint8_t* sR = sL + 16384;
+    V8 lf[8], rf[4];
+#pragma unroll
+    for (int tj = 0; tj < 8; ++tj)
+      lf[tj] = E::as8(*reinterpret_cast<const u32x4*>(sL + (wm * 128 + tj * 16 + l16) * 64 + lq * 16));
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti)
+      rf[ti] = E::as8(*reinterpret_cast<const u32x4*>(sR + (wn * 64 + ti * 16 + l16) * 64 + lq * 16));
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+      for (int tj = 0; tj < 8; ++tj) acc[ti][tj] = E::mfma16(rf[ti], lf[tj], acc[ti][tj]);
+    if (a.c != 1.0f) {
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+        for (int tj = 0; tj < 8; ++tj)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[ti][tj][v] *= a.c;
+    }
+  }
+  asm volatile("" ::: "memory");  // ... and before the waits and barrier below
+  __builtin_amdgcn_sched_barrier(0);
+  if (nk > 1) __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8): step 1 may stay in flight
+  else __builtin_amdgcn_s_waitcnt(0x0F70);
+  // every wave has read L and R (the barrier orders those reads before step 0's copies of step 2
+  // into their stage)
+  __builtin_amdgcn_s_waitcnt(0xC07F);
   __builtin_amdgcn_s_barrier();
   // no scalar loads pending at the loop entry, so the waits at its head count LDS reads only
   __builtin_amdgcn_s_waitcnt(0xC07F);
@@ -720,9 +756,9 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
   // - sub-step 1 reads step kt+1's sub-step-0 fragments and issues the weight copies of step kt+2
   //   into the weight stage of step kt, free since this barrier.
   // The L2-to-LDS path moves about 64 bytes per clock per CU; eight copies in one sub-step stall
-  // their issue, four per sub-step do not. Step nk-2 copies the LoRA operands instead (LR), and
-  // its weight copies go through a zero-record descriptor: they move no memory and write zeros
-  // into a stage no wave reads any more.
+  // their issue, four per sub-step do not. Step nk-2 (LR) has no step nk to copy: its copies go
+  // through a zero-record descriptor (they move no memory and write zeros into stages no wave
+  // reads any more), so every step's waits count the same copies.
   //
   // Waves w and w + 4 share a SIMD. With equal priorities the older one (w < 4) wins every MFMA
   // issue slot it wants, runs a whole sub-step ahead, and the younger one then finishes its
@@ -741,7 +777,7 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
       x[tj] = read_x(sa, 1, tj);
       if (tj == 0) read_w(sw, 1, w1);
       if (tj & 1) {
-        if constexpr (LR) issue_lr(kt + 2, tj >> 1);
+        if constexpr (LR) dma16(rnone, 0u, 0u, abase(kt + 2) + (w * 4 + (tj >> 1)) * 1024);
         else issue_act(kt + 2, tj >> 1);
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -785,13 +821,13 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
 #pragma unroll
     for (int tj = 0; tj < 8; ++tj) mfma4(w1, x[tj], tj);
   }
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // the L and R copies have landed
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // the last zero-record copies have landed
 
-  // epilogue: LoRA up-projection on MFMA (k = 32 per instruction, lanes past the rank supply
-  // zeros), bias, one rounding per output (acc + c lor + bias); each wave stages its 128 x 64
-  // outputs in LDS and stores them as 128-byte row segments. The staging tile's rows of 512 bytes
-  // (16-byte chunks XOR-swizzled by row) fill, 64 rows at a time, the four stages other than
-  // activation stage nk, which holds L and R until every wave has read them.
+  // epilogue: bias and one rounding per output (acc + bias, the LoRA term already in acc; ranks
+  // above 32 add c lor here, their up-projection on MFMA with k = 32 per instruction and lanes
+  // past the rank supplying zeros); each wave stages its 128 x 64 outputs in LDS and stores them
+  // as 128-byte row segments. The staging tile's rows of 512 bytes (16-byte chunks XOR-swizzled
+  // by row) fill, 64 rows at a time, four of the five stages (all copies have landed).
   __syncthreads();
   const int lrs = nk % 3;
   auto srow = [&](int r) { const int q = r >> 6; return smem + (q < lrs ? q : q + 1) * ACT + (r & 63) * 512; };
@@ -805,8 +841,9 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
     if (a.bias != nullptr && nb < Ncols) braw[ti] = *reinterpret_cast<const u32x2*>(a.bias + nb);
   }
 
-  // acc + c lor + bias, rounded once, into the staging tile
-  auto finish = [&](int ti, const f32x4* lor) {
+  // acc (+ c lor with UL) + bias, rounded once, into the staging tile
+  auto finish = [&](int ti, const f32x4* lor, auto ul) {
+    constexpr bool UL = decltype(ul)::value;
     const int nloc = wn * 64 + ti * 16 + lq * 4;  // this lane's four output columns
     if constexpr (SPLIT) {
       // split partial: acc (+ c lor in split 0), f32, 16 bytes per lane and token
@@ -814,7 +851,7 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
       for (int tj = 0; tj < 8; ++tj) {
         const int64_t m = m0 + wm * 128 + tj * 16 + l16, n = n0 + nloc;
         f32x4 o = acc[ti][tj];
-        if (lora) {
+        if (UL && lora) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) o[v] += a.c * lor[tj][v];
         }
@@ -828,30 +865,15 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
       const int mloc = wm * 128 + tj * 16 + l16;
       float o[4];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) o[v] = acc[ti][tj][v] + a.c * lor[tj][v] + bs[v];
+      for (int v = 0; v < 4; ++v) o[v] = UL ? acc[ti][tj][v] + a.c * lor[tj][v] + bs[v] : acc[ti][tj][v] + bs[v];
       const u32x2 pk = {E::pack2_fast(o[0], o[1]), E::pack2_fast(o[2], o[3])};
       const int chunk = (nloc >> 3) ^ (mloc & 31);
       *reinterpret_cast<u32x2*>(srow(mloc) + chunk * 16 + (nloc & 7) * 2) = pk;
     }
   };
-  if (lr_lds) {
-    // the same L fragments serve every column tile: read once
-    const uint8_t* sL = abase(nk);
-    const uint8_t* sR = sL + 16384;
-    V8 lf[8], rf[4];
+  if (lr_lds || !lora) {
 #pragma unroll
-    for (int tj = 0; tj < 8; ++tj)
-      lf[tj] = E::as8(*reinterpret_cast<const u32x4*>(sL + (wm * 128 + tj * 16 + l16) * 64 + lq * 16));
-#pragma unroll
-    for (int ti = 0; ti < 4; ++ti)
-      rf[ti] = E::as8(*reinterpret_cast<const u32x4*>(sR + (wn * 64 + ti * 16 + l16) * 64 + lq * 16));
-#pragma unroll
-    for (int ti = 0; ti < 4; ++ti) {
-      f32x4 lor[8];
-#pragma unroll
-      for (int tj = 0; tj < 8; ++tj) lor[tj] = E::mfma16(rf[ti], lf[tj], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
-      finish(ti, lor);
-    }
+    for (int ti = 0; ti < 4; ++ti) finish(ti, nullptr, std::false_type{});
   } else {
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) {
@@ -876,7 +898,7 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
           }
         }
       }
-      finish(ti, lor);
+      finish(ti, lor, std::true_type{});
     }
   }
   if constexpr (SPLIT) return;  // the partials went straight to global memory
