@@ -530,6 +530,8 @@ class Chain:
                     K=K, N=N, gelu=j == 4, after_gelu=j == 5, x=cur, y=y, gl=gl,
                     fwd=(p(cur), p(W.values), p(W.scales), p(A), p(B), None, M, K, N, r, c, p(y),
                          p(h), p(self.wsf), wsf, self.st),
+                    fwd_gelu=(p(cur), p(W.values), p(W.scales), p(A), p(B), None, M, K, N, r, c,
+                              p(y), p(gl), p(h), p(self.wsf), wsf, self.st) if j == 4 else None,
                     bwd=lambda dy, dx, x=cur, W=W, A=A, B=B, h=h, dA=dA, dB=dB, K=K, N=N: (
                         p(dy), p(x), p(h), p(W.values), p(W.scales), p(A), p(B), M, K, N, r, c,
                         p(dx), p(dA), p(dB), p(self.wsb), wsb, self.st),
@@ -559,6 +561,9 @@ class Chain:
 
     def step(self, L, check, fused=True):
         for lk in self.links:
+            if lk["gelu"] and fused:
+                check("reels_hip_i8lora_fwd_gelu", L.reels_hip_i8lora_fwd_gelu(*lk["fwd_gelu"]))
+                continue
             check("reels_hip_i8lora_fwd", L.reels_hip_i8lora_fwd(*lk["fwd"]))
             if lk["gelu"]:
                 check("reels_hip_gelu_tanh", L.reels_hip_gelu_tanh(
@@ -671,9 +676,10 @@ def _cfg4(dev, L, check, gen):
     ms_sep = _time_ms(lambda: ch.step(L, check, fused=False), reps=3, warmup=1)
     out["cfg4"] = {"what": "30 wan2.1-1.3b layers (q -> k -> v -> o -> ffn.0 -> gelu_tanh -> "
                            "ffn.2) at 32760 tokens, r 32: one forward then one backward through "
-                           "the chain (dX chained, dA and dB per linear); the GELU's pullback "
-                           "fused into ffn.2's dX (reels_hip_i8lora_bwd_gelu)", "ms": round(ms, 2),
-                   "ms_separate_gelu_pullback": round(ms_sep, 2),
+                           "the chain (dX chained, dA and dB per linear); the GELU fused into "
+                           "ffn.0's forward epilogue (reels_hip_i8lora_fwd_gelu) and its pullback "
+                           "into ffn.2's dX (reels_hip_i8lora_bwd_gelu)", "ms": round(ms, 2),
+                   "ms_separate_gelu_passes": round(ms_sep, 2),
                    "tflops": round(ch.flops / (ms * 1e-3) / 1e12, 1),
                    "frac_of_bf16_peak": round(ch.flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
                    "flops": ch.flops}

@@ -213,6 +213,27 @@ int reels_hip_gelu_tanh_bwd(const void* x, const void* dy, void* dx, int64_t n, 
 int reels_hip_gelu_tanh_bwd_f16(const void* x, const void* dy, void* dx, int64_t n, void* stream);
 
 /*
+ * The forward of the Wan FFN's first projection followed by its GELU, transformer.jl:289-292
+ * (ffn.0 -> gelu_tanh), in one call. No single counterpart in the reference (its FFN calls the
+ * linear, lora.jl:56-95, then gelu_tanh, linear.jl:61-68, in turn); the results are those of the
+ * two calls, bit for bit: y [M][N] as reels_hip_i8lora_fwd (the GELU's input, which the
+ * backward's reels_hip_i8lora_bwd_gelu takes as gx) and g [M][N] = gelu_tanh(y). Where the
+ * forward runs on the dequantized-weight GEMM without a split reduction (many tokens, K and N
+ * multiples of 64, 16-byte aligned buffers) the GELU runs in the GEMM's epilogue on the rounded
+ * outputs (y is not read back); elsewhere the separate pass runs after it. Workspace as for
+ * reels_hip_i8lora_fwd. _f16: binary16 operands, as reels_hip_i8lora_fwd_f16.
+ */
+int reels_hip_i8lora_fwd_gelu(const void* x, const int8_t* q, const float* scales, const void* A,
+                              const void* B, const void* bias, int64_t M, int64_t K, int64_t N,
+                              int64_t r, float lora_scale, void* y, void* g, void* h_save,
+                              void* workspace, size_t ws_bytes, void* stream);
+int reels_hip_i8lora_fwd_gelu_f16(const void* x, const int8_t* q, const float* scales,
+                                  const void* A, const void* B, const void* bias, int64_t M,
+                                  int64_t K, int64_t N, int64_t r, float lora_scale, void* y,
+                                  void* g, void* h_save, void* workspace, size_t ws_bytes,
+                                  void* stream);
+
+/*
  * The backward of the Wan FFN's second projection with the GELU's pullback before it,
  * transformer.jl:289-292 (ffn.0 -> gelu_tanh -> ffn.2), in one call. No single counterpart in the
  * reference (its FFN pullback calls the linear's, then gelu_tanh's, linear.jl:61-68, in turn);

@@ -23,6 +23,7 @@ from .layers import (  # noqa: F401
     i8lora_backward,
     i8lora_backward_gelu,
     i8lora_forward,
+    i8lora_forward_gelu,
     linear,
     lora_backward,
     lora_forward,

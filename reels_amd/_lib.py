@@ -35,6 +35,8 @@ EXPORTS = (
     "reels_hip_gelu_tanh_f16",
     "reels_hip_gelu_tanh_bwd",
     "reels_hip_gelu_tanh_bwd_f16",
+    "reels_hip_i8lora_fwd_gelu",
+    "reels_hip_i8lora_fwd_gelu_f16",
     "reels_hip_i8lora_bwd_gelu",
     "reels_hip_i8lora_bwd_gelu_f16",
     "reels_hip_i8lora_workspace_bytes_f32",
@@ -109,6 +111,10 @@ def lib():
         gb.argtypes = [vp, vp, vp, i64, vp]
         gb.restype = ctypes.c_int
     for sfx in ("", "_f16"):
+        fg = getattr(L, "reels_hip_i8lora_fwd_gelu" + sfx)
+        fg.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, ctypes.c_float, vp, vp, vp, vp,
+                       sz, vp]
+        fg.restype = ctypes.c_int
         bg = getattr(L, "reels_hip_i8lora_bwd_gelu" + sfx)
         bg.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, ctypes.c_float, vp, vp,
                        vp, vp, vp, sz, vp]

@@ -26,6 +26,9 @@ struct GemmArgs {
   // out = rnd(rnd(sum) * gelu_tanh'(gx)) with gx [M][Ncols] the GELU's input (the same bits as
   // gelu_bwd_kernel on the stored product), when gx != nullptr
   const uint16_t* gx;
+  // bfgemm only, without a split reduction: gout [M][Ncols] = gelu_tanh(out) from the rounded
+  // 16-bit outputs (the same bits as gelu_kernel on out), written beside out when != nullptr
+  uint16_t* gout;
 };
 
 // mode 0 = FWD (out = s * act q^T + c L R^T + bias), 1 = DX (out = act q + c L R^T, or
@@ -45,6 +48,8 @@ int bfgemm_splits(int64_t M, int64_t Ncols, int64_t Kred);
 // a.ksplit <= 1 and 16-byte aligned buffers (bfgemm_fuses_gelu)
 int launch_bfgemm(int mode, int elt, const GemmArgs& a, const uint16_t* wd, hipStream_t st);
 bool bfgemm_fuses_gelu(const GemmArgs& a);
+// a.gout (the forward GELU epilogue) needs the same: a.ksplit <= 1 and 16-byte aligned buffers
+bool bfgemm_fuses_gelu_fwd(const GemmArgs& a);
 
 // wd[n][k] = deq(q[n][k], s[n]) in element type elt (bf16: bf16(fl32(q s)); f16: f16(q f16(s))),
 // q [N][K] row stride ldq (K % 16 == 0)

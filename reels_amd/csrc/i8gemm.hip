@@ -588,10 +588,10 @@ constexpr int GM = 4;
 // sum); D register v of lane l is output column 4 (l / 16) + v, token l % 16 of the tile.
 // SPLIT: the workgroup takes one of a.ksplit reduction ranges of its tile and writes an f32
 // partial (a separate instantiation, so the unsplit kernel's registers stay as they are).
-// EPI (unsplit only): 0 plain; 2 writes out = rnd(rnd(sum) * gelu_tanh'(gx)), the GELU's pullback
-// of the product, from the rounded 16-bit values the plain kernel would store, so the bits equal
-// the separate pass. (A forward epilogue writing gelu(out) as well measured slower than the
-// separate GELU pass: its VALU work runs while the matrix cores idle, the pass's overlaps HBM.)
+// EPI (unsplit only): 0 plain; 1 writes gout = rnd(gelu_tanh(out)) beside out (the FFN's first
+// projection followed by its GELU), and 2 writes out = rnd(rnd(sum) * gelu_tanh'(gx)), the GELU's
+// pullback of the product; both from the rounded 16-bit values the plain kernel stores, so the
+// bits equal the separate GELU passes.
 template <int ELT, bool SPLIT, int EPI = 0>
 __global__ __launch_bounds__(512)
 void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int tiles_m) {
@@ -943,6 +943,13 @@ void bfgemm_kernel(GemmArgs a, const uint16_t* __restrict__ wd, int tiles_n, int
     if (m < M && n < Ncols) {
       const u32x4 v = *reinterpret_cast<const u32x4*>(srow(row) + ((c ^ (row & 31)) << 4));
       __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(a.out + m * Ncols + n));
+      if constexpr (EPI == 1) {
+        u32x4 gv;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          gv[k] = E::bits(gelu_f(E::lo(v[k]))) | (E::bits(gelu_f(E::hi(v[k]))) << 16);
+        __builtin_nontemporal_store(gv, reinterpret_cast<u32x4*>(a.gout + m * Ncols + n));
+      }
     }
   }
 }
@@ -995,6 +1002,11 @@ bool bfgemm_fuses_gelu(const GemmArgs& a) {
   return a.ksplit <= 1 && a.Ncols % 8 == 0 && al(a.out) && al(a.gx);
 }
 
+bool bfgemm_fuses_gelu_fwd(const GemmArgs& a) {
+  const auto al = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  return a.ksplit <= 1 && a.Ncols % 8 == 0 && al(a.out) && al(a.gout);
+}
+
 bool bfgemm_supported(int64_t M, int64_t Ncols, int64_t Kred) {
   (void)M;  // any token count: launch_bfgemm splits the tokens into chunks (below)
   return Kred % bfg::BK == 0 && Ncols % 16 == 0 && Ncols * Kred * 2 < ((int64_t)1 << 31);
@@ -1008,7 +1020,8 @@ int launch_bfgemm(int mode, int elt, const GemmArgs& a, const uint16_t* wd, hipS
   std::call_once(once, [&] {
     const void* ks[] = {(const void*)bfgemm_kernel<REELS_HIP_BF16, false>, (const void*)bfgemm_kernel<REELS_HIP_F16, false>,
                         (const void*)bfgemm_kernel<REELS_HIP_BF16, true>, (const void*)bfgemm_kernel<REELS_HIP_F16, true>,
-                        (const void*)bfgemm_kernel<REELS_HIP_BF16, false, 2>, (const void*)bfgemm_kernel<REELS_HIP_F16, false, 2>};
+                        (const void*)bfgemm_kernel<REELS_HIP_BF16, false, 2>, (const void*)bfgemm_kernel<REELS_HIP_F16, false, 2>,
+                        (const void*)bfgemm_kernel<REELS_HIP_BF16, false, 1>, (const void*)bfgemm_kernel<REELS_HIP_F16, false, 1>};
     for (const void* k : ks)
       if (attr_err == hipSuccess) attr_err = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, bfg::LDS);
   });
@@ -1020,6 +1033,8 @@ int launch_bfgemm(int mode, int elt, const GemmArgs& a, const uint16_t* wd, hipS
   const int64_t chunk = ((((int64_t)1 << 31) - 1) / (a.Kred * 2)) / bfg::BM * bfg::BM;
   if (a.gx && !bfgemm_fuses_gelu(a))
     return fail(REELS_HIP_EINVAL, "bfgemm: the GELU epilogue needs the unsplit kernel and 16-byte aligned buffers");
+  if (a.gout && (a.gx || !bfgemm_fuses_gelu_fwd(a)))
+    return fail(REELS_HIP_EINVAL, "bfgemm: the forward GELU epilogue needs the unsplit kernel, 16-byte aligned buffers and no pullback");
   if (a.ksplit > 1) {
     // split reduction: few tiles (one chunk of tokens), partials in a.part, then the reduction pass
     if (a.M > chunk || a.part == nullptr || a.Ncols % 4 != 0)
@@ -1039,11 +1054,13 @@ int launch_bfgemm(int mode, int elt, const GemmArgs& a, const uint16_t* wd, hipS
     c.out = a.out + m0 * a.Ncols;
     if (a.L) c.L = a.L + m0 * a.rp;
     if (a.gx) c.gx = a.gx + m0 * a.Ncols;
+    if (a.gout) c.gout = a.gout + m0 * a.Ncols;
     const int tn = (int)ceil_div(c.Ncols, bfg::BN), tm = (int)ceil_div(c.M, bfg::BM);
     { TraceScope _ts(st, mode == 0 ? "bfgemm_kernel<0>" : "bfgemm_kernel<1>");
       with_elt(elt, [&](auto e) {
         constexpr int EL = decltype(e)::value;
         if (c.gx) bfgemm_kernel<EL, false, 2><<<tn * tm, bfg::NT, bfg::LDS, st>>>(c, wd, tn, tm);
+        else if (c.gout) bfgemm_kernel<EL, false, 1><<<tn * tm, bfg::NT, bfg::LDS, st>>>(c, wd, tn, tm);
         else bfgemm_kernel<EL, false><<<tn * tm, bfg::NT, bfg::LDS, st>>>(c, wd, tn, tm);
       }); }
     if (int rc = check_launch("bfgemm_kernel")) return rc;

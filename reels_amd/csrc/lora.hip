@@ -1257,7 +1257,7 @@ static int i8lora_fwd_impl(int elt, const char* fn, const void* x, const int8_t*
                            const float* scales, const void* A, const void* B, const void* bias,
                            int64_t M, int64_t K, int64_t N, int64_t r, float lora_scale, void* y,
                            void* h_save, void* workspace, size_t ws_bytes, void* stream,
-                           bool noalloc = false) {
+                           bool noalloc = false, void* gout = nullptr, bool* gelu_fused = nullptr) {
   clear_error();
   if (M < 0 || K <= 0 || N <= 0 || r < 0 || r > 4096)
     return fail(REELS_HIP_EINVAL, std::string(fn) + ": " "need M >= 0, K > 0, N > 0, 0 <= r <= 4096");
@@ -1340,6 +1340,9 @@ static int i8lora_fwd_impl(int elt, const char* fn, const void* x, const int8_t*
     uint16_t* wd = reinterpret_cast<uint16_t*>(ws + w.wd);
     if ((rc = launch_dequant_rows(elt, q, K, scales, N, K, wd, st))) return rc;
     g.q = nullptr; g.colscale = nullptr;
+    g.gout = static_cast<uint16_t*>(gout);
+    if (g.gout && !bfgemm_fuses_gelu_fwd(g)) g.gout = nullptr;
+    if (g.gout && gelu_fused) *gelu_fused = true;
     return launch_bfgemm(0, elt, g, wd, st);
   }
   return launch_i8gemm(0, elt, g, st);
@@ -1618,6 +1621,45 @@ extern "C" int reels_hip_i8lora_bwd_f16(const void* dy, const void* x, const voi
                                         void* workspace, size_t ws_bytes, void* stream) {
   return i8lora_bwd_impl(REELS_HIP_F16, "reels_hip_i8lora_bwd_f16", dy, x, h, q, scales, A, B, M, K,
                          N, r, lora_scale, dx, dA, dB, nullptr, workspace, ws_bytes, stream);
+}
+
+// The first FFN projection's forward followed by the GELU (transformer.jl:289-292, linear.jl:61-68):
+// g = gelu_tanh(y) written by the GEMM's epilogue beside y where the forward runs on the unsplit
+// dequantized-weight GEMM, otherwise by the separate pass after it (the same bits either way).
+static int i8lora_fwd_gelu_impl(int elt, const char* fn, const void* x, const int8_t* q,
+                                const float* scales, const void* A, const void* B,
+                                const void* bias, int64_t M, int64_t K, int64_t N, int64_t r,
+                                float lora_scale, void* y, void* g, void* h_save, void* workspace,
+                                size_t ws_bytes, void* stream) {
+  if (M > 0 && !g) {
+    clear_error();
+    return fail(REELS_HIP_EINVAL, std::string(fn) + ": NULL g");
+  }
+  bool fused = false;
+  if (int rc = i8lora_fwd_impl(elt, fn, x, q, scales, A, B, bias, M, K, N, r, lora_scale, y, h_save,
+                               workspace, ws_bytes, stream, false, g, &fused))
+    return rc;
+  if (fused || M == 0) return REELS_HIP_OK;
+  return gelu_impl(elt, fn, y, g, M * N, stream);
+}
+
+extern "C" int reels_hip_i8lora_fwd_gelu(const void* x, const int8_t* q, const float* scales,
+                                         const void* A, const void* B, const void* bias, int64_t M,
+                                         int64_t K, int64_t N, int64_t r, float lora_scale, void* y,
+                                         void* g, void* h_save, void* workspace, size_t ws_bytes,
+                                         void* stream) {
+  return i8lora_fwd_gelu_impl(REELS_HIP_BF16, "reels_hip_i8lora_fwd_gelu", x, q, scales, A, B, bias,
+                              M, K, N, r, lora_scale, y, g, h_save, workspace, ws_bytes, stream);
+}
+
+extern "C" int reels_hip_i8lora_fwd_gelu_f16(const void* x, const int8_t* q, const float* scales,
+                                             const void* A, const void* B, const void* bias,
+                                             int64_t M, int64_t K, int64_t N, int64_t r,
+                                             float lora_scale, void* y, void* g, void* h_save,
+                                             void* workspace, size_t ws_bytes, void* stream) {
+  return i8lora_fwd_gelu_impl(REELS_HIP_F16, "reels_hip_i8lora_fwd_gelu_f16", x, q, scales, A, B,
+                              bias, M, K, N, r, lora_scale, y, g, h_save, workspace, ws_bytes,
+                              stream);
 }
 
 // The second FFN projection's backward with the GELU's pullback (transformer.jl:289-292,

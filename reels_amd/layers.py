@@ -223,6 +223,42 @@ def i8lora_forward(x, weight: QuantizedMatrix, A=None, B=None, bias=None, lora_s
     return y, h
 
 
+def i8lora_forward_gelu(x, weight: QuantizedMatrix, A=None, B=None, bias=None, lora_scale=1.0,
+                        save_h: bool = False):
+    """The FFN's first projection followed by gelu_tanh (transformer.jl:289-292): returns
+    (y, g, h or None) with y as i8lora_forward returns it (the GELU's input, gx of
+    i8lora_backward_gelu) and g = gelu_tanh(y) (reels_hip_i8lora_fwd_gelu*: in the forward GEMM's
+    epilogue where that GEMM is unsplit, bit-identical to the two calls). float32 runs the two
+    calls."""
+    if x.dim() == 2 and x.dtype == torch.float32:
+        y, h = i8lora_forward(x, weight, A, B, bias, lora_scale, save_h)
+        return y, gelu_tanh(y), h
+    if x.dim() != 2:
+        raise ValueError(f"x must be a [M][K] matrix, got shape {tuple(x.shape)}")
+    M, K = x.shape
+    N, Kw = weight.values.shape
+    if Kw != K:
+        raise ValueError("DimensionMismatch: LoRA input and weight dimensions differ")
+    r = _validate(weight, M, K, N, A, B, bias=(bias, (N,)))
+    dt = _act_dtype(x, "x")
+    x = x.contiguous()
+    weight = _on_activation_device(weight, x.device)
+    A = _contig(A, dt, "A")
+    B = _contig(B, dt, "B")
+    bias = _contig(bias, dt, "bias")
+    dev = x.device
+    y = torch.empty((M, N), dtype=dt, device=dev)
+    g = torch.empty((M, N), dtype=dt, device=dev)
+    h = torch.empty((M, r), dtype=dt, device=dev) if (save_h and r) else None
+    nbytes = workspace_bytes(M, K, N, r, _lib.WS_FWD, dt)
+    ws = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
+    fn = "reels_hip_i8lora_fwd_gelu" + _ACT_SUFFIX[dt]
+    _lib.check(fn, getattr(_lib.lib(), fn)(
+        _ptr(x), _ptr(weight.values), _ptr(weight.scales), _ptr(A), _ptr(B), _ptr(bias),
+        M, K, N, r, float(lora_scale), _ptr(y), _ptr(g), _ptr(h), _ptr(ws), nbytes, _stream(dev)))
+    return y, g, h
+
+
 def i8lora_backward(dy, x, weight: QuantizedMatrix, A=None, B=None, lora_scale=1.0, h=None,
                     want_dx=True, want_dA=True, want_dB=True, want_dbias=False):
     """(dx [M][K], dA f32 [K][r], dB f32 [r][N]) of lora_backward (lora.jl:106-118). dy, x, h,

@@ -1,10 +1,12 @@
-"""The FFN's second projection's backward with the GELU's pullback in one call
-(reels_hip_i8lora_bwd_gelu and its f16 form). Where dX runs on the unsplit dequantized-weight
-GEMM the pullback runs in its epilogue; elsewhere (few tokens, split reductions) the separate pass
-runs after it. Either way every output must equal the two separate calls bit for bit: the
-linear's backward, then gelu_tanh_backward. The separate calls are checked against the oracle in
-test_gpu_lora.py (shapes, ranks, test_gelu_tanh); one case here also samples rows of the
-composition against the oracle."""
+"""The FFN's GELU fused with its projections: the first projection's forward followed by the GELU
+(reels_hip_i8lora_fwd_gelu) and the second projection's backward with the GELU's pullback
+(reels_hip_i8lora_bwd_gelu), each with its f16 form. Where the GEMM is the unsplit
+dequantized-weight GEMM the GELU (or its pullback) runs in its epilogue; elsewhere (few tokens,
+split reductions) the separate pass runs after it. Either way every output must equal the two
+separate calls bit for bit: the linear, then gelu_tanh (or the linear's backward, then
+gelu_tanh_backward). The separate calls are checked against the oracle in test_gpu_lora.py
+(shapes, ranks, test_gelu_tanh); one case here also samples rows of the composition against the
+oracle."""
 import numpy as np
 import pytest
 
@@ -38,6 +40,45 @@ def _case(dev, M, K, N, r, seed, dt):
 SHAPES = [(4096, 1536, 8960, 32, "bf16"), (1000, 1536, 8960, 32, "bf16"),
           (2048, 1024, 4096, 16, "f16"), (77, 1536, 1536, 16, "bf16"), (300, 1536, 8960, 32, "bf16"),
           (512, 1024, 2048, 8, "f16")]
+
+
+@pytest.mark.parametrize("M,K,N,r,dt", SHAPES)
+def test_fused_gelu_forward_equals_the_separate_calls(dev, M, K, N, r, dt):
+    """y, g and h of i8lora_forward_gelu against i8lora_forward then gelu_tanh: the forward's
+    M x N outputs run the fused epilogue in the first three shapes (unsplit GEMM), the separate
+    pass in the rest."""
+    import torch
+    from reels_amd import gelu_tanh, i8lora_forward, i8lora_forward_gelu
+    print(f"[gelu-fused fwd] M={M} K={K} N={N} r={r} {dt}", flush=True)
+    host, d = _case(dev, M, K, N, r, 700 + M + N, dt)
+    c = 0.75
+    y, g, h = i8lora_forward_gelu(d["x"], d["W"], d["A"], d["B"], d["bias"], c, save_h=True)
+    y2, h2 = i8lora_forward(d["x"], d["W"], d["A"], d["B"], d["bias"], c, save_h=True)
+    g2 = gelu_tanh(y2)
+    torch.cuda.synchronize(dev)
+    assert torch.equal(y, y2), "y differs from i8lora_forward"
+    assert torch.equal(h, h2), "h differs from i8lora_forward"
+    assert torch.equal(g, g2), "g differs from gelu_tanh(y)"
+    if M == 1000:
+        # sampled rows of g against the oracle's GELU of the oracle's rounded linear output
+        rows = np.unique(np.concatenate([np.arange(0, M, 97), [M - 1]]))
+        yo, _ = oracle.lora_forward(host["x"][rows], host["q"], host["s"], host["A"], host["B"], c,
+                                    bias=host["bias"])
+        assert_parity(bf16_f32(y)[rows], yo, "y vs oracle")
+        go = oracle.bf16_to_f32(oracle.gelu_tanh(oracle.f32_to_bf16(bf16_f32(y)[rows])))
+        got = bf16_f32(g)[rows]
+        # the device's and the host's f32 tanh may differ in the last bits: one bf16 ulp
+        assert np.all(np.abs(got - go) <= 2.0 ** -7 * np.abs(go) + 1e-30), "g vs the oracle's GELU of y"
+
+
+def test_fused_gelu_forward_rejects_a_missing_output(dev):
+    import ctypes
+    from reels_amd import _lib
+    L = _lib.lib()
+    fake = ctypes.c_void_p(4096)
+    rc = L.reels_hip_i8lora_fwd_gelu(fake, fake, fake, None, None, None, 4, 64, 64, 0, 1.0, fake,
+                                     None, None, None, 0, None)
+    assert rc == -1 and b"NULL g" in L.reels_hip_last_error()
 
 
 @pytest.mark.parametrize("M,K,N,r,dt", SHAPES)
