@@ -37,8 +37,8 @@ WARM_S = 0.05  # untimed back-to-back calls before timing a call of tens of micr
 # HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs of this script (KiB per
 # dispatch scaled by a 1 GiB device copy: FETCH x 2.0, WRITE x 1.0), averaged over one step's
 # launches; the commands and per-kernel figures are in profiles/.
-GEMM_TRAFFIC_BYTES = 4636370261
-GEMM_TRAFFIC_NOTE = ("mean over one step's 12 GEMM launches (q/k/v/o 3.04 GB, ffn 7.60-8.13 GB); "
+GEMM_TRAFFIC_BYTES = 4663654453
+GEMM_TRAFFIC_NOTE = ("mean over one step's 12 GEMM launches (q/k/v/o 3.04 GB, ffn 7.60-8.30 GB); "
                      "FETCH_SIZE includes Infinity Cache hits; algorithmic mean 0.946 GB")
 PACK_TRAFFIC_BYTES = 14792000000  # mean of the two launches (21.088 + 8.496 GB), ratio 1.000
 PROJECTIONS = [("self_attn.q", 5120, 5120), ("self_attn.k", 5120, 5120),
