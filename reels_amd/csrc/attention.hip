@@ -20,6 +20,9 @@
 // Backward (deterministic, no atomics): correction[q] = sum(dy .* out) (attention.jl:190); a
 // key-tile kernel accumulates dK and dV over all query tiles; a query-tile kernel accumulates dQ
 // over all key tiles. Both recompute P from lse.
+#include <cstdlib>
+#include <cstring>
+
 #include "attention_g.h"
 
 namespace reels {
@@ -419,11 +422,13 @@ __global__ __launch_bounds__(256, 2) void attn_dkdv_kernel(AttArgs a) {
     if (t < 2 * QT) {
       const int64_t qi = (int64_t)j * QT + (t % QT);
       stv = 0.0f;
-      if (qi < Sq) stv = (t < QT) ? a.lse[(b * H + h) * Sq + qi] * LOG2E : a.corr[(b * H + h) * Sq + qi];
+      if (qi < Sq) stv = (t < QT) ? a.lse[(b * H + h) * Sq + qi] : a.corr[(b * H + h) * Sq + qi];
     }
   };
+  // lse to base 2 here, after the step's wait: a product at the load made the wave wait for the
+  // load before issuing the step's copies
   auto stats_store = [&](int j) {
-    if (t < 2 * QT) sstat[(j & 1) * 2 * QT + t] = stv;
+    if (t < 2 * QT) sstat[(j & 1) * 2 * QT + t] = t < QT ? stv * LOG2E : stv;
   };
 
   f32x4 dvacc[NDT], dkacc[NDT];
@@ -517,6 +522,221 @@ __global__ __launch_bounds__(256, 2) void attn_dkdv_kernel(AttArgs a) {
       *reinterpret_cast<u32x2*>(dvrow + 16 * dt + 4 * g) = pv;
       *reinterpret_cast<u32x2*>(dkrow + 16 * dt + 4 * g) = pk;
     }
+  }
+}
+
+// dK, dV for head dim 128 on 32 x 32 x 16 MFMAs: a workgroup takes 128 keys of one (batch,
+// head), 32 per wave, and streams the queries in steps of 32 (Q and dY tiles through a two-stage
+// LDS ring, the workgroup's V rows in LDS for the whole pass, K in registers). Per step and wave:
+// S = Q K^T and dP = dY V^T as one 32 x 32 tile each (lane l: key l % 32; accumulator element v:
+// query 8 (v / 4) + 4 (l / 32) + v % 4), P from lse, dS = P (dP - correction), then
+// dV^T += dY^T P and dK^T += Q^T dS over two 16-query MFMA steps b. Step b's B operands are
+// accumulator elements 8 b .. 8 b + 7 as they are (queries 16 b + 4 (l / 32) + 0..3 and
+// 16 b + 8 + 4 (l / 32) + 0..3), its A operands dY^T and Q^T read transposed from the step tiles
+// in that query order. Each fragment read from LDS feeds one 32 x 32 x 16 MFMA: 40 KB of LDS
+// reads per wave and step against 64 KB for the same products on 16 x 16 x 32 tiles with 16 keys
+// per wave.
+namespace att {
+constexpr int KW2 = 32;   // keys per wave
+constexpr int KB2 = 128;  // keys per workgroup
+constexpr int QS = 32;    // queries per step
+}  // namespace att
+
+// Chunk swizzle of this kernel's tiles (rows of 128 elements, 256 bytes: each row covers all 64
+// banks): the slot of chunk c of row r is c ^ swz32(r), swz32(r) = 4 (r mod 4) + (r / 4 mod 2)
+// + 2 (r / 8 mod 2), a bijection on r mod 16.
+// - fragment reads (ds_read_b128, lane l: row l % 32, chunk 2 s + l / 32): the instruction's
+//   16-lane passes (8-lane groups {0, 3}, {1, 2}, {4, 7}, {5, 6}) take rows {0..7, 24..31} or
+//   {8..15, 16..23} at one chunk: 16 distinct r mod 16, 16 distinct slots;
+// - transposed reads (read_tr32, ds_read_b64_tr_b16; a 32-lane pass reads rows 4 i .. 4 i + 3,
+//   chunks 4 t .. 4 t + 3): swz32(r) / 4 = r mod 4 differs between the four rows, so the four
+//   rows' chunk quads land on four distinct quads of slots.
+__device__ __forceinline__ int swz32(int r) {
+  return ((r & 3) << 2) | ((r >> 2) & 1) | (((r >> 3) & 1) << 1);
+}
+__device__ __forceinline__ uint32_t toff32(int r, int d) {
+  return (uint32_t)(r * 256 + (((d >> 3) ^ swz32(r)) << 4) + (d & 7) * 2);
+}
+// read_tr on the swz32 layout: element e < 4 is row r0 + e, e >= 4 row r1 + e - 4, column
+// c + (lane % 16)
+__device__ __forceinline__ u32x4 read_tr32(const uint8_t* tile, int r0, int r1, int c, int i16) {
+  const int rr0 = r0 + (i16 >> 2), rr1 = r1 + (i16 >> 2), cc = c + 4 * (i16 & 3);
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(i16x4, tile + toff32(rr0, cc)));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(LDS_PTR(i16x4, tile + toff32(rr1, cc)));
+  u32x4 r;
+  r[0] = (uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16);
+  r[1] = (uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16);
+  r[2] = (uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16);
+  r[3] = (uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16);
+  return r;
+}
+
+// LDS: [V rows of the workgroup, 32 KB][2 stages x (Q 8 KB, dY 8 KB)][2 stages x (lse 32, corr 32) f32]
+constexpr int kDkdv32Lds = att::KB2 * 256 + 2 * 2 * att::QS * 256 + 2 * 2 * att::QS * 4;
+
+template <int ELT, int VM>
+__global__ __launch_bounds__(256, 2) void attn_dkdv32_kernel(AttArgs a) {
+  using E = Elt<ELT>;
+  using namespace att;
+  constexpr int D = 128;
+  constexpr int TQ = QS * D * 2;   // bytes of one Q or dY step tile
+  constexpr int TV = KB2 * D * 2;  // bytes of the V rows
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int l32 = lane & 31, hf = lane >> 5, l16 = lane & 15, g = lane >> 4;
+  const int64_t b = blockIdx.z, h = blockIdx.y;
+  const int64_t kb0 = (int64_t)blockIdx.x * KB2;
+  const int64_t Sq = a.Sq, Sk = a.Sk, H = a.H;
+  const float sl2 = a.scale * LOG2E;
+  const int64_t kj = kb0 + w * KW2 + l32;  // this lane's key
+
+  // K fragments (B operands of S): key kj, d = 16 s + 8 hf ..
+  u32x4 kf[D / 16];
+#pragma unroll
+  for (int s = 0; s < D / 16; ++s) {
+    kf[s] = u32x4{0, 0, 0, 0};
+    if (kj < Sk) kf[s] = *reinterpret_cast<const u32x4*>(a.k + ((b * Sk + kj) * H + h) * D + 16 * s + 8 * hf);
+  }
+  const uint32_t nrq = (uint32_t)(((Sq - 1) * H + 1) * D * 2);
+  const uint32_t nrk = (uint32_t)(((Sk - 1) * H + 1) * D * 2);
+  const i32x4 rq = buffer_rsrc(a.q + (b * Sq * H + h) * D, nrq);
+  const i32x4 rd = buffer_rsrc(a.dy + (b * Sq * H + h) * D, nrq);
+  const i32x4 rv = buffer_rsrc(a.v + (b * Sk * H + h) * D, nrk);
+  // LDS-DMA copies of 1 KiB (4 rows): lane L writes row 4 c + L / 16 of copy c, slot L % 16, with
+  // chunk (L % 16) ^ swz32(row) of that row. Per step wave w copies rows 8 w .. 8 w + 7 of the Q
+  // and of the dY tile; before the first step, its own 32 V rows. Rows past the tensor's end read
+  // zeros (buffer range).
+  const int crow = lane >> 4, cslot = lane & 15;
+  uint32_t qoff[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int row = 8 * w + 4 * i + crow;
+    qoff[i] = (uint32_t)((row * H * D + (cslot ^ swz32(row)) * 8) * 2);
+  }
+  // LDS addresses of the copies (M0) in scalar registers
+  const uint32_t sbase = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)LDS_PTR(const uint8_t, smem));
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+  auto issue = [&](int j) {
+    const uint32_t roff = (uint32_t)((int64_t)j * QS * H * D * 2);
+    const uint32_t st = sbase + (uint32_t)(TV + (j & 1) * 2 * TQ + wu * 2048);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      dma16_at(rq, qoff[i] + roff, 0u, st + i * 1024);
+      dma16_at(rd, qoff[i] + roff, 0u, st + TQ + i * 1024);
+    }
+  };
+  auto issue_v = [&]() {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = 32 * w + 4 * i + crow;
+      const uint32_t off = (uint32_t)(((kb0 + row) * H * D + (cslot ^ swz32(row)) * 8) * 2);
+      dma16_at(rv, off, 0u, sbase + (uint32_t)(32 * wu + 4 * i) * 256);
+    }
+  };
+  float* sstat = reinterpret_cast<float*>(smem + TV + 4 * TQ);  // [2 stages][lse QS, corr QS]
+  // lse (to base 2 at the store) and correction of a step's queries (threads 0..63), loaded with
+  // the step's copies and written to LDS after the wait that ends the previous step
+  float stv = 0.0f;
+  auto stats_load = [&](int j) {
+    if (t < 2 * QS) {
+      const int64_t qi = (int64_t)j * QS + (t % QS);
+      stv = 0.0f;
+      if (qi < Sq) stv = (t < QS) ? a.lse[(b * H + h) * Sq + qi] : a.corr[(b * H + h) * Sq + qi];
+    }
+  };
+  auto stats_store = [&](int j) {
+    if (t < 2 * QS) sstat[(j & 1) * 2 * QS + t] = t < QS ? stv * LOG2E : stv;
+  };
+
+  f32x16 dvacc[D / 32], dkacc[D / 32];
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) dvacc[dt][v] = dkacc[dt][v] = 0.0f;
+
+  // causal: queries before the first key of this workgroup see none of its keys
+  int jbeg = 0;
+  if (a.causal) jbeg = (int)(kb0 / QS);
+  const int nsteps = (int)((Sq + QS - 1) / QS);
+  if (jbeg < nsteps) { issue_v(); stats_load(jbeg); issue(jbeg); }
+  const uint8_t* sv = smem + w * KW2 * 256;
+  for (int j = jbeg; j < nsteps; ++j) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // this wave's copies and statistics of step j
+    stats_store(j);
+    __syncthreads();
+    if (j + 1 < nsteps) { stats_load(j + 1); issue(j + 1); }
+    __builtin_amdgcn_s_setprio(0);
+    const uint8_t* sq = smem + TV + (j & 1) * 2 * TQ;
+    const uint8_t* sd = sq + TQ;
+    const float* ls = sstat + (j & 1) * 2 * QS;
+    f32x16 s, dp;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) s[v] = dp[v] = 0.0f;
+#pragma unroll
+    for (int ds = 0; ds < D / 16; ++ds) {
+      const u32x4 qa = *reinterpret_cast<const u32x4*>(sq + toff32(l32, 16 * ds + 8 * hf));
+      const u32x4 da = *reinterpret_cast<const u32x4*>(sd + toff32(l32, 16 * ds + 8 * hf));
+      const u32x4 va = *reinterpret_cast<const u32x4*>(sv + toff32(l32, 16 * ds + 8 * hf));
+      s = E::mfma32(E::as8(qa), E::as8(kf[ds]), s);
+      dp = E::mfma32(E::as8(da), E::as8(va), dp);
+    }
+    float p[16], dsv[16];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      // lse and correction of this lane's queries 8 c + 4 hf .. + 3: one read each
+      const f32x4 lq4 = *reinterpret_cast<const f32x4*>(ls + 8 * c + 4 * hf);
+      const f32x4 cq4 = *reinterpret_cast<const f32x4*>(ls + QS + 8 * c + 4 * hf);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int v = 4 * c + e;
+        const int64_t qi = (int64_t)j * QS + 8 * c + 4 * hf + e;
+        // without a mask nothing needs hiding: a query past Sq has zero Q and dY rows and zero
+        // statistics (P = 1, dS = 0, both products add zeros); a key past Sk only affects its
+        // own, unstored, dK and dV column
+        const bool vis = VM == 0 || att_visible<VM>(a, qi, kj);
+        p[v] = vis ? ex2(s[v] * sl2 - lq4[e]) : 0.0f;
+        dsv[v] = vis ? p[v] * (dp[v] - cq4[e]) : 0.0f;
+      }
+    }
+    u32x4 pb[2], db[2];
+#pragma unroll
+    for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pb[bb][i] = E::pack2_fast(p[8 * bb + 2 * i], p[8 * bb + 2 * i + 1]);
+        db[bb][i] = E::pack2_fast(dsv[8 * bb + 2 * i], dsv[8 * bb + 2 * i + 1]);
+      }
+    // gradient MFMAs at raised wave priority, as in attn_dkdv_kernel
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt) {
+        const int r0 = 16 * bb + 4 * hf, c = 32 * dt + 16 * (g & 1);
+        const u32x4 da = read_tr32(sd, r0, r0 + 8, c, l16);
+        const u32x4 qa = read_tr32(sq, r0, r0 + 8, c, l16);
+        dvacc[dt] = E::mfma32(E::as8(da), E::as8(pb[bb]), dvacc[dt]);
+        dkacc[dt] = E::mfma32(E::as8(qa), E::as8(db[bb]), dkacc[dt]);
+      }
+  }
+  __builtin_amdgcn_s_setprio(0);
+  // dV[kj][d], dK[kj][d] = scale dK^T: element v of tile dt is d = 32 dt + 8 (v / 4) + 4 hf + v % 4
+  if (kj < Sk) {
+    uint16_t* dvrow = a.dv + ((b * Sk + kj) * H + h) * D;
+    uint16_t* dkrow = a.dk + ((b * Sk + kj) * H + h) * D;
+    const float sc = a.scale;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int d = 32 * dt + 8 * c + 4 * hf;
+        const u32x2 pv = {E::pack2(dvacc[dt][4 * c], dvacc[dt][4 * c + 1]),
+                          E::pack2(dvacc[dt][4 * c + 2], dvacc[dt][4 * c + 3])};
+        const u32x2 pk = {E::pack2(dkacc[dt][4 * c] * sc, dkacc[dt][4 * c + 1] * sc),
+                          E::pack2(dkacc[dt][4 * c + 2] * sc, dkacc[dt][4 * c + 3] * sc)};
+        *reinterpret_cast<u32x2*>(dvrow + d) = pv;
+        *reinterpret_cast<u32x2*>(dkrow + d) = pk;
+      }
   }
 }
 
@@ -721,6 +941,23 @@ static int launch_attn_fwd(const AttArgs& a, int64_t B, hipStream_t st) {
   });
 }
 
+// dK / dV at head dim 128: the 128-key workgroups of attn_dkdv32_kernel or the 64-key ones of
+// attn_dkdv_kernel, whichever grid needs less time counted in rounds of 512 workgroups (two per
+// CU on 256 CUs). A 128-key workgroup takes 1.76 times as long as a 64-key one (0.88 of two:
+// 36.3 against 41.4 ms at 32760 x 32760 x 40 heads), so few keys, as in cross-attention on text
+// tokens, go to the 64-key kernel (backward at 32760 queries x 40 heads, 64- / 128-key kernel:
+// 77 keys 1.25 / 1.58 ms, 512 keys 1.77 / 1.81, 1024 keys 3.05 / 2.75, 2048 keys 5.02 / 5.27,
+// 8192 keys 18.1 / 16.2). REELS_HIP_ATTN_DKDV_KEYS=128 or =64 fixes the choice (the tests run
+// both kernels on the same shapes).
+static bool dkdv_wide(int64_t Sk, int64_t H, int64_t B) {
+  if (const char* e = std::getenv("REELS_HIP_ATTN_DKDV_KEYS")) {
+    if (std::strcmp(e, "128") == 0) return true;
+    if (std::strcmp(e, "64") == 0) return false;
+  }
+  const int64_t n128 = ceil_div(Sk, att::KB2) * H * B, n64 = ceil_div(Sk, att::KB) * H * B;
+  return ceil_div(n128, 512) * 176 < ceil_div(n64, 512) * 100;
+}
+
 template <int ELT, int D>
 static int launch_attn_bwd(const AttArgs& a, int64_t B, hipStream_t st) {
   {
@@ -730,7 +967,15 @@ static int launch_attn_bwd(const AttArgs& a, int64_t B, hipStream_t st) {
   if (int rc = check_launch("attn_corr_kernel")) return rc;
   return with_vm(a, [&](auto vm) {
     constexpr int VM = decltype(vm)::value;
-    if (a.Sk > 0) {
+    bool wide = false;
+    if constexpr (D == 128) wide = dkdv_wide(a.Sk, a.H, B);
+    if (a.Sk > 0 && wide) {
+      if (hipError_t e = set_lds(attn_dkdv32_kernel<ELT, VM>, kDkdv32Lds))
+        return fail(REELS_HIP_EHIP, std::string("attention bwd: hipFuncSetAttribute: ") + hipGetErrorString(e));
+      const dim3 grid((unsigned)ceil_div(a.Sk, att::KB2), (unsigned)a.H, (unsigned)B);
+      { TraceScope _ts(st, "attn_dkdv_kernel"); attn_dkdv32_kernel<ELT, VM><<<grid, 256, kDkdv32Lds, st>>>(a); }
+      if (int rc = check_launch("attn_dkdv32_kernel")) return rc;
+    } else if (a.Sk > 0) {
       const int lds = 4 * att::QT * D * 2 + 2 * 2 * att::QT * 4;  // Q, dY rings + lse / corr
       if (hipError_t e = set_lds(attn_dkdv_kernel<ELT, D, VM>, lds))
         return fail(REELS_HIP_EHIP, std::string("attention bwd: hipFuncSetAttribute: ") + hipGetErrorString(e));
