@@ -525,21 +525,25 @@ __global__ __launch_bounds__(256, 2) void attn_dkdv_kernel(AttArgs a) {
   }
 }
 
-// dK, dV for head dim 128 on 32 x 32 x 16 MFMAs: a workgroup takes 128 keys of one (batch,
-// head), 32 per wave, and streams the queries in steps of 32 (Q and dY tiles through a two-stage
-// LDS ring, the workgroup's V rows in LDS for the whole pass, K in registers). Per step and wave:
-// S = Q K^T and dP = dY V^T as one 32 x 32 tile each (lane l: key l % 32; accumulator element v:
-// query 8 (v / 4) + 4 (l / 32) + v % 4), P from lse, dS = P (dP - correction), then
-// dV^T += dY^T P and dK^T += Q^T dS over two 16-query MFMA steps b. Step b's B operands are
-// accumulator elements 8 b .. 8 b + 7 as they are (queries 16 b + 4 (l / 32) + 0..3 and
-// 16 b + 8 + 4 (l / 32) + 0..3), its A operands dY^T and Q^T read transposed from the step tiles
-// in that query order. Each fragment read from LDS feeds one 32 x 32 x 16 MFMA: 40 KB of LDS
-// reads per wave and step against 64 KB for the same products on 16 x 16 x 32 tiles with 16 keys
-// per wave.
+// dK, dV for head dim 128 on 32 x 32 x 16 MFMAs: a workgroup of eight waves takes 256 keys of one
+// (batch, head), 32 per wave, and streams the queries in steps of 64 (Q and dY tiles through a
+// two-stage LDS ring, the workgroup's V rows in LDS for the whole pass, K in registers). Each
+// step is two blocks of 32 queries; per block and wave: S = Q K^T and dP = dY V^T as one 32 x 32
+// tile each (lane l: key l % 32; accumulator element v: query 8 (v / 4) + 4 (l / 32) + v % 4),
+// P from lse, dS = P (dP - correction), then dV^T += dY^T P and dK^T += Q^T dS over two
+// 16-query MFMA steps b. Step b's B operands are accumulator elements 8 b .. 8 b + 7 as they are
+// (queries 16 b + 4 (l / 32) + 0..3 and 16 b + 8 + 4 (l / 32) + 0..3), its A operands dY^T and
+// Q^T read transposed from the step tiles in that query order. Each fragment read from LDS feeds
+// one 32 x 32 x 16 MFMA: 40 KB of LDS reads per wave and 32 queries against 64 KB for the same
+// products on 16 x 16 x 32 tiles with 16 keys per wave. Eight waves share each Q / dY tile (half
+// the L2 reads of four-wave workgroups: measured 1.73 -> 1.79 GHz under the power cap, dK/dV
+// 36.7 -> 36.0 ms), and the 64-query steps keep one barrier per 64 queries.
 namespace att {
 constexpr int KW2 = 32;   // keys per wave
-constexpr int KB2 = 128;  // keys per workgroup
-constexpr int QS = 32;    // queries per step
+constexpr int KB2 = 256;  // keys per workgroup
+constexpr int NW2 = 8;    // waves per workgroup
+constexpr int QT2 = 64;   // queries per step (two 32-query blocks)
+constexpr int QS = 32;    // queries per MFMA block
 }  // namespace att
 
 // Chunk swizzle of this kernel's tiles (rows of 128 elements, 256 bytes: each row covers all 64
@@ -571,15 +575,15 @@ __device__ __forceinline__ u32x4 read_tr32(const uint8_t* tile, int r0, int r1, 
   return r;
 }
 
-// LDS: [V rows of the workgroup, 32 KB][2 stages x (Q 8 KB, dY 8 KB)][2 stages x (lse 32, corr 32) f32]
-constexpr int kDkdv32Lds = att::KB2 * 256 + 2 * 2 * att::QS * 256 + 2 * 2 * att::QS * 4;
+// LDS: [V rows of the workgroup, 64 KB][2 stages x (Q 16 KB, dY 16 KB)][2 stages x (lse 64, corr 64) f32]
+constexpr int kDkdv32Lds = att::KB2 * 256 + 2 * 2 * att::QT2 * 256 + 2 * 2 * att::QT2 * 4;
 
 template <int ELT, int VM>
-__global__ __launch_bounds__(256, 2) void attn_dkdv32_kernel(AttArgs a) {
+__global__ __launch_bounds__(512, 1) void attn_dkdv32_kernel(AttArgs a) {
   using E = Elt<ELT>;
   using namespace att;
   constexpr int D = 128;
-  constexpr int TQ = QS * D * 2;   // bytes of one Q or dY step tile
+  constexpr int TQ = QT2 * D * 2;  // bytes of one Q or dY step tile
   constexpr int TV = KB2 * D * 2;  // bytes of the V rows
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
@@ -603,9 +607,9 @@ __global__ __launch_bounds__(256, 2) void attn_dkdv32_kernel(AttArgs a) {
   const i32x4 rd = buffer_rsrc(a.dy + (b * Sq * H + h) * D, nrq);
   const i32x4 rv = buffer_rsrc(a.v + (b * Sk * H + h) * D, nrk);
   // LDS-DMA copies of 1 KiB (4 rows): lane L writes row 4 c + L / 16 of copy c, slot L % 16, with
-  // chunk (L % 16) ^ swz32(row) of that row. Per step wave w copies rows 8 w .. 8 w + 7 of the Q
-  // and of the dY tile; before the first step, its own 32 V rows. Rows past the tensor's end read
-  // zeros (buffer range).
+  // chunk (L % 16) ^ swz32(row) of that row. Per step wave w copies rows 8 w .. 8 w + 7 of the
+  // 64-row Q and dY tiles; before the first step, its own 32 V rows. Rows past the tensor's end
+  // read zeros (buffer range).
   const int crow = lane >> 4, cslot = lane & 15;
   uint32_t qoff[2];
 #pragma unroll
@@ -617,7 +621,7 @@ __global__ __launch_bounds__(256, 2) void attn_dkdv32_kernel(AttArgs a) {
   const uint32_t sbase = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)LDS_PTR(const uint8_t, smem));
   const int wu = __builtin_amdgcn_readfirstlane(w);
   auto issue = [&](int j) {
-    const uint32_t roff = (uint32_t)((int64_t)j * QS * H * D * 2);
+    const uint32_t roff = (uint32_t)((int64_t)j * QT2 * H * D * 2);
     const uint32_t st = sbase + (uint32_t)(TV + (j & 1) * 2 * TQ + wu * 2048);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -633,19 +637,19 @@ __global__ __launch_bounds__(256, 2) void attn_dkdv32_kernel(AttArgs a) {
       dma16_at(rv, off, 0u, sbase + (uint32_t)(32 * wu + 4 * i) * 256);
     }
   };
-  float* sstat = reinterpret_cast<float*>(smem + TV + 4 * TQ);  // [2 stages][lse QS, corr QS]
+  float* sstat = reinterpret_cast<float*>(smem + TV + 4 * TQ);  // [2 stages][lse QT2, corr QT2]
   // lse (to base 2 at the store) and correction of a step's queries (threads 0..63), loaded with
   // the step's copies and written to LDS after the wait that ends the previous step
   float stv = 0.0f;
   auto stats_load = [&](int j) {
-    if (t < 2 * QS) {
-      const int64_t qi = (int64_t)j * QS + (t % QS);
+    if (t < 2 * QT2) {
+      const int64_t qi = (int64_t)j * QT2 + (t % QT2);
       stv = 0.0f;
-      if (qi < Sq) stv = (t < QS) ? a.lse[(b * H + h) * Sq + qi] : a.corr[(b * H + h) * Sq + qi];
+      if (qi < Sq) stv = (t < QT2) ? a.lse[(b * H + h) * Sq + qi] : a.corr[(b * H + h) * Sq + qi];
     }
   };
   auto stats_store = [&](int j) {
-    if (t < 2 * QS) sstat[(j & 1) * 2 * QS + t] = t < QS ? stv * LOG2E : stv;
+    if (t < 2 * QT2) sstat[(j & 1) * 2 * QT2 + t] = t < QT2 ? stv * LOG2E : stv;
   };
 
   f32x16 dvacc[D / 32], dkacc[D / 32];
@@ -656,8 +660,8 @@ __global__ __launch_bounds__(256, 2) void attn_dkdv32_kernel(AttArgs a) {
 
   // causal: queries before the first key of this workgroup see none of its keys
   int jbeg = 0;
-  if (a.causal) jbeg = (int)(kb0 / QS);
-  const int nsteps = (int)((Sq + QS - 1) / QS);
+  if (a.causal) jbeg = (int)(kb0 / QT2);
+  const int nsteps = (int)((Sq + QT2 - 1) / QT2);
   if (jbeg < nsteps) { issue_v(); stats_load(jbeg); issue(jbeg); }
   const uint8_t* sv = smem + w * KW2 * 256;
   for (int j = jbeg; j < nsteps; ++j) {
@@ -665,10 +669,13 @@ __global__ __launch_bounds__(256, 2) void attn_dkdv32_kernel(AttArgs a) {
     stats_store(j);
     __syncthreads();
     if (j + 1 < nsteps) { stats_load(j + 1); issue(j + 1); }
+    // the two 32-query blocks (kept as a loop: unrolled, the compiler interleaves them and spills)
+#pragma unroll 1
+    for (int sb = 0; sb < QT2 / QS; ++sb) {
     __builtin_amdgcn_s_setprio(0);
-    const uint8_t* sq = smem + TV + (j & 1) * 2 * TQ;
+    const uint8_t* sq = smem + TV + (j & 1) * 2 * TQ + sb * QS * 256;
     const uint8_t* sd = sq + TQ;
-    const float* ls = sstat + (j & 1) * 2 * QS;
+    const float* ls0 = sstat + (j & 1) * 2 * QT2 + sb * QS;
     f32x16 s, dp;
 #pragma unroll
     for (int v = 0; v < 16; ++v) s[v] = dp[v] = 0.0f;
@@ -684,12 +691,12 @@ __global__ __launch_bounds__(256, 2) void attn_dkdv32_kernel(AttArgs a) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       // lse and correction of this lane's queries 8 c + 4 hf .. + 3: one read each
-      const f32x4 lq4 = *reinterpret_cast<const f32x4*>(ls + 8 * c + 4 * hf);
-      const f32x4 cq4 = *reinterpret_cast<const f32x4*>(ls + QS + 8 * c + 4 * hf);
+      const f32x4 lq4 = *reinterpret_cast<const f32x4*>(ls0 + 8 * c + 4 * hf);
+      const f32x4 cq4 = *reinterpret_cast<const f32x4*>(ls0 + QT2 + 8 * c + 4 * hf);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int v = 4 * c + e;
-        const int64_t qi = (int64_t)j * QS + 8 * c + 4 * hf + e;
+        const int64_t qi = (int64_t)j * QT2 + sb * QS + 8 * c + 4 * hf + e;
         // without a mask nothing needs hiding: a query past Sq has zero Q and dY rows and zero
         // statistics (P = 1, dS = 0, both products add zeros); a key past Sk only affects its
         // own, unstored, dK and dV column
@@ -718,6 +725,7 @@ __global__ __launch_bounds__(256, 2) void attn_dkdv32_kernel(AttArgs a) {
         dvacc[dt] = E::mfma32(E::as8(da), E::as8(pb[bb]), dvacc[dt]);
         dkacc[dt] = E::mfma32(E::as8(qa), E::as8(db[bb]), dkacc[dt]);
       }
+    }
   }
   __builtin_amdgcn_s_setprio(0);
   // dV[kj][d], dK[kj][d] = scale dK^T: element v of tile dt is d = 32 dt + 8 (v / 4) + 4 hf + v % 4
@@ -941,21 +949,22 @@ static int launch_attn_fwd(const AttArgs& a, int64_t B, hipStream_t st) {
   });
 }
 
-// dK / dV at head dim 128: the 128-key workgroups of attn_dkdv32_kernel or the 64-key ones of
-// attn_dkdv_kernel, whichever grid needs less time counted in rounds of 512 workgroups (two per
-// CU on 256 CUs). A 128-key workgroup takes 1.76 times as long as a 64-key one (0.88 of two:
-// 36.3 against 41.4 ms at 32760 x 32760 x 40 heads), so few keys, as in cross-attention on text
-// tokens, go to the 64-key kernel (backward at 32760 queries x 40 heads, 64- / 128-key kernel:
-// 77 keys 1.25 / 1.58 ms, 512 keys 1.77 / 1.81, 1024 keys 3.05 / 2.75, 2048 keys 5.02 / 5.27,
-// 8192 keys 18.1 / 16.2). REELS_HIP_ATTN_DKDV_KEYS=128 or =64 fixes the choice (the tests run
-// both kernels on the same shapes).
+// dK / dV at head dim 128: the 256-key workgroups of attn_dkdv32_kernel (one per CU, 256 CUs)
+// or the 64-key ones of attn_dkdv_kernel (two per CU), whichever grid needs less time counted in
+// rounds of workgroups over the CUs. A 256-key round takes 1.74 times as long as a 64-key one
+// (36.0 ms for 20 rounds against 41.4 ms for 40 at 32760 x 32760 x 40 heads), so few keys, as in
+// cross-attention on text tokens, go to the 64-key kernel. Backward at 32760 queries x 40 heads,
+// 64- / 256-key kernel: 77 keys 1.24 / 1.84 ms, 512 keys 1.78 / 2.13, 1024 keys 2.96 / 2.61,
+// 2048 keys 4.90 / 5.35, 3072 keys 6.91 / 6.20, 4096 keys 8.56 / 8.86, 8192 keys 16.7 / 15.2:
+// the rule picks the faster one at each. REELS_HIP_ATTN_DKDV_KEYS=256 or =64 fixes the choice
+// (the tests run both kernels on the same shapes).
 static bool dkdv_wide(int64_t Sk, int64_t H, int64_t B) {
   if (const char* e = std::getenv("REELS_HIP_ATTN_DKDV_KEYS")) {
-    if (std::strcmp(e, "128") == 0) return true;
+    if (std::strcmp(e, "256") == 0) return true;
     if (std::strcmp(e, "64") == 0) return false;
   }
-  const int64_t n128 = ceil_div(Sk, att::KB2) * H * B, n64 = ceil_div(Sk, att::KB) * H * B;
-  return ceil_div(n128, 512) * 176 < ceil_div(n64, 512) * 100;
+  const int64_t nw = ceil_div(Sk, att::KB2) * H * B, n64 = ceil_div(Sk, att::KB) * H * B;
+  return ceil_div(nw, 256) * 174 < ceil_div(n64, 512) * 100;
 }
 
 template <int ELT, int D>
@@ -973,7 +982,7 @@ static int launch_attn_bwd(const AttArgs& a, int64_t B, hipStream_t st) {
       if (hipError_t e = set_lds(attn_dkdv32_kernel<ELT, VM>, kDkdv32Lds))
         return fail(REELS_HIP_EHIP, std::string("attention bwd: hipFuncSetAttribute: ") + hipGetErrorString(e));
       const dim3 grid((unsigned)ceil_div(a.Sk, att::KB2), (unsigned)a.H, (unsigned)B);
-      { TraceScope _ts(st, "attn_dkdv_kernel"); attn_dkdv32_kernel<ELT, VM><<<grid, 256, kDkdv32Lds, st>>>(a); }
+      { TraceScope _ts(st, "attn_dkdv_kernel"); attn_dkdv32_kernel<ELT, VM><<<grid, 64 * att::NW2, kDkdv32Lds, st>>>(a); }
       if (int rc = check_launch("attn_dkdv32_kernel")) return rc;
     } else if (a.Sk > 0) {
       const int lds = 4 * att::QT * D * 2 + 2 * 2 * att::QT * 4;  // Q, dY rings + lse / corr

@@ -13,7 +13,7 @@ coarser scheme). A wrong index or a missing term gives errors of order one. The 
 f32 from exact 16-bit products: absolute 1e-4. Covered: ragged query and key counts (not multiples of the 128-query
 and 64-key tiles), head dims 64 and 128, masks, causal, cross-attention shapes (few keys, many
 queries), batches, f16, queries with no visible key, no keys at all, and a larger case checked
-on a subset of queries; at head dim 128 both dK / dV kernels (64- and 128-key workgroups)."""
+on a subset of queries; at head dim 128 both dK / dV kernels (64- and 256-key workgroups)."""
 import numpy as np
 import pytest
 
@@ -126,7 +126,7 @@ def test_attention_parity(dev, B, Sq, Sk, H, D, causal, masked, dt):
     _check_bwd(grads, what)
 
 
-# The head-dim-128 cases again through the dK / dV kernel with 128-key workgroups, which the
+# The head-dim-128 cases again through the dK / dV kernel with 256-key workgroups, which the
 # launcher picks by grid size (for many keys); the environment
 # variable REELS_HIP_ATTN_DKDV_KEYS fixes the choice. Added: causal with keys past every query
 # (workgroups with no query step store zeros).
@@ -134,12 +134,12 @@ WIDE = [c for c in CASES if c[4] == 128] + [(1, 100, 600, 2, 128, True, False, "
 
 
 @pytest.mark.parametrize("B,Sq,Sk,H,D,causal,masked,dt", WIDE)
-def test_attention_parity_128_key_dkdv(dev, monkeypatch, B, Sq, Sk, H, D, causal, masked, dt):
-    monkeypatch.setenv("REELS_HIP_ATTN_DKDV_KEYS", "128")
+def test_attention_parity_256_key_dkdv(dev, monkeypatch, B, Sq, Sk, H, D, causal, masked, dt):
+    monkeypatch.setenv("REELS_HIP_ATTN_DKDV_KEYS", "256")
     test_attention_parity(dev, B, Sq, Sk, H, D, causal, masked, dt)
 
 
-@pytest.mark.parametrize("D,dkdv_keys", [(64, None), (128, "128"), (128, "64")])
+@pytest.mark.parametrize("D,dkdv_keys", [(64, None), (128, "256"), (128, "64")])
 def test_attention_query_without_visible_key(dev, monkeypatch, D, dkdv_keys):
     # NaN output and lse for that query, as the reference; the other queries and the
     # gradients are unaffected (the query contributes nothing)
@@ -232,7 +232,7 @@ def test_attention_wan14b_self_attention_full_size(dev):
     x 128 (src/models/wan21/transformer.jl:199), bf16 ~N(0, 1). Against the f64 oracle: out, lse
     and dq of 6 sampled queries (the first and the last among them) in every head; dk and dv of
     6 sampled keys (the first and the last among them) in heads 0 and 39, whose oracle streams
-    all 32760 queries (the dK / dV kernel accumulates over 1024 query steps). Every gradient
+    all 32760 queries (the dK / dV kernel accumulates over 512 query steps). Every gradient
     element: the exact identities dq, dk, dv (2 dy) = 2 (dq, dk, dv) (dy enters linearly and
     scaling by 2 commutes with every rounding)."""
     import torch
