@@ -353,23 +353,29 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// backward: correction[b][h][q] = sum_d dy * out (f32), one thread per query row
+// backward: correction[b][h][q] = sum_d dy * out (f32). D / 8 lanes per query row, 16 bytes of
+// dy and of out each (whole rows per load instruction, where one row per thread made every load
+// touch 64 rows), then a fixed-order sum over the row's lanes: the same bits on every run.
 template <int ELT, int D>
 __global__ __launch_bounds__(256) void attn_corr_kernel(AttArgs a, int64_t B) {
   using E = Elt<ELT>;
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // ((b * Sq + q) * H + h)
-  if (i >= B * a.Sq * a.H) return;
-  const int64_t h = i % a.H, bq = i / a.H, qi = bq % a.Sq, b = bq / a.Sq;
-  const u32x4* dy = reinterpret_cast<const u32x4*>(a.dy + i * D);
-  const u32x4* o = reinterpret_cast<const u32x4*>(a.out + i * D);
+  constexpr int LPR = D / 8, RPB = 256 / LPR;  // lanes per row, rows per block
+  const int t = threadIdx.x, c = t % LPR;
+  const int64_t i = (int64_t)blockIdx.x * RPB + t / LPR;  // ((b * Sq + q) * H + h)
+  const bool in = i < B * a.Sq * a.H;
   float acc = 0.0f;
-#pragma unroll
-  for (int c = 0; c < D / 8; ++c) {
-    const u32x4 x = dy[c], y = o[c];
+  if (in) {
+    const u32x4 x = reinterpret_cast<const u32x4*>(a.dy + i * D)[c];
+    const u32x4 y = reinterpret_cast<const u32x4*>(a.out + i * D)[c];
 #pragma unroll
     for (int e = 0; e < 4; ++e) acc += E::lo(x[e]) * E::lo(y[e]) + E::hi(x[e]) * E::hi(y[e]);
   }
-  a.corr_out[(b * a.H + h) * a.Sq + qi] = acc;
+#pragma unroll
+  for (int off = LPR / 2; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, LPR);
+  if (in && c == 0) {
+    const int64_t h = i % a.H, bq = i / a.H, qi = bq % a.Sq, b = bq / a.Sq;
+    a.corr_out[(b * a.H + h) * a.Sq + qi] = acc;
+  }
 }
 
 // dK, dV: a workgroup takes 64 keys of one (batch, head), 16 per wave, and streams the queries
@@ -971,7 +977,7 @@ template <int ELT, int D>
 static int launch_attn_bwd(const AttArgs& a, int64_t B, hipStream_t st) {
   {
     TraceScope _ts(st, "attn_corr_kernel");
-    attn_corr_kernel<ELT, D><<<(unsigned)ceil_div(B * a.Sq * a.H, 256), 256, 0, st>>>(a, B);
+    attn_corr_kernel<ELT, D><<<(unsigned)ceil_div(B * a.Sq * a.H, 256 / (D / 8)), 256, 0, st>>>(a, B);
   }
   if (int rc = check_launch("attn_corr_kernel")) return rc;
   return with_vm(a, [&](auto vm) {
