@@ -719,7 +719,10 @@ __global__ __launch_bounds__(512, 1) void attn_dkdv32_kernel(AttArgs a) {
         pb[bb][i] = E::pack2_fast(p[8 * bb + 2 * i], p[8 * bb + 2 * i + 1]);
         db[bb][i] = E::pack2_fast(dsv[8 * bb + 2 * i], dsv[8 * bb + 2 * i + 1]);
       }
-    // gradient MFMAs at raised wave priority, as in attn_dkdv_kernel
+    // gradient MFMAs at raised wave priority, as in attn_dkdv_kernel: the two waves of a SIMD
+    // belong to this workgroup and leave each barrier together, and the priority puts the one
+    // that reaches its gradient MFMAs first ahead, so that its MFMAs run beside the other's
+    // softmax (without it: 63.2 against 36.7 ms; over the score MFMAs instead: 37.0 ms)
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int bb = 0; bb < 2; ++bb)
