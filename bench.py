@@ -271,7 +271,7 @@ def attention_bench(dev, reps=3):
                        "flops_bwd": fb},
             "ms": round(ms, 3), "fwd_ms": round(fwd_ms, 3), "bwd_ms": round(bwd_ms, 3),
             "kernels": {n: {"launches": c // reps, "avg_ms": round(t / c, 4)} for n, (c, t) in kern.items()},
-            "roofline": {"kernel": "attn_fwd_kernel, attn_dkdv_kernel, attn_dq_kernel", "bound": "mfma",
+            "roofline": {"kernel": "attn_fwd_kernel, attn_dkdv32_kernel (attn_dkdv_kernel for few keys), attn_dq_kernel", "bound": "mfma",
                          "achieved": round(tflops, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
                          "fwd": round(ff / (fwd_ms * 1e-3) / 1e12, 1),

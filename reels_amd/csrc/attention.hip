@@ -991,7 +991,7 @@ static int launch_attn_bwd(const AttArgs& a, int64_t B, hipStream_t st) {
       if (hipError_t e = set_lds(attn_dkdv32_kernel<ELT, VM>, kDkdv32Lds))
         return fail(REELS_HIP_EHIP, std::string("attention bwd: hipFuncSetAttribute: ") + hipGetErrorString(e));
       const dim3 grid((unsigned)ceil_div(a.Sk, att::KB2), (unsigned)a.H, (unsigned)B);
-      { TraceScope _ts(st, "attn_dkdv_kernel"); attn_dkdv32_kernel<ELT, VM><<<grid, 64 * att::NW2, kDkdv32Lds, st>>>(a); }
+      { TraceScope _ts(st, "attn_dkdv32_kernel"); attn_dkdv32_kernel<ELT, VM><<<grid, 64 * att::NW2, kDkdv32Lds, st>>>(a); }
       if (int rc = check_launch("attn_dkdv32_kernel")) return rc;
     } else if (a.Sk > 0) {
       const int lds = 4 * att::QT * D * 2 + 2 * 2 * att::QT * 4;  // Q, dY rings + lse / corr
