@@ -129,8 +129,9 @@ def test_attention_parity(dev, B, Sq, Sk, H, D, causal, masked, dt):
 # The head-dim-128 cases again through the dK / dV kernel with 256-key workgroups, which the
 # launcher picks by grid size (for many keys); the environment
 # variable REELS_HIP_ATTN_DKDV_KEYS fixes the choice. Added: causal with keys past every query
-# (workgroups with no query step store zeros).
-WIDE = [c for c in CASES if c[4] == 128] + [(1, 100, 600, 2, 128, True, False, "bf16")]
+# (workgroups with no query step store zeros), and causal in f16.
+WIDE = [c for c in CASES if c[4] == 128] + [(1, 100, 600, 2, 128, True, False, "bf16"),
+                                            (1, 130, 300, 2, 128, True, False, "f16")]
 
 
 @pytest.mark.parametrize("B,Sq,Sk,H,D,causal,masked,dt", WIDE)
