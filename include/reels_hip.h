@@ -310,7 +310,10 @@ int reels_hip_gelu_tanh_bwd_f32(const float* x, const float* dy, float* dx, int6
  *   reels_hip_attention_fwd: out and (when lse != NULL) lse, the cache the backward needs.
  *   reels_hip_attention_bwd: dq, dk, dv from dy, the forward's out and lse; workspace of
  *     reels_hip_attention_workspace_bytes(B, Sq, H) bytes (the per-query sum(dy .* out)).
- * Deterministic: no atomics, fixed summation order.
+ * Deterministic: no atomics, fixed summation order. At D = 128 the backward picks one of two dK/dV
+ * kernels by grid size (256 or 64 keys per workgroup; their results differ in rounding, within
+ * the same tolerance of the exact math); the environment variable REELS_HIP_ATTN_DKDV_KEYS=256 or
+ * =64 fixes the choice.
  */
 size_t reels_hip_attention_workspace_bytes(int64_t B, int64_t Sq, int64_t H);
 int reels_hip_attention_fwd(const void* q, const void* k, const void* v, const uint8_t* mask,
